@@ -1,0 +1,220 @@
+/*
+ * riemann_hip.h — C ABI of the MI355X (gfx950) sparse-convolution hot path.
+ *
+ * The library is stateless: every buffer is owned by the caller (device
+ * pointers unless stated otherwise), every call takes the HIP stream it runs
+ * on, and nothing throws across the boundary. Each entry point returns an
+ * rhip_status; on failure rhip_last_error() holds a thread-local message.
+ * Calls whose output size is data-dependent (hash build, kernel-map count)
+ * synchronise the stream once to read that size back to the host; all other
+ * calls are asynchronous.
+ *
+ * Coordinates are int32 rows [N, ncol] with ncol = D + 1 and the batch index
+ * first (reference: RiemannEngine/engine/tensor/sparse_tensor.cpp:70-77,
+ * docs/concepts.md:41). Row indices are int32, as the reference's uint32
+ * index_type (engine/foundation/types.hpp:30) restricted to < 2^31.
+ * Weights are [K, Cin, Cout] row-major (engine/nn/conv.cpp:83-86).
+ */
+#ifndef RIEMANN_HIP_H
+#define RIEMANN_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define RHIP_ABI_VERSION 1
+#define RHIP_MAX_COLS 8 /* batch column + up to 7 spatial axes */
+
+typedef enum rhip_status {
+  RHIP_OK = 0,
+  RHIP_ERR_INVALID = 1,     /* bad argument: shape, size, null pointer */
+  RHIP_ERR_HIP = 2,         /* a HIP runtime call failed */
+  RHIP_ERR_UNSUPPORTED = 3, /* valid input this build cannot handle */
+  RHIP_ERR_WORKSPACE = 4    /* workspace smaller than the queried size */
+} rhip_status;
+
+typedef enum rhip_dtype { RHIP_F32 = 0, RHIP_BF16 = 1 } rhip_dtype;
+
+typedef enum rhip_key_mode {
+  /* Rows packed into one 63-bit integer from the per-column [lo, hi]
+   * range of the inserted set; probes compare integers only. */
+  RHIP_KEY_PACKED64 = 0,
+  /* Fallback when the ranges need more than 63 bits: slots hold a 32-bit
+   * row hash plus a unique-row index and probes compare whole rows. */
+  RHIP_KEY_ROWREF = 1
+} rhip_key_mode;
+
+/*
+ * Descriptor of a built coordinate hash table (one coordinate map).
+ * Filled by rhip_hash_build; passed by pointer to lookups and kernel maps.
+ * Replaces CoordinateMapGPU + concurrent_unordered_map
+ * (engine/grid/lattice_gpu.cuh:221-678, vendor/concurrent_unordered_map.cuh).
+ */
+typedef struct rhip_table {
+  void *slots;            /* device, capacity * 16 bytes */
+  int64_t capacity;       /* power of two, >= 2 * n */
+  const int32_t *rows;    /* device [n_unique, ncol] unique coordinates */
+  int64_t n_unique;
+  int32_t ncol;
+  int32_t mode;           /* rhip_key_mode */
+  int32_t key_bits;       /* packed width (RHIP_KEY_PACKED64) */
+  int32_t lo[RHIP_MAX_COLS];
+  int32_t hi[RHIP_MAX_COLS];
+  int32_t shift[RHIP_MAX_COLS];
+} rhip_table;
+
+/* ---------------------------------------------------------------- misc */
+
+const char *rhip_last_error(void);
+int rhip_abi_version(void);
+
+/* ---------------------------------------------------- coordinate hashing */
+
+/* Bytes of slot storage for a table built over n rows (16 B per slot). */
+size_t rhip_table_bytes(int64_t n);
+int rhip_hash_workspace_bytes(int64_t n, int32_t ncol, size_t *bytes);
+
+/*
+ * Deduplicate n coordinate rows into a hash table. Unique rows are numbered
+ * in first-occurrence order, exactly as the reference CPU map does:
+ *   unique_coords = coords[mapping],  coords == unique_coords[inverse].
+ * unique_coords needs room for n rows and mapping for n entries; only the
+ * first table->n_unique are written. inverse (n entries) may be NULL.
+ * Synchronises `stream` once to read n_unique.
+ *
+ * Replaces CoordinateMapGPU::insert_and_map (engine/grid/lattice_gpu.cu:157-243,
+ * insert_and_map_kernel :26-51, remap_inverse_map :54-71), with the semantics
+ * of CoordinateMapCPU::insert_and_map<true> (engine/grid/lattice_cpu.hpp:419-444).
+ */
+int rhip_hash_build(const int32_t *coords, int64_t n, int32_t ncol,
+                    void *slots, size_t slots_bytes, void *workspace,
+                    size_t workspace_bytes, int32_t *unique_coords,
+                    int64_t *mapping, int64_t *inverse, rhip_table *table,
+                    hipStream_t stream);
+
+/*
+ * result[i] = unique row index of queries[i] in the table, or -1.
+ * Replaces CoordinateMapGPU::find (engine/grid/lattice_gpu.cu:265-301), which
+ * returns only the hits; here misses are kept in place as -1.
+ */
+int rhip_hash_lookup(const rhip_table *table, const int32_t *queries,
+                     int64_t n, int32_t *result, hipStream_t stream);
+
+/*
+ * Locality order of a table's unique rows: order[j] is the row processed at
+ * position j (rows sorted by packed key, i.e. batch then x, y, z), pos is its
+ * inverse. Identity in RHIP_KEY_ROWREF mode. Used to tile output rows so a
+ * tile's neighbours cluster; it does not renumber rows.
+ */
+int rhip_order_workspace_bytes(int64_t n, size_t *bytes);
+int rhip_spatial_order(const rhip_table *table, int32_t *order, int32_t *pos,
+                       void *workspace, size_t workspace_bytes,
+                       hipStream_t stream);
+
+/*
+ * out = (b, floor(x_i / s_i) * s_i) for every row; s = out tensor stride
+ * (host array of ncol-1 positive values). Feed `out` to rhip_hash_build to
+ * get the strided coordinate map.
+ * Replaces stride_copy (engine/grid/lattice_gpu.cu:305-336) with the
+ * semantics of detail::stride_coordinate (engine/grid/stencil.hpp:35-52).
+ */
+int rhip_stride_coords(const int32_t *coords, int64_t n, int32_t ncol,
+                       const int32_t *out_tensor_stride, int32_t *out,
+                       hipStream_t stream);
+
+/* ------------------------------------------------------------ kernel map */
+
+int rhip_kmap_workspace_bytes(int64_t n_out, int32_t K, size_t *bytes);
+
+/*
+ * Phase 1 of kernel-map generation. For every output row (taken in
+ * out_order, may be NULL for identity) and every offset k, look up
+ * out_coords[row] + offsets[k] (batch unchanged) in in_table:
+ *   nbr[k * n_out + j] = input row of the neighbour of out_order[j], or -1.
+ * offsets is a device array [K, ncol-1] of already scaled lattice offsets
+ * (kernel_region::coordinate_at, engine/grid/stencil.hpp:223-278).
+ * Writes kmap_offsets (device, K+1 int64: CSR of pairs per offset) and
+ * copies it to kmap_offsets_host. Synchronises `stream` once.
+ * Replaces CoordinateMapGPU::kernel_map / direct_kernel_map / count_kernel
+ * (engine/grid/lattice_gpu.cu:1140-1362, 1366-1549); the live reference
+ * semantics are CoordinateMapCPU::kernel_map (engine/grid/lattice_cpu.hpp:606-673).
+ */
+int rhip_kmap_count(const rhip_table *in_table, const int32_t *out_coords,
+                    const int32_t *out_order, int64_t n_out, int32_t K,
+                    const int32_t *offsets, int32_t *nbr, void *workspace,
+                    size_t workspace_bytes, int64_t *kmap_offsets,
+                    int64_t *kmap_offsets_host, hipStream_t stream);
+
+/*
+ * Phase 2: emit the pairs of offset k at [kmap_offsets[k], kmap_offsets[k+1])
+ * of in_rows / out_rows, ordered by offset then by output position. The
+ * workspace must be the one phase 1 wrote. If nbr_t is not NULL it is filled
+ * as the transposed table over the input map: nbr_t[k * n_in + in_pos[i]] =
+ * output row paired with input row i under offset k, or -1 (in_pos may be
+ * NULL for identity). Replaces gpu_kernel_map::decompose
+ * (engine/grid/lattice_gpu.cuh:438-488); the set of pairs equals the
+ * reference's cpu_kernel_map.
+ */
+int rhip_kmap_fill(const int32_t *nbr, const int32_t *out_order, int64_t n_out,
+                   int32_t K, const void *workspace, size_t workspace_bytes,
+                   const int64_t *kmap_offsets, int32_t *in_rows,
+                   int32_t *out_rows, const int32_t *in_pos, int64_t n_in,
+                   int32_t *nbr_t, hipStream_t stream);
+
+/* ----------------------------------------------------------- convolution */
+
+int rhip_conv_workspace_bytes(int32_t K, int32_t cin, int32_t cout,
+                              int32_t dtype, size_t *bytes);
+
+/*
+ * Y[out_order[j]] = sum_k X[nbr[k*n_out+j]] @ W[k] (+ bias), fp32 accumulate.
+ * x [n_in, cin], weight [K, cin, cout], y [n_out, cout], all in `dtype`;
+ * bias is fp32 [cout] or NULL. Every output row is written.
+ * Replaces the per-offset index_select -> matmul -> index_add_ loop of
+ * evaluate_sparse_convolution (engine/nn/conv.cpp:47-64) and its bias add
+ * (conv.cpp:135-136).
+ */
+int rhip_conv_forward(const void *x, int64_t n_in, int32_t cin,
+                      const void *weight, int32_t K, int32_t cout,
+                      const float *bias, const int32_t *nbr,
+                      const int32_t *out_order, int64_t n_out, void *y,
+                      int32_t dtype, void *workspace, size_t workspace_bytes,
+                      hipStream_t stream);
+
+/*
+ * grad_x[in_order[j]] = sum_k grad_y[nbr_t[k*n_in+j]] @ W[k]^T.
+ * Replaces the autograd replay of IndexAddBackward/MmBackward/
+ * IndexSelectBackward for dX (engine/nn/conv.cpp:62-63).
+ */
+int rhip_conv_backward_input(const void *grad_y, int64_t n_out, int32_t cout,
+                             const void *weight, int32_t K, int32_t cin,
+                             const int32_t *nbr_t, const int32_t *in_order,
+                             int64_t n_in, void *grad_x, int32_t dtype,
+                             void *workspace, size_t workspace_bytes,
+                             hipStream_t stream);
+
+/*
+ * grad_w[k] = sum over pairs p of offset k of x[in_rows[p]]^T grad_y[out_rows[p]]
+ * with fp32 accumulation; grad_w [K, cin, cout] in `dtype` is overwritten.
+ * kmap_offsets is the device CSR from rhip_kmap_count.
+ * Replaces the dW half of MmBackward in the reference's autograd graph
+ * (engine/nn/conv.cpp:62) and sparse_convolution_backward_cpu_kernel's
+ * kernel_grad (engine/ops/convolution_cpu.hpp:55-89).
+ */
+int rhip_conv_backward_weight(const void *x, int64_t n_in, int32_t cin,
+                              const void *grad_y, int64_t n_out, int32_t cout,
+                              int32_t K, const int64_t *kmap_offsets,
+                              int64_t n_pairs, const int32_t *in_rows,
+                              const int32_t *out_rows, void *grad_w,
+                              int32_t dtype, void *workspace,
+                              size_t workspace_bytes, hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* RIEMANN_HIP_H */

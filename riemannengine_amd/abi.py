@@ -1,0 +1,330 @@
+"""ctypes binding of the C ABI in ``include/riemann_hip.h``.
+
+This is the thinnest possible host layer over ``libriemann_hip.so``: torch
+tensors provide device memory and the current HIP stream, every kernel runs
+through the C entry points. It is what the parity tests call, and it fails
+loudly (``RuntimeError``) when the library is missing; there is no CPU path.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from dataclasses import dataclass, field
+from typing import Optional
+
+import numpy as np
+import torch
+
+PKG = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(PKG, "libriemann_hip.so")
+MAX_COLS = 8
+
+F32, BF16 = 0, 1
+KEY_PACKED64, KEY_ROWREF = 0, 1
+
+# Every function the header declares (checked by the CPU test suite).
+EXPORTS = (
+    "rhip_last_error", "rhip_abi_version", "rhip_table_bytes",
+    "rhip_hash_workspace_bytes", "rhip_hash_build", "rhip_hash_lookup",
+    "rhip_order_workspace_bytes", "rhip_spatial_order", "rhip_stride_coords",
+    "rhip_kmap_workspace_bytes", "rhip_kmap_count", "rhip_kmap_fill",
+    "rhip_conv_workspace_bytes", "rhip_conv_forward",
+    "rhip_conv_backward_input", "rhip_conv_backward_weight",
+)
+
+
+class RhipTable(ctypes.Structure):
+    _fields_ = [
+        ("slots", ctypes.c_void_p), ("capacity", ctypes.c_int64),
+        ("rows", ctypes.c_void_p), ("n_unique", ctypes.c_int64),
+        ("ncol", ctypes.c_int32), ("mode", ctypes.c_int32),
+        ("key_bits", ctypes.c_int32),
+        ("lo", ctypes.c_int32 * MAX_COLS), ("hi", ctypes.c_int32 * MAX_COLS),
+        ("shift", ctypes.c_int32 * MAX_COLS),
+    ]
+
+
+_vp, _i64, _i32, _sz = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int32, ctypes.c_size_t
+_P = ctypes.POINTER
+
+
+def _declare(lib):
+    sig = {
+        "rhip_last_error": (ctypes.c_char_p, []),
+        "rhip_abi_version": (ctypes.c_int, []),
+        "rhip_table_bytes": (_sz, [_i64]),
+        "rhip_hash_workspace_bytes": (ctypes.c_int, [_i64, _i32, _P(_sz)]),
+        "rhip_hash_build": (ctypes.c_int, [_vp, _i64, _i32, _vp, _sz, _vp, _sz, _vp,
+                                           _vp, _vp, _P(RhipTable), _vp]),
+        "rhip_hash_lookup": (ctypes.c_int, [_P(RhipTable), _vp, _i64, _vp, _vp]),
+        "rhip_order_workspace_bytes": (ctypes.c_int, [_i64, _P(_sz)]),
+        "rhip_spatial_order": (ctypes.c_int, [_P(RhipTable), _vp, _vp, _vp, _sz, _vp]),
+        "rhip_stride_coords": (ctypes.c_int, [_vp, _i64, _i32, _P(_i32), _vp, _vp]),
+        "rhip_kmap_workspace_bytes": (ctypes.c_int, [_i64, _i32, _P(_sz)]),
+        "rhip_kmap_count": (ctypes.c_int, [_P(RhipTable), _vp, _vp, _i64, _i32, _vp,
+                                           _vp, _vp, _sz, _vp, _P(_i64), _vp]),
+        "rhip_kmap_fill": (ctypes.c_int, [_vp, _vp, _i64, _i32, _vp, _sz, _vp, _vp,
+                                          _vp, _vp, _i64, _vp, _vp]),
+        "rhip_conv_workspace_bytes": (ctypes.c_int, [_i32, _i32, _i32, _i32, _P(_sz)]),
+        "rhip_conv_forward": (ctypes.c_int, [_vp, _i64, _i32, _vp, _i32, _i32, _vp, _vp,
+                                             _vp, _i64, _vp, _i32, _vp, _sz, _vp]),
+        "rhip_conv_backward_input": (ctypes.c_int, [_vp, _i64, _i32, _vp, _i32, _i32,
+                                                    _vp, _vp, _i64, _vp, _i32, _vp,
+                                                    _sz, _vp]),
+        "rhip_conv_backward_weight": (ctypes.c_int, [_vp, _i64, _i32, _vp, _i64, _i32,
+                                                     _i32, _vp, _i64, _vp, _vp, _vp,
+                                                     _i32, _vp, _sz, _vp]),
+    }
+    for name, (res, args) in sig.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    return lib
+
+
+_LIB = None
+
+
+def lib():
+    """Load libriemann_hip.so (torch is imported first so both share one HIP
+    runtime: both libraries ask for the soname libamdhip64.so.7)."""
+    global _LIB
+    if _LIB is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(
+                f"{LIB_PATH} is missing: build it with `python -m riemannengine_amd.build hip`")
+        _LIB = _declare(ctypes.CDLL(LIB_PATH))
+    return _LIB
+
+
+def _check(status: int, what: str) -> None:
+    if status != 0:
+        msg = lib().rhip_last_error().decode(errors="replace")
+        raise RuntimeError(f"{what} failed (status {status}): {msg}")
+
+
+def _ptr(t: Optional[torch.Tensor]):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _stream(device: torch.device):
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def _require_cuda(t: torch.Tensor, name: str) -> None:
+    if not t.is_cuda:
+        raise RuntimeError(f"{name} must be a device tensor (the HIP path has no CPU fallback)")
+
+
+def _sizeq(fn, *args) -> int:
+    out = _sz(0)
+    _check(fn(*args, ctypes.byref(out)), fn.__name__)
+    return int(out.value)
+
+
+def _dtype_code(dt: torch.dtype) -> int:
+    if dt == torch.float32:
+        return F32
+    if dt == torch.bfloat16:
+        return BF16
+    raise RuntimeError(f"unsupported feature dtype {dt}; the HIP path computes fp32 or bf16")
+
+
+# ------------------------------------------------------------------ tables
+
+@dataclass
+class CoordTable:
+    """A built coordinate map: hash slots + unique rows + locality order."""
+    struct: RhipTable
+    slots: torch.Tensor
+    ucoords: torch.Tensor          # [n_unique, ncol] int32
+    mapping: torch.Tensor          # [n_unique] int64 first input row
+    inverse: Optional[torch.Tensor]  # [n] int64
+    order: torch.Tensor            # [n_unique] int32 processing order
+    pos: torch.Tensor              # [n_unique] int32 inverse of order
+    keep: list = field(default_factory=list)
+
+    @property
+    def n(self) -> int:
+        return int(self.struct.n_unique)
+
+    @property
+    def ncol(self) -> int:
+        return int(self.struct.ncol)
+
+    def lookup(self, queries: torch.Tensor) -> torch.Tensor:
+        queries = queries.to(torch.int32).contiguous()
+        _require_cuda(queries, "queries")
+        out = torch.empty(queries.shape[0], dtype=torch.int32, device=queries.device)
+        _check(lib().rhip_hash_lookup(ctypes.byref(self.struct), _ptr(queries),
+                                      queries.shape[0], _ptr(out), _stream(queries.device)),
+               "rhip_hash_lookup")
+        return out
+
+
+def hash_build(coords: torch.Tensor, with_inverse: bool = True,
+               with_order: bool = True) -> CoordTable:
+    """Deduplicate int32 rows [n, ncol] on the GPU (first occurrence wins)."""
+    _require_cuda(coords, "coords")
+    if coords.dtype != torch.int32 or coords.dim() != 2:
+        raise RuntimeError("coords must be a 2-D int32 tensor")
+    coords = coords.contiguous()
+    L, dev = lib(), coords.device
+    n, ncol = coords.shape
+    slots = torch.empty(int(L.rhip_table_bytes(n)), dtype=torch.uint8, device=dev)
+    ws = torch.empty(_sizeq(L.rhip_hash_workspace_bytes, n, ncol), dtype=torch.uint8, device=dev)
+    ucoords = torch.empty((max(n, 1), ncol), dtype=torch.int32, device=dev)
+    mapping = torch.empty(max(n, 1), dtype=torch.int64, device=dev)
+    inverse = torch.empty(max(n, 1), dtype=torch.int64, device=dev) if with_inverse else None
+    st = RhipTable()
+    _check(L.rhip_hash_build(_ptr(coords), n, ncol, _ptr(slots), slots.numel(), _ptr(ws),
+                             ws.numel(), _ptr(ucoords), _ptr(mapping), _ptr(inverse),
+                             ctypes.byref(st), _stream(dev)), "rhip_hash_build")
+    nu = int(st.n_unique)
+    order = torch.empty(max(nu, 1), dtype=torch.int32, device=dev)
+    pos = torch.empty(max(nu, 1), dtype=torch.int32, device=dev)
+    if with_order and nu > 0:
+        ows = torch.empty(_sizeq(L.rhip_order_workspace_bytes, nu), dtype=torch.uint8, device=dev)
+        _check(L.rhip_spatial_order(ctypes.byref(st), _ptr(order), _ptr(pos), _ptr(ows),
+                                    ows.numel(), _stream(dev)), "rhip_spatial_order")
+    elif nu > 0:
+        torch.arange(nu, out=order[:nu])
+        pos[:nu].copy_(order[:nu])
+    return CoordTable(st, slots, ucoords[:nu], mapping[:nu],
+                      inverse[:n] if inverse is not None else None, order[:nu], pos[:nu])
+
+
+def stride_coords(coords: torch.Tensor, out_tensor_stride) -> torch.Tensor:
+    """(b, floor(x/s)*s) per row on the GPU."""
+    _require_cuda(coords, "coords")
+    coords = coords.to(torch.int32).contiguous()
+    n, ncol = coords.shape
+    s = (ctypes.c_int32 * (ncol - 1))(*[int(v) for v in out_tensor_stride])
+    out = torch.empty_like(coords)
+    _check(lib().rhip_stride_coords(_ptr(coords), n, ncol, s, _ptr(out), _stream(coords.device)),
+           "rhip_stride_coords")
+    return out
+
+
+# ------------------------------------------------------------- kernel maps
+
+@dataclass
+class KernelMap:
+    """Per-offset (in, out) pairs plus the dense neighbour tables.
+
+    nbr[k, j]   : input row of output position j (output order) or -1
+    nbr_t[k, i] : output row of input position i (input order) or -1
+    offsets     : CSR over pairs, pairs of offset k at [offsets[k], offsets[k+1])
+    """
+    K: int
+    n_in: int
+    n_out: int
+    offsets: torch.Tensor        # device int64 [K+1]
+    offsets_host: np.ndarray     # int64 [K+1]
+    in_rows: torch.Tensor        # int32 [P]
+    out_rows: torch.Tensor       # int32 [P]
+    nbr: torch.Tensor            # int32 [K, n_out]
+    nbr_t: torch.Tensor          # int32 [K, n_in]
+    in_order: torch.Tensor
+    out_order: torch.Tensor
+
+    @property
+    def n_pairs(self) -> int:
+        return int(self.offsets_host[-1])
+
+    def swapped(self) -> "KernelMap":
+        """Transposed map: in and out exchanged, zero copy."""
+        return KernelMap(self.K, self.n_out, self.n_in, self.offsets, self.offsets_host,
+                         self.out_rows, self.in_rows, self.nbr_t, self.nbr,
+                         self.out_order, self.in_order)
+
+    def pairs(self, k: int):
+        a, b = int(self.offsets_host[k]), int(self.offsets_host[k + 1])
+        return self.in_rows[a:b], self.out_rows[a:b]
+
+
+def kernel_map(in_table: CoordTable, out_table: CoordTable, offsets: torch.Tensor) -> KernelMap:
+    """Pairs (in, out) with coord(in) = coord(out) + offsets[k] (batch kept)."""
+    L = lib()
+    dev = in_table.ucoords.device
+    offsets = offsets.to(device=dev, dtype=torch.int32).contiguous()
+    K = offsets.shape[0]
+    if offsets.dim() != 2 or offsets.shape[1] != in_table.ncol - 1:
+        raise RuntimeError("offsets must be [K, D]")
+    n_out, n_in = out_table.n, in_table.n
+    nbr = torch.empty((K, max(n_out, 1)), dtype=torch.int32, device=dev)
+    ws = torch.empty(_sizeq(L.rhip_kmap_workspace_bytes, n_out, K), dtype=torch.uint8, device=dev)
+    kofs = torch.empty(K + 1, dtype=torch.int64, device=dev)
+    kofs_host = np.zeros(K + 1, dtype=np.int64)
+    _check(L.rhip_kmap_count(ctypes.byref(in_table.struct), _ptr(out_table.ucoords),
+                             _ptr(out_table.order), n_out, K, _ptr(offsets), _ptr(nbr),
+                             _ptr(ws), ws.numel(), _ptr(kofs),
+                             kofs_host.ctypes.data_as(ctypes.POINTER(ctypes.c_int64)),
+                             _stream(dev)), "rhip_kmap_count")
+    P = int(kofs_host[-1])
+    in_rows = torch.empty(max(P, 1), dtype=torch.int32, device=dev)
+    out_rows = torch.empty(max(P, 1), dtype=torch.int32, device=dev)
+    nbr_t = torch.empty((K, max(n_in, 1)), dtype=torch.int32, device=dev)
+    _check(L.rhip_kmap_fill(_ptr(nbr), _ptr(out_table.order), n_out, K, _ptr(ws), ws.numel(),
+                            _ptr(kofs), _ptr(in_rows), _ptr(out_rows), _ptr(in_table.pos),
+                            n_in, _ptr(nbr_t), _stream(dev)), "rhip_kmap_fill")
+    return KernelMap(K, n_in, n_out, kofs, kofs_host, in_rows[:P], out_rows[:P],
+                     nbr[:, :n_out], nbr_t[:, :n_in], in_table.order, out_table.order)
+
+
+# ------------------------------------------------------------ convolution
+
+def _conv_ws(K, cin, cout, dtype, dev) -> torch.Tensor:
+    return torch.empty(_sizeq(lib().rhip_conv_workspace_bytes, K, cin, cout, dtype),
+                       dtype=torch.uint8, device=dev)
+
+
+def conv_forward(x: torch.Tensor, weight: torch.Tensor, kmap: KernelMap,
+                 bias: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Y[out] = sum_k X[in_k] @ W[k] (+ bias) through rhip_conv_forward."""
+    _require_cuda(x, "x")
+    dt = _dtype_code(x.dtype)
+    x = x.contiguous()
+    weight = weight.to(x.dtype).contiguous()
+    K, cin, cout = weight.shape
+    if K != kmap.K or x.shape[1] != cin or x.shape[0] != kmap.n_in:
+        raise RuntimeError("shape mismatch between features, weight and kernel map")
+    b = None if bias is None else bias.reshape(-1).to(torch.float32).contiguous()
+    y = torch.empty((kmap.n_out, cout), dtype=x.dtype, device=x.device)
+    ws = _conv_ws(K, cin, cout, dt, x.device)
+    _check(lib().rhip_conv_forward(_ptr(x), kmap.n_in, cin, _ptr(weight), K, cout, _ptr(b),
+                                   _ptr(kmap.nbr), _ptr(kmap.out_order), kmap.n_out, _ptr(y),
+                                   dt, _ptr(ws), ws.numel(), _stream(x.device)),
+           "rhip_conv_forward")
+    return y
+
+
+def conv_backward_input(grad_y: torch.Tensor, weight: torch.Tensor, kmap: KernelMap) -> torch.Tensor:
+    _require_cuda(grad_y, "grad_y")
+    dt = _dtype_code(grad_y.dtype)
+    grad_y = grad_y.contiguous()
+    weight = weight.to(grad_y.dtype).contiguous()
+    K, cin, cout = weight.shape
+    gx = torch.empty((kmap.n_in, cin), dtype=grad_y.dtype, device=grad_y.device)
+    ws = _conv_ws(K, cin, cout, dt, grad_y.device)
+    _check(lib().rhip_conv_backward_input(_ptr(grad_y), kmap.n_out, cout, _ptr(weight), K, cin,
+                                          _ptr(kmap.nbr_t), _ptr(kmap.in_order), kmap.n_in,
+                                          _ptr(gx), dt, _ptr(ws), ws.numel(),
+                                          _stream(grad_y.device)), "rhip_conv_backward_input")
+    return gx
+
+
+def conv_backward_weight(x: torch.Tensor, grad_y: torch.Tensor, kmap: KernelMap,
+                         K: int, out_dtype: Optional[torch.dtype] = None) -> torch.Tensor:
+    _require_cuda(x, "x")
+    dt = _dtype_code(x.dtype)
+    x, grad_y = x.contiguous(), grad_y.to(x.dtype).contiguous()
+    cin, cout = x.shape[1], grad_y.shape[1]
+    gw = torch.empty((K, cin, cout), dtype=x.dtype, device=x.device)
+    ws = _conv_ws(K, cin, cout, dt, x.device)
+    _check(lib().rhip_conv_backward_weight(_ptr(x), kmap.n_in, cin, _ptr(grad_y), kmap.n_out,
+                                           cout, K, _ptr(kmap.offsets), kmap.n_pairs,
+                                           _ptr(kmap.in_rows), _ptr(kmap.out_rows), _ptr(gw),
+                                           dt, _ptr(ws), ws.numel(), _stream(x.device)),
+           "rhip_conv_backward_weight")
+    return gw if out_dtype is None else gw.to(out_dtype)

@@ -1,0 +1,525 @@
+// Coordinate hashing for gfx950: dedup of int32 coordinate rows into an
+// open-addressing table with 16-byte slots and linear probing.
+//
+// Semantics follow CoordinateMapCPU::insert_and_map<true>
+// (RiemannEngine/engine/grid/lattice_cpu.hpp:419-444): unique rows are
+// numbered by first occurrence, mapping[u] is the first input row of unique
+// row u and inverse[r] the unique row of input row r. The GPU design differs
+// from the reference's cuDF map (which CASes a pointer to the row and keeps
+// the race winner, engine/grid/lattice_gpu.cu:26-51): keys are packed into
+// one integer from the set's own column ranges, the first occurrence wins by
+// atomicMin on the row index, and the unique numbering is a prefix sum over
+// "is first" flags in row order, so the result is deterministic.
+#include <hipcub/hipcub.hpp>
+
+#include <algorithm>
+#include <climits>
+#include <cstring>
+
+#include "rhip_internal.hpp"
+
+namespace rhip {
+
+constexpr int kBlock = 256;
+
+__global__ void minmax_init_kernel(int32_t *mm, int ncol) {
+  int c = threadIdx.x;
+  if (c < ncol) {
+    mm[c] = INT_MAX;
+    mm[ncol + c] = INT_MIN;
+  }
+}
+
+// Column-wise min/max of coords [n, ncol]; block-reduced in LDS then merged
+// with global atomics.
+__global__ __launch_bounds__(kBlock) void minmax_kernel(const int32_t *coords,
+                                                        int64_t n, int ncol,
+                                                        int32_t *mm) {
+  __shared__ int32_t smin[RHIP_MAX_COLS], smax[RHIP_MAX_COLS];
+  if (threadIdx.x < RHIP_MAX_COLS) {
+    smin[threadIdx.x] = INT_MAX;
+    smax[threadIdx.x] = INT_MIN;
+  }
+  __syncthreads();
+  int32_t lmin[RHIP_MAX_COLS], lmax[RHIP_MAX_COLS];
+#pragma unroll
+  for (int c = 0; c < RHIP_MAX_COLS; ++c) {
+    lmin[c] = INT_MAX;
+    lmax[c] = INT_MIN;
+  }
+  for (int64_t r = blockIdx.x * (int64_t)kBlock + threadIdx.x; r < n;
+       r += (int64_t)gridDim.x * kBlock) {
+    const int32_t *row = coords + r * ncol;
+#pragma unroll
+    for (int c = 0; c < RHIP_MAX_COLS; ++c) {
+      if (c < ncol) {
+        int32_t v = row[c];
+        lmin[c] = min(lmin[c], v);
+        lmax[c] = max(lmax[c], v);
+      }
+    }
+  }
+#pragma unroll
+  for (int c = 0; c < RHIP_MAX_COLS; ++c) {
+    if (c < ncol) {
+      int32_t a = lmin[c], b = lmax[c];
+      for (int off = 32; off > 0; off >>= 1) {
+        a = min(a, __shfl_xor(a, off));
+        b = max(b, __shfl_xor(b, off));
+      }
+      if (lane_id() == 0) {
+        atomicMin(&smin[c], a);
+        atomicMax(&smax[c], b);
+      }
+    }
+  }
+  __syncthreads();
+  if (threadIdx.x < ncol) {
+    atomicMin(&mm[threadIdx.x], smin[threadIdx.x]);
+    atomicMax(&mm[ncol + threadIdx.x], smax[threadIdx.x]);
+  }
+}
+
+__global__ __launch_bounds__(kBlock) void slots_init_kernel(Slot *slots,
+                                                            int64_t cap) {
+  int64_t i = blockIdx.x * (int64_t)kBlock + threadIdx.x;
+  if (i < cap) {
+    Slot s;
+    s.word = kEmptyWord;
+    s.first_row = 0xffffffffu;
+    s.uid = 0xffffffffu;
+    slots[i] = s;
+  }
+}
+
+// One lane per input row: claim or find the row's slot, then lower the
+// slot's first_row to this row if it is earlier.
+__global__ __launch_bounds__(kBlock) void insert_kernel(const int32_t *coords,
+                                                        int64_t n,
+                                                        TableView t,
+                                                        uint32_t *slot_of_row) {
+  int64_t r = blockIdx.x * (int64_t)kBlock + threadIdx.x;
+  if (r >= n)
+    return;
+  int32_t c[RHIP_MAX_COLS];
+#pragma unroll
+  for (int i = 0; i < RHIP_MAX_COLS; ++i)
+    c[i] = i < t.ncol ? coords[r * t.ncol + i] : 0;
+
+  uint64_t key, h;
+  uint32_t hr = 0;
+  if (t.mode == RHIP_KEY_PACKED64) {
+    pack_row(t, c, key); // always in range: the bounds come from this set
+    h = mix64(key) & t.mask;
+  } else {
+    hr = hash_row(c, t.ncol);
+    key = (static_cast<uint64_t>(hr) << 32) | static_cast<uint32_t>(r);
+    h = mix64(hr) & t.mask;
+  }
+  while (true) {
+    uint64_t *wp = &t.slots[h].word;
+    uint64_t w = __hip_atomic_load(wp, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (w == kEmptyWord) {
+      uint64_t prev = atomicCAS(reinterpret_cast<unsigned long long *>(wp),
+                                kEmptyWord, key);
+      if (prev == kEmptyWord)
+        break; // claimed
+      w = prev;
+    }
+    bool same;
+    if (t.mode == RHIP_KEY_PACKED64) {
+      same = (w == key);
+    } else {
+      same = static_cast<uint32_t>(w >> 32) == hr &&
+             rows_equal(coords + static_cast<int64_t>(static_cast<uint32_t>(w)) *
+                                     t.ncol,
+                        c, t.ncol);
+    }
+    if (same)
+      break;
+    h = (h + 1) & t.mask;
+  }
+  atomicMin(&t.slots[h].first_row, static_cast<uint32_t>(r));
+  slot_of_row[r] = static_cast<uint32_t>(h);
+}
+
+// Per-block count of rows that are the first occurrence of their key.
+__global__ __launch_bounds__(kBlock) void count_first_kernel(
+    int64_t n, const Slot *slots, const uint32_t *slot_of_row,
+    int32_t *block_counts) {
+  __shared__ int32_t wave_counts[kBlock / kWave];
+  int64_t r = blockIdx.x * (int64_t)kBlock + threadIdx.x;
+  bool first = r < n && slots[slot_of_row[r]].first_row == static_cast<uint32_t>(r);
+  uint64_t b = __ballot(first);
+  if (lane_id() == 0)
+    wave_counts[threadIdx.x / kWave] = __popcll(b);
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int32_t s = 0;
+    for (int w = 0; w < kBlock / kWave; ++w)
+      s += wave_counts[w];
+    block_counts[blockIdx.x] = s;
+  }
+}
+
+// First rows get uid = block base + rank within the block; they also write
+// mapping[uid] and the unique coordinates.
+__global__ __launch_bounds__(kBlock) void assign_uid_kernel(
+    const int32_t *coords, int64_t n, int ncol, const Slot *slots,
+    const uint32_t *slot_of_row, const int64_t *block_base, int32_t *uid_by_row,
+    int64_t *mapping, int32_t *unique_coords) {
+  __shared__ int32_t wave_counts[kBlock / kWave];
+  int64_t r = blockIdx.x * (int64_t)kBlock + threadIdx.x;
+  bool first = r < n && slots[slot_of_row[r]].first_row == static_cast<uint32_t>(r);
+  uint64_t b = __ballot(first);
+  const int w = threadIdx.x / kWave;
+  if (lane_id() == 0)
+    wave_counts[w] = __popcll(b);
+  __syncthreads();
+  int32_t before = 0;
+  for (int i = 0; i < w; ++i)
+    before += wave_counts[i];
+  if (first) {
+    int64_t uid = block_base[blockIdx.x] + before + lanes_below(b);
+    uid_by_row[r] = static_cast<int32_t>(uid);
+    mapping[uid] = r;
+    for (int c = 0; c < ncol; ++c)
+      unique_coords[uid * ncol + c] = coords[r * ncol + c];
+  }
+}
+
+// inverse[r] = uid of r's first occurrence; first rows publish their uid in
+// the slot (and, in row-reference mode, re-point the key at the unique row).
+__global__ __launch_bounds__(kBlock) void resolve_kernel(
+    const int32_t *coords, int64_t n, TableView t, const uint32_t *slot_of_row,
+    const int32_t *uid_by_row, int64_t *inverse) {
+  int64_t r = blockIdx.x * (int64_t)kBlock + threadIdx.x;
+  if (r >= n)
+    return;
+  uint32_t h = slot_of_row[r];
+  uint32_t fr = t.slots[h].first_row;
+  int32_t uid = uid_by_row[fr];
+  if (inverse)
+    inverse[r] = uid;
+  if (fr == static_cast<uint32_t>(r)) {
+    t.slots[h].uid = static_cast<uint32_t>(uid);
+    if (t.mode == RHIP_KEY_ROWREF) {
+      uint32_t hr = static_cast<uint32_t>(t.slots[h].word >> 32);
+      t.slots[h].word = (static_cast<uint64_t>(hr) << 32) | static_cast<uint32_t>(uid);
+    }
+  }
+}
+
+__global__ __launch_bounds__(kBlock) void lookup_kernel(TableView t,
+                                                        const int32_t *queries,
+                                                        int64_t n,
+                                                        int32_t *result) {
+  int64_t i = blockIdx.x * (int64_t)kBlock + threadIdx.x;
+  if (i >= n)
+    return;
+  int32_t c[RHIP_MAX_COLS];
+#pragma unroll
+  for (int j = 0; j < RHIP_MAX_COLS; ++j)
+    c[j] = j < t.ncol ? queries[i * t.ncol + j] : 0;
+  result[i] = table_find(t, c);
+}
+
+__global__ __launch_bounds__(kBlock) void pack_keys_kernel(TableView t,
+                                                           int64_t n,
+                                                           uint64_t *keys,
+                                                           int32_t *rows) {
+  int64_t i = blockIdx.x * (int64_t)kBlock + threadIdx.x;
+  if (i >= n)
+    return;
+  int32_t c[RHIP_MAX_COLS];
+#pragma unroll
+  for (int j = 0; j < RHIP_MAX_COLS; ++j)
+    c[j] = j < t.ncol ? t.rows[i * t.ncol + j] : 0;
+  uint64_t key = 0;
+  pack_row(t, c, key);
+  keys[i] = key;
+  rows[i] = static_cast<int32_t>(i);
+}
+
+__global__ __launch_bounds__(kBlock) void iota_kernel(int64_t n, int32_t *order,
+                                                      int32_t *pos) {
+  int64_t i = blockIdx.x * (int64_t)kBlock + threadIdx.x;
+  if (i < n) {
+    order[i] = static_cast<int32_t>(i);
+    if (pos)
+      pos[i] = static_cast<int32_t>(i);
+  }
+}
+
+__global__ __launch_bounds__(kBlock) void invert_perm_kernel(int64_t n,
+                                                             const int32_t *order,
+                                                             int32_t *pos) {
+  int64_t i = blockIdx.x * (int64_t)kBlock + threadIdx.x;
+  if (i < n)
+    pos[order[i]] = static_cast<int32_t>(i);
+}
+
+// floor(a / s) * s for s > 0, exact in integers.
+__device__ __forceinline__ int32_t floor_align(int32_t a, int32_t s) {
+  int32_t q = a / s;
+  if ((a % s) != 0 && a < 0)
+    --q;
+  return q * s;
+}
+
+struct StrideArg {
+  int32_t s[RHIP_MAX_COLS];
+};
+
+__global__ __launch_bounds__(kBlock) void stride_kernel(const int32_t *in,
+                                                        int64_t n, int ncol,
+                                                        StrideArg st,
+                                                        int32_t *out) {
+  int64_t i = blockIdx.x * (int64_t)kBlock + threadIdx.x;
+  if (i >= n * ncol)
+    return;
+  int c = static_cast<int>(i % ncol);
+  int32_t v = in[i];
+  out[i] = c == 0 ? v : floor_align(v, st.s[c - 1]);
+}
+
+// ------------------------------------------------------------------ host
+
+static int64_t table_capacity(int64_t n) {
+  int64_t cap = 64;
+  while (cap < 2 * n)
+    cap <<= 1;
+  return cap;
+}
+
+struct HashWs {
+  int32_t *minmax;
+  uint32_t *slot_of_row;
+  int32_t *uid_by_row;
+  int32_t *block_counts;
+  int64_t *block_base;
+  int64_t *total;
+};
+
+static HashWs carve_hash(Carve &cv, int64_t n, int ncol) {
+  HashWs w;
+  const int64_t nb = std::max<int64_t>(1, ceil_div(n, kBlock));
+  w.minmax = cv.take<int32_t>(2 * RHIP_MAX_COLS);
+  w.slot_of_row = cv.take<uint32_t>(std::max<int64_t>(n, 1));
+  w.uid_by_row = cv.take<int32_t>(std::max<int64_t>(n, 1));
+  w.block_counts = cv.take<int32_t>(nb);
+  w.block_base = cv.take<int64_t>(nb);
+  w.total = cv.take<int64_t>(1);
+  (void)ncol;
+  return w;
+}
+
+static int bit_width_u32(uint32_t v) { return v == 0 ? 0 : 32 - __builtin_clz(v); }
+
+} // namespace rhip
+
+using namespace rhip;
+
+extern "C" size_t rhip_table_bytes(int64_t n) {
+  return static_cast<size_t>(table_capacity(n < 0 ? 0 : n)) * sizeof(Slot);
+}
+
+extern "C" int rhip_hash_workspace_bytes(int64_t n, int32_t ncol,
+                                         size_t *bytes) {
+  return guarded([&] {
+    RHIP_CHECK_ARG(bytes != nullptr, "bytes is null");
+    RHIP_CHECK_ARG(n >= 0, "n must be >= 0");
+    Carve cv(nullptr, 0);
+    carve_hash(cv, n, ncol);
+    *bytes = cv.used + 256;
+  });
+}
+
+extern "C" int rhip_hash_build(const int32_t *coords, int64_t n, int32_t ncol,
+                               void *slots, size_t slots_bytes, void *workspace,
+                               size_t workspace_bytes, int32_t *unique_coords,
+                               int64_t *mapping, int64_t *inverse,
+                               rhip_table *table, hipStream_t stream) {
+  return guarded([&] {
+    RHIP_CHECK_ARG(table != nullptr, "table is null");
+    RHIP_CHECK_ARG(n >= 0 && n < INT32_MAX, "row count must be in [0, 2^31)");
+    RHIP_CHECK_ARG(ncol >= 2 && ncol <= RHIP_MAX_COLS,
+                   "ncol must be in [2, " + std::to_string(RHIP_MAX_COLS) + "]");
+    RHIP_CHECK_ARG(slots != nullptr, "slots is null");
+    RHIP_CHECK_ARG(n == 0 || (coords && unique_coords && mapping),
+                   "coords/unique_coords/mapping must be non-null");
+    const int64_t cap = table_capacity(n);
+    RHIP_CHECK_ARG(slots_bytes >= static_cast<size_t>(cap) * sizeof(Slot),
+                   "slots buffer smaller than rhip_table_bytes(n)");
+    Carve cv(workspace, workspace_bytes);
+    RHIP_CHECK_ARG(workspace != nullptr, "workspace is null");
+    HashWs w = carve_hash(cv, n, ncol);
+
+    std::memset(table, 0, sizeof(*table));
+    table->slots = slots;
+    table->capacity = cap;
+    table->rows = unique_coords;
+    table->ncol = ncol;
+    Slot *sl = static_cast<Slot *>(slots);
+    hipLaunchKernelGGL(slots_init_kernel, dim3(ceil_div(cap, kBlock)),
+                       dim3(kBlock), 0, stream, sl, cap);
+    RHIP_LAUNCH_CHECK();
+    if (n == 0) {
+      table->mode = RHIP_KEY_PACKED64;
+      table->n_unique = 0;
+      for (int c = 0; c < ncol; ++c)
+        table->hi[c] = -1; // empty range: every probe misses on span check
+      return;
+    }
+
+    // Column bounds -> packing layout (batch column in the top bits so the
+    // packed order is batch-major lexicographic).
+    hipLaunchKernelGGL(minmax_init_kernel, dim3(1), dim3(RHIP_MAX_COLS), 0,
+                       stream, w.minmax, ncol);
+    const int64_t nb = ceil_div(n, kBlock);
+    hipLaunchKernelGGL(minmax_kernel, dim3(std::min<int64_t>(nb, 1024)),
+                       dim3(kBlock), 0, stream, coords, n, ncol, w.minmax);
+    RHIP_LAUNCH_CHECK();
+    int32_t mm[2 * RHIP_MAX_COLS];
+    RHIP_HIP(hipMemcpyAsync(mm, w.minmax, sizeof(int32_t) * 2 * ncol,
+                            hipMemcpyDeviceToHost, stream));
+    RHIP_HIP(hipStreamSynchronize(stream));
+    int total_bits = 0;
+    int bits[RHIP_MAX_COLS];
+    for (int c = 0; c < ncol; ++c) {
+      table->lo[c] = mm[c];
+      table->hi[c] = mm[ncol + c];
+      bits[c] = bit_width_u32(static_cast<uint32_t>(
+          static_cast<int64_t>(mm[ncol + c]) - mm[c]));
+      total_bits += bits[c];
+    }
+    int sh = 0;
+    for (int c = ncol - 1; c >= 0; --c) {
+      table->shift[c] = total_bits <= 63 ? sh : 0;
+      sh += bits[c];
+    }
+    table->mode = total_bits <= 63 ? RHIP_KEY_PACKED64 : RHIP_KEY_ROWREF;
+    table->key_bits = total_bits <= 63 ? total_bits : 0;
+
+    // The row-reference build probes the caller's coordinates; lookups after
+    // the build probe unique_coords (resolve_kernel re-points the slots).
+    TableView tv = make_view(*table);
+    tv.rows = coords;
+    hipLaunchKernelGGL(insert_kernel, dim3(nb), dim3(kBlock), 0, stream, coords,
+                       n, tv, w.slot_of_row);
+    RHIP_LAUNCH_CHECK();
+    hipLaunchKernelGGL(count_first_kernel, dim3(nb), dim3(kBlock), 0, stream, n,
+                       sl, w.slot_of_row, w.block_counts);
+    RHIP_LAUNCH_CHECK();
+    hipLaunchKernelGGL(scan_counts_kernel<0>, dim3(1), dim3(1024), 0, stream,
+                       w.block_counts, nb, w.block_base, w.total);
+    RHIP_LAUNCH_CHECK();
+    hipLaunchKernelGGL(assign_uid_kernel, dim3(nb), dim3(kBlock), 0, stream,
+                       coords, n, ncol, sl, w.slot_of_row, w.block_base,
+                       w.uid_by_row, mapping, unique_coords);
+    RHIP_LAUNCH_CHECK();
+    hipLaunchKernelGGL(resolve_kernel, dim3(nb), dim3(kBlock), 0, stream,
+                       coords, n, tv, w.slot_of_row, w.uid_by_row, inverse);
+    RHIP_LAUNCH_CHECK();
+    int64_t nu = 0;
+    RHIP_HIP(hipMemcpyAsync(&nu, w.total, sizeof(int64_t),
+                            hipMemcpyDeviceToHost, stream));
+    RHIP_HIP(hipStreamSynchronize(stream));
+    table->n_unique = nu;
+  });
+}
+
+extern "C" int rhip_hash_lookup(const rhip_table *table, const int32_t *queries,
+                                int64_t n, int32_t *result, hipStream_t stream) {
+  return guarded([&] {
+    RHIP_CHECK_ARG(table != nullptr, "table is null");
+    RHIP_CHECK_ARG(n >= 0, "n must be >= 0");
+    if (n == 0)
+      return;
+    RHIP_CHECK_ARG(queries && result, "queries/result must be non-null");
+    hipLaunchKernelGGL(lookup_kernel, dim3(ceil_div(n, kBlock)), dim3(kBlock), 0,
+                       stream, make_view(*table), queries, n, result);
+    RHIP_LAUNCH_CHECK();
+  });
+}
+
+static size_t radix_temp_bytes(int64_t n) {
+  size_t temp = 0;
+  (void)hipcub::DeviceRadixSort::SortPairs(nullptr, temp, (uint64_t *)nullptr,
+                                     (uint64_t *)nullptr, (int32_t *)nullptr,
+                                     (int32_t *)nullptr, static_cast<int>(n), 0,
+                                     64, (hipStream_t)0);
+  return temp;
+}
+
+extern "C" int rhip_order_workspace_bytes(int64_t n, size_t *bytes) {
+  return guarded([&] {
+    RHIP_CHECK_ARG(bytes != nullptr, "bytes is null");
+    Carve cv(nullptr, 0);
+    const int64_t m = std::max<int64_t>(n, 1);
+    cv.take<uint64_t>(m);
+    cv.take<uint64_t>(m);
+    cv.take<int32_t>(m);
+    cv.take<char>(radix_temp_bytes(m));
+    *bytes = cv.used + 256;
+  });
+}
+
+extern "C" int rhip_spatial_order(const rhip_table *table, int32_t *order,
+                                  int32_t *pos, void *workspace,
+                                  size_t workspace_bytes, hipStream_t stream) {
+  return guarded([&] {
+    RHIP_CHECK_ARG(table != nullptr, "table is null");
+    const int64_t n = table->n_unique;
+    if (n == 0)
+      return;
+    RHIP_CHECK_ARG(order != nullptr, "order is null");
+    const int64_t nb = ceil_div(n, kBlock);
+    if (table->mode != RHIP_KEY_PACKED64 || table->key_bits == 0) {
+      hipLaunchKernelGGL(iota_kernel, dim3(nb), dim3(kBlock), 0, stream, n,
+                         order, pos);
+      RHIP_LAUNCH_CHECK();
+      return;
+    }
+    RHIP_CHECK_ARG(workspace != nullptr, "workspace is null");
+    Carve cv(workspace, workspace_bytes);
+    uint64_t *keys_in = cv.take<uint64_t>(n);
+    uint64_t *keys_out = cv.take<uint64_t>(n);
+    int32_t *rows_in = cv.take<int32_t>(n);
+    size_t temp = radix_temp_bytes(n);
+    void *tmp = cv.take<char>(temp);
+    hipLaunchKernelGGL(pack_keys_kernel, dim3(nb), dim3(kBlock), 0, stream,
+                       make_view(*table), n, keys_in, rows_in);
+    RHIP_LAUNCH_CHECK();
+    RHIP_HIP(hipcub::DeviceRadixSort::SortPairs(
+        tmp, temp, keys_in, keys_out, rows_in, order, static_cast<int>(n), 0,
+        table->key_bits, stream));
+    if (pos) {
+      hipLaunchKernelGGL(invert_perm_kernel, dim3(nb), dim3(kBlock), 0, stream,
+                         n, order, pos);
+      RHIP_LAUNCH_CHECK();
+    }
+  });
+}
+
+extern "C" int rhip_stride_coords(const int32_t *coords, int64_t n,
+                                  int32_t ncol,
+                                  const int32_t *out_tensor_stride,
+                                  int32_t *out, hipStream_t stream) {
+  return guarded([&] {
+    RHIP_CHECK_ARG(ncol >= 2 && ncol <= RHIP_MAX_COLS, "bad ncol");
+    RHIP_CHECK_ARG(out_tensor_stride != nullptr, "stride is null");
+    StrideArg st{};
+    for (int c = 0; c < ncol - 1; ++c) {
+      RHIP_CHECK_ARG(out_tensor_stride[c] > 0, "stride must be positive");
+      st.s[c] = out_tensor_stride[c];
+    }
+    if (n == 0)
+      return;
+    RHIP_CHECK_ARG(coords && out, "coords/out must be non-null");
+    const int64_t total = n * ncol;
+    hipLaunchKernelGGL(stride_kernel, dim3(ceil_div(total, kBlock)),
+                       dim3(kBlock), 0, stream, coords, n, ncol, st, out);
+    RHIP_LAUNCH_CHECK();
+  });
+}

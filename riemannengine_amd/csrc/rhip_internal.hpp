@@ -1,0 +1,235 @@
+// Internal helpers shared by the HIP translation units of libriemann_hip.
+// gfx950 only: wave64, 64-lane ballots, 16-byte global loads.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <stdexcept>
+#include <string>
+
+#include "riemann_hip.h"
+
+namespace rhip {
+
+constexpr int kWave = 64;
+constexpr uint64_t kEmptyWord = ~0ull;
+
+// One hash slot: the key word (packed coordinates, or hash<<32 | unique row
+// in row-reference mode), the first input row that inserted it (atomicMin
+// target during the build) and the unique row index lookups return.
+struct alignas(16) Slot {
+  uint64_t word;
+  uint32_t first_row;
+  uint32_t uid;
+};
+static_assert(sizeof(Slot) == 16, "slot must stay 16 bytes");
+
+// Error plumbing: entry points catch rhip::Error and return its status with
+// the message stored for rhip_last_error().
+struct Error : std::runtime_error {
+  int status;
+  Error(int s, const std::string &m) : std::runtime_error(m), status(s) {}
+};
+
+void set_last_error(const std::string &msg);
+
+#define RHIP_CHECK_ARG(cond, msg)                                              \
+  do {                                                                         \
+    if (!(cond))                                                               \
+      throw ::rhip::Error(RHIP_ERR_INVALID, std::string(__func__) + ": " + msg); \
+  } while (0)
+
+#define RHIP_HIP(call)                                                         \
+  do {                                                                         \
+    hipError_t e_ = (call);                                                    \
+    if (e_ != hipSuccess)                                                      \
+      throw ::rhip::Error(RHIP_ERR_HIP, std::string(#call) + " failed: " +     \
+                                            hipGetErrorString(e_));            \
+  } while (0)
+
+#define RHIP_LAUNCH_CHECK() RHIP_HIP(hipGetLastError())
+
+// Runs `body` and converts exceptions into a status code.
+template <typename F> int guarded(F &&body) {
+  try {
+    body();
+    return RHIP_OK;
+  } catch (const Error &e) {
+    set_last_error(e.what());
+    return e.status;
+  } catch (const std::exception &e) {
+    set_last_error(e.what());
+    return RHIP_ERR_HIP;
+  }
+}
+
+inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+// Bump allocator over a caller workspace (256-byte aligned pieces).
+struct Carve {
+  char *base;
+  size_t used = 0, cap;
+  Carve(void *p, size_t c) : base(static_cast<char *>(p)), cap(c) {}
+  template <typename T> T *take(size_t count) {
+    size_t off = align_up(used, 256);
+    size_t need = off + count * sizeof(T);
+    if (base != nullptr && need > cap)
+      throw Error(RHIP_ERR_WORKSPACE, "workspace too small: need " +
+                                          std::to_string(need) + " bytes, have " +
+                                          std::to_string(cap));
+    used = need;
+    return base ? reinterpret_cast<T *>(base + off) : nullptr;
+  }
+};
+
+// ---------------------------------------------------------------- device
+
+// MurmurHash3 64-bit finalizer (Appleby, public domain) as the slot mixer.
+__device__ __forceinline__ uint64_t mix64(uint64_t k) {
+  k ^= k >> 33;
+  k *= 0xff51afd7ed558ccdull;
+  k ^= k >> 33;
+  k *= 0xc4ceb9fe1a85ec53ull;
+  k ^= k >> 33;
+  return k;
+}
+
+// Table parameters passed by value to kernels.
+struct TableView {
+  Slot *slots;
+  uint64_t mask;
+  const int32_t *rows; // unique coordinates (row-reference mode probes these)
+  int32_t ncol;
+  int32_t mode;
+  int32_t lo[RHIP_MAX_COLS];
+  uint32_t span[RHIP_MAX_COLS]; // hi - lo
+  int32_t shift[RHIP_MAX_COLS];
+};
+
+inline TableView make_view(const rhip_table &t) {
+  TableView v{};
+  v.slots = static_cast<Slot *>(t.slots);
+  v.mask = static_cast<uint64_t>(t.capacity) - 1;
+  v.rows = t.rows;
+  v.ncol = t.ncol;
+  v.mode = t.mode;
+  for (int c = 0; c < RHIP_MAX_COLS; ++c) {
+    v.lo[c] = t.lo[c];
+    v.span[c] = static_cast<uint32_t>(static_cast<int64_t>(t.hi[c]) - t.lo[c]);
+    v.shift[c] = t.shift[c];
+  }
+  return v;
+}
+
+// Pack a row into its 63-bit key; false when a column leaves [lo, hi]
+// (such a row cannot be in the table).
+__device__ __forceinline__ bool pack_row(const TableView &t, const int32_t *c,
+                                         uint64_t &key) {
+  uint64_t k = 0;
+#pragma unroll
+  for (int i = 0; i < RHIP_MAX_COLS; ++i) {
+    if (i < t.ncol) {
+      uint32_t d = static_cast<uint32_t>(c[i]) - static_cast<uint32_t>(t.lo[i]);
+      if (d > t.span[i])
+        return false;
+      k |= static_cast<uint64_t>(d) << t.shift[i];
+    }
+  }
+  key = k;
+  return true;
+}
+
+// 32-bit row hash for row-reference mode.
+__device__ __forceinline__ uint32_t hash_row(const int32_t *c, int ncol) {
+  uint64_t h = 0x9e3779b97f4a7c15ull;
+  for (int i = 0; i < ncol; ++i)
+    h = mix64(h ^ static_cast<uint32_t>(c[i]));
+  return static_cast<uint32_t>(h >> 32);
+}
+
+__device__ __forceinline__ bool rows_equal(const int32_t *a, const int32_t *b,
+                                           int ncol) {
+  for (int i = 0; i < ncol; ++i)
+    if (a[i] != b[i])
+      return false;
+  return true;
+}
+
+// Probe for a row (coordinates in registers/array `c`); returns its unique
+// index or -1.
+__device__ __forceinline__ int32_t table_find(const TableView &t,
+                                              const int32_t *c) {
+  if (t.mode == RHIP_KEY_PACKED64) {
+    uint64_t key;
+    if (!pack_row(t, c, key))
+      return -1;
+    uint64_t h = mix64(key) & t.mask;
+    while (true) {
+      Slot s = t.slots[h];
+      if (s.word == key)
+        return static_cast<int32_t>(s.uid);
+      if (s.word == kEmptyWord)
+        return -1;
+      h = (h + 1) & t.mask;
+    }
+  } else {
+    uint32_t hr = hash_row(c, t.ncol);
+    uint64_t h = mix64(hr) & t.mask;
+    while (true) {
+      Slot s = t.slots[h];
+      if (s.word == kEmptyWord)
+        return -1;
+      if (static_cast<uint32_t>(s.word >> 32) == hr) {
+        uint32_t u = static_cast<uint32_t>(s.word);
+        if (rows_equal(t.rows + static_cast<int64_t>(u) * t.ncol, c, t.ncol))
+          return static_cast<int32_t>(u);
+      }
+      h = (h + 1) & t.mask;
+    }
+  }
+}
+
+// Lane index within the wave and wave-level prefix of a predicate.
+__device__ __forceinline__ int lane_id() { return __lane_id(); }
+
+__device__ __forceinline__ uint32_t lanes_below(uint64_t mask) {
+  return __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(mask >> 32),
+                                   __builtin_amdgcn_mbcnt_lo(
+                                       static_cast<uint32_t>(mask), 0u));
+}
+
+// Exclusive scan of m int32 counts in one workgroup of 1024 lanes; each lane
+// owns a contiguous run. base[i] = sum(counts[0..i)), *total = sum(counts).
+template <int Dummy = 0>
+__global__ __launch_bounds__(1024) void scan_counts_kernel(const int32_t *counts,
+                                                           int64_t m,
+                                                           int64_t *base,
+                                                           int64_t *total) {
+  __shared__ int64_t partial[1024];
+  const int t = threadIdx.x;
+  const int64_t per = (m + 1023) / 1024;
+  const int64_t b = t * per, e = min(m, b + per);
+  int64_t s = 0;
+  for (int64_t i = b; i < e; ++i)
+    s += counts[i];
+  partial[t] = s;
+  __syncthreads();
+  // Hillis-Steele inclusive scan over the 1024 partial sums.
+  for (int off = 1; off < 1024; off <<= 1) {
+    int64_t v = t >= off ? partial[t - off] : 0;
+    __syncthreads();
+    partial[t] += v;
+    __syncthreads();
+  }
+  int64_t run = partial[t] - s;
+  for (int64_t i = b; i < e; ++i) {
+    base[i] = run;
+    run += counts[i];
+  }
+  if (t == 1023)
+    *total = partial[1023];
+}
+
+} // namespace rhip

@@ -1,0 +1,173 @@
+"""Seeded synthetic point clouds for the five benchmark configurations.
+
+All generators return int32 coordinates [N, 1 + D] (batch first, as
+SparseTensor expects: RiemannEngine/engine/tensor/sparse_tensor.cpp:70-77)
+with unique rows, in a deterministic order fixed by the seed. The reference
+ships no datasets for this path; these shapes follow the workload
+descriptions and are generated on the host with numpy.
+"""
+from __future__ import annotations
+
+import numpy as np
+
+
+def _unique_rows(c: np.ndarray) -> np.ndarray:
+    """First-occurrence unique rows (keeps generator order)."""
+    _, idx = np.unique(c, axis=0, return_index=True)
+    return c[np.sort(idx)]
+
+
+def sphere_shell(radius: float = 64.0, half_width: float = 0.5, batch: int = 0) -> np.ndarray:
+    """Integer voxels whose centre lies within half_width of a sphere surface.
+
+    Config 1 (radius 64, |‖c‖-64| < 0.5) gives 51,554 voxels.
+    """
+    r = int(np.ceil(radius + half_width)) + 1
+    ax = np.arange(-r, r + 1, dtype=np.int64)
+    X, Y = np.meshgrid(ax, ax, indexing="ij")
+    out = []
+    for z in ax:  # slice by z to keep memory small
+        d = np.sqrt(X * X + Y * Y + z * z)
+        m = np.abs(d - radius) < half_width
+        if m.any():
+            pts = np.stack([X[m], Y[m], np.full(m.sum(), z)], axis=1)
+            out.append(pts)
+    p = np.concatenate(out, axis=0)
+    b = np.full((p.shape[0], 1), batch, np.int64)
+    return np.concatenate([b, p], axis=1).astype(np.int32)
+
+
+def _box_surface(lo: np.ndarray, hi: np.ndarray) -> np.ndarray:
+    """Integer voxels on the surface of the axis-aligned box [lo, hi]."""
+    xs = [np.arange(lo[i], hi[i] + 1) for i in range(3)]
+    faces = []
+    for axis in range(3):
+        o1, o2 = [a for a in range(3) if a != axis]
+        A, B = np.meshgrid(xs[o1], xs[o2], indexing="ij")
+        for v in (lo[axis], hi[axis]):
+            f = np.empty((A.size, 3), np.int64)
+            f[:, axis] = v
+            f[:, o1] = A.ravel()
+            f[:, o2] = B.ravel()
+            faces.append(f)
+    return np.concatenate(faces, axis=0)
+
+
+def indoor_scene(rng: np.random.Generator, grid: int = 256, voxel: float = 0.05,
+                 n_boxes: int = 20) -> np.ndarray:
+    """One room (floor, ceiling, 4 walls) plus n_boxes random box surfaces
+    with sides U(0.3, 2) m, voxelised at `voxel` m inside a grid^3 box.
+    Rows are shuffled (scanner order is arbitrary)."""
+    W = int(rng.uniform(5.0, 7.0) / voxel)
+    L = int(rng.uniform(5.0, 7.0) / voxel)
+    H = int(rng.uniform(2.4, 3.0) / voxel)
+    W, L, H = min(W, grid - 2), min(L, grid - 2), min(H, grid - 2)
+    ox = int(rng.integers(0, grid - W))
+    oy = int(rng.integers(0, grid - L))
+    room = _box_surface(np.array([0, 0, 0]), np.array([W, L, H]))
+    parts = [room]
+    for _ in range(n_boxes):
+        size = (rng.uniform(0.3, 2.0, 3) / voxel).astype(np.int64)
+        size[2] = min(size[2], H - 1)
+        lo = np.array([rng.integers(1, max(2, W - size[0])),
+                       rng.integers(1, max(2, L - size[1])), 0])
+        hi = np.minimum(lo + size, [W - 1, L - 1, H - 1])
+        parts.append(_box_surface(lo, hi))
+    p = np.concatenate(parts, axis=0)
+    p[:, 0] += ox
+    p[:, 1] += oy
+    p = np.clip(p, 0, grid - 1)
+    p = _unique_rows(p)
+    return p[rng.permutation(p.shape[0])]
+
+
+def indoor_batch(batch: int = 4, seed: int = 2, **kw) -> np.ndarray:
+    """Config 2 (batch 4) / config 5 (batch 8) coordinates."""
+    rng = np.random.default_rng(seed)
+    out = []
+    for b in range(batch):
+        p = indoor_scene(rng, **kw)
+        out.append(np.concatenate([np.full((p.shape[0], 1), b), p], axis=1))
+    return np.concatenate(out, axis=0).astype(np.int32)
+
+
+def _ray_boxes(o, d, lo, hi):
+    """Nearest positive hit distance of rays (o + t d) with boxes [lo, hi]
+    (slab method); inf where a ray misses every box."""
+    inv = 1.0 / np.where(np.abs(d) < 1e-12, 1e-12, d)
+    best = np.full(d.shape[0], np.inf)
+    for b in range(lo.shape[0]):
+        t1 = (lo[b] - o) * inv
+        t2 = (hi[b] - o) * inv
+        tmin = np.max(np.minimum(t1, t2), axis=1)
+        tmax = np.min(np.maximum(t1, t2), axis=1)
+        hit = (tmax >= np.maximum(tmin, 0.0))
+        t = np.where(tmin > 0, tmin, tmax)
+        best = np.where(hit & (t < best), t, best)
+    return best
+
+
+def lidar_sweep(rng: np.random.Generator, beams: int = 64, azimuths: int = 2048,
+                n_boxes: int = 40, voxel: float = 0.1, height: float = 1.8,
+                max_range: float = 80.0, noise: float = 0.02) -> np.ndarray:
+    """Spinning LiDAR: beams at elevations -25..+3 deg x azimuths against a
+    ground plane (z=0) and random boxes, range noise N(0, noise), voxelised."""
+    el = np.deg2rad(np.linspace(-25.0, 3.0, beams))
+    az = np.linspace(0.0, 2 * np.pi, azimuths, endpoint=False)
+    E, A = np.meshgrid(el, az, indexing="ij")
+    d = np.stack([np.cos(E) * np.cos(A), np.cos(E) * np.sin(A), np.sin(E)], -1).reshape(-1, 3)
+    o = np.array([0.0, 0.0, height])
+    # boxes: footprint 1-6 m, height 1-4 m, centres 4-50 m away
+    r = rng.uniform(4.0, 50.0, n_boxes)
+    th = rng.uniform(0, 2 * np.pi, n_boxes)
+    c = np.stack([r * np.cos(th), r * np.sin(th)], 1)
+    half = rng.uniform(0.5, 3.0, (n_boxes, 2))
+    hgt = rng.uniform(1.0, 4.0, n_boxes)
+    lo = np.concatenate([c - half, np.zeros((n_boxes, 1))], 1)
+    hi = np.concatenate([c + half, hgt[:, None]], 1)
+    t_box = _ray_boxes(o, d, lo, hi)
+    t_gnd = np.where(d[:, 2] < -1e-9, -height / np.minimum(d[:, 2], -1e-9), np.inf)
+    t = np.minimum(t_box, t_gnd)
+    keep = t < max_range
+    t = t[keep] + rng.normal(0.0, noise, keep.sum())
+    pts = o + d[keep] * t[:, None]
+    v = np.floor(pts / voxel).astype(np.int64)
+    return _unique_rows(v)
+
+
+def lidar_batch(batch: int = 2, seed: int = 3, **kw) -> np.ndarray:
+    """Config 3 coordinates."""
+    rng = np.random.default_rng(seed)
+    out = []
+    for b in range(batch):
+        p = lidar_sweep(rng, **kw)
+        out.append(np.concatenate([np.full((p.shape[0], 1), b), p], axis=1))
+    return np.concatenate(out, axis=0).astype(np.int32)
+
+
+def moving_shell_4d(radius: float = 48.0, frames: int = 8, step: int = 2,
+                    half_width: float = 0.5) -> np.ndarray:
+    """Config 4: frames of a sphere shell translating `step` voxels/frame
+    along x; coordinates (b, x, y, z, t). Thickness-1 shells (half width
+    0.5) give 8 x 29,066 = 232,528 voxels at radius 48."""
+    s = sphere_shell(radius, half_width)[:, 1:].astype(np.int64)
+    out = []
+    for f in range(frames):
+        p = s.copy()
+        p[:, 0] += step * f
+        out.append(np.concatenate([np.zeros((p.shape[0], 1), np.int64), p,
+                                   np.full((p.shape[0], 1), f)], axis=1))
+    return np.concatenate(out, axis=0).astype(np.int32)
+
+
+def features(n: int, c: int, seed: int, dist: str = "normal") -> np.ndarray:
+    rng = np.random.default_rng(seed)
+    if dist == "uniform":
+        return rng.uniform(-1.0, 1.0, (n, c)).astype(np.float32)
+    return rng.standard_normal((n, c)).astype(np.float32)
+
+
+def kaiming_weight(K: int, cin: int, cout: int, seed: int) -> np.ndarray:
+    """Kaiming-normal weights [K, cin, cout], std sqrt(2 / (cin * K))."""
+    rng = np.random.default_rng(seed)
+    return (rng.standard_normal((K, cin, cout)) * np.sqrt(2.0 / (cin * K))).astype(np.float32)

@@ -1,0 +1,69 @@
+"""The C-ABI library loads and exports exactly what include/riemann_hip.h
+declares; argument validation works without a GPU. No kernels run here."""
+import ctypes
+import os
+import re
+import subprocess
+
+import pytest
+
+from riemannengine_amd import abi
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "riemann_hip.h")
+
+
+def _declared():
+    txt = open(HEADER).read()
+    txt = re.sub(r"/\*.*?\*/", "", txt, flags=re.S)
+    return set(re.findall(r"\b(rhip_[a-z0-9_]+)\s*\(", txt))
+
+
+def test_library_exports_every_declared_symbol():
+    L = abi.lib()
+    declared = _declared()
+    assert declared == set(abi.EXPORTS)
+    for name in declared:
+        assert hasattr(L, name), name
+    out = subprocess.run(["nm", "-D", "--defined-only", abi.LIB_PATH], capture_output=True,
+                         text=True, check=True).stdout
+    exported = set(re.findall(r"\bT (rhip_[a-z0-9_]+)", out))
+    assert exported == declared
+
+
+def test_abi_version_and_struct_layout():
+    assert abi.lib().rhip_abi_version() == 1
+    # void*, int64, void*, int64, 3 x int32, 3 x int32[8] -> 140 bytes, padded to 144
+    assert ctypes.sizeof(abi.RhipTable) == 144
+
+
+def test_workspace_queries():
+    L = abi.lib()
+    assert abi._sizeq(L.rhip_hash_workspace_bytes, 1000, 4) > 1000 * 8
+    assert abi._sizeq(L.rhip_kmap_workspace_bytes, 1000, 27) > 0
+    assert abi._sizeq(L.rhip_conv_workspace_bytes, 27, 64, 64, abi.BF16) >= 27 * 64 * 64 * 4
+    assert L.rhip_table_bytes(100) == 256 * 16  # next power of two >= 2n, 16 B slots
+
+
+@pytest.mark.parametrize("call,msg", [
+    (lambda L, t: L.rhip_hash_build(None, 10, 1, None, 0, None, 0, None, None, None,
+                                    ctypes.byref(t), None), "ncol"),
+    (lambda L, t: L.rhip_hash_build(None, -1, 4, None, 0, None, 0, None, None, None,
+                                    ctypes.byref(t), None), "row count"),
+    (lambda L, t: L.rhip_kmap_count(ctypes.byref(t), None, None, 10, 0, None, None, None, 0,
+                                    None, None, None), "K must"),
+    (lambda L, t: L.rhip_conv_forward(None, 1, 4, None, 27, 8, None, None, None, 1, None, 7,
+                                      None, 0, None), "dtype"),
+])
+def test_invalid_arguments_are_reported(call, msg):
+    L = abi.lib()
+    t = abi.RhipTable()
+    status = call(L, t)
+    assert status != 0
+    assert msg in L.rhip_last_error().decode()
+
+
+def test_cpu_tensors_are_rejected():
+    import torch
+    with pytest.raises(RuntimeError, match="device tensor"):
+        abi.hash_build(torch.zeros((4, 4), dtype=torch.int32))

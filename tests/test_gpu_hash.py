@@ -1,0 +1,87 @@
+"""GPU coordinate hashing vs the oracle: bit-exact unique rows, mapping and
+inverse (first-occurrence order), lookups, locality order."""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from riemannengine_amd import abi, scenes
+from helpers import DEV, to_dev, random_coords
+
+pytestmark = pytest.mark.gpu
+
+
+def _check_build(c):
+    print(f"hash build n={c.shape[0]} ncol={c.shape[1]}", flush=True)
+    t = abi.hash_build(to_dev(c))
+    uq, mp, inv = oracle.insert_and_map(c)
+    assert t.n == uq.shape[0]
+    np.testing.assert_array_equal(t.ucoords.cpu().numpy(), uq)
+    np.testing.assert_array_equal(t.mapping.cpu().numpy(), mp)
+    np.testing.assert_array_equal(t.inverse.cpu().numpy(), inv)
+    return t
+
+
+@pytest.mark.parametrize("n,D,span", [(1, 3, 5), (1000, 3, 4), (50000, 3, 20), (30000, 4, 6),
+                                      (200000, 3, 60), (5000, 1, 100), (4000, 6, 3)])
+def test_build_matches_oracle(n, D, span):
+    rng = np.random.default_rng(n + D)
+    _check_build(random_coords(rng, n, D, span))
+
+
+def test_build_empty():
+    t = abi.hash_build(torch.zeros((0, 4), dtype=torch.int32, device=DEV))
+    assert t.n == 0
+    assert (t.lookup(torch.tensor([[0, 0, 0, 0]], dtype=torch.int32, device=DEV)) == -1).all()
+
+
+def test_row_reference_mode_for_wide_ranges():
+    """Columns spanning the full int32 range cannot pack into 63 bits; the
+    table falls back to comparing whole rows."""
+    rng = np.random.default_rng(9)
+    base = rng.integers(-2**31, 2**31 - 1, (3000, 4), dtype=np.int64).astype(np.int32)
+    c = np.concatenate([base, base[rng.integers(0, 3000, 2000)]])[rng.permutation(5000)]
+    t = _check_build(c)
+    assert t.struct.mode == abi.KEY_ROWREF
+    q = np.concatenate([c[:100], c[:100] + 1])
+    got = t.lookup(to_dev(q)).cpu().numpy()
+    uq, _, inv = oracle.insert_and_map(c)
+    where = {tuple(r): i for i, r in enumerate(uq.tolist())}
+    exp = [where.get(tuple(r), -1) for r in q.tolist()]
+    np.testing.assert_array_equal(got, exp)
+
+
+def test_lookup_present_absent_and_out_of_range():
+    rng = np.random.default_rng(4)
+    c = random_coords(rng, 20000, 3, 30)
+    t = abi.hash_build(to_dev(c))
+    assert t.struct.mode == abi.KEY_PACKED64
+    q = np.concatenate([c[:5000], random_coords(rng, 5000, 3, 40),
+                        np.array([[0, 2**31 - 1, 0, 0], [-5, 0, 0, 0], [1, -2**31, 7, 7]], np.int32)])
+    got = t.lookup(to_dev(q)).cpu().numpy()
+    uq, _, _ = oracle.insert_and_map(c)
+    where = {tuple(r): i for i, r in enumerate(uq.tolist())}
+    exp = np.array([where.get(tuple(r), -1) for r in q.tolist()])
+    np.testing.assert_array_equal(got, exp)
+
+
+def test_spatial_order_is_sorted_permutation():
+    rng = np.random.default_rng(2)
+    c = random_coords(rng, 40000, 3, 50, batch=3)
+    t = abi.hash_build(to_dev(c))
+    order = t.order.cpu().numpy()
+    pos = t.pos.cpu().numpy()
+    np.testing.assert_array_equal(np.sort(order), np.arange(t.n))
+    np.testing.assert_array_equal(pos[order], np.arange(t.n))
+    rows = t.ucoords.cpu().numpy()[order]
+    keys = np.lexsort(rows.T[::-1])
+    np.testing.assert_array_equal(keys, np.arange(t.n))
+
+
+@pytest.mark.parametrize("cfg", ["sphere", "indoor", "lidar", "shell4d"])
+def test_config_coordinate_sets(cfg):
+    c = {"sphere": scenes.sphere_shell, "indoor": lambda: scenes.indoor_batch(4, 2),
+         "lidar": lambda: scenes.lidar_batch(2, 3), "shell4d": scenes.moving_shell_4d}[cfg]()
+    rng = np.random.default_rng(1)
+    dup = np.concatenate([c, c[rng.integers(0, len(c), len(c) // 3)]])[rng.permutation(len(c) * 4 // 3)]
+    _check_build(dup)

@@ -1,0 +1,141 @@
+"""GPU kernel maps and strided output coordinates vs the oracle: bit-exact
+after canonical ordering, plus the dense neighbour tables."""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from riemannengine_amd import abi, scenes
+from helpers import DEV, to_dev, random_coords, gpu_tables_and_map, gpu_canonical
+
+pytestmark = pytest.mark.gpu
+
+
+def _ref_map(cin, cout, off):
+    kofs, ir, orr = oracle.kernel_map(cin, cout, off)
+    return kofs, oracle.canonical_pairs(kofs, ir, orr)
+
+
+def _check_tables(km, tin, tout):
+    """nbr/nbr_t hold exactly the pairs, at the map's processing positions."""
+    nbr = km.nbr.cpu().numpy()
+    nbr_t = km.nbr_t.cpu().numpy()
+    oo, io = tout.order.cpu().numpy(), tin.order.cpu().numpy()
+    ks = np.repeat(np.arange(km.K), np.diff(km.offsets_host))
+    ir, orr = km.in_rows.cpu().numpy(), km.out_rows.cpu().numpy()
+    dense = np.full((km.K, km.n_out), -1, np.int64)
+    dense[ks, tout.pos.cpu().numpy()[orr]] = ir
+    np.testing.assert_array_equal(nbr, dense)
+    dense_t = np.full((km.K, km.n_in), -1, np.int64)
+    dense_t[ks, tin.pos.cpu().numpy()[ir]] = orr
+    np.testing.assert_array_equal(nbr_t, dense_t)
+    assert oo.shape[0] == km.n_out and io.shape[0] == km.n_in
+
+
+@pytest.mark.parametrize("D,ks,dil,ts,region", [
+    (3, 3, 1, 1, "cube"), (3, 3, 2, 1, "cube"), (3, 3, 1, 2, "cube"), (3, 5, 1, 1, "cube"),
+    (4, 3, 1, 1, "cube"), (3, 3, 1, 1, "cross"), (2, 3, 1, 1, "cube"), (3, 1, 1, 1, "cube")])
+def test_same_set_map_matches_oracle(D, ks, dil, ts, region):
+    rng = np.random.default_rng(D * 100 + ks * 10 + dil)
+    c = random_coords(rng, 20000, D, 14) * np.array([1] + [ts] * D, np.int32)
+    c, _, _ = oracle.insert_and_map(c)
+    off = oracle.region_offsets(D, ks, dil, ts, region)
+    print(f"kmap D={D} ks={ks} dil={dil} ts={ts} {region} K={len(off)}", flush=True)
+    tin, tout, km = gpu_tables_and_map(c, c, off, same=True)
+    kofs, ref = _ref_map(c, c, off)
+    np.testing.assert_array_equal(km.offsets_host, kofs)
+    np.testing.assert_array_equal(gpu_canonical(km), ref)
+    _check_tables(km, tin, tout)
+
+
+def test_custom_region():
+    rng = np.random.default_rng(5)
+    c, _, _ = oracle.insert_and_map(random_coords(rng, 5000, 3, 8))
+    cust = np.array([[0, 0, 0], [2, -1, 0], [-3, 0, 1], [1, 1, 1]])
+    off = oracle.region_offsets(3, 3, region="custom", custom=cust)
+    tin, tout, km = gpu_tables_and_map(c, c, off, same=True)
+    np.testing.assert_array_equal(gpu_canonical(km), _ref_map(c, c, off)[1])
+
+
+@pytest.mark.parametrize("s", [2, 4])
+def test_strided_output_coords_and_map(s):
+    """2^3 stride-s conv: output coords (b, floor(x/s)*s) in first-occurrence
+    order (row order bit-exact with the oracle), map = children per parent."""
+    rng = np.random.default_rng(s)
+    c, _, _ = oracle.insert_and_map(random_coords(rng, 30000, 3, 40))
+    coarse_gpu = abi.stride_coords(to_dev(c), [s] * 3)
+    tout = abi.hash_build(coarse_gpu)
+    ref_coarse = oracle.stride(c, [s] * 3)
+    np.testing.assert_array_equal(tout.ucoords.cpu().numpy(), ref_coarse)
+    tin = abi.hash_build(to_dev(c))
+    off = oracle.region_offsets(3, 2, 1, 1)  # kernel region on the input stride
+    km = abi.kernel_map(tin, tout, to_dev(off))
+    kofs, ref = _ref_map(c, ref_coarse, off)
+    np.testing.assert_array_equal(gpu_canonical(km), ref)
+    if s == 2:
+        assert km.n_pairs == len(c)  # every fine voxel has exactly one parent
+    _check_tables(km, tin, tout)
+
+
+def test_stride_negative_and_mixed():
+    c = np.array([[0, -1, -2, -3], [0, -4, 5, 0], [1, 3, -3, 7], [0, -1, -1, -4]], np.int32)
+    got = abi.stride_coords(to_dev(c), [2, 3, 4]).cpu().numpy()
+    exp = c.copy()
+    exp[:, 1:] = np.floor_divide(c[:, 1:], [2, 3, 4]) * np.array([2, 3, 4])
+    np.testing.assert_array_equal(got, exp)
+
+
+def test_transposed_map_is_swapped_forward_map():
+    """space_impl.hpp:649-697: the transposed map (coarse -> fine) equals the
+    forward map (fine -> coarse) with in/out exchanged; generating it from
+    the fine side with the region on the fine stride gives the same set."""
+    rng = np.random.default_rng(8)
+    c, _, _ = oracle.insert_and_map(random_coords(rng, 20000, 3, 30))
+    tin = abi.hash_build(to_dev(c))
+    tout = abi.hash_build(abi.stride_coords(to_dev(c), [2, 2, 2]))
+    off = oracle.region_offsets(3, 2, 1, 1)
+    fwd = abi.kernel_map(tin, tout, to_dev(off))
+    tr = fwd.swapped()
+    ref_kofs, ir, orr = oracle.kernel_map(c, tout.ucoords.cpu().numpy(), off)
+    np.testing.assert_array_equal(gpu_canonical(tr), oracle.canonical_pairs(ref_kofs, orr, ir))
+    assert tr.n_in == fwd.n_out and tr.n_out == fwd.n_in
+
+
+def test_empty_sides():
+    off = oracle.region_offsets(3, 3)
+    c = np.array([[0, 1, 2, 3], [0, 1, 2, 4]], np.int32)
+    e = abi.hash_build(torch.zeros((0, 4), dtype=torch.int32, device=DEV))
+    t = abi.hash_build(to_dev(c))
+    for tin, tout in ((e, t), (t, e), (e, e)):
+        km = abi.kernel_map(tin, tout, to_dev(off))
+        assert km.n_pairs == 0
+        assert (km.nbr == -1).all() and (km.nbr_t == -1).all()
+
+
+@pytest.mark.parametrize("cfg", ["sphere", "indoor", "shell4d"])
+def test_config_maps_match_oracle(cfg):
+    c = {"sphere": scenes.sphere_shell, "indoor": lambda: scenes.indoor_batch(4, 2),
+         "shell4d": scenes.moving_shell_4d}[cfg]()
+    D = c.shape[1] - 1
+    off = oracle.region_offsets(D, 3)
+    print(f"config map {cfg} n={len(c)} K={len(off)}", flush=True)
+    tin, tout, km = gpu_tables_and_map(c, c, off, same=True)
+    kofs, ref = _ref_map(c, c, off)
+    np.testing.assert_array_equal(km.offsets_host, kofs)
+    np.testing.assert_array_equal(gpu_canonical(km), ref)
+    # same-set stride-1 maps are symmetric: P_k == P_{K-1-k}
+    cnt = np.diff(km.offsets_host)
+    np.testing.assert_array_equal(cnt, cnt[::-1])
+    if cfg == "sphere":
+        assert len(c) == 51554 and km.n_pairs == 544970
+
+
+def test_lidar_down_up_maps():
+    c = scenes.lidar_batch(2, 3)
+    tin = abi.hash_build(to_dev(c))
+    tout = abi.hash_build(abi.stride_coords(to_dev(c), [2, 2, 2]))
+    off = oracle.region_offsets(3, 2)
+    km = abi.kernel_map(tin, tout, to_dev(off))
+    assert km.n_pairs == len(c)  # P_down = N_fine
+    np.testing.assert_array_equal(gpu_canonical(km),
+                                  _ref_map(c, tout.ucoords.cpu().numpy(), off)[1])
