@@ -52,7 +52,30 @@ def parse_args():
     ap.add_argument("--no-cpu-baseline", action="store_true",
                     help="skip the CPU oracle timing (profiling runs)")
     ap.add_argument("--map-reps", type=int, default=5)
+    ap.add_argument("--copy-mib", type=int, default=0,
+                    help="calibration mode: time a plain device copy of this many MiB "
+                         "(the reference kernel for scaling FETCH_SIZE/WRITE_SIZE) and exit")
     return ap.parse_args()
+
+
+def copy_calibration(mib: int) -> None:
+    """Copy an int32 buffer of `mib` MiB five times on the device: a kernel of
+    known traffic (mib MiB read + mib MiB written per launch) against which
+    the HBM byte counters are scaled."""
+    import torch
+    n = mib * (1 << 20) // 4
+    src = torch.arange(n, dtype=torch.int32, device="cuda:0")
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+    ev[0].record()
+    for _ in range(5):
+        dst.copy_(src)
+    ev[1].record()
+    torch.cuda.synchronize()
+    ms = ev[0].elapsed_time(ev[1]) / 5
+    print(json.dumps({"copy_mib": mib, "ms": round(ms, 4),
+                      "GBps": round(2 * mib * (1 << 20) / (ms * 1e-3) / 1e9, 1)}), flush=True)
 
 
 def conv_traffic(n_in, n_out, P, K, cin, cout, s):
@@ -123,6 +146,10 @@ def main():
               "on one GPU only (the path shards by scene; see the sharding notes)",
               file=sys.stderr)
         sys.exit(2)
+
+    if args.copy_mib > 0:
+        copy_calibration(args.copy_mib)
+        return
 
     import torch
     from riemannengine_amd import abi, scenes, stencil
@@ -207,7 +234,7 @@ def main():
     roof["traffic"] = None
     roof["kernel"] = {"forward": "conv_os_kernel (forward)",
                       "backward_input": "conv_os_kernel (dX, transposed weights)",
-                      "backward_weight": "conv_dw_kernel"}[dom]
+                      "backward_weight": "conv_dw_lds_kernel"}[dom]
     roof["kernel_ms"] = round(per[dom], 4)
     roof["algorithmic"] = {"flop": F, "bytes": B}
 

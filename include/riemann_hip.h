@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define RHIP_ABI_VERSION 1
+#define RHIP_ABI_VERSION 2
 #define RHIP_MAX_COLS 8 /* batch column + up to 7 spatial axes */
 
 typedef enum rhip_status {
@@ -128,42 +128,52 @@ int rhip_stride_coords(const int32_t *coords, int64_t n, int32_t ncol,
 
 /* ------------------------------------------------------------ kernel map */
 
-int rhip_kmap_workspace_bytes(int64_t n_out, int32_t K, size_t *bytes);
+/* Workspace shared by the two phases of one kernel map (pass the same
+ * buffer, unchanged, to rhip_kmap_count and rhip_kmap_fill). */
+int rhip_kmap_workspace_bytes(int64_t n_in, int64_t n_out, int32_t K,
+                              size_t *bytes);
 
 /*
- * Phase 1 of kernel-map generation. For every output row (taken in
- * out_order, may be NULL for identity) and every offset k, look up
- * out_coords[row] + offsets[k] (batch unchanged) in in_table:
- *   nbr[k * n_out + j] = input row of the neighbour of out_order[j], or -1.
- * offsets is a device array [K, ncol-1] of already scaled lattice offsets
- * (kernel_region::coordinate_at, engine/grid/stencil.hpp:223-278).
- * Writes kmap_offsets (device, K+1 int64: CSR of pairs per offset) and
- * copies it to kmap_offsets_host. Synchronises `stream` once.
+ * Phase 1 of kernel-map generation. For every output row and every offset
+ * k, look up out_coords[row] + offsets[k] (batch column unchanged) in
+ * in_table. offsets is a device array [K, ncol-1] of already scaled lattice
+ * offsets (kernel_region::coordinate_at, engine/grid/stencil.hpp:223-278).
+ * The rows are queried in out_spatial_order (a locality order of the output
+ * map, e.g. from rhip_spatial_order; NULL = row order) and then put in a
+ * processing order that groups rows with equal neighbour masks (K <= 128;
+ * ties keep the locality order). Outputs:
+ *   out_order[p]   output row at processing position p (n_out entries);
+ *   nbr[k*n_out+p] input row paired with out_order[p] under k, or -1;
+ *   kmap_offsets   device int64 [K+1], CSR of the pairs per offset, copied
+ *                  to kmap_offsets_host.
+ * Synchronises `stream` once (to read the pair counts).
  * Replaces CoordinateMapGPU::kernel_map / direct_kernel_map / count_kernel
  * (engine/grid/lattice_gpu.cu:1140-1362, 1366-1549); the live reference
  * semantics are CoordinateMapCPU::kernel_map (engine/grid/lattice_cpu.hpp:606-673).
  */
 int rhip_kmap_count(const rhip_table *in_table, const int32_t *out_coords,
-                    const int32_t *out_order, int64_t n_out, int32_t K,
-                    const int32_t *offsets, int32_t *nbr, void *workspace,
-                    size_t workspace_bytes, int64_t *kmap_offsets,
-                    int64_t *kmap_offsets_host, hipStream_t stream);
+                    const int32_t *out_spatial_order, int64_t n_out, int32_t K,
+                    const int32_t *offsets, void *workspace,
+                    size_t workspace_bytes, int32_t *nbr, int32_t *out_order,
+                    int64_t *kmap_offsets, int64_t *kmap_offsets_host,
+                    hipStream_t stream);
 
 /*
  * Phase 2: emit the pairs of offset k at [kmap_offsets[k], kmap_offsets[k+1])
- * of in_rows / out_rows, ordered by offset then by output position. The
- * workspace must be the one phase 1 wrote. If nbr_t is not NULL it is filled
- * as the transposed table over the input map: nbr_t[k * n_in + in_pos[i]] =
- * output row paired with input row i under offset k, or -1 (in_pos may be
- * NULL for identity). Replaces gpu_kernel_map::decompose
- * (engine/grid/lattice_gpu.cuh:438-488); the set of pairs equals the
- * reference's cpu_kernel_map.
+ * of in_rows / out_rows, ordered by offset, then by output processing
+ * position. If nbr_t is not NULL, also fix a processing order of the input
+ * rows (in_order, grouping equal transposed masks; ties keep
+ * in_spatial_order, NULL = row order) and fill the transposed table
+ * nbr_t[k*n_in+q] = output row paired with in_order[q] under k, or -1.
+ * The workspace must be the one phase 1 wrote. Asynchronous.
+ * Replaces gpu_kernel_map::decompose (engine/grid/lattice_gpu.cuh:438-488);
+ * the set of pairs equals the reference's cpu_kernel_map.
  */
 int rhip_kmap_fill(const int32_t *nbr, const int32_t *out_order, int64_t n_out,
-                   int32_t K, const void *workspace, size_t workspace_bytes,
-                   const int64_t *kmap_offsets, int32_t *in_rows,
-                   int32_t *out_rows, const int32_t *in_pos, int64_t n_in,
-                   int32_t *nbr_t, hipStream_t stream);
+                   int32_t K, const int32_t *in_spatial_order, int64_t n_in,
+                   void *workspace, size_t workspace_bytes, int32_t *in_rows,
+                   int32_t *out_rows, int32_t *nbr_t, int32_t *in_order,
+                   hipStream_t stream);
 
 /* ----------------------------------------------------------- convolution */
 

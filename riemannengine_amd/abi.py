@@ -60,11 +60,11 @@ def _declare(lib):
         "rhip_order_workspace_bytes": (ctypes.c_int, [_i64, _P(_sz)]),
         "rhip_spatial_order": (ctypes.c_int, [_P(RhipTable), _vp, _vp, _vp, _sz, _vp]),
         "rhip_stride_coords": (ctypes.c_int, [_vp, _i64, _i32, _P(_i32), _vp, _vp]),
-        "rhip_kmap_workspace_bytes": (ctypes.c_int, [_i64, _i32, _P(_sz)]),
+        "rhip_kmap_workspace_bytes": (ctypes.c_int, [_i64, _i64, _i32, _P(_sz)]),
         "rhip_kmap_count": (ctypes.c_int, [_P(RhipTable), _vp, _vp, _i64, _i32, _vp,
-                                           _vp, _vp, _sz, _vp, _P(_i64), _vp]),
-        "rhip_kmap_fill": (ctypes.c_int, [_vp, _vp, _i64, _i32, _vp, _sz, _vp, _vp,
-                                          _vp, _vp, _i64, _vp, _vp]),
+                                           _vp, _sz, _vp, _vp, _vp, _P(_i64), _vp]),
+        "rhip_kmap_fill": (ctypes.c_int, [_vp, _vp, _i64, _i32, _vp, _i64, _vp, _sz,
+                                          _vp, _vp, _vp, _vp, _vp]),
         "rhip_conv_workspace_bytes": (ctypes.c_int, [_i32, _i32, _i32, _i32, _P(_sz)]),
         "rhip_conv_forward": (ctypes.c_int, [_vp, _i64, _i32, _vp, _i32, _i32, _vp, _vp,
                                              _vp, _i64, _vp, _i32, _vp, _sz, _vp]),
@@ -244,32 +244,39 @@ class KernelMap:
 
 
 def kernel_map(in_table: CoordTable, out_table: CoordTable, offsets: torch.Tensor) -> KernelMap:
-    """Pairs (in, out) with coord(in) = coord(out) + offsets[k] (batch kept)."""
+    """Pairs (in, out) with coord(in) = coord(out) + offsets[k] (batch kept),
+    the dense neighbour tables and the processing orders of both sides."""
     L = lib()
     dev = in_table.ucoords.device
     offsets = offsets.to(device=dev, dtype=torch.int32).contiguous()
     K = offsets.shape[0]
     if offsets.dim() != 2 or offsets.shape[1] != in_table.ncol - 1:
         raise RuntimeError("offsets must be [K, D]")
+    if out_table.ncol != in_table.ncol:
+        raise RuntimeError("input and output maps have different coordinate widths")
     n_out, n_in = out_table.n, in_table.n
+    st = _stream(dev)
     nbr = torch.empty((K, max(n_out, 1)), dtype=torch.int32, device=dev)
-    ws = torch.empty(_sizeq(L.rhip_kmap_workspace_bytes, n_out, K), dtype=torch.uint8, device=dev)
+    out_order = torch.empty(max(n_out, 1), dtype=torch.int32, device=dev)
+    ws = torch.empty(_sizeq(L.rhip_kmap_workspace_bytes, n_in, n_out, K), dtype=torch.uint8,
+                     device=dev)
     kofs = torch.empty(K + 1, dtype=torch.int64, device=dev)
     kofs_host = np.zeros(K + 1, dtype=np.int64)
     _check(L.rhip_kmap_count(ctypes.byref(in_table.struct), _ptr(out_table.ucoords),
-                             _ptr(out_table.order), n_out, K, _ptr(offsets), _ptr(nbr),
-                             _ptr(ws), ws.numel(), _ptr(kofs),
-                             kofs_host.ctypes.data_as(ctypes.POINTER(ctypes.c_int64)),
-                             _stream(dev)), "rhip_kmap_count")
+                             _ptr(out_table.order), n_out, K, _ptr(offsets), _ptr(ws), ws.numel(),
+                             _ptr(nbr), _ptr(out_order), _ptr(kofs),
+                             kofs_host.ctypes.data_as(ctypes.POINTER(ctypes.c_int64)), st),
+           "rhip_kmap_count")
     P = int(kofs_host[-1])
     in_rows = torch.empty(max(P, 1), dtype=torch.int32, device=dev)
     out_rows = torch.empty(max(P, 1), dtype=torch.int32, device=dev)
     nbr_t = torch.empty((K, max(n_in, 1)), dtype=torch.int32, device=dev)
-    _check(L.rhip_kmap_fill(_ptr(nbr), _ptr(out_table.order), n_out, K, _ptr(ws), ws.numel(),
-                            _ptr(kofs), _ptr(in_rows), _ptr(out_rows), _ptr(in_table.pos),
-                            n_in, _ptr(nbr_t), _stream(dev)), "rhip_kmap_fill")
+    in_order = torch.empty(max(n_in, 1), dtype=torch.int32, device=dev)
+    _check(L.rhip_kmap_fill(_ptr(nbr), _ptr(out_order), n_out, K, _ptr(in_table.order), n_in,
+                            _ptr(ws), ws.numel(), _ptr(in_rows), _ptr(out_rows), _ptr(nbr_t),
+                            _ptr(in_order), st), "rhip_kmap_fill")
     return KernelMap(K, n_in, n_out, kofs, kofs_host, in_rows[:P], out_rows[:P],
-                     nbr[:, :n_out], nbr_t[:, :n_in], in_table.order, out_table.order)
+                     nbr[:, :n_out], nbr_t[:, :n_in], in_order[:n_in], out_order[:n_out])
 
 
 # ------------------------------------------------------------ convolution

@@ -7,24 +7,25 @@
 //   dW[k] = X[in_k]^T @ dY[out_k].
 //
 // MI355X design:
-//  * forward and dX are one output-stationary implicit GEMM. A workgroup owns
-//    128 output rows (4 waves x 2 groups of 16 rows, in the map's locality
-//    order) and a 16..64-column slice; it walks the offsets whose neighbour
-//    table column has any hit in the tile, stages W[k] in LDS once for the
-//    four waves, gathers the 16 neighbour rows of each row group straight
-//    into MFMA A-fragments (16-byte loads, zero for missing neighbours) and
-//    accumulates every offset in registers, so each output row is written
-//    exactly once, with no atomics and no zero-fill pass. Row groups whose
-//    16 rows have no neighbour under k skip that offset's MFMAs.
+//  * Forward and dX are one output-stationary implicit GEMM over the dense
+//    neighbour table of the kernel map, whose rows come grouped by neighbour
+//    mask (so a 16-row group rarely multiplies a missing neighbour). A
+//    256-thread workgroup owns 128 output rows (4 waves x 2 groups of 16) and
+//    up to 64 columns. It walks only the offsets with a neighbour in its rows;
+//    for each it stages the weight slice in LDS with 16-byte copies from a
+//    [K][ncols][cred] copy of the weights (reduction axis contiguous), gathers
+//    each group's 16 neighbour rows straight into MFMA A-fragments (16-byte
+//    loads, zero for a missing neighbour) and accumulates every offset in
+//    registers. Each output row is written once: no atomics, no zero fill.
 //  * dW is a split-pair reduction over the per-offset pair lists: a
-//    workgroup gathers 64 (in, out) pairs of X and dY rows into LDS
-//    (transposed so the pair axis is contiguous), runs 16x16 MFMA tiles with
-//    the pair axis as the reduction, and adds its partial tile to an fp32
-//    accumulator with one atomic per element per pair segment.
-//  * The reduction order inside an MFMA is a permutation of the channel (or
-//    pair) axis chosen so that each lane reads 16 contiguous bytes; A and B
-//    use the same permutation, so the sum is unchanged.
+//    workgroup stages 64 pairs of X and dY rows in LDS transposed (pair axis
+//    contiguous), runs 16x16 MFMA tiles with pairs as the reduction axis and
+//    adds each offset segment's tile to an fp32 accumulator with atomics.
+//  * The reduction order inside an MFMA is a permutation of the reduced axis
+//    chosen so that each lane reads 16 contiguous bytes; A and B use the same
+//    permutation, so the sum is unchanged.
 #include <algorithm>
+#include <type_traits>
 
 #include "rhip_internal.hpp"
 
@@ -35,7 +36,8 @@ typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
 
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / kWave;
-constexpr int kMaskWords = 4; // fast path handles K <= 128 offsets
+constexpr int kMaskWords = 4; // the MFMA paths handle K <= 128 offsets
+constexpr int kXcds = 8;      // MI355X: 8 XCDs, workgroups dealt round-robin
 
 template <typename T> struct Mfma;
 
@@ -81,15 +83,30 @@ template <> __device__ __forceinline__ __bf16 from_f32<__bf16>(float v) {
   return static_cast<__bf16>(v);
 }
 
+// Workgroup id -> tile id. Workgroups are dealt to the 8 XCDs round-robin
+// (id b runs on XCD b % 8); this mapping hands each XCD runs of kXcdRun
+// consecutive tiles, so tiles that share neighbour rows share an L2, while
+// the runs stay interleaved over the whole map to keep the XCDs balanced.
+// The grid is padded to a multiple of 8 * kXcdRun (padding ids map past the
+// last tile).
+constexpr int kXcdRun = 16;
+__device__ __forceinline__ int64_t xcd_tile(int64_t b) {
+  const int64_t x = b % kXcds, m = b / kXcds;
+  return ((m / kXcdRun) * kXcds + x) * kXcdRun + (m % kXcdRun);
+}
+inline int64_t xcd_grid(int64_t tiles) {
+  return ceil_div(tiles, kXcds * kXcdRun) * kXcds * kXcdRun;
+}
+
 // ------------------------------------------------ output-stationary GEMM
 //
-// y[order[j]][col] = sum_k sum_c x[nbr[k][j]][c] * Wk(c, col) (+ bias[col])
-// Wk(c, n) = WT ? w[(k*ncols + n)*cred + c] : w[(k*cred + c)*ncols + n].
-// NT: output columns per workgroup; RG: 16-row groups per wave;
-// CSUB: 16-byte lane loads per staged channel chunk (chunk = CSUB*kCh).
-template <typename T, int NT, int RG, int CSUB, bool WT>
+// y[order[j]][col] = sum_k sum_c x[nbr[k][j]][c] * wt[k][col][c] (+ bias[col])
+// wt is [K][ncols][cred] (reduction axis contiguous). A workgroup owns
+// 4 * RG * 16 output rows and NT columns; RG: 16-row groups per wave; CSUB:
+// 16-byte lane loads per staged channel chunk (chunk = CSUB * kCh channels).
+template <typename T, int NT, int RG, int CSUB>
 __global__ __launch_bounds__(kThreads) void conv_os_kernel(
-    const T *__restrict__ x, int cred, const T *__restrict__ w, int ncols,
+    const T *__restrict__ x, int cred, const T *__restrict__ wt, int ncols,
     const float *__restrict__ bias, const int32_t *__restrict__ nbr,
     int64_t n_rows, int K, const int32_t *__restrict__ order,
     T *__restrict__ y) {
@@ -102,21 +119,26 @@ __global__ __launch_bounds__(kThreads) void conv_os_kernel(
   constexpr int LDW = CCH + VE;          // LDS row stride (elements)
   constexpr int ROWS = kWaves * RG * 16; // output rows per workgroup
   constexpr int NB = NT / 16;
+  constexpr int NV = NT * (CCH / VE);    // 16-byte pieces per staged chunk
+  constexpr int NPT = (NV + kThreads - 1) / kThreads;
 
   __shared__ __align__(16) T sB[NT * LDW];
   __shared__ uint32_t smask[kWaves * RG][kMaskWords];
-  __shared__ uint32_t sbm[kMaskWords];
+  __shared__ int32_t slist[32 * kMaskWords];
+  __shared__ int32_t scount;
 
   const int lane = threadIdx.x & (kWave - 1);
   const int wv = threadIdx.x / kWave;
   const int i16 = lane & 15;
   const int g = lane >> 4;
-  const int64_t tile0 = static_cast<int64_t>(blockIdx.x) * ROWS;
+  const int64_t tile = xcd_tile(blockIdx.x);
+  const int64_t tile0 = tile * ROWS;
+  if (tile0 >= n_rows)
+    return; // padding workgroup (uniform)
   const int col0 = blockIdx.y * NT;
-  const int KW = (K + 31) >> 5;
 
-  // Which offsets have any neighbour in each 16-row group: lanes of group g
-  // test offset k0+g for the 16 rows, one ballot covers four offsets.
+  // Offsets with any neighbour in each 16-row group: lanes of group g test
+  // offset k0+g for the 16 rows; one ballot covers four offsets.
 #pragma unroll
   for (int r = 0; r < RG; ++r) {
     const int64_t pos = tile0 + (wv * RG + r) * 16 + i16;
@@ -140,13 +162,23 @@ __global__ __launch_bounds__(kThreads) void conv_os_kernel(
     }
   }
   __syncthreads();
-  if (threadIdx.x < kMaskWords) {
-    uint32_t m = 0;
-    for (int q = 0; q < kWaves * RG; ++q)
-      m |= smask[q][threadIdx.x];
-    sbm[threadIdx.x] = m;
+  // The workgroup's active offsets, in ascending order.
+  if (threadIdx.x == 0) {
+    int c = 0;
+    for (int q = 0; q < kMaskWords; ++q) {
+      uint32_t m = 0;
+      for (int i = 0; i < kWaves * RG; ++i)
+        m |= smask[i][q];
+      while (m) {
+        slist[c++] = q * 32 + __builtin_ctz(m);
+        m &= m - 1;
+      }
+    }
+    scount = c;
   }
   __syncthreads();
+  const int nch = cred / CCH;
+  const int S = scount * nch; // stages: (active offset, channel chunk)
 
   v4f acc[RG][NB];
 #pragma unroll
@@ -155,67 +187,53 @@ __global__ __launch_bounds__(kThreads) void conv_os_kernel(
     for (int nb = 0; nb < NB; ++nb)
       acc[r][nb] = v4f{0.f, 0.f, 0.f, 0.f};
 
-  for (int kw = 0; kw < KW; ++kw) {
-    uint32_t bits = sbm[kw];
-    while (bits) {
-      const int k = kw * 32 + __builtin_ctz(bits);
-      bits &= bits - 1;
-      int32_t idx[RG];
-      bool act[RG];
-      bool wave_act = false;
+  for (int s = 0; s < S; ++s) {
+    const int k = slist[s / nch];
+    const int cc0 = (s % nch) * CCH;
+    // stage W[k][col0 : col0+NT][cc0 : cc0+CCH] (16-byte copies)
 #pragma unroll
-      for (int r = 0; r < RG; ++r) {
-        const int64_t pos = tile0 + (wv * RG + r) * 16 + i16;
-        act[r] = (smask[wv * RG + r][kw] >> (k & 31)) & 1u;
-        idx[r] = (act[r] && pos < n_rows) ? nbr[k * n_rows + pos] : -1;
-        wave_act |= act[r];
+    for (int i = 0; i < NPT; ++i) {
+      const int li = threadIdx.x + i * kThreads;
+      if (li < NV) {
+        const int n = li / (CCH / VE), cv = li % (CCH / VE);
+        *reinterpret_cast<uint4 *>(&sB[n * LDW + cv * VE]) = *reinterpret_cast<const uint4 *>(
+            wt + (static_cast<int64_t>(k) * ncols + col0 + n) * cred + cc0 + cv * VE);
       }
-      for (int cc0 = 0; cc0 < cred; cc0 += CCH) {
-        __syncthreads(); // every wave is done reading the previous chunk
-        if (WT) {
-          const T *src = w + static_cast<int64_t>(k) * ncols * cred;
-          for (int li = threadIdx.x; li < NT * (CCH / VE); li += kThreads) {
-            const int n = li / (CCH / VE), cv = li % (CCH / VE);
-            *reinterpret_cast<uint4 *>(&sB[n * LDW + cv * VE]) =
-                *reinterpret_cast<const uint4 *>(
-                    src + static_cast<int64_t>(col0 + n) * cred + cc0 + cv * VE);
-          }
-        } else {
-          const T *src = w + static_cast<int64_t>(k) * cred * ncols;
-          for (int li = threadIdx.x; li < CCH * (NT / VE); li += kThreads) {
-            const int c = li / (NT / VE), nv = li % (NT / VE);
-            const uint4 q = *reinterpret_cast<const uint4 *>(
-                src + static_cast<int64_t>(cc0 + c) * ncols + col0 + nv * VE);
-            const T *e = reinterpret_cast<const T *>(&q);
+    }
+    int32_t idx[RG];
+    bool act[RG];
+    bool wave_act = false;
 #pragma unroll
-            for (int j = 0; j < VE; ++j)
-              sB[(nv * VE + j) * LDW + c] = e[j];
-          }
-        }
-        __syncthreads();
-        if (wave_act) {
+    for (int r = 0; r < RG; ++r) {
+      const int64_t pos = tile0 + (wv * RG + r) * 16 + i16;
+      act[r] = (smask[wv * RG + r][k >> 5] >> (k & 31)) & 1u;
+      idx[r] = (act[r] && pos < n_rows) ? nbr[k * n_rows + pos] : -1;
+      wave_act |= act[r];
+    }
+    __syncthreads(); // chunk staged
+    if (wave_act) {
+      Frag a[RG][CSUB];
 #pragma unroll
-          for (int sub = 0; sub < CSUB; ++sub) {
-            Frag a[RG];
+      for (int r = 0; r < RG; ++r)
 #pragma unroll
-            for (int r = 0; r < RG; ++r)
-              a[r] = idx[r] >= 0
-                         ? M::load(x + static_cast<int64_t>(idx[r]) * cred + cc0 +
-                                   sub * CH + g * EPL)
-                         : M::zero();
+        for (int sub = 0; sub < CSUB; ++sub)
+          a[r][sub] = idx[r] >= 0 ? M::load(x + static_cast<int64_t>(idx[r]) * cred + cc0 +
+                                            sub * CH + g * EPL)
+                                  : M::zero();
 #pragma unroll
-            for (int nb = 0; nb < NB; ++nb) {
-              const Frag b = *reinterpret_cast<const Frag *>(
-                  &sB[(nb * 16 + i16) * LDW + sub * CH + g * EPL]);
+      for (int sub = 0; sub < CSUB; ++sub) {
 #pragma unroll
-              for (int r = 0; r < RG; ++r)
-                if (act[r])
-                  M::mma(a[r], b, acc[r][nb]);
-            }
-          }
+        for (int nb = 0; nb < NB; ++nb) {
+          const Frag b =
+              *reinterpret_cast<const Frag *>(&sB[(nb * 16 + i16) * LDW + sub * CH + g * EPL]);
+#pragma unroll
+          for (int r = 0; r < RG; ++r)
+            if (act[r])
+              M::mma(a[r][sub], b, acc[r][nb]);
         }
       }
     }
+    __syncthreads(); // every wave is done reading the chunk
   }
 
 #pragma unroll
@@ -239,9 +257,9 @@ __global__ __launch_bounds__(kThreads) void conv_os_kernel(
 }
 
 // Any-shape fallback of conv_os_kernel: one lane per output element.
-template <typename T, bool WT>
+template <typename T>
 __global__ __launch_bounds__(kThreads) void conv_os_generic_kernel(
-    const T *__restrict__ x, int cred, const T *__restrict__ w, int ncols,
+    const T *__restrict__ x, int cred, const T *__restrict__ wt, int ncols,
     const float *__restrict__ bias, const int32_t *__restrict__ nbr,
     int64_t n_rows, int K, const int32_t *__restrict__ order,
     T *__restrict__ y) {
@@ -256,11 +274,9 @@ __global__ __launch_bounds__(kThreads) void conv_os_generic_kernel(
     if (s < 0)
       continue;
     const T *xr = x + static_cast<int64_t>(s) * cred;
-    for (int c = 0; c < cred; ++c) {
-      const T wv = WT ? w[(static_cast<int64_t>(k) * ncols + col) * cred + c]
-                      : w[(static_cast<int64_t>(k) * cred + c) * ncols + col];
-      acc += to_f32(xr[c]) * to_f32(wv);
-    }
+    const T *wr = wt + (static_cast<int64_t>(k) * ncols + col) * cred;
+    for (int c = 0; c < cred; ++c)
+      acc += to_f32(xr[c]) * to_f32(wr[c]);
   }
   if (bias)
     acc += bias[col];
@@ -268,14 +284,30 @@ __global__ __launch_bounds__(kThreads) void conv_os_generic_kernel(
   y[o * ncols + col] = from_f32<T>(acc);
 }
 
+// wt[k][n][c] = w[k][c][n] (weights [K, cin, cout] -> [K, cout, cin]).
+template <typename T>
+__global__ __launch_bounds__(kThreads) void transpose_w_kernel(const T *__restrict__ w, int K,
+                                                               int cin, int cout,
+                                                               T *__restrict__ wt) {
+  const int64_t i = blockIdx.x * static_cast<int64_t>(kThreads) + threadIdx.x;
+  const int64_t per = static_cast<int64_t>(cin) * cout;
+  if (i >= K * per)
+    return;
+  const int64_t k = i / per, rem = i % per;
+  const int c = static_cast<int>(rem / cout), n = static_cast<int>(rem % cout);
+  wt[(k * cout + n) * cin + c] = w[i];
+}
+
 // ------------------------------------------------------------------- dW
 
 constexpr int kPairChunk = 64;
 
-// dw[k][ci][co] += sum_{p in k} x[in_rows[p]][ci] * gy[out_rows[p]][co] over
-// the workgroup's pair range [blockIdx.x*ppb, +ppb), tile (MT x NTc).
+// bf16: dw[k][ci][co] += sum_{p in k} x[in_rows[p]][ci] * gy[out_rows[p]][co]
+// over the workgroup's pair range [blockIdx.x*ppb, +ppb), tile (MT x NTc).
+// The pair axis is the MFMA reduction axis, so 64-pair chunks are staged in
+// LDS transposed (pair axis contiguous).
 template <typename T, int MT, int NTc>
-__global__ __launch_bounds__(kThreads) void conv_dw_kernel(
+__global__ __launch_bounds__(kThreads) void conv_dw_lds_kernel(
     const T *__restrict__ x, int cin, const T *__restrict__ gy, int cout,
     const int64_t *__restrict__ kofs, int K, const int32_t *__restrict__ in_rows,
     const int32_t *__restrict__ out_rows, int64_t n_pairs, int64_t ppb,
@@ -422,102 +454,101 @@ static bool aligned16(const void *p) {
 
 template <typename T> constexpr int kChOf = Mfma<T>::kCh;
 
-template <typename T, int NT, int CSUB, bool WT>
-static void launch_os(const T *x, int cred, const T *w, int ncols,
+template <typename T, int NT, int RG, int CSUB>
+static void launch_os(const T *x, int cred, const T *wt, int ncols,
                       const float *bias, const int32_t *nbr, int64_t n_rows,
                       int K, const int32_t *order, T *y, hipStream_t s) {
-  constexpr int RG = 2;
   constexpr int ROWS = kWaves * RG * 16;
-  dim3 grid(static_cast<unsigned>(ceil_div(n_rows, ROWS)), ncols / NT);
-  hipLaunchKernelGGL((conv_os_kernel<T, NT, RG, CSUB, WT>), grid, dim3(kThreads),
-                     0, s, x, cred, w, ncols, bias, nbr, n_rows, K, order, y);
+  dim3 grid(static_cast<unsigned>(xcd_grid(ceil_div(n_rows, ROWS))), ncols / NT);
+  hipLaunchKernelGGL((conv_os_kernel<T, NT, RG, CSUB>), grid, dim3(kThreads), 0, s, x,
+                     cred, wt, ncols, bias, nbr, n_rows, K, order, y);
 }
 
-template <typename T, int NT, bool WT>
-static void pick_csub(const T *x, int cred, const T *w, int ncols,
+template <typename T, int NT>
+static void pick_csub(const T *x, int cred, const T *wt, int ncols,
                       const float *bias, const int32_t *nbr, int64_t n_rows,
                       int K, const int32_t *order, T *y, hipStream_t s) {
   constexpr int CH = kChOf<T>;
-  if (cred % (4 * CH) == 0)
-    launch_os<T, NT, 4, WT>(x, cred, w, ncols, bias, nbr, n_rows, K, order, y, s);
-  else if (cred % (2 * CH) == 0)
-    launch_os<T, NT, 2, WT>(x, cred, w, ncols, bias, nbr, n_rows, K, order, y, s);
+  constexpr int RG = 2;
+  if (cred % (2 * CH) == 0)
+    launch_os<T, NT, RG, 2>(x, cred, wt, ncols, bias, nbr, n_rows, K, order, y, s);
   else
-    launch_os<T, NT, 1, WT>(x, cred, w, ncols, bias, nbr, n_rows, K, order, y, s);
+    launch_os<T, NT, RG, 1>(x, cred, wt, ncols, bias, nbr, n_rows, K, order, y, s);
 }
 
-template <typename T, bool WT>
-static void run_os(const T *x, int cred, const T *w, int ncols,
+// y[order[j]] = sum_k x[nbr[k][j]] @ W'[k] with W'[k][c][n] = wt[k][n][c].
+template <typename T>
+static void run_os(const T *x, int cred, const T *wt, int ncols,
                    const float *bias, const int32_t *nbr, int64_t n_rows, int K,
                    const int32_t *order, T *y, hipStream_t s) {
   if (n_rows == 0)
     return;
   constexpr int CH = kChOf<T>;
   const bool fast = cred % CH == 0 && ncols % 16 == 0 && K <= 32 * kMaskWords &&
-                    aligned16(x) && aligned16(w);
+                    aligned16(x) && aligned16(wt);
   if (!fast) {
-    hipLaunchKernelGGL((conv_os_generic_kernel<T, WT>),
-                       dim3(ceil_div(n_rows * ncols, kThreads)), dim3(kThreads), 0,
-                       s, x, cred, w, ncols, bias, nbr, n_rows, K, order, y);
+    hipLaunchKernelGGL((conv_os_generic_kernel<T>), dim3(ceil_div(n_rows * ncols, kThreads)),
+                       dim3(kThreads), 0, s, x, cred, wt, ncols, bias, nbr, n_rows, K,
+                       order, y);
   } else if (ncols % 64 == 0) {
-    pick_csub<T, 64, WT>(x, cred, w, ncols, bias, nbr, n_rows, K, order, y, s);
+    pick_csub<T, 64>(x, cred, wt, ncols, bias, nbr, n_rows, K, order, y, s);
   } else if (ncols % 32 == 0) {
-    pick_csub<T, 32, WT>(x, cred, w, ncols, bias, nbr, n_rows, K, order, y, s);
+    pick_csub<T, 32>(x, cred, wt, ncols, bias, nbr, n_rows, K, order, y, s);
   } else {
-    pick_csub<T, 16, WT>(x, cred, w, ncols, bias, nbr, n_rows, K, order, y, s);
+    pick_csub<T, 16>(x, cred, wt, ncols, bias, nbr, n_rows, K, order, y, s);
   }
   RHIP_LAUNCH_CHECK();
 }
 
 template <typename T, int MT, int NTc>
-static void launch_dw(const T *x, int cin, const T *gy, int cout,
-                      const int64_t *kofs, int K, const int32_t *in_rows,
-                      const int32_t *out_rows, int64_t n_pairs, float *dw,
-                      hipStream_t s) {
+static void launch_dw_lds(const T *x, int cin, const T *gy, int cout,
+                          const int64_t *kofs, int K, const int32_t *in_rows,
+                          const int32_t *out_rows, int64_t n_pairs, float *dw,
+                          hipStream_t s) {
   const int tiles = (cin / MT) * (cout / NTc);
   // Aim for ~4 workgroups per CU over 256 CUs, at least 4 chunks each.
   const int64_t target = std::max<int64_t>(1, 1024 / tiles);
   int64_t ppb = ceil_div(n_pairs, target);
   ppb = std::max<int64_t>(4 * kPairChunk, ceil_div(ppb, kPairChunk) * kPairChunk);
   dim3 grid(static_cast<unsigned>(ceil_div(n_pairs, ppb)), tiles);
-  hipLaunchKernelGGL((conv_dw_kernel<T, MT, NTc>), grid, dim3(kThreads), 0, s, x,
-                     cin, gy, cout, kofs, K, in_rows, out_rows, n_pairs, ppb, dw);
+  hipLaunchKernelGGL((conv_dw_lds_kernel<T, MT, NTc>), grid, dim3(kThreads), 0, s, x, cin, gy,
+                     cout, kofs, K, in_rows, out_rows, n_pairs, ppb, dw);
 }
 
 template <typename T, int MT>
-static void pick_dw_n(const T *x, int cin, const T *gy, int cout,
-                      const int64_t *kofs, int K, const int32_t *in_rows,
-                      const int32_t *out_rows, int64_t n_pairs, float *dw,
-                      hipStream_t s) {
+static void pick_dw_lds_n(const T *x, int cin, const T *gy, int cout,
+                          const int64_t *kofs, int K, const int32_t *in_rows,
+                          const int32_t *out_rows, int64_t n_pairs, float *dw,
+                          hipStream_t s) {
   if (cout % 64 == 0)
-    launch_dw<T, MT, 64>(x, cin, gy, cout, kofs, K, in_rows, out_rows, n_pairs, dw, s);
+    launch_dw_lds<T, MT, 64>(x, cin, gy, cout, kofs, K, in_rows, out_rows, n_pairs, dw, s);
   else if (cout % 32 == 0)
-    launch_dw<T, MT, 32>(x, cin, gy, cout, kofs, K, in_rows, out_rows, n_pairs, dw, s);
+    launch_dw_lds<T, MT, 32>(x, cin, gy, cout, kofs, K, in_rows, out_rows, n_pairs, dw, s);
   else
-    launch_dw<T, MT, 16>(x, cin, gy, cout, kofs, K, in_rows, out_rows, n_pairs, dw, s);
+    launch_dw_lds<T, MT, 16>(x, cin, gy, cout, kofs, K, in_rows, out_rows, n_pairs, dw, s);
 }
 
+// fp32 result accumulated into dw (zeroed by the caller).
 template <typename T>
-static void run_dw(const T *x, int cin, const T *gy, int cout,
-                   const int64_t *kofs, int K, const int32_t *in_rows,
-                   const int32_t *out_rows, int64_t n_pairs, float *dw,
-                   hipStream_t s) {
+static void run_dw(const T *x, int cin, const T *gy, int cout, const int64_t *kofs, int K,
+                   const int32_t *in_rows, const int32_t *out_rows, int64_t n_pairs,
+                   float *dw, hipStream_t s) {
   if (n_pairs == 0)
     return;
   constexpr int VE = 16 / sizeof(T);
-  const bool fast = cin % 16 == 0 && cout % 16 == 0 && cin % VE == 0 &&
-                    cout % VE == 0 && aligned16(x) && aligned16(gy);
+  const bool fast = cin % 16 == 0 && cout % 16 == 0 && cin % VE == 0 && cout % VE == 0 &&
+                    aligned16(x) && aligned16(gy);
   if (!fast) {
     hipLaunchKernelGGL((conv_dw_generic_kernel<T>),
                        dim3(ceil_div(static_cast<int64_t>(K) * cin * cout, kThreads)),
-                       dim3(kThreads), 0, s, x, cin, gy, cout, kofs, K, in_rows,
-                       out_rows, dw);
+                       dim3(kThreads), 0, s, x, cin, gy, cout, kofs, K, in_rows, out_rows,
+                       dw);
   } else if (cin % 64 == 0) {
-    pick_dw_n<T, 64>(x, cin, gy, cout, kofs, K, in_rows, out_rows, n_pairs, dw, s);
+    pick_dw_lds_n<T, 64>(x, cin, gy, cout, kofs, K, in_rows, out_rows, n_pairs, dw, s);
   } else if (cin % 32 == 0) {
-    pick_dw_n<T, 32>(x, cin, gy, cout, kofs, K, in_rows, out_rows, n_pairs, dw, s);
+    pick_dw_lds_n<T, 32>(x, cin, gy, cout, kofs, K, in_rows, out_rows, n_pairs, dw, s);
   } else {
-    pick_dw_n<T, 16>(x, cin, gy, cout, kofs, K, in_rows, out_rows, n_pairs, dw, s);
+    pick_dw_lds_n<T, 16>(x, cin, gy, cout, kofs, K, in_rows, out_rows, n_pairs, dw, s);
   }
   RHIP_LAUNCH_CHECK();
 }
@@ -525,6 +556,11 @@ static void run_dw(const T *x, int cin, const T *gy, int cout,
 static void check_dtype(int32_t dtype) {
   if (dtype != RHIP_F32 && dtype != RHIP_BF16)
     throw Error(RHIP_ERR_UNSUPPORTED, "dtype must be RHIP_F32 or RHIP_BF16");
+}
+
+static size_t conv_ws_bytes(int32_t K, int32_t cin, int32_t cout) {
+  // transposed weights (forward) or the fp32 dW accumulator (bf16 dW)
+  return align_up(sizeof(float) * static_cast<size_t>(K) * cin * cout, 256) + 256;
 }
 
 } // namespace rhip
@@ -537,10 +573,7 @@ extern "C" int rhip_conv_workspace_bytes(int32_t K, int32_t cin, int32_t cout,
     RHIP_CHECK_ARG(bytes != nullptr, "bytes is null");
     RHIP_CHECK_ARG(K >= 1 && cin >= 1 && cout >= 1, "sizes must be positive");
     check_dtype(dtype);
-    // fp32 dW accumulator when the gradient is stored in bf16.
-    *bytes = dtype == RHIP_F32
-                 ? 256
-                 : align_up(sizeof(float) * static_cast<size_t>(K) * cin * cout, 256) + 256;
+    *bytes = conv_ws_bytes(K, cin, cout);
   });
 }
 
@@ -551,8 +584,6 @@ extern "C" int rhip_conv_forward(const void *x, int64_t n_in, int32_t cin,
                                  int32_t dtype, void *workspace,
                                  size_t workspace_bytes, hipStream_t stream) {
   return guarded([&] {
-    (void)workspace;
-    (void)workspace_bytes;
     check_dtype(dtype);
     RHIP_CHECK_ARG(K >= 1 && cin >= 1 && cout >= 1, "sizes must be positive");
     RHIP_CHECK_ARG(n_in >= 0 && n_out >= 0, "row counts must be >= 0");
@@ -560,14 +591,27 @@ extern "C" int rhip_conv_forward(const void *x, int64_t n_in, int32_t cin,
       return;
     RHIP_CHECK_ARG(y && weight && nbr, "y, weight and nbr are required");
     RHIP_CHECK_ARG(n_in == 0 || x != nullptr, "x is null");
-    if (dtype == RHIP_F32)
-      run_os<float, false>(static_cast<const float *>(x), cin,
-                           static_cast<const float *>(weight), cout, bias, nbr,
-                           n_out, K, out_order, static_cast<float *>(y), stream);
-    else
-      run_os<__bf16, false>(static_cast<const __bf16 *>(x), cin,
-                            static_cast<const __bf16 *>(weight), cout, bias, nbr,
-                            n_out, K, out_order, static_cast<__bf16 *>(y), stream);
+    RHIP_CHECK_ARG(workspace != nullptr, "workspace is null");
+    Carve cv(workspace, workspace_bytes);
+    const int64_t nw = static_cast<int64_t>(K) * cin * cout;
+    // the MFMA path reads W[k] column-wise: stage the [K, cout, cin] copy
+    if (dtype == RHIP_F32) {
+      float *wt = cv.take<float>(nw);
+      hipLaunchKernelGGL((transpose_w_kernel<float>), dim3(ceil_div(nw, kThreads)),
+                         dim3(kThreads), 0, stream, static_cast<const float *>(weight), K, cin,
+                         cout, wt);
+      RHIP_LAUNCH_CHECK();
+      run_os<float>(static_cast<const float *>(x), cin, wt, cout, bias, nbr, n_out, K,
+                    out_order, static_cast<float *>(y), stream);
+    } else {
+      __bf16 *wt = cv.take<__bf16>(nw);
+      hipLaunchKernelGGL((transpose_w_kernel<__bf16>), dim3(ceil_div(nw, kThreads)),
+                         dim3(kThreads), 0, stream, static_cast<const __bf16 *>(weight), K,
+                         cin, cout, wt);
+      RHIP_LAUNCH_CHECK();
+      run_os<__bf16>(static_cast<const __bf16 *>(x), cin, wt, cout, bias, nbr, n_out, K,
+                     out_order, static_cast<__bf16 *>(y), stream);
+    }
   });
 }
 
@@ -589,15 +633,15 @@ extern "C" int rhip_conv_backward_input(const void *grad_y, int64_t n_out,
       return;
     RHIP_CHECK_ARG(grad_x && weight && nbr_t, "grad_x, weight and nbr_t are required");
     RHIP_CHECK_ARG(n_out == 0 || grad_y != nullptr, "grad_y is null");
-    // dX rows gather dY rows; W[k] read as [n = cin][c = cout].
+    // dX rows gather dY rows; W[k] [cin][cout] is already [n = cin][c = cout].
     if (dtype == RHIP_F32)
-      run_os<float, true>(static_cast<const float *>(grad_y), cout,
-                          static_cast<const float *>(weight), cin, nullptr, nbr_t,
-                          n_in, K, in_order, static_cast<float *>(grad_x), stream);
+      run_os<float>(static_cast<const float *>(grad_y), cout,
+                    static_cast<const float *>(weight), cin, nullptr, nbr_t, n_in, K,
+                    in_order, static_cast<float *>(grad_x), stream);
     else
-      run_os<__bf16, true>(static_cast<const __bf16 *>(grad_y), cout,
-                           static_cast<const __bf16 *>(weight), cin, nullptr, nbr_t,
-                           n_in, K, in_order, static_cast<__bf16 *>(grad_x), stream);
+      run_os<__bf16>(static_cast<const __bf16 *>(grad_y), cout,
+                     static_cast<const __bf16 *>(weight), cin, nullptr, nbr_t, n_in, K,
+                     in_order, static_cast<__bf16 *>(grad_x), stream);
   });
 }
 
@@ -622,20 +666,18 @@ extern "C" int rhip_conv_backward_weight(
       Carve cv(workspace, workspace_bytes);
       acc = cv.take<float>(nw);
     }
-    hipLaunchKernelGGL(zero_f32_kernel, dim3(ceil_div(nw, kThreads)),
-                       dim3(kThreads), 0, stream, acc, nw);
+    hipLaunchKernelGGL(zero_f32_kernel, dim3(ceil_div(nw, kThreads)), dim3(kThreads), 0,
+                       stream, acc, nw);
     RHIP_LAUNCH_CHECK();
     if (dtype == RHIP_F32) {
-      run_dw<float>(static_cast<const float *>(x), cin,
-                    static_cast<const float *>(grad_y), cout, kmap_offsets, K,
-                    in_rows, out_rows, n_pairs, acc, stream);
+      run_dw<float>(static_cast<const float *>(x), cin, static_cast<const float *>(grad_y),
+                    cout, kmap_offsets, K, in_rows, out_rows, n_pairs, acc, stream);
     } else {
       run_dw<__bf16>(static_cast<const __bf16 *>(x), cin,
-                     static_cast<const __bf16 *>(grad_y), cout, kmap_offsets, K,
-                     in_rows, out_rows, n_pairs, acc, stream);
+                     static_cast<const __bf16 *>(grad_y), cout, kmap_offsets, K, in_rows,
+                     out_rows, n_pairs, acc, stream);
       hipLaunchKernelGGL((cast_from_f32_kernel<__bf16>), dim3(ceil_div(nw, kThreads)),
-                         dim3(kThreads), 0, stream, acc,
-                         static_cast<__bf16 *>(grad_w), nw);
+                         dim3(kThreads), 0, stream, acc, static_cast<__bf16 *>(grad_w), nw);
       RHIP_LAUNCH_CHECK();
     }
   });

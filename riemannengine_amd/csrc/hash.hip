@@ -10,8 +10,6 @@
 // one integer from the set's own column ranges, the first occurrence wins by
 // atomicMin on the row index, and the unique numbering is a prefix sum over
 // "is first" flags in row order, so the result is deterministic.
-#include <hipcub/hipcub.hpp>
-
 #include <algorithm>
 #include <climits>
 #include <cstring>
@@ -443,15 +441,6 @@ extern "C" int rhip_hash_lookup(const rhip_table *table, const int32_t *queries,
   });
 }
 
-static size_t radix_temp_bytes(int64_t n) {
-  size_t temp = 0;
-  (void)hipcub::DeviceRadixSort::SortPairs(nullptr, temp, (uint64_t *)nullptr,
-                                     (uint64_t *)nullptr, (int32_t *)nullptr,
-                                     (int32_t *)nullptr, static_cast<int>(n), 0,
-                                     64, (hipStream_t)0);
-  return temp;
-}
-
 extern "C" int rhip_order_workspace_bytes(int64_t n, size_t *bytes) {
   return guarded([&] {
     RHIP_CHECK_ARG(bytes != nullptr, "bytes is null");
@@ -460,7 +449,7 @@ extern "C" int rhip_order_workspace_bytes(int64_t n, size_t *bytes) {
     cv.take<uint64_t>(m);
     cv.take<uint64_t>(m);
     cv.take<int32_t>(m);
-    cv.take<char>(radix_temp_bytes(m));
+    cv.take<char>(sort_pairs_u64_bytes(m));
     *bytes = cv.used + 256;
   });
 }
@@ -486,14 +475,13 @@ extern "C" int rhip_spatial_order(const rhip_table *table, int32_t *order,
     uint64_t *keys_in = cv.take<uint64_t>(n);
     uint64_t *keys_out = cv.take<uint64_t>(n);
     int32_t *rows_in = cv.take<int32_t>(n);
-    size_t temp = radix_temp_bytes(n);
+    const size_t temp = sort_pairs_u64_bytes(n);
     void *tmp = cv.take<char>(temp);
     hipLaunchKernelGGL(pack_keys_kernel, dim3(nb), dim3(kBlock), 0, stream,
                        make_view(*table), n, keys_in, rows_in);
     RHIP_LAUNCH_CHECK();
-    RHIP_HIP(hipcub::DeviceRadixSort::SortPairs(
-        tmp, temp, keys_in, keys_out, rows_in, order, static_cast<int>(n), 0,
-        table->key_bits, stream));
+    sort_pairs_u64(tmp, temp, keys_in, keys_out, rows_in, order, n, table->key_bits,
+                   stream);
     if (pos) {
       hipLaunchKernelGGL(invert_perm_kernel, dim3(nb), dim3(kBlock), 0, stream,
                          n, order, pos);

@@ -86,6 +86,15 @@ struct Carve {
 
 // ---------------------------------------------------------------- device
 
+// Stable (key, int32 value) radix sorts over bits [0, end_bit) of the key
+// (sort.hip). *_bytes gives the scratch size for n items.
+size_t sort_pairs_u32_bytes(int64_t n);
+size_t sort_pairs_u64_bytes(int64_t n);
+void sort_pairs_u32(void *tmp, size_t tmp_bytes, const uint32_t *kin, uint32_t *kout,
+                    const int32_t *vin, int32_t *vout, int64_t n, int end_bit, hipStream_t s);
+void sort_pairs_u64(void *tmp, size_t tmp_bytes, const uint64_t *kin, uint64_t *kout,
+                    const int32_t *vin, int32_t *vout, int64_t n, int end_bit, hipStream_t s);
+
 // MurmurHash3 64-bit finalizer (Appleby, public domain) as the slot mixer.
 __device__ __forceinline__ uint64_t mix64(uint64_t k) {
   k ^= k >> 33;

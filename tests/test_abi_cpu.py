@@ -32,7 +32,7 @@ def test_library_exports_every_declared_symbol():
 
 
 def test_abi_version_and_struct_layout():
-    assert abi.lib().rhip_abi_version() == 1
+    assert abi.lib().rhip_abi_version() == 2
     # void*, int64, void*, int64, 3 x int32, 3 x int32[8] -> 140 bytes, padded to 144
     assert ctypes.sizeof(abi.RhipTable) == 144
 
@@ -40,7 +40,7 @@ def test_abi_version_and_struct_layout():
 def test_workspace_queries():
     L = abi.lib()
     assert abi._sizeq(L.rhip_hash_workspace_bytes, 1000, 4) > 1000 * 8
-    assert abi._sizeq(L.rhip_kmap_workspace_bytes, 1000, 27) > 0
+    assert abi._sizeq(L.rhip_kmap_workspace_bytes, 1000, 1000, 27) > 27 * 1000 * 4
     assert abi._sizeq(L.rhip_conv_workspace_bytes, 27, 64, 64, abi.BF16) >= 27 * 64 * 64 * 4
     assert L.rhip_table_bytes(100) == 256 * 16  # next power of two >= 2n, 16 B slots
 
@@ -50,8 +50,8 @@ def test_workspace_queries():
                                     ctypes.byref(t), None), "ncol"),
     (lambda L, t: L.rhip_hash_build(None, -1, 4, None, 0, None, 0, None, None, None,
                                     ctypes.byref(t), None), "row count"),
-    (lambda L, t: L.rhip_kmap_count(ctypes.byref(t), None, None, 10, 0, None, None, None, 0,
-                                    None, None, None), "K must"),
+    (lambda L, t: L.rhip_kmap_count(ctypes.byref(t), None, None, 10, 0, None, None, 0, None,
+                                    None, None, None, None), "K must"),
     (lambda L, t: L.rhip_conv_forward(None, 1, 4, None, 27, 8, None, None, None, 1, None, 7,
                                       None, 0, None), "dtype"),
 ])

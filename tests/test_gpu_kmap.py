@@ -16,20 +16,46 @@ def _ref_map(cin, cout, off):
     return kofs, oracle.canonical_pairs(kofs, ir, orr)
 
 
+def _inverse_perm(order, n):
+    order = np.asarray(order, np.int64)
+    np.testing.assert_array_equal(np.sort(order), np.arange(n))  # a permutation
+    pos = np.empty(n, np.int64)
+    pos[order] = np.arange(n)
+    return pos
+
+
+def _mask_groups(table):
+    """Number of runs of equal neighbour masks along the processing order."""
+    m = (table >= 0).T
+    if m.shape[0] < 2:
+        return m.shape[0]
+    return int(1 + np.any(m[1:] != m[:-1], axis=1).sum())
+
+
 def _check_tables(km, tin, tout):
-    """nbr/nbr_t hold exactly the pairs, at the map's processing positions."""
+    """nbr/nbr_t hold exactly the pairs at the map's processing positions;
+    the orders are permutations that group equal neighbour masks."""
     nbr = km.nbr.cpu().numpy()
     nbr_t = km.nbr_t.cpu().numpy()
-    oo, io = tout.order.cpu().numpy(), tin.order.cpu().numpy()
+    pos_out = _inverse_perm(km.out_order.cpu().numpy(), km.n_out)
+    pos_in = _inverse_perm(km.in_order.cpu().numpy(), km.n_in)
     ks = np.repeat(np.arange(km.K), np.diff(km.offsets_host))
     ir, orr = km.in_rows.cpu().numpy(), km.out_rows.cpu().numpy()
     dense = np.full((km.K, km.n_out), -1, np.int64)
-    dense[ks, tout.pos.cpu().numpy()[orr]] = ir
+    dense[ks, pos_out[orr]] = ir
     np.testing.assert_array_equal(nbr, dense)
     dense_t = np.full((km.K, km.n_in), -1, np.int64)
-    dense_t[ks, tin.pos.cpu().numpy()[ir]] = orr
+    dense_t[ks, pos_in[ir]] = orr
     np.testing.assert_array_equal(nbr_t, dense_t)
-    assert oo.shape[0] == km.n_out and io.shape[0] == km.n_in
+    # pairs of one offset come out in processing order of the output rows
+    for k in range(km.K):
+        a, b = km.offsets_host[k], km.offsets_host[k + 1]
+        assert np.all(np.diff(pos_out[orr[a:b]]) > 0)
+    if km.K <= 128:
+        # equal masks are contiguous: runs == distinct masks
+        for tab in (nbr, nbr_t):
+            distinct = len(np.unique((tab >= 0).T, axis=0)) if tab.shape[1] else 0
+            assert _mask_groups(tab) == distinct
 
 
 @pytest.mark.parametrize("D,ks,dil,ts,region", [
