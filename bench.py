@@ -94,6 +94,19 @@ def conv_traffic(n_in, n_out, P, K, cin, cout, s):
     }
 
 
+def measured_traffic(dtype: str, pass_name: str):
+    """HBM bytes per launch of a pass's kernel, from the committed rocprofv3
+    FETCH_SIZE / WRITE_SIZE passes (profiles/traffic_config2.json, scaled by
+    the counters' reading for a device copy of known size); None if absent."""
+    path = os.path.join(ROOT, "profiles", "traffic_config2.json")
+    try:
+        with open(path) as f:
+            rec = json.load(f)[dtype][pass_name]
+    except (OSError, KeyError, ValueError):
+        return None
+    return round(float(rec["traffic_bytes"]))
+
+
 def cpu_model() -> str:
     try:
         with open("/proc/cpuinfo") as f:
@@ -231,7 +244,7 @@ def main():
         roof = {"bound": "hbm", "achieved": round(B / dur_s / 1e9, 1),
                 "peak": PEAK_HBM_GBS, "unit": "GB/s"}
     roof["frac"] = round(roof["achieved"] / roof["peak"], 4)
-    roof["traffic"] = None
+    roof["traffic"] = measured_traffic(args.dtype, dom)
     roof["kernel"] = {"forward": "conv_os_kernel (forward)",
                       "backward_input": "conv_os_kernel (dX, transposed weights)",
                       "backward_weight": "conv_dw_lds_kernel"}[dom]
