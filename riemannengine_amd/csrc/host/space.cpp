@@ -1,0 +1,522 @@
+// CoordinateMapKey, region offsets, KernelGenerator and the HIP-backed
+// CoordinateManager (coordinate maps + kernel-map cache).
+#include <ATen/DeviceGuard.h>
+#include <c10/hip/HIPStream.h>
+
+#include <algorithm>
+#include <limits>
+#include <random>
+#include <sstream>
+
+#include "riemann.hpp"
+
+namespace riemann {
+
+void check_rhip(int status, const char *what) {
+  TORCH_CHECK(status == RHIP_OK, what, " failed (status ", status, "): ", rhip_last_error());
+}
+
+namespace {
+
+hipStream_t current_stream(const at::Device &device) {
+  return c10::hip::getCurrentHIPStream(device.index()).stream();
+}
+
+at::Tensor device_bytes(size_t bytes, const at::Device &device) {
+  return torch::empty({static_cast<int64_t>(std::max<size_t>(bytes, 1))},
+                      torch::TensorOptions().dtype(torch::kUInt8).device(device));
+}
+
+std::string stride_string(const stride_type &s) {
+  std::ostringstream o;
+  o << "[";
+  for (size_t i = 0; i < s.size(); ++i)
+    o << (i ? ", " : "") << s[i];
+  o << "]";
+  return o.str();
+}
+
+stride_type to_stride_vector(torch::IntArrayRef v) {
+  stride_type out;
+  for (auto x : v) {
+    TORCH_CHECK(x > 0, "kernel parameters must be positive");
+    out.push_back(static_cast<uint32_t>(x));
+  }
+  return out;
+}
+
+} // namespace
+
+// ------------------------------------------------------------ key
+
+CoordinateMapKey::CoordinateMapKey(size_type coordinate_size)
+    : key_set_(false), coordinate_size_(coordinate_size) {}
+
+CoordinateMapKey::CoordinateMapKey(size_type coordinate_size, const coordinate_map_key_type &key)
+    : key_set_(true), coordinate_size_(coordinate_size), key_(key) {
+  TORCH_CHECK(coordinate_size_ - 1 == key_.first.size(),
+              "Invalid tensor_stride: ", stride_string(key_.first),
+              " coordinate_size: ", coordinate_size_);
+}
+
+CoordinateMapKey::CoordinateMapKey(stride_type tensor_stride, std::string string_id)
+    : key_set_(true), coordinate_size_(static_cast<size_type>(tensor_stride.size() + 1)),
+      key_(std::move(tensor_stride), std::move(string_id)) {}
+
+void CoordinateMapKey::set_key(stride_type tensor_stride, std::string string_id) {
+  TORCH_CHECK(coordinate_size_ - 1 == tensor_stride.size(), "Invalid tensor_stride size: ",
+              stride_string(tensor_stride), " coordinate_size: ", coordinate_size_);
+  key_ = {std::move(tensor_stride), std::move(string_id)};
+  key_set_ = true;
+}
+
+void CoordinateMapKey::set_key(const coordinate_map_key_type &key) {
+  set_key(key.first, key.second);
+}
+
+coordinate_map_key_type CoordinateMapKey::get_key() const {
+  TORCH_CHECK(key_set_, "Key not set");
+  return key_;
+}
+
+uint64_t CoordinateMapKey::hash() const {
+  uint64_t h = 1469598103934665603ull; // FNV-1a over the stride, then the id
+  for (auto v : key_.first) {
+    h ^= v;
+    h *= 1099511628211ull;
+  }
+  return h ^ std::hash<std::string>{}(key_.second);
+}
+
+bool CoordinateMapKey::operator==(const CoordinateMapKey &other) const {
+  if (!key_set_ || !other.key_set_)
+    return false;
+  return key_ == other.key_;
+}
+
+std::string CoordinateMapKey::to_string() const {
+  std::ostringstream o;
+  o << "coordinate map key:" << stride_string(key_.first);
+  if (!key_.second.empty())
+    o << ":" << key_.second;
+  return o.str();
+}
+
+// ------------------------------------------------------------ regions
+
+at::Tensor normalize_region_offsets(const at::Tensor &offsets, int dimension) {
+  TORCH_CHECK(dimension > 0, "CUSTOM region dimension must be positive");
+  TORCH_CHECK(offsets.defined(), "region_offsets must be defined for CUSTOM");
+  TORCH_CHECK(offsets.layout() == at::kStrided && offsets.dim() == 2,
+              "region_offsets must be a dense [N, D] tensor");
+  TORCH_CHECK(offsets.size(0) > 0 && offsets.size(0) <= std::numeric_limits<int>::max(),
+              "region_offsets must have a non-empty, representable volume");
+  TORCH_CHECK(offsets.size(1) == dimension, "region_offsets dimension mismatch");
+  TORCH_CHECK(offsets.scalar_type() == at::kInt || offsets.scalar_type() == at::kLong,
+              "region_offsets must contain int32 or int64 spatial offsets");
+  auto host = offsets.to(at::kCPU).contiguous();
+  if (host.scalar_type() == at::kLong) {
+    TORCH_CHECK(host.min().item<int64_t>() >= std::numeric_limits<int32_t>::min() &&
+                    host.max().item<int64_t>() <= std::numeric_limits<int32_t>::max(),
+                "region_offsets values must fit int32");
+  }
+  return host.to(at::kInt).clone();
+}
+
+int region_volume(RegionType::Type region, const stride_type &kernel_size,
+                  const at::Tensor &custom) {
+  switch (region) {
+  case RegionType::HYPER_CUBE: {
+    int v = 1;
+    for (auto k : kernel_size)
+      v *= static_cast<int>(k);
+    return v;
+  }
+  case RegionType::HYPER_CROSS: {
+    int v = 1;
+    for (auto k : kernel_size)
+      v += static_cast<int>(k) - 1;
+    return v;
+  }
+  case RegionType::CUSTOM:
+    return custom.defined() ? static_cast<int>(custom.size(0)) : 0;
+  }
+  TORCH_CHECK(false, "Unknown region type");
+}
+
+at::Tensor region_offsets(RegionType::Type region, const stride_type &kernel_size,
+                          const stride_type &dilation, const stride_type &tensor_stride,
+                          const at::Tensor &custom) {
+  const int D = static_cast<int>(kernel_size.size());
+  TORCH_CHECK(dilation.size() == kernel_size.size() && tensor_stride.size() == kernel_size.size(),
+              "kernel size, dilation and tensor stride must have the same length");
+  const int K = region_volume(region, kernel_size, custom);
+  auto out = torch::zeros({K, D}, torch::kInt64);
+  auto o = out.accessor<int64_t, 2>();
+  std::vector<int64_t> step(D);
+  for (int i = 0; i < D; ++i)
+    step[i] = static_cast<int64_t>(dilation[i]) * tensor_stride[i];
+  if (region == RegionType::HYPER_CUBE) {
+    // axis 0 varies fastest; odd sizes centre on zero, even sizes start at 0
+    for (int k = 0; k < K; ++k) {
+      int64_t rem = k;
+      for (int i = 0; i < D; ++i) {
+        const int64_t ks = kernel_size[i];
+        const int64_t idx = rem % ks;
+        rem /= ks;
+        o[k][i] = (ks % 2 == 0 ? idx : idx - ks / 2) * step[i];
+      }
+    }
+  } else if (region == RegionType::HYPER_CROSS) {
+    // the centre, then per axis: +1 .. +r, then -r .. -1
+    int k = 1;
+    for (int axis = 0; axis < D; ++axis) {
+      const int64_t r = (static_cast<int64_t>(kernel_size[axis]) - 1) / 2;
+      for (int64_t ind = 0; ind < static_cast<int64_t>(kernel_size[axis]) - 1; ++ind, ++k)
+        o[k][axis] = (ind < r ? ind + 1 : ind - 2 * r) * step[axis];
+    }
+  } else {
+    auto c = normalize_region_offsets(custom, D);
+    auto ca = c.accessor<int32_t, 2>();
+    for (int k = 0; k < K; ++k)
+      for (int i = 0; i < D; ++i)
+        o[k][i] = static_cast<int64_t>(ca[k][i]) * step[i];
+  }
+  TORCH_CHECK(K == 0 || (out.abs().max().item<int64_t>() <= std::numeric_limits<int32_t>::max()),
+              "Scaled offsets must fit the coordinate type");
+  return out.to(torch::kInt32);
+}
+
+// ------------------------------------------------------ KernelGenerator
+
+KernelGenerator::KernelGenerator(torch::IntArrayRef kernel_size, torch::IntArrayRef stride,
+                                 torch::IntArrayRef dilation, bool is_transpose,
+                                 RegionType::Type region_type, at::Tensor offsets,
+                                 bool expand_coordinates, int dimension)
+    : kernel_size_(to_stride_vector(kernel_size)), kernel_stride_(to_stride_vector(stride)),
+      kernel_dilation_(to_stride_vector(dilation)), is_transpose_(is_transpose),
+      region_type_(region_type), region_offsets_(std::move(offsets)),
+      expand_coordinates_(expand_coordinates), D_(dimension), kernel_volume_(0) {
+  if (D_ <= 0)
+    D_ = static_cast<int>(kernel_size_.size());
+  // scalars broadcast across every spatial axis (engine/grid/stencil.cpp:108-117)
+  if (kernel_size_.size() == 1 && D_ > 1)
+    kernel_size_.assign(D_, kernel_size_[0]);
+  if (kernel_stride_.size() == 1 && D_ > 1)
+    kernel_stride_.assign(D_, kernel_stride_[0]);
+  if (kernel_dilation_.size() == 1 && D_ > 1)
+    kernel_dilation_.assign(D_, kernel_dilation_[0]);
+  TORCH_CHECK(kernel_size_.size() == static_cast<size_t>(D_), "kernel_size dimension mismatch");
+  TORCH_CHECK(kernel_stride_.size() == static_cast<size_t>(D_), "kernel_stride dimension mismatch");
+  TORCH_CHECK(kernel_dilation_.size() == static_cast<size_t>(D_),
+              "kernel_dilation dimension mismatch");
+  if (region_type_ == RegionType::CUSTOM) {
+    region_offsets_ = normalize_region_offsets(region_offsets_, D_);
+  } else if (region_offsets_.defined()) {
+    TORCH_CHECK(region_offsets_.numel() == 0,
+                "region_offsets must be empty for HYPER_CUBE/HYPER_CROSS");
+  }
+  kernel_volume_ = region_volume(region_type_, kernel_size_, region_offsets_);
+}
+
+KernelGenerator::KernelParams KernelGenerator::get_kernel(const stride_type &tensor_stride,
+                                                          bool is_transpose) const {
+  (void)is_transpose;
+  TORCH_CHECK(tensor_stride.size() == static_cast<size_t>(D_), "tensor_stride dimension mismatch");
+  for (auto s : tensor_stride)
+    TORCH_CHECK(s > 0, "tensor_stride must be positive");
+  KernelParams p;
+  p.kernel_size = kernel_size_;
+  p.kernel_stride = kernel_stride_;
+  p.kernel_dilation = kernel_dilation_;
+  p.region_type = region_type_;
+  p.region_offsets = region_type_ == RegionType::CUSTOM
+                         ? region_offsets_.clone()
+                         : torch::empty({0, D_}, torch::kInt32);
+  p.expand_coordinates = expand_coordinates_;
+  p.D = D_;
+  return p;
+}
+
+// --------------------------------------------------------- kernel maps
+
+HipKernelMap HipKernelMap::swapped() const {
+  HipKernelMap m;
+  m.K = K;
+  m.n_in = n_out;
+  m.n_out = n_in;
+  m.offsets_host = offsets_host;
+  m.offsets = offsets;
+  m.in_rows = out_rows;
+  m.out_rows = in_rows;
+  m.nbr = nbr_t;
+  m.nbr_t = nbr;
+  m.in_order = out_order;
+  m.out_order = in_order;
+  return m;
+}
+
+std::pair<std::vector<at::Tensor>, std::vector<at::Tensor>> HipKernelMap::per_offset() const {
+  std::vector<at::Tensor> ins, outs;
+  for (int k = 0; k < K; ++k) {
+    const int64_t a = offsets_host[k], b = offsets_host[k + 1];
+    ins.push_back(in_rows.slice(0, a, b).to(torch::kLong));
+    outs.push_back(out_rows.slice(0, a, b).to(torch::kLong));
+  }
+  return {ins, outs};
+}
+
+// ------------------------------------------------------ CoordinateManager
+
+CoordinateManager::CoordinateManager(int D, CoordinateMapBackend::Type backend,
+                                     GPUMemoryAllocatorBackend::Type alloc_type,
+                                     RiemannAlgorithm::Mode algo)
+    : D_(D), backend_(backend), alloc_type_(alloc_type), algo_(algo) {
+  TORCH_CHECK(D > 0 && D + 1 <= RHIP_MAX_COLS, "dimension must be in [1, ", RHIP_MAX_COLS - 1,
+              "]");
+  TORCH_CHECK(backend == CoordinateMapBackend::CUDA,
+              "this build implements the device (HIP) coordinate-map backend only; "
+              "there is no CPU coordinate manager");
+}
+
+coordinate_map_key_type CoordinateManager::random_key(const stride_type &tensor_stride,
+                                                      const std::string &string_id) const {
+  static thread_local std::mt19937_64 rng{std::random_device{}()};
+  static const char alphabet[] = "abcdefghijklmnopqrstuvwxyz0123456789";
+  coordinate_map_key_type key;
+  do {
+    std::string id = string_id + "_";
+    for (int i = 0; i < 8; ++i)
+      id.push_back(alphabet[rng() % (sizeof(alphabet) - 1)]);
+    key = {tensor_stride, id};
+  } while (maps_.count(key));
+  return key;
+}
+
+CoordinateMapHIP CoordinateManager::build_map(const at::Tensor &coords,
+                                              const stride_type &tensor_stride,
+                                              at::Tensor *mapping, at::Tensor *inverse) const {
+  const auto dev = coords.device();
+  at::DeviceGuard guard(dev);
+  const hipStream_t st = current_stream(dev);
+  const int64_t n = coords.size(0);
+  const int32_t ncol = static_cast<int32_t>(coords.size(1));
+  CoordinateMapHIP m;
+  m.tensor_stride = tensor_stride;
+  auto iopt = torch::TensorOptions().device(dev);
+  m.slots = device_bytes(rhip_table_bytes(n), dev);
+  size_t ws_bytes = 0;
+  check_rhip(rhip_hash_workspace_bytes(n, ncol, &ws_bytes), "rhip_hash_workspace_bytes");
+  auto ws = device_bytes(ws_bytes, dev);
+  m.storage = torch::empty({std::max<int64_t>(n, 1), ncol}, iopt.dtype(torch::kInt32));
+  auto map_t = torch::empty({std::max<int64_t>(n, 1)}, iopt.dtype(torch::kInt64));
+  at::Tensor inv_t;
+  if (inverse)
+    inv_t = torch::empty({std::max<int64_t>(n, 1)}, iopt.dtype(torch::kInt64));
+  check_rhip(rhip_hash_build(coords.data_ptr<int32_t>(), n, ncol, m.slots.data_ptr(),
+                             m.slots.numel(), ws.data_ptr(), ws.numel(),
+                             m.storage.data_ptr<int32_t>(), map_t.data_ptr<int64_t>(),
+                             inverse ? inv_t.data_ptr<int64_t>() : nullptr, &m.table, st),
+             "rhip_hash_build");
+  const int64_t nu = m.table.n_unique;
+  m.coords = m.storage.slice(0, 0, nu);
+  m.order = torch::empty({std::max<int64_t>(nu, 1)}, iopt.dtype(torch::kInt32));
+  if (nu > 0) {
+    size_t ob = 0;
+    check_rhip(rhip_order_workspace_bytes(nu, &ob), "rhip_order_workspace_bytes");
+    auto ows = device_bytes(ob, dev);
+    check_rhip(rhip_spatial_order(&m.table, m.order.data_ptr<int32_t>(), nullptr, ows.data_ptr(),
+                                  ows.numel(), st),
+               "rhip_spatial_order");
+  }
+  m.order = m.order.slice(0, 0, nu);
+  if (mapping)
+    *mapping = map_t.slice(0, 0, nu);
+  if (inverse)
+    *inverse = inv_t.slice(0, 0, n);
+  return m;
+}
+
+std::pair<CoordinateMapKey, std::pair<at::Tensor, at::Tensor>>
+CoordinateManager::insert_and_map(const at::Tensor &coordinates, stride_type tensor_stride,
+                                  std::string string_id) {
+  // Argument checks of CoordinateMapManager::insert_and_map_cpp
+  // (engine/grid/space_impl.hpp:268-282), with the device backend required.
+  TORCH_CHECK(coordinates.is_contiguous(), "coordinates must be contiguous");
+  TORCH_CHECK(coordinates.scalar_type() == torch::kInt, "coordinates must be int32");
+  TORCH_CHECK(coordinates.is_cuda(),
+              "coordinates must be a device tensor (the HIP path has no CPU fallback)");
+  TORCH_CHECK(coordinates.dim() == 2, "coordinates must be a 2-D tensor");
+  const auto coordinate_size = static_cast<size_type>(coordinates.size(1));
+  TORCH_CHECK(coordinate_size - 1 == tensor_stride.size(),
+              "The coordinate dimension (coordinate_size - 1): ", coordinate_size - 1,
+              " must match the size of tensor stride: ", stride_string(tensor_stride));
+  TORCH_CHECK(static_cast<int>(coordinate_size) == D_ + 1,
+              "coordinates have ", coordinate_size, " columns; this manager expects ", D_ + 1);
+  coordinate_map_key_type key{tensor_stride, string_id};
+  if (maps_.count(key))
+    key = random_key(tensor_stride, string_id);
+  at::Tensor mapping, inverse;
+  maps_.emplace(key, build_map(coordinates, tensor_stride, &mapping, &inverse));
+  return {CoordinateMapKey(coordinate_size, key), {mapping, inverse}};
+}
+
+CoordinateMapKey CoordinateManager::stride(const CoordinateMapKey &in_key,
+                                           const stride_type &kernel_stride,
+                                           std::string string_id) {
+  const auto ik = in_key.get_key();
+  auto it = maps_.find(ik);
+  TORCH_CHECK(it != maps_.end(), "coordinate map not found: ", in_key.to_string());
+  TORCH_CHECK(kernel_stride.size() == ik.first.size(), "stride size mismatch");
+  stride_type out_stride(ik.first);
+  for (size_t i = 0; i < out_stride.size(); ++i) {
+    TORCH_CHECK(kernel_stride[i] > 0, "kernel stride must be positive");
+    out_stride[i] *= kernel_stride[i];
+  }
+  coordinate_map_key_type out_key{out_stride, string_id.empty() ? ik.second : string_id};
+  if (!maps_.count(out_key)) {
+    const CoordinateMapHIP &in_map = it->second;
+    const auto dev = in_map.coords.device();
+    at::DeviceGuard guard(dev);
+    auto strided = torch::empty_like(in_map.coords);
+    std::vector<int32_t> s(out_stride.begin(), out_stride.end());
+    if (in_map.size() > 0)
+      check_rhip(rhip_stride_coords(in_map.coords.data_ptr<int32_t>(), in_map.size(),
+                                    static_cast<int32_t>(in_map.coords.size(1)), s.data(),
+                                    strided.data_ptr<int32_t>(), current_stream(dev)),
+                 "rhip_stride_coords");
+    maps_.emplace(out_key, build_map(strided, out_stride, nullptr, nullptr));
+  }
+  return CoordinateMapKey(static_cast<size_type>(ik.first.size() + 1), out_key);
+}
+
+const CoordinateMapHIP &CoordinateManager::coordinate_map(const CoordinateMapKey &key) const {
+  auto it = maps_.find(key.get_key());
+  TORCH_CHECK(it != maps_.end(), "coordinate map not found: ", key.to_string());
+  return it->second;
+}
+
+at::Tensor CoordinateManager::get_coordinates(const CoordinateMapKey &key) const {
+  return coordinate_map(key).coords;
+}
+
+uint32_t CoordinateManager::size(const CoordinateMapKey &key) const {
+  return static_cast<uint32_t>(coordinate_map(key).size());
+}
+
+bool CoordinateManager::exists(const CoordinateMapKey &key) const {
+  return key.is_key_set() && maps_.count(key.get_key()) > 0;
+}
+
+HipKernelMap CoordinateManager::generate(const CoordinateMapHIP &in_map,
+                                         const CoordinateMapHIP &out_map,
+                                         const at::Tensor &offsets_host) const {
+  const auto dev = in_map.coords.device();
+  at::DeviceGuard guard(dev);
+  const hipStream_t st = current_stream(dev);
+  const int32_t K = static_cast<int32_t>(offsets_host.size(0));
+  const int64_t n_in = in_map.size(), n_out = out_map.size();
+  auto iopt = torch::TensorOptions().device(dev).dtype(torch::kInt32);
+  auto offsets = offsets_host.to(dev).contiguous();
+  HipKernelMap m;
+  m.K = K;
+  m.n_in = n_in;
+  m.n_out = n_out;
+  size_t ws_bytes = 0;
+  check_rhip(rhip_kmap_workspace_bytes(n_in, n_out, K, &ws_bytes), "rhip_kmap_workspace_bytes");
+  auto ws = device_bytes(ws_bytes, dev);
+  auto nbr = torch::empty({K, std::max<int64_t>(n_out, 1)}, iopt);
+  auto out_order = torch::empty({std::max<int64_t>(n_out, 1)}, iopt);
+  m.offsets = torch::empty({K + 1}, iopt.dtype(torch::kInt64));
+  m.offsets_host.assign(K + 1, 0);
+  check_rhip(rhip_kmap_count(&in_map.table, out_map.coords.data_ptr<int32_t>(),
+                             out_map.order.data_ptr<int32_t>(), n_out, K,
+                             offsets.data_ptr<int32_t>(), ws.data_ptr(), ws.numel(),
+                             nbr.data_ptr<int32_t>(), out_order.data_ptr<int32_t>(),
+                             m.offsets.data_ptr<int64_t>(), m.offsets_host.data(), st),
+             "rhip_kmap_count");
+  const int64_t P = m.offsets_host[K];
+  auto in_rows = torch::empty({std::max<int64_t>(P, 1)}, iopt);
+  auto out_rows = torch::empty({std::max<int64_t>(P, 1)}, iopt);
+  auto nbr_t = torch::empty({K, std::max<int64_t>(n_in, 1)}, iopt);
+  auto in_order = torch::empty({std::max<int64_t>(n_in, 1)}, iopt);
+  check_rhip(rhip_kmap_fill(nbr.data_ptr<int32_t>(), out_order.data_ptr<int32_t>(), n_out, K,
+                            in_map.order.data_ptr<int32_t>(), n_in, ws.data_ptr(), ws.numel(),
+                            in_rows.data_ptr<int32_t>(), out_rows.data_ptr<int32_t>(),
+                            nbr_t.data_ptr<int32_t>(), in_order.data_ptr<int32_t>(), st),
+             "rhip_kmap_fill");
+  m.in_rows = in_rows.slice(0, 0, P);
+  m.out_rows = out_rows.slice(0, 0, P);
+  m.nbr = nbr.slice(1, 0, n_out);
+  m.nbr_t = nbr_t.slice(1, 0, n_in);
+  m.in_order = in_order.slice(0, 0, n_in);
+  m.out_order = out_order.slice(0, 0, n_out);
+  return m;
+}
+
+const HipKernelMap &CoordinateManager::kernel_map(
+    const CoordinateMapKey &in_key, const CoordinateMapKey &out_key,
+    const stride_type &kernel_size, const stride_type &kernel_stride,
+    const stride_type &kernel_dilation, RegionType::Type region_type,
+    const at::Tensor &offsets, bool is_transpose, bool is_pool) {
+  const size_t kdim = kernel_size.size();
+  TORCH_CHECK(kdim == kernel_stride.size(), "kernel size mismatch");
+  TORCH_CHECK(kdim == kernel_dilation.size(), "kernel size mismatch");
+  TORCH_CHECK(!(is_pool && region_type != RegionType::CUSTOM && kernel_stride == kernel_size),
+              "pooling stride maps are not part of this build");
+  at::Tensor custom;
+  std::vector<int32_t> custom_values;
+  if (region_type == RegionType::CUSTOM) {
+    custom = normalize_region_offsets(offsets, static_cast<int>(kdim));
+    custom_values.assign(custom.data_ptr<int32_t>(), custom.data_ptr<int32_t>() + custom.numel());
+  }
+  const kernel_map_key_type key = std::make_tuple(in_key.get_key(), out_key.get_key(),
+                                                  kernel_size, kernel_stride, kernel_dilation,
+                                                  region_type, is_transpose, is_pool);
+  auto find = [&](const kernel_map_key_type &k) -> const HipKernelMap * {
+    if (region_type == RegionType::CUSTOM) {
+      auto it = custom_maps_.find({k, custom_values});
+      return it == custom_maps_.end() ? nullptr : &it->second;
+    }
+    auto it = kernel_maps_.find(k);
+    return it == kernel_maps_.end() ? nullptr : &it->second;
+  };
+  auto store = [&](const kernel_map_key_type &k, HipKernelMap m) -> const HipKernelMap & {
+    if (region_type == RegionType::CUSTOM)
+      return custom_maps_[{k, custom_values}] = std::move(m);
+    return kernel_maps_[k] = std::move(m);
+  };
+  if (const HipKernelMap *hit = find(key))
+    return *hit;
+
+  const CoordinateMapHIP &in_map = coordinate_map(in_key);
+  const CoordinateMapHIP &out_map = coordinate_map(out_key);
+  TORCH_CHECK(static_cast<int64_t>(kdim) + 1 == in_map.coords.size(1), "kernel size mismatch");
+  TORCH_CHECK(static_cast<int64_t>(kdim) + 1 == out_map.coords.size(1), "kernel size mismatch");
+
+  if (!is_transpose) {
+    // region on the input map's tensor stride (space_impl.hpp:626-636)
+    auto off = region_offsets(region_type, kernel_size, kernel_dilation, in_map.tensor_stride,
+                              custom);
+    return store(key, generate(in_map, out_map, off));
+  }
+  const kernel_map_key_type fwd_key =
+      std::make_tuple(out_key.get_key(), in_key.get_key(), kernel_size, kernel_stride,
+                      kernel_dilation, region_type, false, is_pool);
+  if (const HipKernelMap *fwd = find(fwd_key))
+    return store(key, fwd->swapped());
+  // generated out -> in with the region on the output (finer) map's stride,
+  // then swapped (space_impl.hpp:649-697)
+  auto off = region_offsets(region_type, kernel_size, kernel_dilation, out_map.tensor_stride,
+                            custom);
+  return store(key, generate(out_map, in_map, off).swapped());
+}
+
+std::string CoordinateManager::to_string() const {
+  std::ostringstream o;
+  o << "CoordinateManager(D=" << D_ << ", maps=" << maps_.size()
+    << ", kernel_maps=" << kernel_map_cache_size() << ")";
+  return o.str();
+}
+
+} // namespace riemann
