@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define RHIP_ABI_VERSION 2
+#define RHIP_ABI_VERSION 3
 #define RHIP_MAX_COLS 8 /* batch column + up to 7 spatial axes */
 
 typedef enum rhip_status {
@@ -177,8 +177,12 @@ int rhip_kmap_fill(const int32_t *nbr, const int32_t *out_order, int64_t n_out,
 
 /* ----------------------------------------------------------- convolution */
 
+/* Workspace of one layer's forward, input-gradient and weight-gradient calls
+ * (the same buffer may serve all three, one call at a time) for a kernel map
+ * with n_in input rows, n_out output rows and n_pairs pairs. */
 int rhip_conv_workspace_bytes(int32_t K, int32_t cin, int32_t cout,
-                              int32_t dtype, size_t *bytes);
+                              int32_t dtype, int64_t n_in, int64_t n_out,
+                              int64_t n_pairs, size_t *bytes);
 
 /*
  * Y[out_order[j]] = sum_k X[nbr[k*n_out+j]] @ W[k] (+ bias), fp32 accumulate.
@@ -210,6 +214,7 @@ int rhip_conv_backward_input(const void *grad_y, int64_t n_out, int32_t cout,
 /*
  * grad_w[k] = sum over pairs p of offset k of x[in_rows[p]]^T grad_y[out_rows[p]]
  * with fp32 accumulation; grad_w [K, cin, cout] in `dtype` is overwritten.
+ * Deterministic: partial sums per pair range are added in a fixed order.
  * kmap_offsets is the device CSR from rhip_kmap_count.
  * Replaces the dW half of MmBackward in the reference's autograd graph
  * (engine/nn/conv.cpp:62) and sparse_convolution_backward_cpu_kernel's

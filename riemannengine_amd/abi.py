@@ -65,7 +65,8 @@ def _declare(lib):
                                            _vp, _sz, _vp, _vp, _vp, _P(_i64), _vp]),
         "rhip_kmap_fill": (ctypes.c_int, [_vp, _vp, _i64, _i32, _vp, _i64, _vp, _sz,
                                           _vp, _vp, _vp, _vp, _vp]),
-        "rhip_conv_workspace_bytes": (ctypes.c_int, [_i32, _i32, _i32, _i32, _P(_sz)]),
+        "rhip_conv_workspace_bytes": (ctypes.c_int, [_i32, _i32, _i32, _i32, _i64, _i64, _i64,
+                                                     _P(_sz)]),
         "rhip_conv_forward": (ctypes.c_int, [_vp, _i64, _i32, _vp, _i32, _i32, _vp, _vp,
                                              _vp, _i64, _vp, _i32, _vp, _sz, _vp]),
         "rhip_conv_backward_input": (ctypes.c_int, [_vp, _i64, _i32, _vp, _i32, _i32,
@@ -281,9 +282,9 @@ def kernel_map(in_table: CoordTable, out_table: CoordTable, offsets: torch.Tenso
 
 # ------------------------------------------------------------ convolution
 
-def _conv_ws(K, cin, cout, dtype, dev) -> torch.Tensor:
-    return torch.empty(_sizeq(lib().rhip_conv_workspace_bytes, K, cin, cout, dtype),
-                       dtype=torch.uint8, device=dev)
+def _conv_ws(K, cin, cout, dtype, dev, kmap: "KernelMap") -> torch.Tensor:
+    return torch.empty(_sizeq(lib().rhip_conv_workspace_bytes, K, cin, cout, dtype, kmap.n_in,
+                              kmap.n_out, kmap.n_pairs), dtype=torch.uint8, device=dev)
 
 
 def conv_forward(x: torch.Tensor, weight: torch.Tensor, kmap: KernelMap,
@@ -298,7 +299,7 @@ def conv_forward(x: torch.Tensor, weight: torch.Tensor, kmap: KernelMap,
         raise RuntimeError("shape mismatch between features, weight and kernel map")
     b = None if bias is None else bias.reshape(-1).to(torch.float32).contiguous()
     y = torch.empty((kmap.n_out, cout), dtype=x.dtype, device=x.device)
-    ws = _conv_ws(K, cin, cout, dt, x.device)
+    ws = _conv_ws(K, cin, cout, dt, x.device, kmap)
     _check(lib().rhip_conv_forward(_ptr(x), kmap.n_in, cin, _ptr(weight), K, cout, _ptr(b),
                                    _ptr(kmap.nbr), _ptr(kmap.out_order), kmap.n_out, _ptr(y),
                                    dt, _ptr(ws), ws.numel(), _stream(x.device)),
@@ -313,7 +314,7 @@ def conv_backward_input(grad_y: torch.Tensor, weight: torch.Tensor, kmap: Kernel
     weight = weight.to(grad_y.dtype).contiguous()
     K, cin, cout = weight.shape
     gx = torch.empty((kmap.n_in, cin), dtype=grad_y.dtype, device=grad_y.device)
-    ws = _conv_ws(K, cin, cout, dt, grad_y.device)
+    ws = _conv_ws(K, cin, cout, dt, grad_y.device, kmap)
     _check(lib().rhip_conv_backward_input(_ptr(grad_y), kmap.n_out, cout, _ptr(weight), K, cin,
                                           _ptr(kmap.nbr_t), _ptr(kmap.in_order), kmap.n_in,
                                           _ptr(gx), dt, _ptr(ws), ws.numel(),
@@ -328,7 +329,7 @@ def conv_backward_weight(x: torch.Tensor, grad_y: torch.Tensor, kmap: KernelMap,
     x, grad_y = x.contiguous(), grad_y.to(x.dtype).contiguous()
     cin, cout = x.shape[1], grad_y.shape[1]
     gw = torch.empty((K, cin, cout), dtype=x.dtype, device=x.device)
-    ws = _conv_ws(K, cin, cout, dt, x.device)
+    ws = _conv_ws(K, cin, cout, dt, x.device, kmap)
     _check(lib().rhip_conv_backward_weight(_ptr(x), kmap.n_in, cin, _ptr(grad_y), kmap.n_out,
                                            cout, K, _ptr(kmap.offsets), kmap.n_pairs,
                                            _ptr(kmap.in_rows), _ptr(kmap.out_rows), _ptr(gw),

@@ -18,9 +18,10 @@
 //    loads, zero for a missing neighbour) and accumulates every offset in
 //    registers. Each output row is written once: no atomics, no zero fill.
 //  * dW is a split-pair reduction over the per-offset pair lists: a
-//    workgroup stages 64 pairs of X and dY rows in LDS transposed (pair axis
-//    contiguous), runs 16x16 MFMA tiles with pairs as the reduction axis and
-//    adds each offset segment's tile to an fp32 accumulator with atomics.
+//    workgroup streams one offset's pair range through double-buffered LDS
+//    (X and dY rows stored row-major with 16-byte writes), runs 16x16 MFMA
+//    tiles with pairs as the reduction axis (bf16 operands through LDS
+//    transpose reads) and adds its tile to an fp32 accumulator with atomics.
 //  * The reduction order inside an MFMA is a permutation of the reduced axis
 //    chosen so that each lane reads 16 contiguous bytes; A and B use the same
 //    permutation, so the sum is unchanged.
@@ -300,117 +301,247 @@ __global__ __launch_bounds__(kThreads) void transpose_w_kernel(const T *__restri
 
 // ------------------------------------------------------------------- dW
 
-constexpr int kPairChunk = 64;
+// ------------------------------------------------------------------- dW
+//
+// dw[k][ci][co] += sum over the pairs p of offset k in this workgroup's range
+// of x[in_rows[p]][ci] * gy[out_rows[p]][co], for a (16*VA) x (16*VB)
+// channel tile (ci0, co0). The pair axis is the MFMA reduction axis.
+//
+// Pairs stream through LDS in chunks of 4 * PW pairs: every thread loads
+// 16-byte pieces of the chunk's X and dY rows (coalesced row reads) and
+// stores them row-major, double-buffered so that the next chunk's rows are in
+// flight while the current one is multiplied. Each wave owns one 16-channel
+// block of dY (waves sharing a block split the chunk's steps) against all
+// 16*VA channels of X:
+//  * fp32 (PW = 16, v_mfma_f32_16x16x4_f32): lane (i16, g) reads VA
+//    consecutive channels of pair row 4s+g (one vector read) and one dY
+//    channel; channel ci0 + VA*m + ea belongs to MFMA block ea, row m, so one
+//    vector read feeds VA blocks and no transpose is needed;
+//  * bf16 (PW = 32, v_mfma_f32_16x16x32_bf16): the K-major operands come
+//    from ds_read_b64_tr_b16. Within a 16-lane group, lane i receives the
+//    (i % 4)-th 16-bit element at the address of lane 4e + i/4 as element e;
+//    lane j points at row (pair) 4h + j/4, channels 4*(j%4) of a 16-channel
+//    block, so lane i gets channel i of four consecutive pairs, two reads
+//    give the eight pairs 8g..8g+7 of group g.
+// The four waves' tiles are summed in LDS; each workgroup stores its tile in
+// its own slot of a partial buffer and a second kernel sums the slots of each
+// offset in a fixed order (deterministic, no atomics).
+template <typename T> struct DwShape;
+template <> struct DwShape<float> { static constexpr int kPairsPerWave = 16; };
+template <> struct DwShape<__bf16> { static constexpr int kPairsPerWave = 32; };
 
-// bf16: dw[k][ci][co] += sum_{p in k} x[in_rows[p]][ci] * gy[out_rows[p]][co]
-// over the workgroup's pair range [blockIdx.x*ppb, +ppb), tile (MT x NTc).
-// The pair axis is the MFMA reduction axis, so 64-pair chunks are staged in
-// LDS transposed (pair axis contiguous).
-template <typename T, int MT, int NTc>
-__global__ __launch_bounds__(kThreads) void conv_dw_lds_kernel(
+typedef short v4s __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) v4s lds_v4s;
+
+__device__ __forceinline__ v4s ds_read_tr16(const void *p) {
+  // generic LDS pointer -> LDS address space (the low 32 bits are the offset)
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      reinterpret_cast<lds_v4s *>(static_cast<uint32_t>(reinterpret_cast<uintptr_t>(p))));
+}
+
+template <typename T, int VA, int VB, bool DB>
+__global__ __launch_bounds__(kThreads) void conv_dw_kernel(
     const T *__restrict__ x, int cin, const T *__restrict__ gy, int cout,
-    const int64_t *__restrict__ kofs, int K, const int32_t *__restrict__ in_rows,
-    const int32_t *__restrict__ out_rows, int64_t n_pairs, int64_t ppb,
-    float *__restrict__ dw) {
-  using M = Mfma<T>;
-  using Frag = typename M::Frag;
-  constexpr int CH = M::kCh;
-  constexpr int EPL = CH / 4;
-  constexpr int VE = 16 / sizeof(T);
-  constexpr int CP = kPairChunk;
-  constexpr int LDP = CP + VE;
-  constexpr int NBN = NTc / 16;
-  constexpr int NBLK = (MT / 16) * NBN;
-  constexpr int BPW = (NBLK + kWaves - 1) / kWaves;
+    const int64_t *__restrict__ kofs, const int32_t *__restrict__ in_rows,
+    const int32_t *__restrict__ out_rows, int64_t ppb, float *__restrict__ partial) {
+  constexpr bool F32 = std::is_same<T, float>::value;
+  constexpr int TM = 16 * VA, TN = 16 * VB;
+  constexpr int PW = DwShape<T>::kPairsPerWave;
+  constexpr int CP = kWaves * PW;      // pairs per chunk
+  constexpr int VE = 16 / sizeof(T);   // elements per 16-byte piece
+  constexpr int LDX = TM + VE, LDG = TN + VE;
+  constexpr int XV = CP * (TM / VE), GV = CP * (TN / VE);  // pieces per chunk
+  constexpr int XPT = (XV + kThreads - 1) / kThreads, GPT = (GV + kThreads - 1) / kThreads;
+  static_assert(CP * LDX * sizeof(T) >= TM * TN * sizeof(float), "reduction reuses sX");
 
-  __shared__ __align__(16) T sX[MT * LDP];
-  __shared__ __align__(16) T sG[NTc * LDP];
+  constexpr int NBUF = DB ? 2 : 1;
+  __shared__ __align__(16) T sX[NBUF][CP * LDX];
+  __shared__ __align__(16) T sG[NBUF][CP * LDG];
+
+  const int k = blockIdx.y;
+  const int tiles_n = cout / TN;
+  const int ci0 = (blockIdx.z / tiles_n) * TM;
+  const int co0 = (blockIdx.z % tiles_n) * TN;
+  const int64_t kb = kofs[k], ke = kofs[k + 1];
+  const int64_t b0 = kb + static_cast<int64_t>(blockIdx.x) * ppb;
+  if (b0 >= ke)
+    return; // uniform across the workgroup
+  const int64_t b1 = min(ke, b0 + ppb);
+  const int nch = static_cast<int>((b1 - b0 + CP - 1) / CP);
 
   const int lane = threadIdx.x & (kWave - 1);
   const int wv = threadIdx.x / kWave;
   const int i16 = lane & 15;
   const int g = lane >> 4;
-  const int tiles_n = cout / NTc;
-  const int ci0 = (blockIdx.y / tiles_n) * MT;
-  const int co0 = (blockIdx.y % tiles_n) * NTc;
-  const int64_t pb = blockIdx.x * ppb;
-  const int64_t pe = min(n_pairs, pb + ppb);
-  if (pb >= pe)
-    return; // uniform across the workgroup
 
-  int k = 0;
-  while (k < K - 1 && kofs[k + 1] <= pb)
-    ++k;
-  int64_t cur = pb;
-  while (cur < pe) {
-    const int64_t seg_end = min(pe, kofs[k + 1]);
-    if (seg_end <= cur) { // offset k has no pairs
-      ++k;
-      continue;
+  // row indices of this thread's pieces of chunk c (-1 past the range)
+  int32_t xi[2][XPT], gi[2][GPT];
+  auto load_idx = [&](int c, int slot) {
+#pragma unroll
+    for (int i = 0; i < XPT; ++i) {
+      const int li = threadIdx.x + i * kThreads;
+      const int64_t pp = b0 + static_cast<int64_t>(c) * CP + li / (TM / VE);
+      xi[slot][i] = (li < XV && c < nch && pp < b1) ? in_rows[pp] : -1;
     }
-    v4f acc[BPW];
 #pragma unroll
-    for (int b = 0; b < BPW; ++b)
-      acc[b] = v4f{0.f, 0.f, 0.f, 0.f};
-    for (int64_t c0 = cur; c0 < seg_end; c0 += CP) {
-      __syncthreads();
-      for (int li = threadIdx.x; li < CP * (MT / VE); li += kThreads) {
-        const int p = li / (MT / VE), cv = li % (MT / VE);
-        const int64_t pr = c0 + p;
-        uint4 q = uint4{0u, 0u, 0u, 0u};
-        if (pr < seg_end)
-          q = *reinterpret_cast<const uint4 *>(
-              x + static_cast<int64_t>(in_rows[pr]) * cin + ci0 + cv * VE);
-        const T *e = reinterpret_cast<const T *>(&q);
+    for (int i = 0; i < GPT; ++i) {
+      const int li = threadIdx.x + i * kThreads;
+      const int64_t pp = b0 + static_cast<int64_t>(c) * CP + li / (TN / VE);
+      gi[slot][i] = (li < GV && c < nch && pp < b1) ? out_rows[pp] : -1;
+    }
+  };
+  uint4 xr[XPT], gr[GPT];
+  auto load_rows = [&](int slot) {
 #pragma unroll
-        for (int j = 0; j < VE; ++j)
-          sX[(cv * VE + j) * LDP + p] = e[j];
+    for (int i = 0; i < XPT; ++i) {
+      const int li = threadIdx.x + i * kThreads;
+      const int cv = li % (TM / VE);
+      xr[i] = xi[slot][i] >= 0
+                  ? *reinterpret_cast<const uint4 *>(
+                        x + static_cast<int64_t>(xi[slot][i]) * cin + ci0 + cv * VE)
+                  : uint4{0u, 0u, 0u, 0u};
+    }
+#pragma unroll
+    for (int i = 0; i < GPT; ++i) {
+      const int li = threadIdx.x + i * kThreads;
+      const int cv = li % (TN / VE);
+      gr[i] = gi[slot][i] >= 0
+                  ? *reinterpret_cast<const uint4 *>(
+                        gy + static_cast<int64_t>(gi[slot][i]) * cout + co0 + cv * VE)
+                  : uint4{0u, 0u, 0u, 0u};
+    }
+  };
+  auto store_rows = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < XPT; ++i) {
+      const int li = threadIdx.x + i * kThreads;
+      if (li < XV)
+        *reinterpret_cast<uint4 *>(&sX[buf][(li / (TM / VE)) * LDX + (li % (TM / VE)) * VE]) =
+            xr[i];
+    }
+#pragma unroll
+    for (int i = 0; i < GPT; ++i) {
+      const int li = threadIdx.x + i * kThreads;
+      if (li < GV)
+        *reinterpret_cast<uint4 *>(&sG[buf][(li / (TN / VE)) * LDG + (li % (TN / VE)) * VE]) =
+            gr[i];
+    }
+  };
+
+  // wave -> one 16-channel block nb of dY and every PG-th step of the chunk
+  constexpr int PG = kWaves / VB; // waves sharing a dY block split the steps
+  const int nb = wv % VB, ps = wv / VB;
+  v4f acc[VA];
+#pragma unroll
+  for (int ea = 0; ea < VA; ++ea)
+    acc[ea] = v4f{0.f, 0.f, 0.f, 0.f};
+
+  load_idx(0, 0);
+  load_idx(1, 1);
+  load_rows(0);
+  store_rows(0);
+  __syncthreads();
+  for (int c = 0; c < nch; ++c) {
+    const int buf = DB ? (c & 1) : 0;
+    const int slot = (c + 1) & 1;
+    if (c + 1 < nch)
+      load_rows(slot); // rows of chunk c+1 (indices loaded one chunk ago)
+    load_idx(c + 2, c & 1);
+    const T *bx = sX[buf];
+    const T *bg = sG[buf];
+    if constexpr (F32) {
+      // step s covers pairs 4s..4s+3, one per 16-lane group
+#pragma unroll 4
+      for (int s = ps; s < CP / 4; s += PG) {
+        const float *ra = reinterpret_cast<const float *>(bx) + (4 * s + g) * LDX + VA * i16;
+        const float b = reinterpret_cast<const float *>(bg)[(4 * s + g) * LDG + 16 * nb + i16];
+        float a[VA];
+        if constexpr (VA == 4) {
+          const v4f t = *reinterpret_cast<const v4f *>(ra);
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            a[e] = t[e];
+        } else {
+#pragma unroll
+          for (int e = 0; e < VA; ++e)
+            a[e] = ra[e];
+        }
+#pragma unroll
+        for (int ea = 0; ea < VA; ++ea)
+          acc[ea] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[ea], b, acc[ea], 0, 0, 0);
       }
-      for (int li = threadIdx.x; li < CP * (NTc / VE); li += kThreads) {
-        const int p = li / (NTc / VE), cv = li % (NTc / VE);
-        const int64_t pr = c0 + p;
-        uint4 q = uint4{0u, 0u, 0u, 0u};
-        if (pr < seg_end)
-          q = *reinterpret_cast<const uint4 *>(
-              gy + static_cast<int64_t>(out_rows[pr]) * cout + co0 + cv * VE);
-        const T *e = reinterpret_cast<const T *>(&q);
+    } else {
+      // step s covers pairs 32s..32s+31; group g takes 8g..8g+7 of them and
+      // lane i16 points at pair 8g + 4h + i16/4, channels 16*blk + 4*(i16%4)
+#pragma unroll 2
+      for (int s = ps; s < CP / 32; s += PG) {
+        const int prow = 32 * s + 8 * g + i16 / 4;
+        const int pcol = 4 * (i16 % 4);
+        const v4s blo = ds_read_tr16(bg + prow * LDG + 16 * nb + pcol);
+        const v4s bhi = ds_read_tr16(bg + (prow + 4) * LDG + 16 * nb + pcol);
+        const v8bf bf = __builtin_bit_cast(v8bf, __builtin_shufflevector(blo, bhi, 0, 1, 2, 3, 4, 5, 6, 7));
 #pragma unroll
-        for (int j = 0; j < VE; ++j)
-          sG[(cv * VE + j) * LDP + p] = e[j];
-      }
-      __syncthreads();
-#pragma unroll
-      for (int s = 0; s < CP / CH; ++s) {
-#pragma unroll
-        for (int b = 0; b < BPW; ++b) {
-          const int blk = wv + kWaves * b;
-          if (blk < NBLK) {
-            const int mi = blk / NBN, ni = blk % NBN;
-            const Frag av = *reinterpret_cast<const Frag *>(
-                &sX[(mi * 16 + i16) * LDP + s * CH + g * EPL]);
-            const Frag bv = *reinterpret_cast<const Frag *>(
-                &sG[(ni * 16 + i16) * LDP + s * CH + g * EPL]);
-            M::mma(av, bv, acc[b]);
-          }
+        for (int ea = 0; ea < VA; ++ea) {
+          const v4s lo = ds_read_tr16(bx + prow * LDX + 16 * ea + pcol);
+          const v4s hi = ds_read_tr16(bx + (prow + 4) * LDX + 16 * ea + pcol);
+          const v8bf af = __builtin_bit_cast(v8bf, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+          acc[ea] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af, bf, acc[ea], 0, 0, 0);
         }
       }
     }
-#pragma unroll
-    for (int b = 0; b < BPW; ++b) {
-      const int blk = wv + kWaves * b;
-      if (blk < NBLK) {
-        const int mi = blk / NBN, ni = blk % NBN;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int ci = ci0 + mi * 16 + 4 * g + e;
-          const int co = co0 + ni * 16 + i16;
-          atomicAdd(&dw[(static_cast<int64_t>(k) * cin + ci) * cout + co], acc[b][e]);
-        }
-      }
+    if (DB) {
+      if (c + 1 < nch)
+        store_rows(buf ^ 1);
+      __syncthreads();
+    } else {
+      __syncthreads(); // every wave is done with the chunk
+      if (c + 1 < nch)
+        store_rows(0);
+      __syncthreads();
     }
-    cur = seg_end;
-    ++k;
   }
+
+  // sum the four waves' tiles in LDS (reusing sX) and store the workgroup's
+  // tile in its partial slot
+  float *red = reinterpret_cast<float *>(sX[0]);
+  for (int i = threadIdx.x; i < TM * TN; i += kThreads)
+    red[i] = 0.f;
+  __syncthreads();
+#pragma unroll
+  for (int ea = 0; ea < VA; ++ea)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      // lane holds D[4g+e][i16] of block (ea, nb)
+      const int m = 4 * g + e;
+      const int ci = F32 ? VA * m + ea : 16 * ea + m;
+      atomicAdd(&red[ci * TN + 16 * nb + i16], acc[ea][e]);
+    }
+  __syncthreads();
+  float *slot = partial + ((static_cast<int64_t>(k) * gridDim.z + blockIdx.z) * gridDim.x +
+                           blockIdx.x) * (TM * TN);
+  for (int i = threadIdx.x; i < TM * TN; i += kThreads)
+    slot[i] = red[i];
+}
+
+// dw[k][ci0 + i / TN][co0 + i % TN] = sum over the chunks c of offset k (in
+// chunk order) of partial[k][tile][c][i]: a deterministic second stage.
+template <typename OutT>
+__global__ __launch_bounds__(kThreads) void conv_dw_reduce_kernel(
+    const float *__restrict__ partial, const int64_t *__restrict__ kofs, int64_t ppb,
+    int chunks, int tiles, int tiles_n, int TM, int TN, int cin, int cout,
+    OutT *__restrict__ dw) {
+  const int k = blockIdx.y, t = blockIdx.z;
+  const int i = blockIdx.x * kThreads + threadIdx.x;
+  if (i >= TM * TN)
+    return;
+  const int64_t pk = kofs[k + 1] - kofs[k];
+  const int nck = static_cast<int>(min<int64_t>(chunks, (pk + ppb - 1) / ppb));
+  const float *src = partial + (static_cast<int64_t>(k) * tiles + t) * chunks * (TM * TN) + i;
+  float sum = 0.f;
+  for (int c = 0; c < nck; ++c)
+    sum += src[static_cast<int64_t>(c) * (TM * TN)];
+  const int ci = (t / tiles_n) * TM + i / TN, co = (t % tiles_n) * TN + i % TN;
+  dw[(static_cast<int64_t>(k) * cin + ci) * cout + co] = from_f32<OutT>(sum);
 }
 
 // Any-shape fallback: one lane per dW element, looping over its pairs.
@@ -500,56 +631,98 @@ static void run_os(const T *x, int cred, const T *wt, int ncols,
   RHIP_LAUNCH_CHECK();
 }
 
-template <typename T, int MT, int NTc>
-static void launch_dw_lds(const T *x, int cin, const T *gy, int cout,
-                          const int64_t *kofs, int K, const int32_t *in_rows,
-                          const int32_t *out_rows, int64_t n_pairs, float *dw,
-                          hipStream_t s) {
-  const int tiles = (cin / MT) * (cout / NTc);
-  // Aim for ~4 workgroups per CU over 256 CUs, at least 4 chunks each.
-  const int64_t target = std::max<int64_t>(1, 1024 / tiles);
-  int64_t ppb = ceil_div(n_pairs, target);
-  ppb = std::max<int64_t>(4 * kPairChunk, ceil_div(ppb, kPairChunk) * kPairChunk);
-  dim3 grid(static_cast<unsigned>(ceil_div(n_pairs, ppb)), tiles);
-  hipLaunchKernelGGL((conv_dw_lds_kernel<T, MT, NTc>), grid, dim3(kThreads), 0, s, x, cin, gy,
-                     cout, kofs, K, in_rows, out_rows, n_pairs, ppb, dw);
+// Launch plan of the dW kernel: pairs per workgroup, chunks per offset and
+// channel tiles, shared by the workspace query and the launch.
+struct DwPlan {
+  int va = 1, vb = 1, tiles = 1;
+  int64_t ppb = 1, chunks = 1;
+  bool fast = false;
+  size_t partial_floats() const {
+    return fast ? static_cast<size_t>(chunks) * tiles * (16 * va) * (16 * vb) : 0;
+  }
+};
+
+static int dw_width(int c) { return c % 64 == 0 ? 4 : (c % 32 == 0 ? 2 : 1); }
+
+// wgs: busy workgroups to aim for over the whole map (0 = the measured best
+// on MI355X: 2048 for fp32, where the MFMA work dominates, 512 for bf16).
+static DwPlan dw_plan(int32_t dtype, int cin, int cout, int64_t n_pairs, int64_t max_pk,
+                      int wgs = 0) {
+  DwPlan p;
+  if (wgs <= 0)
+    wgs = dtype == RHIP_F32 ? 2048 : 512;
+  const int VE = dtype == RHIP_F32 ? 4 : 8;
+  p.fast = n_pairs > 0 && cin % 16 == 0 && cout % 16 == 0 && cin % VE == 0 && cout % VE == 0;
+  if (!p.fast)
+    return p;
+  p.va = dw_width(cin);
+  p.vb = dw_width(cout);
+  p.tiles = (cin / (16 * p.va)) * (cout / (16 * p.vb));
+  const int64_t CP = kWaves * (dtype == RHIP_F32 ? DwShape<float>::kPairsPerWave
+                                                 : DwShape<__bf16>::kPairsPerWave);
+  // ~wgs busy workgroups over the whole map, at least 4 chunks each
+  const int64_t target = std::max<int64_t>(1, wgs / p.tiles);
+  p.ppb = std::max<int64_t>(4 * CP, ceil_div(n_pairs, target));
+  p.ppb = ceil_div(p.ppb, CP) * CP;
+  p.chunks = std::max<int64_t>(1, ceil_div(max_pk, p.ppb));
+  return p;
 }
 
-template <typename T, int MT>
-static void pick_dw_lds_n(const T *x, int cin, const T *gy, int cout,
-                          const int64_t *kofs, int K, const int32_t *in_rows,
-                          const int32_t *out_rows, int64_t n_pairs, float *dw,
-                          hipStream_t s) {
-  if (cout % 64 == 0)
-    launch_dw_lds<T, MT, 64>(x, cin, gy, cout, kofs, K, in_rows, out_rows, n_pairs, dw, s);
-  else if (cout % 32 == 0)
-    launch_dw_lds<T, MT, 32>(x, cin, gy, cout, kofs, K, in_rows, out_rows, n_pairs, dw, s);
+template <typename T, int VA, int VB, bool DB = false>
+static void launch_dw(const T *x, int cin, const T *gy, int cout, const int64_t *kofs, int K,
+                      const int32_t *in_rows, const int32_t *out_rows, const DwPlan &p,
+                      float *partial, hipStream_t s) {
+  dim3 grid(static_cast<unsigned>(p.chunks), K, p.tiles);
+  hipLaunchKernelGGL((conv_dw_kernel<T, VA, VB, DB>), grid, dim3(kThreads), 0, s, x, cin, gy,
+                     cout, kofs, in_rows, out_rows, p.ppb, partial);
+}
+
+template <typename T, int VA>
+static void pick_dw_b(const T *x, int cin, const T *gy, int cout, const int64_t *kofs, int K,
+                      const int32_t *in_rows, const int32_t *out_rows, const DwPlan &p,
+                      float *partial, hipStream_t s) {
+  if (p.vb == 4)
+    launch_dw<T, VA, 4>(x, cin, gy, cout, kofs, K, in_rows, out_rows, p, partial, s);
+  else if (p.vb == 2)
+    launch_dw<T, VA, 2>(x, cin, gy, cout, kofs, K, in_rows, out_rows, p, partial, s);
   else
-    launch_dw_lds<T, MT, 16>(x, cin, gy, cout, kofs, K, in_rows, out_rows, n_pairs, dw, s);
+    launch_dw<T, VA, 1>(x, cin, gy, cout, kofs, K, in_rows, out_rows, p, partial, s);
 }
 
-// fp32 result accumulated into dw (zeroed by the caller).
+// dw [K, cin, cout] in T (fully overwritten). `partial` holds
+// plan.partial_floats() * K floats; `acc` (generic path) K*cin*cout floats.
 template <typename T>
 static void run_dw(const T *x, int cin, const T *gy, int cout, const int64_t *kofs, int K,
                    const int32_t *in_rows, const int32_t *out_rows, int64_t n_pairs,
-                   float *dw, hipStream_t s) {
-  if (n_pairs == 0)
-    return;
-  constexpr int VE = 16 / sizeof(T);
-  const bool fast = cin % 16 == 0 && cout % 16 == 0 && cin % VE == 0 && cout % VE == 0 &&
-                    aligned16(x) && aligned16(gy);
-  if (!fast) {
-    hipLaunchKernelGGL((conv_dw_generic_kernel<T>),
-                       dim3(ceil_div(static_cast<int64_t>(K) * cin * cout, kThreads)),
-                       dim3(kThreads), 0, s, x, cin, gy, cout, kofs, K, in_rows, out_rows,
+                   const DwPlan &p, float *partial, float *acc, T *dw, hipStream_t s) {
+  const int64_t nw = static_cast<int64_t>(K) * cin * cout;
+  if (p.fast && aligned16(x) && aligned16(gy)) {
+    if (p.va == 4)
+      pick_dw_b<T, 4>(x, cin, gy, cout, kofs, K, in_rows, out_rows, p, partial, s);
+    else if (p.va == 2)
+      pick_dw_b<T, 2>(x, cin, gy, cout, kofs, K, in_rows, out_rows, p, partial, s);
+    else
+      pick_dw_b<T, 1>(x, cin, gy, cout, kofs, K, in_rows, out_rows, p, partial, s);
+    RHIP_LAUNCH_CHECK();
+    const int TM = 16 * p.va, TN = 16 * p.vb;
+    dim3 grid(static_cast<unsigned>(ceil_div(TM * TN, kThreads)), K, p.tiles);
+    hipLaunchKernelGGL((conv_dw_reduce_kernel<T>), grid, dim3(kThreads), 0, s, partial, kofs,
+                       p.ppb, static_cast<int>(p.chunks), p.tiles, cout / TN, TM, TN, cin, cout,
                        dw);
-  } else if (cin % 64 == 0) {
-    pick_dw_lds_n<T, 64>(x, cin, gy, cout, kofs, K, in_rows, out_rows, n_pairs, dw, s);
-  } else if (cin % 32 == 0) {
-    pick_dw_lds_n<T, 32>(x, cin, gy, cout, kofs, K, in_rows, out_rows, n_pairs, dw, s);
-  } else {
-    pick_dw_lds_n<T, 16>(x, cin, gy, cout, kofs, K, in_rows, out_rows, n_pairs, dw, s);
+    RHIP_LAUNCH_CHECK();
+    return;
   }
+  // any shape: one lane per dW element into an fp32 accumulator
+  hipLaunchKernelGGL(zero_f32_kernel, dim3(ceil_div(nw, kThreads)), dim3(kThreads), 0, s, acc,
+                     nw);
+  RHIP_LAUNCH_CHECK();
+  if (n_pairs > 0) {
+    hipLaunchKernelGGL((conv_dw_generic_kernel<T>), dim3(ceil_div(nw, kThreads)),
+                       dim3(kThreads), 0, s, x, cin, gy, cout, kofs, K, in_rows, out_rows, acc);
+    RHIP_LAUNCH_CHECK();
+  }
+  hipLaunchKernelGGL((cast_from_f32_kernel<T>), dim3(ceil_div(nw, kThreads)), dim3(kThreads), 0,
+                     s, acc, dw, nw);
   RHIP_LAUNCH_CHECK();
 }
 
@@ -558,9 +731,23 @@ static void check_dtype(int32_t dtype) {
     throw Error(RHIP_ERR_UNSUPPORTED, "dtype must be RHIP_F32 or RHIP_BF16");
 }
 
-static size_t conv_ws_bytes(int32_t K, int32_t cin, int32_t cout) {
-  // transposed weights (forward) or the fp32 dW accumulator (bf16 dW)
-  return align_up(sizeof(float) * static_cast<size_t>(K) * cin * cout, 256) + 256;
+// One workspace serves the three calls of a layer: the transposed weights
+// (forward), and for dW either the per-workgroup partial tiles or an fp32
+// accumulator.
+struct ConvWs {
+  void *wt = nullptr;
+  float *partial = nullptr;
+  float *acc = nullptr;
+};
+
+static ConvWs carve_conv(Carve &cv, int32_t K, int32_t cin, int32_t cout, int32_t dtype,
+                         const DwPlan &p) {
+  ConvWs w;
+  const size_t nw = static_cast<size_t>(K) * cin * cout;
+  w.wt = cv.take<char>(nw * (dtype == RHIP_F32 ? 4 : 2));
+  w.partial = cv.take<float>(std::max<size_t>(1, p.partial_floats() * K));
+  w.acc = cv.take<float>(nw);
+  return w;
 }
 
 } // namespace rhip
@@ -568,12 +755,17 @@ static size_t conv_ws_bytes(int32_t K, int32_t cin, int32_t cout) {
 using namespace rhip;
 
 extern "C" int rhip_conv_workspace_bytes(int32_t K, int32_t cin, int32_t cout,
-                                         int32_t dtype, size_t *bytes) {
+                                         int32_t dtype, int64_t n_in, int64_t n_out,
+                                         int64_t n_pairs, size_t *bytes) {
   return guarded([&] {
     RHIP_CHECK_ARG(bytes != nullptr, "bytes is null");
     RHIP_CHECK_ARG(K >= 1 && cin >= 1 && cout >= 1, "sizes must be positive");
+    RHIP_CHECK_ARG(n_in >= 0 && n_out >= 0 && n_pairs >= 0, "counts must be >= 0");
     check_dtype(dtype);
-    *bytes = conv_ws_bytes(K, cin, cout);
+    Carve cv(nullptr, 0);
+    carve_conv(cv, K, cin, cout, dtype,
+               dw_plan(dtype, cin, cout, n_pairs, std::min(n_in, n_out)));
+    *bytes = cv.used + 256;
   });
 }
 
@@ -596,7 +788,7 @@ extern "C" int rhip_conv_forward(const void *x, int64_t n_in, int32_t cin,
     const int64_t nw = static_cast<int64_t>(K) * cin * cout;
     // the MFMA path reads W[k] column-wise: stage the [K, cout, cin] copy
     if (dtype == RHIP_F32) {
-      float *wt = cv.take<float>(nw);
+      float *wt = reinterpret_cast<float *>(cv.take<char>(nw * sizeof(float)));
       hipLaunchKernelGGL((transpose_w_kernel<float>), dim3(ceil_div(nw, kThreads)),
                          dim3(kThreads), 0, stream, static_cast<const float *>(weight), K, cin,
                          cout, wt);
@@ -604,7 +796,7 @@ extern "C" int rhip_conv_forward(const void *x, int64_t n_in, int32_t cin,
       run_os<float>(static_cast<const float *>(x), cin, wt, cout, bias, nbr, n_out, K,
                     out_order, static_cast<float *>(y), stream);
     } else {
-      __bf16 *wt = cv.take<__bf16>(nw);
+      __bf16 *wt = reinterpret_cast<__bf16 *>(cv.take<char>(nw * sizeof(__bf16)));
       hipLaunchKernelGGL((transpose_w_kernel<__bf16>), dim3(ceil_div(nw, kThreads)),
                          dim3(kThreads), 0, stream, static_cast<const __bf16 *>(weight), K,
                          cin, cout, wt);
@@ -657,28 +849,18 @@ extern "C" int rhip_conv_backward_weight(
     RHIP_CHECK_ARG(grad_w != nullptr, "grad_w is null");
     RHIP_CHECK_ARG(n_pairs == 0 || (x && grad_y && kmap_offsets && in_rows && out_rows),
                    "x, grad_y, kmap_offsets, in_rows and out_rows are required");
-    const int64_t nw = static_cast<int64_t>(K) * cin * cout;
-    float *acc = nullptr;
-    if (dtype == RHIP_F32) {
-      acc = static_cast<float *>(grad_w);
-    } else {
-      RHIP_CHECK_ARG(workspace != nullptr, "workspace is null");
-      Carve cv(workspace, workspace_bytes);
-      acc = cv.take<float>(nw);
-    }
-    hipLaunchKernelGGL(zero_f32_kernel, dim3(ceil_div(nw, kThreads)), dim3(kThreads), 0,
-                       stream, acc, nw);
-    RHIP_LAUNCH_CHECK();
-    if (dtype == RHIP_F32) {
-      run_dw<float>(static_cast<const float *>(x), cin, static_cast<const float *>(grad_y),
-                    cout, kmap_offsets, K, in_rows, out_rows, n_pairs, acc, stream);
-    } else {
-      run_dw<__bf16>(static_cast<const __bf16 *>(x), cin,
-                     static_cast<const __bf16 *>(grad_y), cout, kmap_offsets, K, in_rows,
-                     out_rows, n_pairs, acc, stream);
-      hipLaunchKernelGGL((cast_from_f32_kernel<__bf16>), dim3(ceil_div(nw, kThreads)),
-                         dim3(kThreads), 0, stream, acc, static_cast<__bf16 *>(grad_w), nw);
-      RHIP_LAUNCH_CHECK();
-    }
+    RHIP_CHECK_ARG(workspace != nullptr, "workspace is null");
+    // an offset pairs each input and each output row at most once
+    const DwPlan plan = dw_plan(dtype, cin, cout, n_pairs, std::min(n_in, n_out));
+    Carve cv(workspace, workspace_bytes);
+    const ConvWs w = carve_conv(cv, K, cin, cout, dtype, plan);
+    if (dtype == RHIP_F32)
+      run_dw<float>(static_cast<const float *>(x), cin, static_cast<const float *>(grad_y), cout,
+                    kmap_offsets, K, in_rows, out_rows, n_pairs, plan, w.partial, w.acc,
+                    static_cast<float *>(grad_w), stream);
+    else
+      run_dw<__bf16>(static_cast<const __bf16 *>(x), cin, static_cast<const __bf16 *>(grad_y),
+                     cout, kmap_offsets, K, in_rows, out_rows, n_pairs, plan, w.partial, w.acc,
+                     static_cast<__bf16 *>(grad_w), stream);
   });
 }

@@ -21,11 +21,11 @@ int32_t rhip_dtype(const at::Tensor &t) {
               t.scalar_type());
 }
 
-at::Tensor conv_workspace(int32_t K, int64_t cin, int64_t cout, int32_t dt,
-                          const at::Device &dev) {
+at::Tensor conv_workspace(int32_t K, int64_t cin, int64_t cout, int32_t dt, int64_t n_in,
+                          int64_t n_out, int64_t n_pairs, const at::Device &dev) {
   size_t bytes = 0;
   check_rhip(rhip_conv_workspace_bytes(K, static_cast<int32_t>(cin), static_cast<int32_t>(cout),
-                                       dt, &bytes),
+                                       dt, n_in, n_out, n_pairs, &bytes),
              "rhip_conv_workspace_bytes");
   return torch::empty({static_cast<int64_t>(bytes)},
                       torch::TensorOptions().dtype(torch::kUInt8).device(dev));
@@ -54,7 +54,7 @@ struct HipConvolutionFunction : public torch::autograd::Function<HipConvolutionF
     TORCH_CHECK(x.size(1) == cin, "feature channels ", x.size(1), " != kernel in-channels ", cin);
     const int32_t dt = rhip_dtype(x);
     auto y = torch::empty({n_out, cout}, x.options());
-    auto ws = conv_workspace(K, cin, cout, dt, dev);
+    auto ws = conv_workspace(K, cin, cout, dt, n_in, n_out, n_pairs, dev);
     check_rhip(rhip_conv_forward(x.data_ptr(), n_in, static_cast<int32_t>(cin), w.data_ptr(), K,
                                  static_cast<int32_t>(cout), nullptr, nbr.data_ptr<int32_t>(),
                                  out_order.data_ptr<int32_t>(), n_out, y.data_ptr(), dt,
@@ -80,7 +80,7 @@ struct HipConvolutionFunction : public torch::autograd::Function<HipConvolutionF
     const int32_t K = static_cast<int32_t>(w.size(0));
     const int64_t cin = w.size(1), cout = w.size(2), n_in = x.size(0);
     const int32_t dt = rhip_dtype(x);
-    auto ws = conv_workspace(K, cin, cout, dt, dev);
+    auto ws = conv_workspace(K, cin, cout, dt, n_in, n_out, n_pairs, dev);
     at::Tensor gx, gw;
     if (ctx->needs_input_grad(0)) {
       gx = torch::empty_like(x);

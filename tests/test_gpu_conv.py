@@ -172,14 +172,18 @@ def test_config2_full_size_vs_torch(dtype):
     assert_rel(gw.float().cpu().numpy(), rgw.cpu().numpy(), tol, "dW")
 
 
-def test_repeat_calls_are_deterministic_for_y_and_dx():
-    """Forward and dX accumulate in registers in a fixed order: bitwise
-    repeatable. (dW uses fp32 atomics across workgroups and is not.)"""
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_repeat_calls_are_bitwise_deterministic(dtype):
+    """Forward and dX accumulate in registers in a fixed order; dW writes one
+    partial tile per workgroup and sums them in a fixed order: all three are
+    bitwise repeatable."""
     rng = np.random.default_rng(12)
     c, _, _ = oracle.insert_and_map(random_coords(rng, 10000, 3, 15))
     _, _, km = gpu_tables_and_map(c, c, oracle.region_offsets(3, 3), same=True)
-    x = to_dev(rng.standard_normal((km.n_in, 64)).astype(np.float32))
-    w = to_dev(rng.standard_normal((27, 64, 64)).astype(np.float32))
-    a = abi.conv_forward(x, w, km)
-    b = abi.conv_forward(x, w, km)
-    assert torch.equal(a, b)
+    x = to_dev(rng.standard_normal((km.n_in, 64)).astype(np.float32), dtype)
+    w = to_dev(rng.standard_normal((27, 64, 64)).astype(np.float32), dtype)
+    gy = to_dev(rng.standard_normal((km.n_out, 64)).astype(np.float32), dtype)
+    assert torch.equal(abi.conv_forward(x, w, km), abi.conv_forward(x, w, km))
+    assert torch.equal(abi.conv_backward_input(gy, w, km), abi.conv_backward_input(gy, w, km))
+    assert torch.equal(abi.conv_backward_weight(x, gy, km, 27),
+                       abi.conv_backward_weight(x, gy, km, 27))
