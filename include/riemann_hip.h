@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define RHIP_ABI_VERSION 3
+#define RHIP_ABI_VERSION 4
 #define RHIP_MAX_COLS 8 /* batch column + up to 7 spatial axes */
 
 typedef enum rhip_status {
@@ -133,19 +133,28 @@ int rhip_stride_coords(const int32_t *coords, int64_t n, int32_t ncol,
 int rhip_kmap_workspace_bytes(int64_t n_in, int64_t n_out, int32_t K,
                               size_t *bytes);
 
+/* Set by rhip_kmap_count for a map of a coordinate set onto itself (out_coords
+ * are in_table's own rows, in order) with a point-symmetric stencil (offset
+ * K-1-k == -offset k): only half the offsets are probed and the transposed
+ * table is the forward table with offsets reversed. Pass it to
+ * rhip_kmap_fill. */
+#define RHIP_KMAP_SYMMETRIC 1
+
 /*
  * Phase 1 of kernel-map generation. For every output row and every offset
  * k, look up out_coords[row] + offsets[k] (batch column unchanged) in
- * in_table. offsets is a device array [K, ncol-1] of already scaled lattice
- * offsets (kernel_region::coordinate_at, engine/grid/stencil.hpp:223-278).
- * The rows are queried in out_spatial_order (a locality order of the output
- * map, e.g. from rhip_spatial_order; NULL = row order) and then put in a
- * processing order that groups rows with equal neighbour masks (K <= 128;
- * ties keep the locality order). Outputs:
+ * in_table. offsets_host is a HOST array [K, ncol-1] of already scaled
+ * lattice offsets (kernel_region::coordinate_at, engine/grid/stencil.hpp:
+ * 223-278); the library copies it to the device. The rows are queried in
+ * out_spatial_order (a locality order of the output map, e.g. from
+ * rhip_spatial_order; NULL = row order) and then put in a processing order
+ * that groups rows with equal neighbour masks (K <= 128; ties keep the
+ * locality order). Outputs:
  *   out_order[p]   output row at processing position p (n_out entries);
  *   nbr[k*n_out+p] input row paired with out_order[p] under k, or -1;
  *   kmap_offsets   device int64 [K+1], CSR of the pairs per offset, copied
- *                  to kmap_offsets_host.
+ *                  to kmap_offsets_host;
+ *   *flags         RHIP_KMAP_SYMMETRIC or 0 (flags may be NULL).
  * Synchronises `stream` once (to read the pair counts).
  * Replaces CoordinateMapGPU::kernel_map / direct_kernel_map / count_kernel
  * (engine/grid/lattice_gpu.cu:1140-1362, 1366-1549); the live reference
@@ -153,10 +162,10 @@ int rhip_kmap_workspace_bytes(int64_t n_in, int64_t n_out, int32_t K,
  */
 int rhip_kmap_count(const rhip_table *in_table, const int32_t *out_coords,
                     const int32_t *out_spatial_order, int64_t n_out, int32_t K,
-                    const int32_t *offsets, void *workspace,
+                    const int32_t *offsets_host, void *workspace,
                     size_t workspace_bytes, int32_t *nbr, int32_t *out_order,
                     int64_t *kmap_offsets, int64_t *kmap_offsets_host,
-                    hipStream_t stream);
+                    int32_t *flags, hipStream_t stream);
 
 /*
  * Phase 2: emit the pairs of offset k at [kmap_offsets[k], kmap_offsets[k+1])
@@ -165,13 +174,14 @@ int rhip_kmap_count(const rhip_table *in_table, const int32_t *out_coords,
  * rows (in_order, grouping equal transposed masks; ties keep
  * in_spatial_order, NULL = row order) and fill the transposed table
  * nbr_t[k*n_in+q] = output row paired with in_order[q] under k, or -1.
- * The workspace must be the one phase 1 wrote. Asynchronous.
+ * flags and the workspace must be what phase 1 produced. Asynchronous.
  * Replaces gpu_kernel_map::decompose (engine/grid/lattice_gpu.cuh:438-488);
  * the set of pairs equals the reference's cpu_kernel_map.
  */
 int rhip_kmap_fill(const int32_t *nbr, const int32_t *out_order, int64_t n_out,
                    int32_t K, const int32_t *in_spatial_order, int64_t n_in,
-                   void *workspace, size_t workspace_bytes, int32_t *in_rows,
+                   int32_t flags, void *workspace, size_t workspace_bytes,
+                   const int64_t *kmap_offsets, int32_t *in_rows,
                    int32_t *out_rows, int32_t *nbr_t, int32_t *in_order,
                    hipStream_t stream);
 

@@ -21,6 +21,7 @@ MAX_COLS = 8
 
 F32, BF16 = 0, 1
 KEY_PACKED64, KEY_ROWREF = 0, 1
+KMAP_SYMMETRIC = 1
 
 # Every function the header declares (checked by the CPU test suite).
 EXPORTS = (
@@ -61,10 +62,11 @@ def _declare(lib):
         "rhip_spatial_order": (ctypes.c_int, [_P(RhipTable), _vp, _vp, _vp, _sz, _vp]),
         "rhip_stride_coords": (ctypes.c_int, [_vp, _i64, _i32, _P(_i32), _vp, _vp]),
         "rhip_kmap_workspace_bytes": (ctypes.c_int, [_i64, _i64, _i32, _P(_sz)]),
-        "rhip_kmap_count": (ctypes.c_int, [_P(RhipTable), _vp, _vp, _i64, _i32, _vp,
-                                           _vp, _sz, _vp, _vp, _vp, _P(_i64), _vp]),
-        "rhip_kmap_fill": (ctypes.c_int, [_vp, _vp, _i64, _i32, _vp, _i64, _vp, _sz,
-                                          _vp, _vp, _vp, _vp, _vp]),
+        "rhip_kmap_count": (ctypes.c_int, [_P(RhipTable), _vp, _vp, _i64, _i32, _P(_i32),
+                                           _vp, _sz, _vp, _vp, _vp, _P(_i64), _P(_i32),
+                                           _vp]),
+        "rhip_kmap_fill": (ctypes.c_int, [_vp, _vp, _i64, _i32, _vp, _i64, _i32, _vp, _sz,
+                                          _vp, _vp, _vp, _vp, _vp, _vp]),
         "rhip_conv_workspace_bytes": (ctypes.c_int, [_i32, _i32, _i32, _i32, _i64, _i64, _i64,
                                                      _P(_sz)]),
         "rhip_conv_forward": (ctypes.c_int, [_vp, _i64, _i32, _vp, _i32, _i32, _vp, _vp,
@@ -228,6 +230,7 @@ class KernelMap:
     nbr_t: torch.Tensor          # int32 [K, n_in]
     in_order: torch.Tensor
     out_order: torch.Tensor
+    symmetric: bool = False
 
     @property
     def n_pairs(self) -> int:
@@ -237,19 +240,21 @@ class KernelMap:
         """Transposed map: in and out exchanged, zero copy."""
         return KernelMap(self.K, self.n_out, self.n_in, self.offsets, self.offsets_host,
                          self.out_rows, self.in_rows, self.nbr_t, self.nbr,
-                         self.out_order, self.in_order)
+                         self.out_order, self.in_order, self.symmetric)
 
     def pairs(self, k: int):
         a, b = int(self.offsets_host[k]), int(self.offsets_host[k + 1])
         return self.in_rows[a:b], self.out_rows[a:b]
 
 
-def kernel_map(in_table: CoordTable, out_table: CoordTable, offsets: torch.Tensor) -> KernelMap:
+def kernel_map(in_table: CoordTable, out_table: CoordTable, offsets) -> KernelMap:
     """Pairs (in, out) with coord(in) = coord(out) + offsets[k] (batch kept),
-    the dense neighbour tables and the processing orders of both sides."""
+    the dense neighbour tables and the processing orders of both sides.
+    offsets: [K, D] int32 (numpy or tensor; read on the host)."""
     L = lib()
     dev = in_table.ucoords.device
-    offsets = offsets.to(device=dev, dtype=torch.int32).contiguous()
+    offsets = torch.as_tensor(np.asarray(offsets.cpu() if torch.is_tensor(offsets) else offsets),
+                              dtype=torch.int32).contiguous()
     K = offsets.shape[0]
     if offsets.dim() != 2 or offsets.shape[1] != in_table.ncol - 1:
         raise RuntimeError("offsets must be [K, D]")
@@ -263,21 +268,25 @@ def kernel_map(in_table: CoordTable, out_table: CoordTable, offsets: torch.Tenso
                      device=dev)
     kofs = torch.empty(K + 1, dtype=torch.int64, device=dev)
     kofs_host = np.zeros(K + 1, dtype=np.int64)
+    flags = ctypes.c_int32(0)
+    off_host = offsets.numpy()
     _check(L.rhip_kmap_count(ctypes.byref(in_table.struct), _ptr(out_table.ucoords),
-                             _ptr(out_table.order), n_out, K, _ptr(offsets), _ptr(ws), ws.numel(),
-                             _ptr(nbr), _ptr(out_order), _ptr(kofs),
-                             kofs_host.ctypes.data_as(ctypes.POINTER(ctypes.c_int64)), st),
-           "rhip_kmap_count")
+                             _ptr(out_table.order), n_out, K,
+                             off_host.ctypes.data_as(ctypes.POINTER(ctypes.c_int32)), _ptr(ws),
+                             ws.numel(), _ptr(nbr), _ptr(out_order), _ptr(kofs),
+                             kofs_host.ctypes.data_as(ctypes.POINTER(ctypes.c_int64)),
+                             ctypes.byref(flags), st), "rhip_kmap_count")
     P = int(kofs_host[-1])
     in_rows = torch.empty(max(P, 1), dtype=torch.int32, device=dev)
     out_rows = torch.empty(max(P, 1), dtype=torch.int32, device=dev)
     nbr_t = torch.empty((K, max(n_in, 1)), dtype=torch.int32, device=dev)
     in_order = torch.empty(max(n_in, 1), dtype=torch.int32, device=dev)
     _check(L.rhip_kmap_fill(_ptr(nbr), _ptr(out_order), n_out, K, _ptr(in_table.order), n_in,
-                            _ptr(ws), ws.numel(), _ptr(in_rows), _ptr(out_rows), _ptr(nbr_t),
-                            _ptr(in_order), st), "rhip_kmap_fill")
+                            flags.value, _ptr(ws), ws.numel(), _ptr(kofs), _ptr(in_rows),
+                            _ptr(out_rows), _ptr(nbr_t), _ptr(in_order), st), "rhip_kmap_fill")
     return KernelMap(K, n_in, n_out, kofs, kofs_host, in_rows[:P], out_rows[:P],
-                     nbr[:, :n_out], nbr_t[:, :n_in], in_order[:n_in], out_order[:n_out])
+                     nbr[:, :n_out], nbr_t[:, :n_in], in_order[:n_in], out_order[:n_out],
+                     symmetric=bool(flags.value & KMAP_SYMMETRIC))
 
 
 # ------------------------------------------------------------ convolution

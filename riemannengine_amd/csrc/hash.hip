@@ -409,7 +409,7 @@ extern "C" int rhip_hash_build(const int32_t *coords, int64_t n, int32_t ncol,
     hipLaunchKernelGGL(count_first_kernel, dim3(nb), dim3(kBlock), 0, stream, n,
                        sl, w.slot_of_row, w.block_counts);
     RHIP_LAUNCH_CHECK();
-    hipLaunchKernelGGL(scan_counts_kernel<0>, dim3(1), dim3(1024), 0, stream,
+    hipLaunchKernelGGL(scan_kernel<int32_t>, dim3(1), dim3(1024), 0, stream,
                        w.block_counts, nb, w.block_base, w.total);
     RHIP_LAUNCH_CHECK();
     hipLaunchKernelGGL(assign_uid_kernel, dim3(nb), dim3(kBlock), 0, stream,

@@ -417,7 +417,7 @@ HipKernelMap CoordinateManager::generate(const CoordinateMapHIP &in_map,
   const int32_t K = static_cast<int32_t>(offsets_host.size(0));
   const int64_t n_in = in_map.size(), n_out = out_map.size();
   auto iopt = torch::TensorOptions().device(dev).dtype(torch::kInt32);
-  auto offsets = offsets_host.to(dev).contiguous();
+  auto offsets = offsets_host.to(at::kCPU).to(torch::kInt32).contiguous();
   HipKernelMap m;
   m.K = K;
   m.n_in = n_in;
@@ -429,11 +429,12 @@ HipKernelMap CoordinateManager::generate(const CoordinateMapHIP &in_map,
   auto out_order = torch::empty({std::max<int64_t>(n_out, 1)}, iopt);
   m.offsets = torch::empty({K + 1}, iopt.dtype(torch::kInt64));
   m.offsets_host.assign(K + 1, 0);
+  int32_t flags = 0;
   check_rhip(rhip_kmap_count(&in_map.table, out_map.coords.data_ptr<int32_t>(),
                              out_map.order.data_ptr<int32_t>(), n_out, K,
                              offsets.data_ptr<int32_t>(), ws.data_ptr(), ws.numel(),
                              nbr.data_ptr<int32_t>(), out_order.data_ptr<int32_t>(),
-                             m.offsets.data_ptr<int64_t>(), m.offsets_host.data(), st),
+                             m.offsets.data_ptr<int64_t>(), m.offsets_host.data(), &flags, st),
              "rhip_kmap_count");
   const int64_t P = m.offsets_host[K];
   auto in_rows = torch::empty({std::max<int64_t>(P, 1)}, iopt);
@@ -441,7 +442,8 @@ HipKernelMap CoordinateManager::generate(const CoordinateMapHIP &in_map,
   auto nbr_t = torch::empty({K, std::max<int64_t>(n_in, 1)}, iopt);
   auto in_order = torch::empty({std::max<int64_t>(n_in, 1)}, iopt);
   check_rhip(rhip_kmap_fill(nbr.data_ptr<int32_t>(), out_order.data_ptr<int32_t>(), n_out, K,
-                            in_map.order.data_ptr<int32_t>(), n_in, ws.data_ptr(), ws.numel(),
+                            in_map.order.data_ptr<int32_t>(), n_in, flags, ws.data_ptr(),
+                            ws.numel(), m.offsets.data_ptr<int64_t>(),
                             in_rows.data_ptr<int32_t>(), out_rows.data_ptr<int32_t>(),
                             nbr_t.data_ptr<int32_t>(), in_order.data_ptr<int32_t>(), st),
              "rhip_kmap_fill");

@@ -17,19 +17,29 @@
 //
 // Phase 1 (rhip_kmap_count):
 //   query    one lane per (output, offset) probes the input table in the
-//            output map's locality order -> nbr_sp[k][j];
-//   masks    one lane per output row folds its K hits into a sort key;
-//   sort     stable radix sort of rows by mask key (bits [0, min(K, 32)));
+//            output map's locality order -> nbr_sp[k][j]. For a map of a set
+//            onto itself whose stencil is closed under negation (every offset
+//            k has a partner k' with offset k' = -offset k) only one offset
+//            of each pair is probed: o pairs with i under k iff i pairs with
+//            o under k', so the partner row is a scatter of the probed one and
+//            the zero offset is the identity;
+//   masks    one lane per output row folds its K hits into a sort key (the
+//            mask for K <= 16, else a 16-bit hash of it);
+//   sort     stable radix sort of the rows by key;
 //   permute  nbr[k][p] = nbr_sp[k][j(p)], out_order[p] = row of p, and a
 //            wave-ballot count of hits per (offset, workgroup);
-//   scan     exclusive scan of the counts, offset-major -> CSR of pairs.
+//   scan     per-offset exclusive scans of the counts (one workgroup per
+//            offset), then the CSR offsets of the pairs.
 // Phase 2 (rhip_kmap_fill):
 //   emit     ballot + mbcnt compaction of nbr into per-offset pair lists
-//            (ordered by offset, then processing position), and the input
-//            rows' transposed masks (atomicOr);
-//   sort     input rows by transposed mask -> in_order / in_pos;
-//   transpose nbr_t[k][in_pos[i]] = output row paired with i under k.
+//            (ordered by offset, then processing position);
+//   symmetric maps: the input order is the output order and the transposed
+//            table is the forward table with partner offsets (a copy);
+//   otherwise: the input rows' transposed masks (atomicOr during the emit),
+//            a sort of the input rows by them -> in_order / in_pos, and
+//            nbr_t[k][in_pos[i]] = output row paired with i under k.
 #include <algorithm>
+#include <vector>
 
 #include "rhip_internal.hpp"
 
@@ -37,12 +47,14 @@ namespace rhip {
 
 constexpr int kMapBlock = 256;
 constexpr int kMaskedK = 128; // neighbour masks (and mask order) for K <= 128
+constexpr int kKeyBits = 16;  // sort-key width of a neighbour mask
 
 __global__ __launch_bounds__(kMapBlock) void kmap_query_kernel(
     TableView t, const int32_t *__restrict__ out_coords,
     const int32_t *__restrict__ spatial, int64_t n_out,
-    const int32_t *__restrict__ offsets, int32_t *__restrict__ nbr_sp) {
-  const int k = blockIdx.y;
+    const int32_t *__restrict__ offsets, const int32_t *__restrict__ klist,
+    int32_t *__restrict__ nbr_sp) {
+  const int k = klist ? klist[blockIdx.y] : blockIdx.y;
   const int64_t j = blockIdx.x * (int64_t)kMapBlock + threadIdx.x;
   if (j >= n_out)
     return;
@@ -60,13 +72,53 @@ __global__ __launch_bounds__(kMapBlock) void kmap_query_kernel(
   nbr_sp[k * n_out + j] = table_find(t, c);
 }
 
-// 32-bit sort key of a neighbour mask: the mask itself for K <= 32, else a
+// Symmetric maps: the partner row of every probed offset k = klist[y];
+// nbr_sp[partner[k]][pos[i]] = row of j for every hit i = nbr_sp[k][j].
+__global__ __launch_bounds__(kMapBlock) void kmap_mirror_kernel(
+    int32_t *__restrict__ nbr_sp, const int32_t *__restrict__ spatial,
+    const int32_t *__restrict__ pos, int64_t n, const int32_t *__restrict__ klist,
+    const int32_t *__restrict__ partner) {
+  const int k = klist[blockIdx.y];
+  const int64_t j = blockIdx.x * (int64_t)kMapBlock + threadIdx.x;
+  if (j >= n)
+    return;
+  const int32_t i = nbr_sp[k * n + j];
+  if (i >= 0)
+    nbr_sp[static_cast<int64_t>(partner[k]) * n + (pos ? pos[i] : i)] =
+        spatial ? spatial[j] : static_cast<int32_t>(j);
+}
+
+// table[partner[klist[y]]][j] = v: clears the rows the mirror scatters into.
+__global__ __launch_bounds__(kMapBlock) void fill_partner_rows_kernel(
+    int32_t *__restrict__ table, int64_t n, const int32_t *__restrict__ klist,
+    const int32_t *__restrict__ partner, int32_t v) {
+  const int64_t j = blockIdx.x * (int64_t)kMapBlock + threadIdx.x;
+  if (j < n)
+    table[static_cast<int64_t>(partner[klist[blockIdx.y]]) * n + j] = v;
+}
+
+// The zero offset of a map onto itself: every row is its own neighbour.
+__global__ __launch_bounds__(kMapBlock) void kmap_identity_kernel(
+    int32_t *__restrict__ row, const int32_t *__restrict__ spatial, int64_t n) {
+  const int64_t j = blockIdx.x * (int64_t)kMapBlock + threadIdx.x;
+  if (j < n)
+    row[j] = spatial ? spatial[j] : static_cast<int32_t>(j);
+}
+
+__global__ __launch_bounds__(kMapBlock) void invert_order_kernel(
+    const int32_t *__restrict__ order, int64_t n, int32_t *__restrict__ pos) {
+  const int64_t j = blockIdx.x * (int64_t)kMapBlock + threadIdx.x;
+  if (j < n)
+    pos[order[j]] = static_cast<int32_t>(j);
+}
+
+// Sort key of a neighbour mask: the mask itself for K <= 16, else a 16-bit
 // hash (equal masks get equal keys; unequal ones rarely collide, which only
-// costs locality, never correctness).
-__device__ __forceinline__ uint32_t mask_key32(uint64_t m0, uint64_t m1, int K) {
-  if (K <= 32)
+// costs MFMA fill, never correctness).
+__device__ __forceinline__ uint32_t mask_key(uint64_t m0, uint64_t m1, int K) {
+  if (K <= kKeyBits)
     return static_cast<uint32_t>(m0);
-  return static_cast<uint32_t>(mix64(m0 ^ mix64(m1 ^ 0x9e3779b97f4a7c15ull)) >> 32);
+  return static_cast<uint32_t>(mix64(m0 ^ mix64(m1 ^ 0x9e3779b97f4a7c15ull)) >> 48);
 }
 
 __global__ __launch_bounds__(kMapBlock) void mask_key_kernel(
@@ -83,7 +135,7 @@ __global__ __launch_bounds__(kMapBlock) void mask_key_kernel(
     else
       m1 |= h << (k - 64);
   }
-  keys[j] = mask_key32(m0, m1, K);
+  keys[j] = mask_key(m0, m1, K);
   vals[j] = static_cast<int32_t>(j);
 }
 
@@ -126,14 +178,33 @@ __global__ __launch_bounds__(kMapBlock) void kmap_permute_kernel(
   }
 }
 
-__global__ void kmap_offsets_kernel(const int64_t *block_base,
-                                    const int64_t *total, int K, int64_t nb,
-                                    int64_t *kmap_offsets) {
-  int k = blockIdx.x * blockDim.x + threadIdx.x;
-  if (k < K)
-    kmap_offsets[k] = block_base[static_cast<int64_t>(k) * nb];
-  if (k == K)
-    kmap_offsets[K] = *total;
+// kmap_offsets[k] = sum of the per-offset totals before k (one workgroup).
+__global__ __launch_bounds__(1024) void kmap_offsets_kernel(const int64_t *ktotal, int K,
+                                                            int64_t *kmap_offsets,
+                                                            int64_t *scratch) {
+  __shared__ int64_t partial[1024];
+  const int t = threadIdx.x;
+  const int per = (K + 1023) / 1024;
+  const int b = t * per, e = min(K, b + per);
+  int64_t s = 0;
+  for (int i = b; i < e; ++i)
+    s += ktotal[i];
+  partial[t] = s;
+  __syncthreads();
+  for (int off = 1; off < 1024; off <<= 1) {
+    int64_t v = t >= off ? partial[t - off] : 0;
+    __syncthreads();
+    partial[t] += v;
+    __syncthreads();
+  }
+  int64_t run = partial[t] - s;
+  for (int i = b; i < e; ++i) {
+    kmap_offsets[i] = run;
+    run += ktotal[i];
+  }
+  if (t == 1023)
+    kmap_offsets[K] = partial[1023];
+  (void)scratch;
 }
 
 __global__ __launch_bounds__(kMapBlock) void fill_i32_kernel(int32_t *p,
@@ -153,9 +224,9 @@ __global__ __launch_bounds__(kMapBlock) void zero_u64_kernel(unsigned long long 
 
 __global__ __launch_bounds__(kMapBlock) void kmap_emit_kernel(
     const int32_t *__restrict__ nbr, const int32_t *__restrict__ out_order,
-    int64_t n_out, const int64_t *__restrict__ block_base,
-    int32_t *__restrict__ in_rows, int32_t *__restrict__ out_rows,
-    unsigned long long *__restrict__ mask_t) {
+    int64_t n_out, const int64_t *__restrict__ kofs,
+    const int64_t *__restrict__ block_base, int32_t *__restrict__ in_rows,
+    int32_t *__restrict__ out_rows, unsigned long long *__restrict__ mask_t) {
   __shared__ int32_t wave_counts[kMapBlock / kWave];
   const int k = blockIdx.y;
   const int64_t p = blockIdx.x * (int64_t)kMapBlock + threadIdx.x;
@@ -164,13 +235,34 @@ __global__ __launch_bounds__(kMapBlock) void kmap_emit_kernel(
   uint64_t b;
   const int32_t before = block_hit_base(hit, wave_counts, b);
   if (hit) {
-    const int64_t q = block_base[static_cast<int64_t>(k) * gridDim.x + blockIdx.x] +
+    const int64_t q = kofs[k] + block_base[static_cast<int64_t>(k) * gridDim.x + blockIdx.x] +
                       before + lanes_below(b);
     in_rows[q] = v;
     out_rows[q] = out_order[p];
     if (mask_t)
       atomicOr(&mask_t[2 * static_cast<int64_t>(v) + (k >> 6)], 1ull << (k & 63));
   }
+}
+
+// Symmetric maps: nbr_t[k] = nbr[partner[k]] (rows of one map, same order).
+// A partner outside [0, K) (a workspace not prepared by phase 1) leaves the
+// row untouched instead of reading out of bounds.
+__global__ __launch_bounds__(kMapBlock) void kmap_partner_copy_kernel(
+    const int32_t *__restrict__ nbr, int64_t n, int K, const int32_t *__restrict__ partner,
+    int32_t *__restrict__ nbr_t) {
+  const int k = blockIdx.y;
+  const int64_t j = blockIdx.x * (int64_t)kMapBlock + threadIdx.x;
+  const int32_t pk = partner[k];
+  if (j < n && pk >= 0 && pk < K)
+    nbr_t[k * n + j] = nbr[static_cast<int64_t>(pk) * n + j];
+}
+
+__global__ __launch_bounds__(kMapBlock) void copy_i32_kernel(const int32_t *__restrict__ src,
+                                                             int64_t n,
+                                                             int32_t *__restrict__ dst) {
+  const int64_t j = blockIdx.x * (int64_t)kMapBlock + threadIdx.x;
+  if (j < n)
+    dst[j] = src[j];
 }
 
 __global__ __launch_bounds__(kMapBlock) void in_key_kernel(
@@ -180,7 +272,7 @@ __global__ __launch_bounds__(kMapBlock) void in_key_kernel(
   if (q >= n)
     return;
   const int64_t i = spatial ? spatial[q] : q;
-  keys[q] = mask_key32(mask_t[2 * i], mask_t[2 * i + 1], K);
+  keys[q] = mask_key(mask_t[2 * i], mask_t[2 * i + 1], K);
   vals[q] = static_cast<int32_t>(q);
 }
 
@@ -209,14 +301,21 @@ __global__ __launch_bounds__(kMapBlock) void kmap_transpose_kernel(
     nbr_t[k * n_in + in_pos[v]] = out_order[p];
 }
 
-// Workspace: the per-block counts and their scan persist from phase 1 to
-// phase 2; each phase's scratch reuses the same region after them.
+// Workspace: the per-block counts, their scans and the per-offset totals
+// persist from phase 1 to phase 2; each phase's scratch reuses the same
+// region after them.
 struct KmapWs {
   int32_t *block_counts;
   int64_t *block_base;
-  int64_t *total;
+  int64_t *ktotal;
+  int32_t *offsets;  // [K][D] stencil (D = the table's ncol - 1)
+  int32_t *plan;     // partner[K] | probe list[K] | mirror list[K]
+  int32_t *partner;
+  int32_t *probe;
+  int32_t *mirror;
   // phase 1
   int32_t *nbr_sp;
+  int32_t *pos;
   uint32_t *keys_a, *keys_b;
   int32_t *vals_a, *vals_b;
   void *sort_tmp;
@@ -229,15 +328,21 @@ struct KmapWs {
   size_t tsort_bytes;
 };
 
-static KmapWs carve_kmap(Carve &cv, int64_t n_in, int64_t n_out, int32_t K) {
+static KmapWs carve_kmap(Carve &cv, int64_t n_in, int64_t n_out, int32_t K, int32_t D) {
   const int64_t nb = std::max<int64_t>(1, ceil_div(n_out, kMapBlock));
   const int64_t mo = std::max<int64_t>(n_out, 1), mi = std::max<int64_t>(n_in, 1);
   KmapWs w{};
   w.block_counts = cv.take<int32_t>(nb * K);
   w.block_base = cv.take<int64_t>(nb * K);
-  w.total = cv.take<int64_t>(1);
+  w.ktotal = cv.take<int64_t>(K);
+  w.offsets = cv.take<int32_t>(static_cast<size_t>(K) * std::max(D, 1));
+  w.plan = cv.take<int32_t>(3 * static_cast<size_t>(K));
+  w.partner = w.plan;
+  w.probe = w.plan ? w.plan + K : nullptr;
+  w.mirror = w.plan ? w.plan + 2 * K : nullptr;
   const size_t base = cv.used;
   w.nbr_sp = cv.take<int32_t>(mo * K);
+  w.pos = cv.take<int32_t>(mo);
   w.keys_a = cv.take<uint32_t>(mo);
   w.keys_b = cv.take<uint32_t>(mo);
   w.vals_a = cv.take<int32_t>(mo);
@@ -258,6 +363,64 @@ static KmapWs carve_kmap(Carve &cv, int64_t n_in, int64_t n_out, int32_t K) {
   return w;
 }
 
+// Host plan of a symmetric map: a map of a set onto itself (same rows, same
+// order) whose offsets are distinct and closed under negation: partner[K],
+// the offsets to probe and the probed offsets whose partner row is mirrored
+// from them (the KmapWs::plan layout).
+struct SymPlan {
+  bool ok = false;
+  int zero = -1; // the zero offset (identity row), if any
+  int n_probe = 0, n_mirror = 0;
+  std::vector<int32_t> lists; // partner | probe | mirror, K entries each
+};
+
+static SymPlan symmetric_plan(const rhip_table *in_table, const int32_t *out_coords,
+                              int64_t n_out, int32_t K, const int32_t *offsets_host) {
+  SymPlan p;
+  const int D = in_table->ncol - 1;
+  p.lists.assign(3 * static_cast<size_t>(K), 0);
+  int32_t *partner = p.lists.data();
+  int32_t *probe = partner + K, *mirror = probe + K;
+  if (out_coords != in_table->rows || n_out != in_table->n_unique || n_out < 2 ||
+      K > kMaskedK)
+    return p;
+  auto row = [&](int k) { return offsets_host + static_cast<size_t>(k) * D; };
+  for (int a = 0; a < K; ++a) {
+    partner[a] = -1;
+    bool zero = true;
+    for (int d = 0; d < D; ++d)
+      zero = zero && row(a)[d] == 0;
+    if (zero)
+      p.zero = a;
+    for (int b = 0; b < K; ++b) {
+      bool same = b != a, neg = true;
+      for (int d = 0; d < D; ++d) {
+        same = same && row(b)[d] == row(a)[d];
+        neg = neg && static_cast<uint32_t>(row(b)[d]) ==
+                         0u - static_cast<uint32_t>(row(a)[d]); // wrap-around negation
+      }
+      if (same)
+        return p; // repeated offsets: the general path
+      if (neg)
+        partner[a] = b;
+    }
+    if (partner[a] < 0)
+      return p;
+  }
+  for (int k = 0; k < K; ++k) {
+    if (k == p.zero)
+      continue;
+    if (partner[k] > k) {
+      probe[p.n_probe++] = k;
+      mirror[p.n_mirror++] = k;
+    } else if (partner[k] == k) { // offset == -offset without being zero
+      probe[p.n_probe++] = k;
+    }
+  }
+  p.ok = true;
+  return p;
+}
+
 } // namespace rhip
 
 using namespace rhip;
@@ -268,44 +431,85 @@ extern "C" int rhip_kmap_workspace_bytes(int64_t n_in, int64_t n_out, int32_t K,
     RHIP_CHECK_ARG(bytes != nullptr, "bytes is null");
     RHIP_CHECK_ARG(n_in >= 0 && n_out >= 0 && K >= 1, "need n_in, n_out >= 0 and K >= 1");
     Carve cv(nullptr, 0);
-    carve_kmap(cv, n_in, n_out, K);
+    carve_kmap(cv, n_in, n_out, K, RHIP_MAX_COLS - 1);
     *bytes = cv.used + 256;
   });
 }
 
 extern "C" int rhip_kmap_count(const rhip_table *in_table, const int32_t *out_coords,
                                const int32_t *out_spatial_order, int64_t n_out,
-                               int32_t K, const int32_t *offsets, void *workspace,
+                               int32_t K, const int32_t *offsets_host, void *workspace,
                                size_t workspace_bytes, int32_t *nbr, int32_t *out_order,
                                int64_t *kmap_offsets, int64_t *kmap_offsets_host,
-                               hipStream_t stream) {
+                               int32_t *flags, hipStream_t stream) {
   return guarded([&] {
     RHIP_CHECK_ARG(in_table != nullptr, "in_table is null");
     RHIP_CHECK_ARG(K >= 1 && K <= 65535, "K must be in [1, 65535]");
     RHIP_CHECK_ARG(n_out >= 0 && n_out < INT32_MAX, "bad n_out");
-    RHIP_CHECK_ARG(kmap_offsets && kmap_offsets_host && workspace,
-                   "kmap_offsets, kmap_offsets_host and workspace are required");
+    RHIP_CHECK_ARG(kmap_offsets && kmap_offsets_host && workspace && offsets_host,
+                   "offsets_host, kmap_offsets, kmap_offsets_host and workspace are required");
+    const int D = in_table->ncol - 1;
     Carve cv(workspace, workspace_bytes);
-    KmapWs w = carve_kmap(cv, in_table->n_unique, n_out, K);
+    KmapWs w = carve_kmap(cv, in_table->n_unique, n_out, K, RHIP_MAX_COLS - 1);
     const int64_t nb = std::max<int64_t>(1, ceil_div(n_out, kMapBlock));
+    const SymPlan plan = symmetric_plan(in_table, out_coords, n_out, K, offsets_host);
+    const bool sym = plan.ok;
+    if (flags)
+      *flags = sym ? RHIP_KMAP_SYMMETRIC : 0;
     if (n_out == 0) {
       hipLaunchKernelGGL(fill_i32_kernel, dim3(ceil_div(nb * K, kMapBlock)),
                          dim3(kMapBlock), 0, stream, w.block_counts, nb * K, 0);
       RHIP_LAUNCH_CHECK();
     } else {
-      RHIP_CHECK_ARG(out_coords && offsets && nbr && out_order,
-                     "out_coords, offsets, nbr and out_order are required");
-      hipLaunchKernelGGL(kmap_query_kernel, dim3(nb, K), dim3(kMapBlock), 0, stream,
-                         make_view(*in_table), out_coords, out_spatial_order, n_out,
-                         offsets, w.nbr_sp);
-      RHIP_LAUNCH_CHECK();
+      RHIP_CHECK_ARG(out_coords && nbr && out_order, "out_coords, nbr and out_order are required");
+      // pageable sources: both stay alive until the synchronize below
+      RHIP_HIP(hipMemcpyAsync(w.offsets, offsets_host, sizeof(int32_t) * K * D,
+                              hipMemcpyHostToDevice, stream));
+      if (sym)
+        RHIP_HIP(hipMemcpyAsync(w.plan, plan.lists.data(), sizeof(int32_t) * plan.lists.size(),
+                                hipMemcpyHostToDevice, stream));
+      const TableView tv = make_view(*in_table);
+      if (sym) {
+        if (plan.n_mirror > 0) {
+          hipLaunchKernelGGL(fill_partner_rows_kernel, dim3(nb, plan.n_mirror),
+                             dim3(kMapBlock), 0, stream, w.nbr_sp, n_out, w.mirror, w.partner,
+                             -1);
+          RHIP_LAUNCH_CHECK();
+        }
+        if (plan.n_probe > 0) {
+          hipLaunchKernelGGL(kmap_query_kernel, dim3(nb, plan.n_probe), dim3(kMapBlock), 0,
+                             stream, tv, out_coords, out_spatial_order, n_out, w.offsets,
+                             w.probe, w.nbr_sp);
+          RHIP_LAUNCH_CHECK();
+        }
+        if (plan.n_mirror > 0) {
+          if (out_spatial_order) {
+            hipLaunchKernelGGL(invert_order_kernel, dim3(nb), dim3(kMapBlock), 0, stream,
+                               out_spatial_order, n_out, w.pos);
+            RHIP_LAUNCH_CHECK();
+          }
+          hipLaunchKernelGGL(kmap_mirror_kernel, dim3(nb, plan.n_mirror), dim3(kMapBlock), 0,
+                             stream, w.nbr_sp, out_spatial_order,
+                             out_spatial_order ? w.pos : nullptr, n_out, w.mirror, w.partner);
+          RHIP_LAUNCH_CHECK();
+        }
+        if (plan.zero >= 0) {
+          hipLaunchKernelGGL(kmap_identity_kernel, dim3(nb), dim3(kMapBlock), 0, stream,
+                             w.nbr_sp + plan.zero * n_out, out_spatial_order, n_out);
+          RHIP_LAUNCH_CHECK();
+        }
+      } else {
+        hipLaunchKernelGGL(kmap_query_kernel, dim3(nb, K), dim3(kMapBlock), 0, stream, tv,
+                           out_coords, out_spatial_order, n_out, w.offsets, nullptr, w.nbr_sp);
+        RHIP_LAUNCH_CHECK();
+      }
       const int32_t *jpos = nullptr;
       if (K <= kMaskedK && n_out > 1 && in_table->n_unique > 0) {
         hipLaunchKernelGGL(mask_key_kernel, dim3(nb), dim3(kMapBlock), 0, stream,
                            w.nbr_sp, n_out, K, w.keys_a, w.vals_a);
         RHIP_LAUNCH_CHECK();
         sort_pairs_u32(w.sort_tmp, w.sort_bytes, w.keys_a, w.keys_b, w.vals_a, w.vals_b,
-                       n_out, std::min<int>(K, 32), stream);
+                       n_out, std::min<int>(K, kKeyBits), stream);
         jpos = w.vals_b;
       }
       hipLaunchKernelGGL(kmap_permute_kernel, dim3(nb, K), dim3(kMapBlock), 0, stream,
@@ -313,11 +517,11 @@ extern "C" int rhip_kmap_count(const rhip_table *in_table, const int32_t *out_co
                          w.block_counts);
       RHIP_LAUNCH_CHECK();
     }
-    hipLaunchKernelGGL(scan_counts_kernel<0>, dim3(1), dim3(1024), 0, stream,
-                       w.block_counts, nb * K, w.block_base, w.total);
+    hipLaunchKernelGGL(scan_kernel<int32_t>, dim3(K), dim3(1024), 0, stream, w.block_counts,
+                       nb, w.block_base, w.ktotal);
     RHIP_LAUNCH_CHECK();
-    hipLaunchKernelGGL(kmap_offsets_kernel, dim3(ceil_div(K + 1, 256)), dim3(256), 0,
-                       stream, w.block_base, w.total, K, nb, kmap_offsets);
+    hipLaunchKernelGGL(kmap_offsets_kernel, dim3(1), dim3(1024), 0, stream, w.ktotal, K,
+                       kmap_offsets, nullptr);
     RHIP_LAUNCH_CHECK();
     RHIP_HIP(hipMemcpyAsync(kmap_offsets_host, kmap_offsets, sizeof(int64_t) * (K + 1),
                             hipMemcpyDeviceToHost, stream));
@@ -327,20 +531,24 @@ extern "C" int rhip_kmap_count(const rhip_table *in_table, const int32_t *out_co
 
 extern "C" int rhip_kmap_fill(const int32_t *nbr, const int32_t *out_order, int64_t n_out,
                               int32_t K, const int32_t *in_spatial_order, int64_t n_in,
-                              void *workspace, size_t workspace_bytes, int32_t *in_rows,
+                              int32_t flags, void *workspace, size_t workspace_bytes,
+                              const int64_t *kmap_offsets, int32_t *in_rows,
                               int32_t *out_rows, int32_t *nbr_t, int32_t *in_order,
                               hipStream_t stream) {
   return guarded([&] {
     RHIP_CHECK_ARG(K >= 1 && K <= 65535, "K must be in [1, 65535]");
-    RHIP_CHECK_ARG(workspace != nullptr, "workspace is null");
+    RHIP_CHECK_ARG(workspace != nullptr && kmap_offsets != nullptr,
+                   "workspace and kmap_offsets are required");
     RHIP_CHECK_ARG(n_in >= 0 && n_in < INT32_MAX && n_out >= 0 && n_out < INT32_MAX,
                    "bad sizes");
+    const bool sym = (flags & RHIP_KMAP_SYMMETRIC) != 0;
+    RHIP_CHECK_ARG(!sym || n_in == n_out, "a symmetric map has n_in == n_out");
     Carve cv(workspace, workspace_bytes);
-    KmapWs w = carve_kmap(cv, n_in, n_out, K);
+    KmapWs w = carve_kmap(cv, n_in, n_out, K, RHIP_MAX_COLS - 1);
     const int64_t nb = std::max<int64_t>(1, ceil_div(n_out, kMapBlock));
     const bool want_t = nbr_t != nullptr && n_in > 0;
     RHIP_CHECK_ARG(!want_t || in_order != nullptr, "in_order is required with nbr_t");
-    const bool masks = want_t && K <= kMaskedK && n_in > 1;
+    const bool masks = want_t && !sym && K <= kMaskedK && n_in > 1;
     if (masks) {
       hipLaunchKernelGGL(zero_u64_kernel, dim3(ceil_div(2 * n_in, kMapBlock)),
                          dim3(kMapBlock), 0, stream, w.mask_t, 2 * n_in);
@@ -349,20 +557,29 @@ extern "C" int rhip_kmap_fill(const int32_t *nbr, const int32_t *out_order, int6
     if (n_out > 0) {
       RHIP_CHECK_ARG(nbr && out_order, "nbr and out_order are required");
       hipLaunchKernelGGL(kmap_emit_kernel, dim3(nb, K), dim3(kMapBlock), 0, stream, nbr,
-                         out_order, n_out, w.block_base, in_rows, out_rows,
+                         out_order, n_out, kmap_offsets, w.block_base, in_rows, out_rows,
                          masks ? w.mask_t : nullptr);
       RHIP_LAUNCH_CHECK();
     }
     if (!want_t)
       return;
     const int64_t nbi = ceil_div(n_in, kMapBlock);
+    if (sym) {
+      hipLaunchKernelGGL(copy_i32_kernel, dim3(nbi), dim3(kMapBlock), 0, stream, out_order,
+                         n_in, in_order);
+      RHIP_LAUNCH_CHECK();
+      hipLaunchKernelGGL(kmap_partner_copy_kernel, dim3(nbi, K), dim3(kMapBlock), 0, stream,
+                         nbr, n_in, K, w.partner, nbr_t);
+      RHIP_LAUNCH_CHECK();
+      return;
+    }
     const int32_t *qpos = nullptr;
     if (masks) {
       hipLaunchKernelGGL(in_key_kernel, dim3(nbi), dim3(kMapBlock), 0, stream, w.mask_t,
                          in_spatial_order, n_in, K, w.tkeys_a, w.tvals_a);
       RHIP_LAUNCH_CHECK();
       sort_pairs_u32(w.tsort_tmp, w.tsort_bytes, w.tkeys_a, w.tkeys_b, w.tvals_a, w.tvals_b,
-                     n_in, std::min<int>(K, 32), stream);
+                     n_in, std::min<int>(K, kKeyBits), stream);
       qpos = w.tvals_b;
     }
     hipLaunchKernelGGL(in_order_kernel, dim3(nbi), dim3(kMapBlock), 0, stream, qpos,

@@ -209,20 +209,20 @@ __device__ __forceinline__ uint32_t lanes_below(uint64_t mask) {
                                        static_cast<uint32_t>(mask), 0u));
 }
 
-// Exclusive scan of m int32 counts in one workgroup of 1024 lanes; each lane
-// owns a contiguous run. base[i] = sum(counts[0..i)), *total = sum(counts).
-template <int Dummy = 0>
-__global__ __launch_bounds__(1024) void scan_counts_kernel(const int32_t *counts,
-                                                           int64_t m,
-                                                           int64_t *base,
-                                                           int64_t *total) {
+// Segmented exclusive scan, one 1024-lane workgroup per segment (blockIdx.x):
+// base[s*m + i] = sum(counts[s*m .. s*m+i)), total[s] = sum of segment s.
+// Each lane owns a contiguous run of the segment.
+template <typename TIn>
+__global__ __launch_bounds__(1024) void scan_kernel(const TIn *counts, int64_t m,
+                                                    int64_t *base, int64_t *total) {
   __shared__ int64_t partial[1024];
   const int t = threadIdx.x;
+  const int64_t seg = static_cast<int64_t>(blockIdx.x) * m;
   const int64_t per = (m + 1023) / 1024;
   const int64_t b = t * per, e = min(m, b + per);
   int64_t s = 0;
   for (int64_t i = b; i < e; ++i)
-    s += counts[i];
+    s += counts[seg + i];
   partial[t] = s;
   __syncthreads();
   // Hillis-Steele inclusive scan over the 1024 partial sums.
@@ -234,11 +234,11 @@ __global__ __launch_bounds__(1024) void scan_counts_kernel(const int32_t *counts
   }
   int64_t run = partial[t] - s;
   for (int64_t i = b; i < e; ++i) {
-    base[i] = run;
-    run += counts[i];
+    base[seg + i] = run;
+    run += counts[seg + i];
   }
   if (t == 1023)
-    *total = partial[1023];
+    total[blockIdx.x] = partial[1023];
 }
 
 } // namespace rhip

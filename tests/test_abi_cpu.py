@@ -32,7 +32,7 @@ def test_library_exports_every_declared_symbol():
 
 
 def test_abi_version_and_struct_layout():
-    assert abi.lib().rhip_abi_version() == 3
+    assert abi.lib().rhip_abi_version() == 4
     # void*, int64, void*, int64, 3 x int32, 3 x int32[8] -> 140 bytes, padded to 144
     assert ctypes.sizeof(abi.RhipTable) == 144
 
@@ -54,7 +54,7 @@ def test_workspace_queries():
     (lambda L, t: L.rhip_hash_build(None, -1, 4, None, 0, None, 0, None, None, None,
                                     ctypes.byref(t), None), "row count"),
     (lambda L, t: L.rhip_kmap_count(ctypes.byref(t), None, None, 10, 0, None, None, 0, None,
-                                    None, None, None, None), "K must"),
+                                    None, None, None, None, None), "K must"),
     (lambda L, t: L.rhip_conv_forward(None, 1, 4, None, 27, 8, None, None, None, 1, None, 7,
                                       None, 0, None), "dtype"),
 ])

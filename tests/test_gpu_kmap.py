@@ -32,6 +32,32 @@ def _mask_groups(table):
     return int(1 + np.any(m[1:] != m[:-1], axis=1).sum())
 
 
+_M64 = np.uint64(0xFFFFFFFFFFFFFFFF)
+
+
+def _mix64(k):
+    """MurmurHash3's 64-bit finalizer on uint64 arrays (wrapping products)."""
+    k = k ^ (k >> np.uint64(33))
+    k = k * np.uint64(0xff51afd7ed558ccd)
+    k = k ^ (k >> np.uint64(33))
+    k = k * np.uint64(0xc4ceb9fe1a85ec53)
+    return k ^ (k >> np.uint64(33))
+
+
+def _mask_keys(table):
+    """Sort key of each column's neighbour mask: the mask for K <= 16, else a
+    16-bit hash of its two 64-bit words."""
+    K = table.shape[0]
+    hit = (table >= 0).astype(np.uint64)
+    m = np.zeros((2, table.shape[1]), np.uint64)
+    for k in range(K):
+        m[k // 64] |= hit[k] << np.uint64(k % 64)
+    if K <= 16:
+        return m[0]
+    with np.errstate(over="ignore"):
+        return _mix64(m[0] ^ _mix64(m[1] ^ np.uint64(0x9e3779b97f4a7c15))) >> np.uint64(48)
+
+
 def _check_tables(km, tin, tout):
     """nbr/nbr_t hold exactly the pairs at the map's processing positions;
     the orders are permutations that group equal neighbour masks."""
@@ -52,15 +78,23 @@ def _check_tables(km, tin, tout):
         a, b = km.offsets_host[k], km.offsets_host[k + 1]
         assert np.all(np.diff(pos_out[orr[a:b]]) > 0)
     if km.K <= 128:
-        # equal masks are contiguous: runs == distinct masks
-        for tab in (nbr, nbr_t):
-            distinct = len(np.unique((tab >= 0).T, axis=0)) if tab.shape[1] else 0
-            assert _mask_groups(tab) == distinct
+        # rows are in mask-key order (a symmetric map orders its input side
+        # like its output side); with K <= 16 the key is the mask and equal
+        # masks are contiguous
+        tabs = (nbr,) if km.symmetric else (nbr, nbr_t)
+        if km.symmetric:
+            np.testing.assert_array_equal(km.in_order.cpu().numpy(), km.out_order.cpu().numpy())
+        for tab in tabs:
+            assert np.all(np.diff(_mask_keys(tab).astype(np.int64)) >= 0)
+            if km.K <= 16:
+                distinct = len(np.unique((tab >= 0).T, axis=0)) if tab.shape[1] else 0
+                assert _mask_groups(tab) == distinct
 
 
 @pytest.mark.parametrize("D,ks,dil,ts,region", [
     (3, 3, 1, 1, "cube"), (3, 3, 2, 1, "cube"), (3, 3, 1, 2, "cube"), (3, 5, 1, 1, "cube"),
-    (4, 3, 1, 1, "cube"), (3, 3, 1, 1, "cross"), (2, 3, 1, 1, "cube"), (3, 1, 1, 1, "cube")])
+    (4, 3, 1, 1, "cube"), (3, 3, 1, 1, "cross"), (2, 3, 1, 1, "cube"), (3, 1, 1, 1, "cube"),
+    (3, 2, 1, 1, "cube")])
 def test_same_set_map_matches_oracle(D, ks, dil, ts, region):
     rng = np.random.default_rng(D * 100 + ks * 10 + dil)
     c = random_coords(rng, 20000, D, 14) * np.array([1] + [ts] * D, np.int32)
@@ -72,6 +106,18 @@ def test_same_set_map_matches_oracle(D, ks, dil, ts, region):
     np.testing.assert_array_equal(km.offsets_host, kofs)
     np.testing.assert_array_equal(gpu_canonical(km), ref)
     _check_tables(km, tin, tout)
+    # odd cubes and crosses are closed under negation: half the offsets are probed
+    assert km.symmetric == (ks % 2 == 1)
+    # the same coordinates in a second table take the general path; it must
+    # agree with the mirrored one row for row
+    _, tout2, km2 = gpu_tables_and_map(c, c, off, same=False)
+    assert not km2.symmetric
+    np.testing.assert_array_equal(km2.offsets_host, kofs)
+    np.testing.assert_array_equal(km2.out_order.cpu().numpy(), km.out_order.cpu().numpy())
+    np.testing.assert_array_equal(km2.nbr.cpu().numpy(), km.nbr.cpu().numpy())
+    np.testing.assert_array_equal(km2.in_rows.cpu().numpy(), km.in_rows.cpu().numpy())
+    np.testing.assert_array_equal(km2.out_rows.cpu().numpy(), km.out_rows.cpu().numpy())
+    _check_tables(km2, tin, tout2)
 
 
 def test_custom_region():
@@ -80,7 +126,16 @@ def test_custom_region():
     cust = np.array([[0, 0, 0], [2, -1, 0], [-3, 0, 1], [1, 1, 1]])
     off = oracle.region_offsets(3, 3, region="custom", custom=cust)
     tin, tout, km = gpu_tables_and_map(c, c, off, same=True)
+    assert not km.symmetric
     np.testing.assert_array_equal(gpu_canonical(km), _ref_map(c, c, off)[1])
+    _check_tables(km, tin, tout)
+    # a custom set that is point symmetric takes the mirrored path
+    sym = np.array([[1, 0, -2], [0, 3, 0], [0, 0, 0], [0, -3, 0], [-1, 0, 2]])
+    off = oracle.region_offsets(3, 3, region="custom", custom=sym)
+    tin, tout, km = gpu_tables_and_map(c, c, off, same=True)
+    assert km.symmetric
+    np.testing.assert_array_equal(gpu_canonical(km), _ref_map(c, c, off)[1])
+    _check_tables(km, tin, tout)
 
 
 @pytest.mark.parametrize("s", [2, 4])
