@@ -246,8 +246,8 @@ def main():
     roof["frac"] = round(roof["achieved"] / roof["peak"], 4)
     roof["traffic"] = measured_traffic(args.dtype, dom)
     roof["kernel"] = {"forward": "conv_os_kernel (forward)",
-                      "backward_input": "conv_os_kernel (dX, transposed weights)",
-                      "backward_weight": "conv_dw_lds_kernel"}[dom]
+                      "backward_input": "conv_os_kernel (dX)",
+                      "backward_weight": "conv_dw_kernel + conv_dw_reduce_kernel (dW pass)"}[dom]
     roof["kernel_ms"] = round(per[dom], 4)
     roof["algorithmic"] = {"flop": F, "bytes": B}
 

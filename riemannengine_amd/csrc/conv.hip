@@ -523,25 +523,43 @@ __global__ __launch_bounds__(kThreads) void conv_dw_kernel(
     slot[i] = red[i];
 }
 
-// dw[k][ci0 + i / TN][co0 + i % TN] = sum over the chunks c of offset k (in
-// chunk order) of partial[k][tile][c][i]: a deterministic second stage.
+// dw[k][ci0 + i / TN][co0 + i % TN] = sum over the chunks c of offset k of
+// partial[k][tile][c][i]: a deterministic second stage. A workgroup owns 256
+// consecutive elements (64 lanes x 4 floats); its 4 waves sum the chunks
+// c = wave (mod 4) with 16-byte loads, then the 4 phase sums are added in a
+// fixed order.
 template <typename OutT>
 __global__ __launch_bounds__(kThreads) void conv_dw_reduce_kernel(
     const float *__restrict__ partial, const int64_t *__restrict__ kofs, int64_t ppb,
     int chunks, int tiles, int tiles_n, int TM, int TN, int cin, int cout,
     OutT *__restrict__ dw) {
+  __shared__ v4f phase_sum[kWaves][kWave];
   const int k = blockIdx.y, t = blockIdx.z;
-  const int i = blockIdx.x * kThreads + threadIdx.x;
-  if (i >= TM * TN)
-    return;
+  const int lane = threadIdx.x & (kWave - 1), ph = threadIdx.x / kWave;
+  const int n4 = TM * TN / 4; // a multiple of 64
+  const int i4 = blockIdx.x * kWave + lane;
   const int64_t pk = kofs[k + 1] - kofs[k];
   const int nck = static_cast<int>(min<int64_t>(chunks, (pk + ppb - 1) / ppb));
-  const float *src = partial + (static_cast<int64_t>(k) * tiles + t) * chunks * (TM * TN) + i;
-  float sum = 0.f;
-  for (int c = 0; c < nck; ++c)
-    sum += src[static_cast<int64_t>(c) * (TM * TN)];
-  const int ci = (t / tiles_n) * TM + i / TN, co = (t % tiles_n) * TN + i % TN;
-  dw[(static_cast<int64_t>(k) * cin + ci) * cout + co] = from_f32<OutT>(sum);
+  const v4f *src = reinterpret_cast<const v4f *>(partial) +
+                   (static_cast<int64_t>(k) * tiles + t) * chunks * n4 + i4;
+  v4f sum = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll 4
+  for (int c = ph; c < nck; c += kWaves)
+    sum += src[static_cast<int64_t>(c) * n4];
+  phase_sum[ph][lane] = sum;
+  __syncthreads();
+  if (ph != 0)
+    return;
+  v4f v = phase_sum[0][lane];
+#pragma unroll
+  for (int q = 1; q < kWaves; ++q)
+    v += phase_sum[q][lane];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int i = 4 * i4 + e;
+    const int ci = (t / tiles_n) * TM + i / TN, co = (t % tiles_n) * TN + i % TN;
+    dw[(static_cast<int64_t>(k) * cin + ci) * cout + co] = from_f32<OutT>(v[e]);
+  }
 }
 
 // Any-shape fallback: one lane per dW element, looping over its pairs.
@@ -705,7 +723,7 @@ static void run_dw(const T *x, int cin, const T *gy, int cout, const int64_t *ko
       pick_dw_b<T, 1>(x, cin, gy, cout, kofs, K, in_rows, out_rows, p, partial, s);
     RHIP_LAUNCH_CHECK();
     const int TM = 16 * p.va, TN = 16 * p.vb;
-    dim3 grid(static_cast<unsigned>(ceil_div(TM * TN, kThreads)), K, p.tiles);
+    dim3 grid(static_cast<unsigned>(TM * TN / (4 * kWave)), K, p.tiles);
     hipLaunchKernelGGL((conv_dw_reduce_kernel<T>), grid, dim3(kThreads), 0, s, partial, kofs,
                        p.ppb, static_cast<int>(p.chunks), p.tiles, cout / TN, TM, TN, cin, cout,
                        dw);
