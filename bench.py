@@ -15,8 +15,9 @@ Printed as ONE JSON line:
   roofline     the dominant kernel's algorithmic FLOP/s (fp32, MFMA-bound) or
                bytes/s (bf16, HBM-bound), from HIP events recorded on the
                stream the kernels run on, against MI355X's published peak
-  cpu_baseline the CPU oracle (a scalar C restatement of the reference CPU
-               path) timed on one scene of the same workload
+  cpu_baseline the reference's own CPU path (compiled from its sources into
+               oracle/_ref) timed on one scene of the same workload, or the
+               scalar C oracle where that library was not built
 
 --gpus N > 1 is refused: this build runs on one GPU.
 """
@@ -118,14 +119,35 @@ def cpu_model() -> str:
     return platform.processor() or "unknown"
 
 
-def cpu_baseline(coords, offsets, cin, cout, seed):
-    """The CPU oracle on scene 0 of the workload: kernel map, then forward +
-    backward (input and weight gradients) with the map prebuilt. Scalar C,
-    one thread. Returns the cpu_baseline record."""
+def cpu_baseline(coords, offsets, cin, cout, seed, dtype):
+    """The CPU baseline on scene 0 of the workload (a bounded sample, ~1-3 s).
+
+    Where oracle/_ref was built, it is the reference itself: its CPU path
+    (CoordinateManager + RiemannConvolution over LibTorch, compiled from the
+    reference sources) with LibTorch's intra-op threads. The first forward
+    builds the kernel map; the timed fwd+dX+dW steps reuse it. Otherwise the
+    scalar C oracle on one thread. Returns the cpu_baseline record."""
     import oracle  # checker and CPU baseline only; never on the GPU path
+    from oracle import ref
 
     c1 = coords[coords[:, 0] == 0]
     K = offsets.shape[0]
+    if ref.available():
+        reps = 3
+        P, first_ms, step_ms = ref.conv_time(c1, cin, cout, ks=3, bf16=dtype == "bf16",
+                                             reps=reps, seed=seed)
+        return {
+            "value": round(len(c1) / (step_ms * 1e-3) / 1e6, 6),
+            "unit": "Mvoxels/s",
+            "cores": ref.num_threads(),
+            "kind": "reference",
+            "sample": (f"scene 0 of the workload: {len(c1)} voxels, P={P}, 3^3 C{cin}->{cout} "
+                       f"{dtype} fwd+dX+dW, mean of {reps} steps ({step_ms:.1f} ms each) with "
+                       f"the map cached; first forward incl. kernel map {first_ms:.1f} ms"),
+            "first_forward_ms": round(first_ms, 2),
+            "cpu_model": cpu_model(),
+            "nproc": os.cpu_count(),
+        }
     rng = np.random.default_rng(seed + 100)
     x = rng.standard_normal((len(c1), cin)).astype(np.float32)
     w = (rng.standard_normal((K, cin, cout)) * np.sqrt(2.0 / (cin * K))).astype(np.float32)
@@ -283,7 +305,8 @@ def main():
         "roofline": roof,
     }
     if not args.no_cpu_baseline:
-        line["cpu_baseline"] = cpu_baseline(coords_np, offsets_np, cin, cout, args.seed)
+        line["cpu_baseline"] = cpu_baseline(coords_np, offsets_np, cin, cout, args.seed,
+                                            args.dtype)
     else:
         line["cpu_baseline"] = None
     print(json.dumps(line), flush=True)

@@ -1,0 +1,217 @@
+// Test infrastructure only: C entry points over the reference's own CPU path.
+//
+// oracle/ref.mk compiles the reference sources where they lie (space.cpp,
+// stencil.cpp, conv.cpp, sparse_tensor.cpp under RiemannEngine/engine/) with
+// CPU_ONLY, plus this file, into oracle/_ref/libriemann_ref.so. The functions
+// below drive the reference's public C++ API (riemann::CoordinateManager on
+// the CPU backend, riemann::RiemannConvolution) so that tests can check the
+// oracle and the HIP path against the reference itself, and bench.py can time
+// it as the CPU baseline. Nothing on the product path loads this library.
+//
+// Every function returns a count >= 0 or -1 with ref_last_error() set.
+// Variable-size outputs are written only when they fit `cap`; call once with
+// cap = 0 to learn the size.
+#include "engine/grid/space.hpp"
+#include "engine/nn/conv.hpp"
+#include "engine/tensor/sparse_tensor.hpp"
+
+#include <torch/torch.h>
+
+#include <algorithm>
+#include <chrono>
+#include <cstring>
+#include <exception>
+#include <memory>
+#include <string>
+
+namespace {
+
+thread_local std::string g_error;
+
+template <typename F> int64_t guarded(F &&body) {
+  try {
+    return body();
+  } catch (const std::exception &e) {
+    g_error = e.what();
+    return -1;
+  }
+}
+
+torch::Tensor int_rows(const int32_t *p, int64_t n, int ncol) {
+  return torch::from_blob(const_cast<int32_t *>(p), {n, ncol}, torch::kInt32).clone();
+}
+
+torch::Tensor float_rows(const float *p, int64_t n, int64_t c) {
+  return torch::from_blob(const_cast<float *>(p), {n, c}, torch::kFloat32).clone();
+}
+
+void copy_out(const torch::Tensor &t, void *dst) {
+  auto c = t.contiguous();
+  std::memcpy(dst, c.data_ptr(), c.numel() * c.element_size());
+}
+
+riemann::RegionType::Type region_of(int region) {
+  return region == 1 ? riemann::RegionType::HYPER_CROSS : riemann::RegionType::HYPER_CUBE;
+}
+
+using CpuManager = riemann::cpu_manager_type<int32_t>;
+
+} // namespace
+
+extern "C" {
+
+const char *ref_last_error() { return g_error.c_str(); }
+
+// CoordinateManager::insert_and_map on the CPU backend (space.cpp:17-58):
+// unique rows [n_u, ncol], mapping [n_u] and inverse [n]. Returns n_u.
+int64_t ref_insert_and_map(const int32_t *coords, int64_t n, int ncol, int64_t cap,
+                           int32_t *unique, int64_t *mapping, int64_t *inverse) {
+  return guarded([&]() -> int64_t {
+    riemann::CoordinateManager m(ncol - 1, riemann::CoordinateMapBackend::CPU);
+    auto r = m.insert_and_map(int_rows(coords, n, ncol),
+                              riemann::stride_type(static_cast<size_t>(ncol - 1), 1));
+    auto u = m.get_coordinates(r.first).to(torch::kInt32);
+    const int64_t nu = u.size(0);
+    if (nu <= cap) {
+      copy_out(u, unique);
+      copy_out(r.second.first.to(torch::kInt64), mapping);
+      copy_out(r.second.second.to(torch::kInt64), inverse);
+    }
+    return nu;
+  });
+}
+
+// The kernel map a stride-`stride` convolution with a ks^D cube (region 0)
+// or cross (region 1) builds over the unique rows `coords` (tensor stride 1),
+// exactly as evaluate_sparse_convolution requests it (conv.cpp:38-42). The
+// output map is the input map (stride 1) or CoordinateManager::stride's
+// coarse map, whose rows go to out_coords. kofs [K+1]; pairs when P <= cap.
+// Returns P; *n_out and *K are set.
+int64_t ref_kernel_map(const int32_t *coords, int64_t n, int ncol, int ks, int stride, int dil,
+                       int region, int64_t cap, int64_t *kofs, int32_t *in_rows,
+                       int32_t *out_rows, int64_t out_cap, int32_t *out_coords, int64_t *n_out,
+                       int32_t *K) {
+  return guarded([&]() -> int64_t {
+    const int D = ncol - 1;
+    riemann::CoordinateManager m(D, riemann::CoordinateMapBackend::CPU);
+    auto r = m.insert_and_map(int_rows(coords, n, ncol),
+                              riemann::stride_type(static_cast<size_t>(D), 1));
+    const auto in_key = r.first;
+    const riemann::stride_type s(static_cast<size_t>(D), static_cast<uint32_t>(stride));
+    const auto out_key = stride > 1 ? m.stride(in_key, s) : in_key;
+    const auto &map = m.manager_ptr<CpuManager>()->kernel_map(
+        &in_key, &out_key, riemann::stride_type(static_cast<size_t>(D), ks), s,
+        riemann::stride_type(static_cast<size_t>(D), dil), region_of(region), at::Tensor(),
+        false, false);
+    auto oc = m.get_coordinates(out_key).to(torch::kInt32);
+    *n_out = oc.size(0);
+    if (oc.size(0) <= out_cap)
+      copy_out(oc, out_coords);
+    *K = static_cast<int32_t>(map.first.size());
+    int64_t P = 0;
+    kofs[0] = 0;
+    for (size_t k = 0; k < map.first.size(); ++k) {
+      P += static_cast<int64_t>(map.first[k].size());
+      kofs[k + 1] = P;
+    }
+    if (P <= cap) {
+      for (size_t k = 0; k < map.first.size(); ++k) {
+        for (size_t i = 0; i < map.first[k].size(); ++i) {
+          in_rows[kofs[k] + i] = static_cast<int32_t>(map.first[k][i]);
+          out_rows[kofs[k] + i] = static_cast<int32_t>(map.second[k][i]);
+        }
+      }
+    }
+    return P;
+  });
+}
+
+// RiemannConvolution(cin, cout, ks, stride, dil, bias=false, D) forward and
+// backward on the CPU, in fp32 (dtype 0) or bf16 (dtype 1) exactly as the
+// reference computes them (per-offset index_select -> matmul -> index_add_ in
+// the feature dtype, LibTorch autograd for the gradients). x [n, cin] over
+// the unique rows `coords`, w [K, cin, cout], gy [n_out, cout] in the
+// reference's output row order (may be NULL: forward only). Outputs are fp32:
+// y [n_out, cout], out_coords [n_out, ncol], gx [n, cin], gw [K, cin, cout];
+// y/out_coords/gx/gw are written when n_out <= out_cap. Returns n_out.
+int64_t ref_conv(const int32_t *coords, int64_t n, int ncol, const float *x, int cin,
+                 const float *w, int K, int cout, int ks, int stride, int dil, int dtype,
+                 const float *gy, int64_t out_cap, float *y, int32_t *out_coords, float *gx,
+                 float *gw) {
+  return guarded([&]() -> int64_t {
+    const int D = ncol - 1;
+    const auto dt = dtype == 1 ? torch::kBFloat16 : torch::kFloat32;
+    auto mgr = std::make_shared<riemann::CoordinateManager>(D, riemann::CoordinateMapBackend::CPU);
+    auto X = float_rows(x, n, cin).to(dt).detach().requires_grad_(true);
+    riemann::SparseTensor input(X, int_rows(coords, n, ncol), mgr);
+    riemann::RiemannConvolution conv(cin, cout, ks, stride, dil, false, false,
+                                     riemann::ConvolutionMode::DEFAULT, D);
+    auto &kernel = conv->base()->kernel_;
+    TORCH_CHECK(kernel.size(0) == K, "kernel volume ", kernel.size(0), " != ", K);
+    kernel.set_data(torch::from_blob(const_cast<float *>(w), {K, cin, cout}, torch::kFloat32)
+                        .to(dt)
+                        .clone());
+    auto out = conv->forward(input);
+    const int64_t n_out = out.F().size(0);
+    if (n_out > out_cap)
+      return n_out;
+    copy_out(out.F().detach().to(torch::kFloat32), y);
+    copy_out(mgr->get_coordinates(out.coordinate_map_key()).to(torch::kInt32), out_coords);
+    if (gy != nullptr) {
+      out.F().backward(float_rows(gy, n_out, cout).to(dt));
+      copy_out(X.grad().to(torch::kFloat32), gx);
+      copy_out(kernel.grad().to(torch::kFloat32), gw);
+    }
+    return n_out;
+  });
+}
+
+// Times the reference on the CPU: one RiemannConvolution forward (which
+// builds and caches the kernel map) into *map_ms, then `reps` forward +
+// backward steps reusing the cached map, their mean into *step_ms. Random
+// operands from `seed`. Returns the pair count of the map.
+int64_t ref_conv_time(const int32_t *coords, int64_t n, int ncol, int cin, int cout, int ks,
+                      int dtype, int reps, int seed, double *map_ms, double *step_ms) {
+  return guarded([&]() -> int64_t {
+    const int D = ncol - 1;
+    const auto dt = dtype == 1 ? torch::kBFloat16 : torch::kFloat32;
+    torch::manual_seed(seed);
+    auto mgr = std::make_shared<riemann::CoordinateManager>(D, riemann::CoordinateMapBackend::CPU);
+    auto X = torch::randn({n, cin}).to(dt).detach().requires_grad_(true);
+    riemann::SparseTensor input(X, int_rows(coords, n, ncol), mgr);
+    riemann::RiemannConvolution conv(cin, cout, ks, 1, 1, false, false,
+                                     riemann::ConvolutionMode::DEFAULT, D);
+    auto &kernel = conv->base()->kernel_;
+    kernel.set_data(kernel.detach().to(dt).clone());
+    using clock = std::chrono::steady_clock;
+    auto t0 = clock::now();
+    auto out = conv->forward(input);
+    *map_ms = std::chrono::duration<double, std::milli>(clock::now() - t0).count();
+    auto gy = torch::randn_like(out.F());
+    double total = 0.0;
+    for (int r = 0; r < reps; ++r) {
+      X.mutable_grad() = torch::Tensor();
+      kernel.mutable_grad() = torch::Tensor();
+      auto t1 = clock::now();
+      auto o = conv->forward(input);
+      o.F().backward(gy);
+      total += std::chrono::duration<double, std::milli>(clock::now() - t1).count();
+    }
+    *step_ms = total / std::max(reps, 1);
+    int64_t P = 0;
+    const auto key = input.coordinate_map_key();
+    const auto &map = mgr->manager_ptr<CpuManager>()->kernel_map(
+        &key, &key, riemann::stride_type(static_cast<size_t>(D), ks),
+        riemann::stride_type(static_cast<size_t>(D), 1),
+        riemann::stride_type(static_cast<size_t>(D), 1), riemann::RegionType::HYPER_CUBE,
+        at::Tensor(), false, false);
+    for (const auto &v : map.first)
+      P += static_cast<int64_t>(v.size());
+    return P;
+  });
+}
+
+// Threads LibTorch's CPU kernels use (the cores a baseline timing uses).
+int ref_num_threads() { return at::get_num_threads(); }
+
+} // extern "C"
