@@ -47,8 +47,12 @@ def parse_args():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--dtype", choices=["f32", "bf16"], default="f32",
-                    help="feature/weight dtype of the headline line (fp32 accumulate)")
+    ap.add_argument("--dtype", choices=["f32", "bf16"], default=None,
+                    help="feature/weight dtype (fp32 accumulate); default: the config's own "
+                         "(f32 for configs 1, 2, 4; bf16 for 3, 5)")
+    ap.add_argument("--config", type=int, choices=[1, 2, 3, 4, 5], default=2,
+                    help="benchmark configuration; 2 (the default) is the headline line, the "
+                         "others print a line of their own for the record")
     ap.add_argument("--seed", type=int, default=2)
     ap.add_argument("--no-cpu-baseline", action="store_true",
                     help="skip the CPU oracle timing (profiling runs)")
@@ -173,6 +177,186 @@ def cpu_baseline(coords, offsets, cin, cout, seed, dtype):
     }
 
 
+
+# ------------------------------------------------------- other configs
+
+def _timed_passes(passes, steps, warmup):
+    """Run the named passes in order `warmup` times, then `steps` times with
+    HIP events between passes (torch's current stream, where the C ABI and
+    the host layer launch). Returns (mean ms per pass, wall ms per step)."""
+    import torch
+    for _ in range(warmup):
+        for _, fn in passes:
+            fn()
+    torch.cuda.synchronize()
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(len(passes) + 1)]
+          for _ in range(steps)]
+    t0 = time.perf_counter()
+    for i in range(steps):
+        ev[i][0].record()
+        for j, (_, fn) in enumerate(passes):
+            fn()
+            ev[i][j + 1].record()
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) * 1e3 / steps
+    per = {name: statistics.mean(e[j].elapsed_time(e[j + 1]) for e in ev)
+           for j, (name, _) in enumerate(passes)}
+    return per, wall
+
+
+def _map_time(build, reps):
+    """Host-clock median of `build()` (hash + map calls read sizes back)."""
+    import torch
+    out, ms = None, []
+    for _ in range(reps + 1):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        out = build()
+        torch.cuda.synchronize()
+        ms.append((time.perf_counter() - t0) * 1e3)
+    return out, statistics.median(ms[1:])
+
+
+def run_other_config(args):
+    """Configs 1, 3, 4 and 5 of the benchmark set, one JSON record each:
+      1  sphere shell (N = 51,554), 3^3 C16->32, fwd+dX+dW (C ABI)
+      3  LiDAR batch 2: 2^3 stride-2 conv C64->128, then the 2^3 transposed
+         conv C128->64 back onto the input coordinates, fwd+bwd (C ABI)
+      4  4-D moving shell (N = 232,528), 3^4 (81 offsets) C32->32 (C ABI)
+      5  residual encoder on 8 indoor scenes: 4 stages of 2 BasicBlocks and a
+         2^3 stride-2 conv, channels 32->64->128->256, fwd+bwd through the
+         C++ host layer (autograd, batch norm, maps cached by the manager)
+    value = N_in / ms_per_step (Mvoxels/s) with the maps prebuilt."""
+    import torch
+    from riemannengine_amd import abi, scenes, stencil
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU (the HIP path has no CPU fallback)", file=sys.stderr)
+        sys.exit(1)
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    dt = torch.float32 if args.dtype == "f32" else torch.bfloat16
+    s = 4 if args.dtype == "f32" else 2
+    g = torch.Generator(device="cpu").manual_seed(args.seed)
+    rnd = lambda *shape: torch.randn(shape, generator=g).to(dev, dt)
+    kaiming = lambda K, ci, co: rnd(K, ci, co) * (2.0 / (ci * K)) ** 0.5
+    cfg = args.config
+    extra = {}
+    flop = byts = 0.0
+
+    if cfg in (1, 4):
+        if cfg == 1:
+            c_np, D, cin, cout = scenes.sphere_shell(), 3, 16, 32
+            desc = "config 1: sphere shell r=64, 3^3 stride-1 conv C16->32, fwd+dX+dW"
+        else:
+            c_np, D, cin, cout = scenes.moving_shell_4d(), 4, 32, 32
+            desc = "config 4: 4-D shell, 8 frames, 3^4 (81 offsets) stride-1 conv C32->32, fwd+dX+dW"
+        coords = torch.from_numpy(c_np).to(dev)
+        off = stencil.region_offsets(D, 3)
+        K = off.shape[0]
+        (table, km), map_ms = _map_time(
+            lambda: (lambda t: (t, abi.kernel_map(t, t, off)))(abi.hash_build(coords)),
+            args.map_reps)
+        n_in = km.n_in
+        x, w, gy = rnd(n_in, cin), kaiming(K, cin, cout), rnd(n_in, cout)
+        passes = [("forward", lambda: abi.conv_forward(x, w, km)),
+                  ("backward_input", lambda: abi.conv_backward_input(gy, w, km)),
+                  ("backward_weight", lambda: abi.conv_backward_weight(x, gy, km, K))]
+        for F, B in conv_traffic(n_in, n_in, km.n_pairs, K, cin, cout, s).values():
+            flop, byts = flop + F, byts + B
+        extra = {"n_voxels": n_in, "pairs": km.n_pairs, "offsets": K, "c_in": cin, "c_out": cout}
+    elif cfg == 3:
+        c_np = scenes.lidar_batch(2, 3)
+        coords = torch.from_numpy(c_np).to(dev)
+        off = stencil.region_offsets(3, 2)
+
+        def build():
+            tf = abi.hash_build(coords)
+            tc = abi.hash_build(abi.stride_coords(coords, [2, 2, 2]))
+            return tf, tc, abi.kernel_map(tf, tc, off)
+        (tf, tc, down), map_ms = _map_time(build, args.map_reps)
+        up = down.swapped()
+        n_f, n_c, P = down.n_in, down.n_out, down.n_pairs
+        x, wd, wu = rnd(n_f, 64), kaiming(8, 64, 128), kaiming(8, 128, 64)
+        y = abi.conv_forward(x, wd, down)
+        gz = rnd(n_f, 64)
+        gy = abi.conv_backward_input(gz, wu, up)
+        passes = [("down_forward", lambda: abi.conv_forward(x, wd, down)),
+                  ("up_forward", lambda: abi.conv_forward(y, wu, up)),
+                  ("up_backward_input", lambda: abi.conv_backward_input(gz, wu, up)),
+                  ("up_backward_weight", lambda: abi.conv_backward_weight(y, gz, up, 8)),
+                  ("down_backward_input", lambda: abi.conv_backward_input(gy, wd, down)),
+                  ("down_backward_weight", lambda: abi.conv_backward_weight(x, gy, down, 8))]
+        for (ni, no, ci, co) in ((n_f, n_c, 64, 128), (n_c, n_f, 128, 64)):
+            for F, B in conv_traffic(ni, no, P, 8, ci, co, s).values():
+                flop, byts = flop + F, byts + B
+        n_in = n_f
+        desc = ("config 3: LiDAR batch 2, 2^3 stride-2 conv C64->128 then 2^3 transposed conv "
+                "C128->64 onto the input coordinates, fwd+bwd")
+        extra = {"n_voxels": n_f, "n_coarse": n_c, "pairs": P, "c": [64, 128, 64]}
+    else:  # config 5
+        import riemannengine_amd as re_
+        c_np = scenes.indoor_batch(8, args.seed)
+        coords = torch.from_numpy(c_np).to(dev)
+        chans = [32, 64, 128, 256]
+        mods = []
+        for i, c in enumerate(chans):
+            mods += [re_.nn.BasicBlock(c, c), re_.nn.BasicBlock(c, c),
+                     re_.nn.RiemannConvolution(c, chans[min(i + 1, 3)], kernel_size=2, stride=2,
+                                               dimension=3)]
+        for m in mods:
+            m.to(dev)
+            m.to_dtype(dt)
+        feats = rnd(len(c_np), 32)
+        x0 = re_.SparseTensor(feats, coords)
+        n_in = len(x0)
+        state = {}
+
+        def forward():
+            h = x0
+            for m in mods:
+                h = m(h)
+            state["out"] = h
+
+        def backward():
+            state["out"].F.float().sum().backward()
+            for m in mods:
+                m.zero_grad()
+
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        forward()  # builds every stage's maps; the manager caches them
+        torch.cuda.synchronize()
+        first_ms = (time.perf_counter() - t0) * 1e3
+        backward()
+        passes = [("forward", forward), ("backward", backward)]
+        map_ms = None
+        desc = ("config 5: residual encoder on 8 indoor scenes, 4 stages x (2 BasicBlocks + "
+                "2^3 stride-2 conv), C 32->64->128->256, fwd+bwd through the host layer")
+        extra = {"n_voxels": n_in, "out_voxels": len(state["out"]), "stages": 4,
+                 "channels": chans, "first_forward_ms_incl_maps": round(first_ms, 2)}
+
+    per, wall = _timed_passes(passes, args.steps, args.warmup)
+    step_ms = sum(per.values())
+    line = {
+        "metric": f"sparse conv fwd+bwd Mvoxels/s (config {cfg})",
+        "value": round(n_in / (wall * 1e-3) / 1e6, 3),
+        "unit": "Mvoxels/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(wall, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": args.dtype,
+        "data": "synthetic (seeded scenes; random N(0,1) features, Kaiming-normal weights)",
+        "config": dict({"workload": desc, "seed": args.seed, "accumulate": "f32"}, **extra),
+        "kernel_map_ms": None if map_ms is None else round(map_ms, 3),
+        "breakdown_ms": {k: round(v, 4) for k, v in per.items()},
+    }
+    if flop:
+        t_roof = max(flop / (PEAK_TFLOPS[args.dtype] * 1e12), byts / (PEAK_HBM_GBS * 1e9))
+        line["step_roofline"] = {"t_roof_ms": round(t_roof * 1e3, 4),
+                                 "frac": round(t_roof * 1e3 / step_ms, 4),
+                                 "flop": flop, "bytes": byts}
+    return line
+
+
 def main():
     args = parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -184,6 +368,11 @@ def main():
 
     if args.copy_mib > 0:
         copy_calibration(args.copy_mib)
+        return
+    if args.dtype is None:
+        args.dtype = "bf16" if args.config in (3, 5) else "f32"
+    if args.config != 2:
+        print(json.dumps(run_other_config(args)), flush=True)
         return
 
     import torch

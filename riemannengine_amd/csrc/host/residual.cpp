@@ -21,6 +21,12 @@ RiemannBatchNormImpl::RiemannBatchNormImpl(int64_t num_features, double eps, dou
 
 void RiemannBatchNormImpl::reset() { normalization_->reset(); }
 
+void RiemannBatchNormImpl::to(torch::Dtype, bool) {}
+
+void RiemannBatchNormImpl::to(torch::Device device, torch::Dtype, bool non_blocking) {
+  torch::nn::Module::to(device, non_blocking);
+}
+
 SparseTensor RiemannBatchNormImpl::forward(const SparseTensor &input) {
   const auto &x = input.F();
   // batch statistics in fp32 for bf16 features, result in the feature dtype

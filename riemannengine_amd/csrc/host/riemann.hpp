@@ -387,6 +387,12 @@ public:
                        bool affine = true, bool track_running_stats = true);
   void reset() override;
   SparseTensor forward(const SparseTensor &input);
+  // The affine parameters and running statistics stay fp32 under a dtype
+  // cast of the model: bf16 features are normalised in fp32 (the usual
+  // mixed-precision rule for normalisation layers). Device moves apply.
+  using torch::nn::Module::to;
+  void to(torch::Dtype dtype, bool non_blocking = false) override;
+  void to(torch::Device device, torch::Dtype dtype, bool non_blocking = false) override;
 
 private:
   int64_t num_features_;

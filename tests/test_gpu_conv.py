@@ -187,3 +187,59 @@ def test_repeat_calls_are_bitwise_deterministic(dtype):
     assert torch.equal(abi.conv_backward_input(gy, w, km), abi.conv_backward_input(gy, w, km))
     assert torch.equal(abi.conv_backward_weight(x, gy, km, 27),
                        abi.conv_backward_weight(x, gy, km, 27))
+
+
+def test_config3_lidar_down_up_full_size():
+    """Config 3 at full size in bf16: 2^3 stride-2 conv C64->128 over the
+    LiDAR batch, then the 2^3 transposed conv C128->64 back onto the input
+    coordinates (the swapped map), forward and backward, against the plain
+    PyTorch fp32 gather-matmul-scatter on the same bf16 operands."""
+    c = scenes.lidar_batch(2, 3)
+    tin = abi.hash_build(to_dev(c))
+    tout = abi.hash_build(abi.stride_coords(to_dev(c), [2, 2, 2]))
+    down = abi.kernel_map(tin, tout, oracle.region_offsets(3, 2))
+    up = down.swapped()
+    assert down.n_pairs == down.n_in  # every fine voxel has exactly one parent
+    g = torch.Generator(device="cpu").manual_seed(3)
+    dt = torch.bfloat16
+    x = torch.randn((down.n_in, 64), generator=g).to(DEV, dt)
+    wd = (torch.randn((8, 64, 128), generator=g) * (2.0 / 512) ** 0.5).to(DEV, dt)
+    wu = (torch.randn((8, 128, 64), generator=g) * (2.0 / 1024) ** 0.5).to(DEV, dt)
+    gz = torch.randn((down.n_in, 64), generator=g).to(DEV, dt)
+    print(f"config 3: fine {down.n_in} coarse {down.n_out}", flush=True)
+    y = abi.conv_forward(x, wd, down)
+    z = abi.conv_forward(y, wu, up)
+    gy = abi.conv_backward_input(gz, wu, up)
+    gwu = abi.conv_backward_weight(y, gz, up, 8)
+    gx = abi.conv_backward_input(gy, wd, down)
+    gwd = abi.conv_backward_weight(x, gy, down, 8)
+    tol = TOL[dt]
+    ry, _, _ = _torch_gather_gemm_scatter(down, x, wd, torch.zeros_like(y))
+    assert_rel(y.float().cpu().numpy(), ry.cpu().numpy(), tol, "down Y")
+    rz, rgy, rgwu = _torch_gather_gemm_scatter(up, y, wu, gz)
+    assert_rel(z.float().cpu().numpy(), rz.cpu().numpy(), tol, "up Y")
+    assert_rel(gy.float().cpu().numpy(), rgy.cpu().numpy(), tol, "up dX")
+    assert_rel(gwu.float().cpu().numpy(), rgwu.cpu().numpy(), tol, "up dW")
+    _, rgx, rgwd = _torch_gather_gemm_scatter(down, x, wd, gy)
+    assert_rel(gx.float().cpu().numpy(), rgx.cpu().numpy(), tol, "down dX")
+    assert_rel(gwd.float().cpu().numpy(), rgwd.cpu().numpy(), tol, "down dW")
+
+
+def test_config4_4d_full_size():
+    """Config 4 at full size: the 8-frame 4-D shell (232,528 voxels), 3^4
+    (81 offsets) C32->32 fp32, forward and backward, against the plain
+    PyTorch fp32 gather-matmul-scatter."""
+    c = scenes.moving_shell_4d()
+    _, _, km = gpu_tables_and_map(c, c, oracle.region_offsets(4, 3), same=True)
+    assert km.n_in == 232528 and km.symmetric
+    g = torch.Generator(device="cpu").manual_seed(4)
+    x = torch.randn((km.n_in, 32), generator=g).to(DEV)
+    w = (torch.randn((81, 32, 32), generator=g) * (2.0 / (32 * 81)) ** 0.5).to(DEV)
+    gy = torch.randn((km.n_out, 32), generator=g).to(DEV)
+    y = abi.conv_forward(x, w, km)
+    gx = abi.conv_backward_input(gy, w, km)
+    gw = abi.conv_backward_weight(x, gy, km, 81)
+    ry, rgx, rgw = _torch_gather_gemm_scatter(km, x, w, gy)
+    assert_rel(y.cpu().numpy(), ry.cpu().numpy(), 1e-4, "Y")
+    assert_rel(gx.cpu().numpy(), rgx.cpu().numpy(), 1e-4, "dX")
+    assert_rel(gw.cpu().numpy(), rgw.cpu().numpy(), 1e-4, "dW")
