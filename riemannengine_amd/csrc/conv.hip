@@ -10,8 +10,8 @@
 //  * Forward and dX are one output-stationary implicit GEMM over the dense
 //    neighbour table of the kernel map, whose rows come grouped by neighbour
 //    mask (so a 16-row group rarely multiplies a missing neighbour). A
-//    256-thread workgroup owns 128 output rows (4 waves x 2 groups of 16) and
-//    up to 64 columns. It walks only the offsets with a neighbour in its rows;
+//    256-thread workgroup owns 64 output rows (4 waves x one group of 16)
+//    and up to 64 columns. It walks only the offsets with a neighbour in its rows;
 //    for each it stages the weight slice in LDS with 16-byte copies from a
 //    [K][ncols][cred] copy of the weights (reduction axis contiguous), gathers
 //    each group's 16 neighbour rows straight into MFMA A-fragments (16-byte
@@ -105,8 +105,8 @@ inline int64_t xcd_grid(int64_t tiles) {
 // wt is [K][ncols][cred] (reduction axis contiguous). A workgroup owns
 // 4 * RG * 16 output rows and NT columns; RG: 16-row groups per wave; CSUB:
 // 16-byte lane loads per staged channel chunk (chunk = CSUB * kCh channels).
-template <typename T, int NT, int RG, int CSUB>
-__global__ __launch_bounds__(kThreads) void conv_os_kernel(
+template <typename T, int NT, int RG, int CSUB, int WAVES = 1>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(WAVES))) void conv_os_kernel(
     const T *__restrict__ x, int cred, const T *__restrict__ wt, int ncols,
     const float *__restrict__ bias, const int32_t *__restrict__ nbr,
     int64_t n_rows, int K, const int32_t *__restrict__ order,
@@ -213,7 +213,7 @@ __global__ __launch_bounds__(kThreads) void conv_os_kernel(
     }
     __syncthreads(); // chunk staged
     if (wave_act) {
-      Frag a[RG][CSUB];
+        Frag a[RG][CSUB];
 #pragma unroll
       for (int r = 0; r < RG; ++r)
 #pragma unroll
@@ -221,6 +221,11 @@ __global__ __launch_bounds__(kThreads) void conv_os_kernel(
           a[r][sub] = idx[r] >= 0 ? M::load(x + static_cast<int64_t>(idx[r]) * cred + cc0 +
                                             sub * CH + g * EPL)
                                   : M::zero();
+      // per group: a uniform branch on its activity (fp32 MFMA time is the
+      // bound, so inactive groups are skipped); the 4 k-steps of a 16-byte
+      // fp32 fragment accumulate back to back. Interleaving the MFMAs over
+      // the accumulators measured slower: it costs occupancy, and the
+      // stalls here are the gathers', not the MFMA chain's.
 #pragma unroll
       for (int sub = 0; sub < CSUB; ++sub) {
 #pragma unroll
@@ -603,26 +608,40 @@ static bool aligned16(const void *p) {
 
 template <typename T> constexpr int kChOf = Mfma<T>::kCh;
 
-template <typename T, int NT, int RG, int CSUB>
+template <typename T, int NT, int RG, int CSUB, int WAVES>
 static void launch_os(const T *x, int cred, const T *wt, int ncols,
                       const float *bias, const int32_t *nbr, int64_t n_rows,
                       int K, const int32_t *order, T *y, hipStream_t s) {
   constexpr int ROWS = kWaves * RG * 16;
   dim3 grid(static_cast<unsigned>(xcd_grid(ceil_div(n_rows, ROWS))), ncols / NT);
-  hipLaunchKernelGGL((conv_os_kernel<T, NT, RG, CSUB>), grid, dim3(kThreads), 0, s, x,
+  hipLaunchKernelGGL((conv_os_kernel<T, NT, RG, CSUB, WAVES>), grid, dim3(kThreads), 0, s, x,
                      cred, wt, ncols, bias, nbr, n_rows, K, order, y);
 }
+
+// Launch shape, measured on MI355X (config 2, C64): one 16-row group per
+// wave (64 rows per workgroup: more workgroups in flight hide the gather
+// latency better than more rows per wave), the widest channel chunk the
+// reduction width allows, and a register budget for 7 (fp32) or 8 (bf16)
+// waves per SIMD.
+template <typename T> constexpr int kOsWaves = std::is_same<T, float>::value ? 6 : 8;
 
 template <typename T, int NT>
 static void pick_csub(const T *x, int cred, const T *wt, int ncols,
                       const float *bias, const int32_t *nbr, int64_t n_rows,
                       int K, const int32_t *order, T *y, hipStream_t s) {
   constexpr int CH = kChOf<T>;
-  constexpr int RG = 2;
+  constexpr int RG = 1;
+  constexpr int W = kOsWaves<T>;
+  if constexpr (std::is_same<T, float>::value) {
+    if (cred % (4 * CH) == 0) {
+      launch_os<T, NT, RG, 4, W>(x, cred, wt, ncols, bias, nbr, n_rows, K, order, y, s);
+      return;
+    }
+  }
   if (cred % (2 * CH) == 0)
-    launch_os<T, NT, RG, 2>(x, cred, wt, ncols, bias, nbr, n_rows, K, order, y, s);
+    launch_os<T, NT, RG, 2, W>(x, cred, wt, ncols, bias, nbr, n_rows, K, order, y, s);
   else
-    launch_os<T, NT, RG, 1>(x, cred, wt, ncols, bias, nbr, n_rows, K, order, y, s);
+    launch_os<T, NT, RG, 1, W>(x, cred, wt, ncols, bias, nbr, n_rows, K, order, y, s);
 }
 
 // y[order[j]] = sum_k x[nbr[k][j]] @ W'[k] with W'[k][c][n] = wt[k][n][c].
