@@ -344,8 +344,8 @@ __device__ __forceinline__ v4s ds_read_tr16(const void *p) {
       reinterpret_cast<lds_v4s *>(static_cast<uint32_t>(reinterpret_cast<uintptr_t>(p))));
 }
 
-template <typename T, int VA, int VB, bool DB>
-__global__ __launch_bounds__(kThreads) void conv_dw_kernel(
+template <typename T, int VA, int VB, bool DB, int WAVES = 1>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(WAVES))) void conv_dw_kernel(
     const T *__restrict__ x, int cin, const T *__restrict__ gy, int cout,
     const int64_t *__restrict__ kofs, const int32_t *__restrict__ in_rows,
     const int32_t *__restrict__ out_rows, int64_t ppb, float *__restrict__ partial) {
@@ -435,7 +435,8 @@ __global__ __launch_bounds__(kThreads) void conv_dw_kernel(
 
   // wave -> one 16-channel block nb of dY and every PG-th step of the chunk
   constexpr int PG = kWaves / VB; // waves sharing a dY block split the steps
-  const int nb = wv % VB, ps = wv / VB;
+  const int nb = wv % VB;
+  const int ps = PG == 1 ? 0 : wv / VB; // 0 at compile time when a wave owns its block
   v4f acc[VA];
 #pragma unroll
   for (int ea = 0; ea < VA; ++ea)
@@ -456,7 +457,7 @@ __global__ __launch_bounds__(kThreads) void conv_dw_kernel(
     const T *bg = sG[buf];
     if constexpr (F32) {
       // step s covers pairs 4s..4s+3, one per 16-lane group
-#pragma unroll 4
+#pragma unroll
       for (int s = ps; s < CP / 4; s += PG) {
         const float *ra = reinterpret_cast<const float *>(bx) + (4 * s + g) * LDX + VA * i16;
         const float b = reinterpret_cast<const float *>(bg)[(4 * s + g) * LDG + 16 * nb + i16];
@@ -478,7 +479,7 @@ __global__ __launch_bounds__(kThreads) void conv_dw_kernel(
     } else {
       // step s covers pairs 32s..32s+31; group g takes 8g..8g+7 of them and
       // lane i16 points at pair 8g + 4h + i16/4, channels 16*blk + 4*(i16%4)
-#pragma unroll 2
+#pragma unroll
       for (int s = ps; s < CP / 32; s += PG) {
         const int prow = 32 * s + 8 * g + i16 / 4;
         const int pcol = 4 * (i16 % 4);
@@ -705,12 +706,17 @@ static DwPlan dw_plan(int32_t dtype, int cin, int cout, int64_t n_pairs, int64_t
   return p;
 }
 
+// Register budget of the dW kernel (measured on MI355X, config 2): 4 waves
+// per SIMD for fp32; bf16 gains nothing from a tighter budget.
+template <typename T> constexpr int kDwWaves = std::is_same<T, float>::value ? 3 : 1;
+
 template <typename T, int VA, int VB, bool DB = false>
 static void launch_dw(const T *x, int cin, const T *gy, int cout, const int64_t *kofs, int K,
                       const int32_t *in_rows, const int32_t *out_rows, const DwPlan &p,
                       float *partial, hipStream_t s) {
   dim3 grid(static_cast<unsigned>(p.chunks), K, p.tiles);
-  hipLaunchKernelGGL((conv_dw_kernel<T, VA, VB, DB>), grid, dim3(kThreads), 0, s, x, cin, gy,
+  hipLaunchKernelGGL((conv_dw_kernel<T, VA, VB, DB, kDwWaves<T>>), grid, dim3(kThreads), 0, s, x,
+                     cin, gy,
                      cout, kofs, in_rows, out_rows, p.ppb, partial);
 }
 
