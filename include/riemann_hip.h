@@ -106,9 +106,11 @@ int rhip_hash_lookup(const rhip_table *table, const int32_t *queries,
 
 /*
  * Locality order of a table's unique rows: order[j] is the row processed at
- * position j (rows sorted by packed key, i.e. batch then x, y, z), pos is its
- * inverse. Identity in RHIP_KEY_ROWREF mode. Used to tile output rows so a
- * tile's neighbours cluster; it does not renumber rows.
+ * position j, pos is its inverse. Rows are sorted by batch, then by the
+ * Morton (bit-interleaved) code of their spatial columns when that fits in
+ * 63 bits, else by the packed key (x, then y, then z); identity in
+ * RHIP_KEY_ROWREF mode. Used to order output rows so that neighbouring
+ * positions have neighbouring rows; it does not renumber rows.
  */
 int rhip_order_workspace_bytes(int64_t n, size_t *bytes);
 int rhip_spatial_order(const rhip_table *table, int32_t *order, int32_t *pos,
@@ -134,10 +136,10 @@ int rhip_kmap_workspace_bytes(int64_t n_in, int64_t n_out, int32_t K,
                               size_t *bytes);
 
 /* Set by rhip_kmap_count for a map of a coordinate set onto itself (out_coords
- * are in_table's own rows, in order) with a point-symmetric stencil (offset
- * K-1-k == -offset k): only half the offsets are probed and the transposed
- * table is the forward table with offsets reversed. Pass it to
- * rhip_kmap_fill. */
+ * are in_table's own rows, in order) whose stencil offsets are distinct and
+ * closed under negation: one offset of each +/- pair is probed and the
+ * transposed table is the forward table with each offset's negation. Pass
+ * it to rhip_kmap_fill. */
 #define RHIP_KMAP_SYMMETRIC 1
 
 /*

@@ -222,8 +222,12 @@ __global__ __launch_bounds__(kBlock) void lookup_kernel(TableView t,
   result[i] = table_find(t, c);
 }
 
-__global__ __launch_bounds__(kBlock) void pack_keys_kernel(TableView t,
-                                                           int64_t n,
+// Sort keys of the locality order. morton_bits > 0: batch offset in the top
+// bits, then the spatial offsets (from the column minima) bit-interleaved,
+// morton_bits bits each (bit i of column c at i * D + (D - c)); else the
+// packed key.
+__global__ __launch_bounds__(kBlock) void pack_keys_kernel(TableView t, int64_t n,
+                                                           int morton_bits,
                                                            uint64_t *keys,
                                                            int32_t *rows) {
   int64_t i = blockIdx.x * (int64_t)kBlock + threadIdx.x;
@@ -234,7 +238,18 @@ __global__ __launch_bounds__(kBlock) void pack_keys_kernel(TableView t,
   for (int j = 0; j < RHIP_MAX_COLS; ++j)
     c[j] = j < t.ncol ? t.rows[i * t.ncol + j] : 0;
   uint64_t key = 0;
-  pack_row(t, c, key);
+  if (morton_bits > 0) {
+    const int D = t.ncol - 1;
+    for (int b = 0; b < morton_bits; ++b)
+      for (int j = 1; j <= D; ++j) {
+        const uint32_t v = static_cast<uint32_t>(c[j]) - static_cast<uint32_t>(t.lo[j]);
+        key |= static_cast<uint64_t>((v >> b) & 1u) << (b * D + (D - j));
+      }
+    key |= static_cast<uint64_t>(static_cast<uint32_t>(c[0]) - static_cast<uint32_t>(t.lo[0]))
+           << (morton_bits * D);
+  } else {
+    pack_row(t, c, key);
+  }
   keys[i] = key;
   rows[i] = static_cast<int32_t>(i);
 }
@@ -477,11 +492,22 @@ extern "C" int rhip_spatial_order(const rhip_table *table, int32_t *order,
     int32_t *rows_in = cv.take<int32_t>(n);
     const size_t temp = sort_pairs_u64_bytes(n);
     void *tmp = cv.take<char>(temp);
+    // Morton order within a batch when it fits: batch bits + D * the widest
+    // spatial column
+    const int D = table->ncol - 1;
+    int wide = 0;
+    for (int c = 1; c <= D; ++c)
+      wide = std::max(wide, bit_width_u32(static_cast<uint32_t>(
+                                static_cast<int64_t>(table->hi[c]) - table->lo[c])));
+    const int batch_bits =
+        bit_width_u32(static_cast<uint32_t>(static_cast<int64_t>(table->hi[0]) - table->lo[0]));
+    const int morton_total = batch_bits + D * wide;
+    const bool morton = D >= 1 && wide > 0 && morton_total <= 63;
     hipLaunchKernelGGL(pack_keys_kernel, dim3(nb), dim3(kBlock), 0, stream,
-                       make_view(*table), n, keys_in, rows_in);
+                       make_view(*table), n, morton ? wide : 0, keys_in, rows_in);
     RHIP_LAUNCH_CHECK();
-    sort_pairs_u64(tmp, temp, keys_in, keys_out, rows_in, order, n, table->key_bits,
-                   stream);
+    sort_pairs_u64(tmp, temp, keys_in, keys_out, rows_in, order, n,
+                   morton ? morton_total : table->key_bits, stream);
     if (pos) {
       hipLaunchKernelGGL(invert_perm_kernel, dim3(nb), dim3(kBlock), 0, stream,
                          n, order, pos);

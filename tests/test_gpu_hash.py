@@ -65,7 +65,7 @@ def test_lookup_present_absent_and_out_of_range():
     np.testing.assert_array_equal(got, exp)
 
 
-def test_spatial_order_is_sorted_permutation():
+def test_spatial_order_is_morton_permutation():
     rng = np.random.default_rng(2)
     c = random_coords(rng, 40000, 3, 50, batch=3)
     t = abi.hash_build(to_dev(c))
@@ -73,9 +73,17 @@ def test_spatial_order_is_sorted_permutation():
     pos = t.pos.cpu().numpy()
     np.testing.assert_array_equal(np.sort(order), np.arange(t.n))
     np.testing.assert_array_equal(pos[order], np.arange(t.n))
-    rows = t.ucoords.cpu().numpy()[order]
-    keys = np.lexsort(rows.T[::-1])
-    np.testing.assert_array_equal(keys, np.arange(t.n))
+    # batch first, then the Morton code of the spatial offsets from the
+    # column minima (bit b of column j at b * D + (D - j)), stable
+    rows = t.ucoords.cpu().numpy().astype(np.int64)
+    D = rows.shape[1] - 1
+    rel = rows - rows.min(axis=0)
+    wide = int(max(int(rel[:, j].max()).bit_length() for j in range(1, D + 1)))
+    key = rel[:, 0] << (wide * D)
+    for b in range(wide):
+        for j in range(1, D + 1):
+            key |= ((rel[:, j] >> b) & 1) << (b * D + (D - j))
+    np.testing.assert_array_equal(order, np.argsort(key, kind="stable"))
 
 
 @pytest.mark.parametrize("cfg", ["sphere", "indoor", "lidar", "shell4d"])
