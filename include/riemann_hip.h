@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define RHIP_ABI_VERSION 4
+#define RHIP_ABI_VERSION 5
 #define RHIP_MAX_COLS 8 /* batch column + up to 7 spatial axes */
 
 typedef enum rhip_status {
@@ -126,6 +126,22 @@ int rhip_spatial_order(const rhip_table *table, int32_t *order, int32_t *pos,
  */
 int rhip_stride_coords(const int32_t *coords, int64_t n, int32_t ncol,
                        const int32_t *out_tensor_stride, int32_t *out,
+                       hipStream_t stream);
+
+/*
+ * Generative expansion of a coordinate set through a kernel region:
+ * out[i*K + k] = coords[i] + offsets[k] (batch column kept) for every input
+ * row i and offset k. offsets is a DEVICE array [K, ncol-1] of scaled lattice
+ * offsets: the region at the OUTPUT tensor stride. Feed out ([n*K, ncol]) to
+ * rhip_hash_build; its unique rows (first occurrence in (i, k) order) are the
+ * generated output map of a generative transposed convolution.
+ * Replaces the transposed branch of CoordinateMapCPU::stride_region
+ * (engine/grid/lattice_cpu.hpp:499-534) and kernel_region_insert
+ * (engine/grid/lattice_gpu.cu:426-601); called through
+ * CoordinateMapManager::stride_region (engine/grid/space_impl.hpp:352-381).
+ */
+int rhip_expand_coords(const int32_t *coords, int64_t n, int32_t ncol,
+                       const int32_t *offsets, int32_t K, int32_t *out,
                        hipStream_t stream);
 
 /* ------------------------------------------------------------ kernel map */

@@ -40,6 +40,8 @@ def lib():
         L.oracle_kernel_map.argtypes = [vp, i64, vp, i64, i32, vp, i32, vp, vp, vp]
         L.oracle_stride.restype = i64
         L.oracle_stride.argtypes = [vp, i64, i32, vp, vp]
+        L.oracle_stride_region.restype = i64
+        L.oracle_stride_region.argtypes = [vp, i64, i32, vp, i32, vp]
         L.oracle_conv_forward.restype = None
         L.oracle_conv_forward.argtypes = [vp, i64, i32, vp, i32, i32, vp, vp, vp, i64, vp]
         L.oracle_conv_backward.restype = None
@@ -106,6 +108,18 @@ def stride(coords, out_tensor_stride):
     s = _c(out_tensor_stride, np.int32)
     out = np.empty((max(n, 1), ncol), np.int32)
     nu = lib().oracle_stride(_p(coords), n, ncol, _p(s), _p(out))
+    return out[:nu].copy()
+
+
+def stride_region(coords, offsets):
+    """Generated map of a generative transposed convolution: the unique rows
+    of c + offsets[k] over input rows c and offsets k (first occurrence)."""
+    coords = _c(coords, np.int32)
+    n, ncol = coords.shape
+    off = _c(offsets, np.int32)
+    K = off.shape[0]
+    out = np.empty((max(n * K, 1), ncol), np.int32)
+    nu = lib().oracle_stride_region(_p(coords), n, ncol, _p(off), K, _p(out))
     return out[:nu].copy()
 
 

@@ -15,6 +15,9 @@
  *   oracle_kernel_map       — pinned: brute-force sorted join of coordinate
  *                             sets and the dense active-site indicator.
  *   oracle_stride           — pinned: closed form floor(x/s)*s + np.unique.
+ *   oracle_stride_region    — pinned: brute-force set of c + offset, the
+ *                             closed count of 2^D children, and the
+ *                             reference's own stride_region (oracle/_ref).
  *   oracle_conv_forward /
  *   oracle_conv_backward    — pinned: the three known-answer tests of
  *                             tests/convolution/test_cpu_convolution.cpp:15-61
@@ -224,6 +227,34 @@ int64_t oracle_stride(const int32_t *coords, int64_t n, int ncol,
     }
   }
   int64_t nu = oracle_insert_and_map(tmp, n, ncol, out, mapping, NULL);
+  free(tmp);
+  free(mapping);
+  return nu;
+}
+
+/*
+ * Generative expansion, the transposed branch of
+ * CoordinateMapCPU::stride_region (engine/grid/lattice_cpu.hpp:499-534): every
+ * input row c emits c + offsets[k] for each of the K offsets (the kernel
+ * region at the output tensor stride, batch column kept); the generated map
+ * is their unique set. The reference walks its robin-hood table, so its row
+ * order is implementation-defined; here rows follow first occurrence over
+ * (input row, offset). out needs room for n * K rows; returns the unique
+ * count.
+ */
+int64_t oracle_stride_region(const int32_t *coords, int64_t n, int ncol,
+                             const int32_t *offsets, int K, int32_t *out) {
+  const int64_t m = n * K;
+  int32_t *tmp = (int32_t *)malloc(sizeof(int32_t) * (m > 0 ? m : 1) * ncol);
+  int64_t *mapping = (int64_t *)malloc(sizeof(int64_t) * (m > 0 ? m : 1));
+  for (int64_t r = 0; r < n; ++r)
+    for (int k = 0; k < K; ++k) {
+      int32_t *o = tmp + (r * K + k) * ncol;
+      o[0] = coords[r * ncol];
+      for (int i = 1; i < ncol; ++i)
+        o[i] = (int32_t)((uint32_t)coords[r * ncol + i] + (uint32_t)offsets[k * (ncol - 1) + i - 1]);
+    }
+  int64_t nu = oracle_insert_and_map(tmp, m, ncol, out, mapping, NULL);
   free(tmp);
   free(mapping);
   return nu;

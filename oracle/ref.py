@@ -45,6 +45,9 @@ def lib():
                                     ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
                                     ctypes.POINTER(ctypes.c_double),
                                     ctypes.POINTER(ctypes.c_double)]
+        L.ref_stride_region.restype = _i64
+        L.ref_stride_region.argtypes = [_vp, _i64, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                        ctypes.c_int, ctypes.c_int, ctypes.c_int, _i64, _vp]
         L.ref_num_threads.restype = ctypes.c_int
         _LIB = L
     return _LIB
@@ -123,6 +126,19 @@ def conv_time(coords, cin, cout, ks=3, bf16=False, reps=3, seed=0):
     P = _check(lib().ref_conv_time(_p(c), n, ncol, cin, cout, ks, 1 if bf16 else 0, reps, seed,
                                    ctypes.byref(map_ms), ctypes.byref(step_ms)))
     return P, map_ms.value, step_ms.value
+
+
+def stride_region(coords, in_stride, stride, ks, dilation=1, region="cube"):
+    """Generated rows of CoordinateMapManager::stride_region for a generative
+    transposed conv from tensor stride in_stride to in_stride / stride."""
+    c = np.ascontiguousarray(coords, np.int32)
+    n, ncol = c.shape
+    reg = {"cube": 0, "cross": 1}[region]
+    args = (_p(c), n, ncol, in_stride, stride, ks, dilation, reg)
+    m = _check(lib().ref_stride_region(*args, 0, None))
+    out = np.empty((max(m, 1), ncol), np.int32)
+    _check(lib().ref_stride_region(*args, m, _p(out)))
+    return out[:m]
 
 
 def num_threads() -> int:

@@ -166,6 +166,37 @@ int64_t ref_conv(const int32_t *coords, int64_t n, int ncol, const float *x, int
   });
 }
 
+// The generated map of a generative transposed convolution, from the
+// reference's CoordinateMapManager::stride_region (space_impl.hpp:352-381,
+// lattice_cpu.hpp:499-534), driven as its transposed pooling does
+// (pooling.cpp:46-62): the input rows `coords` form the map at tensor stride
+// in_stride, the region (ks^D cube or cross, dilation dil) sits at the output
+// tensor stride in_stride / stride. Rows go to out when they fit cap.
+// Returns the generated row count.
+int64_t ref_stride_region(const int32_t *coords, int64_t n, int ncol, int in_stride, int stride,
+                          int ks, int dil, int region, int64_t cap, int32_t *out) {
+  return guarded([&]() -> int64_t {
+    const int D = ncol - 1;
+    TORCH_CHECK(stride > 0 && in_stride % stride == 0, "stride must divide in_stride");
+    riemann::CoordinateManager m(D, riemann::CoordinateMapBackend::CPU);
+    auto r = m.insert_and_map(int_rows(coords, n, ncol),
+                              riemann::stride_type(static_cast<size_t>(D), in_stride));
+    riemann::stride_type out_stride(static_cast<size_t>(D), in_stride / stride);
+    riemann::stride_type kernel_size(static_cast<size_t>(D), ks);
+    riemann::stride_type dilation(static_cast<size_t>(D), dil);
+    riemann::cpu_kernel_region<int32_t> kregion(region_of(region), ncol, out_stride.data(),
+                                                kernel_size.data(), dilation.data(), 0, nullptr,
+                                                0, true);
+    const auto generated = m.manager_ptr<CpuManager>()->stride_region(
+        r.first.get_key(), kregion, out_stride, true);
+    auto oc = m.get_coordinates(riemann::CoordinateMapKey(ncol, generated.first))
+                  .to(torch::kInt32);
+    if (oc.size(0) <= cap)
+      copy_out(oc, out);
+    return oc.size(0);
+  });
+}
+
 // Times the reference on the CPU: one RiemannConvolution forward (which
 // builds and caches the kernel map) into *map_ms, then `reps` forward +
 // backward steps reusing the cached map, their mean into *step_ms. Random

@@ -28,7 +28,7 @@ EXPORTS = (
     "rhip_last_error", "rhip_abi_version", "rhip_table_bytes",
     "rhip_hash_workspace_bytes", "rhip_hash_build", "rhip_hash_lookup",
     "rhip_order_workspace_bytes", "rhip_spatial_order", "rhip_stride_coords",
-    "rhip_kmap_workspace_bytes", "rhip_kmap_count", "rhip_kmap_fill",
+    "rhip_expand_coords", "rhip_kmap_workspace_bytes", "rhip_kmap_count", "rhip_kmap_fill",
     "rhip_conv_workspace_bytes", "rhip_conv_forward",
     "rhip_conv_backward_input", "rhip_conv_backward_weight",
 )
@@ -61,6 +61,7 @@ def _declare(lib):
         "rhip_order_workspace_bytes": (ctypes.c_int, [_i64, _P(_sz)]),
         "rhip_spatial_order": (ctypes.c_int, [_P(RhipTable), _vp, _vp, _vp, _sz, _vp]),
         "rhip_stride_coords": (ctypes.c_int, [_vp, _i64, _i32, _P(_i32), _vp, _vp]),
+        "rhip_expand_coords": (ctypes.c_int, [_vp, _i64, _i32, _vp, _i32, _vp, _vp]),
         "rhip_kmap_workspace_bytes": (ctypes.c_int, [_i64, _i64, _i32, _P(_sz)]),
         "rhip_kmap_count": (ctypes.c_int, [_P(RhipTable), _vp, _vp, _i64, _i32, _P(_i32),
                                            _vp, _sz, _vp, _vp, _vp, _P(_i64), _P(_i32),
@@ -206,6 +207,24 @@ def stride_coords(coords: torch.Tensor, out_tensor_stride) -> torch.Tensor:
     out = torch.empty_like(coords)
     _check(lib().rhip_stride_coords(_ptr(coords), n, ncol, s, _ptr(out), _stream(coords.device)),
            "rhip_stride_coords")
+    return out
+
+
+def expand_coords(coords: torch.Tensor, offsets) -> torch.Tensor:
+    """Generative expansion: row i*K + k = coords[i] + offsets[k] (batch
+    kept); offsets [K, D] are the region at the output tensor stride. Hash
+    the result (hash_build) for the generated output map."""
+    _require_cuda(coords, "coords")
+    coords = coords.to(torch.int32).contiguous()
+    n, ncol = coords.shape
+    off = torch.as_tensor(np.asarray(offsets.cpu() if torch.is_tensor(offsets) else offsets),
+                          dtype=torch.int32).to(coords.device).contiguous()
+    K = off.shape[0]
+    if off.dim() != 2 or off.shape[1] != ncol - 1:
+        raise RuntimeError("offsets must be [K, D]")
+    out = torch.empty((n * K, ncol), dtype=torch.int32, device=coords.device)
+    _check(lib().rhip_expand_coords(_ptr(coords), n, ncol, _ptr(off), K, _ptr(out),
+                                    _stream(coords.device)), "rhip_expand_coords")
     return out
 
 

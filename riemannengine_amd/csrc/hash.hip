@@ -296,6 +296,24 @@ __global__ __launch_bounds__(kBlock) void stride_kernel(const int32_t *in,
   out[i] = c == 0 ? v : floor_align(v, st.s[c - 1]);
 }
 
+// Generative expansion: out row i*K + k = in row i + offsets[k] (batch kept,
+// wrap-around int32 arithmetic as the coordinate type has).
+__global__ __launch_bounds__(kBlock) void expand_kernel(const int32_t *in, int64_t n, int ncol,
+                                                        int K, const int32_t *offsets,
+                                                        int32_t *out) {
+  const int64_t i = blockIdx.x * (int64_t)kBlock + threadIdx.x;
+  if (i >= n * K * ncol)
+    return;
+  const int64_t row = i / ncol;
+  const int c = static_cast<int>(i % ncol);
+  const int64_t src = row / K;
+  const int k = static_cast<int>(row % K);
+  const int32_t v = in[src * ncol + c];
+  out[i] = c == 0 ? v
+                  : static_cast<int32_t>(static_cast<uint32_t>(v) +
+                                         static_cast<uint32_t>(offsets[k * (ncol - 1) + c - 1]));
+}
+
 // ------------------------------------------------------------------ host
 
 static int64_t table_capacity(int64_t n) {
@@ -534,6 +552,24 @@ extern "C" int rhip_stride_coords(const int32_t *coords, int64_t n,
     const int64_t total = n * ncol;
     hipLaunchKernelGGL(stride_kernel, dim3(ceil_div(total, kBlock)),
                        dim3(kBlock), 0, stream, coords, n, ncol, st, out);
+    RHIP_LAUNCH_CHECK();
+  });
+}
+
+extern "C" int rhip_expand_coords(const int32_t *coords, int64_t n, int32_t ncol,
+                                  const int32_t *offsets, int32_t K, int32_t *out,
+                                  hipStream_t stream) {
+  return guarded([&] {
+    RHIP_CHECK_ARG(ncol >= 2 && ncol <= RHIP_MAX_COLS, "bad ncol");
+    RHIP_CHECK_ARG(K >= 1, "K must be >= 1");
+    RHIP_CHECK_ARG(n >= 0 && n <= INT64_MAX / (static_cast<int64_t>(K) * ncol),
+                   "n * K * ncol overflows");
+    if (n == 0)
+      return;
+    RHIP_CHECK_ARG(coords && offsets && out, "coords, offsets and out must be non-null");
+    const int64_t total = n * K * ncol;
+    hipLaunchKernelGGL(expand_kernel, dim3(ceil_div(total, kBlock)), dim3(kBlock), 0, stream,
+                       coords, n, ncol, K, offsets, out);
     RHIP_LAUNCH_CHECK();
   });
 }

@@ -155,6 +155,15 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
             return self.stride(key, as_stride(kernel_stride), std::move(string_id));
           },
           py::arg("coordinate_map_key"), py::arg("kernel_stride"), py::arg("string_id") = "")
+      .def(
+          "stride_region",
+          [](CoordinateManager &self, const CoordinateMapKey &key, const at::Tensor &offsets,
+             const std::vector<int64_t> &out_tensor_stride, bool expand) {
+            return self.stride_region(key, offsets.to(at::kCPU), as_stride(out_tensor_stride),
+                                      expand);
+          },
+          py::arg("coordinate_map_key"), py::arg("region_offsets"),
+          py::arg("out_tensor_stride"), py::arg("expand_coordinates") = true)
       .def("size", [](const CoordinateManager &self,
                       const CoordinateMapKey &key) { return self.size(key); })
       .def("exists", &CoordinateManager::exists)

@@ -171,6 +171,19 @@ SparseTensor RiemannConvolutionBaseImpl::forward(const SparseTensor &input) {
   auto manager = input.coordinate_manager();
   if (!is_transpose_ && params.kernel_stride != stride_type(dimension_, 1))
     output_key = manager->stride(input.coordinate_map_key(), params.kernel_stride);
+  if (is_transpose_ && params.expand_coordinates) {
+    // Generative transposed convolution: the output map is generated from
+    // the input through the kernel region at the output stride
+    // (CoordinateMapManager::stride_region, engine/grid/space_impl.hpp:
+    // 352-381), as the reference's transposed pooling builds it
+    // (engine/nn/pooling.cpp:46-62); the reference's convolution stores the
+    // flag but does not generate (engine/nn/conv.cpp:104-138).
+    const auto offsets = region_offsets(params.region_type, params.kernel_size,
+                                        params.kernel_dilation, output_stride,
+                                        params.region_offsets);
+    output_key = manager->stride_region(input.coordinate_map_key(), offsets, output_stride, true)
+                     .first;
+  }
   const HipKernelMap &map = manager->kernel_map(
       input.coordinate_map_key(), output_key, params.kernel_size, params.kernel_stride,
       params.kernel_dilation, params.region_type, params.region_offsets, is_transpose_, false);

@@ -208,6 +208,17 @@ public:
   CoordinateMapKey stride(const CoordinateMapKey &in_key, const stride_type &kernel_stride,
                           std::string string_id = "");
 
+  // Generated map of a generative transposed convolution
+  // (CoordinateMapManager::stride_region, engine/grid/space_impl.hpp:352-381):
+  // the unique rows of c + offsets[k] over the input map's rows c, offsets
+  // the region [K, D] (int32, host) at out_tensor_stride. Keyed by
+  // (out_tensor_stride, ""); built when that key is new or `expand` is set
+  // (then under a random id if the key exists). Returns (key, built).
+  std::pair<CoordinateMapKey, bool> stride_region(const CoordinateMapKey &in_key,
+                                                  const at::Tensor &offsets,
+                                                  const stride_type &out_tensor_stride,
+                                                  bool expand);
+
   at::Tensor get_coordinates(const CoordinateMapKey &key) const;
   uint32_t size(const CoordinateMapKey &key) const;
   bool exists(const CoordinateMapKey &key) const;

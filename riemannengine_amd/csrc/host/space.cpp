@@ -390,6 +390,37 @@ CoordinateMapKey CoordinateManager::stride(const CoordinateMapKey &in_key,
   return CoordinateMapKey(static_cast<size_type>(ik.first.size() + 1), out_key);
 }
 
+std::pair<CoordinateMapKey, bool>
+CoordinateManager::stride_region(const CoordinateMapKey &in_key, const at::Tensor &offsets,
+                                 const stride_type &out_tensor_stride, bool expand) {
+  const auto ik = in_key.get_key();
+  auto it = maps_.find(ik);
+  TORCH_CHECK(it != maps_.end(), "coordinate map not found: ", in_key.to_string());
+  TORCH_CHECK(out_tensor_stride.size() == ik.first.size(), "tensor stride size mismatch");
+  TORCH_CHECK(offsets.dim() == 2 && offsets.size(1) == static_cast<int64_t>(ik.first.size()),
+              "region offsets must be [K, D]");
+  coordinate_map_key_type out_key{out_tensor_stride, ""};
+  const bool exists = maps_.count(out_key) > 0;
+  if (exists && !expand)
+    return {CoordinateMapKey(static_cast<size_type>(ik.first.size() + 1), out_key), false};
+  const CoordinateMapHIP &in_map = it->second;
+  const auto dev = in_map.coords.device();
+  at::DeviceGuard guard(dev);
+  const int64_t K = offsets.size(0), n = in_map.size();
+  const int32_t ncol = static_cast<int32_t>(in_map.coords.size(1));
+  auto off = offsets.to(torch::kInt32).contiguous().to(dev);
+  auto expanded = torch::empty({n * K, ncol}, in_map.coords.options());
+  if (n > 0)
+    check_rhip(rhip_expand_coords(in_map.coords.data_ptr<int32_t>(), n, ncol,
+                                  off.data_ptr<int32_t>(), static_cast<int32_t>(K),
+                                  expanded.data_ptr<int32_t>(), current_stream(dev)),
+               "rhip_expand_coords");
+  if (exists)
+    out_key = random_key(out_tensor_stride, "");
+  maps_.emplace(out_key, build_map(expanded, out_tensor_stride, nullptr, nullptr));
+  return {CoordinateMapKey(static_cast<size_type>(ik.first.size() + 1), out_key), true};
+}
+
 const CoordinateMapHIP &CoordinateManager::coordinate_map(const CoordinateMapKey &key) const {
   auto it = maps_.find(key.get_key());
   TORCH_CHECK(it != maps_.end(), "coordinate map not found: ", key.to_string());

@@ -243,3 +243,42 @@ def test_config5_encoder_full_size():
         assert k0.grad is not None and torch.isfinite(k0.grad.float()).all()
         outs[dtype] = h.F.detach().float().cpu().numpy()
     assert_rel(outs[torch.bfloat16], outs[torch.float32], 5e-2, "bf16 vs fp32 encoder output")
+
+
+@pytest.mark.parametrize("ks", [2, 3])
+def test_generative_transposed_convolution(ks):
+    """RiemannGenerativeConvolutionTranspose generates its output map from
+    the coarse input (stride_region, the region at the output stride) instead
+    of requiring the finer map: output rows = the oracle's generated set;
+    since a stride-1 map already exists, the generated one gets its own key.
+    Values and gradients vs the oracle over the swapped forward map."""
+    c, _, _ = oracle.insert_and_map(_cloud(17, n=4000, span=20, dup=0))
+    torch.manual_seed(5)
+    down = re_.nn.RiemannConvolution(8, 16, kernel_size=2, stride=2, dimension=3)
+    gen = re_.nn.RiemannGenerativeConvolutionTranspose(16, 8, kernel_size=ks, stride=2,
+                                                        dimension=3)
+    down.to(DEV)
+    gen.to(DEV)
+    x = re_.SparseTensor(torch.randn(len(c), 8, device=DEV), torch.from_numpy(c).to(DEV))
+    y = down(x)
+    yf = y.F.detach().clone().requires_grad_(True)
+    ys = re_.SparseTensor(yf, y.coordinate_map_key, y.coordinate_manager)
+    z = gen(ys)
+    coarse = y.C.cpu().numpy()
+    off = oracle.region_offsets(3, ks, 1, 1)
+    fine = oracle.stride_region(coarse, off)
+    np.testing.assert_array_equal(z.C.cpu().numpy(), fine)
+    assert z.tensor_stride == [1, 1, 1] and not (z.coordinate_map_key == x.coordinate_map_key)
+    gz = torch.randn(tuple(z.F.shape), generator=torch.Generator().manual_seed(6)).to(DEV)
+    (z.F * gz).sum().backward()
+    kofs, ir, orr = oracle.kernel_map(fine, coarse, off)  # fine <- coarse, then swapped
+    w = _np(gen.kernel)
+    assert_rel(_np(z.F), oracle.conv_forward(_np(yf), w, kofs, orr, ir, len(fine)), 1e-4, "Y")
+    rgx, rgw = oracle.conv_backward(_np(yf), _np(gz), w, kofs, orr, ir)
+    assert_rel(_np(yf.grad), rgx, 1e-4, "dX")
+    assert_rel(_np(gen.kernel.grad), rgw, 1e-4, "dW")
+    # the manager's own entry point: an existing (stride, "") key is kept
+    # unless expansion is asked for
+    mgr = y.coordinate_manager
+    k1, built = mgr.stride_region(y.coordinate_map_key, torch.from_numpy(off), [1, 1, 1], False)
+    assert not built and k1.tensor_stride == [1, 1, 1]

@@ -220,3 +220,24 @@ def test_lidar_down_up_maps():
     assert km.n_pairs == len(c)  # P_down = N_fine
     np.testing.assert_array_equal(gpu_canonical(km),
                                   _ref_map(c, tout.ucoords.cpu().numpy(), off)[1])
+
+
+@pytest.mark.parametrize("ks,region", [(2, "cube"), (3, "cube"), (3, "cross")])
+def test_generative_expansion_matches_oracle_and_reference(ks, region):
+    """Generated map of a generative transposed conv (stride 2 -> 1): the
+    unique rows of c + offset over the coarse rows c, offsets at the output
+    stride. Bit-exact with the oracle in first-occurrence order over (row,
+    offset); the same set as the reference's own stride_region."""
+    from oracle import ref
+    rng = np.random.default_rng(ks + 7)
+    c, _, _ = oracle.insert_and_map(random_coords(rng, 20000, 3, 30))
+    coarse = oracle.stride(c, [2, 2, 2])
+    off = oracle.region_offsets(3, ks, 1, 1, region)
+    gen = abi.hash_build(abi.expand_coords(to_dev(coarse), off))
+    got = gen.ucoords.cpu().numpy()
+    np.testing.assert_array_equal(got, oracle.stride_region(coarse, off))
+    if ks == 2:  # the 2^3 children of every coarse voxel, all distinct
+        assert len(got) == 8 * len(coarse)
+    if ref.available():
+        exp = ref.stride_region(coarse, 2, 2, ks, 1, region)
+        assert sorted(map(tuple, got.tolist())) == sorted(map(tuple, exp.tolist()))
