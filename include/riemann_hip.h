@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define RHIP_ABI_VERSION 5
+#define RHIP_ABI_VERSION 6
 #define RHIP_MAX_COLS 8 /* batch column + up to 7 spatial axes */
 
 typedef enum rhip_status {
@@ -255,6 +255,151 @@ int rhip_conv_backward_weight(const void *x, int64_t n_in, int32_t cin,
                               const int32_t *out_rows, void *grad_w,
                               int32_t dtype, void *workspace,
                               size_t workspace_bytes, hipStream_t stream);
+
+/* --------------------------------------------------------------- pooling */
+
+/* Reductions of local and global pooling (engine/foundation/types.hpp:121-136:
+ * LOCAL_{SUM,AVG,MAX}_POOLING and the GLOBAL_* modes, which reduce the same
+ * three ways). */
+typedef enum rhip_pool_mode {
+  RHIP_POOL_SUM = 0,
+  RHIP_POOL_AVG = 1, /* sum / number of pooled rows */
+  RHIP_POOL_MAX = 2  /* NaN propagates; the gradient splits evenly between ties */
+} rhip_pool_mode;
+
+/* Workspace shared by the two phases of one stride map (pass the same
+ * buffer, unchanged, to rhip_stride_map_count and rhip_stride_map_fill). */
+int rhip_stride_map_workspace_bytes(int64_t n_in, int64_t n_out, size_t *bytes);
+
+/*
+ * Phase 1 of a pooling stride map (kernel size == stride): every input row
+ * maps to the output row holding its floor-aligned coordinates
+ * (b, floor(x_d / s_d) * s_d) in out_table; out_tensor_stride is a HOST array
+ * [ncol-1]. The inputs are grouped by output (ascending input row within a
+ * group) in the workspace and *k_max_host receives the largest group, the
+ * height of the neighbour table of phase 2. Synchronises the stream once.
+ * Fails with RHIP_ERR_INVALID when an input row has no output row, as the
+ * reference's ASSERT does.
+ * Replaces CoordinateMapCPU::stride_map (engine/grid/lattice_cpu.hpp:675-710)
+ * behind stride_map_functor (engine/grid/space_impl.hpp:617-626, 660-669) and
+ * CoordinateMapGPU::stride_map (engine/grid/lattice_gpu.cu:1553-1670).
+ */
+int rhip_stride_map_count(const rhip_table *out_table, const int32_t *in_coords,
+                          int64_t n_in, const int32_t *out_tensor_stride,
+                          void *workspace, size_t workspace_bytes,
+                          int32_t *k_max_host, hipStream_t stream);
+
+/*
+ * Phase 2: the stride map in the neighbour-table form of a kernel map
+ * (columns by processing position, as rhip_kmap_count / rhip_kmap_fill):
+ *   nbr [k_max, n_out]: nbr[k*n_out+p] = k-th input row (ascending) of the
+ *                       output out_order[p], -1 past its group;
+ *   nbr_t [k_max, n_in]: nbr_t[k*n_in+q] = the output row whose k-th input
+ *                       is in_order[q], else -1;
+ *   in_rows/out_rows [n_in]: the reference's single pair list (one kernel
+ *                       offset), grouped by output.
+ * in_order / out_order are processing orders (permutations; NULL = row order),
+ * e.g. the locality orders of the two maps.
+ */
+int rhip_stride_map_fill(int64_t n_in, int64_t n_out, int32_t k_max,
+                         const int32_t *in_order, const int32_t *out_order,
+                         void *workspace, size_t workspace_bytes, int32_t *nbr,
+                         int32_t *nbr_t, int32_t *in_rows, int32_t *out_rows,
+                         hipStream_t stream);
+
+/* Workspace of rhip_pool_backward (max pooling keeps one fp32 per output
+ * element; sum and average need none). */
+int rhip_pool_workspace_bytes(int64_t n_out, int32_t C, int32_t mode,
+                              size_t *bytes);
+
+/*
+ * Local pooling: y[out_order[p]] = reduce over k < K with i = nbr[k*n_out+p]
+ * >= 0 of x[i] (channel-wise, fp32 accumulation, x and y in `dtype`); an
+ * output with no input row is 0. counts [n_out] (optional) receives the
+ * number of rows pooled into each output row, which average-pooling backward
+ * needs. nbr and out_order are a kernel map's (rhip_kmap_count) or a stride
+ * map's (rhip_stride_map_fill); out_order NULL = row order.
+ * Replaces evaluate_pooling's per-output index_select + sum/mean/amax + stack
+ * (engine/nn/pooling.cpp:80-150).
+ */
+int rhip_pool_forward(const void *x, int64_t n_in, int32_t C,
+                      const int32_t *nbr, int32_t K, const int32_t *out_order,
+                      int64_t n_out, int32_t mode, void *y, int32_t *counts,
+                      int32_t dtype, hipStream_t stream);
+
+/*
+ * Local pooling backward: grad_x[i] for i = in_order[q] is the sum over k
+ * with o = nbr_t[k*n_in+q] >= 0 of  sum: grad_y[o];  average: grad_y[o] /
+ * counts[o];  max: grad_y[o] / t where x[i] == y[o] (t = number of pooled
+ * rows equal to y[o], per channel), else 0. grad_x [n_in, C] is overwritten.
+ * Max pooling also needs x, y, nbr, out_order and the workspace; average
+ * needs counts from rhip_pool_forward.
+ * Replaces the autograd replay of StackBackward / SumBackward / MeanBackward /
+ * AmaxBackward / IndexSelectBackward of evaluate_pooling
+ * (engine/nn/pooling.cpp:120-140).
+ */
+int rhip_pool_backward(const void *grad_y, const void *y, const void *x,
+                       int64_t n_out, int32_t C, const int32_t *nbr,
+                       const int32_t *out_order, const int32_t *nbr_t,
+                       int32_t K, const int32_t *in_order,
+                       int64_t n_in, const int32_t *counts, int32_t mode,
+                       void *grad_x, int32_t dtype, void *workspace,
+                       size_t workspace_bytes, hipStream_t stream);
+
+/* Workspace of the global-pooling calls over n rows, C channels and
+ * n_batches batches (rhip_batch_count and rhip_batch_segments accept it with
+ * any n_batches). */
+int rhip_global_pool_workspace_bytes(int64_t n, int32_t C, int32_t n_batches,
+                                     size_t *bytes);
+
+/*
+ * Number of batches of a coordinate set: max(batch column) + 1, 0 when every
+ * batch index is negative or n == 0. Synchronises the stream once.
+ * Replaces coordinates.select(1, 0).max() + 1
+ * (engine/nn/pooling.cpp:207-212).
+ */
+int rhip_batch_count(const int32_t *coords, int64_t n, int32_t ncol,
+                     void *workspace, size_t workspace_bytes,
+                     int32_t *n_batches_host, hipStream_t stream);
+
+/*
+ * Rows grouped by batch: rows of batch b are members[seg[b] .. seg[b+1]) in
+ * ascending row order (members [n], seg [n_batches+1]); rows whose batch is
+ * outside [0, n_batches) follow seg[n_batches] and belong to no batch.
+ * Replaces the per-batch at::nonzero(coordinates.select(1, 0) == batch)
+ * (engine/nn/pooling.cpp:220-224).
+ */
+int rhip_batch_segments(const int32_t *coords, int64_t n, int32_t ncol,
+                        int32_t n_batches, void *workspace, size_t workspace_bytes,
+                        int32_t *members, int32_t *seg, hipStream_t stream);
+
+/*
+ * Global pooling: y[b] = reduce of x over the rows of batch b ([n_batches, C],
+ * fp32 accumulation in a fixed order, 0 for an empty batch).
+ * Replaces RiemannGlobalPoolingImpl::forward's per-batch reduction
+ * (engine/nn/pooling.cpp:203-260).
+ */
+int rhip_global_pool_forward(const void *x, int64_t n, int32_t C,
+                             const int32_t *members, const int32_t *seg,
+                             int32_t n_batches, int32_t mode, void *y,
+                             int32_t dtype, void *workspace,
+                             size_t workspace_bytes, hipStream_t stream);
+
+/*
+ * Global pooling backward: grad_x[i] for a row of batch b = coords[i][0]:
+ * sum: grad_y[b]; average: grad_y[b] / rows of b; max: grad_y[b] / t where
+ * x[i] == y[b] (t tied rows per channel), else 0; 0 for rows outside every
+ * batch. Max pooling also needs x, y, members and the workspace.
+ * Replaces the autograd replay of the reference's global pooling graph
+ * (engine/nn/pooling.cpp:225-259).
+ */
+int rhip_global_pool_backward(const void *grad_y, const void *y, const void *x,
+                              const int32_t *coords, int32_t ncol, int64_t n,
+                              int32_t C, const int32_t *members,
+                              const int32_t *seg, int32_t n_batches,
+                              int32_t mode, void *grad_x, int32_t dtype,
+                              void *workspace, size_t workspace_bytes,
+                              hipStream_t stream);
 
 #ifdef __cplusplus
 }

@@ -47,6 +47,16 @@ def lib():
         L.oracle_conv_backward.restype = None
         L.oracle_conv_backward.argtypes = [vp, i64, i32, vp, i64, i32, vp, i32, vp, vp, vp,
                                            vp, vp]
+        L.oracle_stride_map.restype = i64
+        L.oracle_stride_map.argtypes = [vp, i64, i32, vp, i64, vp, vp]
+        L.oracle_pool_forward.restype = None
+        L.oracle_pool_forward.argtypes = [vp, i64, i32, vp, vp, i64, i64, i32, vp, vp]
+        L.oracle_pool_backward.restype = None
+        L.oracle_pool_backward.argtypes = [vp, vp, vp, i64, i64, i32, vp, vp, i64, i32, vp]
+        L.oracle_global_pool_forward.restype = i64
+        L.oracle_global_pool_forward.argtypes = [vp, vp, i64, i32, i32, i32, i64, vp]
+        L.oracle_global_pool_backward.restype = None
+        L.oracle_global_pool_backward.argtypes = [vp, vp, vp, vp, i64, i32, i32, i64, i32, vp]
         _lib = L
     return _lib
 
@@ -160,3 +170,60 @@ def canonical_pairs(kofs, in_rows, out_rows, in_coords=None, out_coords=None):
         return t
     idx = np.lexsort(t.T[::-1])
     return t[idx]
+
+
+POOL_MODE = {"sum": 0, "avg": 1, "max": 2}
+
+
+def stride_map(in_coords, out_coords, out_tensor_stride):
+    """in_to_out [n_in]: the output row of each input's floor-aligned
+    coordinates (-1 where there is none) and the number of such misses."""
+    a, b = _c(in_coords, np.int32), _c(out_coords, np.int32)
+    ncol = a.shape[1]
+    s = _c(out_tensor_stride, np.int32)
+    r = np.empty(max(a.shape[0], 1), np.int32)
+    miss = lib().oracle_stride_map(_p(a), a.shape[0], ncol, _p(b), b.shape[0], _p(s), _p(r))
+    return r[:a.shape[0]], int(miss)
+
+
+def pool_forward(x, in_rows, out_rows, n_out, mode):
+    """(y [n_out, C], counts [n_out]) of local pooling over the pair list."""
+    x = _c(x, np.float32)
+    C = x.shape[1]
+    ir, orr = _c(in_rows, np.int32), _c(out_rows, np.int32)
+    y = np.empty((max(n_out, 1), C), np.float32)
+    cnt = np.empty(max(n_out, 1), np.int32)
+    lib().oracle_pool_forward(_p(x), x.shape[0], C, _p(ir), _p(orr), ir.shape[0], n_out,
+                              POOL_MODE[mode], _p(y), _p(cnt))
+    return y[:n_out], cnt[:n_out]
+
+
+def pool_backward(x, y, grad_y, in_rows, out_rows, mode):
+    x, y, gy = _c(x, np.float32), _c(y, np.float32), _c(grad_y, np.float32)
+    C = x.shape[1]
+    ir, orr = _c(in_rows, np.int32), _c(out_rows, np.int32)
+    gx = np.empty((max(x.shape[0], 1), C), np.float32)
+    lib().oracle_pool_backward(_p(x), _p(y), _p(gy), x.shape[0], y.shape[0], C, _p(ir),
+                               _p(orr), ir.shape[0], POOL_MODE[mode], _p(gx))
+    return gx[:x.shape[0]]
+
+
+def global_pool_forward(x, coords, mode):
+    """y [B, C] with B = max batch index + 1."""
+    x, c = _c(x, np.float32), _c(coords, np.int32)
+    n, ncol = c.shape
+    C = x.shape[1]
+    B = lib().oracle_global_pool_forward(_p(x), _p(c), n, ncol, C, POOL_MODE[mode], 0, None)
+    y = np.empty((max(B, 1), C), np.float32)
+    lib().oracle_global_pool_forward(_p(x), _p(c), n, ncol, C, POOL_MODE[mode], B, _p(y))
+    return y[:B]
+
+
+def global_pool_backward(x, y, grad_y, coords, mode):
+    x, y, gy, c = (_c(x, np.float32), _c(y, np.float32), _c(grad_y, np.float32),
+                   _c(coords, np.int32))
+    n, ncol = c.shape
+    gx = np.empty((max(n, 1), x.shape[1]), np.float32)
+    lib().oracle_global_pool_backward(_p(x), _p(y), _p(gy), _p(c), n, ncol, x.shape[1],
+                                      y.shape[0], POOL_MODE[mode], _p(gx))
+    return gx[:n]

@@ -23,6 +23,17 @@
  *                             tests/convolution/test_cpu_convolution.cpp:15-61
  *                             and dense torch conv3d (a textbook routine) on
  *                             voxelised inputs, plus fp64 brute force.
+ *   oracle_stride_map       — pinned: brute-force floor division per row and
+ *                             the reference's own pooling (oracle/_ref).
+ *   oracle_pool_forward /
+ *   oracle_pool_backward    — pinned: the known answers of
+ *                             tests/engine/test_layers.cpp:80-115, torch's
+ *                             sum/mean/amax and their autograd (ties split
+ *                             evenly) on the same groups, closed forms (sum of
+ *                             ones = group sizes) and the reference (_ref).
+ *   oracle_global_pool_*    — pinned: tests/engine/test_layers.cpp:58-78,
+ *                             torch per-batch reductions + autograd, and the
+ *                             reference (_ref).
  */
 #include <math.h>
 #include <stdint.h>
@@ -335,4 +346,166 @@ void oracle_conv_backward(const float *x, int64_t n_in, int cin,
     grad_w[e] = (float)gw[e];
   free(gx);
   free(gw);
+}
+
+/* ---------------------------------------------------------------- pooling */
+
+/*
+ * Stride map: CoordinateMapCPU::stride_map (engine/grid/lattice_cpu.hpp:675-710)
+ * with detail::stride_coordinate (engine/grid/stencil.hpp:46-53): input row i
+ * maps to the row of (b, floor((float)x / s) * s) in out_coords. in_to_out[i]
+ * is that row or -1; returns the number of rows with none (the reference
+ * ASSERTs there are none).
+ */
+int64_t oracle_stride_map(const int32_t *in_coords, int64_t n_in, int ncol,
+                          const int32_t *out_coords, int64_t n_out,
+                          const int32_t *stride, int32_t *in_to_out) {
+  otab t;
+  int32_t *tmp = (int32_t *)malloc(sizeof(int32_t) * ncol);
+  int64_t miss = 0;
+  otab_init(&t, n_out, out_coords, ncol);
+  for (int64_t u = 0; u < n_out; ++u)
+    if (otab_find(&t, out_coords + u * ncol) < 0)
+      otab_put(&t, out_coords + u * ncol, u);
+  for (int64_t r = 0; r < n_in; ++r) {
+    tmp[0] = in_coords[r * ncol];
+    for (int i = 1; i < ncol; ++i) {
+      int s = stride[i - 1];
+      tmp[i] = (int32_t)(floorf((float)in_coords[r * ncol + i] / (float)s) * (float)s);
+    }
+    int64_t o = otab_find(&t, tmp);
+    in_to_out[r] = (int32_t)o;
+    miss += o < 0;
+  }
+  free(tmp);
+  free(t.slot);
+  return miss;
+}
+
+/* mode: 0 sum, 1 average, 2 max (PoolingMode LOCAL_{SUM,AVG,MAX}_POOLING) */
+
+/*
+ * Local pooling: evaluate_pooling (engine/nn/pooling.cpp:80-150). The pairs
+ * (in_rows[p], out_rows[p]) are gathered per output in pair order
+ * (inputs_by_output), each group reduced by values.sum(0) / mean(0) /
+ * amax({0}) (amax propagates NaN), an empty group gives zeros. Sums in double.
+ * counts [n_out] (may be NULL) receives the group sizes.
+ */
+void oracle_pool_forward(const float *x, int64_t n_in, int C, const int32_t *in_rows,
+                         const int32_t *out_rows, int64_t P, int64_t n_out, int mode,
+                         float *y, int32_t *counts) {
+  double *acc = (double *)malloc(sizeof(double) * (size_t)(n_out > 0 ? n_out : 1) * C);
+  int64_t *cnt = (int64_t *)calloc((size_t)(n_out > 0 ? n_out : 1), sizeof(int64_t));
+  for (int64_t e = 0; e < n_out * C; ++e)
+    acc[e] = mode == 2 ? -INFINITY : 0.0;
+  for (int64_t p = 0; p < P; ++p) {
+    int64_t i = in_rows[p], o = out_rows[p];
+    if (i < 0 || i >= n_in || o < 0 || o >= n_out)
+      continue;
+    ++cnt[o];
+    for (int c = 0; c < C; ++c) {
+      double v = x[i * C + c];
+      double *a = acc + o * C + c;
+      if (mode == 2)
+        *a = (v > *a || isnan(v)) && !isnan(*a) ? v : *a;
+      else
+        *a += v;
+    }
+  }
+  for (int64_t o = 0; o < n_out; ++o) {
+    for (int c = 0; c < C; ++c) {
+      double a = acc[o * C + c];
+      y[o * C + c] = cnt[o] == 0 ? 0.f : (float)(mode == 1 ? a / (double)cnt[o] : a);
+    }
+    if (counts)
+      counts[o] = (int32_t)cnt[o];
+  }
+  free(acc);
+  free(cnt);
+}
+
+/*
+ * Local pooling backward: the gradient LibTorch's autograd gives
+ * evaluate_pooling's graph (pooling.cpp:120-140): sum passes grad_y[o] to
+ * every pooled row, mean grad_y[o] / n, amax grad_y[o] / t to the t rows
+ * equal to y[o] (per channel) and 0 to the rest. Accumulates in double over
+ * the pairs; grad_x [n_in, C] is overwritten.
+ */
+void oracle_pool_backward(const float *x, const float *y, const float *grad_y, int64_t n_in,
+                          int64_t n_out, int C, const int32_t *in_rows, const int32_t *out_rows,
+                          int64_t P, int mode, float *grad_x) {
+  double *gx = (double *)calloc((size_t)(n_in > 0 ? n_in : 1) * C, sizeof(double));
+  int64_t *cnt = (int64_t *)calloc((size_t)(n_out > 0 ? n_out : 1), sizeof(int64_t));
+  int64_t *ties = (int64_t *)calloc((size_t)(n_out > 0 ? n_out : 1) * C, sizeof(int64_t));
+  for (int64_t p = 0; p < P; ++p) {
+    int64_t i = in_rows[p], o = out_rows[p];
+    if (i < 0 || i >= n_in || o < 0 || o >= n_out)
+      continue;
+    ++cnt[o];
+    for (int c = 0; c < C; ++c)
+      ties[o * C + c] += x[i * C + c] == y[o * C + c];
+  }
+  for (int64_t p = 0; p < P; ++p) {
+    int64_t i = in_rows[p], o = out_rows[p];
+    if (i < 0 || i >= n_in || o < 0 || o >= n_out)
+      continue;
+    for (int c = 0; c < C; ++c) {
+      double g = grad_y[o * C + c];
+      if (mode == 1)
+        g /= (double)cnt[o];
+      else if (mode == 2)
+        g = x[i * C + c] == y[o * C + c] ? g / (double)ties[o * C + c] : 0.0;
+      gx[i * C + c] += g;
+    }
+  }
+  for (int64_t e = 0; e < n_in * C; ++e)
+    grad_x[e] = (float)gx[e];
+  free(gx);
+  free(cnt);
+  free(ties);
+}
+
+/*
+ * Global pooling: RiemannGlobalPoolingImpl::forward (engine/nn/pooling.cpp:
+ * 203-260): B = max batch index + 1 (0 for no rows); output row b reduces the
+ * rows whose batch index is b (sum / mean / amax; zeros for an empty batch).
+ * y needs [min(B, max_b), C]; returns B.
+ */
+int64_t oracle_global_pool_forward(const float *x, const int32_t *coords, int64_t n, int ncol,
+                                   int C, int mode, int64_t max_b, float *y) {
+  int64_t B = 0;
+  for (int64_t r = 0; r < n; ++r)
+    if ((int64_t)coords[r * ncol] + 1 > B)
+      B = (int64_t)coords[r * ncol] + 1;
+  if (B > max_b)
+    return B;
+  int32_t *in_rows = (int32_t *)malloc(sizeof(int32_t) * (n > 0 ? n : 1));
+  int32_t *out_rows = (int32_t *)malloc(sizeof(int32_t) * (n > 0 ? n : 1));
+  int64_t P = 0;
+  for (int64_t r = 0; r < n; ++r)
+    if (coords[r * ncol] >= 0) {
+      in_rows[P] = (int32_t)r;
+      out_rows[P++] = coords[r * ncol];
+    }
+  oracle_pool_forward(x, n, C, in_rows, out_rows, P, B, mode, y, NULL);
+  free(in_rows);
+  free(out_rows);
+  return B;
+}
+
+/* Backward of the above (autograd of the per-batch index_select + reduce). */
+void oracle_global_pool_backward(const float *x, const float *y, const float *grad_y,
+                                 const int32_t *coords, int64_t n, int ncol, int C, int64_t B,
+                                 int mode, float *grad_x) {
+  int32_t *in_rows = (int32_t *)malloc(sizeof(int32_t) * (n > 0 ? n : 1));
+  int32_t *out_rows = (int32_t *)malloc(sizeof(int32_t) * (n > 0 ? n : 1));
+  int64_t P = 0;
+  for (int64_t r = 0; r < n; ++r)
+    if (coords[r * ncol] >= 0 && coords[r * ncol] < B) {
+      in_rows[P] = (int32_t)r;
+      out_rows[P++] = coords[r * ncol];
+    }
+  oracle_pool_backward(x, y, grad_y, n, B, C, in_rows, out_rows, P, mode, grad_x);
+  free(in_rows);
+  free(out_rows);
 }

@@ -4,8 +4,9 @@
 #
 # The reference sources are compiled where they lie (nothing is copied): the
 # coordinate manager (space.cpp), the stencil generator (stencil.cpp), the
-# convolution layer (conv.cpp) and SparseTensor (sparse_tensor.cpp), with
-# CPU_ONLY, against the LibTorch headers and libraries of the installed torch.
+# convolution and pooling layers (conv.cpp, pooling.cpp) and SparseTensor
+# (sparse_tensor.cpp), with CPU_ONLY, against the LibTorch headers and
+# libraries of the installed torch.
 # The only source of this repository in the library is ref_driver.cpp, which
 # calls the reference's public C++ API. Outputs go to oracle/_ref/ only.
 #
@@ -24,7 +25,7 @@ CXXFLAGS := -std=c++20 -O2 -fPIC -fopenmp -DCPU_ONLY -DRIEMANN_NO_PYBIND \
 LDFLAGS := -shared -fopenmp -L$(TORCH)/lib -ltorch -ltorch_cpu -lc10 \
 	-Wl,-rpath,$(TORCH)/lib -Wl,--no-undefined
 
-REF_SRCS := grid/space.cpp grid/stencil.cpp nn/conv.cpp tensor/sparse_tensor.cpp
+REF_SRCS := grid/space.cpp grid/stencil.cpp nn/conv.cpp nn/pooling.cpp tensor/sparse_tensor.cpp
 REF_OBJS := $(addprefix $(OUT)/,$(subst /,_,$(REF_SRCS:.cpp=.o)))
 
 all: $(OUT)/libriemann_ref.so

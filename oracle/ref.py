@@ -1,7 +1,8 @@
 """Test infrastructure only: ctypes access to the reference's own CPU path.
 
 oracle/ref.mk compiles the reference sources (RiemannEngine/engine/grid/
-space.cpp, stencil.cpp, nn/conv.cpp, tensor/sparse_tensor.cpp) with CPU_ONLY
+space.cpp, stencil.cpp, nn/conv.cpp, nn/pooling.cpp, tensor/sparse_tensor.cpp)
+with CPU_ONLY
 plus oracle/ref_driver.cpp into oracle/_ref/libriemann_ref.so. Tests use it to
 check the oracle and the HIP path against the reference itself; bench.py
 times it as the CPU baseline. ``available()`` is False where the library was
@@ -48,6 +49,14 @@ def lib():
         L.ref_stride_region.restype = _i64
         L.ref_stride_region.argtypes = [_vp, _i64, ctypes.c_int, ctypes.c_int, ctypes.c_int,
                                         ctypes.c_int, ctypes.c_int, ctypes.c_int, _i64, _vp]
+        L.ref_pool.restype = _i64
+        L.ref_pool.argtypes = [_vp, _i64, ctypes.c_int, ctypes.c_int, _vp, ctypes.c_int,
+                               ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                               ctypes.c_int, ctypes.c_int, ctypes.c_int, _vp, _i64, _vp, _vp,
+                               _vp]
+        L.ref_global_pool.restype = _i64
+        L.ref_global_pool.argtypes = [_vp, _i64, ctypes.c_int, _vp, ctypes.c_int, ctypes.c_int,
+                                      ctypes.c_int, _vp, _i64, _vp, _vp, _vp]
         L.ref_num_threads.restype = ctypes.c_int
         _LIB = L
     return _LIB
@@ -139,6 +148,51 @@ def stride_region(coords, in_stride, stride, ks, dilation=1, region="cube"):
     out = np.empty((max(m, 1), ncol), np.int32)
     _check(lib().ref_stride_region(*args, m, _p(out)))
     return out[:m]
+
+
+POOL_MODE = {"sum": 0, "avg": 1, "max": 2}
+
+
+def pool(coords, x, mode="avg", ks=2, stride=2, dilation=1, gy=None, in_stride=1,
+         transpose=False, expand=False, bf16=False):
+    """The reference's local pooling layer (RiemannSumPooling / AvgPooling /
+    MaxPooling, or RiemannPoolingTranspose with that mode) on the unique rows
+    `coords` at tensor stride in_stride with features x (row order of coords).
+    Returns (y, out_coords, gx); gy follows out_coords' row order, or is a
+    callable(out_coords) that builds it; gx is None without gy."""
+    c = np.ascontiguousarray(coords, np.int32)
+    n, ncol = c.shape
+    x = np.ascontiguousarray(x, np.float32)
+    C = x.shape[1]
+    args = (_p(c), n, ncol, in_stride, _p(x), C, ks, stride, dilation, POOL_MODE[mode],
+            int(transpose), int(expand), 1 if bf16 else 0)
+    n_out = _check(lib().ref_pool(*args, None, 0, None, None, None))
+    y = np.empty((max(n_out, 1), C), np.float32)
+    oc = np.empty((max(n_out, 1), ncol), np.int32)
+    if callable(gy):
+        _check(lib().ref_pool(*args, None, n_out, _p(y), _p(oc), None))
+        gy = gy(oc[:n_out])
+    g = None if gy is None else np.ascontiguousarray(gy, np.float32)
+    gx = np.empty((n, C), np.float32) if g is not None else None
+    _check(lib().ref_pool(*args, _p(g), n_out, _p(y), _p(oc), _p(gx)))
+    return y[:n_out], oc[:n_out], gx
+
+
+def global_pool(coords, x, mode="avg", gy=None, bf16=False):
+    """RiemannGlobalPooling (GLOBAL_*_POOLING_PYTORCH_INDEX) on the CPU.
+    Returns (y [B, C], out_coords [B, ncol], gx)."""
+    c = np.ascontiguousarray(coords, np.int32)
+    n, ncol = c.shape
+    x = np.ascontiguousarray(x, np.float32)
+    C = x.shape[1]
+    args = (_p(c), n, ncol, _p(x), C, POOL_MODE[mode], 1 if bf16 else 0)
+    B = _check(lib().ref_global_pool(*args, None, 0, None, None, None))
+    g = None if gy is None else np.ascontiguousarray(gy, np.float32)
+    y = np.empty((max(B, 1), C), np.float32)
+    oc = np.empty((max(B, 1), ncol), np.int32)
+    gx = np.empty((n, C), np.float32) if g is not None else None
+    _check(lib().ref_global_pool(*args, _p(g), B, _p(y), _p(oc), _p(gx)))
+    return y[:B], oc[:B], gx
 
 
 def num_threads() -> int:

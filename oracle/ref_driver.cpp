@@ -13,6 +13,7 @@
 // cap = 0 to learn the size.
 #include "engine/grid/space.hpp"
 #include "engine/nn/conv.hpp"
+#include "engine/nn/pooling.hpp"
 #include "engine/tensor/sparse_tensor.hpp"
 
 #include <torch/torch.h>
@@ -239,6 +240,90 @@ int64_t ref_conv_time(const int32_t *coords, int64_t n, int ncol, int cin, int c
     for (const auto &v : map.first)
       P += static_cast<int64_t>(v.size());
     return P;
+  });
+}
+
+// The reference's local pooling layers on the CPU (pooling.cpp:80-200):
+// RiemannSumPooling / RiemannAvgPooling / RiemannMaxPooling (mode 0 / 1 / 2)
+// with (ks, stride, dil), or, with transpose set, RiemannPoolingTranspose
+// through its KernelGenerator constructor with that mode and
+// expand_coordinates = expand. The input is the map of the unique rows
+// `coords` at tensor stride in_stride with features x [n, C] (row order of
+// `coords`), in fp32 (dtype 0) or bf16 (dtype 1). gy [n_out, C] in the
+// output's row order (may be NULL: forward only). Outputs are fp32: y
+// [n_out, C], out_coords [n_out, ncol], gx [n, C]; written when n_out <=
+// out_cap. Returns n_out.
+int64_t ref_pool(const int32_t *coords, int64_t n, int ncol, int in_stride, const float *x,
+                 int C, int ks, int stride, int dil, int mode, int transpose, int expand,
+                 int dtype, const float *gy, int64_t out_cap, float *y, int32_t *out_coords,
+                 float *gx) {
+  return guarded([&]() -> int64_t {
+    const int D = ncol - 1;
+    const auto dt = dtype == 1 ? torch::kBFloat16 : torch::kFloat32;
+    auto mgr = std::make_shared<riemann::CoordinateManager>(D, riemann::CoordinateMapBackend::CPU);
+    auto r = mgr->insert_and_map(int_rows(coords, n, ncol),
+                                 riemann::stride_type(static_cast<size_t>(D), in_stride));
+    TORCH_CHECK(r.second.first.numel() == n, "coordinates must be unique");
+    auto X = float_rows(x, n, C).to(dt).detach().requires_grad_(true);
+    riemann::SparseTensor input(X.index_select(0, r.second.first.to(torch::kLong)), r.first, mgr);
+    const riemann::PoolingMode::Type pm =
+        mode == 0 ? riemann::PoolingMode::LOCAL_SUM_POOLING
+                  : (mode == 1 ? riemann::PoolingMode::LOCAL_AVG_POOLING
+                               : riemann::PoolingMode::LOCAL_MAX_POOLING);
+    riemann::SparseTensor out = [&] {
+      if (transpose) {
+        riemann::KernelGenerator gen({ks}, {stride}, {dil}, true, riemann::RegionType::HYPER_CUBE,
+                                     {}, expand != 0, {}, D);
+        riemann::RiemannPoolingTranspose layer(gen, D, pm);
+        return layer->forward(input);
+      }
+      if (mode == 0)
+        return riemann::RiemannSumPooling(ks, stride, dil, D)->forward(input);
+      if (mode == 1)
+        return riemann::RiemannAvgPooling(ks, stride, dil, D)->forward(input);
+      return riemann::RiemannMaxPooling(ks, stride, dil, D)->forward(input);
+    }();
+    const int64_t n_out = out.F().size(0);
+    if (n_out > out_cap)
+      return n_out;
+    copy_out(out.F().detach().to(torch::kFloat32), y);
+    copy_out(mgr->get_coordinates(out.coordinate_map_key()).to(torch::kInt32), out_coords);
+    if (gy != nullptr) {
+      out.F().backward(float_rows(gy, n_out, C).to(dt));
+      copy_out(X.grad().to(torch::kFloat32), gx);
+    }
+    return n_out;
+  });
+}
+
+// RiemannGlobalPooling (pooling.cpp:203-260) with the GLOBAL_{SUM,AVG,MAX}_
+// POOLING_PYTORCH_INDEX mode (mode 0 / 1 / 2) over the rows `coords` with
+// features x [n, C]. Same conventions as ref_pool. Returns the batch count.
+int64_t ref_global_pool(const int32_t *coords, int64_t n, int ncol, const float *x, int C,
+                        int mode, int dtype, const float *gy, int64_t out_cap, float *y,
+                        int32_t *out_coords, float *gx) {
+  return guarded([&]() -> int64_t {
+    const int D = ncol - 1;
+    const auto dt = dtype == 1 ? torch::kBFloat16 : torch::kFloat32;
+    auto mgr = std::make_shared<riemann::CoordinateManager>(D, riemann::CoordinateMapBackend::CPU);
+    auto X = float_rows(x, n, C).to(dt).detach().requires_grad_(true);
+    riemann::SparseTensor input(X, int_rows(coords, n, ncol), mgr);
+    const riemann::PoolingMode::Type pm =
+        mode == 0 ? riemann::PoolingMode::GLOBAL_SUM_POOLING_PYTORCH_INDEX
+                  : (mode == 1 ? riemann::PoolingMode::GLOBAL_AVG_POOLING_PYTORCH_INDEX
+                               : riemann::PoolingMode::GLOBAL_MAX_POOLING_PYTORCH_INDEX);
+    riemann::RiemannGlobalPooling layer(pm);
+    auto out = layer->forward(input);
+    const int64_t B = out.F().size(0);
+    if (B > out_cap)
+      return B;
+    copy_out(out.F().detach().to(torch::kFloat32), y);
+    copy_out(mgr->get_coordinates(out.coordinate_map_key()).to(torch::kInt32), out_coords);
+    if (gy != nullptr) {
+      out.F().backward(float_rows(gy, B, C).to(dt));
+      copy_out(X.grad().to(torch::kFloat32), gx);
+    }
+    return B;
   });
 }
 

@@ -1,7 +1,8 @@
 """MI355X-native sparse-convolution hot path of RiemannEngine.
 
-Coordinate hashing, kernel-map generation and gather-GEMM-scatter sparse
-convolution (forward, dX, dW) as hand-written gfx950 HIP kernels behind the C
+Coordinate hashing, kernel-map generation, gather-GEMM-scatter sparse
+convolution (forward, dX, dW) and sparse pooling (stride maps, local and
+global sum / average / max) as hand-written gfx950 HIP kernels behind the C
 ABI in include/riemann_hip.h (libriemann_hip.so).
 
 * ``SparseTensor``, ``CoordinateManager``, ``CoordinateMapKey``, ``nn`` and
@@ -19,7 +20,7 @@ __version__ = "0.1.0"
 
 _HOST_NAMES = ("SparseTensor", "CoordinateManager", "CoordinateMapKey", "QuantizationMode",
                "CoordinateMapBackend", "RiemannAlgorithm", "RegionType", "ConvolutionMode",
-               "region_offsets", "nn")
+               "PoolingMode", "region_offsets", "nn")
 
 
 def __getattr__(name):

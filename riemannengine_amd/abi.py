@@ -22,6 +22,8 @@ MAX_COLS = 8
 F32, BF16 = 0, 1
 KEY_PACKED64, KEY_ROWREF = 0, 1
 KMAP_SYMMETRIC = 1
+POOL_SUM, POOL_AVG, POOL_MAX = 0, 1, 2
+POOL_MODES = {"sum": POOL_SUM, "avg": POOL_AVG, "max": POOL_MAX}
 
 # Every function the header declares (checked by the CPU test suite).
 EXPORTS = (
@@ -31,6 +33,10 @@ EXPORTS = (
     "rhip_expand_coords", "rhip_kmap_workspace_bytes", "rhip_kmap_count", "rhip_kmap_fill",
     "rhip_conv_workspace_bytes", "rhip_conv_forward",
     "rhip_conv_backward_input", "rhip_conv_backward_weight",
+    "rhip_stride_map_workspace_bytes", "rhip_stride_map_count", "rhip_stride_map_fill",
+    "rhip_pool_workspace_bytes", "rhip_pool_forward", "rhip_pool_backward",
+    "rhip_global_pool_workspace_bytes", "rhip_batch_count", "rhip_batch_segments",
+    "rhip_global_pool_forward", "rhip_global_pool_backward",
 )
 
 
@@ -78,6 +84,25 @@ def _declare(lib):
         "rhip_conv_backward_weight": (ctypes.c_int, [_vp, _i64, _i32, _vp, _i64, _i32,
                                                      _i32, _vp, _i64, _vp, _vp, _vp,
                                                      _i32, _vp, _sz, _vp]),
+        "rhip_stride_map_workspace_bytes": (ctypes.c_int, [_i64, _i64, _P(_sz)]),
+        "rhip_stride_map_count": (ctypes.c_int, [_P(RhipTable), _vp, _i64, _P(_i32), _vp, _sz,
+                                                 _P(_i32), _vp]),
+        "rhip_stride_map_fill": (ctypes.c_int, [_i64, _i64, _i32, _vp, _vp, _vp, _sz, _vp, _vp,
+                                                _vp, _vp, _vp]),
+        "rhip_pool_workspace_bytes": (ctypes.c_int, [_i64, _i32, _i32, _P(_sz)]),
+        "rhip_pool_forward": (ctypes.c_int, [_vp, _i64, _i32, _vp, _i32, _vp, _i64, _i32, _vp,
+                                             _vp, _i32, _vp]),
+        "rhip_pool_backward": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i32, _vp, _vp, _vp, _i32,
+                                              _vp, _i64, _vp, _i32, _vp, _i32, _vp, _sz, _vp]),
+        "rhip_global_pool_workspace_bytes": (ctypes.c_int, [_i64, _i32, _i32, _P(_sz)]),
+        "rhip_batch_count": (ctypes.c_int, [_vp, _i64, _i32, _vp, _sz, _P(_i32), _vp]),
+        "rhip_batch_segments": (ctypes.c_int, [_vp, _i64, _i32, _i32, _vp, _sz, _vp, _vp,
+                                               _vp]),
+        "rhip_global_pool_forward": (ctypes.c_int, [_vp, _i64, _i32, _vp, _vp, _i32, _i32,
+                                                    _vp, _i32, _vp, _sz, _vp]),
+        "rhip_global_pool_backward": (ctypes.c_int, [_vp, _vp, _vp, _vp, _i32, _i64, _i32,
+                                                     _vp, _vp, _i32, _i32, _vp, _i32, _vp,
+                                                     _sz, _vp]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -364,3 +389,138 @@ def conv_backward_weight(x: torch.Tensor, grad_y: torch.Tensor, kmap: KernelMap,
                                            dt, _ptr(ws), ws.numel(), _stream(x.device)),
            "rhip_conv_backward_weight")
     return gw if out_dtype is None else gw.to(out_dtype)
+
+
+# ---------------------------------------------------------------- pooling
+
+def stride_map(in_table: CoordTable, out_table: CoordTable, out_tensor_stride) -> KernelMap:
+    """Pooling stride map (kernel size == stride): every input row onto the
+    output row of its floor-aligned coordinates, in the neighbour-table form
+    (K = largest number of inputs on one output). The pair list is the
+    reference's single offset: offsets = [0, P, ..., P]."""
+    L = lib()
+    dev = in_table.ucoords.device
+    n_in, n_out = in_table.n, out_table.n
+    s = (ctypes.c_int32 * MAX_COLS)(*[int(v) for v in out_tensor_stride])
+    st = _stream(dev)
+    ws = torch.empty(_sizeq(L.rhip_stride_map_workspace_bytes, n_in, n_out), dtype=torch.uint8,
+                     device=dev)
+    kmax = ctypes.c_int32(0)
+    _check(L.rhip_stride_map_count(ctypes.byref(out_table.struct), _ptr(in_table.ucoords), n_in,
+                                   s, _ptr(ws), ws.numel(), ctypes.byref(kmax), st),
+           "rhip_stride_map_count")
+    K = max(int(kmax.value), 1)
+    # phase 2 writes every entry of the tables (-1 where no input lies)
+    table = torch.empty if kmax.value > 0 else (lambda *a, **k: torch.full(*a, -1, **k))
+    nbr = table((K, max(n_out, 1)), dtype=torch.int32, device=dev)
+    nbr_t = table((K, max(n_in, 1)), dtype=torch.int32, device=dev)
+    in_rows = torch.empty(max(n_in, 1), dtype=torch.int32, device=dev)
+    out_rows = torch.empty(max(n_in, 1), dtype=torch.int32, device=dev)
+    _check(L.rhip_stride_map_fill(n_in, n_out, int(kmax.value), _ptr(in_table.order),
+                                  _ptr(out_table.order), _ptr(ws), ws.numel(), _ptr(nbr),
+                                  _ptr(nbr_t), _ptr(in_rows), _ptr(out_rows), st),
+           "rhip_stride_map_fill")
+    kofs_host = np.full(K + 1, n_in, dtype=np.int64)
+    kofs_host[0] = 0
+    return KernelMap(K, n_in, n_out, torch.as_tensor(kofs_host).to(dev), kofs_host,
+                     in_rows[:n_in], out_rows[:n_in], nbr[:, :n_out], nbr_t[:, :n_in],
+                     in_table.order, out_table.order)
+
+
+def _pool_mode(mode) -> int:
+    if isinstance(mode, str):
+        return POOL_MODES[mode]
+    return int(mode)
+
+
+def pool_forward(x: torch.Tensor, kmap: KernelMap, mode="avg"):
+    """(y [n_out, C], counts [n_out]) of local pooling over kmap.nbr."""
+    _require_cuda(x, "x")
+    dt = _dtype_code(x.dtype)
+    x = x.contiguous()
+    if x.shape[0] != kmap.n_in:
+        raise RuntimeError("features do not match the map's input rows")
+    C = x.shape[1]
+    y = torch.empty((kmap.n_out, C), dtype=x.dtype, device=x.device)
+    counts = torch.empty(max(kmap.n_out, 1), dtype=torch.int32, device=x.device)
+    _check(lib().rhip_pool_forward(_ptr(x), kmap.n_in, C, _ptr(kmap.nbr), kmap.K,
+                                   _ptr(kmap.out_order), kmap.n_out, _pool_mode(mode), _ptr(y),
+                                   _ptr(counts), dt, _stream(x.device)), "rhip_pool_forward")
+    return y, counts[:kmap.n_out]
+
+
+def pool_backward(grad_y: torch.Tensor, y: torch.Tensor, x: torch.Tensor, kmap: KernelMap,
+                  counts: torch.Tensor, mode="avg") -> torch.Tensor:
+    _require_cuda(grad_y, "grad_y")
+    dt = _dtype_code(x.dtype)
+    m = _pool_mode(mode)
+    grad_y, y, x = grad_y.to(x.dtype).contiguous(), y.contiguous(), x.contiguous()
+    C = x.shape[1]
+    gx = torch.empty((kmap.n_in, C), dtype=x.dtype, device=x.device)
+    ws = torch.empty(_sizeq(lib().rhip_pool_workspace_bytes, kmap.n_out, C, m),
+                     dtype=torch.uint8, device=x.device)
+    _check(lib().rhip_pool_backward(_ptr(grad_y), _ptr(y), _ptr(x), kmap.n_out, C,
+                                    _ptr(kmap.nbr), _ptr(kmap.out_order), _ptr(kmap.nbr_t), kmap.K,
+                                    _ptr(kmap.in_order), kmap.n_in, _ptr(counts), m, _ptr(gx),
+                                    dt, _ptr(ws), ws.numel(), _stream(x.device)),
+           "rhip_pool_backward")
+    return gx
+
+
+@dataclass
+class BatchSegments:
+    """Rows grouped by batch: rows of batch b are members[seg[b]:seg[b+1]]."""
+    n_batches: int
+    members: torch.Tensor
+    seg: torch.Tensor
+
+
+def batch_segments(coords: torch.Tensor) -> BatchSegments:
+    _require_cuda(coords, "coords")
+    L = lib()
+    coords = coords.to(torch.int32).contiguous()
+    n, ncol = coords.shape
+    dev = coords.device
+    ws = torch.empty(_sizeq(L.rhip_global_pool_workspace_bytes, n, 1, 0), dtype=torch.uint8,
+                     device=dev)
+    B = ctypes.c_int32(0)
+    _check(L.rhip_batch_count(_ptr(coords), n, ncol, _ptr(ws), ws.numel(), ctypes.byref(B),
+                              _stream(dev)), "rhip_batch_count")
+    members = torch.empty(max(n, 1), dtype=torch.int32, device=dev)
+    seg = torch.empty(B.value + 1, dtype=torch.int32, device=dev)
+    _check(L.rhip_batch_segments(_ptr(coords), n, ncol, B.value, _ptr(ws), ws.numel(),
+                                 _ptr(members), _ptr(seg), _stream(dev)), "rhip_batch_segments")
+    return BatchSegments(int(B.value), members[:n], seg)
+
+
+def global_pool_forward(x: torch.Tensor, segs: BatchSegments, mode="avg") -> torch.Tensor:
+    _require_cuda(x, "x")
+    dt = _dtype_code(x.dtype)
+    x = x.contiguous()
+    n, C = x.shape
+    y = torch.empty((segs.n_batches, C), dtype=x.dtype, device=x.device)
+    ws = torch.empty(_sizeq(lib().rhip_global_pool_workspace_bytes, n, C, segs.n_batches),
+                     dtype=torch.uint8, device=x.device)
+    _check(lib().rhip_global_pool_forward(_ptr(x), n, C, _ptr(segs.members), _ptr(segs.seg),
+                                          segs.n_batches, _pool_mode(mode), _ptr(y), dt,
+                                          _ptr(ws), ws.numel(), _stream(x.device)),
+           "rhip_global_pool_forward")
+    return y
+
+
+def global_pool_backward(grad_y: torch.Tensor, y: torch.Tensor, x: torch.Tensor,
+                         coords: torch.Tensor, segs: BatchSegments, mode="avg") -> torch.Tensor:
+    _require_cuda(x, "x")
+    dt = _dtype_code(x.dtype)
+    grad_y, y, x = grad_y.to(x.dtype).contiguous(), y.contiguous(), x.contiguous()
+    coords = coords.to(torch.int32).contiguous()
+    n, C = x.shape
+    gx = torch.empty((n, C), dtype=x.dtype, device=x.device)
+    ws = torch.empty(_sizeq(lib().rhip_global_pool_workspace_bytes, n, C, segs.n_batches),
+                     dtype=torch.uint8, device=x.device)
+    _check(lib().rhip_global_pool_backward(_ptr(grad_y), _ptr(y), _ptr(x), _ptr(coords),
+                                           coords.shape[1], n, C, _ptr(segs.members),
+                                           _ptr(segs.seg), segs.n_batches, _pool_mode(mode),
+                                           _ptr(gx), dt, _ptr(ws), ws.numel(),
+                                           _stream(x.device)), "rhip_global_pool_backward")
+    return gx

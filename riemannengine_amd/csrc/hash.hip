@@ -272,18 +272,6 @@ __global__ __launch_bounds__(kBlock) void invert_perm_kernel(int64_t n,
     pos[order[i]] = static_cast<int32_t>(i);
 }
 
-// floor(a / s) * s for s > 0, exact in integers.
-__device__ __forceinline__ int32_t floor_align(int32_t a, int32_t s) {
-  int32_t q = a / s;
-  if ((a % s) != 0 && a < 0)
-    --q;
-  return q * s;
-}
-
-struct StrideArg {
-  int32_t s[RHIP_MAX_COLS];
-};
-
 __global__ __launch_bounds__(kBlock) void stride_kernel(const int32_t *in,
                                                         int64_t n, int ncol,
                                                         StrideArg st,

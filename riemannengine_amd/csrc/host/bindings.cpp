@@ -12,6 +12,7 @@ using namespace riemann;
 namespace {
 
 template <typename Impl> using ModuleClass = py::class_<Impl, std::shared_ptr<Impl>>;
+template <typename T> struct type_tag { using type = T; };
 
 // torch_python registers torch::nn::Module itself, so the layers expose the
 // module surface they need directly.
@@ -67,6 +68,7 @@ py::dict kernel_map_dict(const HipKernelMap &m) {
   d["nbr_t"] = m.nbr_t;
   d["in_order"] = m.in_order;
   d["out_order"] = m.out_order;
+  d["stride_map"] = m.stride_map;
   return d;
 }
 
@@ -105,6 +107,19 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
       .value("DEFAULT", ConvolutionMode::DEFAULT)
       .value("DIRECT_GEMM", ConvolutionMode::DIRECT_GEMM)
       .value("COPY_GEMM", ConvolutionMode::COPY_GEMM);
+  py::enum_<PoolingMode::Type>(m, "PoolingMode")
+      .value("LOCAL_SUM_POOLING", PoolingMode::LOCAL_SUM_POOLING)
+      .value("LOCAL_AVG_POOLING", PoolingMode::LOCAL_AVG_POOLING)
+      .value("LOCAL_MAX_POOLING", PoolingMode::LOCAL_MAX_POOLING)
+      .value("GLOBAL_SUM_POOLING_DEFAULT", PoolingMode::GLOBAL_SUM_POOLING_DEFAULT)
+      .value("GLOBAL_AVG_POOLING_DEFAULT", PoolingMode::GLOBAL_AVG_POOLING_DEFAULT)
+      .value("GLOBAL_MAX_POOLING_DEFAULT", PoolingMode::GLOBAL_MAX_POOLING_DEFAULT)
+      .value("GLOBAL_SUM_POOLING_KERNEL", PoolingMode::GLOBAL_SUM_POOLING_KERNEL)
+      .value("GLOBAL_AVG_POOLING_KERNEL", PoolingMode::GLOBAL_AVG_POOLING_KERNEL)
+      .value("GLOBAL_MAX_POOLING_KERNEL", PoolingMode::GLOBAL_MAX_POOLING_KERNEL)
+      .value("GLOBAL_SUM_POOLING_PYTORCH_INDEX", PoolingMode::GLOBAL_SUM_POOLING_PYTORCH_INDEX)
+      .value("GLOBAL_AVG_POOLING_PYTORCH_INDEX", PoolingMode::GLOBAL_AVG_POOLING_PYTORCH_INDEX)
+      .value("GLOBAL_MAX_POOLING_PYTORCH_INDEX", PoolingMode::GLOBAL_MAX_POOLING_PYTORCH_INDEX);
 
   m.def(
       "region_offsets",
@@ -290,6 +305,48 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   bind_unary<RiemannReLUImpl>(nn, "RiemannReLU")
       .def(py::init([](bool inplace) { return std::make_shared<RiemannReLUImpl>(inplace); }),
            py::arg("inplace") = false);
+  // pooling (python/src/nn_bindings.cpp:344-403)
+  auto local_pool = [&](auto tag, const char *name) {
+    using Impl = typename decltype(tag)::type;
+    bind_unary<Impl>(nn, name)
+        .def(py::init([](int kernel_size, int stride, int dilation, int dimension) {
+               return std::make_shared<Impl>(kernel_size, stride, dilation, dimension);
+             }),
+             py::arg("kernel_size"), py::arg("stride") = 1, py::arg("dilation") = 1,
+             py::arg("dimension") = 3);
+  };
+  local_pool(type_tag<RiemannAvgPoolingImpl>{}, "RiemannAvgPooling");
+  local_pool(type_tag<RiemannSumPoolingImpl>{}, "RiemannSumPooling");
+  local_pool(type_tag<RiemannMaxPoolingImpl>{}, "RiemannMaxPooling");
+  bind_unary<RiemannPoolingTransposeImpl>(nn, "RiemannPoolingTranspose")
+      .def(py::init([](int kernel_size, int stride, int dilation, bool expand_coordinates,
+                       int dimension) {
+             return std::make_shared<RiemannPoolingTransposeImpl>(
+                 kernel_size, stride, dilation, expand_coordinates, dimension);
+           }),
+           py::arg("kernel_size"), py::arg("stride"), py::arg("dilation") = 1,
+           py::arg("expand_coordinates") = false, py::arg("dimension") = 3)
+      .def(py::init([](int kernel_size, int stride, int dilation, bool expand_coordinates,
+                       int dimension, PoolingMode::Type mode) {
+             return std::make_shared<RiemannPoolingTransposeImpl>(
+                 KernelGenerator({kernel_size}, {stride}, {dilation}, true,
+                                 RegionType::HYPER_CUBE, {}, expand_coordinates, dimension),
+                 dimension, mode);
+           }),
+           py::arg("kernel_size"), py::arg("stride"), py::arg("dilation"),
+           py::arg("expand_coordinates"), py::arg("dimension"), py::arg("mode"));
+  bind_unary<RiemannGlobalPoolingImpl>(nn, "RiemannGlobalPooling")
+      .def(py::init([](PoolingMode::Type mode) {
+             return std::make_shared<RiemannGlobalPoolingImpl>(mode);
+           }),
+           py::arg("mode") = PoolingMode::GLOBAL_AVG_POOLING_PYTORCH_INDEX);
+  bind_unary<RiemannGlobalSumPoolingImpl>(nn, "RiemannGlobalSumPooling")
+      .def(py::init([]() { return std::make_shared<RiemannGlobalSumPoolingImpl>(); }));
+  bind_unary<RiemannGlobalAvgPoolingImpl>(nn, "RiemannGlobalAvgPooling")
+      .def(py::init([]() { return std::make_shared<RiemannGlobalAvgPoolingImpl>(); }));
+  bind_unary<RiemannGlobalMaxPoolingImpl>(nn, "RiemannGlobalMaxPooling")
+      .def(py::init([]() { return std::make_shared<RiemannGlobalMaxPoolingImpl>(); }));
+
   bind_unary<BasicBlockImpl>(nn, "BasicBlock")
       .def(py::init([](int inplanes, int planes, int stride, int dilation, double bn_momentum,
                        int dimension) {

@@ -15,6 +15,8 @@
 //   RiemannBatchNorm, BasicBlock
 //                               RiemannEngine/engine/nn/normalization.hpp:11-37,
 //                               residual.hpp:12-29
+//   Riemann{Sum,Avg,Max}Pooling, RiemannPoolingTranspose, RiemannGlobal*Pooling
+//                               RiemannEngine/engine/nn/pooling.hpp:11-131
 // Only the device (HIP) backend exists here: a CPU coordinate manager or CPU
 // coordinates raise an error instead of falling back to another path.
 #pragma once
@@ -63,6 +65,22 @@ enum Type { HYPER_CUBE, HYPER_CROSS, CUSTOM };
 }
 namespace ConvolutionMode {
 enum Type { DEFAULT, DIRECT_GEMM, COPY_GEMM };
+}
+namespace PoolingMode {
+enum Type {
+  LOCAL_SUM_POOLING,
+  LOCAL_AVG_POOLING,
+  LOCAL_MAX_POOLING,
+  GLOBAL_SUM_POOLING_DEFAULT,
+  GLOBAL_AVG_POOLING_DEFAULT,
+  GLOBAL_MAX_POOLING_DEFAULT,
+  GLOBAL_SUM_POOLING_KERNEL,
+  GLOBAL_AVG_POOLING_KERNEL,
+  GLOBAL_MAX_POOLING_KERNEL,
+  GLOBAL_SUM_POOLING_PYTORCH_INDEX,
+  GLOBAL_AVG_POOLING_PYTORCH_INDEX,
+  GLOBAL_MAX_POOLING_PYTORCH_INDEX
+};
 }
 
 // (in key, out key, kernel size, kernel stride, dilation, region type,
@@ -170,9 +188,12 @@ struct CoordinateMapHIP {
 };
 
 // A kernel map: per-offset pair lists (CSR) plus the dense neighbour tables
-// and processing orders the convolution kernels consume.
+// and processing orders the convolution kernels consume. A pooling stride map
+// (stride_map set) has the reference's single pair list (offsets = [0, P, ...,
+// P]) and neighbour tables K rows high, K = most inputs on one output.
 struct HipKernelMap {
   int32_t K = 0;
+  bool stride_map = false;
   int64_t n_in = 0, n_out = 0;
   std::vector<int64_t> offsets_host; // [K+1]
   at::Tensor offsets;                // device int64 [K+1]
@@ -247,6 +268,10 @@ private:
                              at::Tensor *mapping, at::Tensor *inverse) const;
   HipKernelMap generate(const CoordinateMapHIP &in_map, const CoordinateMapHIP &out_map,
                         const at::Tensor &offsets_host) const;
+  // Every in_map row onto the out_map row of its floor-aligned coordinates
+  // (CoordinateMapCPU::stride_map, engine/grid/lattice_cpu.hpp:675-710).
+  HipKernelMap generate_stride_map(const CoordinateMapHIP &in_map,
+                                   const CoordinateMapHIP &out_map) const;
 
   int D_;
   CoordinateMapBackend::Type backend_;
@@ -370,8 +395,8 @@ private:
 };
 TORCH_MODULE(RiemannConvolutionTranspose);
 
-// As in the reference (engine/nn/conv.cpp:104-138, 173-182), the generative
-// flag is stored but the output coordinates are the existing finer map.
+// Transposed convolution whose output map is generated from the input
+// through the kernel region (CoordinateManager::stride_region).
 class RiemannGenerativeConvolutionTransposeImpl
     : public torch::nn::Cloneable<RiemannGenerativeConvolutionTransposeImpl> {
 public:
@@ -423,6 +448,110 @@ private:
   bool inplace_;
 };
 TORCH_MODULE(RiemannReLU);
+
+// ---------------------------------------------------------------- pooling
+
+// Local pooling of features over a kernel or stride map through the HIP
+// kernels (autograd-aware): mode LOCAL_{SUM,AVG,MAX}_POOLING.
+at::Tensor hip_sparse_pooling(const at::Tensor &features, const HipKernelMap &map,
+                              PoolingMode::Type mode);
+
+class RiemannPoolingBaseImpl : public torch::nn::Cloneable<RiemannPoolingBaseImpl> {
+public:
+  RiemannPoolingBaseImpl(int kernel_size, int stride = 1, int dilation = 1,
+                         PoolingMode::Type mode = PoolingMode::LOCAL_AVG_POOLING,
+                         int dimension = 3);
+  RiemannPoolingBaseImpl(KernelGenerator kernel_generator, PoolingMode::Type mode, int dimension);
+  void reset() override {}
+  SparseTensor forward(const SparseTensor &input);
+
+private:
+  KernelGenerator kernel_generator_;
+  PoolingMode::Type mode_;
+  int dimension_;
+};
+TORCH_MODULE(RiemannPoolingBase);
+
+// RiemannSumPooling / RiemannAvgPooling / RiemannMaxPooling: the base layer
+// with its mode fixed (engine/nn/pooling.hpp:26-63).
+template <PoolingMode::Type Mode>
+class RiemannLocalPoolingImpl : public torch::nn::Cloneable<RiemannLocalPoolingImpl<Mode>> {
+public:
+  RiemannLocalPoolingImpl(int kernel_size, int stride = 1, int dilation = 1, int dimension = 3)
+      : kernel_size_(kernel_size), stride_(stride), dilation_(dilation), dimension_(dimension) {
+    reset();
+  }
+  void reset() override {
+    pooling_ = this->register_module(
+        "pooling", RiemannPoolingBase(kernel_size_, stride_, dilation_, Mode, dimension_));
+  }
+  SparseTensor forward(const SparseTensor &input) { return pooling_->forward(input); }
+
+private:
+  int kernel_size_, stride_, dilation_, dimension_;
+  RiemannPoolingBase pooling_{nullptr};
+};
+using RiemannSumPoolingImpl = RiemannLocalPoolingImpl<PoolingMode::LOCAL_SUM_POOLING>;
+using RiemannAvgPoolingImpl = RiemannLocalPoolingImpl<PoolingMode::LOCAL_AVG_POOLING>;
+using RiemannMaxPoolingImpl = RiemannLocalPoolingImpl<PoolingMode::LOCAL_MAX_POOLING>;
+TORCH_MODULE(RiemannSumPooling);
+TORCH_MODULE(RiemannAvgPooling);
+TORCH_MODULE(RiemannMaxPooling);
+
+// Unpooling onto a generated finer map (engine/nn/pooling.hpp:65-81,
+// pooling.cpp:188-201); the output map is built from the input through the
+// kernel region at the output stride.
+class RiemannPoolingTransposeImpl : public torch::nn::Cloneable<RiemannPoolingTransposeImpl> {
+public:
+  RiemannPoolingTransposeImpl(int kernel_size, int stride, int dilation = 1,
+                              bool expand_coordinates = false, int dimension = 3);
+  RiemannPoolingTransposeImpl(KernelGenerator kernel_generator, int dimension,
+                              PoolingMode::Type mode = PoolingMode::LOCAL_SUM_POOLING);
+  void reset() override {}
+  SparseTensor forward(const SparseTensor &input);
+
+private:
+  KernelGenerator kernel_generator_;
+  int dimension_;
+  PoolingMode::Type mode_ = PoolingMode::LOCAL_SUM_POOLING;
+};
+TORCH_MODULE(RiemannPoolingTranspose);
+
+// One output row per batch index 0 .. max batch (engine/nn/pooling.hpp:83-131,
+// pooling.cpp:203-260).
+class RiemannGlobalPoolingImpl : public torch::nn::Cloneable<RiemannGlobalPoolingImpl> {
+public:
+  explicit RiemannGlobalPoolingImpl(
+      PoolingMode::Type mode = PoolingMode::GLOBAL_AVG_POOLING_PYTORCH_INDEX);
+  void reset() override {}
+  SparseTensor forward(const SparseTensor &input);
+
+private:
+  PoolingMode::Type mode_;
+};
+TORCH_MODULE(RiemannGlobalPooling);
+
+template <PoolingMode::Type Mode>
+class RiemannGlobalModePoolingImpl
+    : public torch::nn::Cloneable<RiemannGlobalModePoolingImpl<Mode>> {
+public:
+  explicit RiemannGlobalModePoolingImpl(PoolingMode::Type mode = Mode) : mode_(mode) { reset(); }
+  void reset() override { pooling_ = this->register_module("pooling", RiemannGlobalPooling(mode_)); }
+  SparseTensor forward(const SparseTensor &input) { return pooling_->forward(input); }
+
+private:
+  PoolingMode::Type mode_;
+  RiemannGlobalPooling pooling_{nullptr};
+};
+using RiemannGlobalSumPoolingImpl =
+    RiemannGlobalModePoolingImpl<PoolingMode::GLOBAL_SUM_POOLING_PYTORCH_INDEX>;
+using RiemannGlobalAvgPoolingImpl =
+    RiemannGlobalModePoolingImpl<PoolingMode::GLOBAL_AVG_POOLING_PYTORCH_INDEX>;
+using RiemannGlobalMaxPoolingImpl =
+    RiemannGlobalModePoolingImpl<PoolingMode::GLOBAL_MAX_POOLING_PYTORCH_INDEX>;
+TORCH_MODULE(RiemannGlobalSumPooling);
+TORCH_MODULE(RiemannGlobalAvgPooling);
+TORCH_MODULE(RiemannGlobalMaxPooling);
 
 // conv3 -> BN -> ReLU -> conv3 -> BN -> (+ residual) -> ReLU
 // (RiemannEngine/engine/nn/residual.cpp:16-52)

@@ -243,6 +243,7 @@ KernelGenerator::KernelParams KernelGenerator::get_kernel(const stride_type &ten
 HipKernelMap HipKernelMap::swapped() const {
   HipKernelMap m;
   m.K = K;
+  m.stride_map = stride_map;
   m.n_in = n_out;
   m.n_out = n_in;
   m.offsets_host = offsets_host;
@@ -258,7 +259,7 @@ HipKernelMap HipKernelMap::swapped() const {
 
 std::pair<std::vector<at::Tensor>, std::vector<at::Tensor>> HipKernelMap::per_offset() const {
   std::vector<at::Tensor> ins, outs;
-  for (int k = 0; k < K; ++k) {
+  for (int k = 0; k < (stride_map ? 1 : K); ++k) {
     const int64_t a = offsets_host[k], b = offsets_host[k + 1];
     ins.push_back(in_rows.slice(0, a, b).to(torch::kLong));
     outs.push_back(out_rows.slice(0, a, b).to(torch::kLong));
@@ -487,6 +488,53 @@ HipKernelMap CoordinateManager::generate(const CoordinateMapHIP &in_map,
   return m;
 }
 
+HipKernelMap CoordinateManager::generate_stride_map(const CoordinateMapHIP &in_map,
+                                                    const CoordinateMapHIP &out_map) const {
+  const auto dev = in_map.coords.device();
+  at::DeviceGuard guard(dev);
+  const hipStream_t st = current_stream(dev);
+  const int64_t n_in = in_map.size(), n_out = out_map.size();
+  auto iopt = torch::TensorOptions().device(dev).dtype(torch::kInt32);
+  std::vector<int32_t> s(out_map.tensor_stride.begin(), out_map.tensor_stride.end());
+  size_t ws_bytes = 0;
+  check_rhip(rhip_stride_map_workspace_bytes(n_in, n_out, &ws_bytes),
+             "rhip_stride_map_workspace_bytes");
+  auto ws = device_bytes(ws_bytes, dev);
+  int32_t kmax = 0;
+  check_rhip(rhip_stride_map_count(&out_map.table, in_map.coords.data_ptr<int32_t>(), n_in,
+                                   s.data(), ws.data_ptr(), ws.numel(), &kmax, st),
+             "rhip_stride_map_count");
+  HipKernelMap m;
+  m.stride_map = true;
+  m.K = std::max<int32_t>(kmax, 1);
+  m.n_in = n_in;
+  m.n_out = n_out;
+  // phase 2 writes every entry of the tables (-1 where no input lies)
+  auto table = [&](int64_t cols) {
+    return kmax > 0 ? torch::empty({m.K, std::max<int64_t>(cols, 1)}, iopt)
+                    : torch::full({m.K, std::max<int64_t>(cols, 1)}, -1, iopt);
+  };
+  auto nbr = table(n_out);
+  auto nbr_t = table(n_in);
+  auto in_rows = torch::empty({std::max<int64_t>(n_in, 1)}, iopt);
+  auto out_rows = torch::empty({std::max<int64_t>(n_in, 1)}, iopt);
+  check_rhip(rhip_stride_map_fill(n_in, n_out, kmax, in_map.order.data_ptr<int32_t>(),
+                                  out_map.order.data_ptr<int32_t>(), ws.data_ptr(), ws.numel(),
+                                  nbr.data_ptr<int32_t>(), nbr_t.data_ptr<int32_t>(),
+                                  in_rows.data_ptr<int32_t>(), out_rows.data_ptr<int32_t>(), st),
+             "rhip_stride_map_fill");
+  m.offsets_host.assign(m.K + 1, n_in);
+  m.offsets_host[0] = 0;
+  m.offsets = torch::tensor(m.offsets_host, torch::kInt64).to(dev);
+  m.in_rows = in_rows.slice(0, 0, n_in);
+  m.out_rows = out_rows.slice(0, 0, n_in);
+  m.nbr = nbr.slice(1, 0, n_out);
+  m.nbr_t = nbr_t.slice(1, 0, n_in);
+  m.in_order = in_map.order;
+  m.out_order = out_map.order;
+  return m;
+}
+
 const HipKernelMap &CoordinateManager::kernel_map(
     const CoordinateMapKey &in_key, const CoordinateMapKey &out_key,
     const stride_type &kernel_size, const stride_type &kernel_stride,
@@ -495,8 +543,10 @@ const HipKernelMap &CoordinateManager::kernel_map(
   const size_t kdim = kernel_size.size();
   TORCH_CHECK(kdim == kernel_stride.size(), "kernel size mismatch");
   TORCH_CHECK(kdim == kernel_dilation.size(), "kernel size mismatch");
-  TORCH_CHECK(!(is_pool && region_type != RegionType::CUSTOM && kernel_stride == kernel_size),
-              "pooling stride maps are not part of this build");
+  // a pooling layer whose kernel tiles the stride uses the stride map
+  // (space_impl.hpp:617-626, 660-669)
+  const bool use_stride_map =
+      is_pool && region_type != RegionType::CUSTOM && kernel_stride == kernel_size;
   at::Tensor custom;
   std::vector<int32_t> custom_values;
   if (region_type == RegionType::CUSTOM) {
@@ -528,6 +578,8 @@ const HipKernelMap &CoordinateManager::kernel_map(
   TORCH_CHECK(static_cast<int64_t>(kdim) + 1 == out_map.coords.size(1), "kernel size mismatch");
 
   if (!is_transpose) {
+    if (use_stride_map)
+      return store(key, generate_stride_map(in_map, out_map));
     // region on the input map's tensor stride (space_impl.hpp:626-636)
     auto off = region_offsets(region_type, kernel_size, kernel_dilation, in_map.tensor_stride,
                               custom);
@@ -538,6 +590,9 @@ const HipKernelMap &CoordinateManager::kernel_map(
                       kernel_dilation, region_type, false, is_pool);
   if (const HipKernelMap *fwd = find(fwd_key))
     return store(key, fwd->swapped());
+  // the stride map runs out -> in, then swapped (space_impl.hpp:660-669)
+  if (use_stride_map)
+    return store(key, generate_stride_map(out_map, in_map).swapped());
   // generated out -> in with the region on the output (finer) map's stride,
   // then swapped (space_impl.hpp:649-697)
   auto off = region_offsets(region_type, kernel_size, kernel_dilation, out_map.tensor_stride,

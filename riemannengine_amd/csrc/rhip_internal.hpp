@@ -200,6 +200,22 @@ __device__ __forceinline__ int32_t table_find(const TableView &t,
   }
 }
 
+// floor(a / s) * s for s > 0, exact in integers. The reference computes it
+// through float division (CPU: floor((float)a / s) * s, engine/grid/
+// stencil.hpp:46-53; GPU: __float2int_rd(__fdiv_rd(a, s)) * s,
+// lattice_gpu.cu:328-332); both equal this for |a| < 2^24.
+__device__ __forceinline__ int32_t floor_align(int32_t a, int32_t s) {
+  int32_t q = a / s;
+  if ((a % s) != 0 && a < 0)
+    --q;
+  return q * s;
+}
+
+// Stride of each spatial column, by value.
+struct StrideArg {
+  int32_t s[RHIP_MAX_COLS];
+};
+
 // Lane index within the wave and wave-level prefix of a predicate.
 __device__ __forceinline__ int lane_id() { return __lane_id(); }
 

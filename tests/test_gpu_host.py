@@ -76,8 +76,14 @@ def test_manager_insert_stride_and_cache():
     np.testing.assert_array_equal(
         oracle.canonical_pairs(tr["offsets_host"], tr["in_rows"].cpu().numpy(), tr["out_rows"].cpu().numpy()),
         oracle.canonical_pairs(fwd["offsets_host"], fwd["out_rows"].cpu().numpy(), fwd["in_rows"].cpu().numpy()))
-    with pytest.raises(RuntimeError, match="pooling"):
-        mgr.kernel_map(key, skey, [2, 2, 2], [2, 2, 2], [1, 1, 1], is_pool=True)
+    # a pooling map whose kernel tiles the stride is the stride map: one pair
+    # list, each input on its floor-aligned output (the same pairs here)
+    sm = mgr.kernel_map(key, skey, [2, 2, 2], [2, 2, 2], [1, 1, 1], is_pool=True)
+    assert sm["stride_map"] and sm["offsets_host"][1] == len(uq) == sm["offsets_host"][-1]
+    np.testing.assert_array_equal(
+        np.sort(sm["in_rows"].cpu().numpy()), np.arange(len(uq)))
+    pairs = lambda m: sorted(zip(m["in_rows"].cpu().tolist(), m["out_rows"].cpu().tolist()))  # noqa: E731
+    assert pairs(sm) == pairs(fwd)
 
 
 def _conv_check(x_np, c, conv, dtype, out_coords_ref=None, in_coords=None, offsets=None, seed=5):

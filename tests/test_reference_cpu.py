@@ -94,3 +94,82 @@ def test_reference_bf16_is_within_the_bf16_bar():
     errs = [np.abs(g - e).max() / np.abs(e).max() for g, e in ((y, ry), (gx, rgx), (gw, rgw))]
     assert max(errs) <= 2e-2, errs
     assert max(errs) > 1e-4  # it really is bf16 arithmetic
+
+
+# ---------------------------------------------------------------- pooling
+
+from helpers import oracle_pool_layer, coord_grad, align  # noqa: E402
+
+
+@pytest.mark.parametrize("mode", ["sum", "avg", "max"])
+@pytest.mark.parametrize("ks,stride,transpose,expand", [
+    (2, 2, False, False), (3, 2, False, False), (3, 1, False, False),
+    (2, 2, True, False), (3, 2, True, False), (2, 2, True, True)])
+def test_pool_layer_matches_reference(mode, ks, stride, transpose, expand):
+    """The reference's pooling layers (stride map when kernel == stride, else
+    the kernel map; transposed: generated finer map, swapped map) against the
+    oracle: same output coordinates, values and input gradients (fp32)."""
+    rng = np.random.default_rng(ks * 7 + stride + 3 * transpose)
+    c, _, _ = oracle.insert_and_map(random_coords(rng, 1500, 3, 12))
+    in_stride = 1
+    if transpose:
+        c, in_stride = oracle.stride(c, [2, 2, 2]), 2
+    x = rng.integers(-4, 5, (len(c), 3)).astype(np.float32)  # ties for max
+    gy = lambda oc: coord_grad(oc, 3)  # noqa: E731
+    y, oc, gx = ref.pool(c, x, mode, ks, stride, in_stride=in_stride, transpose=transpose,
+                         expand=expand, gy=gy)
+    out, oy, ogx = oracle_pool_layer(c, x, mode, ks, stride, in_stride=in_stride,
+                                     transpose=transpose, expand=expand, gy=gy)
+    p = align(oc, out)
+    np.testing.assert_allclose(y, oy[p], rtol=1e-5, atol=1e-5)
+    np.testing.assert_allclose(gx, ogx, rtol=1e-5, atol=1e-5)
+
+
+def test_pool_layer_bf16_matches_reference_within_tolerance():
+    """The reference computes bf16 pooling in bf16 tensors; the oracle in
+    fp32 on the same (bf16-representable) inputs: within the bf16 bound."""
+    rng = np.random.default_rng(9)
+    c, _, _ = oracle.insert_and_map(random_coords(rng, 1500, 3, 12))
+    x = rng.standard_normal((len(c), 4)).astype(np.float32)
+    x = np.asarray(torch_bf16_round(x), np.float32)
+    for mode in ("sum", "avg", "max"):
+        y, oc, _ = ref.pool(c, x, mode, 3, 2, bf16=True)
+        out, oy, _ = oracle_pool_layer(c, x, mode, 3, 2)
+        p = align(oc, out)
+        scale = np.abs(oy).max()
+        assert np.abs(y - oy[p]).max() <= 2e-2 * scale, mode
+
+
+def torch_bf16_round(a):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(a)).to(torch.bfloat16).float().numpy()
+
+
+def test_transposed_odd_stride_map_raises_like_reference():
+    """Kernel 3 == stride 3 transposed: the generated rows c - 1 floor onto a
+    coarse row that may not exist; the reference ASSERTs, the oracle counts
+    the misses."""
+    rng = np.random.default_rng(4)
+    c, _, _ = oracle.insert_and_map(random_coords(rng, 500, 3, 12))
+    coarse = oracle.stride(c, [3, 3, 3])
+    with pytest.raises(RuntimeError, match="Invalid out_coordinate_map"):
+        ref.pool(coarse, np.ones((len(coarse), 1), np.float32), "sum", 3, 3, in_stride=3,
+                 transpose=True)
+    fine = oracle.stride_region(coarse, oracle.region_offsets(3, 3, 1, 1))
+    _, miss = oracle.stride_map(fine, coarse, [3, 3, 3])
+    assert miss > 0
+
+
+@pytest.mark.parametrize("mode", ["sum", "avg", "max"])
+def test_global_pool_matches_reference(mode):
+    rng = np.random.default_rng(21)
+    c, _, _ = oracle.insert_and_map(random_coords(rng, 900, 3, 10, batch=4))
+    c = c[c[:, 0] != 2]  # an empty batch
+    x = rng.integers(-3, 4, (len(c), 5)).astype(np.float32)
+    gy = rng.standard_normal((4, 5)).astype(np.float32)
+    y, oc, gx = ref.global_pool(c, x, mode, gy=gy)
+    assert oc.tolist() == [[b, 0, 0, 0] for b in range(4)]
+    oy = oracle.global_pool_forward(x, c, mode)
+    np.testing.assert_allclose(y, oy, rtol=1e-5, atol=1e-6)
+    np.testing.assert_allclose(gx, oracle.global_pool_backward(x, oy, gy, c, mode),
+                               rtol=1e-5, atol=1e-6)
