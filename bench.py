@@ -53,6 +53,9 @@ def parse_args():
     ap.add_argument("--config", type=int, choices=[1, 2, 3, 4, 5], default=2,
                     help="benchmark configuration; 2 (the default) is the headline line, the "
                          "others print a line of their own for the record")
+    ap.add_argument("--op", choices=["conv", "pool"], default="conv",
+                    help="conv (default): the headline convolution line; pool: a line of its "
+                         "own for the pooling path on the config-2 coordinates")
     ap.add_argument("--seed", type=int, default=2)
     ap.add_argument("--no-cpu-baseline", action="store_true",
                     help="skip the CPU oracle timing (profiling runs)")
@@ -357,6 +360,142 @@ def run_other_config(args):
     return line
 
 
+def pool_traffic(kind, n_in, n_out, K, C, s, ncol=4):
+    """Algorithmic HBM bytes of one pooling kernel pass: every feature row it
+    must touch read (or written) once, plus its index tables; no re-reads."""
+    if kind == "forward":      # x rows, nbr [K, n_out], order; y, counts
+        return n_in * C * s + K * n_out * 4 + n_out * 4 + n_out * C * s + n_out * 4
+    if kind == "backward":     # gy rows, counts, nbr_t [K, n_in], order; gx
+        return n_out * C * s + n_out * 4 + K * n_in * 4 + n_in * 4 + n_in * C * s
+    if kind == "max_backward":  # share pass (y, gy, x, nbr; gs fp32) + gather pass
+        share = 2 * n_out * C * s + n_in * C * s + K * n_out * 4 + n_out * 4 + n_out * C * 4
+        gather = n_in * C * s + n_out * C * s + n_out * C * 4 + K * n_in * 4 + n_in * 4 \
+            + n_in * C * s
+        return share + gather
+    if kind == "global_forward":   # x rows + members; y (n_out = batches) negligible
+        return n_in * C * s + n_in * 4 + n_out * C * s
+    if kind == "global_backward":  # coordinate rows (batch column) + gx
+        return n_in * ncol * 4 + n_in * C * s + n_out * C * s
+    raise ValueError(kind)
+
+
+def pool_cpu_baseline(coords_np, C, seed, rows=20000):
+    """The reference's pooling layers on the CPU (oracle/_ref) over a bounded
+    sample of the workload: the first `rows` voxels of scene 0 in (x, y, z)
+    order (a slab of the scene), RiemannMaxPooling(2, 2), RiemannAvgPooling
+    (3, 2) and RiemannGlobalAvgPooling, forward + backward each, fp32. The
+    reference builds its pooling maps on every call (pooling.cpp:17-75), so
+    they are part of its time; it pools output by output, which is why the
+    sample is a slab (the whole 100k-voxel scene takes minutes)."""
+    from oracle import ref
+    if not ref.available():
+        return None
+    scene = coords_np[coords_np[:, 0] == 0]
+    scene = scene[np.lexsort(scene[:, ::-1].T)][:rows]
+    rng = np.random.default_rng(seed)
+    x = rng.standard_normal((len(scene), C)).astype(np.float32)
+    total = 0.0
+    for mode, ks in (("max", 2), ("avg", 3)):
+        y, _, _ = ref.pool(scene, x, mode, ks, 2)
+        gy = np.ones_like(y)
+        t0 = time.perf_counter()
+        ref.pool(scene, x, mode, ks, 2, gy=gy)
+        total += time.perf_counter() - t0
+    gy = np.ones((1, C), np.float32)
+    t0 = time.perf_counter()
+    ref.global_pool(scene, x, "avg", gy=gy)
+    total += time.perf_counter() - t0
+    return {"value": round(len(scene) / total / 1e6, 5), "unit": "Mvoxels/s",
+            "cores": ref.num_threads(), "kind": "reference",
+            "sample": f"first {len(scene)} voxels of scene 0 in (x, y, z) order, C={C} fp32, "
+                      "one max 2^3/2 + avg 3^3/2 + global avg forward+backward, maps included",
+            "ms": round(total * 1e3, 1), "cpu": cpu_model()}
+
+
+def run_pool(args):
+    """Pooling line: on the config-2 coordinates (4 indoor scenes), C = 64,
+    one step = RiemannMaxPooling(2, 2) over the stride map, RiemannAvgPooling
+    (3, 2) over the 3^3 kernel map and global average pooling, forward and
+    backward each, through the C ABI with the maps prebuilt."""
+    import torch
+    from riemannengine_amd import abi, scenes, stencil
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU (the HIP path has no CPU fallback)", file=sys.stderr)
+        sys.exit(1)
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    dt = torch.float32 if args.dtype == "f32" else torch.bfloat16
+    s = 4 if args.dtype == "f32" else 2
+    C = 64
+    coords_np = scenes.indoor_batch(4, args.seed)
+    coords = torch.from_numpy(coords_np).to(dev)
+    off3 = stencil.region_offsets(3, 3)
+
+    def build():
+        tf = abi.hash_build(coords)
+        tc = abi.hash_build(abi.stride_coords(coords, [2, 2, 2]))
+        return tf, tc, abi.stride_map(tf, tc, [2, 2, 2]), abi.kernel_map(tf, tc, off3), \
+            abi.batch_segments(coords)
+    (tf, tc, sm, km, segs), map_ms = _map_time(build, args.map_reps)
+    n_in, n_out = tf.n, tc.n
+    g = torch.Generator(device="cpu").manual_seed(args.seed)
+    x = torch.randn((n_in, C), generator=g).to(dev, dt)
+    gy = torch.randn((n_out, C), generator=g).to(dev, dt)
+    gyb = torch.randn((segs.n_batches, C), generator=g).to(dev, dt)
+    ym, cm = abi.pool_forward(x, sm, "max")
+    ya, ca = abi.pool_forward(x, km, "avg")
+    yg = abi.global_pool_forward(x, segs, "avg")
+    passes = [("max2_forward", lambda: abi.pool_forward(x, sm, "max")),
+              ("max2_backward", lambda: abi.pool_backward(gy, ym, x, sm, cm, "max")),
+              ("avg3_forward", lambda: abi.pool_forward(x, km, "avg")),
+              ("avg3_backward", lambda: abi.pool_backward(gy, ya, x, km, ca, "avg")),
+              ("global_forward", lambda: abi.global_pool_forward(x, segs, "avg")),
+              ("global_backward", lambda: abi.global_pool_backward(gyb, yg, x, coords, segs,
+                                                                   "avg"))]
+    per, wall = _timed_passes(passes, args.steps, args.warmup)
+    B = {"max2_forward": pool_traffic("forward", n_in, n_out, sm.K, C, s),
+         "max2_backward": pool_traffic("max_backward", n_in, n_out, sm.K, C, s),
+         "avg3_forward": pool_traffic("forward", n_in, n_out, km.K, C, s),
+         "avg3_backward": pool_traffic("backward", n_in, n_out, km.K, C, s),
+         "global_forward": pool_traffic("global_forward", n_in, segs.n_batches, 0, C, s),
+         "global_backward": pool_traffic("global_backward", n_in, segs.n_batches, 0, C, s)}
+    dom = max(per, key=per.get)
+    achieved = B[dom] / (per[dom] * 1e-3) / 1e9
+    kernels = {"max2_forward": "pool_fwd_kernel (max, stride map)",
+               "max2_backward": "pool_maxshare_kernel + pool_bwd_kernel (max, stride map)",
+               "avg3_forward": "pool_fwd_kernel (avg, 3^3 kernel map)",
+               "avg3_backward": "pool_bwd_kernel (avg, 3^3 kernel map)",
+               "global_forward": "gpool_partial_kernel + gpool_final_kernel (avg)",
+               "global_backward": "gpool_bwd_kernel (avg)"}
+    roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+            "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None, "kernel": kernels[dom],
+            "kernel_ms": round(per[dom], 4), "algorithmic": {"bytes": B[dom]}}
+    step_ms = sum(per.values())
+    t_roof = sum(B.values()) / (PEAK_HBM_GBS * 1e9)
+    line = {
+        "metric": "sparse pooling fwd+bwd Mvoxels/s (max 2^3/2 + avg 3^3/2 + global avg, C64)",
+        "value": round(n_in / (wall * 1e-3) / 1e6, 3), "unit": "Mvoxels/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(wall, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": args.dtype,
+        "data": "synthetic (seeded indoor scenes; random N(0,1) features and gradients)",
+        "config": {"workload": "pooling on the config-2 coordinates (indoor scenes batch 4): "
+                               "max 2^3 stride 2 (stride map), avg 3^3 stride 2 (kernel map), "
+                               "global avg; forward+backward, maps prebuilt",
+                   "n_voxels": n_in, "n_coarse": n_out, "stride_map_rows": sm.K,
+                   "kernel_map_pairs": km.n_pairs, "batches": segs.n_batches, "channels": C,
+                   "seed": args.seed, "accumulate": "f32"},
+        "kernel_map_ms": round(map_ms, 3),
+        "breakdown_ms": {k: round(v, 4) for k, v in per.items()},
+        "step_roofline": {"t_roof_ms": round(t_roof * 1e3, 4),
+                          "frac": round(t_roof * 1e3 / step_ms, 4), "bytes": sum(B.values())},
+        "roofline": roof,
+        "cpu_baseline": None if args.no_cpu_baseline else pool_cpu_baseline(coords_np, C,
+                                                                            args.seed),
+    }
+    return line
+
+
 def main():
     args = parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -371,6 +510,9 @@ def main():
         return
     if args.dtype is None:
         args.dtype = "bf16" if args.config in (3, 5) else "f32"
+    if args.op == "pool":
+        print(json.dumps(run_pool(args)), flush=True)
+        return
     if args.config != 2:
         print(json.dumps(run_other_config(args)), flush=True)
         return

@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define RHIP_ABI_VERSION 6
+#define RHIP_ABI_VERSION 7
 #define RHIP_MAX_COLS 8 /* batch column + up to 7 spatial axes */
 
 typedef enum rhip_status {
@@ -264,7 +264,13 @@ int rhip_conv_backward_weight(const void *x, int64_t n_in, int32_t cin,
 typedef enum rhip_pool_mode {
   RHIP_POOL_SUM = 0,
   RHIP_POOL_AVG = 1, /* sum / number of pooled rows */
-  RHIP_POOL_MAX = 2  /* NaN propagates; the gradient splits evenly between ties */
+  RHIP_POOL_MAX = 2, /* NaN propagates; the gradient splits evenly between ties */
+  /* Max as zeros.scatter_reduce("amax", include_self=False) computes it
+   * (SparseTensor MAX_POOL quantization, engine/tensor/sparse_tensor.cpp:
+   * 474-479): the forward equals RHIP_POOL_MAX; the backward also counts the
+   * excluded zero as a tie when the maximum is 0 (t + 1 ways). Local pooling
+   * only. */
+  RHIP_POOL_MAX_SCATTER = 3
 } rhip_pool_mode;
 
 /* Workspace shared by the two phases of one stride map (pass the same
@@ -290,12 +296,27 @@ int rhip_stride_map_count(const rhip_table *out_table, const int32_t *in_coords,
                           int32_t *k_max_host, hipStream_t stream);
 
 /*
+ * Phase 1 of a group map, the same grouping for rows whose group is given:
+ * row i belongs to group[i] in [0, n_groups) (e.g. the inverse map of
+ * rhip_hash_build, each row's unique coordinate). Phase 2 is
+ * rhip_stride_map_fill with n_in = n, n_out = n_groups; local pooling over
+ * the result reduces each group (SparseTensor quantization). Workspace:
+ * rhip_stride_map_workspace_bytes(n, n_groups). Synchronises once; fails
+ * with RHIP_ERR_INVALID for a group outside [0, n_groups).
+ * Replaces the index_add_ / scatter_reduce("amax") by row_to_unique of
+ * SparseTensor::quantize_features (engine/tensor/sparse_tensor.cpp:447-481).
+ */
+int rhip_group_map_count(const int32_t *group, int64_t n, int64_t n_groups,
+                         void *workspace, size_t workspace_bytes,
+                         int32_t *k_max_host, hipStream_t stream);
+
+/*
  * Phase 2: the stride map in the neighbour-table form of a kernel map
  * (columns by processing position, as rhip_kmap_count / rhip_kmap_fill):
  *   nbr [k_max, n_out]: nbr[k*n_out+p] = k-th input row (ascending) of the
  *                       output out_order[p], -1 past its group;
- *   nbr_t [k_max, n_in]: nbr_t[k*n_in+q] = the output row whose k-th input
- *                       is in_order[q], else -1;
+ *   nbr_t [1, n_in]:    nbr_t[q] = the output row of input in_order[q] (each
+ *                       input has exactly one);
  *   in_rows/out_rows [n_in]: the reference's single pair list (one kernel
  *                       offset), grouped by output.
  * in_order / out_order are processing orders (permutations; NULL = row order),
@@ -328,20 +349,21 @@ int rhip_pool_forward(const void *x, int64_t n_in, int32_t C,
                       int32_t dtype, hipStream_t stream);
 
 /*
- * Local pooling backward: grad_x[i] for i = in_order[q] is the sum over k
- * with o = nbr_t[k*n_in+q] >= 0 of  sum: grad_y[o];  average: grad_y[o] /
+ * Local pooling backward: grad_x[i] for i = in_order[q] is the sum over k <
+ * K_t with o = nbr_t[k*n_in+q] >= 0 of  sum: grad_y[o];  average: grad_y[o] /
  * counts[o];  max: grad_y[o] / t where x[i] == y[o] (t = number of pooled
  * rows equal to y[o], per channel), else 0. grad_x [n_in, C] is overwritten.
- * Max pooling also needs x, y, nbr, out_order and the workspace; average
- * needs counts from rhip_pool_forward.
+ * K and K_t are the row counts of nbr and nbr_t (equal for a kernel map; a
+ * stride map's nbr_t has one row). Max pooling also needs x, y, nbr,
+ * out_order and the workspace; average needs counts from rhip_pool_forward.
  * Replaces the autograd replay of StackBackward / SumBackward / MeanBackward /
  * AmaxBackward / IndexSelectBackward of evaluate_pooling
  * (engine/nn/pooling.cpp:120-140).
  */
 int rhip_pool_backward(const void *grad_y, const void *y, const void *x,
-                       int64_t n_out, int32_t C, const int32_t *nbr,
+                       int64_t n_out, int32_t C, const int32_t *nbr, int32_t K,
                        const int32_t *out_order, const int32_t *nbr_t,
-                       int32_t K, const int32_t *in_order,
+                       int32_t K_t, const int32_t *in_order,
                        int64_t n_in, const int32_t *counts, int32_t mode,
                        void *grad_x, int32_t dtype, void *workspace,
                        size_t workspace_bytes, hipStream_t stream);

@@ -172,7 +172,7 @@ def canonical_pairs(kofs, in_rows, out_rows, in_coords=None, out_coords=None):
     return t[idx]
 
 
-POOL_MODE = {"sum": 0, "avg": 1, "max": 2}
+POOL_MODE = {"sum": 0, "avg": 1, "max": 2, "max_scatter": 3}
 
 
 def stride_map(in_coords, out_coords, out_tensor_stride):

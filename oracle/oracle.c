@@ -382,7 +382,11 @@ int64_t oracle_stride_map(const int32_t *in_coords, int64_t n_in, int ncol,
   return miss;
 }
 
-/* mode: 0 sum, 1 average, 2 max (PoolingMode LOCAL_{SUM,AVG,MAX}_POOLING) */
+/* mode: 0 sum, 1 average, 2 max (PoolingMode LOCAL_{SUM,AVG,MAX}_POOLING),
+ * 3 max as zeros.scatter_reduce("amax", include_self=False): forward as 2,
+ * backward counting the excluded zero as one more tie where the max is 0
+ * (LibTorch's scatter_reduce backward; SparseTensor MAX_POOL quantization,
+ * engine/tensor/sparse_tensor.cpp:474-479). */
 
 /*
  * Local pooling: evaluate_pooling (engine/nn/pooling.cpp:80-150). The pairs
@@ -397,7 +401,7 @@ void oracle_pool_forward(const float *x, int64_t n_in, int C, const int32_t *in_
   double *acc = (double *)malloc(sizeof(double) * (size_t)(n_out > 0 ? n_out : 1) * C);
   int64_t *cnt = (int64_t *)calloc((size_t)(n_out > 0 ? n_out : 1), sizeof(int64_t));
   for (int64_t e = 0; e < n_out * C; ++e)
-    acc[e] = mode == 2 ? -INFINITY : 0.0;
+    acc[e] = mode >= 2 ? -INFINITY : 0.0;
   for (int64_t p = 0; p < P; ++p) {
     int64_t i = in_rows[p], o = out_rows[p];
     if (i < 0 || i >= n_in || o < 0 || o >= n_out)
@@ -406,7 +410,7 @@ void oracle_pool_forward(const float *x, int64_t n_in, int C, const int32_t *in_
     for (int c = 0; c < C; ++c) {
       double v = x[i * C + c];
       double *a = acc + o * C + c;
-      if (mode == 2)
+      if (mode >= 2)
         *a = (v > *a || isnan(v)) && !isnan(*a) ? v : *a;
       else
         *a += v;
@@ -445,6 +449,9 @@ void oracle_pool_backward(const float *x, const float *y, const float *grad_y, i
     for (int c = 0; c < C; ++c)
       ties[o * C + c] += x[i * C + c] == y[o * C + c];
   }
+  if (mode == 3)
+    for (int64_t e = 0; e < n_out * C; ++e)
+      ties[e] += y[e] == 0.0f;
   for (int64_t p = 0; p < P; ++p) {
     int64_t i = in_rows[p], o = out_rows[p];
     if (i < 0 || i >= n_in || o < 0 || o >= n_out)
@@ -453,7 +460,7 @@ void oracle_pool_backward(const float *x, const float *y, const float *grad_y, i
       double g = grad_y[o * C + c];
       if (mode == 1)
         g /= (double)cnt[o];
-      else if (mode == 2)
+      else if (mode >= 2)
         g = x[i * C + c] == y[o * C + c] ? g / (double)ties[o * C + c] : 0.0;
       gx[i * C + c] += g;
     }

@@ -57,6 +57,9 @@ def lib():
         L.ref_global_pool.restype = _i64
         L.ref_global_pool.argtypes = [_vp, _i64, ctypes.c_int, _vp, ctypes.c_int, ctypes.c_int,
                                       ctypes.c_int, _vp, _i64, _vp, _vp, _vp]
+        L.ref_quantize.restype = _i64
+        L.ref_quantize.argtypes = [_vp, _i64, ctypes.c_int, _vp, ctypes.c_int, ctypes.c_int,
+                                   ctypes.c_int, _vp, _i64, _vp, _vp, _vp]
         L.ref_num_threads.restype = ctypes.c_int
         _LIB = L
     return _LIB
@@ -193,6 +196,30 @@ def global_pool(coords, x, mode="avg", gy=None, bf16=False):
     gx = np.empty((n, C), np.float32) if g is not None else None
     _check(lib().ref_global_pool(*args, _p(g), B, _p(y), _p(oc), _p(gx)))
     return y[:B], oc[:B], gx
+
+
+QUANT_MODE = {"subsample": 0, "avg": 1, "sum": 2, "max": 3}
+
+
+def quantize(coords, x, mode="avg", gy=None, bf16=False):
+    """SparseTensor(x, coords, quantization_mode) on the CPU: (features [n_u, C],
+    unique coordinates [n_u, ncol], gx); gy in the unique rows' order, or a
+    callable(unique coords) that builds it."""
+    c = np.ascontiguousarray(coords, np.int32)
+    n, ncol = c.shape
+    x = np.ascontiguousarray(x, np.float32)
+    C = x.shape[1]
+    args = (_p(c), n, ncol, _p(x), C, QUANT_MODE[mode], 1 if bf16 else 0)
+    nu = _check(lib().ref_quantize(*args, None, 0, None, None, None))
+    y = np.empty((max(nu, 1), C), np.float32)
+    oc = np.empty((max(nu, 1), ncol), np.int32)
+    if callable(gy):
+        _check(lib().ref_quantize(*args, None, nu, _p(y), _p(oc), None))
+        gy = gy(oc[:nu])
+    g = None if gy is None else np.ascontiguousarray(gy, np.float32)
+    gx = np.empty((n, C), np.float32) if g is not None else None
+    _check(lib().ref_quantize(*args, _p(g), nu, _p(y), _p(oc), _p(gx)))
+    return y[:nu], oc[:nu], gx
 
 
 def num_threads() -> int:

@@ -327,6 +327,34 @@ int64_t ref_global_pool(const int32_t *coords, int64_t n, int ncol, const float 
   });
 }
 
+// SparseTensor construction with a quantization mode (sparse_tensor.cpp:62-114,
+// 447-481): qmode is SparseTensorQuantizationMode (0 random subsample, 1
+// unweighted average, 2 unweighted sum, 3 max pool) over the rows `coords`
+// (duplicates allowed) with features x [n, C]. Same conventions as ref_pool.
+// Returns the unique row count.
+int64_t ref_quantize(const int32_t *coords, int64_t n, int ncol, const float *x, int C, int qmode,
+                     int dtype, const float *gy, int64_t out_cap, float *y, int32_t *out_coords,
+                     float *gx) {
+  return guarded([&]() -> int64_t {
+    const int D = ncol - 1;
+    const auto dt = dtype == 1 ? torch::kBFloat16 : torch::kFloat32;
+    auto mgr = std::make_shared<riemann::CoordinateManager>(D, riemann::CoordinateMapBackend::CPU);
+    auto X = float_rows(x, n, C).to(dt).detach().requires_grad_(true);
+    riemann::SparseTensor t(X, int_rows(coords, n, ncol), mgr,
+                            static_cast<riemann::SparseTensorQuantizationMode::Type>(qmode));
+    const int64_t nu = t.F().size(0);
+    if (nu > out_cap)
+      return nu;
+    copy_out(t.F().detach().to(torch::kFloat32), y);
+    copy_out(mgr->get_coordinates(t.coordinate_map_key()).to(torch::kInt32), out_coords);
+    if (gy != nullptr) {
+      t.F().backward(float_rows(gy, nu, C).to(dt));
+      copy_out(X.grad().to(torch::kFloat32), gx);
+    }
+    return nu;
+  });
+}
+
 // Threads LibTorch's CPU kernels use (the cores a baseline timing uses).
 int ref_num_threads() { return at::get_num_threads(); }
 

@@ -22,8 +22,8 @@ MAX_COLS = 8
 F32, BF16 = 0, 1
 KEY_PACKED64, KEY_ROWREF = 0, 1
 KMAP_SYMMETRIC = 1
-POOL_SUM, POOL_AVG, POOL_MAX = 0, 1, 2
-POOL_MODES = {"sum": POOL_SUM, "avg": POOL_AVG, "max": POOL_MAX}
+POOL_SUM, POOL_AVG, POOL_MAX, POOL_MAX_SCATTER = 0, 1, 2, 3
+POOL_MODES = {"sum": POOL_SUM, "avg": POOL_AVG, "max": POOL_MAX, "max_scatter": POOL_MAX_SCATTER}
 
 # Every function the header declares (checked by the CPU test suite).
 EXPORTS = (
@@ -33,7 +33,8 @@ EXPORTS = (
     "rhip_expand_coords", "rhip_kmap_workspace_bytes", "rhip_kmap_count", "rhip_kmap_fill",
     "rhip_conv_workspace_bytes", "rhip_conv_forward",
     "rhip_conv_backward_input", "rhip_conv_backward_weight",
-    "rhip_stride_map_workspace_bytes", "rhip_stride_map_count", "rhip_stride_map_fill",
+    "rhip_stride_map_workspace_bytes", "rhip_stride_map_count", "rhip_group_map_count",
+    "rhip_stride_map_fill",
     "rhip_pool_workspace_bytes", "rhip_pool_forward", "rhip_pool_backward",
     "rhip_global_pool_workspace_bytes", "rhip_batch_count", "rhip_batch_segments",
     "rhip_global_pool_forward", "rhip_global_pool_backward",
@@ -87,13 +88,15 @@ def _declare(lib):
         "rhip_stride_map_workspace_bytes": (ctypes.c_int, [_i64, _i64, _P(_sz)]),
         "rhip_stride_map_count": (ctypes.c_int, [_P(RhipTable), _vp, _i64, _P(_i32), _vp, _sz,
                                                  _P(_i32), _vp]),
+        "rhip_group_map_count": (ctypes.c_int, [_vp, _i64, _i64, _vp, _sz, _P(_i32), _vp]),
         "rhip_stride_map_fill": (ctypes.c_int, [_i64, _i64, _i32, _vp, _vp, _vp, _sz, _vp, _vp,
                                                 _vp, _vp, _vp]),
         "rhip_pool_workspace_bytes": (ctypes.c_int, [_i64, _i32, _i32, _P(_sz)]),
         "rhip_pool_forward": (ctypes.c_int, [_vp, _i64, _i32, _vp, _i32, _vp, _i64, _i32, _vp,
                                              _vp, _i32, _vp]),
-        "rhip_pool_backward": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i32, _vp, _vp, _vp, _i32,
-                                              _vp, _i64, _vp, _i32, _vp, _i32, _vp, _sz, _vp]),
+        "rhip_pool_backward": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i32, _vp, _i32, _vp, _vp,
+                                              _i32, _vp, _i64, _vp, _i32, _vp, _i32, _vp, _sz,
+                                              _vp]),
         "rhip_global_pool_workspace_bytes": (ctypes.c_int, [_i64, _i32, _i32, _P(_sz)]),
         "rhip_batch_count": (ctypes.c_int, [_vp, _i64, _i32, _vp, _sz, _P(_i32), _vp]),
         "rhip_batch_segments": (ctypes.c_int, [_vp, _i64, _i32, _i32, _vp, _sz, _vp, _vp,
@@ -396,8 +399,8 @@ def conv_backward_weight(x: torch.Tensor, grad_y: torch.Tensor, kmap: KernelMap,
 def stride_map(in_table: CoordTable, out_table: CoordTable, out_tensor_stride) -> KernelMap:
     """Pooling stride map (kernel size == stride): every input row onto the
     output row of its floor-aligned coordinates, in the neighbour-table form
-    (K = largest number of inputs on one output). The pair list is the
-    reference's single offset: offsets = [0, P, ..., P]."""
+    (nbr: K = largest number of inputs on one output rows; nbr_t: one row).
+    The pair list is the reference's single offset: offsets = [0, P]."""
     L = lib()
     dev = in_table.ucoords.device
     n_in, n_out = in_table.n, out_table.n
@@ -413,18 +416,47 @@ def stride_map(in_table: CoordTable, out_table: CoordTable, out_tensor_stride) -
     # phase 2 writes every entry of the tables (-1 where no input lies)
     table = torch.empty if kmax.value > 0 else (lambda *a, **k: torch.full(*a, -1, **k))
     nbr = table((K, max(n_out, 1)), dtype=torch.int32, device=dev)
-    nbr_t = table((K, max(n_in, 1)), dtype=torch.int32, device=dev)
+    nbr_t = table((1, max(n_in, 1)), dtype=torch.int32, device=dev)
     in_rows = torch.empty(max(n_in, 1), dtype=torch.int32, device=dev)
     out_rows = torch.empty(max(n_in, 1), dtype=torch.int32, device=dev)
     _check(L.rhip_stride_map_fill(n_in, n_out, int(kmax.value), _ptr(in_table.order),
                                   _ptr(out_table.order), _ptr(ws), ws.numel(), _ptr(nbr),
                                   _ptr(nbr_t), _ptr(in_rows), _ptr(out_rows), st),
            "rhip_stride_map_fill")
-    kofs_host = np.full(K + 1, n_in, dtype=np.int64)
-    kofs_host[0] = 0
+    kofs_host = np.array([0, n_in], dtype=np.int64)
     return KernelMap(K, n_in, n_out, torch.as_tensor(kofs_host).to(dev), kofs_host,
                      in_rows[:n_in], out_rows[:n_in], nbr[:, :n_out], nbr_t[:, :n_in],
                      in_table.order, out_table.order)
+
+
+def group_map(group: torch.Tensor, n_groups: int) -> KernelMap:
+    """Rows grouped by a given group id (e.g. a hash build's inverse map), in
+    the stride map's form: nbr [K, n_groups] (rows of each group ascending,
+    K = largest group), nbr_t [1, n] (each row's group), row order."""
+    _require_cuda(group, "group")
+    L = lib()
+    dev = group.device
+    group = group.to(torch.int32).contiguous()
+    n = group.shape[0]
+    st = _stream(dev)
+    ws = torch.empty(_sizeq(L.rhip_stride_map_workspace_bytes, n, n_groups), dtype=torch.uint8,
+                     device=dev)
+    kmax = ctypes.c_int32(0)
+    _check(L.rhip_group_map_count(_ptr(group), n, n_groups, _ptr(ws), ws.numel(),
+                                  ctypes.byref(kmax), st), "rhip_group_map_count")
+    K = max(int(kmax.value), 1)
+    table = torch.empty if kmax.value > 0 else (lambda *a, **k: torch.full(*a, -1, **k))
+    nbr = table((K, max(n_groups, 1)), dtype=torch.int32, device=dev)
+    nbr_t = table((1, max(n, 1)), dtype=torch.int32, device=dev)
+    in_rows = torch.empty(max(n, 1), dtype=torch.int32, device=dev)
+    out_rows = torch.empty(max(n, 1), dtype=torch.int32, device=dev)
+    _check(L.rhip_stride_map_fill(n, n_groups, int(kmax.value), None, None, _ptr(ws), ws.numel(),
+                                  _ptr(nbr), _ptr(nbr_t), _ptr(in_rows), _ptr(out_rows), st),
+           "rhip_stride_map_fill")
+    kofs_host = np.array([0, n], dtype=np.int64)
+    iota = lambda m: torch.arange(m, dtype=torch.int32, device=dev)  # noqa: E731
+    return KernelMap(K, n, n_groups, torch.as_tensor(kofs_host).to(dev), kofs_host, in_rows[:n],
+                     out_rows[:n], nbr[:, :n_groups], nbr_t[:, :n], iota(n), iota(n_groups))
 
 
 def _pool_mode(mode) -> int:
@@ -443,7 +475,7 @@ def pool_forward(x: torch.Tensor, kmap: KernelMap, mode="avg"):
     C = x.shape[1]
     y = torch.empty((kmap.n_out, C), dtype=x.dtype, device=x.device)
     counts = torch.empty(max(kmap.n_out, 1), dtype=torch.int32, device=x.device)
-    _check(lib().rhip_pool_forward(_ptr(x), kmap.n_in, C, _ptr(kmap.nbr), kmap.K,
+    _check(lib().rhip_pool_forward(_ptr(x), kmap.n_in, C, _ptr(kmap.nbr), kmap.nbr.shape[0],
                                    _ptr(kmap.out_order), kmap.n_out, _pool_mode(mode), _ptr(y),
                                    _ptr(counts), dt, _stream(x.device)), "rhip_pool_forward")
     return y, counts[:kmap.n_out]
@@ -460,7 +492,8 @@ def pool_backward(grad_y: torch.Tensor, y: torch.Tensor, x: torch.Tensor, kmap: 
     ws = torch.empty(_sizeq(lib().rhip_pool_workspace_bytes, kmap.n_out, C, m),
                      dtype=torch.uint8, device=x.device)
     _check(lib().rhip_pool_backward(_ptr(grad_y), _ptr(y), _ptr(x), kmap.n_out, C,
-                                    _ptr(kmap.nbr), _ptr(kmap.out_order), _ptr(kmap.nbr_t), kmap.K,
+                                    _ptr(kmap.nbr), kmap.nbr.shape[0], _ptr(kmap.out_order),
+                                    _ptr(kmap.nbr_t), kmap.nbr_t.shape[0],
                                     _ptr(kmap.in_order), kmap.n_in, _ptr(counts), m, _ptr(gx),
                                     dt, _ptr(ws), ws.numel(), _stream(x.device)),
            "rhip_pool_backward")

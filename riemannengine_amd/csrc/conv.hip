@@ -38,7 +38,6 @@ typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / kWave;
 constexpr int kMaskWords = 4; // the MFMA paths handle K <= 128 offsets
-constexpr int kXcds = 8;      // MI355X: 8 XCDs, workgroups dealt round-robin
 
 template <typename T> struct Mfma;
 
@@ -84,20 +83,6 @@ template <> __device__ __forceinline__ __bf16 from_f32<__bf16>(float v) {
   return static_cast<__bf16>(v);
 }
 
-// Workgroup id -> tile id. Workgroups are dealt to the 8 XCDs round-robin
-// (id b runs on XCD b % 8); this mapping hands each XCD runs of kXcdRun
-// consecutive tiles, so tiles that share neighbour rows share an L2, while
-// the runs stay interleaved over the whole map to keep the XCDs balanced.
-// The grid is padded to a multiple of 8 * kXcdRun (padding ids map past the
-// last tile).
-constexpr int kXcdRun = 16;
-__device__ __forceinline__ int64_t xcd_tile(int64_t b) {
-  const int64_t x = b % kXcds, m = b / kXcds;
-  return ((m / kXcdRun) * kXcds + x) * kXcdRun + (m % kXcdRun);
-}
-inline int64_t xcd_grid(int64_t tiles) {
-  return ceil_div(tiles, kXcds * kXcdRun) * kXcds * kXcdRun;
-}
 
 // ------------------------------------------------ output-stationary GEMM
 //

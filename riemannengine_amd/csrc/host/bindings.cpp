@@ -235,7 +235,9 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         return s += o;
       })
       .def("detach", &SparseTensor::detach)
-      .def("to_dtype", &SparseTensor::to)
+      .def("to_dtype", py::overload_cast<c10::ScalarType>(&SparseTensor::to, py::const_))
+      .def("to", py::overload_cast<torch::Device>(&SparseTensor::to, py::const_),
+           py::arg("device"))
       .def("__repr__", [](const SparseTensor &s) {
         return "SparseTensor(rows=" + std::to_string(s.F().size(0)) +
                ", channels=" + std::to_string(s.F().size(1)) + ", " +

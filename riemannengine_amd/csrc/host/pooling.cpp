@@ -53,6 +53,11 @@ at::Tensor byte_buffer(size_t bytes, const at::Device &dev) {
                       torch::TensorOptions().dtype(torch::kUInt8).device(dev));
 }
 
+// Processing orders are optional (an empty tensor = row order).
+const int32_t *ptr_or_null(const at::Tensor &t) {
+  return t.defined() && t.numel() > 0 ? t.data_ptr<int32_t>() : nullptr;
+}
+
 using torch::autograd::AutogradContext;
 using torch::autograd::tensor_list;
 
@@ -72,11 +77,11 @@ struct HipPoolingFunction : public torch::autograd::Function<HipPoolingFunction>
     auto counts = torch::empty({std::max<int64_t>(n_out, 1)},
                                torch::TensorOptions().dtype(torch::kInt32).device(dev));
     check_rhip(rhip_pool_forward(x.data_ptr(), n_in, static_cast<int32_t>(C),
-                                 nbr.data_ptr<int32_t>(), K, out_order.data_ptr<int32_t>(), n_out,
+                                 nbr.data_ptr<int32_t>(), K, ptr_or_null(out_order), n_out,
                                  static_cast<int32_t>(reduction), y.data_ptr(),
                                  counts.data_ptr<int32_t>(), pool_dtype(x), stream_of(dev)),
                "rhip_pool_forward");
-    ctx->save_for_backward({x, reduction == RHIP_POOL_MAX ? y : at::Tensor(), nbr, out_order,
+    ctx->save_for_backward({x, reduction >= RHIP_POOL_MAX ? y : at::Tensor(), nbr, out_order,
                             nbr_t, in_order, counts});
     ctx->saved_data["reduction"] = reduction;
     return y;
@@ -91,6 +96,7 @@ struct HipPoolingFunction : public torch::autograd::Function<HipPoolingFunction>
     at::DeviceGuard guard(dev);
     const int64_t n_in = x.size(0), C = x.size(1), n_out = nbr.size(1);
     const int32_t K = static_cast<int32_t>(nbr.size(0));
+    const int32_t K_t = static_cast<int32_t>(nbr_t.size(0));
     auto gy = grads[0].to(x.scalar_type()).contiguous();
     size_t bytes = 0;
     check_rhip(rhip_pool_workspace_bytes(n_out, static_cast<int32_t>(C),
@@ -100,9 +106,9 @@ struct HipPoolingFunction : public torch::autograd::Function<HipPoolingFunction>
     auto gx = torch::empty_like(x);
     check_rhip(rhip_pool_backward(gy.data_ptr(), y.defined() ? y.data_ptr() : nullptr,
                                   x.data_ptr(), n_out, static_cast<int32_t>(C),
-                                  nbr.data_ptr<int32_t>(), out_order.data_ptr<int32_t>(),
-                                  nbr_t.data_ptr<int32_t>(), K,
-                                  in_order.data_ptr<int32_t>(), n_in, counts.data_ptr<int32_t>(),
+                                  nbr.data_ptr<int32_t>(), K, ptr_or_null(out_order),
+                                  nbr_t.data_ptr<int32_t>(), K_t, ptr_or_null(in_order), n_in,
+                                  counts.data_ptr<int32_t>(),
                                   static_cast<int32_t>(reduction), gx.data_ptr(), pool_dtype(x),
                                   ws.data_ptr(), ws.numel(), stream_of(dev)),
                "rhip_pool_backward");
@@ -226,6 +232,40 @@ at::Tensor hip_sparse_pooling(const at::Tensor &features, const HipKernelMap &ma
               features.size(0), " != input map size ", map.n_in);
   return HipPoolingFunction::apply(features, map.nbr, map.out_order, map.nbr_t, map.in_order,
                                    map.n_out, pool_reduction(mode));
+}
+
+at::Tensor hip_group_reduce(const at::Tensor &features, const at::Tensor &group,
+                            int64_t n_groups, int32_t reduction) {
+  TORCH_CHECK(features.is_cuda() && group.is_cuda(), "features and groups must be device tensors");
+  TORCH_CHECK(features.dim() == 2 && group.dim() == 1 && group.size(0) == features.size(0),
+              "one group per feature row");
+  const auto dev = features.device();
+  at::DeviceGuard guard(dev);
+  const hipStream_t st = stream_of(dev);
+  const int64_t n = features.size(0);
+  auto g = group.to(torch::kInt32).contiguous();
+  size_t bytes = 0;
+  check_rhip(rhip_stride_map_workspace_bytes(n, n_groups, &bytes),
+             "rhip_stride_map_workspace_bytes");
+  auto ws = byte_buffer(bytes, dev);
+  int32_t kmax = 0;
+  check_rhip(rhip_group_map_count(g.data_ptr<int32_t>(), n, n_groups, ws.data_ptr(), ws.numel(),
+                                  &kmax, st),
+             "rhip_group_map_count");
+  auto iopt = torch::TensorOptions().dtype(torch::kInt32).device(dev);
+  const int64_t K = std::max<int32_t>(kmax, 1);
+  auto nbr = kmax > 0 ? torch::empty({K, std::max<int64_t>(n_groups, 1)}, iopt)
+                      : torch::full({K, std::max<int64_t>(n_groups, 1)}, -1, iopt);
+  auto nbr_t = kmax > 0 ? torch::empty({1, std::max<int64_t>(n, 1)}, iopt)
+                        : torch::full({1, std::max<int64_t>(n, 1)}, -1, iopt);
+  auto pairs = torch::empty({2, std::max<int64_t>(n, 1)}, iopt);
+  check_rhip(rhip_stride_map_fill(n, n_groups, kmax, nullptr, nullptr, ws.data_ptr(), ws.numel(),
+                                  nbr.data_ptr<int32_t>(), nbr_t.data_ptr<int32_t>(),
+                                  pairs[0].data_ptr<int32_t>(), pairs[1].data_ptr<int32_t>(), st),
+             "rhip_stride_map_fill");
+  auto row_order = torch::empty({0}, iopt); // row order on both sides
+  return HipPoolingFunction::apply(features, nbr.slice(1, 0, n_groups), row_order,
+                                   nbr_t.slice(1, 0, n), row_order, n_groups, reduction);
 }
 
 // ------------------------------------------------------------ layers

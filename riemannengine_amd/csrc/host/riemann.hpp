@@ -189,8 +189,9 @@ struct CoordinateMapHIP {
 
 // A kernel map: per-offset pair lists (CSR) plus the dense neighbour tables
 // and processing orders the convolution kernels consume. A pooling stride map
-// (stride_map set) has the reference's single pair list (offsets = [0, P, ...,
-// P]) and neighbour tables K rows high, K = most inputs on one output.
+// (stride_map set) has the reference's single pair list (offsets = [0, P]),
+// an nbr K rows high (K = most inputs on one output) and a one-row nbr_t
+// (each input has one output); swapped() exchanges the two tables.
 struct HipKernelMap {
   int32_t K = 0;
   bool stride_map = false;
@@ -309,6 +310,10 @@ public:
   SparseTensor operator+(at::Scalar scalar) const;
   SparseTensor operator*(at::Scalar scalar) const;
   SparseTensor to(c10::ScalarType dtype) const;
+  // Re-hash onto `device` (RiemannEngine/engine/tensor/sparse_tensor.cpp:
+  // 397-429): a new manager holding this map's rows, features aligned to its
+  // representative rows. Device targets only (there is no CPU manager).
+  SparseTensor to(torch::Device device) const;
   SparseTensor detach() const;
 
 private:
@@ -455,6 +460,12 @@ TORCH_MODULE(RiemannReLU);
 // kernels (autograd-aware): mode LOCAL_{SUM,AVG,MAX}_POOLING.
 at::Tensor hip_sparse_pooling(const at::Tensor &features, const HipKernelMap &map,
                               PoolingMode::Type mode);
+
+// Reduce feature rows by group (rows with equal group[i] in [0, n_groups)),
+// reduction RHIP_POOL_SUM / AVG / MAX, through the group map and the pooling
+// kernels (autograd-aware); features fp32 or bf16 on the device.
+at::Tensor hip_group_reduce(const at::Tensor &features, const at::Tensor &group,
+                            int64_t n_groups, int32_t reduction);
 
 class RiemannPoolingBaseImpl : public torch::nn::Cloneable<RiemannPoolingBaseImpl> {
 public:

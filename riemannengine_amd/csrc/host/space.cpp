@@ -515,7 +515,8 @@ HipKernelMap CoordinateManager::generate_stride_map(const CoordinateMapHIP &in_m
                     : torch::full({m.K, std::max<int64_t>(cols, 1)}, -1, iopt);
   };
   auto nbr = table(n_out);
-  auto nbr_t = table(n_in);
+  auto nbr_t = kmax > 0 ? torch::empty({1, std::max<int64_t>(n_in, 1)}, iopt)
+                        : torch::full({1, std::max<int64_t>(n_in, 1)}, -1, iopt);
   auto in_rows = torch::empty({std::max<int64_t>(n_in, 1)}, iopt);
   auto out_rows = torch::empty({std::max<int64_t>(n_in, 1)}, iopt);
   check_rhip(rhip_stride_map_fill(n_in, n_out, kmax, in_map.order.data_ptr<int32_t>(),
@@ -523,8 +524,7 @@ HipKernelMap CoordinateManager::generate_stride_map(const CoordinateMapHIP &in_m
                                   nbr.data_ptr<int32_t>(), nbr_t.data_ptr<int32_t>(),
                                   in_rows.data_ptr<int32_t>(), out_rows.data_ptr<int32_t>(), st),
              "rhip_stride_map_fill");
-  m.offsets_host.assign(m.K + 1, n_in);
-  m.offsets_host[0] = 0;
+  m.offsets_host = {0, n_in}; // the reference's single pair list
   m.offsets = torch::tensor(m.offsets_host, torch::kInt64).to(dev);
   m.in_rows = in_rows.slice(0, 0, n_in);
   m.out_rows = out_rows.slice(0, 0, n_in);

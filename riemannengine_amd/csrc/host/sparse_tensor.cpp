@@ -72,6 +72,23 @@ SparseTensor SparseTensor::to(c10::ScalarType dtype) const {
   return SparseTensor(features_.to(dtype), key_, manager_);
 }
 
+SparseTensor SparseTensor::to(torch::Device device) const {
+  TORCH_CHECK(device.is_cuda(),
+              "this build keeps sparse tensors on the device (HIP) coordinate manager; "
+              "there is no CPU manager to move to");
+  at::DeviceGuard guard(device);
+  auto coordinates = C().to(device).contiguous();
+  auto moved = features_.to(device);
+  auto manager = std::make_shared<CoordinateManager>(dimension_, CoordinateMapBackend::CUDA);
+  const auto key = key_.get_key();
+  auto inserted = manager->insert_and_map(coordinates, key.first, key.second);
+  const auto &first_rows = inserted.second.first;
+  TORCH_CHECK(first_rows.numel() == manager->size(inserted.first),
+              "Coordinate map representative rows do not match map size");
+  return SparseTensor(moved.index_select(0, first_rows.to(device, torch::kLong)),
+                      std::move(inserted.first), std::move(manager));
+}
+
 SparseTensor SparseTensor::detach() const {
   return SparseTensor(features_.detach(), key_, manager_);
 }
@@ -92,6 +109,30 @@ at::Tensor SparseTensor::quantize_features(const at::Tensor &features,
     return features.index_select(0, rows);
   case SparseTensorQuantizationMode::NO_QUANTIZATION:
     return features;
+  default:
+    break;
+  }
+  switch (mode) {
+  case SparseTensorQuantizationMode::UNWEIGHTED_SUM:
+  case SparseTensorQuantizationMode::UNWEIGHTED_AVERAGE:
+  case SparseTensorQuantizationMode::MAX_POOL:
+    // fp32 / bf16 device features: the group map and the pooling kernels
+    // (deterministic; the max gradient is shared as scatter_reduce's, the
+    // zero it starts from counting as a tie); other dtypes use torch's
+    // index_add_ / scatter_reduce on the device, as the reference does
+    if (features.is_cuda() && (features.scalar_type() == torch::kFloat ||
+                               features.scalar_type() == torch::kBFloat16))
+      return hip_group_reduce(features, inv, unique_count,
+                              mode == SparseTensorQuantizationMode::UNWEIGHTED_SUM
+                                  ? RHIP_POOL_SUM
+                                  : (mode == SparseTensorQuantizationMode::UNWEIGHTED_AVERAGE
+                                         ? RHIP_POOL_AVG
+                                         : RHIP_POOL_MAX_SCATTER));
+    break;
+  default:
+    break;
+  }
+  switch (mode) {
   case SparseTensorQuantizationMode::UNWEIGHTED_SUM:
   case SparseTensorQuantizationMode::UNWEIGHTED_AVERAGE: {
     auto result = torch::zeros({unique_count, features.size(1)}, features.options());
@@ -107,6 +148,8 @@ at::Tensor SparseTensor::quantize_features(const at::Tensor &features,
     return at::scatter_reduce(result, 0, inv.unsqueeze(1).expand_as(features), features, "amax",
                               false);
   }
+  default:
+    break;
   }
   TORCH_CHECK(false, "Unknown quantization mode");
 }

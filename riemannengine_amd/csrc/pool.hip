@@ -37,16 +37,32 @@ static int bit_width_u64(uint64_t v) { return v == 0 ? 0 : 64 - __builtin_clzll(
 // 8 bf16), or V = 1 for rows whose width is not a multiple of 16 bytes.
 template <typename T, int V> struct Slice;
 
+// Raw is the loaded 16 bytes (kept in registers until reduced): load_raw
+// then widen = load.
 template <> struct Slice<float, 4> {
-  __device__ static __forceinline__ void load(const float *p, float *v) {
-    const float4 f = *reinterpret_cast<const float4 *>(p);
+  using Raw = float4;
+  __device__ static __forceinline__ Raw load_raw(const float *p) {
+    return *reinterpret_cast<const float4 *>(p);
+  }
+  __device__ static __forceinline__ void widen(const Raw &f, float *v) {
     v[0] = f.x, v[1] = f.y, v[2] = f.z, v[3] = f.w;
   }
+  __device__ static __forceinline__ void load(const float *p, float *v) { widen(load_raw(p), v); }
   __device__ static __forceinline__ void store(float *p, const float *v) {
     *reinterpret_cast<float4 *>(p) = make_float4(v[0], v[1], v[2], v[3]);
   }
 };
 template <> struct Slice<float, 8> {
+  struct Raw {
+    float4 a, b;
+  };
+  __device__ static __forceinline__ Raw load_raw(const float *p) {
+    return {Slice<float, 4>::load_raw(p), Slice<float, 4>::load_raw(p + 4)};
+  }
+  __device__ static __forceinline__ void widen(const Raw &r, float *v) {
+    Slice<float, 4>::widen(r.a, v);
+    Slice<float, 4>::widen(r.b, v + 4);
+  }
   __device__ static __forceinline__ void load(const float *p, float *v) {
     Slice<float, 4>::load(p, v);
     Slice<float, 4>::load(p + 4, v + 4);
@@ -57,13 +73,19 @@ template <> struct Slice<float, 8> {
   }
 };
 template <> struct Slice<float, 1> {
+  using Raw = float;
+  __device__ static __forceinline__ Raw load_raw(const float *p) { return *p; }
+  __device__ static __forceinline__ void widen(const Raw &f, float *v) { v[0] = f; }
   __device__ static __forceinline__ void load(const float *p, float *v) { v[0] = *p; }
   __device__ static __forceinline__ void store(float *p, const float *v) { *p = v[0]; }
 };
 template <> struct Slice<__bf16, 8> {
+  using Raw = uint4;
+  __device__ static __forceinline__ Raw load_raw(const __bf16 *p) {
+    return *reinterpret_cast<const uint4 *>(p);
+  }
   // bf16 -> fp32 is exact: the 16 bits become the high half of the float.
-  __device__ static __forceinline__ void load(const __bf16 *p, float *v) {
-    const uint4 u = *reinterpret_cast<const uint4 *>(p);
+  __device__ static __forceinline__ void widen(const Raw &u, float *v) {
     const uint32_t w[4] = {u.x, u.y, u.z, u.w};
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -71,6 +93,7 @@ template <> struct Slice<__bf16, 8> {
       v[2 * j + 1] = __uint_as_float(w[j] & 0xffff0000u);
     }
   }
+  __device__ static __forceinline__ void load(const __bf16 *p, float *v) { widen(load_raw(p), v); }
   // fp32 -> bf16 rounds to nearest even
   __device__ static __forceinline__ void store(__bf16 *p, const float *v) {
     uint32_t w[4];
@@ -84,6 +107,11 @@ template <> struct Slice<__bf16, 8> {
   }
 };
 template <> struct Slice<__bf16, 1> {
+  using Raw = __bf16;
+  __device__ static __forceinline__ Raw load_raw(const __bf16 *p) { return *p; }
+  __device__ static __forceinline__ void widen(const Raw &f, float *v) {
+    v[0] = static_cast<float>(f);
+  }
   __device__ static __forceinline__ void load(const __bf16 *p, float *v) {
     v[0] = static_cast<float>(*p);
   }
@@ -102,16 +130,27 @@ template <int MODE> __device__ __forceinline__ float pool_init() {
 }
 
 // -------------------------------------------------------- local pooling
+//
+// Thread t = tile * 256 + threadIdx.x owns processing position j = t / lpr
+// and channels [(t % lpr) * V, +V); tiles come from xcd_tile, so runs of
+// neighbouring positions (which gather the same rows) share an XCD's L2.
+// The neighbour loop reads kChunk table entries first, then issues the
+// chunk's gathers (each under its own lane mask), then reduces: up to kChunk
+// row loads in flight per thread instead of one.
+constexpr int kChunk = 8;
+
+__device__ __forceinline__ int64_t pool_thread(int lane) {
+  return xcd_tile(blockIdx.x) * static_cast<int64_t>(kPoolThreads) + lane;
+}
 
 // y[o] = reduce over k of x[nbr[k*n_out+j]] for the output o = order[j] at
-// processing position j; counts[o] = number of rows pooled. Thread t owns
-// position j = t / lpr and channels [(t % lpr) * V, +V).
+// processing position j; counts[o] = number of rows pooled.
 template <typename T, int MODE, int V>
 __global__ __launch_bounds__(kPoolThreads) void pool_fwd_kernel(
     const T *__restrict__ x, int C, int lpr, const int32_t *__restrict__ nbr, int K,
     int64_t n_out, const int32_t *__restrict__ order, T *__restrict__ y,
     int32_t *__restrict__ counts) {
-  const int64_t t = blockIdx.x * static_cast<int64_t>(kPoolThreads) + threadIdx.x;
+  const int64_t t = pool_thread(threadIdx.x);
   const int64_t j = t / lpr;
   if (j >= n_out)
     return;
@@ -122,16 +161,27 @@ __global__ __launch_bounds__(kPoolThreads) void pool_fwd_kernel(
   for (int e = 0; e < V; ++e)
     acc[e] = pool_init<MODE>();
   int cnt = 0;
-  for (int k = 0; k < K; ++k) {
-    const int32_t i = nbr[k * n_out + j];
-    if (i < 0)
-      continue;
-    ++cnt;
-    float v[V];
-    Slice<T, V>::load(x + static_cast<int64_t>(i) * C + c0, v);
+  for (int k0 = 0; k0 < K; k0 += kChunk) {
+    int32_t idx[kChunk];
 #pragma unroll
-    for (int e = 0; e < V; ++e)
-      acc[e] = MODE == RHIP_POOL_MAX ? max_nan(acc[e], v[e]) : acc[e] + v[e];
+    for (int u = 0; u < kChunk; ++u)
+      idx[u] = k0 + u < K ? nbr[(k0 + u) * n_out + j] : -1;
+    typename Slice<T, V>::Raw raw[kChunk];
+#pragma unroll
+    for (int u = 0; u < kChunk; ++u)
+      if (idx[u] >= 0)
+        raw[u] = Slice<T, V>::load_raw(x + static_cast<int64_t>(idx[u]) * C + c0);
+#pragma unroll
+    for (int u = 0; u < kChunk; ++u) {
+      if (idx[u] < 0)
+        continue;
+      ++cnt;
+      float v[V];
+      Slice<T, V>::widen(raw[u], v);
+#pragma unroll
+      for (int e = 0; e < V; ++e)
+        acc[e] = MODE == RHIP_POOL_MAX ? max_nan(acc[e], v[e]) : acc[e] + v[e];
+    }
   }
   float out[V];
 #pragma unroll
@@ -145,12 +195,13 @@ __global__ __launch_bounds__(kPoolThreads) void pool_fwd_kernel(
 
 // Max-pooling gradient share per output channel: gs[o][c] = gy[o][c] / (number
 // of pooled rows whose value equals y[o][c]), 0 when none does.
+// zero_tie: one more tie where y[o][c] == 0 (RHIP_POOL_MAX_SCATTER).
 template <typename T, int V>
 __global__ __launch_bounds__(kPoolThreads) void pool_maxshare_kernel(
     const T *__restrict__ gy, const T *__restrict__ x, const T *__restrict__ y, int C, int lpr,
     const int32_t *__restrict__ nbr, int K, int64_t n_out, const int32_t *__restrict__ order,
-    float *__restrict__ gs) {
-  const int64_t t = blockIdx.x * static_cast<int64_t>(kPoolThreads) + threadIdx.x;
+    int zero_tie, float *__restrict__ gs) {
+  const int64_t t = pool_thread(threadIdx.x);
   const int64_t j = t / lpr;
   if (j >= n_out)
     return;
@@ -160,16 +211,27 @@ __global__ __launch_bounds__(kPoolThreads) void pool_maxshare_kernel(
   Slice<T, V>::load(y + o * C + c0, yv);
 #pragma unroll
   for (int e = 0; e < V; ++e)
-    cnt[e] = 0.f;
-  for (int k = 0; k < K; ++k) {
-    const int32_t i = nbr[k * n_out + j];
-    if (i < 0)
-      continue;
-    float v[V];
-    Slice<T, V>::load(x + static_cast<int64_t>(i) * C + c0, v);
+    cnt[e] = (zero_tie && yv[e] == 0.f) ? 1.f : 0.f;
+  for (int k0 = 0; k0 < K; k0 += kChunk) {
+    int32_t idx[kChunk];
 #pragma unroll
-    for (int e = 0; e < V; ++e)
-      cnt[e] += v[e] == yv[e] ? 1.f : 0.f;
+    for (int u = 0; u < kChunk; ++u)
+      idx[u] = k0 + u < K ? nbr[(k0 + u) * n_out + j] : -1;
+    typename Slice<T, V>::Raw raw[kChunk];
+#pragma unroll
+    for (int u = 0; u < kChunk; ++u)
+      if (idx[u] >= 0)
+        raw[u] = Slice<T, V>::load_raw(x + static_cast<int64_t>(idx[u]) * C + c0);
+#pragma unroll
+    for (int u = 0; u < kChunk; ++u) {
+      if (idx[u] < 0)
+        continue;
+      float v[V];
+      Slice<T, V>::widen(raw[u], v);
+#pragma unroll
+      for (int e = 0; e < V; ++e)
+        cnt[e] += v[e] == yv[e] ? 1.f : 0.f;
+    }
   }
   float g[V], share[V];
   Slice<T, V>::load(gy + o * C + c0, g);
@@ -188,7 +250,7 @@ __global__ __launch_bounds__(kPoolThreads) void pool_bwd_kernel(
     const T *__restrict__ y, int C, int lpr, const int32_t *__restrict__ nbr_t, int K,
     int64_t n_in, const int32_t *__restrict__ order, const int32_t *__restrict__ counts,
     T *__restrict__ gx) {
-  const int64_t t = blockIdx.x * static_cast<int64_t>(kPoolThreads) + threadIdx.x;
+  const int64_t t = pool_thread(threadIdx.x);
   const int64_t j = t / lpr;
   if (j >= n_in)
     return;
@@ -200,24 +262,54 @@ __global__ __launch_bounds__(kPoolThreads) void pool_bwd_kernel(
     acc[e] = 0.f;
   if (MODE == RHIP_POOL_MAX)
     Slice<T, V>::load(x + i * C + c0, xv);
-  for (int k = 0; k < K; ++k) {
-    const int32_t o = nbr_t[k * n_in + j];
-    if (o < 0)
-      continue;
-    float v[V];
+  // max keeps two slices (y and the fp32 share) per entry: half the chunk
+  constexpr int CH = MODE == RHIP_POOL_MAX ? kChunk / 2 : kChunk;
+  for (int k0 = 0; k0 < K; k0 += CH) {
+    int32_t idx[CH];
+#pragma unroll
+    for (int u = 0; u < CH; ++u)
+      idx[u] = k0 + u < K ? nbr_t[(k0 + u) * n_in + j] : -1;
     if (MODE == RHIP_POOL_MAX) {
-      float yv[V];
-      Slice<T, V>::load(y + static_cast<int64_t>(o) * C + c0, yv);
-      Slice<float, V>::load(gs + static_cast<int64_t>(o) * C + c0, v);
+      typename Slice<T, V>::Raw yraw[CH];
+      typename Slice<float, V>::Raw sraw[CH];
 #pragma unroll
-      for (int e = 0; e < V; ++e)
-        acc[e] += xv[e] == yv[e] ? v[e] : 0.f;
+      for (int u = 0; u < CH; ++u) {
+        if (idx[u] >= 0) {
+          yraw[u] = Slice<T, V>::load_raw(y + static_cast<int64_t>(idx[u]) * C + c0);
+          sraw[u] = Slice<float, V>::load_raw(gs + static_cast<int64_t>(idx[u]) * C + c0);
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < CH; ++u) {
+        if (idx[u] < 0)
+          continue;
+        float yv[V], sv[V];
+        Slice<T, V>::widen(yraw[u], yv);
+        Slice<float, V>::widen(sraw[u], sv);
+#pragma unroll
+        for (int e = 0; e < V; ++e)
+          acc[e] += xv[e] == yv[e] ? sv[e] : 0.f;
+      }
     } else {
-      Slice<T, V>::load(gy + static_cast<int64_t>(o) * C + c0, v);
-      const float n = MODE == RHIP_POOL_AVG ? static_cast<float>(counts[o]) : 1.f;
+      typename Slice<T, V>::Raw raw[CH];
+      float n[CH];
 #pragma unroll
-      for (int e = 0; e < V; ++e)
-        acc[e] += MODE == RHIP_POOL_AVG ? v[e] / n : v[e];
+      for (int u = 0; u < CH; ++u) {
+        if (idx[u] >= 0) {
+          raw[u] = Slice<T, V>::load_raw(gy + static_cast<int64_t>(idx[u]) * C + c0);
+          n[u] = MODE == RHIP_POOL_AVG ? static_cast<float>(counts[idx[u]]) : 1.f;
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < CH; ++u) {
+        if (idx[u] < 0)
+          continue;
+        float v[V];
+        Slice<T, V>::widen(raw[u], v);
+#pragma unroll
+        for (int e = 0; e < V; ++e)
+          acc[e] += MODE == RHIP_POOL_AVG ? v[e] / n[u] : v[e];
+      }
     }
   }
   Slice<T, V>::store(gx + i * C + c0, acc);
@@ -248,6 +340,24 @@ __global__ __launch_bounds__(kPoolThreads) void stride_lookup_kernel(
   vals[i] = static_cast<int32_t>(i);
 }
 
+// keys[i] = group[i], vals[i] = i; a group outside [0, n_groups) counts in
+// miss[0] and its row goes to miss[1].
+__global__ __launch_bounds__(kPoolThreads) void group_keys_kernel(
+    const int32_t *__restrict__ group, int64_t n, int64_t n_groups, uint32_t *__restrict__ keys,
+    int32_t *__restrict__ vals, unsigned long long *__restrict__ miss) {
+  const int64_t i = blockIdx.x * static_cast<int64_t>(kPoolThreads) + threadIdx.x;
+  if (i >= n)
+    return;
+  const int32_t g = group[i];
+  const bool ok = g >= 0 && g < n_groups;
+  if (!ok) {
+    atomicAdd(&miss[0], 1ull);
+    atomicMin(&miss[1], static_cast<unsigned long long>(i));
+  }
+  keys[i] = ok ? static_cast<uint32_t>(g) : 0u;
+  vals[i] = static_cast<int32_t>(i);
+}
+
 // start[o] = first sorted position of output o.
 __global__ __launch_bounds__(kPoolThreads) void group_start_kernel(
     const uint32_t *__restrict__ skeys, int64_t n, int32_t *__restrict__ start) {
@@ -266,19 +376,38 @@ __device__ __forceinline__ int wave_max(int v) {
   return v;
 }
 
+// Maximum over the workgroup (every thread gets it).
+__device__ __forceinline__ int block_max(int v) {
+  __shared__ int red[kPoolThreads / kWave];
+  v = wave_max(v);
+  if (lane_id() == 0)
+    red[threadIdx.x / kWave] = v;
+  __syncthreads();
+  int m = red[0];
+#pragma unroll
+  for (int w = 1; w < kPoolThreads / kWave; ++w)
+    m = max(m, red[w]);
+  return m;
+}
+
+// Grid of the reductions below: grid-stride loops over at most this many
+// workgroups, one atomic each (atomics on one address serialise).
+constexpr int kReduceBlocks = 512;
+
 // rank[s] = position of sorted entry s within its output's group; kmax =
-// largest group size (one atomic per wave).
+// largest group size.
 __global__ __launch_bounds__(kPoolThreads) void group_rank_kernel(
     const uint32_t *__restrict__ skeys, int64_t n, const int32_t *__restrict__ start,
     int32_t *__restrict__ rank, int32_t *__restrict__ kmax) {
-  const int64_t s = blockIdx.x * static_cast<int64_t>(kPoolThreads) + threadIdx.x;
-  int r = 0;
-  if (s < n) {
-    r = static_cast<int>(s - start[skeys[s]]);
+  int m = 0;
+  for (int64_t s = blockIdx.x * static_cast<int64_t>(kPoolThreads) + threadIdx.x; s < n;
+       s += static_cast<int64_t>(gridDim.x) * kPoolThreads) {
+    const int r = static_cast<int>(s - start[skeys[s]]);
     rank[s] = r;
+    m = max(m, r + 1);
   }
-  const int m = wave_max(s < n ? r + 1 : 0);
-  if (lane_id() == 0 && m > 0)
+  m = block_max(m);
+  if (threadIdx.x == 0 && m > 0)
     atomicMax(kmax, m);
 }
 
@@ -305,8 +434,9 @@ __global__ __launch_bounds__(kPoolThreads) void fill_i32_kernel(int32_t *__restr
     p[i] = v;
 }
 
-// Tables by processing position: nbr column pos_out[o], nbr_t column
-// pos_in[i]. Rows past k_max (a k_max smaller than phase 1 found) are not
+// Tables by processing position: nbr column pos_out[o] (row = rank within
+// the output's group), nbr_t column pos_in[i] (one row: each input has one
+// output). Ranks past k_max (a k_max smaller than phase 1 found) are not
 // written.
 __global__ __launch_bounds__(kPoolThreads) void stride_scatter_kernel(
     const uint32_t *__restrict__ skeys, const int32_t *__restrict__ svals,
@@ -323,7 +453,7 @@ __global__ __launch_bounds__(kPoolThreads) void stride_scatter_kernel(
   if (r >= k_max || o >= n_out)
     return;
   nbr[r * n_out + (pos_out ? pos_out[o] : o)] = i;
-  nbr_t[r * n_in + (pos_in ? pos_in[i] : i)] = o;
+  nbr_t[pos_in ? pos_in[i] : i] = o;
   in_rows[s] = i;
   out_rows[s] = o;
 }
@@ -332,9 +462,12 @@ __global__ __launch_bounds__(kPoolThreads) void stride_scatter_kernel(
 
 __global__ __launch_bounds__(kPoolThreads) void batch_max_kernel(
     const int32_t *__restrict__ coords, int64_t n, int ncol, int32_t *__restrict__ bmax) {
-  const int64_t i = blockIdx.x * static_cast<int64_t>(kPoolThreads) + threadIdx.x;
-  const int m = wave_max(i < n ? coords[i * ncol] : INT_MIN);
-  if (lane_id() == 0 && m != INT_MIN)
+  int m = INT_MIN;
+  for (int64_t i = blockIdx.x * static_cast<int64_t>(kPoolThreads) + threadIdx.x; i < n;
+       i += static_cast<int64_t>(gridDim.x) * kPoolThreads)
+    m = max(m, coords[i * ncol]);
+  m = block_max(m);
+  if (threadIdx.x == 0 && m != INT_MIN)
     atomicMax(bmax, m);
 }
 
@@ -540,9 +673,11 @@ void check_dtype(int32_t dtype) {
     throw Error(RHIP_ERR_UNSUPPORTED, "dtype must be RHIP_F32 or RHIP_BF16");
 }
 
-void check_mode(int32_t mode) {
-  if (mode != RHIP_POOL_SUM && mode != RHIP_POOL_AVG && mode != RHIP_POOL_MAX)
-    throw Error(RHIP_ERR_INVALID, "mode must be RHIP_POOL_SUM, RHIP_POOL_AVG or RHIP_POOL_MAX");
+void check_mode(int32_t mode, bool local = true) {
+  if (mode != RHIP_POOL_SUM && mode != RHIP_POOL_AVG && mode != RHIP_POOL_MAX &&
+      !(local && mode == RHIP_POOL_MAX_SCATTER))
+    throw Error(RHIP_ERR_INVALID, local ? "mode must be RHIP_POOL_SUM, _AVG, _MAX or _MAX_SCATTER"
+                                        : "mode must be RHIP_POOL_SUM, _AVG or _MAX");
 }
 
 bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
@@ -565,6 +700,14 @@ unsigned grid_for(int64_t threads) {
   return static_cast<unsigned>(blocks < 1 ? 1 : blocks);
 }
 
+// Workgroups of the local-pooling kernels: whole XCD runs (pool_thread).
+unsigned pool_grid(int64_t threads) {
+  const int64_t blocks = xcd_grid(ceil_div(std::max<int64_t>(threads, 1), kPoolThreads));
+  if (blocks > INT_MAX)
+    throw Error(RHIP_ERR_UNSUPPORTED, "launch exceeds the grid limit");
+  return static_cast<unsigned>(blocks);
+}
+
 // Dispatch f<V>() on the slice width.
 template <typename T, typename F> void with_width(int V, F &&f) {
   if (V == 1)
@@ -572,6 +715,7 @@ template <typename T, typename F> void with_width(int V, F &&f) {
   else
     f(std::integral_constant<int, 16 / sizeof(T)>{});
 }
+// RHIP_POOL_MAX_SCATTER runs the max kernels (its zero tie is a flag).
 template <typename F> void with_mode(int32_t mode, F &&f) {
   if (mode == RHIP_POOL_SUM)
     f(std::integral_constant<int, RHIP_POOL_SUM>{});
@@ -669,6 +813,34 @@ void global_reduce(const T *x, const T *ref, int C, const int32_t *members, cons
   RHIP_LAUNCH_CHECK();
 }
 
+// Shared tail of the stride-map and group-map counts: sort (key, row) by key,
+// rank rows within their key's group, read back the miss count and the
+// largest group (one synchronisation). `message(row, count)` names a miss.
+template <typename Msg>
+int32_t group_rows(StrideWs &w, int64_t n, int64_t n_groups, hipStream_t stream, Msg message) {
+  const unsigned grid = grid_for(n);
+  sort_pairs_u32(w.sort_tmp, w.sort_bytes, w.keys, w.skeys, w.vals, w.svals, n,
+                 bit_width_u64(static_cast<uint64_t>(n_groups - 1)), stream);
+  hipLaunchKernelGGL(group_start_kernel, dim3(grid), dim3(kPoolThreads), 0, stream, w.skeys, n,
+                     w.start);
+  RHIP_LAUNCH_CHECK();
+  hipLaunchKernelGGL(group_rank_kernel, dim3(std::min<unsigned>(grid, kReduceBlocks)),
+                     dim3(kPoolThreads), 0, stream, w.skeys, n, w.start, w.rank, w.kmax);
+  RHIP_LAUNCH_CHECK();
+  unsigned long long miss[2];
+  int32_t kmax = 0;
+  RHIP_HIP(hipMemcpyAsync(miss, w.miss, sizeof(miss), hipMemcpyDeviceToHost, stream));
+  RHIP_HIP(hipMemcpyAsync(&kmax, w.kmax, sizeof(kmax), hipMemcpyDeviceToHost, stream));
+  RHIP_HIP(hipStreamSynchronize(stream));
+  if (miss[0] != 0)
+    throw Error(RHIP_ERR_INVALID, message(miss[1], miss[0]));
+  const int64_t cells = static_cast<int64_t>(kmax) * std::max(n, n_groups);
+  if (cells > (int64_t{1} << 31))
+    throw Error(RHIP_ERR_UNSUPPORTED, std::to_string(kmax) +
+                                          " rows in one group make the neighbour table too large");
+  return kmax;
+}
+
 } // namespace
 } // namespace rhip
 
@@ -717,30 +889,39 @@ extern "C" int rhip_stride_map_count(const rhip_table *out_table, const int32_t 
     hipLaunchKernelGGL(stride_lookup_kernel, dim3(grid), dim3(kPoolThreads), 0, stream,
                        make_view(*out_table), in_coords, n_in, st, w.keys, w.vals, w.miss);
     RHIP_LAUNCH_CHECK();
-    sort_pairs_u32(w.sort_tmp, w.sort_bytes, w.keys, w.skeys, w.vals, w.svals, n_in,
-                   bit_width_u64(static_cast<uint64_t>(n_out - 1)), stream);
-    hipLaunchKernelGGL(group_start_kernel, dim3(grid), dim3(kPoolThreads), 0, stream, w.skeys,
-                       n_in, w.start);
+    *k_max_host = group_rows(w, n_in, n_out, stream, [](unsigned long long row,
+                                                        unsigned long long count) {
+      return "Invalid out_coordinate_map: input row " + std::to_string(row) +
+             " has no floor-aligned output row (" + std::to_string(count) + " such rows)";
+    });
+  });
+}
+
+extern "C" int rhip_group_map_count(const int32_t *group, int64_t n, int64_t n_groups,
+                                    void *workspace, size_t ws_bytes, int32_t *k_max_host,
+                                    hipStream_t stream) {
+  return guarded([&] {
+    RHIP_CHECK_ARG(k_max_host != nullptr, "k_max_host is null");
+    RHIP_CHECK_ARG(n >= 0 && n < INT_MAX && n_groups >= 0 && n_groups < INT_MAX, "bad sizes");
+    *k_max_host = 0;
+    if (n == 0)
+      return;
+    RHIP_CHECK_ARG(n_groups >= 1, "rows but no groups");
+    RHIP_CHECK_ARG(group != nullptr && workspace != nullptr, "group and workspace required");
+    Carve cv(workspace, ws_bytes);
+    StrideWs w = carve_stride(cv, n, n_groups);
+    hipLaunchKernelGGL(fill_i32_kernel, dim3(1), dim3(kPoolThreads), 0, stream, w.kmax, 1, 0);
     RHIP_LAUNCH_CHECK();
-    hipLaunchKernelGGL(group_rank_kernel, dim3(grid), dim3(kPoolThreads), 0, stream, w.skeys,
-                       n_in, w.start, w.rank, w.kmax);
+    hipLaunchKernelGGL(miss_init_kernel, dim3(1), dim3(kWave), 0, stream, w.miss);
     RHIP_LAUNCH_CHECK();
-    unsigned long long miss[2];
-    int32_t kmax = 0;
-    RHIP_HIP(hipMemcpyAsync(miss, w.miss, sizeof(miss), hipMemcpyDeviceToHost, stream));
-    RHIP_HIP(hipMemcpyAsync(&kmax, w.kmax, sizeof(kmax), hipMemcpyDeviceToHost, stream));
-    RHIP_HIP(hipStreamSynchronize(stream));
-    if (miss[0] != 0)
-      throw Error(RHIP_ERR_INVALID,
-                  "Invalid out_coordinate_map: input row " + std::to_string(miss[1]) +
-                      " has no floor-aligned output row (" + std::to_string(miss[0]) +
-                      " such rows)");
-    const int64_t cells = static_cast<int64_t>(kmax) * std::max(n_in, n_out);
-    if (cells > (int64_t{1} << 31))
-      throw Error(RHIP_ERR_UNSUPPORTED,
-                  "stride map: " + std::to_string(kmax) +
-                      " inputs on one output make the neighbour table too large");
-    *k_max_host = kmax;
+    hipLaunchKernelGGL(group_keys_kernel, dim3(grid_for(n)), dim3(kPoolThreads), 0, stream, group,
+                       n, n_groups, w.keys, w.vals, w.miss);
+    RHIP_LAUNCH_CHECK();
+    *k_max_host = group_rows(w, n, n_groups, stream, [](unsigned long long row,
+                                                        unsigned long long count) {
+      return "group of row " + std::to_string(row) + " is outside [0, n_groups) (" +
+             std::to_string(count) + " such rows)";
+    });
   });
 }
 
@@ -757,12 +938,9 @@ extern "C" int rhip_stride_map_fill(int64_t n_in, int64_t n_out, int32_t k_max,
     RHIP_CHECK_ARG(nbr && nbr_t && in_rows && out_rows && workspace, "outputs are required");
     Carve cv(workspace, ws_bytes);
     StrideWs w = carve_stride(cv, n_in, n_out);
-    const int64_t nn = static_cast<int64_t>(k_max) * n_out, nt = static_cast<int64_t>(k_max) * n_in;
+    const int64_t nn = static_cast<int64_t>(k_max) * n_out;
     hipLaunchKernelGGL(fill_i32_kernel, dim3(grid_for(nn)), dim3(kPoolThreads), 0, stream, nbr, nn,
                        -1);
-    RHIP_LAUNCH_CHECK();
-    hipLaunchKernelGGL(fill_i32_kernel, dim3(grid_for(nt)), dim3(kPoolThreads), 0, stream, nbr_t,
-                       nt, -1);
     RHIP_LAUNCH_CHECK();
     if (in_order != nullptr) {
       hipLaunchKernelGGL(invert_order_kernel, dim3(grid_for(n_in)), dim3(kPoolThreads), 0,
@@ -789,7 +967,7 @@ extern "C" int rhip_pool_workspace_bytes(int64_t n_out, int32_t C, int32_t mode,
     RHIP_CHECK_ARG(bytes != nullptr, "bytes is null");
     RHIP_CHECK_ARG(n_out >= 0 && C >= 1, "bad sizes");
     check_mode(mode);
-    *bytes = mode == RHIP_POOL_MAX ? align_up(sizeof(float) * n_out * C, 256) + 256 : 256;
+    *bytes = mode >= RHIP_POOL_MAX ? align_up(sizeof(float) * n_out * C, 256) + 256 : 256;
   });
 }
 
@@ -812,7 +990,7 @@ extern "C" int rhip_pool_forward(const void *x, int64_t n_in, int32_t C, const i
         with_width<T>(V, [&](auto v) {
           constexpr int M = decltype(m)::value, W = decltype(v)::value;
           const int lpr = C / W;
-          hipLaunchKernelGGL((pool_fwd_kernel<T, M, W>), dim3(grid_for(n_out * lpr)),
+          hipLaunchKernelGGL((pool_fwd_kernel<T, M, W>), dim3(pool_grid(n_out * lpr)),
                              dim3(kPoolThreads), 0, stream, static_cast<const T *>(x), C, lpr,
                              nbr, K, n_out, out_order, static_cast<T *>(y), counts);
           RHIP_LAUNCH_CHECK();
@@ -827,27 +1005,27 @@ extern "C" int rhip_pool_forward(const void *x, int64_t n_in, int32_t C, const i
 }
 
 extern "C" int rhip_pool_backward(const void *grad_y, const void *y, const void *x, int64_t n_out,
-                                  int32_t C, const int32_t *nbr, const int32_t *out_order,
-                                  const int32_t *nbr_t, int32_t K, const int32_t *in_order,
-                                  int64_t n_in, const int32_t *counts, int32_t mode, void *grad_x,
-                                  int32_t dtype, void *workspace, size_t ws_bytes,
-                                  hipStream_t stream) {
+                                  int32_t C, const int32_t *nbr, int32_t K,
+                                  const int32_t *out_order, const int32_t *nbr_t, int32_t K_t,
+                                  const int32_t *in_order, int64_t n_in, const int32_t *counts,
+                                  int32_t mode, void *grad_x, int32_t dtype, void *workspace,
+                                  size_t ws_bytes, hipStream_t stream) {
   return guarded([&] {
     check_dtype(dtype);
     check_mode(mode);
-    RHIP_CHECK_ARG(C >= 1 && K >= 0 && n_in >= 0 && n_out >= 0, "bad sizes");
+    RHIP_CHECK_ARG(C >= 1 && K >= 0 && K_t >= 0 && n_in >= 0 && n_out >= 0, "bad sizes");
     if (n_in == 0)
       return;
     RHIP_CHECK_ARG(grad_x != nullptr, "grad_x is null");
-    RHIP_CHECK_ARG(K == 0 || nbr_t != nullptr, "nbr_t is null");
+    RHIP_CHECK_ARG(K_t == 0 || nbr_t != nullptr, "nbr_t is null");
     RHIP_CHECK_ARG(n_out == 0 || grad_y != nullptr, "grad_y is null");
     RHIP_CHECK_ARG(mode != RHIP_POOL_AVG || n_out == 0 || counts != nullptr,
                    "average pooling needs the forward counts");
-    RHIP_CHECK_ARG(mode != RHIP_POOL_MAX || n_out == 0 ||
+    RHIP_CHECK_ARG(mode < RHIP_POOL_MAX || n_out == 0 ||
                        (x != nullptr && y != nullptr && nbr != nullptr && workspace != nullptr),
                    "max pooling needs x, y, nbr and the workspace");
     float *gs = nullptr;
-    if (mode == RHIP_POOL_MAX) {
+    if (mode >= RHIP_POOL_MAX) {
       Carve cv(workspace, ws_bytes);
       gs = cv.take<float>(std::max<int64_t>(n_out, 1) * C);
     }
@@ -859,16 +1037,16 @@ extern "C" int rhip_pool_backward(const void *grad_y, const void *y, const void 
           constexpr int M = decltype(m)::value, W = decltype(v)::value;
           const int lpr = C / W;
           if (M == RHIP_POOL_MAX && n_out > 0) {
-            hipLaunchKernelGGL((pool_maxshare_kernel<T, W>), dim3(grid_for(n_out * lpr)),
+            hipLaunchKernelGGL((pool_maxshare_kernel<T, W>), dim3(pool_grid(n_out * lpr)),
                                dim3(kPoolThreads), 0, stream, static_cast<const T *>(grad_y),
                                static_cast<const T *>(x), static_cast<const T *>(y), C, lpr, nbr,
-                               K, n_out, out_order, gs);
+                               K, n_out, out_order, mode == RHIP_POOL_MAX_SCATTER ? 1 : 0, gs);
             RHIP_LAUNCH_CHECK();
           }
-          hipLaunchKernelGGL((pool_bwd_kernel<T, M, W>), dim3(grid_for(n_in * lpr)),
+          hipLaunchKernelGGL((pool_bwd_kernel<T, M, W>), dim3(pool_grid(n_in * lpr)),
                              dim3(kPoolThreads), 0, stream, static_cast<const T *>(grad_y), gs,
                              static_cast<const T *>(x), static_cast<const T *>(y), C, lpr,
-                             nbr_t, n_out == 0 ? 0 : K, n_in, in_order, counts,
+                             nbr_t, n_out == 0 ? 0 : K_t, n_in, in_order, counts,
                              static_cast<T *>(grad_x));
           RHIP_LAUNCH_CHECK();
         });
@@ -908,8 +1086,8 @@ extern "C" int rhip_batch_count(const int32_t *coords, int64_t n, int32_t ncol, 
     hipLaunchKernelGGL(fill_i32_kernel, dim3(1), dim3(kPoolThreads), 0, stream, w.bmax, 1,
                        INT_MIN);
     RHIP_LAUNCH_CHECK();
-    hipLaunchKernelGGL(batch_max_kernel, dim3(grid_for(n)), dim3(kPoolThreads), 0, stream, coords,
-                       n, ncol, w.bmax);
+    hipLaunchKernelGGL(batch_max_kernel, dim3(std::min<unsigned>(grid_for(n), kReduceBlocks)),
+                       dim3(kPoolThreads), 0, stream, coords, n, ncol, w.bmax);
     RHIP_LAUNCH_CHECK();
     int32_t bmax = 0;
     RHIP_HIP(hipMemcpyAsync(&bmax, w.bmax, sizeof(bmax), hipMemcpyDeviceToHost, stream));
@@ -953,7 +1131,7 @@ extern "C" int rhip_global_pool_forward(const void *x, int64_t n, int32_t C,
                                         void *workspace, size_t ws_bytes, hipStream_t stream) {
   return guarded([&] {
     check_dtype(dtype);
-    check_mode(mode);
+    check_mode(mode, false);
     RHIP_CHECK_ARG(n >= 0 && C >= 1 && n_batches >= 0, "bad sizes");
     if (n_batches == 0)
       return;
@@ -991,7 +1169,7 @@ extern "C" int rhip_global_pool_backward(const void *grad_y, const void *y, cons
                                          hipStream_t stream) {
   return guarded([&] {
     check_dtype(dtype);
-    check_mode(mode);
+    check_mode(mode, false);
     RHIP_CHECK_ARG(n >= 0 && C >= 1 && n_batches >= 0 && ncol >= 1 && ncol <= RHIP_MAX_COLS,
                    "bad sizes");
     if (n == 0)

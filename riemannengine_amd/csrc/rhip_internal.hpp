@@ -216,6 +216,22 @@ struct StrideArg {
   int32_t s[RHIP_MAX_COLS];
 };
 
+// Workgroup id -> tile id. Workgroups are dealt to the 8 XCDs of an MI355X
+// round-robin (id b runs on XCD b % 8); this mapping hands each XCD runs of
+// kXcdRun consecutive tiles, so tiles that share neighbour rows share an L2,
+// while the runs stay interleaved over the whole map to keep the XCDs
+// balanced. The grid is padded to a multiple of 8 * kXcdRun (padding ids map
+// past the last tile).
+constexpr int kXcds = 8;
+constexpr int kXcdRun = 16;
+__device__ __forceinline__ int64_t xcd_tile(int64_t b) {
+  const int64_t x = b % kXcds, m = b / kXcds;
+  return ((m / kXcdRun) * kXcds + x) * kXcdRun + (m % kXcdRun);
+}
+inline int64_t xcd_grid(int64_t tiles) {
+  return ceil_div(tiles, kXcds * kXcdRun) * kXcds * kXcdRun;
+}
+
 // Lane index within the wave and wave-level prefix of a predicate.
 __device__ __forceinline__ int lane_id() { return __lane_id(); }
 

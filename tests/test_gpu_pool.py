@@ -31,7 +31,8 @@ def _bf16_round(a):
 def _check_table(km, in_to_out):
     """nbr / nbr_t of a stride map, columns by processing position (output
     out_order[p], input in_order[q]): every input in exactly one (k, out)
-    slot, nbr_t the transpose of nbr, inputs ascending within an output."""
+    slot, nbr_t (one row) each input's output, inputs ascending within an
+    output."""
     nbr, nbr_t = km.nbr.cpu().numpy(), km.nbr_t.cpu().numpy()
     oo, io = km.out_order.cpu().numpy(), km.in_order.cpu().numpy()
     K, n_out = nbr.shape
@@ -42,7 +43,8 @@ def _check_table(km, in_to_out):
     np.testing.assert_array_equal(in_to_out[ins], os_)
     pos_in = np.empty(n_in, np.int64)
     pos_in[io] = np.arange(n_in)
-    np.testing.assert_array_equal(nbr_t[ks, pos_in[ins]], os_)
+    assert nbr_t.shape == (1, n_in)
+    np.testing.assert_array_equal(nbr_t[0, pos_in[ins]], os_)
     assert (nbr_t >= 0).sum() == n_in
     counts = np.bincount(in_to_out, minlength=n_out)
     assert K == counts.max()
@@ -329,3 +331,64 @@ def test_pool_down_up_full_size_properties():
     parent = np.concatenate([c[:, :1], np.floor_divide(c[:, 1:], 2) * 2], 1)
     sc = _np(s.F)[lookup(s.C.cpu().numpy(), parent)]
     np.testing.assert_allclose(_np(us.F)[pos], sc, rtol=1e-6, atol=1e-6)
+
+
+# ------------------------------------------------------ quantization
+
+def test_group_map_matches_oracle():
+    rng = np.random.default_rng(60)
+    c = random_coords(rng, 40000, 3, 10)  # heavy duplication
+    uq, _, inv = oracle.insert_and_map(c)
+    km = abi.group_map(to_dev(inv.astype(np.int32)), len(uq))
+    _check_table(km, inv.astype(np.int64))
+    with pytest.raises(RuntimeError, match="outside"):
+        abi.group_map(to_dev(np.array([0, 3, 1], np.int32)), 2)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("mode", ["avg", "sum", "max"])
+def test_quantization_matches_oracle_and_reference(mode, dtype):
+    """SparseTensor(features, coords, quantization_mode) reduces duplicate
+    rows through the group map + pooling kernels: values and gradients vs
+    the oracle (pooling over rows -> inverse; max with scatter_reduce's zero
+    tie) and the reference's own constructor; deterministic."""
+    from oracle import ref
+    rng = np.random.default_rng(70 + len(mode))
+    c = random_coords(rng, 30000, 3, 12)
+    x = rng.integers(-3, 3, (len(c), 8)).astype(np.float32)  # maxima at 0 and ties
+    Q = re_.QuantizationMode
+    q = {"avg": Q.UNWEIGHTED_AVERAGE, "sum": Q.UNWEIGHTED_SUM, "max": Q.MAX_POOL}[mode]
+    xf = to_dev(x, dtype).requires_grad_(True)
+    t = re_.SparseTensor(xf, to_dev(c), quantization_mode=q)
+    uq, _, inv = oracle.insert_and_map(c)
+    np.testing.assert_array_equal(t.C.cpu().numpy(), uq)
+    gy = coord_grad(uq, 8)
+    if dtype == torch.bfloat16:
+        gy = _bf16_round(gy)
+    (t.F * to_dev(gy, dtype)).sum().backward()
+    om = "max_scatter" if mode == "max" else mode
+    rows = np.arange(len(c), dtype=np.int32)
+    oy, _ = oracle.pool_forward(x, rows, inv.astype(np.int32), len(uq), om)
+    assert_rel(_np(t.F), oy, TOL[dtype], "y")
+    assert_rel(_np(xf.grad), oracle.pool_backward(x, oy, gy, rows, inv.astype(np.int32), om),
+               TOL[dtype], "dX")
+    again = re_.SparseTensor(xf.detach(), to_dev(c), quantization_mode=q)
+    assert torch.equal(again.F, t.F.detach())
+    if ref.available() and dtype == torch.float32:
+        ry, roc, rgx = ref.quantize(c, x, mode, gy=lambda o: coord_grad(o, 8))
+        p = align(roc, uq)
+        assert_rel(_np(t.F)[p], ry, 1e-5, "y vs reference")
+        assert_rel(_np(xf.grad), rgx, 1e-5, "dX vs reference")
+
+
+def test_sparse_tensor_to_device_rehashes():
+    rng = np.random.default_rng(80)
+    c, _, _ = oracle.insert_and_map(random_coords(rng, 5000, 3, 15))
+    x = torch.randn(len(c), 4, device=DEV)
+    t = re_.SparseTensor(x, to_dev(c))
+    m = t.to(DEV)
+    assert m.coordinate_manager is not t.coordinate_manager
+    np.testing.assert_array_equal(m.C.cpu().numpy(), t.C.cpu().numpy())
+    assert torch.equal(m.F, t.F)
+    with pytest.raises(RuntimeError, match="no CPU manager"):
+        t.to(torch.device("cpu"))

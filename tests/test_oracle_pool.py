@@ -145,3 +145,28 @@ def test_planted_mistake_fails_the_torch_check():
     assert not np.allclose(wrong, ty, rtol=1e-5)
     good, _ = oracle.pool_forward(x, in_rows, out_rows, 2, "avg")
     np.testing.assert_allclose(good, ty, rtol=1e-6)
+
+
+def test_scatter_max_gradient_matches_torch():
+    """Mode max_scatter = zeros.scatter_reduce("amax", include_self=False) as
+    the reference's MAX_POOL quantization computes it: torch's backward
+    counts the excluded zero as a tie where the maximum is 0."""
+    rng = np.random.default_rng(17)
+    n, G, C = 200, 40, 3
+    group = rng.integers(0, G, n).astype(np.int32)
+    group[:G] = np.arange(G)  # every group non-empty
+    x = rng.integers(-3, 2, (n, C)).astype(np.float32)  # many maxima at 0
+    gy = rng.standard_normal((G, C)).astype(np.float32)
+    xt = torch.tensor(x, dtype=torch.float64, requires_grad=True)
+    idx = torch.tensor(group, dtype=torch.long)[:, None].expand(n, C)
+    r = torch.zeros(G, C, dtype=torch.float64).scatter_reduce(0, idx, xt, "amax",
+                                                              include_self=False)
+    (r * torch.tensor(gy, dtype=torch.float64)).sum().backward()
+    rows = np.arange(n, dtype=np.int32)
+    y, _ = oracle.pool_forward(x, rows, group, G, "max_scatter")
+    np.testing.assert_array_equal(y, r.detach().numpy())
+    np.testing.assert_allclose(oracle.pool_backward(x, y, gy, rows, group, "max_scatter"),
+                               xt.grad.numpy(), rtol=1e-6, atol=1e-7)
+    assert (y == 0).any()  # the case that differs from plain max is exercised
+    plain = oracle.pool_backward(x, y, gy, rows, group, "max")
+    assert not np.allclose(plain, xt.grad.numpy())

@@ -173,3 +173,24 @@ def test_global_pool_matches_reference(mode):
     np.testing.assert_allclose(y, oy, rtol=1e-5, atol=1e-6)
     np.testing.assert_allclose(gx, oracle.global_pool_backward(x, oy, gy, c, mode),
                                rtol=1e-5, atol=1e-6)
+
+
+@pytest.mark.parametrize("mode", ["avg", "sum", "max"])
+def test_quantization_matches_reference(mode):
+    """SparseTensor quantization (reduce feature rows by their unique
+    coordinate) = local pooling over the group map rows -> inverse map:
+    the oracle's pooling on (arange, inverse) against the reference's
+    SparseTensor constructor, values and gradients."""
+    rng = np.random.default_rng(50 + len(mode))
+    c = random_coords(rng, 3000, 3, 6)  # many duplicates
+    x = rng.integers(-3, 4, (len(c), 4)).astype(np.float32)
+    gy = lambda oc: coord_grad(oc, 4)  # noqa: E731
+    y, oc, gx = ref.quantize(c, x, mode, gy=gy)
+    uq, _, inv = oracle.insert_and_map(c)
+    p = align(oc, uq)
+    rows = np.arange(len(c), dtype=np.int32)
+    om = "max_scatter" if mode == "max" else mode  # scatter_reduce's gradient
+    oy, _ = oracle.pool_forward(x, rows, inv.astype(np.int32), len(uq), om)
+    np.testing.assert_allclose(y, oy[p], rtol=1e-5, atol=1e-5)
+    ogx = oracle.pool_backward(x, oy, gy(uq), rows, inv.astype(np.int32), om)
+    np.testing.assert_allclose(gx, ogx, rtol=1e-5, atol=1e-5)
