@@ -102,11 +102,12 @@ def conv_traffic(n_in, n_out, P, K, cin, cout, s):
     }
 
 
-def measured_traffic(dtype: str, pass_name: str):
+def measured_traffic(dtype: str, pass_name: str, record: str = "traffic_config2.json"):
     """HBM bytes per launch of a pass's kernel, from the committed rocprofv3
-    FETCH_SIZE / WRITE_SIZE passes (profiles/traffic_config2.json, scaled by
-    the counters' reading for a device copy of known size); None if absent."""
-    path = os.path.join(ROOT, "profiles", "traffic_config2.json")
+    FETCH_SIZE / WRITE_SIZE passes (profiles/traffic_config2.json for the
+    convolution, traffic_pool.json for pooling; scaled by the counters'
+    reading for a device copy of known size); None if absent."""
+    path = os.path.join(ROOT, "profiles", record)
     try:
         with open(path) as f:
             rec = json.load(f)[dtype][pass_name]
@@ -360,16 +361,18 @@ def run_other_config(args):
     return line
 
 
-def pool_traffic(kind, n_in, n_out, K, C, s, ncol=4):
+def pool_traffic(kind, n_in, n_out, K, C, s, ncol=4, K_t=None):
     """Algorithmic HBM bytes of one pooling kernel pass: every feature row it
-    must touch read (or written) once, plus its index tables; no re-reads."""
+    must touch read (or written) once, plus its index tables (nbr K rows,
+    nbr_t K_t rows, default K); no re-reads."""
+    K_t = K if K_t is None else K_t
     if kind == "forward":      # x rows, nbr [K, n_out], order; y, counts
         return n_in * C * s + K * n_out * 4 + n_out * 4 + n_out * C * s + n_out * 4
-    if kind == "backward":     # gy rows, counts, nbr_t [K, n_in], order; gx
-        return n_out * C * s + n_out * 4 + K * n_in * 4 + n_in * 4 + n_in * C * s
+    if kind == "backward":     # gy rows, counts, nbr_t [K_t, n_in], order; gx
+        return n_out * C * s + n_out * 4 + K_t * n_in * 4 + n_in * 4 + n_in * C * s
     if kind == "max_backward":  # share pass (y, gy, x, nbr; gs fp32) + gather pass
         share = 2 * n_out * C * s + n_in * C * s + K * n_out * 4 + n_out * 4 + n_out * C * 4
-        gather = n_in * C * s + n_out * C * s + n_out * C * 4 + K * n_in * 4 + n_in * 4 \
+        gather = n_in * C * s + n_out * C * s + n_out * C * 4 + K_t * n_in * 4 + n_in * 4 \
             + n_in * C * s
         return share + gather
     if kind == "global_forward":   # x rows + members; y (n_out = batches) negligible
@@ -435,8 +438,8 @@ def run_pool(args):
     def build():
         tf = abi.hash_build(coords)
         tc = abi.hash_build(abi.stride_coords(coords, [2, 2, 2]))
-        return tf, tc, abi.stride_map(tf, tc, [2, 2, 2]), abi.kernel_map(tf, tc, off3), \
-            abi.batch_segments(coords)
+        return tf, tc, abi.stride_map(tf, tc, [2, 2, 2]), \
+            abi.pooling_map(abi.kernel_map(tf, tc, off3)), abi.batch_segments(coords)
     (tf, tc, sm, km, segs), map_ms = _map_time(build, args.map_reps)
     n_in, n_out = tf.n, tc.n
     g = torch.Generator(device="cpu").manual_seed(args.seed)
@@ -455,9 +458,11 @@ def run_pool(args):
                                                                    "avg"))]
     per, wall = _timed_passes(passes, args.steps, args.warmup)
     B = {"max2_forward": pool_traffic("forward", n_in, n_out, sm.K, C, s),
-         "max2_backward": pool_traffic("max_backward", n_in, n_out, sm.K, C, s),
+         "max2_backward": pool_traffic("max_backward", n_in, n_out, sm.K, C, s,
+                                       K_t=sm.nbr_t.shape[0]),
          "avg3_forward": pool_traffic("forward", n_in, n_out, km.K, C, s),
-         "avg3_backward": pool_traffic("backward", n_in, n_out, km.K, C, s),
+         "avg3_backward": pool_traffic("backward", n_in, n_out, km.K, C, s,
+                                       K_t=km.nbr_t.shape[0]),
          "global_forward": pool_traffic("global_forward", n_in, segs.n_batches, 0, C, s),
          "global_backward": pool_traffic("global_backward", n_in, segs.n_batches, 0, C, s)}
     dom = max(per, key=per.get)
@@ -469,7 +474,8 @@ def run_pool(args):
                "global_forward": "gpool_partial_kernel + gpool_final_kernel (avg)",
                "global_backward": "gpool_bwd_kernel (avg)"}
     roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-            "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None, "kernel": kernels[dom],
+            "frac": round(achieved / PEAK_HBM_GBS, 4),
+            "traffic": measured_traffic(args.dtype, dom, "traffic_pool.json"), "kernel": kernels[dom],
             "kernel_ms": round(per[dom], 4), "algorithmic": {"bytes": B[dom]}}
     step_ms = sum(per.values())
     t_roof = sum(B.values()) / (PEAK_HBM_GBS * 1e9)

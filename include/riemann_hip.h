@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define RHIP_ABI_VERSION 7
+#define RHIP_ABI_VERSION 8
 #define RHIP_MAX_COLS 8 /* batch column + up to 7 spatial axes */
 
 typedef enum rhip_status {
@@ -327,6 +327,19 @@ int rhip_stride_map_fill(int64_t n_in, int64_t n_out, int32_t k_max,
                          void *workspace, size_t workspace_bytes, int32_t *nbr,
                          int32_t *nbr_t, int32_t *in_rows, int32_t *out_rows,
                          hipStream_t stream);
+
+/*
+ * Pooling form of a neighbour table [K, n] (a kernel map's nbr or nbr_t):
+ * each column's entries >= 0 moved to its first rows in row order, -1 after
+ * them, into out [K, n] (no aliasing); *k_used_host = the most entries of
+ * one column, so that a pooling kernel reads only rows [0, k_used). Pooling
+ * reduces a set of rows, so the offset a row came from does not matter
+ * there (a convolution table must not be compacted). workspace: 4 bytes of
+ * device memory. Synchronises once.
+ */
+int rhip_table_compact(const int32_t *table, int32_t K, int64_t n,
+                       void *workspace, size_t workspace_bytes, int32_t *out,
+                       int32_t *k_used_host, hipStream_t stream);
 
 /* Workspace of rhip_pool_backward (max pooling keeps one fp32 per output
  * element; sum and average need none). */

@@ -35,7 +35,8 @@ EXPORTS = (
     "rhip_conv_backward_input", "rhip_conv_backward_weight",
     "rhip_stride_map_workspace_bytes", "rhip_stride_map_count", "rhip_group_map_count",
     "rhip_stride_map_fill",
-    "rhip_pool_workspace_bytes", "rhip_pool_forward", "rhip_pool_backward",
+    "rhip_table_compact", "rhip_pool_workspace_bytes", "rhip_pool_forward",
+    "rhip_pool_backward",
     "rhip_global_pool_workspace_bytes", "rhip_batch_count", "rhip_batch_segments",
     "rhip_global_pool_forward", "rhip_global_pool_backward",
 )
@@ -91,6 +92,7 @@ def _declare(lib):
         "rhip_group_map_count": (ctypes.c_int, [_vp, _i64, _i64, _vp, _sz, _P(_i32), _vp]),
         "rhip_stride_map_fill": (ctypes.c_int, [_i64, _i64, _i32, _vp, _vp, _vp, _sz, _vp, _vp,
                                                 _vp, _vp, _vp]),
+        "rhip_table_compact": (ctypes.c_int, [_vp, _i32, _i64, _vp, _sz, _vp, _P(_i32), _vp]),
         "rhip_pool_workspace_bytes": (ctypes.c_int, [_i64, _i32, _i32, _P(_sz)]),
         "rhip_pool_forward": (ctypes.c_int, [_vp, _i64, _i32, _vp, _i32, _vp, _i64, _i32, _vp,
                                              _vp, _i32, _vp]),
@@ -457,6 +459,29 @@ def group_map(group: torch.Tensor, n_groups: int) -> KernelMap:
     iota = lambda m: torch.arange(m, dtype=torch.int32, device=dev)  # noqa: E731
     return KernelMap(K, n, n_groups, torch.as_tensor(kofs_host).to(dev), kofs_host, in_rows[:n],
                      out_rows[:n], nbr[:, :n_groups], nbr_t[:, :n], iota(n), iota(n_groups))
+
+
+def table_compact(table: torch.Tensor) -> torch.Tensor:
+    """Pooling form of a neighbour table [K, n]: each column's entries moved
+    to its first rows; returns the rows in use [k_used, n] (at least one)."""
+    _require_cuda(table, "table")
+    table = table.contiguous()
+    K, n = table.shape
+    out = torch.empty_like(table)
+    ws = torch.empty(256, dtype=torch.uint8, device=table.device)
+    used = ctypes.c_int32(0)
+    _check(lib().rhip_table_compact(_ptr(table), K, n, _ptr(ws), ws.numel(), _ptr(out),
+                                    ctypes.byref(used), _stream(table.device)),
+           "rhip_table_compact")
+    return out[:max(int(used.value), 1)]
+
+
+def pooling_map(kmap: KernelMap) -> KernelMap:
+    """A kernel map for pooling: its transposed table compacted (the input
+    side of a strided pooling map has few of the K offsets)."""
+    return KernelMap(kmap.K, kmap.n_in, kmap.n_out, kmap.offsets, kmap.offsets_host,
+                     kmap.in_rows, kmap.out_rows, kmap.nbr, table_compact(kmap.nbr_t),
+                     kmap.in_order, kmap.out_order, kmap.symmetric)
 
 
 def _pool_mode(mode) -> int:

@@ -571,6 +571,25 @@ const HipKernelMap &CoordinateManager::kernel_map(
   };
   if (const HipKernelMap *hit = find(key))
     return *hit;
+  // A pooling map through a kernel region keeps its transposed table
+  // compacted (rhip_table_compact): pooling reduces sets of rows, and the
+  // input side of a strided map uses few of the K offsets.
+  auto store_pool = [&](HipKernelMap m) -> const HipKernelMap & {
+    if (is_pool && !m.stride_map && m.n_in > 0 && m.K > 1) {
+      const auto dev = m.nbr_t.device();
+      at::DeviceGuard guard(dev);
+      auto src = m.nbr_t.contiguous();
+      auto out = torch::empty_like(src);
+      auto ws = device_bytes(256, dev);
+      int32_t used = 0;
+      check_rhip(rhip_table_compact(src.data_ptr<int32_t>(), static_cast<int32_t>(src.size(0)),
+                                    src.size(1), ws.data_ptr(), ws.numel(),
+                                    out.data_ptr<int32_t>(), &used, current_stream(dev)),
+                 "rhip_table_compact");
+      m.nbr_t = out.slice(0, 0, std::max<int32_t>(used, 1));
+    }
+    return store(key, std::move(m));
+  };
 
   const CoordinateMapHIP &in_map = coordinate_map(in_key);
   const CoordinateMapHIP &out_map = coordinate_map(out_key);
@@ -583,13 +602,13 @@ const HipKernelMap &CoordinateManager::kernel_map(
     // region on the input map's tensor stride (space_impl.hpp:626-636)
     auto off = region_offsets(region_type, kernel_size, kernel_dilation, in_map.tensor_stride,
                               custom);
-    return store(key, generate(in_map, out_map, off));
+    return store_pool(generate(in_map, out_map, off));
   }
   const kernel_map_key_type fwd_key =
       std::make_tuple(out_key.get_key(), in_key.get_key(), kernel_size, kernel_stride,
                       kernel_dilation, region_type, false, is_pool);
   if (const HipKernelMap *fwd = find(fwd_key))
-    return store(key, fwd->swapped());
+    return store_pool(fwd->swapped());
   // the stride map runs out -> in, then swapped (space_impl.hpp:660-669)
   if (use_stride_map)
     return store(key, generate_stride_map(out_map, in_map).swapped());
@@ -597,7 +616,7 @@ const HipKernelMap &CoordinateManager::kernel_map(
   // then swapped (space_impl.hpp:649-697)
   auto off = region_offsets(region_type, kernel_size, kernel_dilation, out_map.tensor_stride,
                             custom);
-  return store(key, generate(out_map, in_map, off).swapped());
+  return store_pool(generate(out_map, in_map, off).swapped());
 }
 
 std::string CoordinateManager::to_string() const {

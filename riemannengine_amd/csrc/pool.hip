@@ -458,6 +458,29 @@ __global__ __launch_bounds__(kPoolThreads) void stride_scatter_kernel(
   out_rows[s] = o;
 }
 
+// Column q of table [K, n]: its entries >= 0 moved to its first rows (row
+// order kept), -1 after them; kmax = most such entries in one column.
+__global__ __launch_bounds__(kPoolThreads) void table_compact_kernel(
+    const int32_t *__restrict__ table, int K, int64_t n, int32_t *__restrict__ out,
+    int32_t *__restrict__ kmax) {
+  int m = 0;
+  for (int64_t q = blockIdx.x * static_cast<int64_t>(kPoolThreads) + threadIdx.x; q < n;
+       q += static_cast<int64_t>(gridDim.x) * kPoolThreads) {
+    int c = 0;
+    for (int k = 0; k < K; ++k) {
+      const int32_t v = table[k * n + q];
+      if (v >= 0)
+        out[static_cast<int64_t>(c++) * n + q] = v;
+    }
+    for (int k = c; k < K; ++k)
+      out[k * n + q] = -1;
+    m = max(m, c);
+  }
+  m = block_max(m);
+  if (threadIdx.x == 0 && m > 0)
+    atomicMax(kmax, m);
+}
+
 // --------------------------------------------------------- global pooling
 
 __global__ __launch_bounds__(kPoolThreads) void batch_max_kernel(
@@ -1056,6 +1079,31 @@ extern "C" int rhip_pool_backward(const void *grad_y, const void *y, const void 
       launch(float{});
     else
       launch(__bf16{});
+  });
+}
+
+extern "C" int rhip_table_compact(const int32_t *table, int32_t K, int64_t n, void *workspace,
+                                  size_t ws_bytes, int32_t *out, int32_t *k_used_host,
+                                  hipStream_t stream) {
+  return guarded([&] {
+    RHIP_CHECK_ARG(k_used_host != nullptr, "k_used_host is null");
+    RHIP_CHECK_ARG(K >= 1 && n >= 0, "bad sizes");
+    *k_used_host = 0;
+    if (n == 0)
+      return;
+    RHIP_CHECK_ARG(table && out && workspace, "table, out and workspace are required");
+    RHIP_CHECK_ARG(table != out, "table and out must not alias");
+    RHIP_CHECK_ARG(ws_bytes >= sizeof(int32_t), "workspace too small");
+    int32_t *kmax = static_cast<int32_t *>(workspace);
+    hipLaunchKernelGGL(fill_i32_kernel, dim3(1), dim3(kPoolThreads), 0, stream, kmax, 1, 0);
+    RHIP_LAUNCH_CHECK();
+    hipLaunchKernelGGL(table_compact_kernel, dim3(std::min<unsigned>(grid_for(n), kReduceBlocks)),
+                       dim3(kPoolThreads), 0, stream, table, K, n, out, kmax);
+    RHIP_LAUNCH_CHECK();
+    int32_t used = 0;
+    RHIP_HIP(hipMemcpyAsync(&used, kmax, sizeof(used), hipMemcpyDeviceToHost, stream));
+    RHIP_HIP(hipStreamSynchronize(stream));
+    *k_used_host = used;
   });
 }
 

@@ -82,8 +82,8 @@ def test_stride_map_unmatched_input_raises():
 
 
 def _maps(kind, c):
-    """GPU map + the oracle's pair list: kind 'stride' (kernel 2 == stride 2)
-    or 'kernel' (kernel 3, stride 2)."""
+    """GPU map + the oracle's pair list: kind 'stride' (kernel 2 == stride 2),
+    'kernel' (kernel 3, stride 2) or 'compact' (the same, in pooling form)."""
     tin = abi.hash_build(to_dev(c))
     tout = abi.hash_build(abi.stride_coords(tin.ucoords, [2, 2, 2]))
     out = tout.ucoords.cpu().numpy()
@@ -93,14 +93,17 @@ def _maps(kind, c):
         return km, np.arange(len(c), dtype=np.int32), m, len(out)
     off = oracle.region_offsets(3, 3, 1, 1)
     km = abi.kernel_map(tin, tout, off)
+    if kind == "compact":
+        km = abi.pooling_map(km)
+        assert km.nbr_t.shape[0] <= 8  # stride 2, kernel 3: at most 2 coarse rows per axis
     _, ir, orr = oracle.kernel_map(c, out, off)
     return km, ir, orr, len(out)
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("mode", ["sum", "avg", "max"])
-@pytest.mark.parametrize("kind,C", [("stride", 32), ("kernel", 64), ("stride", 3),
-                                    ("kernel", 5)])
+@pytest.mark.parametrize("kind,C", [("stride", 32), ("kernel", 64), ("compact", 64),
+                                    ("stride", 3), ("kernel", 5), ("compact", 5)])
 def test_pool_matches_oracle(kind, C, mode, dtype):
     """C = 32/64: 16-byte channel slices; C = 3/5: one channel per lane."""
     rng = np.random.default_rng(C + len(mode))
@@ -121,6 +124,19 @@ def test_pool_matches_oracle(kind, C, mode, dtype):
     gx = abi.pool_backward(to_dev(gy, dtype), y, xd, km, counts, mode)
     ogx = oracle.pool_backward(x, _np(y), gy, ir, orr, mode)
     assert_rel(_np(gx), ogx, TOL[dtype], "dX")
+
+
+def test_table_compact():
+    rng = np.random.default_rng(12)
+    t = np.where(rng.random((27, 5000)) < 0.2, rng.integers(0, 900, (27, 5000)), -1)
+    t[:, 7] = -1  # an empty column
+    got = abi.table_compact(to_dev(t.astype(np.int32))).cpu().numpy()
+    counts = (t >= 0).sum(0)
+    assert got.shape == (counts.max(), 5000)
+    for q in range(5000):
+        col = t[:, q][t[:, q] >= 0]
+        np.testing.assert_array_equal(got[:len(col), q], col)
+        assert np.all(got[len(col):, q] == -1)
 
 
 def test_pool_empty_outputs_and_nan():
