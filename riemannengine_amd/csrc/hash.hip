@@ -45,6 +45,7 @@ __global__ __launch_bounds__(kBlock) void minmax_kernel(const int32_t *coords,
     lmin[c] = INT_MAX;
     lmax[c] = INT_MIN;
   }
+#pragma unroll 4
   for (int64_t r = blockIdx.x * (int64_t)kBlock + threadIdx.x; r < n;
        r += (int64_t)gridDim.x * kBlock) {
     const int32_t *row = coords + r * ncol;
@@ -396,7 +397,9 @@ extern "C" int rhip_hash_build(const int32_t *coords, int64_t n, int32_t ncol,
     hipLaunchKernelGGL(minmax_init_kernel, dim3(1), dim3(RHIP_MAX_COLS), 0,
                        stream, w.minmax, ncol);
     const int64_t nb = ceil_div(n, kBlock);
-    hipLaunchKernelGGL(minmax_kernel, dim3(std::min<int64_t>(nb, 1024)),
+    // few workgroups: each merges its result with 2 * ncol atomics on the
+    // same 2 * ncol addresses, which serialise
+    hipLaunchKernelGGL(minmax_kernel, dim3(std::min<int64_t>(nb, 256)),
                        dim3(kBlock), 0, stream, coords, n, ncol, w.minmax);
     RHIP_LAUNCH_CHECK();
     int32_t mm[2 * RHIP_MAX_COLS];

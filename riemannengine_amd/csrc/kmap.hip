@@ -72,6 +72,76 @@ __global__ __launch_bounds__(kMapBlock) void kmap_query_kernel(
   nbr_sp[k * n_out + j] = table_find(t, c);
 }
 
+// Packed-key tables: one thread per output row j (spatial order) answers all
+// n_probe offsets k = klist[p] (klist NULL: k = p). The row's coordinates are
+// read once; a neighbour's key is packed column by column from them (a
+// column leaving the table's [lo, hi] range is a miss, as in pack_row), and
+// the first slots of kChunk probes are loaded before any is resolved.
+__global__ __launch_bounds__(kMapBlock) void kmap_query_rows_kernel(
+    TableView t, const int32_t *__restrict__ out_coords, const int32_t *__restrict__ spatial,
+    int64_t n_out, const int32_t *__restrict__ offsets, const int32_t *__restrict__ klist,
+    int n_probe, int32_t *__restrict__ nbr_sp) {
+  constexpr int kChunk = 8;
+  const int64_t j = blockIdx.x * (int64_t)kMapBlock + threadIdx.x;
+  if (j >= n_out)
+    return;
+  const int D = t.ncol - 1;
+  const int64_t o = spatial ? spatial[j] : j;
+  int32_t c[RHIP_MAX_COLS];
+#pragma unroll
+  for (int i = 0; i < RHIP_MAX_COLS; ++i)
+    c[i] = i < t.ncol ? out_coords[o * t.ncol + i] : 0;
+  const uint32_t d0 = static_cast<uint32_t>(c[0]) - static_cast<uint32_t>(t.lo[0]);
+  const bool row_ok = d0 <= t.span[0];
+  const uint64_t base = static_cast<uint64_t>(d0) << t.shift[0];
+  for (int p0 = 0; p0 < n_probe; p0 += kChunk) {
+    uint64_t key[kChunk], h[kChunk];
+    bool ok[kChunk];
+    Slot sl[kChunk];
+#pragma unroll
+    for (int u = 0; u < kChunk; ++u) {
+      const int p = p0 + u;
+      ok[u] = row_ok && p < n_probe;
+      key[u] = base;
+      if (p < n_probe) {
+        const int k = klist ? klist[p] : p;
+#pragma unroll
+        for (int i = 1; i < RHIP_MAX_COLS; ++i) {
+          if (i <= D) { // wrap-around add, as int32 coordinate arithmetic does
+            const uint32_t v = static_cast<uint32_t>(c[i]) +
+                               static_cast<uint32_t>(offsets[k * D + (i - 1)]);
+            const uint32_t d = v - static_cast<uint32_t>(t.lo[i]);
+            ok[u] = ok[u] && d <= t.span[i];
+            key[u] |= static_cast<uint64_t>(d) << t.shift[i];
+          }
+        }
+      }
+      h[u] = mix64(key[u]) & t.mask;
+    }
+#pragma unroll
+    for (int u = 0; u < kChunk; ++u)
+      if (ok[u])
+        sl[u] = t.slots[h[u]];
+#pragma unroll
+    for (int u = 0; u < kChunk; ++u) {
+      const int p = p0 + u;
+      if (p >= n_probe)
+        continue;
+      int32_t r = -1;
+      if (ok[u]) {
+        while (sl[u].word != key[u] && sl[u].word != kEmptyWord) {
+          h[u] = (h[u] + 1) & t.mask;
+          sl[u] = t.slots[h[u]];
+        }
+        if (sl[u].word == key[u])
+          r = static_cast<int32_t>(sl[u].uid);
+      }
+      const int k = klist ? klist[p] : p;
+      nbr_sp[k * n_out + j] = r;
+    }
+  }
+}
+
 // Symmetric maps: the partner row of every probed offset k = klist[y];
 // nbr_sp[partner[k]][pos[i]] = row of j for every hit i = nbr_sp[k][j].
 __global__ __launch_bounds__(kMapBlock) void kmap_mirror_kernel(
@@ -469,6 +539,19 @@ extern "C" int rhip_kmap_count(const rhip_table *in_table, const int32_t *out_co
         RHIP_HIP(hipMemcpyAsync(w.plan, plan.lists.data(), sizeof(int32_t) * plan.lists.size(),
                                 hipMemcpyHostToDevice, stream));
       const TableView tv = make_view(*in_table);
+      // all probes of a row in one thread for packed keys; one thread per
+      // (row, offset) for row-reference tables
+      auto query = [&](int n_probe, const int32_t *klist) {
+        if (in_table->mode == RHIP_KEY_PACKED64)
+          hipLaunchKernelGGL(kmap_query_rows_kernel, dim3(nb), dim3(kMapBlock), 0, stream, tv,
+                             out_coords, out_spatial_order, n_out, w.offsets, klist, n_probe,
+                             w.nbr_sp);
+        else
+          hipLaunchKernelGGL(kmap_query_kernel, dim3(nb, n_probe), dim3(kMapBlock), 0, stream,
+                             tv, out_coords, out_spatial_order, n_out, w.offsets, klist,
+                             w.nbr_sp);
+        RHIP_LAUNCH_CHECK();
+      };
       if (sym) {
         if (plan.n_mirror > 0) {
           hipLaunchKernelGGL(fill_partner_rows_kernel, dim3(nb, plan.n_mirror),
@@ -476,12 +559,8 @@ extern "C" int rhip_kmap_count(const rhip_table *in_table, const int32_t *out_co
                              -1);
           RHIP_LAUNCH_CHECK();
         }
-        if (plan.n_probe > 0) {
-          hipLaunchKernelGGL(kmap_query_kernel, dim3(nb, plan.n_probe), dim3(kMapBlock), 0,
-                             stream, tv, out_coords, out_spatial_order, n_out, w.offsets,
-                             w.probe, w.nbr_sp);
-          RHIP_LAUNCH_CHECK();
-        }
+        if (plan.n_probe > 0)
+          query(plan.n_probe, w.probe);
         if (plan.n_mirror > 0) {
           if (out_spatial_order) {
             hipLaunchKernelGGL(invert_order_kernel, dim3(nb), dim3(kMapBlock), 0, stream,
@@ -499,9 +578,7 @@ extern "C" int rhip_kmap_count(const rhip_table *in_table, const int32_t *out_co
           RHIP_LAUNCH_CHECK();
         }
       } else {
-        hipLaunchKernelGGL(kmap_query_kernel, dim3(nb, K), dim3(kMapBlock), 0, stream, tv,
-                           out_coords, out_spatial_order, n_out, w.offsets, nullptr, w.nbr_sp);
-        RHIP_LAUNCH_CHECK();
+        query(K, nullptr);
       }
       const int32_t *jpos = nullptr;
       if (K <= kMaskedK && n_out > 1 && in_table->n_unique > 0) {
