@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define RHIP_ABI_VERSION 8
+#define RHIP_ABI_VERSION 9
 #define RHIP_MAX_COLS 8 /* batch column + up to 7 spatial axes */
 
 typedef enum rhip_status {
@@ -435,6 +435,61 @@ int rhip_global_pool_backward(const void *grad_y, const void *y, const void *x,
                               int32_t mode, void *grad_x, int32_t dtype,
                               void *workspace, size_t workspace_bytes,
                               hipStream_t stream);
+
+/* ------------------------------------------------------------ batch norm
+ *
+ * Batch normalisation of [n, C] features (fp32 or bf16) with fp32
+ * statistics and parameters, as torch BatchNorm1d computes it for
+ * RiemannBatchNorm (engine/nn/normalization.hpp:11-37): biased batch
+ * variance for normalising, unbiased variance into running_var. The
+ * forward optionally adds a residual and applies ReLU after the affine
+ * transform, BasicBlock's `norm2 -> += residual -> relu` tail and the
+ * `norm1 -> relu` of its first half (engine/nn/residual.cpp:44-51).
+ */
+
+/* Workspace bytes for rhip_bn_stats and rhip_bn_backward over n rows. */
+int rhip_bn_workspace_bytes(int64_t n, int32_t C, size_t *bytes);
+
+/*
+ * Batch statistics: mean[c] and invstd[c] = 1 / sqrt(var_biased[c] + eps)
+ * over n > 1 rows (fp64 sums in a fixed order: deterministic). When
+ * running_mean / running_var are given they become
+ * (1 - momentum) * old + momentum * (mean | var * n / (n - 1)).
+ * Replaces BatchNorm1d's training-mode statistics (torch batch_norm).
+ */
+int rhip_bn_stats(const void *x, int64_t n, int32_t C, int32_t dtype, double eps,
+                  double momentum, float *running_mean, float *running_var,
+                  float *mean, float *invstd, void *workspace,
+                  size_t workspace_bytes, hipStream_t stream);
+
+/* invstd[c] = 1 / sqrt(var[c] + eps): evaluation with running statistics. */
+int rhip_bn_invstd(const float *var, int32_t C, double eps, float *invstd,
+                   hipStream_t stream);
+
+/*
+ * y = act((x - mean) * invstd * gamma + beta [+ residual]), act = ReLU when
+ * relu != 0; gamma / beta may be null (affine = false), residual may be
+ * null. y may alias x or residual.
+ */
+int rhip_bn_forward(const void *x, int64_t n, int32_t C, const float *mean,
+                    const float *invstd, const float *gamma, const float *beta,
+                    const void *residual, int32_t relu, void *y, int32_t dtype,
+                    hipStream_t stream);
+
+/*
+ * Backward of rhip_bn_forward. g = grad_y, masked to y > 0 when relu != 0
+ * (y = the forward's output); grad_residual = g; with batch statistics
+ * (batch_stats != 0) grad_x = gamma * invstd * (g - mean(g) - xhat *
+ * mean(g * xhat)), with running statistics grad_x = gamma * invstd * g;
+ * grad_beta = sum g, grad_gamma = sum g * xhat, xhat = (x - mean) * invstd.
+ * Any of grad_x, grad_residual, grad_gamma, grad_beta may be null.
+ */
+int rhip_bn_backward(const void *grad_y, const void *y, const void *x, int64_t n,
+                     int32_t C, const float *mean, const float *invstd,
+                     const float *gamma, int32_t relu, int32_t batch_stats,
+                     void *grad_x, void *grad_residual, float *grad_gamma,
+                     float *grad_beta, int32_t dtype, void *workspace,
+                     size_t workspace_bytes, hipStream_t stream);
 
 #ifdef __cplusplus
 }

@@ -39,6 +39,8 @@ EXPORTS = (
     "rhip_pool_backward",
     "rhip_global_pool_workspace_bytes", "rhip_batch_count", "rhip_batch_segments",
     "rhip_global_pool_forward", "rhip_global_pool_backward",
+    "rhip_bn_workspace_bytes", "rhip_bn_stats", "rhip_bn_invstd", "rhip_bn_forward",
+    "rhip_bn_backward",
 )
 
 
@@ -108,6 +110,14 @@ def _declare(lib):
         "rhip_global_pool_backward": (ctypes.c_int, [_vp, _vp, _vp, _vp, _i32, _i64, _i32,
                                                      _vp, _vp, _i32, _i32, _vp, _i32, _vp,
                                                      _sz, _vp]),
+        "rhip_bn_workspace_bytes": (ctypes.c_int, [_i64, _i32, _P(_sz)]),
+        "rhip_bn_stats": (ctypes.c_int, [_vp, _i64, _i32, _i32, ctypes.c_double,
+                                         ctypes.c_double, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
+        "rhip_bn_invstd": (ctypes.c_int, [_vp, _i32, ctypes.c_double, _vp, _vp]),
+        "rhip_bn_forward": (ctypes.c_int, [_vp, _i64, _i32, _vp, _vp, _vp, _vp, _vp, _i32, _vp,
+                                           _i32, _vp]),
+        "rhip_bn_backward": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i32, _vp, _vp, _vp, _i32,
+                                            _i32, _vp, _vp, _vp, _vp, _i32, _vp, _sz, _vp]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -582,3 +592,72 @@ def global_pool_backward(grad_y: torch.Tensor, y: torch.Tensor, x: torch.Tensor,
                                            _ptr(gx), dt, _ptr(ws), ws.numel(),
                                            _stream(x.device)), "rhip_global_pool_backward")
     return gx
+
+
+def bn_stats(x: torch.Tensor, eps: float = 1e-5, momentum: float = 0.1,
+             running_mean: Optional[torch.Tensor] = None,
+             running_var: Optional[torch.Tensor] = None):
+    """(mean, invstd) fp32 [C] of x's batch statistics; the running
+    statistics, when given (fp32 [C], contiguous), are updated in place."""
+    _require_cuda(x, "x")
+    dt = _dtype_code(x.dtype)
+    x = x.contiguous()
+    n, C = x.shape
+    f32 = dict(dtype=torch.float32, device=x.device)
+    mean, invstd = torch.empty(C, **f32), torch.empty(C, **f32)
+    ws = torch.empty(_sizeq(lib().rhip_bn_workspace_bytes, n, C), dtype=torch.uint8,
+                     device=x.device)
+    _check(lib().rhip_bn_stats(_ptr(x), n, C, dt, eps, momentum, _ptr(running_mean),
+                               _ptr(running_var), _ptr(mean), _ptr(invstd), _ptr(ws),
+                               ws.numel(), _stream(x.device)), "rhip_bn_stats")
+    return mean, invstd
+
+
+def bn_invstd(var: torch.Tensor, eps: float = 1e-5) -> torch.Tensor:
+    _require_cuda(var, "var")
+    var = var.float().contiguous()
+    out = torch.empty_like(var)
+    _check(lib().rhip_bn_invstd(_ptr(var), var.numel(), eps, _ptr(out), _stream(var.device)),
+           "rhip_bn_invstd")
+    return out
+
+
+def bn_forward(x: torch.Tensor, mean: torch.Tensor, invstd: torch.Tensor,
+               gamma: Optional[torch.Tensor] = None, beta: Optional[torch.Tensor] = None,
+               residual: Optional[torch.Tensor] = None, relu: bool = False) -> torch.Tensor:
+    _require_cuda(x, "x")
+    dt = _dtype_code(x.dtype)
+    x = x.contiguous()
+    n, C = x.shape
+    if residual is not None:
+        residual = residual.to(x.dtype).contiguous()
+        if residual.shape != x.shape:
+            raise RuntimeError("residual does not match the features")
+    y = torch.empty_like(x)
+    _check(lib().rhip_bn_forward(_ptr(x), n, C, _ptr(mean), _ptr(invstd), _ptr(gamma),
+                                 _ptr(beta), _ptr(residual), int(relu), _ptr(y), dt,
+                                 _stream(x.device)), "rhip_bn_forward")
+    return y
+
+
+def bn_backward(grad_y: torch.Tensor, y: Optional[torch.Tensor], x: torch.Tensor,
+                mean: torch.Tensor, invstd: torch.Tensor, gamma: Optional[torch.Tensor] = None,
+                relu: bool = False, batch_stats: bool = True, want_residual: bool = False):
+    """(grad_x, grad_residual or None, grad_gamma, grad_beta)."""
+    _require_cuda(x, "x")
+    dt = _dtype_code(x.dtype)
+    x = x.contiguous()
+    grad_y = grad_y.to(x.dtype).contiguous()
+    y = None if y is None else y.contiguous()
+    n, C = x.shape
+    gx = torch.empty_like(x)
+    gr = torch.empty_like(x) if want_residual else None
+    f32 = dict(dtype=torch.float32, device=x.device)
+    gg, gb = torch.empty(C, **f32), torch.empty(C, **f32)
+    ws = torch.empty(_sizeq(lib().rhip_bn_workspace_bytes, n, C), dtype=torch.uint8,
+                     device=x.device)
+    _check(lib().rhip_bn_backward(_ptr(grad_y), _ptr(y), _ptr(x), n, C, _ptr(mean),
+                                  _ptr(invstd), _ptr(gamma), int(relu), int(batch_stats),
+                                  _ptr(gx), _ptr(gr), _ptr(gg), _ptr(gb), dt, _ptr(ws),
+                                  ws.numel(), _stream(x.device)), "rhip_bn_backward")
+    return gx, gr, gg, gb

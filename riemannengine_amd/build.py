@@ -27,7 +27,7 @@ HIP_LIB = os.path.join(PKG, "libriemann_hip.so")
 ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 HIPCC = os.path.join(ROCM, "bin", "hipcc")
 
-HIP_SOURCES = ["abi.hip", "sort.hip", "hash.hip", "kmap.hip", "conv.hip", "pool.hip"]
+HIP_SOURCES = ["abi.hip", "sort.hip", "hash.hip", "kmap.hip", "conv.hip", "pool.hip", "norm.hip"]
 # gfx950 only. Packed-FP32 instructions are disabled: the compiler would
 # otherwise form v_pk_* FP32 ops from plain float code.
 HIP_FLAGS = [

@@ -31,6 +31,15 @@ template <typename Impl> ModuleClass<Impl> bind_module(py::module_ &m, const cha
       },
       py::arg("recurse") = true);
   cls.def(
+      "named_buffers",
+      [](Impl &self, bool recurse) {
+        py::dict result;
+        for (const auto &pair : self.named_buffers(recurse))
+          result[py::str(pair.key())] = pair.value();
+        return result;
+      },
+      py::arg("recurse") = true);
+  cls.def(
       "train", [](Impl &self, bool mode) { self.train(mode); }, py::arg("mode") = true);
   cls.def("eval", [](Impl &self) { self.eval(); });
   cls.def_property_readonly("training", [](const Impl &self) { return self.is_training(); });

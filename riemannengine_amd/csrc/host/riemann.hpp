@@ -428,6 +428,10 @@ public:
                        bool affine = true, bool track_running_stats = true);
   void reset() override;
   SparseTensor forward(const SparseTensor &input);
+  // act(normalised input [+ residual]), act = ReLU when `relu`: the
+  // BasicBlock tails in one pass. residual must share input's manager and
+  // key (SparseTensor::operator+=).
+  SparseTensor forward_fused(const SparseTensor &input, const SparseTensor *residual, bool relu);
   // The affine parameters and running statistics stay fp32 under a dtype
   // cast of the model: bf16 features are normalised in fp32 (the usual
   // mixed-precision rule for normalisation layers). Device moves apply.

@@ -82,8 +82,21 @@ def test_basic_block_structure():
     names = set(blk.named_parameters())
     assert {"conv1.base.kernel", "conv2.base.kernel", "norm1.normalization.weight",
             "norm2.normalization.bias"} <= names
+    assert {"norm1.normalization.running_mean", "norm2.normalization.running_var",
+            "norm1.normalization.num_batches_tracked"} <= set(blk.named_buffers())
     blk.eval()
     assert not blk.training
+
+
+def test_batch_norm_state_names_match_torch():
+    """RiemannBatchNorm keeps torch BatchNorm1d's parameters and buffers
+    under `normalization.` (engine/nn/normalization.hpp:14-23)."""
+    bn = re_.nn.RiemannBatchNorm(6)
+    ref = torch.nn.BatchNorm1d(6)
+    assert set(bn.named_parameters()) == {"normalization." + k for k, _ in
+                                          ref.named_parameters()}
+    assert set(bn.named_buffers()) == {"normalization." + k for k, _ in ref.named_buffers()}
+    assert set(re_.nn.RiemannBatchNorm(6, affine=False).named_parameters()) == set()
 
 
 def test_invalid_layer_arguments():
