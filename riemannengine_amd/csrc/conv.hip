@@ -51,6 +51,13 @@ template <> struct Mfma<float> {
     return *reinterpret_cast<const v4f *>(p);
   }
   __device__ static __forceinline__ Frag zero() { return v4f{0.f, 0.f, 0.f, 0.f}; }
+  // v where keep, else zeros (bitwise, so the load it masks stays unconditional)
+  __device__ static __forceinline__ Frag mask(const Frag &v, bool keep) {
+    const uint32_t m = keep ? ~0u : 0u;
+    uint4 u = __builtin_bit_cast(uint4, v);
+    u.x &= m, u.y &= m, u.z &= m, u.w &= m;
+    return __builtin_bit_cast(Frag, u);
+  }
   __device__ static __forceinline__ void mma(const Frag &a, const Frag &b, v4f &c) {
     c = __builtin_amdgcn_mfma_f32_16x16x4f32(a[0], b[0], c, 0, 0, 0);
     c = __builtin_amdgcn_mfma_f32_16x16x4f32(a[1], b[1], c, 0, 0, 0);
@@ -73,6 +80,13 @@ template <> struct Mfma<__bf16> {
   __device__ static __forceinline__ void mma(const Frag &a, const Frag &b, v4f &c) {
     c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
   }
+  // v where keep, else zeros (bitwise, so the load it masks stays unconditional)
+  __device__ static __forceinline__ Frag mask(const Frag &v, bool keep) {
+    const uint32_t m = keep ? ~0u : 0u;
+    uint4 u = __builtin_bit_cast(uint4, v);
+    u.x &= m, u.y &= m, u.z &= m, u.w &= m;
+    return __builtin_bit_cast(Frag, u);
+  }
 };
 
 __device__ __forceinline__ float to_f32(float v) { return v; }
@@ -90,12 +104,16 @@ template <> __device__ __forceinline__ __bf16 from_f32<__bf16>(float v) {
 // wt is [K][ncols][cred] (reduction axis contiguous). A workgroup owns
 // 4 * RG * 16 output rows and NT columns; RG: 16-row groups per wave; CSUB:
 // 16-byte lane loads per staged channel chunk (chunk = CSUB * kCh channels).
-template <typename T, int NT, int RG, int CSUB, int WAVES = 1>
+// A stage is one (active offset, channel chunk); G stages go at once: their
+// neighbour indices, then their weight chunks (to G LDS slots) and gathered
+// rows (to registers) are all in flight together, so a group costs about
+// two memory latencies and two barriers however many stages it holds.
+template <typename T, int NT, int RG, int CSUB, int G, int WAVES = 1>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(WAVES))) void conv_os_kernel(
     const T *__restrict__ x, int cred, const T *__restrict__ wt, int ncols,
     const float *__restrict__ bias, const int32_t *__restrict__ nbr,
     int64_t n_rows, int K, const int32_t *__restrict__ order,
-    T *__restrict__ y) {
+    T *__restrict__ y, float *__restrict__ partial) {
   using M = Mfma<T>;
   using Frag = typename M::Frag;
   constexpr int CH = M::kCh;
@@ -108,7 +126,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(WAVES)
   constexpr int NV = NT * (CCH / VE);    // 16-byte pieces per staged chunk
   constexpr int NPT = (NV + kThreads - 1) / kThreads;
 
-  __shared__ __align__(16) T sB[NT * LDW];
+  __shared__ __align__(16) T sB[G][NT * LDW];
   __shared__ uint32_t smask[kWaves * RG][kMaskWords];
   __shared__ int32_t slist[32 * kMaskWords];
   __shared__ int32_t scount;
@@ -164,7 +182,11 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(WAVES)
   }
   __syncthreads();
   const int nch = cred / CCH;
-  const int S = scount * nch; // stages: (active offset, channel chunk)
+  // stages: (active offset, channel chunk); split z of gridDim.z takes an
+  // equal share of them and writes fp32 partial sums
+  const int S = scount * nch;
+  const int s_begin = static_cast<int>(static_cast<int64_t>(S) * blockIdx.z / gridDim.z);
+  const int s_end = static_cast<int>(static_cast<int64_t>(S) * (blockIdx.z + 1) / gridDim.z);
 
   v4f acc[RG][NB];
 #pragma unroll
@@ -173,60 +195,100 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(WAVES)
     for (int nb = 0; nb < NB; ++nb)
       acc[r][nb] = v4f{0.f, 0.f, 0.f, 0.f};
 
-  for (int s = 0; s < S; ++s) {
-    const int k = slist[s / nch];
-    const int cc0 = (s % nch) * CCH;
-    // stage W[k][col0 : col0+NT][cc0 : cc0+CCH] (16-byte copies)
+  const int64_t pos0 = tile0 + wv * RG * 16 + i16;
+  for (int s0 = s_begin; s0 < s_end; s0 += G) {
+    // The loads of a group are branch-free so that they issue back to back:
+    // a stage past the end repeats the last one (its results are unused),
+    // indices are read at clamped positions and masked, and a missing
+    // neighbour reads row 0 (an active stage has at least one input row)
+    // and is replaced by zeros.
+    int kj[G], ccj[G];
 #pragma unroll
-    for (int i = 0; i < NPT; ++i) {
-      const int li = threadIdx.x + i * kThreads;
-      if (li < NV) {
-        const int n = li / (CCH / VE), cv = li % (CCH / VE);
-        *reinterpret_cast<uint4 *>(&sB[n * LDW + cv * VE]) = *reinterpret_cast<const uint4 *>(
-            wt + (static_cast<int64_t>(k) * ncols + col0 + n) * cred + cc0 + cv * VE);
+    for (int j = 0; j < G; ++j) {
+      const int sj = min(s0 + j, s_end - 1);
+      kj[j] = slist[sj / nch];
+      ccj[j] = (sj % nch) * CCH;
+    }
+    int32_t idx[G][RG];
+#pragma unroll
+    for (int j = 0; j < G; ++j)
+#pragma unroll
+      for (int r = 0; r < RG; ++r) {
+        const int64_t pos = pos0 + r * 16;
+        const int32_t v = nbr[kj[j] * n_rows + (pos < n_rows ? pos : n_rows - 1)];
+        const bool act = s0 + j < s_end && pos < n_rows &&
+                         ((smask[wv * RG + r][kj[j] >> 5] >> (kj[j] & 31)) & 1u);
+        idx[j][r] = v | (act ? 0 : -1); // a mask, not a select of the load
       }
-    }
-    int32_t idx[RG];
-    bool act[RG];
-    bool wave_act = false;
+    uint4 wreg[G][NPT];
 #pragma unroll
-    for (int r = 0; r < RG; ++r) {
-      const int64_t pos = tile0 + (wv * RG + r) * 16 + i16;
-      act[r] = (smask[wv * RG + r][k >> 5] >> (k & 31)) & 1u;
-      idx[r] = (act[r] && pos < n_rows) ? nbr[k * n_rows + pos] : -1;
-      wave_act |= act[r];
-    }
-    __syncthreads(); // chunk staged
-    if (wave_act) {
-        Frag a[RG][CSUB];
+    for (int j = 0; j < G; ++j)
+#pragma unroll
+      for (int i = 0; i < NPT; ++i) {
+        const int li = min(static_cast<int>(threadIdx.x) + i * kThreads, NV - 1);
+        wreg[j][i] = *reinterpret_cast<const uint4 *>(
+            wt + (static_cast<int64_t>(kj[j]) * ncols + col0 + li / (CCH / VE)) * cred +
+            ccj[j] + (li % (CCH / VE)) * VE);
+      }
+    Frag a[G][RG][CSUB];
+#pragma unroll
+    for (int j = 0; j < G; ++j)
 #pragma unroll
       for (int r = 0; r < RG; ++r)
 #pragma unroll
-        for (int sub = 0; sub < CSUB; ++sub)
-          a[r][sub] = idx[r] >= 0 ? M::load(x + static_cast<int64_t>(idx[r]) * cred + cc0 +
-                                            sub * CH + g * EPL)
-                                  : M::zero();
-      // per group: a uniform branch on its activity (fp32 MFMA time is the
-      // bound, so inactive groups are skipped); the 4 k-steps of a 16-byte
-      // fp32 fragment accumulate back to back. Interleaving the MFMAs over
-      // the accumulators measured slower: it costs occupancy, and the
-      // stalls here are the gathers', not the MFMA chain's.
+        for (int sub = 0; sub < CSUB; ++sub) {
+          const Frag v = M::load(x + static_cast<int64_t>(idx[j][r] < 0 ? 0 : idx[j][r]) * cred +
+                                 ccj[j] + sub * CH + g * EPL);
+          a[j][r][sub] = M::mask(v, idx[j][r] >= 0);
+        }
 #pragma unroll
-      for (int sub = 0; sub < CSUB; ++sub) {
+    for (int j = 0; j < G; ++j)
 #pragma unroll
-        for (int nb = 0; nb < NB; ++nb) {
-          const Frag b =
-              *reinterpret_cast<const Frag *>(&sB[(nb * 16 + i16) * LDW + sub * CH + g * EPL]);
+      for (int i = 0; i < NPT; ++i) {
+        const int li = threadIdx.x + i * kThreads;
+        if (NV % kThreads == 0 || li < NV)
+          *reinterpret_cast<uint4 *>(&sB[j][(li / (CCH / VE)) * LDW + (li % (CCH / VE)) * VE]) =
+              wreg[j][i];
+      }
+    __syncthreads(); // the group's weights are staged
 #pragma unroll
-          for (int r = 0; r < RG; ++r)
-            if (act[r])
-              M::mma(a[r][sub], b, acc[r][nb]);
+    for (int j = 0; j < G; ++j) {
+      bool wave_act = false;
+#pragma unroll
+      for (int r = 0; r < RG; ++r)
+        wave_act |= __ballot(idx[j][r] >= 0) != 0;
+      if (wave_act) { // uniform; false for j >= ns
+#pragma unroll
+        for (int sub = 0; sub < CSUB; ++sub) {
+#pragma unroll
+          for (int nb = 0; nb < NB; ++nb) {
+            const Frag b = *reinterpret_cast<const Frag *>(
+                &sB[j][(nb * 16 + i16) * LDW + sub * CH + g * EPL]);
+#pragma unroll
+            for (int r = 0; r < RG; ++r)
+              M::mma(a[j][r][sub], b, acc[r][nb]);
+          }
         }
       }
     }
-    __syncthreads(); // every wave is done reading the chunk
+    __syncthreads(); // every wave is done reading the group's weights
   }
 
+  if (partial) { // [split][position][column], reduced by conv_os_reduce_kernel
+#pragma unroll
+    for (int r = 0; r < RG; ++r)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int64_t pos = tile0 + (wv * RG + r) * 16 + 4 * g + e;
+        if (pos < n_rows) {
+          float *dst = partial + (blockIdx.z * n_rows + pos) * ncols + col0 + i16;
+#pragma unroll
+          for (int nb = 0; nb < NB; ++nb)
+            dst[nb * 16] = acc[r][nb][e];
+        }
+      }
+    return;
+  }
 #pragma unroll
   for (int r = 0; r < RG; ++r) {
 #pragma unroll
@@ -273,6 +335,33 @@ __global__ __launch_bounds__(kThreads) void conv_os_generic_kernel(
     acc += bias[col];
   const int64_t o = order ? order[pos] : pos;
   y[o * ncols + col] = from_f32<T>(acc);
+}
+
+// y[order[pos]][c] = sum over splits z (in order) of partial[z][pos][c]
+// (+ bias[c]); four columns per lane.
+template <typename T>
+__global__ __launch_bounds__(kThreads) void conv_os_reduce_kernel(
+    const float *__restrict__ partial, int splits, int64_t n_rows, int ncols,
+    const float *__restrict__ bias, const int32_t *__restrict__ order, T *__restrict__ y) {
+  const int64_t t = blockIdx.x * static_cast<int64_t>(kThreads) + threadIdx.x;
+  const int q = ncols / 4;
+  const int64_t pos = t / q;
+  if (pos >= n_rows)
+    return;
+  const int c = static_cast<int>(t - pos * q) * 4;
+  float4 a = *reinterpret_cast<const float4 *>(partial + pos * ncols + c);
+  for (int z = 1; z < splits; ++z) {
+    const float4 b =
+        *reinterpret_cast<const float4 *>(partial + (z * n_rows + pos) * ncols + c);
+    a.x += b.x, a.y += b.y, a.z += b.z, a.w += b.w;
+  }
+  if (bias)
+    a.x += bias[c], a.y += bias[c + 1], a.z += bias[c + 2], a.w += bias[c + 3];
+  T *dst = y + (order ? order[pos] : pos) * ncols + c;
+  dst[0] = from_f32<T>(a.x);
+  dst[1] = from_f32<T>(a.y);
+  dst[2] = from_f32<T>(a.z);
+  dst[3] = from_f32<T>(a.w);
 }
 
 // wt[k][n][c] = w[k][c][n] (weights [K, cin, cout] -> [K, cout, cin]).
@@ -594,62 +683,123 @@ static bool aligned16(const void *p) {
 
 template <typename T> constexpr int kChOf = Mfma<T>::kCh;
 
-template <typename T, int NT, int RG, int CSUB, int WAVES>
+template <typename T, int NT, int RG, int CSUB, int WAVES, int G>
 static void launch_os(const T *x, int cred, const T *wt, int ncols,
                       const float *bias, const int32_t *nbr, int64_t n_rows,
-                      int K, const int32_t *order, T *y, hipStream_t s) {
+                      int K, const int32_t *order, T *y, int splits, float *partial,
+                      hipStream_t s) {
   constexpr int ROWS = kWaves * RG * 16;
-  dim3 grid(static_cast<unsigned>(xcd_grid(ceil_div(n_rows, ROWS))), ncols / NT);
-  hipLaunchKernelGGL((conv_os_kernel<T, NT, RG, CSUB, WAVES>), grid, dim3(kThreads), 0, s, x,
-                     cred, wt, ncols, bias, nbr, n_rows, K, order, y);
+  dim3 grid(static_cast<unsigned>(xcd_grid(ceil_div(n_rows, ROWS))), ncols / NT, splits);
+  hipLaunchKernelGGL((conv_os_kernel<T, NT, RG, CSUB, G, WAVES>), grid, dim3(kThreads), 0, s, x,
+                     cred, wt, ncols, bias, nbr, n_rows, K, order, y,
+                     splits > 1 ? partial : nullptr);
+  if (splits > 1) {
+    RHIP_LAUNCH_CHECK();
+    hipLaunchKernelGGL((conv_os_reduce_kernel<T>),
+                       dim3(static_cast<unsigned>(ceil_div(n_rows * (ncols / 4), kThreads))),
+                       dim3(kThreads), 0, s, partial, splits, n_rows, ncols, bias, order, y);
+  }
 }
 
-// Launch shape, measured on MI355X (config 2, C64): one 16-row group per
-// wave (64 rows per workgroup: more workgroups in flight hide the gather
-// latency better than more rows per wave), the widest channel chunk the
-// reduction width allows, and a register budget for 7 (fp32) or 8 (bf16)
-// waves per SIMD.
-template <typename T> constexpr int kOsWaves = std::is_same<T, float>::value ? 6 : 8;
+// Launch shape, measured on MI355X. One 16-row group per wave (64 rows per
+// workgroup: more workgroups in flight hide the gather latency better than
+// more rows per wave) and the widest channel chunk the reduction width
+// allows. fp32 (config 2, C64): a register budget for 6 waves per SIMD, one
+// stage per barrier. bf16 (config-5 stages): 8 waves per SIMD and one stage
+// per barrier at 64 columns; 128-column tiles (4 waves per SIMD, 2 stages
+// per barrier) for 128 and 256 channels; 4 stages per barrier for 32-channel
+// chunks.
+template <typename T> constexpr bool kIsF32 = std::is_same<T, float>::value;
+
+template <typename T> static int os_nt(int ncols) {
+  if (!kIsF32<T> && ncols % 128 == 0)
+    return 128;
+  return ncols % 64 == 0 ? 64 : (ncols % 32 == 0 ? 32 : 16);
+}
+
+template <typename T, int NT, int CSUB>
+static void launch_shape(const T *x, int cred, const T *wt, int ncols, const float *bias,
+                         const int32_t *nbr, int64_t n_rows, int K, const int32_t *order, T *y,
+                         int splits, float *partial, hipStream_t s) {
+  constexpr int W = kIsF32<T> ? 6 : (NT >= 128 ? 4 : 8);
+  constexpr int G = kIsF32<T> ? 1 : (CSUB == 1 ? 4 : (NT >= 128 ? 2 : 1));
+  launch_os<T, NT, 1, CSUB, W, G>(x, cred, wt, ncols, bias, nbr, n_rows, K, order, y, splits,
+                                  partial, s);
+}
 
 template <typename T, int NT>
 static void pick_csub(const T *x, int cred, const T *wt, int ncols,
                       const float *bias, const int32_t *nbr, int64_t n_rows,
-                      int K, const int32_t *order, T *y, hipStream_t s) {
+                      int K, const int32_t *order, T *y, int splits, float *partial,
+                      hipStream_t s) {
   constexpr int CH = kChOf<T>;
-  constexpr int RG = 1;
-  constexpr int W = kOsWaves<T>;
-  if constexpr (std::is_same<T, float>::value) {
+  if constexpr (kIsF32<T>) {
     if (cred % (4 * CH) == 0) {
-      launch_os<T, NT, RG, 4, W>(x, cred, wt, ncols, bias, nbr, n_rows, K, order, y, s);
+      launch_shape<T, NT, 4>(x, cred, wt, ncols, bias, nbr, n_rows, K, order, y, splits, partial,
+                             s);
       return;
     }
   }
   if (cred % (2 * CH) == 0)
-    launch_os<T, NT, RG, 2, W>(x, cred, wt, ncols, bias, nbr, n_rows, K, order, y, s);
+    launch_shape<T, NT, 2>(x, cred, wt, ncols, bias, nbr, n_rows, K, order, y, splits, partial,
+                           s);
   else
-    launch_os<T, NT, RG, 1, W>(x, cred, wt, ncols, bias, nbr, n_rows, K, order, y, s);
+    launch_shape<T, NT, 1>(x, cred, wt, ncols, bias, nbr, n_rows, K, order, y, splits, partial,
+                           s);
+}
+
+// Whether run_os takes the MFMA kernel for these operands.
+template <typename T>
+static bool os_fast(const T *x, int cred, const T *wt, int ncols, int K) {
+  return cred % kChOf<T> == 0 && ncols % 16 == 0 && K <= 32 * kMaskWords && aligned16(x) &&
+         aligned16(wt);
+}
+
+// Splits of the offset axis for the MFMA kernel: a map with few rows and
+// wide channels gives too few workgroups to hide the gathers (one per CU
+// for 9k rows at 256 channels), so the (offset, channel chunk) stages are
+// shared among up to 8 workgroups per tile, aiming at ~640 workgroups
+// (measured on the config-5 stages), each keeping at least 4 stages on
+// average. 1 = no split.
+template <typename T> static int os_splits(int64_t n_rows, int cred, int ncols, int K) {
+  if (n_rows <= 0 || ncols % 16 != 0)
+    return 1;
+  const int64_t blocks = ceil_div(n_rows, kWaves * 16) * (ncols / os_nt<T>(ncols));
+  const int64_t stages = static_cast<int64_t>(K) * std::max(1, cred / 64);
+  const int64_t want = (640 + blocks / 2) / blocks; // nearest
+  return static_cast<int>(
+      std::max<int64_t>(1, std::min<int64_t>({8, want, std::max<int64_t>(1, stages / 4)})));
+}
+
+// Floats of split partial sums run_os needs (0 without a split).
+template <typename T>
+static size_t os_partial_floats(int64_t n_rows, int cred, int ncols, int K) {
+  const int sp = os_splits<T>(n_rows, cred, ncols, K);
+  return sp > 1 ? static_cast<size_t>(sp) * n_rows * ncols : 0;
 }
 
 // y[order[j]] = sum_k x[nbr[k][j]] @ W'[k] with W'[k][c][n] = wt[k][n][c].
+// partial: os_partial_floats(...) floats, or null to run without a split.
 template <typename T>
 static void run_os(const T *x, int cred, const T *wt, int ncols,
                    const float *bias, const int32_t *nbr, int64_t n_rows, int K,
-                   const int32_t *order, T *y, hipStream_t s) {
+                   const int32_t *order, T *y, float *partial, hipStream_t s) {
   if (n_rows == 0)
     return;
-  constexpr int CH = kChOf<T>;
-  const bool fast = cred % CH == 0 && ncols % 16 == 0 && K <= 32 * kMaskWords &&
-                    aligned16(x) && aligned16(wt);
-  if (!fast) {
+  const int splits = partial ? os_splits<T>(n_rows, cred, ncols, K) : 1;
+  if (!os_fast(x, cred, wt, ncols, K)) {
     hipLaunchKernelGGL((conv_os_generic_kernel<T>), dim3(ceil_div(n_rows * ncols, kThreads)),
                        dim3(kThreads), 0, s, x, cred, wt, ncols, bias, nbr, n_rows, K,
                        order, y);
+  } else if (os_nt<T>(ncols) == 128) {
+    if constexpr (!kIsF32<T>)
+      pick_csub<T, 128>(x, cred, wt, ncols, bias, nbr, n_rows, K, order, y, splits, partial, s);
   } else if (ncols % 64 == 0) {
-    pick_csub<T, 64>(x, cred, wt, ncols, bias, nbr, n_rows, K, order, y, s);
+    pick_csub<T, 64>(x, cred, wt, ncols, bias, nbr, n_rows, K, order, y, splits, partial, s);
   } else if (ncols % 32 == 0) {
-    pick_csub<T, 32>(x, cred, wt, ncols, bias, nbr, n_rows, K, order, y, s);
+    pick_csub<T, 32>(x, cred, wt, ncols, bias, nbr, n_rows, K, order, y, splits, partial, s);
   } else {
-    pick_csub<T, 16>(x, cred, wt, ncols, bias, nbr, n_rows, K, order, y, s);
+    pick_csub<T, 16>(x, cred, wt, ncols, bias, nbr, n_rows, K, order, y, splits, partial, s);
   }
   RHIP_LAUNCH_CHECK();
 }
@@ -760,19 +910,27 @@ static void check_dtype(int32_t dtype) {
 }
 
 // One workspace serves the three calls of a layer: the transposed weights
-// (forward), and for dW either the per-workgroup partial tiles or an fp32
-// accumulator.
+// (forward), the split partial sums of the output-stationary kernel
+// (forward and input gradient), and for dW either the per-workgroup partial
+// tiles or an fp32 accumulator.
 struct ConvWs {
   void *wt = nullptr;
+  float *os_partial = nullptr;
   float *partial = nullptr;
   float *acc = nullptr;
 };
 
 static ConvWs carve_conv(Carve &cv, int32_t K, int32_t cin, int32_t cout, int32_t dtype,
-                         const DwPlan &p) {
+                         int64_t n_in, int64_t n_out, const DwPlan &p) {
   ConvWs w;
   const size_t nw = static_cast<size_t>(K) * cin * cout;
   w.wt = cv.take<char>(nw * (dtype == RHIP_F32 ? 4 : 2));
+  const bool f32 = dtype == RHIP_F32;
+  auto osp = [&](int64_t n, int cred, int ncols) {
+    return f32 ? os_partial_floats<float>(n, cred, ncols, K)
+               : os_partial_floats<__bf16>(n, cred, ncols, K);
+  };
+  w.os_partial = cv.take<float>(std::max<size_t>({1, osp(n_out, cin, cout), osp(n_in, cout, cin)}));
   w.partial = cv.take<float>(std::max<size_t>(1, p.partial_floats() * K));
   w.acc = cv.take<float>(nw);
   return w;
@@ -791,7 +949,7 @@ extern "C" int rhip_conv_workspace_bytes(int32_t K, int32_t cin, int32_t cout,
     RHIP_CHECK_ARG(n_in >= 0 && n_out >= 0 && n_pairs >= 0, "counts must be >= 0");
     check_dtype(dtype);
     Carve cv(nullptr, 0);
-    carve_conv(cv, K, cin, cout, dtype,
+    carve_conv(cv, K, cin, cout, dtype, n_in, n_out,
                dw_plan(dtype, cin, cout, n_pairs, std::min(n_in, n_out)));
     *bytes = cv.used + 256;
   });
@@ -812,25 +970,28 @@ extern "C" int rhip_conv_forward(const void *x, int64_t n_in, int32_t cin,
     RHIP_CHECK_ARG(y && weight && nbr, "y, weight and nbr are required");
     RHIP_CHECK_ARG(n_in == 0 || x != nullptr, "x is null");
     RHIP_CHECK_ARG(workspace != nullptr, "workspace is null");
+    // the workspace was sized for this layer's map (n_in, n_out); the dW
+    // plan does not change the forward's pieces
     Carve cv(workspace, workspace_bytes);
+    const ConvWs w = carve_conv(cv, K, cin, cout, dtype, n_in, n_out, DwPlan{});
     const int64_t nw = static_cast<int64_t>(K) * cin * cout;
     // the MFMA path reads W[k] column-wise: stage the [K, cout, cin] copy
     if (dtype == RHIP_F32) {
-      float *wt = reinterpret_cast<float *>(cv.take<char>(nw * sizeof(float)));
+      float *wt = static_cast<float *>(w.wt);
       hipLaunchKernelGGL((transpose_w_kernel<float>), dim3(ceil_div(nw, kThreads)),
                          dim3(kThreads), 0, stream, static_cast<const float *>(weight), K, cin,
                          cout, wt);
       RHIP_LAUNCH_CHECK();
       run_os<float>(static_cast<const float *>(x), cin, wt, cout, bias, nbr, n_out, K,
-                    out_order, static_cast<float *>(y), stream);
+                    out_order, static_cast<float *>(y), w.os_partial, stream);
     } else {
-      __bf16 *wt = reinterpret_cast<__bf16 *>(cv.take<char>(nw * sizeof(__bf16)));
+      __bf16 *wt = static_cast<__bf16 *>(w.wt);
       hipLaunchKernelGGL((transpose_w_kernel<__bf16>), dim3(ceil_div(nw, kThreads)),
                          dim3(kThreads), 0, stream, static_cast<const __bf16 *>(weight), K,
                          cin, cout, wt);
       RHIP_LAUNCH_CHECK();
       run_os<__bf16>(static_cast<const __bf16 *>(x), cin, wt, cout, bias, nbr, n_out, K,
-                     out_order, static_cast<__bf16 *>(y), stream);
+                     out_order, static_cast<__bf16 *>(y), w.os_partial, stream);
     }
   });
 }
@@ -844,8 +1005,6 @@ extern "C" int rhip_conv_backward_input(const void *grad_y, int64_t n_out,
                                         void *workspace, size_t workspace_bytes,
                                         hipStream_t stream) {
   return guarded([&] {
-    (void)workspace;
-    (void)workspace_bytes;
     check_dtype(dtype);
     RHIP_CHECK_ARG(K >= 1 && cin >= 1 && cout >= 1, "sizes must be positive");
     RHIP_CHECK_ARG(n_in >= 0 && n_out >= 0, "row counts must be >= 0");
@@ -853,15 +1012,21 @@ extern "C" int rhip_conv_backward_input(const void *grad_y, int64_t n_out,
       return;
     RHIP_CHECK_ARG(grad_x && weight && nbr_t, "grad_x, weight and nbr_t are required");
     RHIP_CHECK_ARG(n_out == 0 || grad_y != nullptr, "grad_y is null");
+    // without a workspace the offset axis is not split
+    float *os_partial = nullptr;
+    if (workspace != nullptr) {
+      Carve cv(workspace, workspace_bytes);
+      os_partial = carve_conv(cv, K, cin, cout, dtype, n_in, n_out, DwPlan{}).os_partial;
+    }
     // dX rows gather dY rows; W[k] [cin][cout] is already [n = cin][c = cout].
     if (dtype == RHIP_F32)
       run_os<float>(static_cast<const float *>(grad_y), cout,
                     static_cast<const float *>(weight), cin, nullptr, nbr_t, n_in, K,
-                    in_order, static_cast<float *>(grad_x), stream);
+                    in_order, static_cast<float *>(grad_x), os_partial, stream);
     else
       run_os<__bf16>(static_cast<const __bf16 *>(grad_y), cout,
                      static_cast<const __bf16 *>(weight), cin, nullptr, nbr_t, n_in, K,
-                     in_order, static_cast<__bf16 *>(grad_x), stream);
+                     in_order, static_cast<__bf16 *>(grad_x), os_partial, stream);
   });
 }
 
@@ -881,7 +1046,7 @@ extern "C" int rhip_conv_backward_weight(
     // an offset pairs each input and each output row at most once
     const DwPlan plan = dw_plan(dtype, cin, cout, n_pairs, std::min(n_in, n_out));
     Carve cv(workspace, workspace_bytes);
-    const ConvWs w = carve_conv(cv, K, cin, cout, dtype, plan);
+    const ConvWs w = carve_conv(cv, K, cin, cout, dtype, n_in, n_out, plan);
     if (dtype == RHIP_F32)
       run_dw<float>(static_cast<const float *>(x), cin, static_cast<const float *>(grad_y), cout,
                     kmap_offsets, K, in_rows, out_rows, n_pairs, plan, w.partial, w.acc,

@@ -26,6 +26,8 @@ namespace {
 
 constexpr int kNormThreads = 256;
 constexpr int kChunkRows = 1024; // rows per workgroup of a reduction pass
+constexpr int kUnroll = 4;       // rows loaded together by a reduction thread
+constexpr int kApplyRows = 4;    // rows per thread of an elementwise pass
 
 template <typename T, int V> struct Row;
 template <> struct Row<float, 4> {
@@ -70,6 +72,28 @@ template <> struct Row<__bf16, 1> {
     *p = static_cast<__bf16>(v[0]);
   }
 };
+
+// V consecutive fp32 per-channel values (16-byte loads when V > 1).
+template <int V> __device__ __forceinline__ void load_coef(const float *p, float *v) {
+  if constexpr (V == 1) {
+    v[0] = *p;
+  } else {
+#pragma unroll
+    for (int j = 0; j < V / 4; ++j) {
+      const float4 f = reinterpret_cast<const float4 *>(p)[j];
+      v[4 * j] = f.x, v[4 * j + 1] = f.y, v[4 * j + 2] = f.z, v[4 * j + 3] = f.w;
+    }
+  }
+}
+template <int V> __device__ __forceinline__ void load_coef_or(const float *p, float dflt, float *v) {
+  if (p) {
+    load_coef<V>(p, v);
+  } else {
+#pragma unroll
+    for (int e = 0; e < V; ++e)
+      v[e] = dflt;
+  }
+}
 
 // Lane layout of a reduction workgroup: lpt lanes per row (channel slices of
 // this channel tile), rl = 256 / lpt row lanes.
@@ -116,7 +140,8 @@ __device__ __forceinline__ void combine_rows(const Lanes &l, double (&a)[V], dou
   }
 }
 
-// part[b] = (sum x, sum x^2) over the rows of chunk b.
+// part[b] = (sum x, sum x^2) over the rows of chunk b. A thread's rows are
+// rl apart; kUnroll of them are loaded before any is summed.
 template <typename T, int V>
 __global__ __launch_bounds__(kNormThreads) void bn_sums_kernel(const T *__restrict__ x,
                                                                int64_t n, int C, int lpr, int lpt,
@@ -127,15 +152,25 @@ __global__ __launch_bounds__(kNormThreads) void bn_sums_kernel(const T *__restri
   for (int e = 0; e < V; ++e)
     s[e] = q[e] = 0.0;
   if (l.active) {
-    const int64_t r0 = static_cast<int64_t>(blockIdx.x) * kChunkRows;
-    const int64_t r1 = min(n, r0 + kChunkRows);
-    for (int64_t r = r0 + l.rlane; r < r1; r += l.rl) {
-      float v[V];
-      Row<T, V>::load(x + r * C + l.cc * V, v);
+    const int64_t r1 = min(n, (static_cast<int64_t>(blockIdx.x) + 1) * kChunkRows);
+    const T *p = x + l.cc * V;
+    for (int64_t r = static_cast<int64_t>(blockIdx.x) * kChunkRows + l.rlane; r < r1;
+         r += kUnroll * l.rl) {
+      // rows past the chunk load the chunk's last row and count as zero: the
+      // loads stay unconditional, so all kUnroll are in flight together
+      float v[kUnroll][V];
 #pragma unroll
-      for (int e = 0; e < V; ++e) {
-        s[e] += v[e];
-        q[e] += static_cast<double>(v[e]) * v[e];
+      for (int u = 0; u < kUnroll; ++u)
+        Row<T, V>::load(p + min(r + u * l.rl, r1 - 1) * C, v[u]);
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) {
+        const bool in = r + u * l.rl < r1;
+#pragma unroll
+        for (int e = 0; e < V; ++e) {
+          const float t = in ? v[u][e] : 0.f;
+          s[e] += t;
+          q[e] += static_cast<double>(t) * t;
+        }
       }
     }
   }
@@ -156,25 +191,29 @@ __global__ __launch_bounds__(kNormThreads) void bn_grad_sums_kernel(
     s[e] = q[e] = 0.0;
   if (l.active) {
     float mu[V], is[V];
+    load_coef<V>(mean + l.cc * V, mu);
+    load_coef<V>(invstd + l.cc * V, is);
+    const int64_t r1 = min(n, (static_cast<int64_t>(blockIdx.x) + 1) * kChunkRows);
+    const int64_t c0 = l.cc * V;
+    for (int64_t r = static_cast<int64_t>(blockIdx.x) * kChunkRows + l.rlane; r < r1;
+         r += kUnroll * l.rl) {
+      float g[kUnroll][V], xv[kUnroll][V], yv[kUnroll][V];
 #pragma unroll
-    for (int e = 0; e < V; ++e) {
-      mu[e] = mean[l.cc * V + e];
-      is[e] = invstd[l.cc * V + e];
-    }
-    const int64_t r0 = static_cast<int64_t>(blockIdx.x) * kChunkRows;
-    const int64_t r1 = min(n, r0 + kChunkRows);
-    for (int64_t r = r0 + l.rlane; r < r1; r += l.rl) {
-      const int64_t o = r * C + l.cc * V;
-      float g[V], xv[V], yv[V];
-      Row<T, V>::load(dy + o, g);
-      Row<T, V>::load(x + o, xv);
-      if (relu)
-        Row<T, V>::load(y + o, yv);
+      for (int u = 0; u < kUnroll; ++u) { // unconditional loads, as in bn_sums_kernel
+        const int64_t o = min(r + u * l.rl, r1 - 1) * C + c0;
+        Row<T, V>::load(dy + o, g[u]);
+        Row<T, V>::load(x + o, xv[u]);
+        Row<T, V>::load((relu ? y : dy) + o, yv[u]);
+      }
 #pragma unroll
-      for (int e = 0; e < V; ++e) {
-        const float ge = (relu && !(yv[e] > 0.f)) ? 0.f : g[e];
-        s[e] += ge;
-        q[e] += static_cast<double>(ge) * ((xv[e] - mu[e]) * is[e]);
+      for (int u = 0; u < kUnroll; ++u) {
+        const bool in = r + u * l.rl < r1;
+#pragma unroll
+        for (int e = 0; e < V; ++e) {
+          const float ge = (!in || (relu && !(yv[u][e] > 0.f))) ? 0.f : g[u][e];
+          s[e] += ge;
+          q[e] += static_cast<double>(ge) * ((xv[u][e] - mu[e]) * is[e]);
+        }
       }
     }
   }
@@ -240,76 +279,118 @@ __global__ void bn_invstd_kernel(const float *__restrict__ var, int C, double ep
     invstd[c] = static_cast<float>(1.0 / sqrt(static_cast<double>(var[c]) + eps));
 }
 
-// y = act(((x - mean) * invstd) * gamma + beta [+ residual]). y may alias x
-// or residual: each thread reads its slice before writing it.
+// y = act((x - mean) * invstd * gamma + beta [+ residual]) over rows
+// blockIdx.x * rl * kApplyRows + rlane + j * rl, j < kApplyRows: a thread
+// keeps its channel slice's coefficients and loads all its rows before the
+// first store. y may alias x or residual: a thread writes only the slices it
+// has read.
 template <typename T, int V>
 __global__ __launch_bounds__(kNormThreads) void bn_apply_kernel(
-    const T *x, const T *residual, int64_t n, int C, int lpr, const float *__restrict__ mean,
-    const float *__restrict__ invstd, const float *__restrict__ gamma,
-    const float *__restrict__ beta, int relu, T *y) {
-  const int64_t t = blockIdx.x * static_cast<int64_t>(kNormThreads) + threadIdx.x;
-  const int64_t r = t / lpr;
-  if (r >= n)
+    const T *x, const T *residual, int64_t n, int C, int lpr, int lpt,
+    const float *__restrict__ mean, const float *__restrict__ invstd,
+    const float *__restrict__ gamma, const float *__restrict__ beta, int relu, T *y) {
+  const Lanes l = lanes(lpr, lpt);
+  if (!l.active)
     return;
-  const int c0 = static_cast<int>(t - r * lpr) * V;
-  float v[V], rv[V];
-  Row<T, V>::load(x + r * C + c0, v);
-  if (residual)
-    Row<T, V>::load(residual + r * C + c0, rv);
+  const int c0 = l.cc * V;
+  float mu[V], k[V], b[V], is[V];
+  load_coef<V>(mean + c0, mu);
+  load_coef<V>(invstd + c0, is);
+  load_coef_or<V>(gamma ? gamma + c0 : nullptr, 1.f, k);
+  load_coef_or<V>(beta ? beta + c0 : nullptr, 0.f, b);
 #pragma unroll
-  for (int e = 0; e < V; ++e) {
-    float o = (v[e] - mean[c0 + e]) * invstd[c0 + e];
-    o = o * (gamma ? gamma[c0 + e] : 1.f) + (beta ? beta[c0 + e] : 0.f);
-    if (residual)
-      o += rv[e];
-    v[e] = relu ? fmaxf(o, 0.f) : o;
+  for (int e = 0; e < V; ++e)
+    k[e] *= is[e];
+  const int64_t r0 = static_cast<int64_t>(blockIdx.x) * l.rl * kApplyRows + l.rlane;
+  if (r0 >= n)
+    return;
+  // rows past n load row n - 1 (unconditional loads stay in flight together)
+  // and are not stored
+  float v[kApplyRows][V], rv[kApplyRows][V];
+#pragma unroll
+  for (int u = 0; u < kApplyRows; ++u) {
+    const int64_t o = min(r0 + u * l.rl, n - 1) * C + c0;
+    Row<T, V>::load(x + o, v[u]);
+    Row<T, V>::load((residual ? residual : x) + o, rv[u]);
   }
-  Row<T, V>::store(y + r * C + c0, v);
+#pragma unroll
+  for (int u = 0; u < kApplyRows; ++u) {
+    const int64_t rr = r0 + u * l.rl;
+    if (rr >= n)
+      continue;
+#pragma unroll
+    for (int e = 0; e < V; ++e) {
+      float o = (v[u][e] - mu[e]) * k[e] + b[e];
+      if (residual)
+        o += rv[u][e];
+      v[u][e] = relu ? fmaxf(o, 0.f) : o;
+    }
+    Row<T, V>::store(y + rr * C + c0, v[u]);
+  }
 }
 
 // g = dy masked by y > 0 when relu is set; dresidual = g;
 // batch statistics: dx = gamma * invstd * (g - sum_g / n - xhat * sum_gxhat / n);
-// running statistics: dx = gamma * invstd * g.
+// running statistics: dx = gamma * invstd * g. Rows as in bn_apply_kernel.
 template <typename T, int V>
 __global__ __launch_bounds__(kNormThreads) void bn_grad_apply_kernel(
     const T *__restrict__ dy, const T *__restrict__ y, const T *__restrict__ x, int64_t n, int C,
-    int lpr, const float *__restrict__ mean, const float *__restrict__ invstd,
+    int lpr, int lpt, const float *__restrict__ mean, const float *__restrict__ invstd,
     const float *__restrict__ gamma, const float *__restrict__ sum_g,
     const float *__restrict__ sum_gx, int relu, int batch_stats, T *__restrict__ dx,
     T *__restrict__ dres) {
-  const int64_t t = blockIdx.x * static_cast<int64_t>(kNormThreads) + threadIdx.x;
-  const int64_t r = t / lpr;
-  if (r >= n)
+  const Lanes l = lanes(lpr, lpt);
+  if (!l.active)
     return;
-  const int c0 = static_cast<int>(t - r * lpr) * V;
-  const int64_t o = r * C + c0;
-  float g[V], xv[V], yv[V], out[V];
-  Row<T, V>::load(dy + o, g);
-  if (relu) {
-    Row<T, V>::load(y + o, yv);
-#pragma unroll
-    for (int e = 0; e < V; ++e)
-      g[e] = yv[e] > 0.f ? g[e] : 0.f;
-  }
-  if (dres)
-    Row<T, V>::store(dres + o, g);
-  if (dx == nullptr)
-    return;
-  if (batch_stats)
-    Row<T, V>::load(x + o, xv);
+  const int c0 = l.cc * V;
+  const bool need_x = dx != nullptr && batch_stats;
+  float mu[V], is[V], k[V], a[V], b[V];
   const float inv_n = 1.f / static_cast<float>(n);
+  load_coef<V>(mean + c0, mu);
+  load_coef<V>(invstd + c0, is);
+  load_coef_or<V>(gamma ? gamma + c0 : nullptr, 1.f, k);
+  load_coef_or<V>(batch_stats ? sum_g + c0 : nullptr, 0.f, a);
+  load_coef_or<V>(batch_stats ? sum_gx + c0 : nullptr, 0.f, b);
 #pragma unroll
   for (int e = 0; e < V; ++e) {
-    const int c = c0 + e;
-    const float k = (gamma ? gamma[c] : 1.f) * invstd[c];
-    if (batch_stats) {
-      const float xhat = (xv[e] - mean[c]) * invstd[c];
-      out[e] = k * (g[e] - sum_g[c] * inv_n - xhat * sum_gx[c] * inv_n);
-    } else {
-      out[e] = k * g[e];
-    }
+    k[e] *= is[e];
+    a[e] *= inv_n;
+    b[e] *= inv_n;
   }
-  Row<T, V>::store(dx + o, out);
+  const int64_t r0 = static_cast<int64_t>(blockIdx.x) * l.rl * kApplyRows + l.rlane;
+  if (r0 >= n)
+    return;
+  // rows past n load row n - 1 (as in bn_apply_kernel) and are not stored
+  float g[kApplyRows][V], yv[kApplyRows][V], xv[kApplyRows][V];
+#pragma unroll
+  for (int u = 0; u < kApplyRows; ++u) {
+    const int64_t o = min(r0 + u * l.rl, n - 1) * C + c0;
+    Row<T, V>::load(dy + o, g[u]);
+    Row<T, V>::load((relu ? y : dy) + o, yv[u]);
+    Row<T, V>::load((need_x ? x : dy) + o, xv[u]);
+  }
+#pragma unroll
+  for (int u = 0; u < kApplyRows; ++u) {
+    const int64_t rr = r0 + u * l.rl;
+    if (rr >= n)
+      continue;
+    const int64_t o = rr * C + c0;
+    if (relu)
+#pragma unroll
+      for (int e = 0; e < V; ++e)
+        g[u][e] = yv[u][e] > 0.f ? g[u][e] : 0.f;
+    if (dres)
+      Row<T, V>::store(dres + o, g[u]);
+    if (dx == nullptr)
+      continue;
+    float out[V];
+#pragma unroll
+    for (int e = 0; e < V; ++e) {
+      const float xhat = need_x ? (xv[u][e] - mu[e]) * is[e] : 0.f;
+      out[e] = k[e] * (g[u][e] - a[e] - xhat * b[e]);
+    }
+    Row<T, V>::store(dx + o, out);
+  }
 }
 
 // ------------------------------------------------------------------ host
@@ -345,13 +426,6 @@ template <typename F> void with_type(int32_t dtype, F &&f) {
     f(__bf16{});
 }
 
-unsigned blocks_for(int64_t threads) {
-  const int64_t b = ceil_div(std::max<int64_t>(threads, 1), kNormThreads);
-  if (b > INT_MAX)
-    throw Error(RHIP_ERR_UNSUPPORTED, "launch exceeds the grid limit");
-  return static_cast<unsigned>(b);
-}
-
 int64_t chunks_of(int64_t n) { return std::max<int64_t>(1, ceil_div(n, kChunkRows)); }
 
 struct NormWs {
@@ -366,12 +440,16 @@ NormWs carve_norm(Carve &cv, int64_t n, int C) {
   return w;
 }
 
-// Reduction pass + per-channel combine over [n, C] features.
+// Launch shape over [n, C] features: lpr slices per row, lpt of them per
+// workgroup (grid.y over channel tiles), rl = 256 / lpt rows side by side.
+// Reductions take kChunkRows rows per workgroup, elementwise passes
+// rl * kApplyRows.
 template <typename T, int V, typename Launch>
-void reduce_rows(int64_t n, int C, Launch &&launch) {
-  const int lpr = C / V, lpt = std::min(lpr, kNormThreads);
-  dim3 grid(static_cast<unsigned>(chunks_of(n)), static_cast<unsigned>(ceil_div(lpr, lpt)));
-  launch(grid, lpr, lpt);
+void over_rows(int64_t n, int C, bool reduction, Launch &&launch) {
+  const int lpr = C / V, lpt = std::min(lpr, kNormThreads), rl = kNormThreads / lpt;
+  const int64_t gx = reduction ? chunks_of(n) : std::max<int64_t>(1, ceil_div(n, rl * kApplyRows));
+  RHIP_CHECK_ARG(gx <= INT_MAX, "too many rows for one launch");
+  launch(dim3(static_cast<unsigned>(gx), static_cast<unsigned>(ceil_div(lpr, lpt))), lpr, lpt);
 }
 
 } // namespace
@@ -405,7 +483,7 @@ extern "C" int rhip_bn_stats(const void *x, int64_t n, int32_t C, int32_t dtype,
       using T = decltype(tag);
       with_width<T>(width<T>(C, {x}), [&](auto v) {
         constexpr int V = decltype(v)::value;
-        reduce_rows<T, V>(n, C, [&](dim3 grid, int lpr, int lpt) {
+        over_rows<T, V>(n, C, true, [&](dim3 grid, int lpr, int lpt) {
           hipLaunchKernelGGL((bn_sums_kernel<T, V>), grid, dim3(kNormThreads), 0, stream,
                              static_cast<const T *>(x), n, C, lpr, lpt, w.part);
           RHIP_LAUNCH_CHECK();
@@ -441,14 +519,14 @@ extern "C" int rhip_bn_forward(const void *x, int64_t n, int32_t C, const float 
     RHIP_CHECK_ARG(x && y && mean && invstd, "x, y, mean and invstd are required");
     with_type(dtype, [&](auto tag) {
       using T = decltype(tag);
-      with_width<T>(width<T>(C, {x, y, residual}), [&](auto v) {
+      with_width<T>(width<T>(C, {x, y, residual, mean, invstd, gamma, beta}), [&](auto v) {
         constexpr int V = decltype(v)::value;
-        const int lpr = C / V;
-        hipLaunchKernelGGL((bn_apply_kernel<T, V>), dim3(blocks_for(n * lpr)),
-                           dim3(kNormThreads), 0, stream, static_cast<const T *>(x),
-                           static_cast<const T *>(residual), n, C, lpr, mean, invstd, gamma, beta,
-                           relu, static_cast<T *>(y));
-        RHIP_LAUNCH_CHECK();
+        over_rows<T, V>(n, C, false, [&](dim3 grid, int lpr, int lpt) {
+          hipLaunchKernelGGL((bn_apply_kernel<T, V>), grid, dim3(kNormThreads), 0, stream,
+                             static_cast<const T *>(x), static_cast<const T *>(residual), n, C,
+                             lpr, lpt, mean, invstd, gamma, beta, relu, static_cast<T *>(y));
+          RHIP_LAUNCH_CHECK();
+        });
       });
     });
   });
@@ -471,10 +549,11 @@ extern "C" int rhip_bn_backward(const void *grad_y, const void *y, const void *x
     const bool sums = (batch_stats && grad_x) || grad_gamma || grad_beta;
     with_type(dtype, [&](auto tag) {
       using T = decltype(tag);
-      with_width<T>(width<T>(C, {grad_y, y, x, grad_x, grad_residual}), [&](auto v) {
+      with_width<T>(width<T>(C, {grad_y, y, x, grad_x, grad_residual, mean, invstd, gamma}),
+                    [&](auto v) {
         constexpr int V = decltype(v)::value;
         if (sums) { // n = 0: one empty chunk, zero sums
-          reduce_rows<T, V>(n, C, [&](dim3 grid, int lpr, int lpt) {
+          over_rows<T, V>(n, C, true, [&](dim3 grid, int lpr, int lpt) {
             hipLaunchKernelGGL((bn_grad_sums_kernel<T, V>), grid, dim3(kNormThreads), 0, stream,
                                static_cast<const T *>(grad_y), static_cast<const T *>(y),
                                static_cast<const T *>(x), n, C, lpr, lpt, mean, invstd, relu,
@@ -487,13 +566,14 @@ extern "C" int rhip_bn_backward(const void *grad_y, const void *y, const void *x
           RHIP_LAUNCH_CHECK();
         }
         if (n > 0 && (grad_x || grad_residual)) {
-          const int lpr = C / V;
-          hipLaunchKernelGGL((bn_grad_apply_kernel<T, V>), dim3(blocks_for(n * lpr)),
-                             dim3(kNormThreads), 0, stream, static_cast<const T *>(grad_y),
-                             static_cast<const T *>(y), static_cast<const T *>(x), n, C, lpr,
-                             mean, invstd, gamma, w.sum_g, w.sum_gx, relu, batch_stats,
-                             static_cast<T *>(grad_x), static_cast<T *>(grad_residual));
-          RHIP_LAUNCH_CHECK();
+          over_rows<T, V>(n, C, false, [&](dim3 grid, int lpr, int lpt) {
+            hipLaunchKernelGGL((bn_grad_apply_kernel<T, V>), grid, dim3(kNormThreads), 0,
+                               stream, static_cast<const T *>(grad_y), static_cast<const T *>(y),
+                               static_cast<const T *>(x), n, C, lpr, lpt, mean, invstd, gamma,
+                               w.sum_g, w.sum_gx, relu, batch_stats, static_cast<T *>(grad_x),
+                               static_cast<T *>(grad_residual));
+            RHIP_LAUNCH_CHECK();
+          });
         }
       });
     });

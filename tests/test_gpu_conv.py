@@ -70,6 +70,29 @@ def test_conv_bias_fp32():
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_offset_split_matches_unsplit_and_oracle(dtype):
+    """Few rows with wide channels split the offset axis over workgroups
+    (fp32 partial sums reduced in a fixed order, bias added once): forward
+    with bias and dX vs the oracle, and dX vs the unsplit kernel (no
+    workspace)."""
+    rng = np.random.default_rng(21)
+    c, _, _ = oracle.insert_and_map(random_coords(rng, 2500, 3, 9))
+    _, _, km = gpu_tables_and_map(c, c, oracle.region_offsets(3, 3), same=True)
+    _run_and_check(km, 256, 256, dtype, seed=5, bias=True, tag="split")
+    g = torch.Generator().manual_seed(3)
+    gy = torch.randn(km.n_out, 256, generator=g).to(dtype).to(DEV)
+    w = (torch.randn(27, 256, 256, generator=g) / 80).to(dtype).to(DEV)
+    split = abi.conv_backward_input(gy, w, km)
+    plain = torch.empty_like(split)
+    abi._check(abi.lib().rhip_conv_backward_input(
+        abi._ptr(gy), km.n_out, 256, abi._ptr(w), 27, 256, abi._ptr(km.nbr_t),
+        abi._ptr(km.in_order), km.n_in, abi._ptr(plain), abi._dtype_code(dtype), None, 0,
+        abi._stream(gy.device)), "rhip_conv_backward_input")
+    assert_rel(split.float().cpu().numpy(), plain.float().cpu().numpy(),
+               1e-5 if dtype == torch.float32 else 1e-2, "split vs unsplit dX")
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_conv_4d_81_offsets(dtype):
     rng = np.random.default_rng(81)
     c, _, _ = oracle.insert_and_map(random_coords(rng, 8000, 4, 7, batch=1))
