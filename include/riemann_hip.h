@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define RHIP_ABI_VERSION 9
+#define RHIP_ABI_VERSION 10
 #define RHIP_MAX_COLS 8 /* batch column + up to 7 spatial axes */
 
 typedef enum rhip_status {
@@ -255,6 +255,24 @@ int rhip_conv_backward_weight(const void *x, int64_t n_in, int32_t cin,
                               const int32_t *out_rows, void *grad_w,
                               int32_t dtype, void *workspace,
                               size_t workspace_bytes, hipStream_t stream);
+
+/*
+ * The same weight gradient from the dense neighbour table instead of the
+ * pair list: grad_w[k] = sum over output positions j with
+ * nbr[k*n_out+j] >= 0 of x[nbr[k*n_out+j]]^T grad_y[out_order[j]]
+ * (out_order NULL = identity), fp32 accumulation, deterministic. For bf16
+ * layers with 16 or 32 input and output channels, where each dY row is read
+ * once per group of offsets rather than once per pair; other shapes return
+ * RHIP_ERR_UNSUPPORTED. Workspace as for rhip_conv_workspace_bytes.
+ * Replaces the dW half of MmBackward (engine/nn/conv.cpp:62), like
+ * rhip_conv_backward_weight.
+ */
+int rhip_conv_backward_weight_rows(const void *x, int64_t n_in, int32_t cin,
+                                   const void *grad_y, int64_t n_out,
+                                   int32_t cout, int32_t K, const int32_t *nbr,
+                                   const int32_t *out_order, void *grad_w,
+                                   int32_t dtype, void *workspace,
+                                   size_t workspace_bytes, hipStream_t stream);
 
 /* --------------------------------------------------------------- pooling */
 

@@ -32,7 +32,7 @@ EXPORTS = (
     "rhip_order_workspace_bytes", "rhip_spatial_order", "rhip_stride_coords",
     "rhip_expand_coords", "rhip_kmap_workspace_bytes", "rhip_kmap_count", "rhip_kmap_fill",
     "rhip_conv_workspace_bytes", "rhip_conv_forward",
-    "rhip_conv_backward_input", "rhip_conv_backward_weight",
+    "rhip_conv_backward_input", "rhip_conv_backward_weight", "rhip_conv_backward_weight_rows",
     "rhip_stride_map_workspace_bytes", "rhip_stride_map_count", "rhip_group_map_count",
     "rhip_stride_map_fill",
     "rhip_table_compact", "rhip_pool_workspace_bytes", "rhip_pool_forward",
@@ -88,6 +88,8 @@ def _declare(lib):
         "rhip_conv_backward_weight": (ctypes.c_int, [_vp, _i64, _i32, _vp, _i64, _i32,
                                                      _i32, _vp, _i64, _vp, _vp, _vp,
                                                      _i32, _vp, _sz, _vp]),
+        "rhip_conv_backward_weight_rows": (ctypes.c_int, [_vp, _i64, _i32, _vp, _i64, _i32, _i32,
+                                                          _vp, _vp, _vp, _i32, _vp, _sz, _vp]),
         "rhip_stride_map_workspace_bytes": (ctypes.c_int, [_i64, _i64, _P(_sz)]),
         "rhip_stride_map_count": (ctypes.c_int, [_P(RhipTable), _vp, _i64, _P(_i32), _vp, _sz,
                                                  _P(_i32), _vp]),
@@ -404,6 +406,23 @@ def conv_backward_weight(x: torch.Tensor, grad_y: torch.Tensor, kmap: KernelMap,
                                            dt, _ptr(ws), ws.numel(), _stream(x.device)),
            "rhip_conv_backward_weight")
     return gw if out_dtype is None else gw.to(out_dtype)
+
+
+def conv_backward_weight_rows(x: torch.Tensor, grad_y: torch.Tensor, kmap: KernelMap,
+                              K: int) -> torch.Tensor:
+    """dW from the kernel map's neighbour table (bf16, 16 or 32 channels)."""
+    _require_cuda(x, "x")
+    dt = _dtype_code(x.dtype)
+    x, grad_y = x.contiguous(), grad_y.to(x.dtype).contiguous()
+    cin, cout = x.shape[1], grad_y.shape[1]
+    gw = torch.empty((K, cin, cout), dtype=x.dtype, device=x.device)
+    ws = _conv_ws(K, cin, cout, dt, x.device, kmap)
+    _check(lib().rhip_conv_backward_weight_rows(_ptr(x), kmap.n_in, cin, _ptr(grad_y),
+                                                kmap.n_out, cout, K, _ptr(kmap.nbr),
+                                                _ptr(kmap.out_order), _ptr(gw), dt, _ptr(ws),
+                                                ws.numel(), _stream(x.device)),
+           "rhip_conv_backward_weight_rows")
+    return gw
 
 
 # ---------------------------------------------------------------- pooling

@@ -642,6 +642,227 @@ __global__ __launch_bounds__(kThreads) void conv_dw_reduce_kernel(
   }
 }
 
+// ------------------------------------------------------------ dW by rows
+//
+// For narrow bf16 layers (cin, cout in {16, 32}) dW is computed from the
+// dense neighbour table instead of the pair list: each dY row is read once
+// per group of offsets rather than once per pair, which halves the gathered
+// bytes of a 3^3 map (about 10 neighbours per row).
+//
+// A workgroup owns a range of output positions and KW offsets (grid.y picks
+// the offset group); its four waves take alternate 32-position sub-tiles and
+// work independently, each with its own LDS rows: the sub-tile's dY rows
+// (32 x cout) and, one offset at a time, the gathered X rows (32 x cin),
+// read back K-major with ds_read_tr16 (as in conv_dw_kernel) and multiplied
+// on v_mfma_f32_16x16x32_bf16 with the positions as the reduction axis. The
+// next offset's rows are in flight while the current one multiplies. LDS
+// traffic of a wave is ordered within the wave, so no workgroup barrier is
+// needed until the end, where the four waves' tiles are added in wave order
+// and the workgroup writes one partial slot per offset.
+constexpr int kDwRowsSP = 32; // positions per sub-tile (one MFMA reduction step)
+
+template <int VA, int VB, int KW>
+__global__ __launch_bounds__(kThreads) void conv_dw_rows_kernel(
+    const __bf16 *__restrict__ x, const __bf16 *__restrict__ gy,
+    const int32_t *__restrict__ nbr, const int32_t *__restrict__ out_order, int64_t n_out,
+    int K, int64_t rows_per_block, float *__restrict__ partial) {
+  constexpr int TM = 16 * VA, TN = 16 * VB, SP = kDwRowsSP;
+  constexpr int LDX = TM + 8, LDG = TN + 8; // 16-byte row padding
+  __shared__ __align__(16) __bf16 sG[kWaves][SP * LDG];
+  __shared__ __align__(16) __bf16 sX[kWaves][SP * LDX];
+  __shared__ __align__(16) float red[KW * TM * TN];
+
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wv = threadIdx.x / kWave;
+  const int i16 = lane & 15;
+  const int g = lane >> 4;
+  const int64_t p0 = blockIdx.x * rows_per_block;
+  const int64_t p1 = min(n_out, p0 + rows_per_block);
+  const int k0 = blockIdx.y * KW;
+
+  v4f acc[KW][VA][VB];
+#pragma unroll
+  for (int j = 0; j < KW; ++j)
+#pragma unroll
+    for (int ea = 0; ea < VA; ++ea)
+#pragma unroll
+      for (int eb = 0; eb < VB; ++eb)
+        acc[j][ea][eb] = v4f{0.f, 0.f, 0.f, 0.f};
+
+  // lane pieces (16 bytes) of a 32-row sub-tile: X piece i of offset j is
+  // row (lane + 64 i) / (TM / 8), 8 channels at (lane + 64 i) % (TM / 8)
+  const int prow = 8 * g + i16 / 4, pcol = 4 * (i16 % 4);
+  // indices of sub-tile q: the dY rows' output rows and every offset's
+  // neighbours (-1: none or past the range; clamped reads, masked)
+  int64_t orow[VB];
+  int32_t id[KW][VA];
+  auto load_ids = [&](int64_t q, int64_t (&orow_)[VB], int32_t (&id_)[KW][VA]) {
+#pragma unroll
+    for (int i = 0; i < VB; ++i) {
+      const int64_t pos = q + (lane + kWave * i) / (TN / 8);
+      const int64_t pc_ = pos < p1 ? pos : p1 - 1;
+      orow_[i] = (out_order ? out_order[pc_] : pc_) | (pos < p1 ? 0 : -1);
+    }
+#pragma unroll
+    for (int j = 0; j < KW; ++j)
+#pragma unroll
+      for (int i = 0; i < VA; ++i) {
+        const int64_t pos = q + (lane + kWave * i) / (TM / 8);
+        const int kk = k0 + j < K ? k0 + j : K - 1;
+        const int32_t v = nbr[kk * n_out + (pos < p1 ? pos : p1 - 1)];
+        id_[j][i] = v | ((k0 + j < K && pos < p1) ? 0 : -1);
+      }
+  };
+  const int64_t q_first = p0 + wv * SP;
+  if (q_first < p1)
+    load_ids(q_first, orow, id);
+  for (int64_t q = q_first; q < p1; q += kWaves * SP) {
+    // this sub-tile's dY rows and first offset's rows, then the next
+    // sub-tile's indices, all in flight together
+    uint4 gv[VB];
+#pragma unroll
+    for (int i = 0; i < VB; ++i) {
+      const int pc = lane + kWave * i;
+      gv[i] = *reinterpret_cast<const uint4 *>(gy + (orow[i] < 0 ? 0 : orow[i]) * TN +
+                                               (pc % (TN / 8)) * 8);
+    }
+    uint4 xv[VA], xn[VA];
+#pragma unroll
+    for (int i = 0; i < VA; ++i) {
+      const int pc = lane + kWave * i;
+      xv[i] = *reinterpret_cast<const uint4 *>(
+          x + static_cast<int64_t>(id[0][i] < 0 ? 0 : id[0][i]) * TM + (pc % (TM / 8)) * 8);
+    }
+    int64_t orow_n[VB];
+    int32_t id_n[KW][VA];
+    const bool more = q + kWaves * SP < p1; // uniform
+    if (more)
+      load_ids(q + kWaves * SP, orow_n, id_n);
+#pragma unroll
+    for (int i = 0; i < VB; ++i) {
+      const int pc = lane + kWave * i;
+      uint4 v = gv[i];
+      const uint32_t m = orow[i] >= 0 ? ~0u : 0u;
+      v.x &= m, v.y &= m, v.z &= m, v.w &= m;
+      *reinterpret_cast<uint4 *>(&sG[wv][(pc / (TN / 8)) * LDG + (pc % (TN / 8)) * 8]) = v;
+    }
+    __builtin_amdgcn_wave_barrier();
+    v8bf bfr[VB];
+#pragma unroll
+    for (int eb = 0; eb < VB; ++eb) {
+      const v4s lo = ds_read_tr16(&sG[wv][prow * LDG + 16 * eb + pcol]);
+      const v4s hi = ds_read_tr16(&sG[wv][(prow + 4) * LDG + 16 * eb + pcol]);
+      bfr[eb] = __builtin_bit_cast(v8bf, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+    }
+#pragma unroll
+    for (int j = 0; j < KW; ++j) {
+      if (j + 1 < KW) { // the next offset's rows
+#pragma unroll
+        for (int i = 0; i < VA; ++i) {
+          const int pc = lane + kWave * i;
+          xn[i] = *reinterpret_cast<const uint4 *>(
+              x + static_cast<int64_t>(id[j + 1][i] < 0 ? 0 : id[j + 1][i]) * TM +
+              (pc % (TM / 8)) * 8);
+        }
+      }
+      bool any = false;
+#pragma unroll
+      for (int i = 0; i < VA; ++i) {
+        const int pc = lane + kWave * i;
+        uint4 v = xv[i];
+        const uint32_t m = id[j][i] >= 0 ? ~0u : 0u;
+        v.x &= m, v.y &= m, v.z &= m, v.w &= m;
+        *reinterpret_cast<uint4 *>(&sX[wv][(pc / (TM / 8)) * LDX + (pc % (TM / 8)) * 8]) = v;
+        any |= id[j][i] >= 0;
+      }
+      __builtin_amdgcn_wave_barrier();
+      if (__ballot(any) != 0) { // uniform
+#pragma unroll
+        for (int ea = 0; ea < VA; ++ea) {
+          const v4s lo = ds_read_tr16(&sX[wv][prow * LDX + 16 * ea + pcol]);
+          const v4s hi = ds_read_tr16(&sX[wv][(prow + 4) * LDX + 16 * ea + pcol]);
+          const v8bf af =
+              __builtin_bit_cast(v8bf, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+#pragma unroll
+          for (int eb = 0; eb < VB; ++eb)
+            acc[j][ea][eb] =
+                __builtin_amdgcn_mfma_f32_16x16x32_bf16(af, bfr[eb], acc[j][ea][eb], 0, 0, 0);
+        }
+      }
+      __builtin_amdgcn_wave_barrier();
+      if (j + 1 < KW) {
+#pragma unroll
+        for (int i = 0; i < VA; ++i)
+          xv[i] = xn[i];
+      }
+    }
+    if (more) {
+#pragma unroll
+      for (int i = 0; i < VB; ++i)
+        orow[i] = orow_n[i];
+#pragma unroll
+      for (int j = 0; j < KW; ++j)
+#pragma unroll
+        for (int i = 0; i < VA; ++i)
+          id[j][i] = id_n[j][i];
+    }
+  }
+
+  // add the four waves' tiles in wave order, then one partial slot per
+  // offset: partial[blockIdx.x][k][ci][co]; lane holds D[4g+e][i16] of
+  // block (ea, eb), i.e. ci = 16 ea + 4 g + e, co = 16 eb + i16
+  for (int w = 0; w < kWaves; ++w) {
+    if (wv == w) {
+#pragma unroll
+      for (int j = 0; j < KW; ++j)
+#pragma unroll
+        for (int ea = 0; ea < VA; ++ea)
+#pragma unroll
+          for (int eb = 0; eb < VB; ++eb)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              float &r = red[(j * TM + 16 * ea + 4 * g + e) * TN + 16 * eb + i16];
+              r = w == 0 ? acc[j][ea][eb][e] : r + acc[j][ea][eb][e];
+            }
+    }
+    __syncthreads();
+  }
+  const int kn = min(KW, K - k0);
+  float *slot = partial + (static_cast<int64_t>(blockIdx.x) * K + k0) * (TM * TN);
+  for (int i = threadIdx.x; i < kn * TM * TN; i += kThreads)
+    slot[i] = red[i];
+}
+
+// dw[k][ci][co] = sum over the slots s (in order) of partial[s][k][ci][co].
+// A workgroup of 16 waves owns 256 consecutive elements (a float4 per lane);
+// wave w sums the slots s = w (mod 16), the 16 sums are then added in order.
+template <typename OutT>
+__global__ __launch_bounds__(1024) void conv_dw_rows_reduce_kernel(
+    const float *__restrict__ partial, int slots, int64_t n_elem, OutT *__restrict__ dw) {
+  __shared__ v4f part[16][kWave];
+  const int lane = threadIdx.x & (kWave - 1), w = threadIdx.x / kWave;
+  const int64_t i4 = static_cast<int64_t>(blockIdx.x) * kWave + lane;
+  const int64_t n4 = n_elem / 4;
+  v4f sum = v4f{0.f, 0.f, 0.f, 0.f};
+  if (i4 < n4) {
+    const v4f *src = reinterpret_cast<const v4f *>(partial) + i4;
+#pragma unroll 4
+    for (int s = w; s < slots; s += 16)
+      sum += src[static_cast<int64_t>(s) * n4];
+  }
+  part[w][lane] = sum;
+  __syncthreads();
+  if (w != 0 || i4 >= n4)
+    return;
+  v4f v = part[0][lane];
+#pragma unroll
+  for (int q = 1; q < 16; ++q)
+    v += part[q][lane];
+#pragma unroll
+  for (int e = 0; e < 4; ++e)
+    dw[4 * i4 + e] = from_f32<OutT>(v[e]);
+}
+
 // Any-shape fallback: one lane per dW element, looping over its pairs.
 template <typename T>
 __global__ __launch_bounds__(kThreads) void conv_dw_generic_kernel(
@@ -909,6 +1130,62 @@ static void check_dtype(int32_t dtype) {
     throw Error(RHIP_ERR_UNSUPPORTED, "dtype must be RHIP_F32 or RHIP_BF16");
 }
 
+// dW from the neighbour table (conv_dw_rows_kernel): bf16 with 16 or 32
+// input and output channels. Measured on MI355X (config-5 stage 1, 808k
+// rows, C32): 3 offsets per wave and 64 row blocks (about 2.2x the
+// pair-list kernel's rate).
+constexpr int kDwRowsKW = 3;
+constexpr int kDwRowsBlocks = 64;
+
+static bool dw_rows_supported(int32_t dtype, int cin, int cout) {
+  return dtype == RHIP_BF16 && (cin == 16 || cin == 32) && (cout == 16 || cout == 32);
+}
+
+// Partial floats of the row kernel: one slot per row block and offset.
+static size_t dw_rows_floats(int K, int cin, int cout) {
+  return static_cast<size_t>(kDwRowsBlocks) * K * cin * cout;
+}
+
+template <int VA, int VB>
+static void launch_dw_rows(const __bf16 *x, const __bf16 *gy, const int32_t *nbr,
+                           const int32_t *out_order, int64_t n_out, int K, int64_t rpb,
+                           int blocks, float *partial, hipStream_t s) {
+  dim3 grid(static_cast<unsigned>(blocks), static_cast<unsigned>(ceil_div(K, kDwRowsKW)));
+  hipLaunchKernelGGL((conv_dw_rows_kernel<VA, VB, kDwRowsKW>), grid, dim3(kThreads), 0, s, x, gy,
+                     nbr, out_order, n_out, K, rpb, partial);
+}
+
+// grad_w [K, cin, cout] (bf16, overwritten) from the neighbour table.
+static void run_dw_rows(const __bf16 *x, int64_t n_in, int cin, const __bf16 *gy, int64_t n_out,
+                        int cout, int K, const int32_t *nbr, const int32_t *out_order,
+                        float *partial, __bf16 *dw, hipStream_t s) {
+  int blocks = 0;
+  if (n_in > 0 && n_out > 0) { // without rows every slot sum is empty: zeros
+    const int64_t rb = std::min<int64_t>(kDwRowsBlocks, ceil_div(n_out, kDwRowsSP));
+    const int64_t rpb = ceil_div(ceil_div(n_out, rb), kDwRowsSP) * kDwRowsSP;
+    blocks = static_cast<int>(ceil_div(n_out, rpb));
+    auto go = [&](auto va, auto vb) {
+      launch_dw_rows<decltype(va)::value, decltype(vb)::value>(x, gy, nbr, out_order, n_out, K,
+                                                               rpb, blocks, partial, s);
+    };
+    using I1 = std::integral_constant<int, 1>;
+    using I2 = std::integral_constant<int, 2>;
+    if (cin == 32 && cout == 32)
+      go(I2{}, I2{});
+    else if (cin == 32)
+      go(I2{}, I1{});
+    else if (cout == 32)
+      go(I1{}, I2{});
+    else
+      go(I1{}, I1{});
+    RHIP_LAUNCH_CHECK();
+  }
+  const int64_t ne = static_cast<int64_t>(K) * cin * cout;
+  hipLaunchKernelGGL((conv_dw_rows_reduce_kernel<__bf16>), dim3(static_cast<unsigned>(
+                         ceil_div(ne / 4, kWave))), dim3(1024), 0, s, partial, blocks, ne, dw);
+  RHIP_LAUNCH_CHECK();
+}
+
 // One workspace serves the three calls of a layer: the transposed weights
 // (forward), the split partial sums of the output-stationary kernel
 // (forward and input gradient), and for dW either the per-workgroup partial
@@ -931,7 +1208,7 @@ static ConvWs carve_conv(Carve &cv, int32_t K, int32_t cin, int32_t cout, int32_
                : os_partial_floats<__bf16>(n, cred, ncols, K);
   };
   w.os_partial = cv.take<float>(std::max<size_t>({1, osp(n_out, cin, cout), osp(n_in, cout, cin)}));
-  w.partial = cv.take<float>(std::max<size_t>(1, p.partial_floats() * K));
+  w.partial = cv.take<float>(std::max<size_t>({1, p.partial_floats() * K, dw_rows_floats(K, cin, cout)}));
   w.acc = cv.take<float>(nw);
   return w;
 }
@@ -1055,5 +1332,29 @@ extern "C" int rhip_conv_backward_weight(
       run_dw<__bf16>(static_cast<const __bf16 *>(x), cin, static_cast<const __bf16 *>(grad_y),
                      cout, kmap_offsets, K, in_rows, out_rows, n_pairs, plan, w.partial, w.acc,
                      static_cast<__bf16 *>(grad_w), stream);
+  });
+}
+
+extern "C" int rhip_conv_backward_weight_rows(
+    const void *x, int64_t n_in, int32_t cin, const void *grad_y, int64_t n_out,
+    int32_t cout, int32_t K, const int32_t *nbr, const int32_t *out_order, void *grad_w,
+    int32_t dtype, void *workspace, size_t workspace_bytes, hipStream_t stream) {
+  return guarded([&] {
+    check_dtype(dtype);
+    RHIP_CHECK_ARG(K >= 1 && cin >= 1 && cout >= 1, "sizes must be positive");
+    RHIP_CHECK_ARG(n_in >= 0 && n_out >= 0, "bad sizes");
+    if (!dw_rows_supported(dtype, cin, cout))
+      throw Error(RHIP_ERR_UNSUPPORTED,
+                  "rhip_conv_backward_weight_rows: bf16 with 16 or 32 input and output "
+                  "channels only (use rhip_conv_backward_weight)");
+    RHIP_CHECK_ARG(grad_w != nullptr, "grad_w is null");
+    RHIP_CHECK_ARG(n_in == 0 || n_out == 0 || (x && grad_y && nbr),
+                   "x, grad_y and nbr are required");
+    RHIP_CHECK_ARG(workspace != nullptr, "workspace is null");
+    RHIP_CHECK_ARG(aligned16(x) && aligned16(grad_y), "x and grad_y must be 16-byte aligned");
+    Carve cv(workspace, workspace_bytes);
+    const ConvWs w = carve_conv(cv, K, cin, cout, dtype, n_in, n_out, DwPlan{});
+    run_dw_rows(static_cast<const __bf16 *>(x), n_in, cin, static_cast<const __bf16 *>(grad_y),
+                n_out, cout, K, nbr, out_order, w.partial, static_cast<__bf16 *>(grad_w), stream);
   });
 }

@@ -61,7 +61,7 @@ struct HipConvolutionFunction : public torch::autograd::Function<HipConvolutionF
                                  ws.data_ptr(), ws.numel(),
                                  c10::hip::getCurrentHIPStream(dev.index()).stream()),
                "rhip_conv_forward");
-    ctx->save_for_backward({x, w, nbr_t, in_order, offsets, in_rows, out_rows});
+    ctx->save_for_backward({x, w, nbr_t, in_order, offsets, in_rows, out_rows, nbr, out_order});
     ctx->saved_data["n_pairs"] = n_pairs;
     ctx->saved_data["n_out"] = n_out;
     return y;
@@ -71,6 +71,7 @@ struct HipConvolutionFunction : public torch::autograd::Function<HipConvolutionF
     auto saved = ctx->get_saved_variables();
     auto x = saved[0], w = saved[1], nbr_t = saved[2], in_order = saved[3];
     auto offsets = saved[4], in_rows = saved[5], out_rows = saved[6];
+    auto nbr = saved[7], out_order = saved[8];
     const int64_t n_pairs = ctx->saved_data["n_pairs"].toInt();
     const int64_t n_out = ctx->saved_data["n_out"].toInt();
     const auto dev = x.device();
@@ -93,13 +94,23 @@ struct HipConvolutionFunction : public torch::autograd::Function<HipConvolutionF
     }
     if (ctx->needs_input_grad(1)) {
       gw = torch::empty_like(w);
-      check_rhip(rhip_conv_backward_weight(x.data_ptr(), n_in, static_cast<int32_t>(cin),
-                                           gy.data_ptr(), n_out, static_cast<int32_t>(cout), K,
-                                           offsets.data_ptr<int64_t>(), n_pairs,
-                                           in_rows.data_ptr<int32_t>(),
-                                           out_rows.data_ptr<int32_t>(), gw.data_ptr(), dt,
-                                           ws.data_ptr(), ws.numel(), st),
-                 "rhip_conv_backward_weight");
+      // narrow bf16 layers: dW from the neighbour table (one dY read per row)
+      const bool rows = dt == RHIP_BF16 && (cin == 16 || cin == 32) && (cout == 16 || cout == 32);
+      if (rows)
+        check_rhip(rhip_conv_backward_weight_rows(
+                       x.data_ptr(), n_in, static_cast<int32_t>(cin), gy.data_ptr(), n_out,
+                       static_cast<int32_t>(cout), K, nbr.data_ptr<int32_t>(),
+                       out_order.numel() > 0 ? out_order.data_ptr<int32_t>() : nullptr,
+                       gw.data_ptr(), dt, ws.data_ptr(), ws.numel(), st),
+                   "rhip_conv_backward_weight_rows");
+      else
+        check_rhip(rhip_conv_backward_weight(x.data_ptr(), n_in, static_cast<int32_t>(cin),
+                                             gy.data_ptr(), n_out, static_cast<int32_t>(cout), K,
+                                             offsets.data_ptr<int64_t>(), n_pairs,
+                                             in_rows.data_ptr<int32_t>(),
+                                             out_rows.data_ptr<int32_t>(), gw.data_ptr(), dt,
+                                             ws.data_ptr(), ws.numel(), st),
+                   "rhip_conv_backward_weight");
     }
     return {gx, gw, {}, {}, {}, {}, {}, {}, {}, {}, {}};
   }

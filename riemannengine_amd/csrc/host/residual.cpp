@@ -104,10 +104,12 @@ struct HipBatchNormFunction : public torch::autograd::Function<HipBatchNormFunct
       gx = torch::empty_like(x);
     if (has_residual && ctx->needs_input_grad(1))
       gres = torch::empty_like(x);
+    // the kernels write every parameter gradient; zeros only for no rows
+    auto param_grad = [&] { return n > 0 ? torch::empty({C}, f32) : torch::zeros({C}, f32); };
     if (present(weight) && ctx->needs_input_grad(2))
-      gw = torch::zeros({C}, f32);
+      gw = param_grad();
     if (present(weight) && ctx->needs_input_grad(3))
-      gb = torch::zeros({C}, f32);
+      gb = param_grad();
     if (n > 0 && (gx.defined() || gres.defined() || gw.defined() || gb.defined())) {
       size_t bytes = 0;
       check_rhip(rhip_bn_workspace_bytes(n, static_cast<int32_t>(C), &bytes),

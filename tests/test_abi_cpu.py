@@ -32,7 +32,7 @@ def test_library_exports_every_declared_symbol():
 
 
 def test_abi_version_and_struct_layout():
-    assert abi.lib().rhip_abi_version() == 9
+    assert abi.lib().rhip_abi_version() == 10
     # void*, int64, void*, int64, 3 x int32, 3 x int32[8] -> 140 bytes, padded to 144
     assert ctypes.sizeof(abi.RhipTable) == 144
 
@@ -42,9 +42,13 @@ def test_workspace_queries():
     assert abi._sizeq(L.rhip_hash_workspace_bytes, 1000, 4) > 1000 * 8
     assert abi._sizeq(L.rhip_kmap_workspace_bytes, 1000, 1000, 27) > 27 * 1000 * 4
     # transposed weights + fp32 accumulator, plus the dW partial tiles
-    small = abi._sizeq(L.rhip_conv_workspace_bytes, 27, 64, 64, abi.BF16, 1000, 1000, 0)
-    assert small >= 27 * 64 * 64 * (2 + 4)
-    assert abi._sizeq(L.rhip_conv_workspace_bytes, 27, 64, 64, abi.BF16, 10**5, 10**5, 10**6) > small
+    base = 27 * 64 * 64 * (2 + 4)
+    assert abi._sizeq(L.rhip_conv_workspace_bytes, 27, 64, 64, abi.BF16, 1000, 1000, 0) >= base
+    assert abi._sizeq(L.rhip_conv_workspace_bytes, 27, 64, 64, abi.BF16, 10**5, 10**5,
+                      10**6) > base
+    # few rows, wide channels: fp32 partial sums of the split offset axis
+    wide = abi._sizeq(L.rhip_conv_workspace_bytes, 27, 256, 256, abi.BF16, 1000, 1000, 0)
+    assert wide >= 27 * 256 * 256 * (2 + 4) + 2 * 1000 * 256 * 4
     assert L.rhip_table_bytes(100) == 256 * 16  # next power of two >= 2n, 16 B slots
 
 

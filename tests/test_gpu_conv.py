@@ -113,6 +113,58 @@ def test_strided_and_transposed(dtype):
     _run_and_check(km.swapped(), 128, 64, dtype, seed=6, tag="up")
 
 
+def _rows_check(km, cin, cout, seed, tag):
+    """dW from the neighbour table vs the oracle on the map's own pairs (bf16
+    operands, so the oracle sees the rounded values) and vs the pair-list
+    kernel."""
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(km.n_in, cin, generator=g).to(torch.bfloat16).to(DEV)
+    gy = torch.randn(km.n_out, cout, generator=g).to(torch.bfloat16).to(DEV)
+    print(f"dW rows {tag} cin={cin} cout={cout} n_in={km.n_in} n_out={km.n_out}", flush=True)
+    rows = abi.conv_backward_weight_rows(x, gy, km, km.K)
+    pairs = abi.conv_backward_weight(x, gy, km, km.K)
+    _, _, rgw = _oracle_conv(km, x.float().cpu().numpy(),
+                             np.zeros((km.K, cin, cout), np.float32), gy.float().cpu().numpy())
+    assert_rel(rows.float().cpu().numpy(), rgw, TOL[torch.bfloat16], f"{tag} rows dW")
+    assert_rel(rows.float().cpu().numpy(), pairs.float().cpu().numpy(), 1e-2,
+               f"{tag} rows vs pairs dW")
+
+
+@pytest.mark.parametrize("cin,cout", [(16, 16), (16, 32), (32, 16), (32, 32)])
+def test_weight_gradient_from_neighbour_table(cin, cout):
+    rng = np.random.default_rng(cin * 3 + cout)
+    c, _, _ = oracle.insert_and_map(random_coords(rng, 9000, 3, 14))
+    _, _, km = gpu_tables_and_map(c, c, oracle.region_offsets(3, 3), same=True)
+    _rows_check(km, cin, cout, seed=cin + cout, tag="3^3")
+
+
+def test_weight_gradient_from_neighbour_table_strided_and_4d():
+    """A 2^3 stride-2 map (n_in != n_out), its swapped (transposed) map, and
+    an 81-offset 4D map (offset groups not dividing K)."""
+    rng = np.random.default_rng(29)
+    c, _, _ = oracle.insert_and_map(random_coords(rng, 20000, 3, 30))
+    tin = abi.hash_build(to_dev(c))
+    tout = abi.hash_build(abi.stride_coords(to_dev(c), [2, 2, 2]))
+    km = abi.kernel_map(tin, tout, to_dev(oracle.region_offsets(3, 2)))
+    _rows_check(km, 32, 32, seed=1, tag="down")
+    _rows_check(km.swapped(), 32, 16, seed=2, tag="up")
+    c4, _, _ = oracle.insert_and_map(random_coords(rng, 6000, 4, 7, batch=1))
+    _, _, km4 = gpu_tables_and_map(c4, c4, oracle.region_offsets(4, 3), same=True)
+    _rows_check(km4, 32, 32, seed=3, tag="3^4")
+
+
+def test_weight_gradient_from_neighbour_table_rejects_other_shapes():
+    rng = np.random.default_rng(2)
+    c, _, _ = oracle.insert_and_map(random_coords(rng, 500, 3, 8))
+    _, _, km = gpu_tables_and_map(c, c, oracle.region_offsets(3, 3), same=True)
+    x = torch.zeros(km.n_in, 64, dtype=torch.bfloat16, device=DEV)
+    gy = torch.zeros(km.n_out, 32, dtype=torch.bfloat16, device=DEV)
+    with pytest.raises(RuntimeError, match="16 or 32"):
+        abi.conv_backward_weight_rows(x, gy, km, km.K)
+    with pytest.raises(RuntimeError, match="16 or 32"):
+        abi.conv_backward_weight_rows(x[:, :32].float().contiguous(), gy.float(), km, km.K)
+
+
 def test_kats_through_the_gpu(golden_dir):
     """The reference KATs (identity and permuted K=1 maps) run through the
     C-ABI kernels with hand-built maps."""
