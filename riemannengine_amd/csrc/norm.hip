@@ -25,7 +25,8 @@ namespace rhip {
 namespace {
 
 constexpr int kNormThreads = 256;
-constexpr int kChunkRows = 1024; // rows per workgroup of a reduction pass
+constexpr int kMaxChunkRows = 1024; // rows per workgroup of a reduction pass, at most
+constexpr int kReduceBlocks = 1024;  // reduction workgroups to aim for
 constexpr int kUnroll = 4;       // rows loaded together by a reduction thread
 constexpr int kApplyRows = 4;    // rows per thread of an elementwise pass
 
@@ -145,6 +146,7 @@ __device__ __forceinline__ void combine_rows(const Lanes &l, double (&a)[V], dou
 template <typename T, int V>
 __global__ __launch_bounds__(kNormThreads) void bn_sums_kernel(const T *__restrict__ x,
                                                                int64_t n, int C, int lpr, int lpt,
+                                                               int64_t chunk,
                                                                double *__restrict__ part) {
   const Lanes l = lanes(lpr, lpt);
   double s[V], q[V];
@@ -152,9 +154,9 @@ __global__ __launch_bounds__(kNormThreads) void bn_sums_kernel(const T *__restri
   for (int e = 0; e < V; ++e)
     s[e] = q[e] = 0.0;
   if (l.active) {
-    const int64_t r1 = min(n, (static_cast<int64_t>(blockIdx.x) + 1) * kChunkRows);
+    const int64_t r1 = min(n, (static_cast<int64_t>(blockIdx.x) + 1) * chunk);
     const T *p = x + l.cc * V;
-    for (int64_t r = static_cast<int64_t>(blockIdx.x) * kChunkRows + l.rlane; r < r1;
+    for (int64_t r = static_cast<int64_t>(blockIdx.x) * chunk + l.rlane; r < r1;
          r += kUnroll * l.rl) {
       // rows past the chunk load the chunk's last row and count as zero: the
       // loads stay unconditional, so all kUnroll are in flight together
@@ -182,8 +184,8 @@ __global__ __launch_bounds__(kNormThreads) void bn_sums_kernel(const T *__restri
 template <typename T, int V>
 __global__ __launch_bounds__(kNormThreads) void bn_grad_sums_kernel(
     const T *__restrict__ dy, const T *__restrict__ y, const T *__restrict__ x, int64_t n, int C,
-    int lpr, int lpt, const float *__restrict__ mean, const float *__restrict__ invstd, int relu,
-    double *__restrict__ part) {
+    int lpr, int lpt, int64_t chunk, const float *__restrict__ mean,
+    const float *__restrict__ invstd, int relu, double *__restrict__ part) {
   const Lanes l = lanes(lpr, lpt);
   double s[V], q[V];
 #pragma unroll
@@ -193,9 +195,9 @@ __global__ __launch_bounds__(kNormThreads) void bn_grad_sums_kernel(
     float mu[V], is[V];
     load_coef<V>(mean + l.cc * V, mu);
     load_coef<V>(invstd + l.cc * V, is);
-    const int64_t r1 = min(n, (static_cast<int64_t>(blockIdx.x) + 1) * kChunkRows);
+    const int64_t r1 = min(n, (static_cast<int64_t>(blockIdx.x) + 1) * chunk);
     const int64_t c0 = l.cc * V;
-    for (int64_t r = static_cast<int64_t>(blockIdx.x) * kChunkRows + l.rlane; r < r1;
+    for (int64_t r = static_cast<int64_t>(blockIdx.x) * chunk + l.rlane; r < r1;
          r += kUnroll * l.rl) {
       float g[kUnroll][V], xv[kUnroll][V], yv[kUnroll][V];
 #pragma unroll
@@ -426,7 +428,13 @@ template <typename F> void with_type(int32_t dtype, F &&f) {
     f(__bf16{});
 }
 
-int64_t chunks_of(int64_t n) { return std::max<int64_t>(1, ceil_div(n, kChunkRows)); }
+// Rows per reduction workgroup: enough workgroups to fill the chip for small
+// row counts (a multiple of 64 rows), at most kMaxChunkRows.
+int64_t chunk_rows(int64_t n) {
+  return std::min<int64_t>(kMaxChunkRows,
+                           std::max<int64_t>(64, ceil_div(ceil_div(n, kReduceBlocks), 64) * 64));
+}
+int64_t chunks_of(int64_t n) { return std::max<int64_t>(1, ceil_div(n, chunk_rows(n))); }
 
 struct NormWs {
   double *part;
@@ -442,7 +450,7 @@ NormWs carve_norm(Carve &cv, int64_t n, int C) {
 
 // Launch shape over [n, C] features: lpr slices per row, lpt of them per
 // workgroup (grid.y over channel tiles), rl = 256 / lpt rows side by side.
-// Reductions take kChunkRows rows per workgroup, elementwise passes
+// Reductions take chunk_rows(n) rows per workgroup, elementwise passes
 // rl * kApplyRows.
 template <typename T, int V, typename Launch>
 void over_rows(int64_t n, int C, bool reduction, Launch &&launch) {
@@ -485,7 +493,7 @@ extern "C" int rhip_bn_stats(const void *x, int64_t n, int32_t C, int32_t dtype,
         constexpr int V = decltype(v)::value;
         over_rows<T, V>(n, C, true, [&](dim3 grid, int lpr, int lpt) {
           hipLaunchKernelGGL((bn_sums_kernel<T, V>), grid, dim3(kNormThreads), 0, stream,
-                             static_cast<const T *>(x), n, C, lpr, lpt, w.part);
+                             static_cast<const T *>(x), n, C, lpr, lpt, chunk_rows(n), w.part);
           RHIP_LAUNCH_CHECK();
         });
       });
@@ -556,8 +564,8 @@ extern "C" int rhip_bn_backward(const void *grad_y, const void *y, const void *x
           over_rows<T, V>(n, C, true, [&](dim3 grid, int lpr, int lpt) {
             hipLaunchKernelGGL((bn_grad_sums_kernel<T, V>), grid, dim3(kNormThreads), 0, stream,
                                static_cast<const T *>(grad_y), static_cast<const T *>(y),
-                               static_cast<const T *>(x), n, C, lpr, lpt, mean, invstd, relu,
-                               w.part);
+                               static_cast<const T *>(x), n, C, lpr, lpt, chunk_rows(n), mean,
+                               invstd, relu, w.part);
             RHIP_LAUNCH_CHECK();
           });
           hipLaunchKernelGGL(bn_final_kernel, dim3(C), dim3(kNormThreads), 0, stream, w.part,
