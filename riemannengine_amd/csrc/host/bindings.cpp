@@ -358,13 +358,19 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   bind_unary<RiemannGlobalMaxPoolingImpl>(nn, "RiemannGlobalMaxPooling")
       .def(py::init([]() { return std::make_shared<RiemannGlobalMaxPoolingImpl>(); }));
 
+  // downsample: an optional projection of the block input (a convolution),
+  // registered as the module's "downsample" (residual.hpp:12-29)
   bind_unary<BasicBlockImpl>(nn, "BasicBlock")
-      .def(py::init([](int inplanes, int planes, int stride, int dilation, double bn_momentum,
+      .def(py::init([](int inplanes, int planes, int stride, int dilation,
+                       std::shared_ptr<RiemannConvolutionImpl> downsample, double bn_momentum,
                        int dimension) {
+             torch::nn::AnyModule ds;
+             if (downsample)
+               ds = torch::nn::AnyModule(RiemannConvolution(downsample));
              return std::make_shared<BasicBlockImpl>(inplanes, planes, stride, dilation,
-                                                     torch::nn::AnyModule(), bn_momentum,
-                                                     dimension);
+                                                     std::move(ds), bn_momentum, dimension);
            }),
            py::arg("inplanes"), py::arg("planes"), py::arg("stride") = 1,
-           py::arg("dilation") = 1, py::arg("bn_momentum") = 0.1, py::arg("dimension") = 3);
+           py::arg("dilation") = 1, py::arg("downsample") = py::none(), py::arg("bn_momentum") = 0.1,
+           py::arg("dimension") = 3);
 }

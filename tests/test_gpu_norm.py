@@ -278,3 +278,42 @@ def test_basic_block_backward_matches_torch_composition():
     assert_rel(_np(feats.grad), xr.grad.numpy(), 1e-4, "block grad x")
     for k, v in p.items():
         assert_rel(_np(v.grad), leaf[k].grad.numpy(), 1e-4, "block grad " + k)
+
+
+def test_basic_block_with_downsample_matches_torch_composition():
+    """BasicBlock(8, 16, stride=2) with a 1x1 stride-2 projection
+    (tests/engine/test_layers.cpp:303-318): output channels and tensor
+    stride as the reference checks, values and gradients against
+    relu(bn2(conv2(relu(bn1(conv1 x)))) + proj x) in float64 torch autograd
+    over the oracle's maps."""
+    rng = np.random.default_rng(43)
+    c, _, _ = oracle.insert_and_map(random_coords(rng, 3000, 3, 14))
+    torch.manual_seed(6)
+    proj = re_.nn.RiemannConvolution(8, 16, kernel_size=1, stride=2)
+    blk = re_.nn.BasicBlock(8, 16, stride=2, downsample=proj)
+    blk.to(DEV)
+    x_np = rng.standard_normal((len(c), 8)).astype(np.float32)
+    feats = torch.from_numpy(x_np).to(DEV).requires_grad_(True)
+    out = blk(re_.SparseTensor(feats, torch.from_numpy(c).to(DEV)))
+    assert out.F.shape[1] == 16 and out.tensor_stride == [2, 2, 2]
+    gy = torch.randn(out.F.shape, generator=torch.Generator().manual_seed(7))
+    (out.F * gy.to(DEV)).sum().backward()
+    p = blk.named_parameters()
+    c2 = out.C.cpu().numpy()
+    np.testing.assert_array_equal(np.unique(c2, axis=0), np.unique(oracle.stride(c, [2, 2, 2]), axis=0))
+    m1 = oracle.kernel_map(c, c2, oracle.region_offsets(3, 3))
+    m2 = oracle.kernel_map(c2, c2, oracle.region_offsets(3, 3) * 2)
+    mp = oracle.kernel_map(c, c2, oracle.region_offsets(3, 1))
+    leaf = {k: v.detach().cpu().double().requires_grad_(True) for k, v in p.items()}
+    xr = torch.from_numpy(x_np).double().requires_grad_(True)
+    bn = lambda v, i: F.batch_norm(v, None, None, leaf[f"norm{i}.normalization.weight"],
+                                   leaf[f"norm{i}.normalization.bias"], True, 0.1, 1e-5)
+    n2 = len(c2)
+    h = torch.relu(bn(_torch_conv(xr, leaf["conv1.base.kernel"], *m1, n2), 1))
+    res = _torch_conv(xr, leaf["downsample.base.kernel"], *mp, n2)
+    ref = torch.relu(bn(_torch_conv(h, leaf["conv2.base.kernel"], *m2, n2), 2) + res)
+    (ref * gy.double()).sum().backward()
+    assert_rel(_np(out.F), ref.detach().numpy(), 1e-4, "block y")
+    assert_rel(_np(feats.grad), xr.grad.numpy(), 1e-4, "block grad x")
+    for k, v in p.items():
+        assert_rel(_np(v.grad), leaf[k].grad.numpy(), 1e-4, "block grad " + k)

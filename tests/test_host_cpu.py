@@ -88,6 +88,17 @@ def test_basic_block_structure():
     assert not blk.training
 
 
+def test_basic_block_registers_downsample():
+    """A projection passed as `downsample` is one of the block's parameters
+    (tests/engine/test_layers.cpp:303-318)."""
+    proj = re_.nn.RiemannConvolution(8, 16, kernel_size=1, stride=2)
+    blk = re_.nn.BasicBlock(8, 16, stride=2, downsample=proj)
+    p = blk.named_parameters()
+    assert "downsample.base.kernel" in p
+    assert p["downsample.base.kernel"].data_ptr() == proj.kernel.data_ptr()
+    assert "downsample.base.kernel" not in re_.nn.BasicBlock(8, 8).named_parameters()
+
+
 def test_batch_norm_state_names_match_torch():
     """RiemannBatchNorm keeps torch BatchNorm1d's parameters and buffers
     under `normalization.` (engine/nn/normalization.hpp:14-23)."""
