@@ -665,7 +665,7 @@ template <int VA, int VB, int KW>
 __global__ __launch_bounds__(kThreads) void conv_dw_rows_kernel(
     const __bf16 *__restrict__ x, const __bf16 *__restrict__ gy,
     const int32_t *__restrict__ nbr, const int32_t *__restrict__ out_order, int64_t n_out,
-    int K, int64_t rows_per_block, float *__restrict__ partial) {
+    int K, int64_t rows_per_block, int row_blocks, int xcd_map, float *__restrict__ partial) {
   constexpr int TM = 16 * VA, TN = 16 * VB, SP = kDwRowsSP;
   constexpr int LDX = TM + 8, LDG = TN + 8; // 16-byte row padding
   __shared__ __align__(16) __bf16 sG[kWaves][SP * LDG];
@@ -676,9 +676,20 @@ __global__ __launch_bounds__(kThreads) void conv_dw_rows_kernel(
   const int wv = threadIdx.x / kWave;
   const int i16 = lane & 15;
   const int g = lane >> 4;
-  const int64_t p0 = blockIdx.x * rows_per_block;
+  // row block and offset group: with xcd_map the grid is 1-D and each XCD
+  // runs every offset group of its row blocks back to back (shared L2)
+  int rb = blockIdx.x, grp = blockIdx.y;
+  if (xcd_map) {
+    const int groups = (K + KW - 1) / KW;
+    const int xcd = static_cast<int>(blockIdx.x % kXcds), m = static_cast<int>(blockIdx.x / kXcds);
+    grp = m % groups;
+    rb = (m / groups) * kXcds + xcd;
+  }
+  if (rb >= row_blocks)
+    return; // padding workgroup (uniform)
+  const int64_t p0 = rb * rows_per_block;
   const int64_t p1 = min(n_out, p0 + rows_per_block);
-  const int k0 = blockIdx.y * KW;
+  const int k0 = grp * KW;
 
   v4f acc[KW][VA][VB];
 #pragma unroll
@@ -828,7 +839,7 @@ __global__ __launch_bounds__(kThreads) void conv_dw_rows_kernel(
     __syncthreads();
   }
   const int kn = min(KW, K - k0);
-  float *slot = partial + (static_cast<int64_t>(blockIdx.x) * K + k0) * (TM * TN);
+  float *slot = partial + (static_cast<int64_t>(rb) * K + k0) * (TM * TN);
   for (int i = threadIdx.x; i < kn * TM * TN; i += kThreads)
     slot[i] = red[i];
 }
@@ -1132,10 +1143,11 @@ static void check_dtype(int32_t dtype) {
 
 // dW from the neighbour table (conv_dw_rows_kernel): bf16 with 16 or 32
 // input and output channels. Measured on MI355X (config-5 stage 1, 808k
-// rows, C32): 3 offsets per wave and 64 row blocks (about 2.2x the
-// pair-list kernel's rate).
+// rows, C32): 3 offsets per wave, 256 row blocks, each XCD running all
+// offset groups of its row blocks back to back (183 us against the
+// pair-list kernel's 397; 225 us with the groups spread over the XCDs).
 constexpr int kDwRowsKW = 3;
-constexpr int kDwRowsBlocks = 64;
+constexpr int kDwRowsBlocks = 256;
 
 static bool dw_rows_supported(int32_t dtype, int cin, int cout) {
   return dtype == RHIP_BF16 && (cin == 16 || cin == 32) && (cout == 16 || cout == 32);
@@ -1146,13 +1158,15 @@ static size_t dw_rows_floats(int K, int cin, int cout) {
   return static_cast<size_t>(kDwRowsBlocks) * K * cin * cout;
 }
 
-template <int VA, int VB>
+template <int VA, int VB, int KW = kDwRowsKW>
 static void launch_dw_rows(const __bf16 *x, const __bf16 *gy, const int32_t *nbr,
                            const int32_t *out_order, int64_t n_out, int K, int64_t rpb,
-                           int blocks, float *partial, hipStream_t s) {
-  dim3 grid(static_cast<unsigned>(blocks), static_cast<unsigned>(ceil_div(K, kDwRowsKW)));
-  hipLaunchKernelGGL((conv_dw_rows_kernel<VA, VB, kDwRowsKW>), grid, dim3(kThreads), 0, s, x, gy,
-                     nbr, out_order, n_out, K, rpb, partial);
+                           int blocks, float *partial, hipStream_t s, bool xcd_map = false) {
+  const int groups = static_cast<int>(ceil_div(K, KW));
+  dim3 grid = xcd_map ? dim3(static_cast<unsigned>(ceil_div(blocks, kXcds) * kXcds * groups))
+                      : dim3(static_cast<unsigned>(blocks), static_cast<unsigned>(groups));
+  hipLaunchKernelGGL((conv_dw_rows_kernel<VA, VB, KW>), grid, dim3(kThreads), 0, s, x, gy, nbr,
+                     out_order, n_out, K, rpb, blocks, xcd_map ? 1 : 0, partial);
 }
 
 // grad_w [K, cin, cout] (bf16, overwritten) from the neighbour table.
@@ -1166,7 +1180,7 @@ static void run_dw_rows(const __bf16 *x, int64_t n_in, int cin, const __bf16 *gy
     blocks = static_cast<int>(ceil_div(n_out, rpb));
     auto go = [&](auto va, auto vb) {
       launch_dw_rows<decltype(va)::value, decltype(vb)::value>(x, gy, nbr, out_order, n_out, K,
-                                                               rpb, blocks, partial, s);
+                                                               rpb, blocks, partial, s, true);
     };
     using I1 = std::integral_constant<int, 1>;
     using I2 = std::integral_constant<int, 2>;
