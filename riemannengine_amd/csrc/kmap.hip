@@ -39,6 +39,7 @@
 //            a sort of the input rows by them -> in_order / in_pos, and
 //            nbr_t[k][in_pos[i]] = output row paired with i under k.
 #include <algorithm>
+#include <cstring>
 #include <vector>
 
 #include "rhip_internal.hpp"
@@ -374,6 +375,28 @@ __global__ __launch_bounds__(kMapBlock) void kmap_transpose_kernel(
 // Workspace: the per-block counts, their scans and the per-offset totals
 // persist from phase 1 to phase 2; each phase's scratch reuses the same
 // region after them.
+// Host-to-device upload of a few int32 through kernel arguments: launched
+// asynchronously like any kernel, no staging copy. 960 values per launch
+// keep the arguments under 4 KB.
+constexpr int kUploadInts = 960;
+struct UploadArg {
+  int32_t v[kUploadInts];
+};
+static __global__ void upload_i32_kernel(UploadArg a, int32_t *__restrict__ dst, int n) {
+  for (int i = threadIdx.x; i < n; i += blockDim.x)
+    dst[i] = a.v[i];
+}
+
+static void upload_i32(int32_t *dst, const int32_t *src, size_t n, hipStream_t stream) {
+  for (size_t o = 0; o < n; o += kUploadInts) {
+    UploadArg a{};
+    const int m = static_cast<int>(std::min<size_t>(kUploadInts, n - o));
+    std::memcpy(a.v, src + o, sizeof(int32_t) * m);
+    hipLaunchKernelGGL(upload_i32_kernel, dim3(1), dim3(256), 0, stream, a, dst + o, m);
+    RHIP_LAUNCH_CHECK();
+  }
+}
+
 struct KmapWs {
   int32_t *block_counts;
   int64_t *block_base;
@@ -532,12 +555,11 @@ extern "C" int rhip_kmap_count(const rhip_table *in_table, const int32_t *out_co
       RHIP_LAUNCH_CHECK();
     } else {
       RHIP_CHECK_ARG(out_coords && nbr && out_order, "out_coords, nbr and out_order are required");
-      // pageable sources: both stay alive until the synchronize below
-      RHIP_HIP(hipMemcpyAsync(w.offsets, offsets_host, sizeof(int32_t) * K * D,
-                              hipMemcpyHostToDevice, stream));
+      // small host arrays go in kernel arguments (a copy from pageable
+      // memory would wait for the device)
+      upload_i32(w.offsets, offsets_host, static_cast<size_t>(K) * D, stream);
       if (sym)
-        RHIP_HIP(hipMemcpyAsync(w.plan, plan.lists.data(), sizeof(int32_t) * plan.lists.size(),
-                                hipMemcpyHostToDevice, stream));
+        upload_i32(w.plan, plan.lists.data(), plan.lists.size(), stream);
       const TableView tv = make_view(*in_table);
       // all probes of a row in one thread for packed keys; one thread per
       // (row, offset) for row-reference tables
