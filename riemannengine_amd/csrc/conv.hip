@@ -940,7 +940,7 @@ static void launch_os(const T *x, int cred, const T *wt, int ncols,
 // stage per barrier. bf16 (config-5 stages): 8 waves per SIMD and one stage
 // per barrier at 64 columns; 128-column tiles (4 waves per SIMD, 2 stages
 // per barrier) for 128 and 256 channels; 4 stages per barrier for 32-channel
-// chunks.
+// chunks (6 waves per SIMD at 64 columns, where 8 do not fit the registers).
 template <typename T> constexpr bool kIsF32 = std::is_same<T, float>::value;
 
 template <typename T> static int os_nt(int ncols) {
@@ -953,7 +953,7 @@ template <typename T, int NT, int CSUB>
 static void launch_shape(const T *x, int cred, const T *wt, int ncols, const float *bias,
                          const int32_t *nbr, int64_t n_rows, int K, const int32_t *order, T *y,
                          int splits, float *partial, hipStream_t s) {
-  constexpr int W = kIsF32<T> ? 6 : (NT >= 128 ? 4 : 8);
+  constexpr int W = kIsF32<T> ? 6 : (NT >= 128 ? 4 : (CSUB == 1 && NT >= 64 ? 6 : 8));
   constexpr int G = kIsF32<T> ? 1 : (CSUB == 1 ? 4 : (NT >= 128 ? 2 : 1));
   launch_os<T, NT, 1, CSUB, W, G>(x, cred, wt, ncols, bias, nbr, n_rows, K, order, y, splits,
                                   partial, s);
