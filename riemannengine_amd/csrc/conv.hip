@@ -954,7 +954,7 @@ static void launch_shape(const T *x, int cred, const T *wt, int ncols, const flo
                          const int32_t *nbr, int64_t n_rows, int K, const int32_t *order, T *y,
                          int splits, float *partial, hipStream_t s) {
   constexpr int W = kIsF32<T> ? 6 : (NT >= 128 ? 4 : (CSUB == 1 && NT >= 64 ? 6 : 8));
-  constexpr int G = kIsF32<T> ? 1 : (CSUB == 1 ? 4 : (NT >= 128 ? 2 : 1));
+  constexpr int G = kIsF32<T> ? 1 : (NT >= 128 ? 2 : (CSUB == 1 ? 4 : 1));
   launch_os<T, NT, 1, CSUB, W, G>(x, cred, wt, ncols, bias, nbr, n_rows, K, order, y, splits,
                                   partial, s);
 }
