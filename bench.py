@@ -265,7 +265,7 @@ def run_other_config(args):
         x, w, gy = rnd(n_in, cin), kaiming(K, cin, cout), rnd(n_in, cout)
         passes = [("forward", lambda: abi.conv_forward(x, w, km)),
                   ("backward_input", lambda: abi.conv_backward_input(gy, w, km)),
-                  ("backward_weight", lambda: abi.conv_backward_weight(x, gy, km, K))]
+                  ("backward_weight", lambda: abi.conv_weight_grad(x, gy, km, K))]
         for F, B in conv_traffic(n_in, n_in, km.n_pairs, K, cin, cout, s).values():
             flop, byts = flop + F, byts + B
         extra = {"n_voxels": n_in, "pairs": km.n_pairs, "offsets": K, "c_in": cin, "c_out": cout}
@@ -288,9 +288,9 @@ def run_other_config(args):
         passes = [("down_forward", lambda: abi.conv_forward(x, wd, down)),
                   ("up_forward", lambda: abi.conv_forward(y, wu, up)),
                   ("up_backward_input", lambda: abi.conv_backward_input(gz, wu, up)),
-                  ("up_backward_weight", lambda: abi.conv_backward_weight(y, gz, up, 8)),
+                  ("up_backward_weight", lambda: abi.conv_weight_grad(y, gz, up, 8)),
                   ("down_backward_input", lambda: abi.conv_backward_input(gy, wd, down)),
-                  ("down_backward_weight", lambda: abi.conv_backward_weight(x, gy, down, 8))]
+                  ("down_backward_weight", lambda: abi.conv_weight_grad(x, gy, down, 8))]
         for (ni, no, ci, co) in ((n_f, n_c, 64, 128), (n_c, n_f, 128, 64)):
             for F, B in conv_traffic(ni, no, P, 8, ci, co, s).values():
                 flop, byts = flop + F, byts + B
@@ -572,7 +572,7 @@ def main():
         abi.conv_backward_input(gy, w, km)
         if ev is not None:
             ev[2].record()
-        abi.conv_backward_weight(x, gy, km, K)
+        abi.conv_weight_grad(x, gy, km, K)
         if ev is not None:
             ev[3].record()
 
@@ -606,7 +606,10 @@ def main():
     roof["traffic"] = measured_traffic(args.dtype, dom)
     roof["kernel"] = {"forward": "conv_os_kernel (forward)",
                       "backward_input": "conv_os_kernel (dX)",
-                      "backward_weight": "conv_dw_kernel + conv_dw_reduce_kernel (dW pass)"}[dom]
+                      "backward_weight": (
+                          "conv_dw_pos_kernel + conv_dw_rows_reduce_kernel (dW pass)"
+                          if args.dtype == "f32" else
+                          "conv_dw_kernel + conv_dw_reduce_kernel (dW pass)")}[dom]
     roof["kernel_ms"] = round(per[dom], 4)
     roof["algorithmic"] = {"flop": F, "bytes": B}
 

@@ -260,10 +260,15 @@ int rhip_conv_backward_weight(const void *x, int64_t n_in, int32_t cin,
  * The same weight gradient from the dense neighbour table instead of the
  * pair list: grad_w[k] = sum over output positions j with
  * nbr[k*n_out+j] >= 0 of x[nbr[k*n_out+j]]^T grad_y[out_order[j]]
- * (out_order NULL = identity), fp32 accumulation, deterministic. For bf16
- * layers with 16 or 32 input and output channels, where each dY row is read
- * once per group of offsets rather than once per pair; other shapes return
- * RHIP_ERR_UNSUPPORTED. Workspace as for rhip_conv_workspace_bytes.
+ * (out_order NULL = identity), fp32 accumulation, deterministic. Each dY
+ * row is read once per group of offsets rather than once per pair, and the
+ * X rows that neighbouring positions share are read once per position
+ * range. Supported: bf16 with 16 or 32 input and output channels, and fp32
+ * with at least 20 offsets, input channels a multiple of 16 and output
+ * channels a multiple of 64 (each of x, grad_y and the table under 2 GiB);
+ * other shapes return
+ * RHIP_ERR_UNSUPPORTED, for which rhip_conv_backward_weight is the
+ * fallback. Workspace as for rhip_conv_workspace_bytes.
  * Replaces the dW half of MmBackward (engine/nn/conv.cpp:62), like
  * rhip_conv_backward_weight.
  */

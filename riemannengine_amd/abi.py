@@ -408,9 +408,36 @@ def conv_backward_weight(x: torch.Tensor, grad_y: torch.Tensor, kmap: KernelMap,
     return gw if out_dtype is None else gw.to(out_dtype)
 
 
+RHIP_ERR_UNSUPPORTED = 3
+
+
+def conv_weight_grad(x: torch.Tensor, grad_y: torch.Tensor, kmap: KernelMap,
+                     K: int) -> torch.Tensor:
+    """dW as the convolution layer computes it: from the neighbour table where
+    the library has a kernel for the shape, else from the pair list."""
+    _require_cuda(x, "x")
+    dt = _dtype_code(x.dtype)
+    x, grad_y = x.contiguous(), grad_y.to(x.dtype).contiguous()
+    cin, cout = x.shape[1], grad_y.shape[1]
+    gw = torch.empty((K, cin, cout), dtype=x.dtype, device=x.device)
+    ws = _conv_ws(K, cin, cout, dt, x.device, kmap)
+    st = lib().rhip_conv_backward_weight_rows(_ptr(x), kmap.n_in, cin, _ptr(grad_y), kmap.n_out,
+                                              cout, K, _ptr(kmap.nbr), _ptr(kmap.out_order),
+                                              _ptr(gw), dt, _ptr(ws), ws.numel(),
+                                              _stream(x.device))
+    if st == RHIP_ERR_UNSUPPORTED:
+        st = lib().rhip_conv_backward_weight(_ptr(x), kmap.n_in, cin, _ptr(grad_y), kmap.n_out,
+                                             cout, K, _ptr(kmap.offsets), kmap.n_pairs,
+                                             _ptr(kmap.in_rows), _ptr(kmap.out_rows), _ptr(gw),
+                                             dt, _ptr(ws), ws.numel(), _stream(x.device))
+    _check(st, "rhip_conv_backward_weight(_rows)")
+    return gw
+
+
 def conv_backward_weight_rows(x: torch.Tensor, grad_y: torch.Tensor, kmap: KernelMap,
                               K: int) -> torch.Tensor:
-    """dW from the kernel map's neighbour table (bf16, 16 or 32 channels)."""
+    """dW from the kernel map's neighbour table (bf16 with 16 or 32 channels,
+    fp32 with K >= 20, cin % 16 == 0 and cout % 64 == 0; other shapes raise)."""
     _require_cuda(x, "x")
     dt = _dtype_code(x.dtype)
     x, grad_y = x.contiguous(), grad_y.to(x.dtype).contiguous()

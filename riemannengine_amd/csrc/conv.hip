@@ -34,6 +34,8 @@ namespace rhip {
 
 typedef float v4f __attribute__((ext_vector_type(4)));
 typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+typedef uint32_t v2u __attribute__((ext_vector_type(2)));
+typedef uint32_t v4u __attribute__((ext_vector_type(4)));
 
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / kWave;
@@ -874,6 +876,247 @@ __global__ __launch_bounds__(1024) void conv_dw_rows_reduce_kernel(
     dw[4 * i4 + e] = from_f32<OutT>(v[e]);
 }
 
+// ---------------------------------------------------- fp32 dW by positions
+//
+// fp32 dW from the neighbour table, position-stationary: a workgroup owns a
+// range of processing positions, a 16-channel input slice ci0 and 16*VB
+// output channels co0, and up to 4*KPW offsets (one offset group); wave w
+// keeps the 16 x 16*VB tiles of offsets k0 + w + 4j (j < KPW) in registers
+// for the whole range. A step covers 4 consecutive positions (the reduction
+// axis of v_mfma_f32_16x16x4f32):
+//  * lane (i16, g) reads dY[out_order[p0 + 4s + g]][co0 + VB*i16 .. +VB-1]
+//    (one vector load; channel co0 + VB*n + eb belongs to MFMA block eb,
+//    column n) and, per offset, X[nbr[k][p0 + 4s + g]][ci0 + i16];
+//  * a step whose four positions have no neighbour under k skips that
+//    offset's MFMAs (wave-uniform); in the mask-grouped processing order
+//    nearly every step is full or empty;
+//  * absent neighbours and positions past the range are buffer loads with
+//    an offset past the buffer's size, which the hardware returns as zero
+//    without a memory access, so no load is predicated.
+// Indices are loaded two steps ahead, rows one step ahead. Every X row a
+// range touches is read from memory about once and then hits the caches
+// (neighbouring positions share rows under different offsets); the pair
+// list kernel reads one X row and one dY row per pair.
+// Each wave writes its offsets' tiles to the range's partial slot
+// [range][k][cin][cout]; conv_dw_rows_reduce_kernel sums the slots.
+constexpr uint32_t kBufOob = 0x80000000u; // past every buffer the kernel makes
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void *p, int64_t bytes) {
+  // raw buffer (stride 0): loads at byte offsets >= bytes return zero
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), 0, static_cast<int>(bytes),
+                                           0x00020000);
+}
+
+template <int VB> struct DyVec;
+template <> struct DyVec<1> {
+  using T = float;
+  __device__ static __forceinline__ T load(__amdgpu_buffer_rsrc_t r, uint32_t o) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, o, 0, 0));
+  }
+  __device__ static __forceinline__ float at(T v, int) { return v; }
+};
+template <> struct DyVec<2> {
+  using T = v2u;
+  __device__ static __forceinline__ T load(__amdgpu_buffer_rsrc_t r, uint32_t o) {
+    return __builtin_amdgcn_raw_buffer_load_b64(r, o, 0, 0);
+  }
+  __device__ static __forceinline__ float at(T v, int e) {
+    const uint32_t t = v[e]; // bit_cast of the subscript itself reads element 0
+    return __builtin_bit_cast(float, t);
+  }
+};
+template <> struct DyVec<4> {
+  using T = v4u;
+  __device__ static __forceinline__ T load(__amdgpu_buffer_rsrc_t r, uint32_t o) {
+    return __builtin_amdgcn_raw_buffer_load_b128(r, o, 0, 0);
+  }
+  __device__ static __forceinline__ float at(T v, int e) {
+    const uint32_t t = v[e]; // bit_cast of the subscript itself reads element 0
+    return __builtin_bit_cast(float, t);
+  }
+};
+
+// A value the optimiser cannot see through: keeps `load | mask` a bitwise
+// OR instead of a select that would become a branch around the load.
+__device__ __forceinline__ int32_t opaque(int32_t v) {
+  asm volatile("" : "+v"(v));
+  return v;
+}
+
+template <int VB, int KPW, int NSLOT, int WAVES>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(WAVES))) void
+conv_dw_pos_kernel(const float *__restrict__ x, int64_t n_in, int cin,
+                   const float *__restrict__ gy, int cout, const int32_t *__restrict__ nbr,
+                   const int32_t *__restrict__ out_order, int64_t n_out, int K, int ranges,
+                   int ci_tiles, int co_tiles, float *__restrict__ partial) {
+  using DV = DyVec<VB>;
+  constexpr int GK = kWaves * KPW; // offsets per group
+  const int groups = (K + GK - 1) / GK;
+  const int units = ci_tiles * co_tiles * groups;
+  // XCD x runs ranges [x*R8, (x+1)*R8) with every unit (slice, group) of a
+  // range back to back; ranges is a multiple of 8
+  const int r8 = ranges / kXcds;
+  const int xcd = static_cast<int>(blockIdx.x % kXcds), m = static_cast<int>(blockIdx.x / kXcds);
+  const int rg = xcd * r8 + m / units;
+  int u = m % units;
+  const int grp = u % groups;
+  u /= groups;
+  const int ci0 = (u % ci_tiles) * 16, co0 = (u / ci_tiles) * (16 * VB);
+
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const int i16 = lane & 15;
+  const int g = lane >> 4;
+  // segments of 64 positions (16 steps) are dealt to the ranges in turn
+  // (range rg takes segments rg, rg + ranges, ...), which spreads the dense
+  // and the sparse neighbour masks of the processing order evenly; an even
+  // count per range: segments past the end load nothing and multiply nothing
+  const int64_t total = (n_out + 63) / 64;
+  const int segs = static_cast<int>((total + 2LL * ranges - 1) / (2LL * ranges)) * 2;
+  int kk[KPW], kval[KPW];
+#pragma unroll
+  for (int j = 0; j < KPW; ++j) {
+    kk[j] = grp * GK + wv + kWaves * j;
+    kval[j] = opaque(kk[j] < K ? -1 : 0);
+  }
+
+  const __amdgpu_buffer_rsrc_t rx = buf_rsrc(x, n_in * cin * 4);
+  const __amdgpu_buffer_rsrc_t ry = buf_rsrc(gy, n_out * cout * 4);
+  const __amdgpu_buffer_rsrc_t rn = buf_rsrc(nbr, static_cast<int64_t>(K) * n_out * 4);
+  const __amdgpu_buffer_rsrc_t ro = buf_rsrc(out_order, out_order ? n_out * 4 : 0);
+  // offsets are chosen with opaque all-ones / zero masks rather than
+  // selects, so that no load ends up behind a divergent branch
+  auto pick = [](uint32_t off, int32_t keep) {
+    return (off & static_cast<uint32_t>(keep)) | (kBufOob & ~static_cast<uint32_t>(keep));
+  };
+
+  // a segment's indices, lane l holding position 64*sg + l: the neighbour
+  // row under each offset (-1 = none) and the dY row (-1 past the range)
+  struct Seg {
+    int32_t id[KPW];
+    int32_t orow;
+  };
+  struct Dat {
+    float a[KPW];
+    typename DV::T d;
+  };
+  auto load_seg = [&](int sg, Seg &S) {
+    const int64_t p = 64 * (rg + static_cast<int64_t>(sg) * ranges) + lane;
+    const int32_t in = opaque(static_cast<int32_t>((p - n_out) >> 63)); // -1 for a position
+#pragma unroll
+    for (int j = 0; j < KPW; ++j) {
+      const int32_t keep = in & kval[j];
+      S.id[j] = static_cast<int32_t>(__builtin_amdgcn_raw_buffer_load_b32(
+                    rn, pick(static_cast<uint32_t>((kk[j] * n_out + p) * 4), keep), 0, 0)) |
+                ~keep;
+    }
+    if (out_order)
+      S.orow = static_cast<int32_t>(__builtin_amdgcn_raw_buffer_load_b32(
+                   ro, pick(static_cast<uint32_t>(p * 4), in), 0, 0)) |
+               ~in;
+    else
+      S.orow = static_cast<int32_t>(p) | ~in;
+  };
+  // Once a segment's indices have arrived: the live masks (bit l: position
+  // l has a neighbour under offset j), then the indices become byte offsets
+  // of the rows' first channel (out of range for an absent row).
+  auto prep = [&](Seg &S, uint64_t (&live)[KPW]) {
+#pragma unroll
+    for (int j = 0; j < KPW; ++j) {
+      const int32_t r = S.id[j];
+      live[j] = __ballot(r >= 0);
+      S.id[j] = static_cast<int32_t>(pick(static_cast<uint32_t>((r * cin + ci0) * 4), opaque(~(r >> 31))));
+    }
+    const int32_t r = S.orow;
+    S.orow = static_cast<int32_t>(pick(static_cast<uint32_t>((r * cout + co0) * 4), opaque(~(r >> 31))));
+  };
+  // rows of step s of a segment: lane (i16, g) takes position 4s + g's
+  // offsets from lane 4s + g (ds_bpermute); an absent row's offset stays
+  // out of range after the lane's channel is added
+  auto load_dat = [&](const Seg &S, int s, Dat &D) {
+    const int src = (4 * s + g) * 4;
+#pragma unroll
+    for (int j = 0; j < KPW; ++j) {
+      const uint32_t o = static_cast<uint32_t>(__builtin_amdgcn_ds_bpermute(src, S.id[j])) + 4 * i16;
+      D.a[j] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rx, o, 0, 0));
+    }
+    const uint32_t o = static_cast<uint32_t>(__builtin_amdgcn_ds_bpermute(src, S.orow)) + 4 * VB * i16;
+    D.d = DV::load(ry, o);
+  };
+
+  v4f acc[KPW][VB];
+#pragma unroll
+  for (int j = 0; j < KPW; ++j)
+#pragma unroll
+    for (int eb = 0; eb < VB; ++eb)
+      acc[j][eb] = v4f{0.f, 0.f, 0.f, 0.f};
+  auto compute = [&](const Dat &D, const uint64_t (&live)[KPW], int s) {
+#pragma unroll
+    for (int j = 0; j < KPW; ++j)
+      if ((live[j] >> (4 * s)) & 0xfu) { // wave-uniform
+#pragma unroll
+        for (int eb = 0; eb < VB; ++eb)
+          acc[j][eb] = __builtin_amdgcn_mfma_f32_16x16x4f32(D.a[j], DV::at(D.d, eb), acc[j][eb], 0,
+                                                             0, 0);
+      }
+  };
+
+  // Two segment slots used in alternation and NSLOT row slots (NSLOT
+  // divides 16, so step s of every segment uses slot s % NSLOT): no
+  // in-flight load is ever copied. Indices are loaded one segment ahead,
+  // rows NSLOT - 1 steps ahead.
+  static_assert(16 % NSLOT == 0, "row slots must divide a segment");
+  Seg SA, SB;
+  uint64_t LA[KPW], LB[KPW];
+  Dat D[NSLOT];
+  auto run_seg = [&](Seg &S, const uint64_t (&LS)[KPW], Seg &N, uint64_t (&LN)[KPW],
+                     int next_load) {
+#pragma unroll
+    for (int s = 0; s < 16; ++s) {
+      const int ahead = s + NSLOT - 1;
+      if (ahead < 16) {
+        load_dat(S, ahead, D[ahead % NSLOT]);
+      } else {
+        if (ahead == 16)
+          prep(N, LN);
+        load_dat(N, ahead - 16, D[ahead % NSLOT]);
+      }
+      compute(D[s % NSLOT], LS, s);
+    }
+    load_seg(next_load, S);
+  };
+  load_seg(0, SA);
+  load_seg(1, SB);
+  prep(SA, LA);
+#pragma unroll
+  for (int s = 0; s + 1 < NSLOT; ++s)
+    load_dat(SA, s, D[s]);
+  for (int sg = 0; sg < segs; sg += 2) {
+    run_seg(SA, LA, SB, LB, sg + 2);
+    run_seg(SB, LB, SA, LA, sg + 3);
+  }
+
+  // lane holds D[4g+e][i16] of block eb: dW[k][ci0 + 4g + e][co0 + VB*i16 + eb]
+#pragma unroll
+  for (int j = 0; j < KPW; ++j) {
+    if (kk[j] >= K)
+      continue;
+    float *dst = partial + ((static_cast<int64_t>(rg) * K + kk[j]) * cin + ci0 + 4 * g) * cout +
+                 co0 + VB * i16;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      if constexpr (VB == 4) {
+        *reinterpret_cast<v4f *>(dst + static_cast<int64_t>(e) * cout) =
+            v4f{acc[j][0][e], acc[j][1][e], acc[j][2][e], acc[j][3][e]};
+      } else {
+#pragma unroll
+        for (int eb = 0; eb < VB; ++eb)
+          dst[static_cast<int64_t>(e) * cout + eb] = acc[j][eb][e];
+      }
+    }
+  }
+}
+
 // Any-shape fallback: one lane per dW element, looping over its pairs.
 template <typename T>
 __global__ __launch_bounds__(kThreads) void conv_dw_generic_kernel(
@@ -1149,8 +1392,65 @@ static void check_dtype(int32_t dtype) {
 constexpr int kDwRowsKW = 3;
 constexpr int kDwRowsBlocks = 256;
 
-static bool dw_rows_supported(int32_t dtype, int cin, int cout) {
-  return dtype == RHIP_BF16 && (cin == 16 || cin == 32) && (cout == 16 || cout == 32);
+// fp32 dW from the neighbour table (conv_dw_pos_kernel): 16-channel input
+// slices, 64 output channels per tile, 7 offsets per wave (all 27 of a 3^3
+// stencil in one workgroup), rows loaded 3 steps ahead, 2 waves per SIMD.
+// Measured on MI355X (config 2, 410k rows, C64, 128 ranges): 419 us
+// against the pair-list kernel's 578; contiguous ranges instead of dealt
+// segments 481 us, 4 offsets per wave 434-444 us. Stencils of fewer than 20
+// offsets leave most of a wave's offset slots empty and stay on the pair
+// list (config 3's 2^3 transposed map, C128->64: 118 us against 71).
+constexpr int kDwPosKPW = 7;
+constexpr int kDwPosMinK = 20;
+constexpr int kDwPosSlots = 4;
+constexpr int kDwPosWaves = 2;
+constexpr int64_t kBufMaxBytes = (int64_t(1) << 31) - 256; // buffer offsets stay below kBufOob
+
+static bool dw_pos_supported(int32_t dtype, int cin, int cout, int K, int64_t n_in,
+                             int64_t n_out) {
+  return dtype == RHIP_F32 && K >= kDwPosMinK && cin % 16 == 0 && cout % 64 == 0 &&
+         n_in * cin * 4 <= kBufMaxBytes && n_out * cout * 4 <= kBufMaxBytes &&
+         static_cast<int64_t>(K) * n_out * 4 <= kBufMaxBytes;
+}
+
+static bool dw_rows_supported(int32_t dtype, int cin, int cout, int K, int64_t n_in,
+                              int64_t n_out) {
+  return (dtype == RHIP_BF16 && (cin == 16 || cin == 32) && (cout == 16 || cout == 32)) ||
+         dw_pos_supported(dtype, cin, cout, K, n_in, n_out);
+}
+
+// Ranges of the fp32 kernel: a multiple of 8 (one share per XCD), about 512
+// workgroups (two per CU: the whole grid resident at once), at most
+// kDwRowsBlocks (the partial slots of the workspace), at least 4 segments
+// of 64 positions each.
+static int dw_pos_ranges(int K, int cin, int cout, int64_t n_out) {
+  const int groups = static_cast<int>(ceil_div(K, kWaves * kDwPosKPW));
+  const int units = (cin / 16) * (cout / 64) * groups;
+  int64_t r = std::max<int64_t>(kXcds, (512 / units) / kXcds * kXcds);
+  const int64_t segs = ceil_div(std::max<int64_t>(n_out, 1), 64);
+  r = std::min<int64_t>(r, std::max<int64_t>(kXcds, segs / 4 / kXcds * kXcds));
+  return static_cast<int>(std::min<int64_t>(r, kDwRowsBlocks));
+}
+
+// grad_w [K, cin, cout] (fp32, overwritten) from the neighbour table.
+static void run_dw_pos(const float *x, int64_t n_in, int cin, const float *gy, int64_t n_out,
+                       int cout, int K, const int32_t *nbr, const int32_t *out_order,
+                       float *partial, float *dw, hipStream_t s) {
+  const int ranges = dw_pos_ranges(K, cin, cout, n_out);
+  const int groups = static_cast<int>(ceil_div(K, kWaves * kDwPosKPW));
+  const int ct = cin / 16, ot = cout / 64;
+  if (n_in > 0 && n_out > 0) {
+    hipLaunchKernelGGL((conv_dw_pos_kernel<4, kDwPosKPW, kDwPosSlots, kDwPosWaves>),
+                       dim3(static_cast<unsigned>(ranges * ct * ot * groups)), dim3(kThreads), 0, s,
+                       x, n_in, cin, gy, cout, nbr, out_order, n_out, K, ranges, ct, ot, partial);
+    RHIP_LAUNCH_CHECK();
+  }
+  const int64_t ne = static_cast<int64_t>(K) * cin * cout;
+  // without rows every slot sum is empty: zeros
+  hipLaunchKernelGGL((conv_dw_rows_reduce_kernel<float>), dim3(static_cast<unsigned>(
+                         ceil_div(ne / 4, kWave))), dim3(1024), 0, s, partial,
+                     n_in > 0 && n_out > 0 ? ranges : 0, ne, dw);
+  RHIP_LAUNCH_CHECK();
 }
 
 // Partial floats of the row kernel: one slot per row block and offset.
@@ -1357,10 +1657,12 @@ extern "C" int rhip_conv_backward_weight_rows(
     check_dtype(dtype);
     RHIP_CHECK_ARG(K >= 1 && cin >= 1 && cout >= 1, "sizes must be positive");
     RHIP_CHECK_ARG(n_in >= 0 && n_out >= 0, "bad sizes");
-    if (!dw_rows_supported(dtype, cin, cout))
+    if (!dw_rows_supported(dtype, cin, cout, K, n_in, n_out))
       throw Error(RHIP_ERR_UNSUPPORTED,
                   "rhip_conv_backward_weight_rows: bf16 with 16 or 32 input and output "
-                  "channels only (use rhip_conv_backward_weight)");
+                  "channels, or fp32 with at least 20 offsets, input channels a multiple "
+                  "of 16 and output channels a multiple of 64 (use "
+                  "rhip_conv_backward_weight)");
     RHIP_CHECK_ARG(grad_w != nullptr, "grad_w is null");
     RHIP_CHECK_ARG(n_in == 0 || n_out == 0 || (x && grad_y && nbr),
                    "x, grad_y and nbr are required");
@@ -1368,7 +1670,12 @@ extern "C" int rhip_conv_backward_weight_rows(
     RHIP_CHECK_ARG(aligned16(x) && aligned16(grad_y), "x and grad_y must be 16-byte aligned");
     Carve cv(workspace, workspace_bytes);
     const ConvWs w = carve_conv(cv, K, cin, cout, dtype, n_in, n_out, DwPlan{});
-    run_dw_rows(static_cast<const __bf16 *>(x), n_in, cin, static_cast<const __bf16 *>(grad_y),
-                n_out, cout, K, nbr, out_order, w.partial, static_cast<__bf16 *>(grad_w), stream);
+    if (dtype == RHIP_F32)
+      run_dw_pos(static_cast<const float *>(x), n_in, cin, static_cast<const float *>(grad_y),
+                 n_out, cout, K, nbr, out_order, w.partial, static_cast<float *>(grad_w), stream);
+    else
+      run_dw_rows(static_cast<const __bf16 *>(x), n_in, cin,
+                  static_cast<const __bf16 *>(grad_y), n_out, cout, K, nbr, out_order, w.partial,
+                  static_cast<__bf16 *>(grad_w), stream);
   });
 }

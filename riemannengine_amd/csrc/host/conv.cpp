@@ -94,23 +94,21 @@ struct HipConvolutionFunction : public torch::autograd::Function<HipConvolutionF
     }
     if (ctx->needs_input_grad(1)) {
       gw = torch::empty_like(w);
-      // narrow bf16 layers: dW from the neighbour table (one dY read per row)
-      const bool rows = dt == RHIP_BF16 && (cin == 16 || cin == 32) && (cout == 16 || cout == 32);
-      if (rows)
-        check_rhip(rhip_conv_backward_weight_rows(
-                       x.data_ptr(), n_in, static_cast<int32_t>(cin), gy.data_ptr(), n_out,
-                       static_cast<int32_t>(cout), K, nbr.data_ptr<int32_t>(),
-                       out_order.numel() > 0 ? out_order.data_ptr<int32_t>() : nullptr,
-                       gw.data_ptr(), dt, ws.data_ptr(), ws.numel(), st),
-                   "rhip_conv_backward_weight_rows");
-      else
-        check_rhip(rhip_conv_backward_weight(x.data_ptr(), n_in, static_cast<int32_t>(cin),
-                                             gy.data_ptr(), n_out, static_cast<int32_t>(cout), K,
-                                             offsets.data_ptr<int64_t>(), n_pairs,
-                                             in_rows.data_ptr<int32_t>(),
-                                             out_rows.data_ptr<int32_t>(), gw.data_ptr(), dt,
-                                             ws.data_ptr(), ws.numel(), st),
-                   "rhip_conv_backward_weight");
+      // dW from the neighbour table where the library has a kernel for the
+      // shape (fp32 C%16 -> C%64 with K >= 20, narrow bf16), else from the
+      // pair list
+      int rc = rhip_conv_backward_weight_rows(
+          x.data_ptr(), n_in, static_cast<int32_t>(cin), gy.data_ptr(), n_out,
+          static_cast<int32_t>(cout), K, nbr.data_ptr<int32_t>(),
+          out_order.numel() > 0 ? out_order.data_ptr<int32_t>() : nullptr, gw.data_ptr(), dt,
+          ws.data_ptr(), ws.numel(), st);
+      if (rc == RHIP_ERR_UNSUPPORTED)
+        rc = rhip_conv_backward_weight(x.data_ptr(), n_in, static_cast<int32_t>(cin),
+                                       gy.data_ptr(), n_out, static_cast<int32_t>(cout), K,
+                                       offsets.data_ptr<int64_t>(), n_pairs,
+                                       in_rows.data_ptr<int32_t>(), out_rows.data_ptr<int32_t>(),
+                                       gw.data_ptr(), dt, ws.data_ptr(), ws.numel(), st);
+      check_rhip(rc, "rhip_conv_backward_weight(_rows)");
     }
     return {gx, gw, {}, {}, {}, {}, {}, {}, {}, {}, {}};
   }

@@ -113,21 +113,22 @@ def test_strided_and_transposed(dtype):
     _run_and_check(km.swapped(), 128, 64, dtype, seed=6, tag="up")
 
 
-def _rows_check(km, cin, cout, seed, tag):
-    """dW from the neighbour table vs the oracle on the map's own pairs (bf16
-    operands, so the oracle sees the rounded values) and vs the pair-list
-    kernel."""
+def _rows_check(km, cin, cout, seed, tag, dtype=torch.bfloat16):
+    """dW from the neighbour table vs the oracle on the map's own pairs (the
+    oracle sees the operands rounded to dtype) and vs the pair-list kernel."""
     g = torch.Generator().manual_seed(seed)
-    x = torch.randn(km.n_in, cin, generator=g).to(torch.bfloat16).to(DEV)
-    gy = torch.randn(km.n_out, cout, generator=g).to(torch.bfloat16).to(DEV)
-    print(f"dW rows {tag} cin={cin} cout={cout} n_in={km.n_in} n_out={km.n_out}", flush=True)
+    x = torch.randn(km.n_in, cin, generator=g).to(dtype).to(DEV)
+    gy = torch.randn(km.n_out, cout, generator=g).to(dtype).to(DEV)
+    print(f"dW rows {tag} {dtype} cin={cin} cout={cout} n_in={km.n_in} n_out={km.n_out}",
+          flush=True)
     rows = abi.conv_backward_weight_rows(x, gy, km, km.K)
     pairs = abi.conv_backward_weight(x, gy, km, km.K)
     _, _, rgw = _oracle_conv(km, x.float().cpu().numpy(),
                              np.zeros((km.K, cin, cout), np.float32), gy.float().cpu().numpy())
-    assert_rel(rows.float().cpu().numpy(), rgw, TOL[torch.bfloat16], f"{tag} rows dW")
-    assert_rel(rows.float().cpu().numpy(), pairs.float().cpu().numpy(), 1e-2,
-               f"{tag} rows vs pairs dW")
+    assert_rel(rows.float().cpu().numpy(), rgw, TOL[dtype], f"{tag} rows dW")
+    assert_rel(rows.float().cpu().numpy(), pairs.float().cpu().numpy(),
+               1e-5 if dtype == torch.float32 else 1e-2, f"{tag} rows vs pairs dW")
+    return x, gy, rows
 
 
 @pytest.mark.parametrize("cin,cout", [(16, 16), (16, 32), (32, 16), (32, 32)])
@@ -151,6 +152,86 @@ def test_weight_gradient_from_neighbour_table_strided_and_4d():
     c4, _, _ = oracle.insert_and_map(random_coords(rng, 6000, 4, 7, batch=1))
     _, _, km4 = gpu_tables_and_map(c4, c4, oracle.region_offsets(4, 3), same=True)
     _rows_check(km4, 32, 32, seed=3, tag="3^4")
+
+
+@pytest.mark.parametrize("cin,cout", [(16, 64), (64, 64), (48, 128)])
+def test_weight_gradient_from_neighbour_table_f32(cin, cout):
+    """fp32: the position-stationary kernel (16-channel input slices, 64
+    output channels per tile, all 27 offsets in one workgroup)."""
+    rng = np.random.default_rng(cin + 7 * cout)
+    c, _, _ = oracle.insert_and_map(random_coords(rng, 9000, 3, 14))
+    _, _, km = gpu_tables_and_map(c, c, oracle.region_offsets(3, 3), same=True)
+    _rows_check(km, cin, cout, seed=cin + cout, tag="3^3", dtype=torch.float32)
+
+
+def test_weight_gradient_from_neighbour_table_f32_strided_4d_and_tiny():
+    """fp32 over a 3^3 stride-2 map and its transpose (n_in != n_out), an
+    81-offset 4D map (three offset groups), and maps smaller than one
+    64-position segment. A 2^3 map (8 offsets) stays on the pair list: the
+    table entry rejects it and the layer dispatch falls back."""
+    rng = np.random.default_rng(31)
+    c, _, _ = oracle.insert_and_map(random_coords(rng, 20000, 3, 30))
+    tin = abi.hash_build(to_dev(c))
+    tout = abi.hash_build(abi.stride_coords(to_dev(c), [2, 2, 2]))
+    km = abi.kernel_map(tin, tout, to_dev(oracle.region_offsets(3, 3)))
+    _rows_check(km, 64, 128, seed=1, tag="down", dtype=torch.float32)
+    _rows_check(km.swapped(), 128, 64, seed=2, tag="up", dtype=torch.float32)
+    km8 = abi.kernel_map(tin, tout, to_dev(oracle.region_offsets(3, 2)))
+    x8 = torch.randn(km8.n_in, 64, device=DEV)
+    gy8 = torch.randn(km8.n_out, 64, device=DEV)
+    with pytest.raises(RuntimeError, match="at least 20 offsets"):
+        abi.conv_backward_weight_rows(x8, gy8, km8, km8.K)
+    assert torch.equal(abi.conv_weight_grad(x8, gy8, km8, km8.K),
+                       abi.conv_backward_weight(x8, gy8, km8, km8.K))
+    c4, _, _ = oracle.insert_and_map(random_coords(rng, 6000, 4, 7, batch=1))
+    _, _, km4 = gpu_tables_and_map(c4, c4, oracle.region_offsets(4, 3), same=True)
+    _rows_check(km4, 16, 64, seed=3, tag="3^4", dtype=torch.float32)
+    for npts in (1, 5, 63, 65):
+        ct, _, _ = oracle.insert_and_map(random_coords(rng, npts, 3, 3))
+        _, _, kmt = gpu_tables_and_map(ct, ct, oracle.region_offsets(3, 3), same=True)
+        _rows_check(kmt, 16, 64, seed=npts, tag=f"tiny{npts}", dtype=torch.float32)
+
+
+def test_weight_gradient_from_neighbour_table_f32_row_order_and_empty():
+    """out_order NULL (the table indexed by output row) gives the same dW as
+    the processing-order table; no output rows gives zeros."""
+    import types
+    rng = np.random.default_rng(37)
+    c, _, _ = oracle.insert_and_map(random_coords(rng, 5000, 3, 12))
+    _, _, km = gpu_tables_and_map(c, c, oracle.region_offsets(3, 3), same=True)
+    x, gy, rows = _rows_check(km, 32, 64, seed=4, tag="order", dtype=torch.float32)
+    nbr = km.nbr.view(km.K, km.n_out)
+    by_row = torch.empty_like(nbr)
+    by_row[:, km.out_order.long()] = nbr
+    km_rows = types.SimpleNamespace(n_in=km.n_in, n_out=km.n_out, n_pairs=km.n_pairs, K=km.K,
+                                    nbr=by_row.contiguous().view(-1), out_order=None)
+    rows2 = abi.conv_backward_weight_rows(x, gy, km_rows, km.K)
+    # the positions are summed in another order: equal to rounding
+    assert_rel(rows2.cpu().numpy(), rows.cpu().numpy(), 1e-5, "row-indexed table dW")
+    km0 = types.SimpleNamespace(n_in=km.n_in, n_out=0, n_pairs=0, K=km.K,
+                                nbr=km.nbr, out_order=km.out_order)
+    z = abi.conv_backward_weight_rows(x, gy[:0], km0, km.K)
+    assert z.shape == (km.K, 32, 64) and not z.any()
+
+
+def test_weight_gradient_from_neighbour_table_f32_full_size():
+    """Config-2 size (4 indoor scenes, about 410k rows, C64): the table kernel
+    against the pair-list kernel, which sums the same products in another
+    order (fp32, rel 1e-5)."""
+    c = scenes.indoor_batch(4, 2)
+    t = abi.hash_build(to_dev(c))
+    km = abi.kernel_map(t, t, to_dev(oracle.region_offsets(3, 3)))
+    g = torch.Generator().manual_seed(9)
+    x = torch.randn(km.n_in, 64, generator=g).to(DEV)
+    gy = torch.randn(km.n_out, 64, generator=g).to(DEV)
+    print(f"dW rows full size n={km.n_out} P={km.n_pairs}", flush=True)
+    rows = abi.conv_backward_weight_rows(x, gy, km, km.K)
+    pairs = abi.conv_backward_weight(x, gy, km, km.K)
+    assert_rel(rows.cpu().numpy(), pairs.cpu().numpy(), 1e-5, "full-size rows vs pairs dW")
+    auto = abi.conv_weight_grad(x, gy, km, km.K)
+    assert torch.equal(auto, rows), "the layer dispatch takes the table kernel for fp32 C64"
+    again = abi.conv_backward_weight_rows(x, gy, km, km.K)
+    assert torch.equal(again, rows), "dW is deterministic"
 
 
 def test_weight_gradient_from_neighbour_table_rejects_other_shapes():
