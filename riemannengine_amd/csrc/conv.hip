@@ -1393,22 +1393,27 @@ constexpr int kDwRowsKW = 3;
 constexpr int kDwRowsBlocks = 256;
 
 // fp32 dW from the neighbour table (conv_dw_pos_kernel): 16-channel input
-// slices, 64 output channels per tile, 7 offsets per wave (all 27 of a 3^3
-// stencil in one workgroup), rows loaded 3 steps ahead, 2 waves per SIMD.
-// Measured on MI355X (config 2, 410k rows, C64, 128 ranges): 419 us
-// against the pair-list kernel's 578; contiguous ranges instead of dealt
-// segments 481 us, 4 offsets per wave 434-444 us. Stencils of fewer than 20
+// slices, 64 output channels per tile (32 where C_out is not a multiple of
+// 64), 7 offsets per wave (all 27 of a 3^3 stencil in one workgroup), rows
+// loaded 3 steps ahead; 2 waves per SIMD for 64-channel tiles, 3 for
+// 32-channel ones. The grid is one round of resident workgroups.
+// Measured on MI355X, kernel + reduce: config 2 (410k rows, C64, 128
+// ranges) 419 us against the pair-list kernel's 578 (contiguous ranges
+// instead of dealt segments 481, 4 offsets per wave 434-444); config 4
+// (233k rows, 81 offsets, C32->32, 128 ranges) 217 against 242; config 1
+// (52k rows, C16->32, 256 ranges) 35 against 46. Stencils of fewer than 20
 // offsets leave most of a wave's offset slots empty and stay on the pair
 // list (config 3's 2^3 transposed map, C128->64: 118 us against 71).
 constexpr int kDwPosKPW = 7;
-constexpr int kDwPosMinK = 20;
 constexpr int kDwPosSlots = 4;
-constexpr int kDwPosWaves = 2;
+constexpr int kDwPosMinK = 20;
 constexpr int64_t kBufMaxBytes = (int64_t(1) << 31) - 256; // buffer offsets stay below kBufOob
+
+template <int VB> constexpr int kDwPosWaves = VB == 4 ? 2 : 3;
 
 static bool dw_pos_supported(int32_t dtype, int cin, int cout, int K, int64_t n_in,
                              int64_t n_out) {
-  return dtype == RHIP_F32 && K >= kDwPosMinK && cin % 16 == 0 && cout % 64 == 0 &&
+  return dtype == RHIP_F32 && K >= kDwPosMinK && cin % 16 == 0 && cout % 32 == 0 &&
          n_in * cin * 4 <= kBufMaxBytes && n_out * cout * 4 <= kBufMaxBytes &&
          static_cast<int64_t>(K) * n_out * 4 <= kBufMaxBytes;
 }
@@ -1419,14 +1424,14 @@ static bool dw_rows_supported(int32_t dtype, int cin, int cout, int K, int64_t n
          dw_pos_supported(dtype, cin, cout, K, n_in, n_out);
 }
 
-// Ranges of the fp32 kernel: a multiple of 8 (one share per XCD), about 512
-// workgroups (two per CU: the whole grid resident at once), at most
-// kDwRowsBlocks (the partial slots of the workspace), at least 4 segments
-// of 64 positions each.
-static int dw_pos_ranges(int K, int cin, int cout, int64_t n_out) {
+// Ranges of the fp32 kernel: a multiple of 8 (one share per XCD), one round
+// of resident workgroups (256 CUs x the waves per SIMD: each workgroup puts
+// one wave on every SIMD of its CU), at most kDwRowsBlocks (the partial
+// slots of the workspace), at least 4 segments of 64 positions each.
+static int dw_pos_ranges(int K, int cin, int cout, int vb, int waves, int64_t n_out) {
   const int groups = static_cast<int>(ceil_div(K, kWaves * kDwPosKPW));
-  const int units = (cin / 16) * (cout / 64) * groups;
-  int64_t r = std::max<int64_t>(kXcds, (512 / units) / kXcds * kXcds);
+  const int units = (cin / 16) * (cout / (16 * vb)) * groups;
+  int64_t r = std::max<int64_t>(kXcds, (256 * waves / units) / kXcds * kXcds);
   const int64_t segs = ceil_div(std::max<int64_t>(n_out, 1), 64);
   r = std::min<int64_t>(r, std::max<int64_t>(kXcds, segs / 4 / kXcds * kXcds));
   return static_cast<int>(std::min<int64_t>(r, kDwRowsBlocks));
@@ -1436,13 +1441,21 @@ static int dw_pos_ranges(int K, int cin, int cout, int64_t n_out) {
 static void run_dw_pos(const float *x, int64_t n_in, int cin, const float *gy, int64_t n_out,
                        int cout, int K, const int32_t *nbr, const int32_t *out_order,
                        float *partial, float *dw, hipStream_t s) {
-  const int ranges = dw_pos_ranges(K, cin, cout, n_out);
+  const int vb = cout % 64 == 0 ? 4 : 2;
+  const int waves = vb == 4 ? kDwPosWaves<4> : kDwPosWaves<2>;
+  const int ranges = dw_pos_ranges(K, cin, cout, vb, waves, n_out);
   const int groups = static_cast<int>(ceil_div(K, kWaves * kDwPosKPW));
-  const int ct = cin / 16, ot = cout / 64;
+  const int ct = cin / 16, ot = cout / (16 * vb);
   if (n_in > 0 && n_out > 0) {
-    hipLaunchKernelGGL((conv_dw_pos_kernel<4, kDwPosKPW, kDwPosSlots, kDwPosWaves>),
-                       dim3(static_cast<unsigned>(ranges * ct * ot * groups)), dim3(kThreads), 0, s,
-                       x, n_in, cin, gy, cout, nbr, out_order, n_out, K, ranges, ct, ot, partial);
+    const dim3 grid(static_cast<unsigned>(ranges * ct * ot * groups));
+    if (vb == 4)
+      hipLaunchKernelGGL((conv_dw_pos_kernel<4, kDwPosKPW, kDwPosSlots, kDwPosWaves<4>>), grid,
+                         dim3(kThreads), 0, s, x, n_in, cin, gy, cout, nbr, out_order, n_out, K,
+                         ranges, ct, ot, partial);
+    else
+      hipLaunchKernelGGL((conv_dw_pos_kernel<2, kDwPosKPW, kDwPosSlots, kDwPosWaves<2>>), grid,
+                         dim3(kThreads), 0, s, x, n_in, cin, gy, cout, nbr, out_order, n_out, K,
+                         ranges, ct, ot, partial);
     RHIP_LAUNCH_CHECK();
   }
   const int64_t ne = static_cast<int64_t>(K) * cin * cout;
@@ -1661,7 +1674,7 @@ extern "C" int rhip_conv_backward_weight_rows(
       throw Error(RHIP_ERR_UNSUPPORTED,
                   "rhip_conv_backward_weight_rows: bf16 with 16 or 32 input and output "
                   "channels, or fp32 with at least 20 offsets, input channels a multiple "
-                  "of 16 and output channels a multiple of 64 (use "
+                  "of 16 and output channels a multiple of 32 (use "
                   "rhip_conv_backward_weight)");
     RHIP_CHECK_ARG(grad_w != nullptr, "grad_w is null");
     RHIP_CHECK_ARG(n_in == 0 || n_out == 0 || (x && grad_y && nbr),

@@ -154,10 +154,10 @@ def test_weight_gradient_from_neighbour_table_strided_and_4d():
     _rows_check(km4, 32, 32, seed=3, tag="3^4")
 
 
-@pytest.mark.parametrize("cin,cout", [(16, 64), (64, 64), (48, 128)])
+@pytest.mark.parametrize("cin,cout", [(16, 64), (64, 64), (48, 128), (16, 32), (32, 96)])
 def test_weight_gradient_from_neighbour_table_f32(cin, cout):
-    """fp32: the position-stationary kernel (16-channel input slices, 64
-    output channels per tile, all 27 offsets in one workgroup)."""
+    """fp32: the position-stationary kernel (16-channel input slices, 64 or
+    32 output channels per tile, all 27 offsets in one workgroup)."""
     rng = np.random.default_rng(cin + 7 * cout)
     c, _, _ = oracle.insert_and_map(random_coords(rng, 9000, 3, 14))
     _, _, km = gpu_tables_and_map(c, c, oracle.region_offsets(3, 3), same=True)
@@ -186,6 +186,7 @@ def test_weight_gradient_from_neighbour_table_f32_strided_4d_and_tiny():
     c4, _, _ = oracle.insert_and_map(random_coords(rng, 6000, 4, 7, batch=1))
     _, _, km4 = gpu_tables_and_map(c4, c4, oracle.region_offsets(4, 3), same=True)
     _rows_check(km4, 16, 64, seed=3, tag="3^4", dtype=torch.float32)
+    _rows_check(km4, 32, 32, seed=5, tag="3^4 C32", dtype=torch.float32)
     for npts in (1, 5, 63, 65):
         ct, _, _ = oracle.insert_and_map(random_coords(rng, npts, 3, 3))
         _, _, kmt = gpu_tables_and_map(ct, ct, oracle.region_offsets(3, 3), same=True)
@@ -242,8 +243,9 @@ def test_weight_gradient_from_neighbour_table_rejects_other_shapes():
     gy = torch.zeros(km.n_out, 32, dtype=torch.bfloat16, device=DEV)
     with pytest.raises(RuntimeError, match="16 or 32"):
         abi.conv_backward_weight_rows(x, gy, km, km.K)
+    gy48 = torch.zeros(km.n_out, 48, dtype=torch.float32, device=DEV)
     with pytest.raises(RuntimeError, match="16 or 32"):
-        abi.conv_backward_weight_rows(x[:, :32].float().contiguous(), gy.float(), km, km.K)
+        abi.conv_backward_weight_rows(x[:, :32].float().contiguous(), gy48, km, km.K)
 
 
 def test_kats_through_the_gpu(golden_dir):
