@@ -183,14 +183,21 @@ __global__ __launch_bounds__(kMapBlock) void invert_order_kernel(
     pos[order[j]] = static_cast<int32_t>(j);
 }
 
-// Sort key of a neighbour mask: the mask itself for K <= 16, else a 16-bit
-// hash (equal masks get equal keys; unequal ones rarely collide, which only
-// costs MFMA fill, never correctness).
+// Sort key of a neighbour mask: the mask itself for K <= 16; else the
+// neighbour count, largest first, then a 16-bit hash of the mask (equal
+// masks get equal keys; unequal ones rarely collide, which only costs MFMA
+// fill, never correctness). Largest first puts the tiles with the most
+// stages at the front of the convolution grid, so the grid does not end on
+// a few long workgroups.
 __device__ __forceinline__ uint32_t mask_key(uint64_t m0, uint64_t m1, int K) {
   if (K <= kKeyBits)
     return static_cast<uint32_t>(m0);
-  return static_cast<uint32_t>(mix64(m0 ^ mix64(m1 ^ 0x9e3779b97f4a7c15ull)) >> 48);
+  const uint32_t count = static_cast<uint32_t>(__popcll(m0) + __popcll(m1)); // <= 128
+  return ((128u - count) << 16) |
+         static_cast<uint32_t>(mix64(m0 ^ mix64(m1 ^ 0x9e3779b97f4a7c15ull)) >> 48);
 }
+// Bits of mask_key for K offsets.
+static int mask_key_bits(int K) { return K <= kKeyBits ? K : kKeyBits + 8; }
 
 __global__ __launch_bounds__(kMapBlock) void mask_key_kernel(
     const int32_t *__restrict__ nbr_sp, int64_t n, int K,
@@ -608,7 +615,7 @@ extern "C" int rhip_kmap_count(const rhip_table *in_table, const int32_t *out_co
                            w.nbr_sp, n_out, K, w.keys_a, w.vals_a);
         RHIP_LAUNCH_CHECK();
         sort_pairs_u32(w.sort_tmp, w.sort_bytes, w.keys_a, w.keys_b, w.vals_a, w.vals_b,
-                       n_out, std::min<int>(K, kKeyBits), stream);
+                       n_out, mask_key_bits(K), stream);
         jpos = w.vals_b;
       }
       hipLaunchKernelGGL(kmap_permute_kernel, dim3(nb, K), dim3(kMapBlock), 0, stream,
@@ -678,7 +685,7 @@ extern "C" int rhip_kmap_fill(const int32_t *nbr, const int32_t *out_order, int6
                          in_spatial_order, n_in, K, w.tkeys_a, w.tvals_a);
       RHIP_LAUNCH_CHECK();
       sort_pairs_u32(w.tsort_tmp, w.tsort_bytes, w.tkeys_a, w.tkeys_b, w.tvals_a, w.tvals_b,
-                     n_in, std::min<int>(K, kKeyBits), stream);
+                     n_in, mask_key_bits(K), stream);
       qpos = w.tvals_b;
     }
     hipLaunchKernelGGL(in_order_kernel, dim3(nbi), dim3(kMapBlock), 0, stream, qpos,
