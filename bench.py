@@ -609,7 +609,7 @@ def main():
                       "backward_weight": (
                           "conv_dw_pos_kernel + conv_dw_rows_reduce_kernel (dW pass)"
                           if args.dtype == "f32" else
-                          "conv_dw_kernel + conv_dw_reduce_kernel (dW pass)")}[dom]
+                          "conv_dw_pos_bf16_kernel + conv_dw_rows_reduce_kernel (dW pass)")}[dom]
     roof["kernel_ms"] = round(per[dom], 4)
     roof["algorithmic"] = {"flop": F, "bytes": B}
 

@@ -1117,6 +1117,190 @@ conv_dw_pos_kernel(const float *__restrict__ x, int64_t n_in, int cin,
   }
 }
 
+// bf16 dW from the neighbour table, position-stationary like
+// conv_dw_pos_kernel: a workgroup owns a 16-channel input slice ci0, 64
+// output channels co0 and up to 4*KPW offsets; wave w keeps the 16 x 64
+// tiles of offsets k0 + w + 4j in registers. A step covers 32 positions
+// (the reduction axis of v_mfma_f32_16x16x32_bf16), and its rows go through
+// the wave's own LDS rows so that ds_read_b64_tr_b16 can hand each lane the
+// eight positions of one channel:
+//  * lane l loads half of position l/2's dY row (32 channels, 4 x 16 bytes)
+//    and, per offset, half of its X slice (8 channels, 16 bytes);
+//  * at the step, the wave writes them row-major to its LDS rows and reads
+//    the K-major operands back (two transposed reads per 16 x 32 operand);
+//    LDS traffic of one wave completes in order, so no barrier is needed;
+//  * an offset without a neighbour among the step's 32 positions skips its
+//    LDS traffic and MFMAs (wave-uniform).
+// Indices, out-of-range buffer loads, segments dealt to ranges and the
+// partial slots are as in conv_dw_pos_kernel; rows are loaded one step
+// (32 positions) ahead.
+template <int KPW, int WAVES>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(WAVES))) void
+conv_dw_pos_bf16_kernel(const __bf16 *__restrict__ x, int64_t n_in, int cin,
+                        const __bf16 *__restrict__ gy, int cout, const int32_t *__restrict__ nbr,
+                        const int32_t *__restrict__ out_order, int64_t n_out, int K, int ranges,
+                        int ci_tiles, int co_tiles, float *__restrict__ partial) {
+  constexpr int GK = kWaves * KPW;
+  constexpr int LDY = 64 + 8, LDX = 16 + 8; // LDS row strides (elements), 16-byte multiples
+  __shared__ __align__(16) __bf16 sY[kWaves][32 * LDY];
+  __shared__ __align__(16) __bf16 sX[kWaves][32 * LDX];
+  const int groups = (K + GK - 1) / GK;
+  const int units = ci_tiles * co_tiles * groups;
+  const int r8 = ranges / kXcds;
+  const int xcd = static_cast<int>(blockIdx.x % kXcds), m = static_cast<int>(blockIdx.x / kXcds);
+  const int rg = xcd * r8 + m / units;
+  int u = m % units;
+  const int grp = u % groups;
+  u /= groups;
+  const int ci0 = (u % ci_tiles) * 16, co0 = (u / ci_tiles) * 64;
+
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const int i16 = lane & 15;
+  const int g = lane >> 4;
+  const int half = lane & 1;
+  const int64_t total = (n_out + 63) / 64;
+  const int segs = static_cast<int>((total + 2LL * ranges - 1) / (2LL * ranges)) * 2;
+  int kk[KPW], kval[KPW];
+#pragma unroll
+  for (int j = 0; j < KPW; ++j) {
+    kk[j] = grp * GK + wv + kWaves * j;
+    kval[j] = opaque(kk[j] < K ? -1 : 0);
+  }
+
+  const __amdgpu_buffer_rsrc_t rx = buf_rsrc(x, n_in * cin * 2);
+  const __amdgpu_buffer_rsrc_t ry = buf_rsrc(gy, n_out * cout * 2);
+  const __amdgpu_buffer_rsrc_t rn = buf_rsrc(nbr, static_cast<int64_t>(K) * n_out * 4);
+  const __amdgpu_buffer_rsrc_t ro = buf_rsrc(out_order, out_order ? n_out * 4 : 0);
+  auto pick = [](uint32_t off, int32_t keep) {
+    return (off & static_cast<uint32_t>(keep)) | (kBufOob & ~static_cast<uint32_t>(keep));
+  };
+
+  struct Seg {
+    int32_t id[KPW];
+    int32_t orow;
+  };
+  struct Dat {
+    v4u xv[KPW];
+    v4u yv[4];
+  };
+  auto load_seg = [&](int sg, Seg &S) {
+    const int64_t p = 64 * (rg + static_cast<int64_t>(sg) * ranges) + lane;
+    const int32_t in = opaque(static_cast<int32_t>((p - n_out) >> 63));
+#pragma unroll
+    for (int j = 0; j < KPW; ++j) {
+      const int32_t keep = in & kval[j];
+      S.id[j] = static_cast<int32_t>(__builtin_amdgcn_raw_buffer_load_b32(
+                    rn, pick(static_cast<uint32_t>((kk[j] * n_out + p) * 4), keep), 0, 0)) |
+                ~keep;
+    }
+    if (out_order)
+      S.orow = static_cast<int32_t>(__builtin_amdgcn_raw_buffer_load_b32(
+                   ro, pick(static_cast<uint32_t>(p * 4), in), 0, 0)) |
+               ~in;
+    else
+      S.orow = static_cast<int32_t>(p) | ~in;
+  };
+  auto prep = [&](Seg &S, uint64_t (&live)[KPW]) {
+#pragma unroll
+    for (int j = 0; j < KPW; ++j) {
+      const int32_t r = S.id[j];
+      live[j] = __ballot(r >= 0);
+      S.id[j] = static_cast<int32_t>(pick(static_cast<uint32_t>((r * cin + ci0) * 2), opaque(~(r >> 31))));
+    }
+    const int32_t r = S.orow;
+    S.orow = static_cast<int32_t>(pick(static_cast<uint32_t>((r * cout + co0) * 2), opaque(~(r >> 31))));
+  };
+  // step s (0 or 1) of a segment: lane l takes position 32s + l/2's offsets
+  auto load_dat = [&](const Seg &S, int s, Dat &D) {
+    const int src = (32 * s + (lane >> 1)) * 4;
+#pragma unroll
+    for (int j = 0; j < KPW; ++j) {
+      const uint32_t o = static_cast<uint32_t>(__builtin_amdgcn_ds_bpermute(src, S.id[j])) + 16 * half;
+      D.xv[j] = __builtin_amdgcn_raw_buffer_load_b128(rx, o, 0, 0);
+    }
+    const uint32_t o = static_cast<uint32_t>(__builtin_amdgcn_ds_bpermute(src, S.orow)) + 64 * half;
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      D.yv[q] = __builtin_amdgcn_raw_buffer_load_b128(ry, o + 16 * q, 0, 0);
+  };
+
+  v4f acc[KPW][4];
+#pragma unroll
+  for (int j = 0; j < KPW; ++j)
+#pragma unroll
+    for (int nb = 0; nb < 4; ++nb)
+      acc[j][nb] = v4f{0.f, 0.f, 0.f, 0.f};
+  __bf16 *const wy = sY[wv];
+  __bf16 *const wx = sX[wv];
+  const int prow = 8 * g + i16 / 4, pcol = 4 * (i16 % 4);
+  auto operand = [&](const __bf16 *base, int ld, int col) {
+    const v4s lo = ds_read_tr16(base + prow * ld + col + pcol);
+    const v4s hi = ds_read_tr16(base + (prow + 4) * ld + col + pcol);
+    return __builtin_bit_cast(v8bf, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+  };
+  auto compute = [&](const Dat &D, const uint64_t (&live)[KPW], int s) {
+    bool any = false;
+#pragma unroll
+    for (int j = 0; j < KPW; ++j)
+      any |= ((live[j] >> (32 * s)) & 0xffffffffull) != 0;
+    if (!any)
+      return; // wave-uniform
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      *reinterpret_cast<v4u *>(wy + (lane >> 1) * LDY + 32 * half + 8 * q) = D.yv[q];
+    v8bf b[4];
+#pragma unroll
+    for (int nb = 0; nb < 4; ++nb)
+      b[nb] = operand(wy, LDY, 16 * nb);
+#pragma unroll
+    for (int j = 0; j < KPW; ++j)
+      if ((live[j] >> (32 * s)) & 0xffffffffull) { // wave-uniform
+        *reinterpret_cast<v4u *>(wx + (lane >> 1) * LDX + 8 * half) = D.xv[j];
+        const v8bf a = operand(wx, LDX, 0);
+#pragma unroll
+        for (int nb = 0; nb < 4; ++nb)
+          acc[j][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b[nb], acc[j][nb], 0, 0, 0);
+      }
+  };
+
+  // segments in two slots, steps in two row slots (two steps a segment)
+  Seg SA, SB;
+  uint64_t LA[KPW], LB[KPW];
+  Dat DA, DB;
+  auto run_seg = [&](Seg &S, const uint64_t (&LS)[KPW], Seg &N, uint64_t (&LN)[KPW],
+                     int next_load) {
+    load_dat(S, 1, DB);
+    compute(DA, LS, 0);
+    prep(N, LN);
+    load_dat(N, 0, DA);
+    compute(DB, LS, 1);
+    load_seg(next_load, S);
+  };
+  load_seg(0, SA);
+  load_seg(1, SB);
+  prep(SA, LA);
+  load_dat(SA, 0, DA);
+  for (int sg = 0; sg < segs; sg += 2) {
+    run_seg(SA, LA, SB, LB, sg + 2);
+    run_seg(SB, LB, SA, LA, sg + 3);
+  }
+
+  // lane holds D[4g+e][i16] of block nb: dW[k][ci0 + 4g + e][co0 + 16nb + i16]
+#pragma unroll
+  for (int j = 0; j < KPW; ++j) {
+    if (kk[j] >= K)
+      continue;
+    float *dst = partial + ((static_cast<int64_t>(rg) * K + kk[j]) * cin + ci0 + 4 * g) * cout +
+                 co0 + i16;
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+#pragma unroll
+      for (int nb = 0; nb < 4; ++nb)
+        dst[static_cast<int64_t>(e) * cout + 16 * nb] = acc[j][nb][e];
+  }
+}
+
 // Any-shape fallback: one lane per dW element, looping over its pairs.
 template <typename T>
 __global__ __launch_bounds__(kThreads) void conv_dw_generic_kernel(
@@ -1411,17 +1595,27 @@ constexpr int64_t kBufMaxBytes = (int64_t(1) << 31) - 256; // buffer offsets sta
 
 template <int VB> constexpr int kDwPosWaves = VB == 4 ? 2 : 3;
 
+// bf16 (conv_dw_pos_bf16_kernel): 64-channel output tiles only, 7 offsets
+// per wave, 2 waves per SIMD, the same one-round grid. Measured on MI355X,
+// kernel + reduce against the pair-list kernel: config 2 (C64, 410k rows,
+// 128 ranges) 157 us against 230; config 5's stages C64 (191k rows) 91
+// against 141, C128 (43k rows, 32 ranges) 89 against 142, C256 (9k rows,
+// 8 ranges) 93 against 146.
 static bool dw_pos_supported(int32_t dtype, int cin, int cout, int K, int64_t n_in,
                              int64_t n_out) {
-  return dtype == RHIP_F32 && K >= kDwPosMinK && cin % 16 == 0 && cout % 32 == 0 &&
-         n_in * cin * 4 <= kBufMaxBytes && n_out * cout * 4 <= kBufMaxBytes &&
+  const int64_t s = dtype == RHIP_F32 ? 4 : 2;
+  return K >= kDwPosMinK && cin % 16 == 0 && cout % (dtype == RHIP_F32 ? 32 : 64) == 0 &&
+         n_in * cin * s <= kBufMaxBytes && n_out * cout * s <= kBufMaxBytes &&
          static_cast<int64_t>(K) * n_out * 4 <= kBufMaxBytes;
+}
+
+static bool dw_narrow_bf16(int32_t dtype, int cin, int cout) {
+  return dtype == RHIP_BF16 && (cin == 16 || cin == 32) && (cout == 16 || cout == 32);
 }
 
 static bool dw_rows_supported(int32_t dtype, int cin, int cout, int K, int64_t n_in,
                               int64_t n_out) {
-  return (dtype == RHIP_BF16 && (cin == 16 || cin == 32) && (cout == 16 || cout == 32)) ||
-         dw_pos_supported(dtype, cin, cout, K, n_in, n_out);
+  return dw_narrow_bf16(dtype, cin, cout) || dw_pos_supported(dtype, cin, cout, K, n_in, n_out);
 }
 
 // Ranges of the fp32 kernel: a multiple of 8 (one share per XCD), one round
@@ -1435,6 +1629,28 @@ static int dw_pos_ranges(int K, int cin, int cout, int vb, int waves, int64_t n_
   const int64_t segs = ceil_div(std::max<int64_t>(n_out, 1), 64);
   r = std::min<int64_t>(r, std::max<int64_t>(kXcds, segs / 4 / kXcds * kXcds));
   return static_cast<int>(std::min<int64_t>(r, kDwRowsBlocks));
+}
+
+// grad_w [K, cin, cout] (bf16, overwritten) from the neighbour table.
+static void run_dw_pos_bf16(const __bf16 *x, int64_t n_in, int cin, const __bf16 *gy,
+                            int64_t n_out, int cout, int K, const int32_t *nbr,
+                            const int32_t *out_order, float *partial, __bf16 *dw,
+                            hipStream_t s) {
+  constexpr int kWavesBf16 = 2;
+  const int ranges = dw_pos_ranges(K, cin, cout, 4, kWavesBf16, n_out);
+  const int groups = static_cast<int>(ceil_div(K, kWaves * kDwPosKPW));
+  const int ct = cin / 16, ot = cout / 64;
+  if (n_in > 0 && n_out > 0) {
+    hipLaunchKernelGGL((conv_dw_pos_bf16_kernel<kDwPosKPW, kWavesBf16>),
+                       dim3(static_cast<unsigned>(ranges * ct * ot * groups)), dim3(kThreads), 0, s,
+                       x, n_in, cin, gy, cout, nbr, out_order, n_out, K, ranges, ct, ot, partial);
+    RHIP_LAUNCH_CHECK();
+  }
+  const int64_t ne = static_cast<int64_t>(K) * cin * cout;
+  hipLaunchKernelGGL((conv_dw_rows_reduce_kernel<__bf16>), dim3(static_cast<unsigned>(
+                         ceil_div(ne / 4, kWave))), dim3(1024), 0, s, partial,
+                     n_in > 0 && n_out > 0 ? ranges : 0, ne, dw);
+  RHIP_LAUNCH_CHECK();
 }
 
 // grad_w [K, cin, cout] (fp32, overwritten) from the neighbour table.
@@ -1673,8 +1889,8 @@ extern "C" int rhip_conv_backward_weight_rows(
     if (!dw_rows_supported(dtype, cin, cout, K, n_in, n_out))
       throw Error(RHIP_ERR_UNSUPPORTED,
                   "rhip_conv_backward_weight_rows: bf16 with 16 or 32 input and output "
-                  "channels, or fp32 with at least 20 offsets, input channels a multiple "
-                  "of 16 and output channels a multiple of 32 (use "
+                  "channels, or at least 20 offsets with input channels a multiple of 16 "
+                  "and output channels a multiple of 32 (fp32) or 64 (bf16) (use "
                   "rhip_conv_backward_weight)");
     RHIP_CHECK_ARG(grad_w != nullptr, "grad_w is null");
     RHIP_CHECK_ARG(n_in == 0 || n_out == 0 || (x && grad_y && nbr),
@@ -1686,6 +1902,10 @@ extern "C" int rhip_conv_backward_weight_rows(
     if (dtype == RHIP_F32)
       run_dw_pos(static_cast<const float *>(x), n_in, cin, static_cast<const float *>(grad_y),
                  n_out, cout, K, nbr, out_order, w.partial, static_cast<float *>(grad_w), stream);
+    else if (!dw_narrow_bf16(dtype, cin, cout))
+      run_dw_pos_bf16(static_cast<const __bf16 *>(x), n_in, cin,
+                      static_cast<const __bf16 *>(grad_y), n_out, cout, K, nbr, out_order,
+                      w.partial, static_cast<__bf16 *>(grad_w), stream);
     else
       run_dw_rows(static_cast<const __bf16 *>(x), n_in, cin,
                   static_cast<const __bf16 *>(grad_y), n_out, cout, K, nbr, out_order, w.partial,

@@ -235,6 +235,48 @@ def test_weight_gradient_from_neighbour_table_f32_full_size():
     assert torch.equal(again, rows), "dW is deterministic"
 
 
+@pytest.mark.parametrize("cin,cout", [(64, 64), (16, 128), (48, 64)])
+def test_weight_gradient_from_neighbour_table_bf16_wide(cin, cout):
+    """bf16 with 64-channel output tiles: the position-stationary kernel with
+    the step's rows transposed through each wave's LDS rows."""
+    rng = np.random.default_rng(cin + 11 * cout)
+    c, _, _ = oracle.insert_and_map(random_coords(rng, 9000, 3, 14))
+    _, _, km = gpu_tables_and_map(c, c, oracle.region_offsets(3, 3), same=True)
+    _rows_check(km, cin, cout, seed=cin + cout, tag="3^3")
+
+
+def test_weight_gradient_from_neighbour_table_bf16_wide_strided_4d_tiny_full():
+    """bf16 64-channel tiles over a 3^3 stride-2 map and its transpose, an
+    81-offset 4D map, maps smaller than one segment, and config 2's full
+    size against the pair-list kernel."""
+    rng = np.random.default_rng(41)
+    c, _, _ = oracle.insert_and_map(random_coords(rng, 20000, 3, 30))
+    tin = abi.hash_build(to_dev(c))
+    tout = abi.hash_build(abi.stride_coords(to_dev(c), [2, 2, 2]))
+    km = abi.kernel_map(tin, tout, to_dev(oracle.region_offsets(3, 3)))
+    _rows_check(km, 64, 128, seed=1, tag="down")
+    _rows_check(km.swapped(), 128, 64, seed=2, tag="up")
+    c4, _, _ = oracle.insert_and_map(random_coords(rng, 6000, 4, 7, batch=1))
+    _, _, km4 = gpu_tables_and_map(c4, c4, oracle.region_offsets(4, 3), same=True)
+    _rows_check(km4, 32, 64, seed=3, tag="3^4")
+    for npts in (1, 33, 65):
+        ct, _, _ = oracle.insert_and_map(random_coords(rng, npts, 3, 3))
+        _, _, kmt = gpu_tables_and_map(ct, ct, oracle.region_offsets(3, 3), same=True)
+        _rows_check(kmt, 16, 64, seed=npts, tag=f"tiny{npts}")
+    cf = scenes.indoor_batch(4, 2)
+    t = abi.hash_build(to_dev(cf))
+    kmf = abi.kernel_map(t, t, to_dev(oracle.region_offsets(3, 3)))
+    g = torch.Generator().manual_seed(9)
+    x = torch.randn(kmf.n_in, 64, generator=g).to(torch.bfloat16).to(DEV)
+    gy = torch.randn(kmf.n_out, 64, generator=g).to(torch.bfloat16).to(DEV)
+    print(f"dW rows bf16 full size n={kmf.n_out}", flush=True)
+    rows = abi.conv_backward_weight_rows(x, gy, kmf, kmf.K)
+    pairs = abi.conv_backward_weight(x, gy, kmf, kmf.K)
+    assert_rel(rows.float().cpu().numpy(), pairs.float().cpu().numpy(), 1e-2,
+               "bf16 full-size rows vs pairs dW")
+    assert torch.equal(abi.conv_weight_grad(x, gy, kmf, kmf.K), rows)
+
+
 def test_weight_gradient_from_neighbour_table_rejects_other_shapes():
     rng = np.random.default_rng(2)
     c, _, _ = oracle.insert_and_map(random_coords(rng, 500, 3, 8))
