@@ -265,8 +265,8 @@ int rhip_conv_backward_weight(const void *x, int64_t n_in, int32_t cin,
  * X rows that neighbouring positions share are read once per position
  * range. Supported: bf16 with 16 or 32 input and output channels, and at
  * least 20 offsets with input channels a multiple of 16 and output channels
- * a multiple of 32 (fp32) or 64 (bf16) (each of x, grad_y and the table
- * under 2 GiB); other shapes return
+ * a multiple of 32 (each of x, grad_y and the table under 2 GiB); other
+ * shapes return
  * RHIP_ERR_UNSUPPORTED, for which rhip_conv_backward_weight is the
  * fallback. Workspace as for rhip_conv_workspace_bytes.
  * Replaces the dW half of MmBackward (engine/nn/conv.cpp:62), like

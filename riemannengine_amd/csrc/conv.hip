@@ -1118,14 +1118,14 @@ conv_dw_pos_kernel(const float *__restrict__ x, int64_t n_in, int cin,
 }
 
 // bf16 dW from the neighbour table, position-stationary like
-// conv_dw_pos_kernel: a workgroup owns a 16-channel input slice ci0, 64
-// output channels co0 and up to 4*KPW offsets; wave w keeps the 16 x 64
+// conv_dw_pos_kernel: a workgroup owns a 16-channel input slice ci0, 16*NB
+// output channels co0 and up to 4*KPW offsets; wave w keeps the 16 x 16*NB
 // tiles of offsets k0 + w + 4j in registers. A step covers 32 positions
 // (the reduction axis of v_mfma_f32_16x16x32_bf16), and its rows go through
 // the wave's own LDS rows so that ds_read_b64_tr_b16 can hand each lane the
 // eight positions of one channel:
-//  * lane l loads half of position l/2's dY row (32 channels, 4 x 16 bytes)
-//    and, per offset, half of its X slice (8 channels, 16 bytes);
+//  * lane l loads half of position l/2's dY row (8*NB channels, NB x 16
+//    bytes) and, per offset, half of its X slice (8 channels, 16 bytes);
 //  * at the step, the wave writes them row-major to its LDS rows and reads
 //    the K-major operands back (two transposed reads per 16 x 32 operand);
 //    LDS traffic of one wave completes in order, so no barrier is needed;
@@ -1134,14 +1134,14 @@ conv_dw_pos_kernel(const float *__restrict__ x, int64_t n_in, int cin,
 // Indices, out-of-range buffer loads, segments dealt to ranges and the
 // partial slots are as in conv_dw_pos_kernel; rows are loaded one step
 // (32 positions) ahead.
-template <int KPW, int WAVES>
+template <int NB, int KPW, int WAVES>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(WAVES))) void
 conv_dw_pos_bf16_kernel(const __bf16 *__restrict__ x, int64_t n_in, int cin,
                         const __bf16 *__restrict__ gy, int cout, const int32_t *__restrict__ nbr,
                         const int32_t *__restrict__ out_order, int64_t n_out, int K, int ranges,
                         int ci_tiles, int co_tiles, float *__restrict__ partial) {
   constexpr int GK = kWaves * KPW;
-  constexpr int LDY = 64 + 8, LDX = 16 + 8; // LDS row strides (elements), 16-byte multiples
+  constexpr int LDY = 16 * NB + 8, LDX = 16 + 8; // LDS row strides (elements), 16-byte multiples
   __shared__ __align__(16) __bf16 sY[kWaves][32 * LDY];
   __shared__ __align__(16) __bf16 sX[kWaves][32 * LDX];
   const int groups = (K + GK - 1) / GK;
@@ -1152,7 +1152,7 @@ conv_dw_pos_bf16_kernel(const __bf16 *__restrict__ x, int64_t n_in, int cin,
   int u = m % units;
   const int grp = u % groups;
   u /= groups;
-  const int ci0 = (u % ci_tiles) * 16, co0 = (u / ci_tiles) * 64;
+  const int ci0 = (u % ci_tiles) * 16, co0 = (u / ci_tiles) * (16 * NB);
 
   const int lane = threadIdx.x & (kWave - 1);
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
@@ -1182,7 +1182,7 @@ conv_dw_pos_bf16_kernel(const __bf16 *__restrict__ x, int64_t n_in, int cin,
   };
   struct Dat {
     v4u xv[KPW];
-    v4u yv[4];
+    v4u yv[NB];
   };
   auto load_seg = [&](int sg, Seg &S) {
     const int64_t p = 64 * (rg + static_cast<int64_t>(sg) * ranges) + lane;
@@ -1219,17 +1219,17 @@ conv_dw_pos_bf16_kernel(const __bf16 *__restrict__ x, int64_t n_in, int cin,
       const uint32_t o = static_cast<uint32_t>(__builtin_amdgcn_ds_bpermute(src, S.id[j])) + 16 * half;
       D.xv[j] = __builtin_amdgcn_raw_buffer_load_b128(rx, o, 0, 0);
     }
-    const uint32_t o = static_cast<uint32_t>(__builtin_amdgcn_ds_bpermute(src, S.orow)) + 64 * half;
+    const uint32_t o = static_cast<uint32_t>(__builtin_amdgcn_ds_bpermute(src, S.orow)) + 16 * NB * half;
 #pragma unroll
-    for (int q = 0; q < 4; ++q)
+    for (int q = 0; q < NB; ++q)
       D.yv[q] = __builtin_amdgcn_raw_buffer_load_b128(ry, o + 16 * q, 0, 0);
   };
 
-  v4f acc[KPW][4];
+  v4f acc[KPW][NB];
 #pragma unroll
   for (int j = 0; j < KPW; ++j)
 #pragma unroll
-    for (int nb = 0; nb < 4; ++nb)
+    for (int nb = 0; nb < NB; ++nb)
       acc[j][nb] = v4f{0.f, 0.f, 0.f, 0.f};
   __bf16 *const wy = sY[wv];
   __bf16 *const wx = sX[wv];
@@ -1247,11 +1247,11 @@ conv_dw_pos_bf16_kernel(const __bf16 *__restrict__ x, int64_t n_in, int cin,
     if (!any)
       return; // wave-uniform
 #pragma unroll
-    for (int q = 0; q < 4; ++q)
-      *reinterpret_cast<v4u *>(wy + (lane >> 1) * LDY + 32 * half + 8 * q) = D.yv[q];
-    v8bf b[4];
+    for (int q = 0; q < NB; ++q)
+      *reinterpret_cast<v4u *>(wy + (lane >> 1) * LDY + 8 * NB * half + 8 * q) = D.yv[q];
+    v8bf b[NB];
 #pragma unroll
-    for (int nb = 0; nb < 4; ++nb)
+    for (int nb = 0; nb < NB; ++nb)
       b[nb] = operand(wy, LDY, 16 * nb);
 #pragma unroll
     for (int j = 0; j < KPW; ++j)
@@ -1259,7 +1259,7 @@ conv_dw_pos_bf16_kernel(const __bf16 *__restrict__ x, int64_t n_in, int cin,
         *reinterpret_cast<v4u *>(wx + (lane >> 1) * LDX + 8 * half) = D.xv[j];
         const v8bf a = operand(wx, LDX, 0);
 #pragma unroll
-        for (int nb = 0; nb < 4; ++nb)
+        for (int nb = 0; nb < NB; ++nb)
           acc[j][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b[nb], acc[j][nb], 0, 0, 0);
       }
   };
@@ -1296,7 +1296,7 @@ conv_dw_pos_bf16_kernel(const __bf16 *__restrict__ x, int64_t n_in, int cin,
 #pragma unroll
     for (int e = 0; e < 4; ++e)
 #pragma unroll
-      for (int nb = 0; nb < 4; ++nb)
+      for (int nb = 0; nb < NB; ++nb)
         dst[static_cast<int64_t>(e) * cout + 16 * nb] = acc[j][nb][e];
   }
 }
@@ -1595,16 +1595,18 @@ constexpr int64_t kBufMaxBytes = (int64_t(1) << 31) - 256; // buffer offsets sta
 
 template <int VB> constexpr int kDwPosWaves = VB == 4 ? 2 : 3;
 
-// bf16 (conv_dw_pos_bf16_kernel): 64-channel output tiles only, 7 offsets
-// per wave, 2 waves per SIMD, the same one-round grid. Measured on MI355X,
-// kernel + reduce against the pair-list kernel: config 2 (C64, 410k rows,
-// 128 ranges) 157 us against 230; config 5's stages C64 (191k rows) 91
-// against 141, C128 (43k rows, 32 ranges) 89 against 142, C256 (9k rows,
-// 8 ranges) 93 against 146.
+// bf16 (conv_dw_pos_bf16_kernel): 64-channel output tiles (32 where C_out
+// is not a multiple of 64), 7 offsets per wave, 2 waves per SIMD, the same
+// one-round grid. Measured on MI355X, kernel + reduce against the pair-list
+// kernel: config 2 (C64, 410k rows, 128 ranges) 157 us against 230; config
+// 5's stages C64 (191k rows) 91 against 141, C128 (43k rows, 32 ranges) 89
+// against 142, C256 (9k rows, 8 ranges) 93 against 146; its 808k-row stage
+// against the narrow-channel conv_dw_rows_kernel: C32->32 139 us against
+// 189, C16->32 94 against 161 (3 waves per SIMD spills: 200 and 153).
 static bool dw_pos_supported(int32_t dtype, int cin, int cout, int K, int64_t n_in,
                              int64_t n_out) {
   const int64_t s = dtype == RHIP_F32 ? 4 : 2;
-  return K >= kDwPosMinK && cin % 16 == 0 && cout % (dtype == RHIP_F32 ? 32 : 64) == 0 &&
+  return K >= kDwPosMinK && cin % 16 == 0 && cout % 32 == 0 &&
          n_in * cin * s <= kBufMaxBytes && n_out * cout * s <= kBufMaxBytes &&
          static_cast<int64_t>(K) * n_out * 4 <= kBufMaxBytes;
 }
@@ -1637,13 +1639,20 @@ static void run_dw_pos_bf16(const __bf16 *x, int64_t n_in, int cin, const __bf16
                             const int32_t *out_order, float *partial, __bf16 *dw,
                             hipStream_t s) {
   constexpr int kWavesBf16 = 2;
-  const int ranges = dw_pos_ranges(K, cin, cout, 4, kWavesBf16, n_out);
+  const int vb = cout % 64 == 0 ? 4 : 2;
+  const int ranges = dw_pos_ranges(K, cin, cout, vb, kWavesBf16, n_out);
   const int groups = static_cast<int>(ceil_div(K, kWaves * kDwPosKPW));
-  const int ct = cin / 16, ot = cout / 64;
+  const int ct = cin / 16, ot = cout / (16 * vb);
   if (n_in > 0 && n_out > 0) {
-    hipLaunchKernelGGL((conv_dw_pos_bf16_kernel<kDwPosKPW, kWavesBf16>),
-                       dim3(static_cast<unsigned>(ranges * ct * ot * groups)), dim3(kThreads), 0, s,
-                       x, n_in, cin, gy, cout, nbr, out_order, n_out, K, ranges, ct, ot, partial);
+    const dim3 grid(static_cast<unsigned>(ranges * ct * ot * groups));
+    if (vb == 4)
+      hipLaunchKernelGGL((conv_dw_pos_bf16_kernel<4, kDwPosKPW, kWavesBf16>), grid,
+                         dim3(kThreads), 0, s, x, n_in, cin, gy, cout, nbr, out_order, n_out, K,
+                         ranges, ct, ot, partial);
+    else
+      hipLaunchKernelGGL((conv_dw_pos_bf16_kernel<2, kDwPosKPW, kWavesBf16>), grid,
+                         dim3(kThreads), 0, s, x, n_in, cin, gy, cout, nbr, out_order, n_out, K,
+                         ranges, ct, ot, partial);
     RHIP_LAUNCH_CHECK();
   }
   const int64_t ne = static_cast<int64_t>(K) * cin * cout;
@@ -1890,8 +1899,7 @@ extern "C" int rhip_conv_backward_weight_rows(
       throw Error(RHIP_ERR_UNSUPPORTED,
                   "rhip_conv_backward_weight_rows: bf16 with 16 or 32 input and output "
                   "channels, or at least 20 offsets with input channels a multiple of 16 "
-                  "and output channels a multiple of 32 (fp32) or 64 (bf16) (use "
-                  "rhip_conv_backward_weight)");
+                  "and output channels a multiple of 32 (use rhip_conv_backward_weight)");
     RHIP_CHECK_ARG(grad_w != nullptr, "grad_w is null");
     RHIP_CHECK_ARG(n_in == 0 || n_out == 0 || (x && grad_y && nbr),
                    "x, grad_y and nbr are required");
@@ -1902,7 +1910,7 @@ extern "C" int rhip_conv_backward_weight_rows(
     if (dtype == RHIP_F32)
       run_dw_pos(static_cast<const float *>(x), n_in, cin, static_cast<const float *>(grad_y),
                  n_out, cout, K, nbr, out_order, w.partial, static_cast<float *>(grad_w), stream);
-    else if (!dw_narrow_bf16(dtype, cin, cout))
+    else if (dw_pos_supported(dtype, cin, cout, K, n_in, n_out))
       run_dw_pos_bf16(static_cast<const __bf16 *>(x), n_in, cin,
                       static_cast<const __bf16 *>(grad_y), n_out, cout, K, nbr, out_order,
                       w.partial, static_cast<__bf16 *>(grad_w), stream);

@@ -282,7 +282,7 @@ def test_weight_gradient_from_neighbour_table_rejects_other_shapes():
     c, _, _ = oracle.insert_and_map(random_coords(rng, 500, 3, 8))
     _, _, km = gpu_tables_and_map(c, c, oracle.region_offsets(3, 3), same=True)
     x = torch.zeros(km.n_in, 64, dtype=torch.bfloat16, device=DEV)
-    gy = torch.zeros(km.n_out, 32, dtype=torch.bfloat16, device=DEV)
+    gy = torch.zeros(km.n_out, 48, dtype=torch.bfloat16, device=DEV)
     with pytest.raises(RuntimeError, match="16 or 32"):
         abi.conv_backward_weight_rows(x, gy, km, km.K)
     gy48 = torch.zeros(km.n_out, 48, dtype=torch.float32, device=DEV)
