@@ -183,21 +183,22 @@ __global__ __launch_bounds__(kMapBlock) void invert_order_kernel(
     pos[order[j]] = static_cast<int32_t>(j);
 }
 
-// Sort key of a neighbour mask: the mask itself for K <= 16; else the
-// neighbour count, largest first, then a 16-bit hash of the mask (equal
-// masks get equal keys; unequal ones rarely collide, which only costs MFMA
-// fill, never correctness). Largest first puts the tiles with the most
-// stages at the front of the convolution grid, so the grid does not end on
-// a few long workgroups.
+// Sort key of a neighbour mask: the mask itself for K <= 16; else 22 bits,
+// the neighbour count (largest first, 127 and more alike) above a 15-bit
+// hash of the mask (equal masks get equal keys; unequal ones rarely
+// collide, which only costs MFMA fill, never correctness). Largest first
+// puts the tiles with the most stages at the front of the convolution grid,
+// so the grid does not end on a few long workgroups; 22 bits sort in two
+// 11-bit passes.
 __device__ __forceinline__ uint32_t mask_key(uint64_t m0, uint64_t m1, int K) {
   if (K <= kKeyBits)
     return static_cast<uint32_t>(m0);
-  const uint32_t count = static_cast<uint32_t>(__popcll(m0) + __popcll(m1)); // <= 128
-  return ((128u - count) << 16) |
-         static_cast<uint32_t>(mix64(m0 ^ mix64(m1 ^ 0x9e3779b97f4a7c15ull)) >> 48);
+  const uint32_t count = min(127u, static_cast<uint32_t>(__popcll(m0) + __popcll(m1)));
+  return ((127u - count) << 15) |
+         static_cast<uint32_t>(mix64(m0 ^ mix64(m1 ^ 0x9e3779b97f4a7c15ull)) >> 49);
 }
 // Bits of mask_key for K offsets.
-static int mask_key_bits(int K) { return K <= kKeyBits ? K : kKeyBits + 8; }
+static int mask_key_bits(int K) { return K <= kKeyBits ? K : 22; }
 
 __global__ __launch_bounds__(kMapBlock) void mask_key_kernel(
     const int32_t *__restrict__ nbr_sp, int64_t n, int K,

@@ -46,7 +46,8 @@ def _mix64(k):
 
 def _mask_keys(table):
     """Sort key of each column's neighbour mask: the mask for K <= 16, else
-    (128 - neighbour count) above a 16-bit hash of its two 64-bit words."""
+    (127 - min(neighbour count, 127)) above a 15-bit hash of its two 64-bit
+    words."""
     K = table.shape[0]
     hit = (table >= 0).astype(np.uint64)
     m = np.zeros((2, table.shape[1]), np.uint64)
@@ -54,10 +55,10 @@ def _mask_keys(table):
         m[k // 64] |= hit[k] << np.uint64(k % 64)
     if K <= 16:
         return m[0]
-    count = (np.bitwise_count(m[0]) + np.bitwise_count(m[1])).astype(np.uint64)
+    count = np.minimum(np.bitwise_count(m[0]) + np.bitwise_count(m[1]), 127).astype(np.uint64)
     with np.errstate(over="ignore"):
-        h = _mix64(m[0] ^ _mix64(m[1] ^ np.uint64(0x9e3779b97f4a7c15))) >> np.uint64(48)
-    return ((np.uint64(128) - count) << np.uint64(16)) | h
+        h = _mix64(m[0] ^ _mix64(m[1] ^ np.uint64(0x9e3779b97f4a7c15))) >> np.uint64(49)
+    return ((np.uint64(127) - count) << np.uint64(15)) | h
 
 
 def _check_tables(km, tin, tout):
