@@ -1363,8 +1363,9 @@ static void launch_os(const T *x, int cred, const T *wt, int ncols,
 // Launch shape, measured on MI355X. One 16-row group per wave (64 rows per
 // workgroup: more workgroups in flight hide the gather latency better than
 // more rows per wave) and the widest channel chunk the reduction width
-// allows. fp32 (config 2, C64): a register budget for 6 waves per SIMD, one
-// stage per barrier. bf16 (config-5 stages): 8 waves per SIMD and one stage
+// allows. fp32 (config 2, C64): a register budget for 8 waves per SIMD (62
+// registers: 356-360 us against 368-370 with the 6-wave budget's 64, in the
+// largest-first tile order), one stage per barrier. bf16 (config-5 stages): 8 waves per SIMD and one stage
 // per barrier at 64 columns; 128-column tiles (4 waves per SIMD, 2 stages
 // per barrier) for 128 and 256 channels; 4 stages per barrier for 32-channel
 // chunks (6 waves per SIMD at 64 columns, where 8 do not fit the registers).
@@ -1380,7 +1381,7 @@ template <typename T, int NT, int CSUB>
 static void launch_shape(const T *x, int cred, const T *wt, int ncols, const float *bias,
                          const int32_t *nbr, int64_t n_rows, int K, const int32_t *order, T *y,
                          int splits, float *partial, hipStream_t s) {
-  constexpr int W = kIsF32<T> ? 6 : (NT >= 128 ? 4 : (CSUB == 1 && NT >= 64 ? 6 : 8));
+  constexpr int W = kIsF32<T> ? 8 : (NT >= 128 ? 4 : (CSUB == 1 && NT >= 64 ? 6 : 8));
   constexpr int G = kIsF32<T> ? 1 : (NT >= 128 ? 2 : (CSUB == 1 ? 4 : 1));
   launch_os<T, NT, 1, CSUB, W, G>(x, cred, wt, ncols, bias, nbr, n_rows, K, order, y, splits,
                                   partial, s);
