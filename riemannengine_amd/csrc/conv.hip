@@ -144,14 +144,23 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(WAVES)
   const int col0 = blockIdx.y * NT;
 
   // Offsets with any neighbour in each 16-row group: lanes of group g test
-  // offset k0+g for the 16 rows; one ballot covers four offsets.
+  // offset k0+g for the 16 rows; one ballot covers four offsets. For
+  // K <= 4*kRegQ the bf16 kernels keep the indices in registers (lane
+  // (i16, g) holds row i16's under offsets g, g+4, ...): their loads issue
+  // back to back, and a stage later takes its rows' indices from them with
+  // ds_bpermute instead of a second global load. Measured on MI355X, config
+  // 2 forward: bf16 115-123 us against 122-131; the fp32 kernel, whose
+  // 8-wave budget has no room for the 8 registers, spills and loses (446
+  // against 351 us), so it keeps the global loads.
+  constexpr int kRegQ = 8;
+  constexpr bool kRegIdx = !std::is_same<T, float>::value;
+  const bool kreg = kRegIdx && K <= 4 * kRegQ;
+  int32_t kidx[RG][kRegQ];
 #pragma unroll
   for (int r = 0; r < RG; ++r) {
     const int64_t pos = tile0 + (wv * RG + r) * 16 + i16;
     uint32_t words[kMaskWords] = {0u, 0u, 0u, 0u};
-    for (int k0 = 0; k0 < K; k0 += 4) {
-      const int k = k0 + g;
-      const int32_t v = (k < K && pos < n_rows) ? nbr[k * n_rows + pos] : -1;
+    auto note = [&](int k0, int32_t v) {
       const uint64_t bal = __ballot(v >= 0);
 #pragma unroll
       for (int gg = 0; gg < 4; ++gg) {
@@ -159,6 +168,26 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(WAVES)
           const int kk = k0 + gg;
           words[kk >> 5] |= 1u << (kk & 31);
         }
+      }
+    };
+    if (kreg) {
+      const bool in = pos < n_rows;
+      const int64_t pc = in ? pos : n_rows - 1;
+#pragma unroll
+      for (int q = 0; q < kRegQ; ++q) {
+        const int k = 4 * q + g;
+        const bool ok = in && k < K;
+        // a mask, not a select of the load: the loads issue back to back
+        kidx[r][q] = nbr[(k < K ? k : K - 1) * n_rows + pc] | (ok ? 0 : -1);
+      }
+#pragma unroll
+      for (int q = 0; q < kRegQ; ++q)
+        if (4 * q < K)
+          note(4 * q, kidx[r][q]);
+    } else {
+      for (int k0 = 0; k0 < K; k0 += 4) {
+        const int k = k0 + g;
+        note(k0, (k < K && pos < n_rows) ? nbr[k * n_rows + pos] : -1);
       }
     }
     if (lane == 0) {
@@ -217,7 +246,17 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(WAVES)
 #pragma unroll
       for (int r = 0; r < RG; ++r) {
         const int64_t pos = pos0 + r * 16;
-        const int32_t v = nbr[kj[j] * n_rows + (pos < n_rows ? pos : n_rows - 1)];
+        int32_t v;
+        if (kreg) { // row i16's index under kj from lane (kj % 4, i16)
+          const int q = kj[j] >> 2;
+          int32_t held = kidx[r][0];
+#pragma unroll
+          for (int qq = 1; qq < kRegQ; ++qq)
+            held = qq == q ? kidx[r][qq] : held;
+          v = __builtin_amdgcn_ds_bpermute(((kj[j] & 3) * 16 + i16) * 4, held);
+        } else {
+          v = nbr[kj[j] * n_rows + (pos < n_rows ? pos : n_rows - 1)];
+        }
         const bool act = s0 + j < s_end && pos < n_rows &&
                          ((smask[wv * RG + r][kj[j] >> 5] >> (kj[j] & 31)) & 1u);
         idx[j][r] = v | (act ? 0 : -1); // a mask, not a select of the load
