@@ -264,9 +264,9 @@ int rhip_conv_backward_weight(const void *x, int64_t n_in, int32_t cin,
  * row is read once per group of offsets rather than once per pair, and the
  * X rows that neighbouring positions share are read once per position
  * range. Supported: bf16 with 16 or 32 input and output channels, and at
- * least 20 offsets with input channels a multiple of 16 and output channels
- * a multiple of 32 (each of x, grad_y and the table under 2 GiB); other
- * shapes return
+ * most 8 or at least 20 offsets with input channels a multiple of 16 and
+ * output channels a multiple of 32 (each of x, grad_y and the table under
+ * 2 GiB); other shapes return
  * RHIP_ERR_UNSUPPORTED, for which rhip_conv_backward_weight is the
  * fallback. Workspace as for rhip_conv_workspace_bytes.
  * Replaces the dW half of MmBackward (engine/nn/conv.cpp:62), like

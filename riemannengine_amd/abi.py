@@ -437,7 +437,8 @@ def conv_weight_grad(x: torch.Tensor, grad_y: torch.Tensor, kmap: KernelMap,
 def conv_backward_weight_rows(x: torch.Tensor, grad_y: torch.Tensor, kmap: KernelMap,
                               K: int) -> torch.Tensor:
     """dW from the kernel map's neighbour table (bf16 with 16 or 32 channels;
-    K >= 20 with cin % 16 == 0 and cout % 32 == 0; other shapes raise)."""
+    K <= 8 or K >= 20 with cin % 16 == 0 and cout % 32 == 0; other shapes
+    raise)."""
     _require_cuda(x, "x")
     dt = _dtype_code(x.dtype)
     x, grad_y = x.contiguous(), grad_y.to(x.dtype).contiguous()

@@ -1626,11 +1626,18 @@ constexpr int kDwRowsBlocks = 256;
 // instead of dealt segments 481, 4 offsets per wave 434-444); config 4
 // (233k rows, 81 offsets, C32->32, 128 ranges) 217 against 242; config 1
 // (52k rows, C16->32, 256 ranges) 35 against 46. Stencils of fewer than 20
-// offsets leave most of a wave's offset slots empty and stay on the pair
-// list (config 3's 2^3 transposed map, C128->64: 118 us against 71).
+// offsets would leave most of 7 offset slots per wave empty (config 3's 2^3
+// transposed map, C128->64: 118 us against the pair list's 71); stencils of
+// at most 8 offsets take 2 offsets per wave instead (config 3, kernel +
+// reduce against the pair list: fp32 down 45 us against 70, up 58 against
+// 71; bf16 down 32 against 48, up 45 against 52), and 9 to 19 offsets stay
+// on the pair list.
 constexpr int kDwPosKPW = 7;
+constexpr int kDwPosKPWSmall = 2;
 constexpr int kDwPosSlots = 4;
 constexpr int kDwPosMinK = 20;
+constexpr int kDwPosMaxKSmall = 4 * kDwPosKPWSmall;
+static int dw_pos_kpw(int K) { return K <= kDwPosMaxKSmall ? kDwPosKPWSmall : kDwPosKPW; }
 constexpr int64_t kBufMaxBytes = (int64_t(1) << 31) - 256; // buffer offsets stay below kBufOob
 
 template <int VB> constexpr int kDwPosWaves = VB == 4 ? 2 : 3;
@@ -1646,7 +1653,7 @@ template <int VB> constexpr int kDwPosWaves = VB == 4 ? 2 : 3;
 static bool dw_pos_supported(int32_t dtype, int cin, int cout, int K, int64_t n_in,
                              int64_t n_out) {
   const int64_t s = dtype == RHIP_F32 ? 4 : 2;
-  return K >= kDwPosMinK && cin % 16 == 0 && cout % 32 == 0 &&
+  return (K >= kDwPosMinK || K <= kDwPosMaxKSmall) && cin % 16 == 0 && cout % 32 == 0 &&
          n_in * cin * s <= kBufMaxBytes && n_out * cout * s <= kBufMaxBytes &&
          static_cast<int64_t>(K) * n_out * 4 <= kBufMaxBytes;
 }
@@ -1660,16 +1667,20 @@ static bool dw_rows_supported(int32_t dtype, int cin, int cout, int K, int64_t n
   return dw_narrow_bf16(dtype, cin, cout) || dw_pos_supported(dtype, cin, cout, K, n_in, n_out);
 }
 
-// Ranges of the fp32 kernel: a multiple of 8 (one share per XCD), one round
-// of resident workgroups (256 CUs x the waves per SIMD: each workgroup puts
-// one wave on every SIMD of its CU), at most kDwRowsBlocks (the partial
-// slots of the workspace), at least 4 segments of 64 positions each.
-static int dw_pos_ranges(int K, int cin, int cout, int vb, int waves, int64_t n_out) {
-  const int groups = static_cast<int>(ceil_div(K, kWaves * kDwPosKPW));
+// Ranges of the neighbour-table kernels: a multiple of 8 (one share per
+// XCD), one round of resident workgroups (256 CUs x the waves per SIMD:
+// each workgroup puts one wave on every SIMD of its CU), at most
+// kDwRowsBlocks (the partial slots of the workspace), at least min_segs
+// segments of 64 positions each (4 for fp32; 16 for bf16, whose small maps
+// lose more to partial slots than they gain from a full round: config 3's
+// down map 32 us at 32 ranges, 38 at 128).
+static int dw_pos_ranges(int K, int cin, int cout, int vb, int waves, int64_t n_out,
+                         int min_segs) {
+  const int groups = static_cast<int>(ceil_div(K, kWaves * dw_pos_kpw(K)));
   const int units = (cin / 16) * (cout / (16 * vb)) * groups;
   int64_t r = std::max<int64_t>(kXcds, (256 * waves / units) / kXcds * kXcds);
   const int64_t segs = ceil_div(std::max<int64_t>(n_out, 1), 64);
-  r = std::min<int64_t>(r, std::max<int64_t>(kXcds, segs / 4 / kXcds * kXcds));
+  r = std::min<int64_t>(r, std::max<int64_t>(kXcds, segs / min_segs / kXcds * kXcds));
   return static_cast<int>(std::min<int64_t>(r, kDwRowsBlocks));
 }
 
@@ -1678,21 +1689,28 @@ static void run_dw_pos_bf16(const __bf16 *x, int64_t n_in, int cin, const __bf16
                             int64_t n_out, int cout, int K, const int32_t *nbr,
                             const int32_t *out_order, float *partial, __bf16 *dw,
                             hipStream_t s) {
-  constexpr int kWavesBf16 = 2;
+  const bool small = K <= kDwPosMaxKSmall;
+  const int waves = small ? 4 : 2;
   const int vb = cout % 64 == 0 ? 4 : 2;
-  const int ranges = dw_pos_ranges(K, cin, cout, vb, kWavesBf16, n_out);
-  const int groups = static_cast<int>(ceil_div(K, kWaves * kDwPosKPW));
+  const int ranges = dw_pos_ranges(K, cin, cout, vb, waves, n_out, 16);
+  const int groups = static_cast<int>(ceil_div(K, kWaves * dw_pos_kpw(K)));
   const int ct = cin / 16, ot = cout / (16 * vb);
   if (n_in > 0 && n_out > 0) {
     const dim3 grid(static_cast<unsigned>(ranges * ct * ot * groups));
-    if (vb == 4)
-      hipLaunchKernelGGL((conv_dw_pos_bf16_kernel<4, kDwPosKPW, kWavesBf16>), grid,
-                         dim3(kThreads), 0, s, x, n_in, cin, gy, cout, nbr, out_order, n_out, K,
-                         ranges, ct, ot, partial);
+    auto go = [&](auto nb, auto kpw, auto w) {
+      hipLaunchKernelGGL((conv_dw_pos_bf16_kernel<decltype(nb)::value, decltype(kpw)::value,
+                                                  decltype(w)::value>),
+                         grid, dim3(kThreads), 0, s, x, n_in, cin, gy, cout, nbr, out_order, n_out,
+                         K, ranges, ct, ot, partial);
+    };
+    using I2 = std::integral_constant<int, 2>;
+    using I4 = std::integral_constant<int, 4>;
+    using IK = std::integral_constant<int, kDwPosKPW>;
+    using IKS = std::integral_constant<int, kDwPosKPWSmall>;
+    if (small)
+      vb == 4 ? go(I4{}, IKS{}, I4{}) : go(I2{}, IKS{}, I4{});
     else
-      hipLaunchKernelGGL((conv_dw_pos_bf16_kernel<2, kDwPosKPW, kWavesBf16>), grid,
-                         dim3(kThreads), 0, s, x, n_in, cin, gy, cout, nbr, out_order, n_out, K,
-                         ranges, ct, ot, partial);
+      vb == 4 ? go(I4{}, IK{}, I2{}) : go(I2{}, IK{}, I2{});
     RHIP_LAUNCH_CHECK();
   }
   const int64_t ne = static_cast<int64_t>(K) * cin * cout;
@@ -1706,21 +1724,31 @@ static void run_dw_pos_bf16(const __bf16 *x, int64_t n_in, int cin, const __bf16
 static void run_dw_pos(const float *x, int64_t n_in, int cin, const float *gy, int64_t n_out,
                        int cout, int K, const int32_t *nbr, const int32_t *out_order,
                        float *partial, float *dw, hipStream_t s) {
+  const bool small = K <= kDwPosMaxKSmall;
   const int vb = cout % 64 == 0 ? 4 : 2;
-  const int waves = vb == 4 ? kDwPosWaves<4> : kDwPosWaves<2>;
-  const int ranges = dw_pos_ranges(K, cin, cout, vb, waves, n_out);
-  const int groups = static_cast<int>(ceil_div(K, kWaves * kDwPosKPW));
+  const int waves = small ? 3 : (vb == 4 ? kDwPosWaves<4> : kDwPosWaves<2>);
+  const int ranges = dw_pos_ranges(K, cin, cout, vb, waves, n_out, 4);
+  const int groups = static_cast<int>(ceil_div(K, kWaves * dw_pos_kpw(K)));
   const int ct = cin / 16, ot = cout / (16 * vb);
   if (n_in > 0 && n_out > 0) {
     const dim3 grid(static_cast<unsigned>(ranges * ct * ot * groups));
-    if (vb == 4)
-      hipLaunchKernelGGL((conv_dw_pos_kernel<4, kDwPosKPW, kDwPosSlots, kDwPosWaves<4>>), grid,
-                         dim3(kThreads), 0, s, x, n_in, cin, gy, cout, nbr, out_order, n_out, K,
-                         ranges, ct, ot, partial);
+    auto go = [&](auto v, auto kpw, auto w) {
+      hipLaunchKernelGGL((conv_dw_pos_kernel<decltype(v)::value, decltype(kpw)::value, kDwPosSlots,
+                                             decltype(w)::value>),
+                         grid, dim3(kThreads), 0, s, x, n_in, cin, gy, cout, nbr, out_order, n_out,
+                         K, ranges, ct, ot, partial);
+    };
+    using I2 = std::integral_constant<int, 2>;
+    using I3 = std::integral_constant<int, 3>;
+    using I4 = std::integral_constant<int, 4>;
+    using IK = std::integral_constant<int, kDwPosKPW>;
+    using IKS = std::integral_constant<int, kDwPosKPWSmall>;
+    using W4 = std::integral_constant<int, kDwPosWaves<4>>;
+    using W2 = std::integral_constant<int, kDwPosWaves<2>>;
+    if (small)
+      vb == 4 ? go(I4{}, IKS{}, I3{}) : go(I2{}, IKS{}, I3{});
     else
-      hipLaunchKernelGGL((conv_dw_pos_kernel<2, kDwPosKPW, kDwPosSlots, kDwPosWaves<2>>), grid,
-                         dim3(kThreads), 0, s, x, n_in, cin, gy, cout, nbr, out_order, n_out, K,
-                         ranges, ct, ot, partial);
+      vb == 4 ? go(I4{}, IK{}, W4{}) : go(I2{}, IK{}, W2{});
     RHIP_LAUNCH_CHECK();
   }
   const int64_t ne = static_cast<int64_t>(K) * cin * cout;
@@ -1938,8 +1966,9 @@ extern "C" int rhip_conv_backward_weight_rows(
     if (!dw_rows_supported(dtype, cin, cout, K, n_in, n_out))
       throw Error(RHIP_ERR_UNSUPPORTED,
                   "rhip_conv_backward_weight_rows: bf16 with 16 or 32 input and output "
-                  "channels, or at least 20 offsets with input channels a multiple of 16 "
-                  "and output channels a multiple of 32 (use rhip_conv_backward_weight)");
+                  "channels, or at most 8 or at least 20 offsets with input channels a "
+                  "multiple of 16 and output channels a multiple of 32 (use "
+                  "rhip_conv_backward_weight)");
     RHIP_CHECK_ARG(grad_w != nullptr, "grad_w is null");
     RHIP_CHECK_ARG(n_in == 0 || n_out == 0 || (x && grad_y && nbr),
                    "x, grad_y and nbr are required");

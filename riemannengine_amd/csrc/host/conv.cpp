@@ -95,8 +95,8 @@ struct HipConvolutionFunction : public torch::autograd::Function<HipConvolutionF
     if (ctx->needs_input_grad(1)) {
       gw = torch::empty_like(w);
       // dW from the neighbour table where the library has a kernel for the
-      // shape (K >= 20 with C_in % 16 and C_out % 32; narrow bf16), else
-      // from the pair list
+      // shape (K <= 8 or K >= 20 with C_in % 16 and C_out % 32; narrow bf16),
+      // else from the pair list
       int rc = rhip_conv_backward_weight_rows(
           x.data_ptr(), n_in, static_cast<int32_t>(cin), gy.data_ptr(), n_out,
           static_cast<int32_t>(cout), K, nbr.data_ptr<int32_t>(),

@@ -166,9 +166,9 @@ def test_weight_gradient_from_neighbour_table_f32(cin, cout):
 
 def test_weight_gradient_from_neighbour_table_f32_strided_4d_and_tiny():
     """fp32 over a 3^3 stride-2 map and its transpose (n_in != n_out), an
-    81-offset 4D map (three offset groups), and maps smaller than one
-    64-position segment. A 2^3 map (8 offsets) stays on the pair list: the
-    table entry rejects it and the layer dispatch falls back."""
+    81-offset 4D map (three offset groups), maps smaller than one
+    64-position segment, and 2^3 stride-2 maps (8 offsets: 2 per wave) in
+    fp32 and bf16."""
     rng = np.random.default_rng(31)
     c, _, _ = oracle.insert_and_map(random_coords(rng, 20000, 3, 30))
     tin = abi.hash_build(to_dev(c))
@@ -177,12 +177,21 @@ def test_weight_gradient_from_neighbour_table_f32_strided_4d_and_tiny():
     _rows_check(km, 64, 128, seed=1, tag="down", dtype=torch.float32)
     _rows_check(km.swapped(), 128, 64, seed=2, tag="up", dtype=torch.float32)
     km8 = abi.kernel_map(tin, tout, to_dev(oracle.region_offsets(3, 2)))
-    x8 = torch.randn(km8.n_in, 64, device=DEV)
-    gy8 = torch.randn(km8.n_out, 64, device=DEV)
-    with pytest.raises(RuntimeError, match="at least 20 offsets"):
-        abi.conv_backward_weight_rows(x8, gy8, km8, km8.K)
-    assert torch.equal(abi.conv_weight_grad(x8, gy8, km8, km8.K),
-                       abi.conv_backward_weight(x8, gy8, km8, km8.K))
+    _rows_check(km8, 64, 128, seed=6, tag="2^3 down", dtype=torch.float32)
+    _rows_check(km8.swapped(), 128, 64, seed=7, tag="2^3 up", dtype=torch.float32)
+    _rows_check(km8, 64, 128, seed=8, tag="2^3 down bf16")
+    _rows_check(km8.swapped(), 128, 32, seed=9, tag="2^3 up bf16")
+    # 13 offsets (5^3 cross) stay on the pair list: the table entry rejects
+    # them and the layer dispatch falls back
+    c13 = oracle.region_offsets(3, 5, region="cross")
+    assert c13.shape[0] == 13
+    km13 = abi.kernel_map(tin, tin, to_dev(c13))
+    x13 = torch.randn(km13.n_in, 64, device=DEV)
+    gy13 = torch.randn(km13.n_out, 64, device=DEV)
+    with pytest.raises(RuntimeError, match="at most 8 or at least 20 offsets"):
+        abi.conv_backward_weight_rows(x13, gy13, km13, km13.K)
+    assert torch.equal(abi.conv_weight_grad(x13, gy13, km13, km13.K),
+                       abi.conv_backward_weight(x13, gy13, km13, km13.K))
     c4, _, _ = oracle.insert_and_map(random_coords(rng, 6000, 4, 7, batch=1))
     _, _, km4 = gpu_tables_and_map(c4, c4, oracle.region_offsets(4, 3), same=True)
     _rows_check(km4, 16, 64, seed=3, tag="3^4", dtype=torch.float32)
