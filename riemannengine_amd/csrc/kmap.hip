@@ -188,8 +188,8 @@ __global__ __launch_bounds__(kMapBlock) void invert_order_kernel(
 // hash of the mask (equal masks get equal keys; unequal ones rarely
 // collide, which only costs MFMA fill, never correctness). Largest first
 // puts the tiles with the most stages at the front of the convolution grid,
-// so the grid does not end on a few long workgroups; 22 bits sort in two
-// 11-bit passes.
+// so the grid does not end on a few long workgroups; 22 bits sort in three
+// 8-bit passes.
 __device__ __forceinline__ uint32_t mask_key(uint64_t m0, uint64_t m1, int K) {
   if (K <= kKeyBits)
     return static_cast<uint32_t>(m0);

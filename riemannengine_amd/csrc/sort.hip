@@ -1,8 +1,11 @@
 // Stable device radix sorts of (key, int32 value) pairs, used by the hash
 // table (locality order), the kernel map (neighbour-mask order) and pooling
-// (grouping rows by output). Least-significant-digit first with 8- to 11-bit
+// (grouping rows by output). Least-significant-digit first with 8- or 9-bit
 // digits: the fewest passes the key bits allow, then the narrowest digit for
-// that many passes (26 bits: 3 passes of 9); three kernels per pass:
+// that many passes (26 bits: 3 passes of 9; 22 bits: 3 of 8). Wider digits
+// cost more than they save: the tile scan runs one workgroup per digit, and
+// on MI355X (410k keys) an 11-bit pass takes about 42 us against 21 for an
+// 8-bit one. Three kernels per pass:
 //
 //   radix_hist_kernel     one wave per tile of 1024 keys: the tile's digit
 //                         histogram, written tile-major [tiles][256];
@@ -27,7 +30,7 @@
 namespace rhip {
 namespace {
 
-constexpr int kMaxRadixBits = 11;
+constexpr int kMaxRadixBits = 9;
 constexpr int kSortItems = 16;
 constexpr int kSortTile = kWave * kSortItems;
 
@@ -207,7 +210,7 @@ void sort_run(void *tmp, size_t tmp_bytes, const K *kin, K *kout, const int32_t 
   constexpr int kBits = 8 * static_cast<int>(sizeof(K));
   end_bit = end_bit < 1 ? 1 : (end_bit > kBits ? kBits : end_bit);
   const int passes = (end_bit + kMaxRadixBits - 1) / kMaxRadixBits;
-  const int bits = std::max(8, (end_bit + passes - 1) / passes); // 8..11
+  const int bits = std::max(8, (end_bit + passes - 1) / passes); // 8 or 9
   const int64_t tiles = ceil_div(n, kSortTile);
   // pass p writes the caller's output when (passes - 1 - p) is even, the
   // scratch pair otherwise, so the last pass lands in the output
@@ -234,12 +237,8 @@ void sort_run(void *tmp, size_t tmp_bytes, const K *kin, K *kout, const int32_t 
     };
     if (bits == 8)
       pass(std::integral_constant<int, 8>{});
-    else if (bits == 9)
-      pass(std::integral_constant<int, 9>{});
-    else if (bits == 10)
-      pass(std::integral_constant<int, 10>{});
     else
-      pass(std::integral_constant<int, 11>{});
+      pass(std::integral_constant<int, 9>{});
     src_k = dst_k;
     src_v = dst_v;
   }
