@@ -286,6 +286,25 @@ def test_weight_gradient_from_neighbour_table_bf16_wide_strided_4d_tiny_full():
     assert torch.equal(abi.conv_weight_grad(x, gy, kmf, kmf.K), rows)
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("cin,cout", [(256, 256), (128, 64), (96, 192)])
+def test_weight_gradient_from_neighbour_table_wide_channels(dtype, cin, cout):
+    """Many channel slices and output tiles per range (the grid's unit
+    decomposition, few ranges): the table kernels against the pair-list
+    kernel, which sums the same products in another order."""
+    rng = np.random.default_rng(cin + cout)
+    c, _, _ = oracle.insert_and_map(random_coords(rng, 12000, 3, 16))
+    _, _, km = gpu_tables_and_map(c, c, oracle.region_offsets(3, 3), same=True)
+    g = torch.Generator().manual_seed(cin)
+    x = torch.randn(km.n_in, cin, generator=g).to(dtype).to(DEV)
+    gy = torch.randn(km.n_out, cout, generator=g).to(dtype).to(DEV)
+    print(f"dW rows wide {dtype} {cin}->{cout} n={km.n_out}", flush=True)
+    rows = abi.conv_backward_weight_rows(x, gy, km, km.K)
+    pairs = abi.conv_backward_weight(x, gy, km, km.K)
+    assert_rel(rows.float().cpu().numpy(), pairs.float().cpu().numpy(),
+               1e-5 if dtype == torch.float32 else 1e-2, f"wide {cin}->{cout} rows vs pairs dW")
+
+
 def test_weight_gradient_from_neighbour_table_rejects_other_shapes():
     rng = np.random.default_rng(2)
     c, _, _ = oracle.insert_and_map(random_coords(rng, 500, 3, 8))
