@@ -180,7 +180,13 @@ def test_weight_gradient_from_neighbour_table_f32_strided_4d_and_tiny():
     _rows_check(km8, 64, 128, seed=6, tag="2^3 down", dtype=torch.float32)
     _rows_check(km8.swapped(), 128, 64, seed=7, tag="2^3 up", dtype=torch.float32)
     _rows_check(km8, 64, 128, seed=8, tag="2^3 down bf16")
-    _rows_check(km8.swapped(), 128, 32, seed=9, tag="2^3 up bf16")
+    xb, gyb, _ = _rows_check(km8.swapped(), 128, 32, seed=9, tag="2^3 up bf16")
+    # the layer dispatch keeps a bf16 map of at most 8 offsets with fewer than
+    # 2 pairs per output row (the transposed map: one each) on the pair list
+    up8 = km8.swapped()
+    assert up8.n_pairs < 2 * up8.n_out
+    assert torch.equal(abi.conv_weight_grad(xb, gyb, up8, up8.K),
+                       abi.conv_backward_weight(xb, gyb, up8, up8.K))
     # 13 offsets (5^3 cross) stay on the pair list: the table entry rejects
     # them and the layer dispatch falls back
     c13 = oracle.region_offsets(3, 5, region="cross")
