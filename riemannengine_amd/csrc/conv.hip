@@ -9,19 +9,22 @@
 // MI355X design:
 //  * Forward and dX are one output-stationary implicit GEMM over the dense
 //    neighbour table of the kernel map, whose rows come grouped by neighbour
-//    mask (so a 16-row group rarely multiplies a missing neighbour). A
-//    256-thread workgroup owns 64 output rows (4 waves x one group of 16)
-//    and up to 64 columns. It walks only the offsets with a neighbour in its rows;
-//    for each it stages the weight slice in LDS with 16-byte copies from a
-//    [K][ncols][cred] copy of the weights (reduction axis contiguous), gathers
-//    each group's 16 neighbour rows straight into MFMA A-fragments (16-byte
-//    loads, zero for a missing neighbour) and accumulates every offset in
-//    registers. Each output row is written once: no atomics, no zero fill.
-//  * dW is a split-pair reduction over the per-offset pair lists: a
-//    workgroup streams one offset's pair range through double-buffered LDS
-//    (X and dY rows stored row-major with 16-byte writes), runs 16x16 MFMA
-//    tiles with pairs as the reduction axis (bf16 operands through LDS
-//    transpose reads) and adds its tile to an fp32 accumulator with atomics.
+//    mask (so a 16-row group rarely multiplies a missing neighbour):
+//    conv_os_kernel stages each active offset's weight slice in LDS and
+//    gathers the rows straight into MFMA operands; conv_fr_kernel keeps every
+//    offset's weights for its columns resident in LDS for the whole launch
+//    (large maps whose weights fit). Each output row is written once: no
+//    atomics, no zero fill.
+//  * Gathered rows are loaded in quad order (four consecutive lanes read 64
+//    contiguous bytes of one row, one L1 access) and moved to the MFMA layout
+//    with ds_bpermute.
+//  * dW has three kernels, all writing per-workgroup partial tiles that a
+//    second kernel adds in a fixed order (deterministic, no atomics):
+//    conv_dw_kernel over the per-offset pair lists (split-pair reduction),
+//    conv_dw_rows_kernel over the neighbour table for narrow bf16 layers, and
+//    the position-stationary conv_dw_pos_kernel / conv_dw_pos_bf16_kernel,
+//    which keep the tiles of up to 28 offsets in registers while they stream
+//    the output positions.
 //  * The reduction order inside an MFMA is a permutation of the reduced axis
 //    chosen so that each lane reads 16 contiguous bytes; A and B use the same
 //    permutation, so the sum is unchanged.
@@ -99,6 +102,47 @@ template <> __device__ __forceinline__ __bf16 from_f32<__bf16>(float v) {
   return static_cast<__bf16>(v);
 }
 
+// Raw buffer loads (stride 0): a load at a byte offset at or past the
+// buffer's size returns zero without a memory access, so an absent row needs
+// no predicate. Kernels put such offsets at kBufOob, past every buffer they
+// make (host code keeps buffers below kBufMaxBytes).
+constexpr uint32_t kBufOob = 0x80000000u;
+constexpr int64_t kBufMaxBytes = (int64_t(1) << 31) - 256; // offsets stay below kBufOob
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void *p, int64_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), 0, static_cast<int>(bytes),
+                                           0x00020000);
+}
+
+// A value the optimiser cannot see through: keeps `load | mask` a bitwise
+// OR instead of a select that would become a branch around the load.
+__device__ __forceinline__ int32_t opaque(int32_t v) {
+  asm volatile("" : "+v"(v));
+  return v;
+}
+
+// off where keep is all ones, else kBufOob (keep is 0 or -1)
+__device__ __forceinline__ uint32_t pick_off(uint32_t off, int32_t keep) {
+  return (off & static_cast<uint32_t>(keep)) | (kBufOob & ~static_cast<uint32_t>(keep));
+}
+
+// Gathered rows in quad order. The L1 serves a vector load four lanes at a
+// time and looks up one cache line per distinct line among them; in the MFMA
+// operand layout (lane (i16, g): row i16, bytes 16g..16g+15 of a 64-byte
+// slice) the four lanes of a quad hold four rows, so every lane costs an
+// access. Loading lane 4m + c with row m's bytes 16c..16c+15 instead makes
+// each quad one 64-byte access (a quarter of the accesses); quad_to_mfma
+// then moves lane 4m + c's 16 bytes to lane 16c + m with four ds_bpermute.
+__device__ __forceinline__ int quad_src(int lane) { return (4 * (lane & 15) + (lane >> 4)) * 4; }
+
+__device__ __forceinline__ v4u quad_to_mfma(const v4u &v, int src) {
+  v4u o;
+#pragma unroll
+  for (int d = 0; d < 4; ++d)
+    o[d] = static_cast<uint32_t>(__builtin_amdgcn_ds_bpermute(src, static_cast<int32_t>(v[d])));
+  return o;
+}
+
 
 // ------------------------------------------------ output-stationary GEMM
 //
@@ -110,7 +154,7 @@ template <> __device__ __forceinline__ __bf16 from_f32<__bf16>(float v) {
 // neighbour indices, then their weight chunks (to G LDS slots) and gathered
 // rows (to registers) are all in flight together, so a group costs about
 // two memory latencies and two barriers however many stages it holds.
-template <typename T, int NT, int RG, int CSUB, int G, int WAVES = 1>
+template <typename T, int NT, int RG, int CSUB, int G, int WAVES = 1, bool COAL = true>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(WAVES))) void conv_os_kernel(
     const T *__restrict__ x, int cred, const T *__restrict__ wt, int ncols,
     const float *__restrict__ bias, const int32_t *__restrict__ nbr,
@@ -226,7 +270,11 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(WAVES)
     for (int nb = 0; nb < NB; ++nb)
       acc[r][nb] = v4f{0.f, 0.f, 0.f, 0.f};
 
-  const int64_t pos0 = tile0 + wv * RG * 16 + i16;
+  // the row this lane loads: row i16 in the MFMA layout, row lane / 4 when
+  // the rows are gathered in quad order (then moved with quad_to_mfma)
+  const int rsel = COAL ? (lane >> 2) : i16;
+  const int tsrc = quad_src(lane);
+  const int64_t pos0 = tile0 + wv * RG * 16 + rsel;
   for (int s0 = s_begin; s0 < s_end; s0 += G) {
     // The loads of a group are branch-free so that they issue back to back:
     // a stage past the end repeats the last one (its results are unused),
@@ -253,7 +301,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(WAVES)
 #pragma unroll
           for (int qq = 1; qq < kRegQ; ++qq)
             held = qq == q ? kidx[r][qq] : held;
-          v = __builtin_amdgcn_ds_bpermute(((kj[j] & 3) * 16 + i16) * 4, held);
+          v = __builtin_amdgcn_ds_bpermute(((kj[j] & 3) * 16 + rsel) * 4, held);
         } else {
           v = nbr[kj[j] * n_rows + (pos < n_rows ? pos : n_rows - 1)];
         }
@@ -279,7 +327,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(WAVES)
 #pragma unroll
         for (int sub = 0; sub < CSUB; ++sub) {
           const Frag v = M::load(x + static_cast<int64_t>(idx[j][r] < 0 ? 0 : idx[j][r]) * cred +
-                                 ccj[j] + sub * CH + g * EPL);
+                                 ccj[j] + sub * CH + (COAL ? (lane & 3) : g) * EPL);
           a[j][r][sub] = M::mask(v, idx[j][r] >= 0);
         }
 #pragma unroll
@@ -301,13 +349,19 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(WAVES)
       if (wave_act) { // uniform; false for j >= ns
 #pragma unroll
         for (int sub = 0; sub < CSUB; ++sub) {
+          Frag at[RG];
+#pragma unroll
+          for (int r = 0; r < RG; ++r)
+            at[r] = COAL ? __builtin_bit_cast(
+                               Frag, quad_to_mfma(__builtin_bit_cast(v4u, a[j][r][sub]), tsrc))
+                         : a[j][r][sub];
 #pragma unroll
           for (int nb = 0; nb < NB; ++nb) {
             const Frag b = *reinterpret_cast<const Frag *>(
                 &sB[j][(nb * 16 + i16) * LDW + sub * CH + g * EPL]);
 #pragma unroll
             for (int r = 0; r < RG; ++r)
-              M::mma(a[j][r][sub], b, acc[r][nb]);
+              M::mma(at[r], b, acc[r][nb]);
           }
         }
       }
@@ -376,6 +430,229 @@ __global__ __launch_bounds__(kThreads) void conv_os_generic_kernel(
     acc += bias[col];
   const int64_t o = order ? order[pos] : pos;
   y[o * ncols + col] = from_f32<T>(acc);
+}
+
+// ------------------------------------ resident-weight gather GEMM (bf16)
+//
+// The product of conv_os_kernel for bf16 maps whose weights for NT output
+// columns of every offset fit in LDS (4*KQ offset slots of NT rows of
+// cred + 8 elements): a workgroup copies them in once, and after that one
+// barrier its waves never wait for each other. A wave takes units of 32
+// output rows (two 16-row MFMA groups, which share every B-fragment read)
+// and walks the offsets with a neighbour among them, with the gathered rows
+// of D offsets in flight:
+//  * a unit's neighbour indices arrive one unit ahead, lane (i16, g) holding
+//    row i16 of group r under offsets g, g + 4, ...; a stage takes its rows'
+//    indices from the owning lanes with ds_bpermute;
+//  * rows are raw buffer loads: a missing neighbour, or a stage past the
+//    unit's last offset, reads past the buffer and gets zeros without a
+//    memory access, so the D slots always hold D stages' loads and the waits
+//    for them are static;
+//  * a group without a neighbour under an offset skips its MFMAs.
+// The grid is one workgroup per CU. XCD x takes chunks x, x + 8, ... of
+// consecutive units and runs every column slice of a chunk at the same time,
+// so the slices after the first find the chunk's rows in its L2.
+template <int NT, int KS, int KQ, int D, int WAVES, bool COAL = true>
+__global__ __launch_bounds__(WAVES *kWave) void conv_fr_kernel(
+    const __bf16 *__restrict__ x, int64_t n_x, const __bf16 *__restrict__ wt, int ncols,
+    const float *__restrict__ bias, const int32_t *__restrict__ nbr, int64_t n_rows, int K,
+    const int32_t *__restrict__ order, __bf16 *__restrict__ y) {
+  constexpr int C = 32 * KS; // reduction width
+  constexpr int LDW = C + 8; // LDS row stride (elements)
+  constexpr int NB = NT / 16;
+  constexpr int RG = 2; // 16-row groups per unit
+  constexpr int KL = KQ == 2 ? 8 : 28; // offset slots in LDS
+  __shared__ __align__(16) __bf16 sW[KL * NT * LDW];
+
+  const int slices = ncols / NT;
+  const int xcd = static_cast<int>(blockIdx.x % kXcds);
+  const int m = static_cast<int>(blockIdx.x / kXcds);
+  const int slots = static_cast<int>(gridDim.x / kXcds) / slices;
+  const int slice = m % slices, slot = m / slices;
+  if (slot >= slots)
+    return; // a workgroup the slices do not divide (uniform)
+  const int col0 = slice * NT;
+
+  { // this slice's weights, [k][n][c] with padded rows
+    constexpr int VPR = C / 8;
+    const int total = K * NT * VPR;
+    for (int i = threadIdx.x; i < total; i += WAVES * kWave) {
+      const int row = i / VPR, v = i - row * VPR;
+      const int k = row / NT, n = row - k * NT;
+      *reinterpret_cast<v4u *>(&sW[row * LDW + 8 * v]) = *reinterpret_cast<const v4u *>(
+          wt + (static_cast<int64_t>(k) * ncols + col0 + n) * C + 8 * v);
+    }
+  }
+  __syncthreads();
+
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const int i16 = lane & 15, g = lane >> 4;
+  const int64_t units = (n_rows + 31) / 32;
+  const int64_t chunk = static_cast<int64_t>(slots) * WAVES;
+  const int64_t ustep = kXcds * chunk;
+  int64_t u = xcd * chunk + slot * WAVES + wv;
+
+  const __amdgpu_buffer_rsrc_t rx = buf_rsrc(x, n_x * C * 2);
+  const __amdgpu_buffer_rsrc_t rn = buf_rsrc(nbr, static_cast<int64_t>(K) * n_rows * 4);
+  const __amdgpu_buffer_rsrc_t ro = buf_rsrc(order, order ? n_rows * 4 : 0);
+  const int tsrc = quad_src(lane);
+  float bv[NB];
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb)
+    bv[nb] = bias ? bias[col0 + nb * 16 + i16] : 0.f;
+
+  // an index vector, read with a wave-uniform subscript (v_movrels, no
+  // memory): an array would be demoted to scratch by the dynamic subscript
+  typedef int32_t IdxVec __attribute__((ext_vector_type(KQ)));
+  struct Idx {
+    IdxVec k[RG]; // row 16r + i16 under offset 4q + g (-1 = none)
+    int32_t orow; // output row of position 32u + lane % 32 (-1 past the end)
+  };
+  auto load_idx = [&](int64_t uu, Idx &I) {
+#pragma unroll
+    for (int r = 0; r < RG; ++r) {
+      const int64_t pos = uu * 32 + r * 16 + i16;
+      const int32_t in = opaque(static_cast<int32_t>((pos - n_rows) >> 63));
+#pragma unroll
+      for (int q = 0; q < KQ; ++q) {
+        const int k = 4 * q + g;
+        const int32_t keep = in & opaque(k < K ? -1 : 0);
+        I.k[r][q] = static_cast<int32_t>(__builtin_amdgcn_raw_buffer_load_b32(
+                        rn, pick_off(static_cast<uint32_t>((k * n_rows + pos) * 4), keep), 0,
+                        0)) |
+                    ~keep;
+      }
+    }
+    const int64_t pos = uu * 32 + (lane & 31);
+    const int32_t in = opaque(static_cast<int32_t>((pos - n_rows) >> 63));
+    if (order)
+      I.orow = static_cast<int32_t>(__builtin_amdgcn_raw_buffer_load_b32(
+                   ro, pick_off(static_cast<uint32_t>(pos * 4), in), 0, 0)) |
+               ~in;
+    else
+      I.orow = static_cast<int32_t>(pos) | ~in;
+  };
+
+  v4f acc[RG][NB];
+#pragma unroll
+  for (int r = 0; r < RG; ++r)
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+      acc[r][nb] = v4f{0.f, 0.f, 0.f, 0.f};
+
+  struct Rows {
+    v4u a[RG][KS];
+  };
+  auto run_unit = [&](const Idx &I) {
+    // offsets with a neighbour in each group (wave-uniform)
+    uint32_t mr[RG];
+#pragma unroll
+    for (int r = 0; r < RG; ++r) {
+      uint32_t w = 0;
+#pragma unroll
+      for (int q = 0; q < KQ; ++q) {
+        const uint64_t bal = __ballot(I.k[r][q] >= 0);
+#pragma unroll
+        for (int gg = 0; gg < 4; ++gg)
+          w |= (((bal >> (16 * gg)) & 0xffffull) != 0 ? 1u : 0u) << (4 * q + gg);
+      }
+      mr[r] = __builtin_amdgcn_readfirstlane(w);
+    }
+    uint32_t mi = 0;
+#pragma unroll
+    for (int r = 0; r < RG; ++r)
+      mi |= mr[r];
+    uint32_t mc = mi;
+    const int na = __builtin_popcount(mi);
+
+    // stage = the next offset of mi (none left: zeros without memory access)
+    auto issue = [&](Rows &R) {
+      const bool real = mi != 0;
+      const int k = real ? __builtin_ctz(mi) : 0;
+      mi &= mi - 1;
+      const int q = k >> 2;
+      const int src = ((k & 3) * 16 + (COAL ? (lane >> 2) : i16)) * 4;
+#pragma unroll
+      for (int r = 0; r < RG; ++r) {
+        const int32_t idx = __builtin_amdgcn_ds_bpermute(src, I.k[r][q]);
+        const int32_t keep = opaque(real ? ~(idx >> 31) : 0);
+        const uint32_t base = pick_off(
+            static_cast<uint32_t>(idx * (2 * C) + 16 * (COAL ? (lane & 3) : g)), keep);
+#pragma unroll
+        for (int s = 0; s < KS; ++s)
+          R.a[r][s] = __builtin_amdgcn_raw_buffer_load_b128(rx, base + 64 * s, 0, 0);
+      }
+    };
+    auto consume = [&](const Rows &R) {
+      const int k = __builtin_ctz(mc);
+      mc &= mc - 1;
+      v8bf b[KS][NB];
+#pragma unroll
+      for (int s = 0; s < KS; ++s)
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb)
+          b[s][nb] = *reinterpret_cast<const v8bf *>(
+              &sW[(k * NT + nb * 16 + i16) * LDW + 32 * s + 8 * g]);
+#pragma unroll
+      for (int r = 0; r < RG; ++r)
+        if ((mr[r] >> k) & 1u) { // wave-uniform
+#pragma unroll
+          for (int s = 0; s < KS; ++s) {
+            const v8bf a = __builtin_bit_cast(v8bf, COAL ? quad_to_mfma(R.a[r][s], tsrc) : R.a[r][s]);
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb)
+              acc[r][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b[s][nb], acc[r][nb], 0, 0, 0);
+          }
+        }
+    };
+
+    Rows R[D];
+#pragma unroll
+    for (int j = 0; j < D; ++j)
+      issue(R[j]);
+    for (int t = 0; t < na; t += D) {
+#pragma unroll
+      for (int j = 0; j < D; ++j) {
+        if (t + j < na)
+          consume(R[j]);
+        issue(R[j]);
+      }
+    }
+
+    // lane (i16, g) holds row 16r + 4g + e, column 16nb + i16
+#pragma unroll
+    for (int r = 0; r < RG; ++r)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int32_t o = __builtin_amdgcn_ds_bpermute((r * 16 + 4 * g + e) * 4, I.orow);
+        if (o >= 0) {
+          __bf16 *dst = y + static_cast<int64_t>(o) * ncols + col0 + i16;
+#pragma unroll
+          for (int nb = 0; nb < NB; ++nb)
+            dst[nb * 16] = static_cast<__bf16>(acc[r][nb][e] + bv[nb]);
+        }
+      }
+#pragma unroll
+    for (int r = 0; r < RG; ++r)
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb)
+        acc[r][nb] = v4f{0.f, 0.f, 0.f, 0.f};
+  };
+
+  // two index slots in alternation: no in-flight load is ever copied
+  Idx IA, IB;
+  load_idx(u, IA);
+  while (u < units) {
+    load_idx(u + ustep, IB);
+    run_unit(IA);
+    u += ustep;
+    if (u >= units)
+      break;
+    load_idx(u + ustep, IA);
+    run_unit(IB);
+    u += ustep;
+  }
 }
 
 // y[order[pos]][c] = sum over splits z (in order) of partial[z][pos][c]
@@ -938,13 +1215,6 @@ __global__ __launch_bounds__(1024) void conv_dw_rows_reduce_kernel(
 // list kernel reads one X row and one dY row per pair.
 // Each wave writes its offsets' tiles to the range's partial slot
 // [range][k][cin][cout]; conv_dw_rows_reduce_kernel sums the slots.
-constexpr uint32_t kBufOob = 0x80000000u; // past every buffer the kernel makes
-
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void *p, int64_t bytes) {
-  // raw buffer (stride 0): loads at byte offsets >= bytes return zero
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), 0, static_cast<int>(bytes),
-                                           0x00020000);
-}
 
 template <int VB> struct DyVec;
 template <> struct DyVec<1> {
@@ -974,13 +1244,6 @@ template <> struct DyVec<4> {
     return __builtin_bit_cast(float, t);
   }
 };
-
-// A value the optimiser cannot see through: keeps `load | mask` a bitwise
-// OR instead of a select that would become a branch around the load.
-__device__ __forceinline__ int32_t opaque(int32_t v) {
-  asm volatile("" : "+v"(v));
-  return v;
-}
 
 template <int VB, int KPW, int NSLOT, int WAVES>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(WAVES))) void
@@ -1420,10 +1683,15 @@ template <typename T, int NT, int CSUB>
 static void launch_shape(const T *x, int cred, const T *wt, int ncols, const float *bias,
                          const int32_t *nbr, int64_t n_rows, int K, const int32_t *order, T *y,
                          int splits, float *partial, hipStream_t s) {
-  constexpr int W = kIsF32<T> ? 8 : (NT >= 128 ? 4 : (CSUB == 1 && NT >= 64 ? 6 : 8));
-  constexpr int G = kIsF32<T> ? 1 : (NT >= 128 ? 2 : (CSUB == 1 ? 4 : 1));
-  launch_os<T, NT, 1, CSUB, W, G>(x, cred, wt, ncols, bias, nbr, n_rows, K, order, y, splits,
-                                  partial, s);
+  // bf16 at 64 columns and 64 reduction channels: two row groups per wave
+  // share each weight fragment read (config 2, quad-order gathers: 104 us
+  // against 117 with one group per wave)
+  constexpr int RG = !kIsF32<T> && NT == 64 && CSUB == 2 ? 2 : 1;
+  constexpr int W = kIsF32<T> ? (NT == 64 ? 6 : 8)
+                              : (NT >= 128 || RG == 2 ? 4 : (CSUB == 1 && NT >= 64 ? 6 : 8));
+  constexpr int G = kIsF32<T> ? 1 : (NT >= 128 || RG == 2 ? 2 : (CSUB == 1 ? 4 : 1));
+  launch_os<T, NT, RG, CSUB, W, G>(x, cred, wt, ncols, bias, nbr, n_rows, K, order, y, splits,
+                                   partial, s);
 }
 
 template <typename T, int NT>
@@ -1477,14 +1745,120 @@ static size_t os_partial_floats(int64_t n_rows, int cred, int ncols, int K) {
   return sp > 1 ? static_cast<size_t>(sp) * n_rows * ncols : 0;
 }
 
-// y[order[j]] = sum_k x[nbr[k][j]] @ W'[k] with W'[k][c][n] = wt[k][n][c].
-// partial: os_partial_floats(...) floats, or null to run without a split.
-template <typename T>
-static void run_os(const T *x, int cred, const T *wt, int ncols,
+// Shape of the resident-weight kernel (conv_fr_kernel) for a bf16 map: the
+// widest column slice whose weights fit in LDS, taken only when one slice
+// covers every column of a large map. Each further slice would gather every
+// row again, which costs more than the per-stage weight reloads of
+// conv_os_kernel save; measured on MI355X (quad-order gathers both):
+// config-5 stage 1 (808k rows, C32->32, 27 offsets) 105 us against 133, its
+// 2^3 downsample (C32->64) 28 against 33; config 2 (C64, two slices) 117
+// against 104; config 3's maps (40k-85k rows) 19-20 against 16-19.
+constexpr int kCus = 256;
+constexpr int kFrLdsBytes = 160 * 1024;
+constexpr int kFrMaxSlices = 1;
+constexpr int64_t kFrMinRows = 131072;
+// waves per workgroup and stages in flight, within the register budget
+template <int NT, int KS> constexpr int kFrWaves = NT <= 32 && KS == 1 ? 12 : 8;
+template <int KS> constexpr int kFrDepth = KS == 4 ? 2 : 4;
+static int fr_kq(int K) { return K <= 8 ? 2 : (K <= 28 ? 8 : 0); }
+static int64_t fr_lds(int kq, int nt, int cred) {
+  return static_cast<int64_t>(kq == 2 ? 8 : 28) * nt * (cred + 8) * 2;
+}
+static int fr_nt(int cred, int ncols, int K, int64_t n_x, int64_t n_rows) {
+  const int kq = fr_kq(K);
+  if (kq == 0 || (cred != 32 && cred != 64 && cred != 128) || ncols % 16 != 0)
+    return 0;
+  if (n_rows < kFrMinRows || n_x * cred * 2 > kBufMaxBytes ||
+      static_cast<int64_t>(K) * n_rows * 4 > kBufMaxBytes)
+    return 0;
+  for (int nt : {128, 64, 32, 16}) {
+    if (ncols % nt != 0 || fr_lds(kq, nt, cred) > kFrLdsBytes)
+      continue;
+    return ncols / nt <= kFrMaxSlices ? nt : 0;
+  }
+  return 0;
+}
+
+// Grid of the resident-weight kernel: at most one workgroup per CU (its LDS
+// allows no more), fewer for a small map (each wave at least one unit),
+// always a multiple of 8 (one share per XCD) whose per-XCD count the slices
+// divide.
+static int fr_grid(int64_t n_rows, int slices, int waves) {
+  const int64_t per_xcd = ceil_div(ceil_div(n_rows, 32) * slices, int64_t(kXcds) * waves);
+  const int64_t q = std::min<int64_t>(kCus / kXcds, ceil_div(per_xcd, slices) * slices);
+  return static_cast<int>(kXcds * std::max<int64_t>(q, slices));
+}
+
+template <int NT, int KS, int KQ>
+static void launch_fr(const __bf16 *x, int64_t n_x, const __bf16 *wt, int ncols,
+                      const float *bias, const int32_t *nbr, int64_t n_rows, int K,
+                      const int32_t *order, __bf16 *y, hipStream_t s) {
+  constexpr int W = kFrWaves<NT, KS>;
+  hipLaunchKernelGGL((conv_fr_kernel<NT, KS, KQ, kFrDepth<KS>, W>),
+                     dim3(fr_grid(n_rows, ncols / NT, W)), dim3(W * kWave), 0, s, x, n_x, wt,
+                     ncols, bias, nbr, n_rows, K, order, y);
+}
+
+// Runs the resident-weight kernel where fr_nt takes the map; false if not.
+static bool run_fr(const __bf16 *x, int64_t n_x, int cred, const __bf16 *wt, int ncols,
                    const float *bias, const int32_t *nbr, int64_t n_rows, int K,
-                   const int32_t *order, T *y, float *partial, hipStream_t s) {
+                   const int32_t *order, __bf16 *y, hipStream_t s) {
+  if (!aligned16(x) || !aligned16(wt))
+    return false;
+  const int nt = fr_nt(cred, ncols, K, n_x, n_rows);
+  if (nt == 0)
+    return false;
+  auto go = [&](auto ntc, auto ksc, auto kqc) {
+    launch_fr<decltype(ntc)::value, decltype(ksc)::value, decltype(kqc)::value>(
+        x, n_x, wt, ncols, bias, nbr, n_rows, K, order, y, s);
+  };
+  using I1 = std::integral_constant<int, 1>;
+  using I2 = std::integral_constant<int, 2>;
+  using I4 = std::integral_constant<int, 4>;
+  using I8 = std::integral_constant<int, 8>;
+  using N16 = std::integral_constant<int, 16>;
+  using N32 = std::integral_constant<int, 32>;
+  using N64 = std::integral_constant<int, 64>;
+  using N128 = std::integral_constant<int, 128>;
+  if (fr_kq(K) == 8) {
+    if (cred == 32)
+      nt == 64 ? go(N64{}, I1{}, I8{}) : nt == 32 ? go(N32{}, I1{}, I8{}) : go(N16{}, I1{}, I8{});
+    else if (cred == 64)
+      nt == 32 ? go(N32{}, I2{}, I8{}) : go(N16{}, I2{}, I8{});
+    else
+      go(N16{}, I4{}, I8{});
+  } else {
+    if (cred == 32)
+      nt == 128  ? go(N128{}, I1{}, I2{})
+      : nt == 64 ? go(N64{}, I1{}, I2{})
+      : nt == 32 ? go(N32{}, I1{}, I2{})
+                 : go(N16{}, I1{}, I2{});
+    else if (cred == 64)
+      nt == 128  ? go(N128{}, I2{}, I2{})
+      : nt == 64 ? go(N64{}, I2{}, I2{})
+      : nt == 32 ? go(N32{}, I2{}, I2{})
+                 : go(N16{}, I2{}, I2{});
+    else
+      nt == 64 ? go(N64{}, I4{}, I2{}) : nt == 32 ? go(N32{}, I4{}, I2{}) : go(N16{}, I4{}, I2{});
+  }
+  RHIP_LAUNCH_CHECK();
+  return true;
+}
+
+// y[order[j]] = sum_k x[nbr[k][j]] @ W'[k] with W'[k][c][n] = wt[k][n][c];
+// x has n_x rows. partial: os_partial_floats(...) floats, or null to run
+// without a split.
+template <typename T>
+static void run_os(const T *x, int64_t n_x, int cred, const T *wt, int ncols,
+                   const float *bias, const int32_t *nbr, int64_t n_rows, int K,
+                   const int32_t *order, T *y, float *partial, hipStream_t s,
+                   bool resident = true) {
   if (n_rows == 0)
     return;
+  if constexpr (!kIsF32<T>) {
+    if (resident && run_fr(x, n_x, cred, wt, ncols, bias, nbr, n_rows, K, order, y, s))
+      return;
+  }
   const int splits = partial ? os_splits<T>(n_rows, cred, ncols, K) : 1;
   if (!os_fast(x, cred, wt, ncols, K)) {
     hipLaunchKernelGGL((conv_os_generic_kernel<T>), dim3(ceil_div(n_rows * ncols, kThreads)),
@@ -1638,7 +2012,6 @@ constexpr int kDwPosSlots = 4;
 constexpr int kDwPosMinK = 20;
 constexpr int kDwPosMaxKSmall = 4 * kDwPosKPWSmall;
 static int dw_pos_kpw(int K) { return K <= kDwPosMaxKSmall ? kDwPosKPWSmall : kDwPosKPW; }
-constexpr int64_t kBufMaxBytes = (int64_t(1) << 31) - 256; // buffer offsets stay below kBufOob
 
 template <int VB> constexpr int kDwPosWaves = VB == 4 ? 2 : 3;
 
@@ -1879,7 +2252,7 @@ extern "C" int rhip_conv_forward(const void *x, int64_t n_in, int32_t cin,
                          dim3(kThreads), 0, stream, static_cast<const float *>(weight), K, cin,
                          cout, wt);
       RHIP_LAUNCH_CHECK();
-      run_os<float>(static_cast<const float *>(x), cin, wt, cout, bias, nbr, n_out, K,
+      run_os<float>(static_cast<const float *>(x), n_in, cin, wt, cout, bias, nbr, n_out, K,
                     out_order, static_cast<float *>(y), w.os_partial, stream);
     } else {
       __bf16 *wt = static_cast<__bf16 *>(w.wt);
@@ -1887,7 +2260,7 @@ extern "C" int rhip_conv_forward(const void *x, int64_t n_in, int32_t cin,
                          dim3(kThreads), 0, stream, static_cast<const __bf16 *>(weight), K,
                          cin, cout, wt);
       RHIP_LAUNCH_CHECK();
-      run_os<__bf16>(static_cast<const __bf16 *>(x), cin, wt, cout, bias, nbr, n_out, K,
+      run_os<__bf16>(static_cast<const __bf16 *>(x), n_in, cin, wt, cout, bias, nbr, n_out, K,
                      out_order, static_cast<__bf16 *>(y), w.os_partial, stream);
     }
   });
@@ -1917,11 +2290,11 @@ extern "C" int rhip_conv_backward_input(const void *grad_y, int64_t n_out,
     }
     // dX rows gather dY rows; W[k] [cin][cout] is already [n = cin][c = cout].
     if (dtype == RHIP_F32)
-      run_os<float>(static_cast<const float *>(grad_y), cout,
+      run_os<float>(static_cast<const float *>(grad_y), n_out, cout,
                     static_cast<const float *>(weight), cin, nullptr, nbr_t, n_in, K,
                     in_order, static_cast<float *>(grad_x), os_partial, stream);
     else
-      run_os<__bf16>(static_cast<const __bf16 *>(grad_y), cout,
+      run_os<__bf16>(static_cast<const __bf16 *>(grad_y), n_out, cout,
                      static_cast<const __bf16 *>(weight), cin, nullptr, nbr_t, n_in, K,
                      in_order, static_cast<__bf16 *>(grad_x), os_partial, stream);
   });

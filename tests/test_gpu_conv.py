@@ -399,11 +399,47 @@ def test_config2_full_size_vs_torch(dtype):
     y = abi.conv_forward(x, w, km)
     gx = abi.conv_backward_input(gy, w, km)
     gw = abi.conv_backward_weight(x, gy, km, 27)
+    # the dW dispatch the layer and the bench time (neighbour-table kernels)
+    gw_timed = abi.conv_weight_grad(x, gy, km, 27)
     ry, rgx, rgw = _torch_gather_gemm_scatter(km, x, w, gy)
     tol = TOL[dtype]
     assert_rel(y.float().cpu().numpy(), ry.cpu().numpy(), tol, "Y")
     assert_rel(gx.float().cpu().numpy(), rgx.cpu().numpy(), tol, "dX")
-    assert_rel(gw.float().cpu().numpy(), rgw.cpu().numpy(), tol, "dW")
+    assert_rel(gw.float().cpu().numpy(), rgw.cpu().numpy(), tol, "dW (pair list)")
+    assert_rel(gw_timed.float().cpu().numpy(), rgw.cpu().numpy(), tol, "dW (timed dispatch)")
+
+
+def test_resident_weight_kernel_on_large_maps():
+    """bf16 maps of at least 131072 output rows whose weights for all output
+    columns fit in LDS take the resident-weight kernel: a 3^3 same-set map
+    with 32 channels and the transposed 2^3 map (8 offsets, C64->32), forward
+    and input gradient, against the plain PyTorch fp32 gather-matmul-scatter
+    on the same bf16 operands."""
+    c = scenes.indoor_batch(4, 3)
+    _, _, km = gpu_tables_and_map(c, c, oracle.region_offsets(3, 3), same=True)
+    assert km.n_out >= 131072
+    g = torch.Generator(device="cpu").manual_seed(5)
+    dt = torch.bfloat16
+    x = torch.randn((km.n_in, 32), generator=g).to(DEV, dt)
+    w = (torch.randn((27, 32, 32), generator=g) * 0.05).to(DEV, dt)
+    gy = torch.randn((km.n_out, 32), generator=g).to(DEV, dt)
+    ry, rgx, _ = _torch_gather_gemm_scatter(km, x, w, gy)
+    assert_rel(abi.conv_forward(x, w, km).float().cpu().numpy(), ry.cpu().numpy(), TOL[dt],
+               "3^3 Y")
+    assert_rel(abi.conv_backward_input(gy, w, km).float().cpu().numpy(), rgx.cpu().numpy(),
+               TOL[dt], "3^3 dX")
+    tf = abi.hash_build(to_dev(c))
+    tc = abi.hash_build(abi.stride_coords(to_dev(c), [2, 2, 2]))
+    up = abi.kernel_map(tf, tc, oracle.region_offsets(3, 2)).swapped()
+    assert up.n_out >= 131072
+    xc = torch.randn((up.n_in, 64), generator=g).to(DEV, dt)
+    wu = (torch.randn((8, 64, 32), generator=g) * 0.1).to(DEV, dt)
+    gyf = torch.randn((up.n_out, 32), generator=g).to(DEV, dt)
+    ry, rgx, _ = _torch_gather_gemm_scatter(up, xc, wu, gyf)
+    assert_rel(abi.conv_forward(xc, wu, up).float().cpu().numpy(), ry.cpu().numpy(), TOL[dt],
+               "2^3 transposed Y")
+    assert_rel(abi.conv_backward_input(gyf, wu, up).float().cpu().numpy(), rgx.cpu().numpy(),
+               TOL[dt], "2^3 transposed dX")
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
