@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define RHIP_ABI_VERSION 10
+#define RHIP_ABI_VERSION 11
 #define RHIP_MAX_COLS 8 /* batch column + up to 7 spatial axes */
 
 typedef enum rhip_status {
@@ -226,6 +226,22 @@ int rhip_conv_forward(const void *x, int64_t n_in, int32_t cin,
                       const int32_t *out_order, int64_t n_out, void *y,
                       int32_t dtype, void *workspace, size_t workspace_bytes,
                       hipStream_t stream);
+
+/*
+ * rhip_conv_forward without a workspace: no counterpart in the reference.
+ * For callers that cannot allocate (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc): it calls no allocating
+ * routine. The transposed weights go to an 8 MiB device array of the
+ * library (one per GPU, held until the process ends), so K*cin*cout times
+ * the dtype size must not exceed 8 MiB (RHIP_ERR_UNSUPPORTED otherwise),
+ * and the offset axis is never split. Calls that overlap on one GPU share
+ * that array and race. Same arguments and results as rhip_conv_forward.
+ */
+int rhip_conv_forward_noalloc(const void *x, int64_t n_in, int32_t cin,
+                              const void *weight, int32_t K, int32_t cout,
+                              const float *bias, const int32_t *nbr,
+                              const int32_t *out_order, int64_t n_out, void *y,
+                              int32_t dtype, hipStream_t stream);
 
 /*
  * grad_x[in_order[j]] = sum_k grad_y[nbr_t[k*n_in+j]] @ W[k]^T.

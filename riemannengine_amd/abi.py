@@ -31,7 +31,7 @@ EXPORTS = (
     "rhip_hash_workspace_bytes", "rhip_hash_build", "rhip_hash_lookup",
     "rhip_order_workspace_bytes", "rhip_spatial_order", "rhip_stride_coords",
     "rhip_expand_coords", "rhip_kmap_workspace_bytes", "rhip_kmap_count", "rhip_kmap_fill",
-    "rhip_conv_workspace_bytes", "rhip_conv_forward",
+    "rhip_conv_workspace_bytes", "rhip_conv_forward", "rhip_conv_forward_noalloc",
     "rhip_conv_backward_input", "rhip_conv_backward_weight", "rhip_conv_backward_weight_rows",
     "rhip_stride_map_workspace_bytes", "rhip_stride_map_count", "rhip_group_map_count",
     "rhip_stride_map_fill",
@@ -82,6 +82,8 @@ def _declare(lib):
                                                      _P(_sz)]),
         "rhip_conv_forward": (ctypes.c_int, [_vp, _i64, _i32, _vp, _i32, _i32, _vp, _vp,
                                              _vp, _i64, _vp, _i32, _vp, _sz, _vp]),
+        "rhip_conv_forward_noalloc": (ctypes.c_int, [_vp, _i64, _i32, _vp, _i32, _i32, _vp,
+                                                     _vp, _vp, _i64, _vp, _i32, _vp]),
         "rhip_conv_backward_input": (ctypes.c_int, [_vp, _i64, _i32, _vp, _i32, _i32,
                                                     _vp, _vp, _i64, _vp, _i32, _vp,
                                                     _sz, _vp]),
@@ -375,6 +377,26 @@ def conv_forward(x: torch.Tensor, weight: torch.Tensor, kmap: KernelMap,
                                    dt, _ptr(ws), ws.numel(), _stream(x.device)),
            "rhip_conv_forward")
     return y
+
+
+def conv_forward_noalloc(x: torch.Tensor, weight: torch.Tensor, kmap: KernelMap,
+                         bias: Optional[torch.Tensor] = None,
+                         out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """The forward through rhip_conv_forward_noalloc (the library's own
+    device scratch instead of a workspace). `out` may be given so that the
+    call itself allocates nothing."""
+    _require_cuda(x, "x")
+    dt = _dtype_code(x.dtype)
+    K, cin, cout = weight.shape
+    if K != kmap.K or x.shape[1] != cin or x.shape[0] != kmap.n_in:
+        raise RuntimeError("shape mismatch between features, weight and kernel map")
+    if out is None:
+        out = torch.empty((kmap.n_out, cout), dtype=x.dtype, device=x.device)
+    _check(lib().rhip_conv_forward_noalloc(_ptr(x), kmap.n_in, cin, _ptr(weight), K, cout,
+                                           _ptr(bias), _ptr(kmap.nbr), _ptr(kmap.out_order),
+                                           kmap.n_out, _ptr(out), dt, _stream(x.device)),
+           "rhip_conv_forward_noalloc")
+    return out
 
 
 def conv_backward_input(grad_y: torch.Tensor, weight: torch.Tensor, kmap: KernelMap) -> torch.Tensor:

@@ -29,6 +29,7 @@
 //    chosen so that each lane reads 16 contiguous bytes; A and B use the same
 //    permutation, so the sum is unchanged.
 #include <algorithm>
+#include <mutex>
 #include <type_traits>
 
 #include "rhip_internal.hpp"
@@ -2206,6 +2207,58 @@ static ConvWs carve_conv(Carve &cv, int32_t K, int32_t cin, int32_t cout, int32_
   return w;
 }
 
+// The forward with the transposed weights at wt (K * cin * cout elements) and
+// the split partial sums at os_partial (null: no split).
+static void conv_forward_into(const void *x, int64_t n_in, int32_t cin, const void *weight,
+                              int32_t K, int32_t cout, const float *bias, const int32_t *nbr,
+                              const int32_t *out_order, int64_t n_out, void *y, int32_t dtype,
+                              void *wt, float *os_partial, hipStream_t stream) {
+  const int64_t nw = static_cast<int64_t>(K) * cin * cout;
+  // the MFMA path reads W[k] column-wise: stage the [K, cout, cin] copy
+  if (dtype == RHIP_F32) {
+    float *w = static_cast<float *>(wt);
+    hipLaunchKernelGGL((transpose_w_kernel<float>), dim3(ceil_div(nw, kThreads)),
+                       dim3(kThreads), 0, stream, static_cast<const float *>(weight), K, cin,
+                       cout, w);
+    RHIP_LAUNCH_CHECK();
+    run_os<float>(static_cast<const float *>(x), n_in, cin, w, cout, bias, nbr, n_out, K,
+                  out_order, static_cast<float *>(y), os_partial, stream);
+  } else {
+    __bf16 *w = static_cast<__bf16 *>(wt);
+    hipLaunchKernelGGL((transpose_w_kernel<__bf16>), dim3(ceil_div(nw, kThreads)),
+                       dim3(kThreads), 0, stream, static_cast<const __bf16 *>(weight), K, cin,
+                       cout, w);
+    RHIP_LAUNCH_CHECK();
+    run_os<__bf16>(static_cast<const __bf16 *>(x), n_in, cin, w, cout, bias, nbr, n_out, K,
+                   out_order, static_cast<__bf16 *>(y), os_partial, stream);
+  }
+}
+
+// Device scratch of rhip_conv_forward_noalloc: the transposed weights go
+// here instead of into a caller workspace. Every GPU the library runs on
+// holds its own copy until the process ends; calls that overlap on one GPU
+// share it and race.
+constexpr size_t kConvScratchBytes = size_t(8) << 20;
+static __device__ __align__(256) char scratch[kConvScratchBytes];
+
+// This device's address of `scratch` (the host-side name is only a stand-in
+// for it), looked up once per device with that device current.
+static void *device_scratch() {
+  constexpr int kMaxDevices = 64;
+  static std::mutex mu;
+  static void *addr[kMaxDevices] = {};
+  int dev = 0;
+  RHIP_HIP(hipGetDevice(&dev));
+  RHIP_CHECK_ARG(dev >= 0 && dev < kMaxDevices, "device index out of range");
+  std::lock_guard<std::mutex> lock(mu);
+  if (addr[dev] == nullptr) {
+    void *p = nullptr;
+    RHIP_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    addr[dev] = p;
+  }
+  return addr[dev];
+}
+
 } // namespace rhip
 
 using namespace rhip;
@@ -2244,25 +2297,35 @@ extern "C" int rhip_conv_forward(const void *x, int64_t n_in, int32_t cin,
     // plan does not change the forward's pieces
     Carve cv(workspace, workspace_bytes);
     const ConvWs w = carve_conv(cv, K, cin, cout, dtype, n_in, n_out, DwPlan{});
-    const int64_t nw = static_cast<int64_t>(K) * cin * cout;
-    // the MFMA path reads W[k] column-wise: stage the [K, cout, cin] copy
-    if (dtype == RHIP_F32) {
-      float *wt = static_cast<float *>(w.wt);
-      hipLaunchKernelGGL((transpose_w_kernel<float>), dim3(ceil_div(nw, kThreads)),
-                         dim3(kThreads), 0, stream, static_cast<const float *>(weight), K, cin,
-                         cout, wt);
-      RHIP_LAUNCH_CHECK();
-      run_os<float>(static_cast<const float *>(x), n_in, cin, wt, cout, bias, nbr, n_out, K,
-                    out_order, static_cast<float *>(y), w.os_partial, stream);
-    } else {
-      __bf16 *wt = static_cast<__bf16 *>(w.wt);
-      hipLaunchKernelGGL((transpose_w_kernel<__bf16>), dim3(ceil_div(nw, kThreads)),
-                         dim3(kThreads), 0, stream, static_cast<const __bf16 *>(weight), K,
-                         cin, cout, wt);
-      RHIP_LAUNCH_CHECK();
-      run_os<__bf16>(static_cast<const __bf16 *>(x), n_in, cin, wt, cout, bias, nbr, n_out, K,
-                     out_order, static_cast<__bf16 *>(y), w.os_partial, stream);
-    }
+    conv_forward_into(x, n_in, cin, weight, K, cout, bias, nbr, out_order, n_out, y, dtype, w.wt,
+                      w.os_partial, stream);
+  });
+}
+
+extern "C" int rhip_conv_forward_noalloc(const void *x, int64_t n_in, int32_t cin,
+                                         const void *weight, int32_t K, int32_t cout,
+                                         const float *bias, const int32_t *nbr,
+                                         const int32_t *out_order, int64_t n_out, void *y,
+                                         int32_t dtype, hipStream_t stream) {
+  return guarded([&] {
+    check_dtype(dtype);
+    RHIP_CHECK_ARG(K >= 1 && cin >= 1 && cout >= 1, "sizes must be positive");
+    RHIP_CHECK_ARG(n_in >= 0 && n_out >= 0, "row counts must be >= 0");
+    const size_t wt_bytes =
+        static_cast<size_t>(K) * cin * cout * (dtype == RHIP_F32 ? 4 : 2);
+    if (wt_bytes > kConvScratchBytes)
+      throw Error(RHIP_ERR_UNSUPPORTED,
+                  "rhip_conv_forward_noalloc: the weights need " + std::to_string(wt_bytes) +
+                      " bytes of device scratch, more than its " +
+                      std::to_string(kConvScratchBytes) +
+                      " (use rhip_conv_forward with a workspace)");
+    if (n_out == 0)
+      return;
+    RHIP_CHECK_ARG(y && weight && nbr, "y, weight and nbr are required");
+    RHIP_CHECK_ARG(n_in == 0 || x != nullptr, "x is null");
+    // no split of the offset axis: it would need partial sums beyond the scratch
+    conv_forward_into(x, n_in, cin, weight, K, cout, bias, nbr, out_order, n_out, y, dtype,
+                      device_scratch(), nullptr, stream);
   });
 }
 

@@ -32,7 +32,7 @@ def test_library_exports_every_declared_symbol():
 
 
 def test_abi_version_and_struct_layout():
-    assert abi.lib().rhip_abi_version() == 10
+    assert abi.lib().rhip_abi_version() == 11
     # void*, int64, void*, int64, 3 x int32, 3 x int32[8] -> 140 bytes, padded to 144
     assert ctypes.sizeof(abi.RhipTable) == 144
 

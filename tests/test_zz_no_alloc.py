@@ -1,0 +1,43 @@
+"""rhip_conv_forward_noalloc (the forward without a workspace, with the
+transposed weights in the library's own device scratch) against
+rhip_conv_forward: two calls in a row, the second on a smaller map with other
+weights, fp32 and bf16, within the path's tolerance (rel 1e-4 fp32, 2e-2
+bf16; the workspace call may split the offset axis of a small map and add
+the splits' partial sums, which rounds differently). The size limit is
+rejected without a GPU call."""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from riemannengine_amd import abi
+from helpers import DEV, TOL, assert_rel, random_coords, gpu_tables_and_map, to_dev
+
+
+def test_noalloc_rejects_weights_beyond_the_scratch():
+    L = abi.lib()
+    # 27 x 256 x 512 fp32 weights = 13.5 MiB > 8 MiB
+    st = L.rhip_conv_forward_noalloc(None, 1, 256, None, 27, 512, None, None, None, 1, None,
+                                     abi.F32, None)
+    assert st == 3  # RHIP_ERR_UNSUPPORTED
+    assert "scratch" in L.rhip_last_error().decode()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_noalloc_forward_matches_workspace_forward(dtype):
+    rng = np.random.default_rng(3)
+    for n, cin, cout, bias in ((12000, 64, 64, True), (3000, 32, 16, False)):
+        c, _, _ = oracle.insert_and_map(random_coords(rng, n, 3, 18))
+        _, _, km = gpu_tables_and_map(c, c, oracle.region_offsets(3, 3), same=True)
+        print(f"noalloc {dtype} n={km.n_in} cin={cin} cout={cout} bias={bias}", flush=True)
+        x = to_dev(rng.standard_normal((km.n_in, cin)).astype(np.float32), dtype)
+        w = to_dev((rng.standard_normal((27, cin, cout)) / 20).astype(np.float32), dtype)
+        b = to_dev(rng.standard_normal(cout).astype(np.float32)) if bias else None
+        ref = abi.conv_forward(x, w, km, bias=b)
+        out = torch.empty_like(ref)
+        got = abi.conv_forward_noalloc(x, w, km, bias=b, out=out)
+        torch.cuda.synchronize()
+        assert got.data_ptr() == out.data_ptr()
+        assert_rel(got.float().cpu().numpy(), ref.float().cpu().numpy(), TOL[dtype],
+                   f"noalloc vs workspace forward, n={km.n_in}")
