@@ -212,6 +212,13 @@ int rhip_conv_workspace_bytes(int32_t K, int32_t cin, int32_t cout,
                               int32_t dtype, int64_t n_in, int64_t n_out,
                               int64_t n_pairs, size_t *bytes);
 
+/* Workspace of one layer's forward, input-gradient and bias-gradient calls
+ * alone (no weight gradient): the front part of the rhip_conv_workspace_bytes
+ * layout. */
+int rhip_conv_forward_workspace_bytes(int32_t K, int32_t cin, int32_t cout,
+                                      int32_t dtype, int64_t n_in, int64_t n_out,
+                                      size_t *bytes);
+
 /*
  * Y[out_order[j]] = sum_k X[nbr[k*n_out+j]] @ W[k] (+ bias), fp32 accumulate.
  * x [n_in, cin], weight [K, cin, cout], y [n_out, cout], all in `dtype`;
@@ -242,6 +249,17 @@ int rhip_conv_forward_noalloc(const void *x, int64_t n_in, int32_t cin,
                               const float *bias, const int32_t *nbr,
                               const int32_t *out_order, int64_t n_out, void *y,
                               int32_t dtype, hipStream_t stream);
+
+/*
+ * grad_bias[c] = sum over rows of grad_y[r][c] (grad_y [n_out, cout] in
+ * dtype, grad_bias fp32 [cout], overwritten), fp32 accumulation in a fixed
+ * order (deterministic). Workspace: either layer workspace above.
+ * Replaces the bias half of the reference's autograd graph for
+ * `output + bias_` (engine/nn/conv.cpp:135-136).
+ */
+int rhip_conv_bias_grad(const void *grad_y, int64_t n_out, int32_t cout,
+                        int32_t dtype, float *grad_bias, void *workspace,
+                        size_t workspace_bytes, hipStream_t stream);
 
 /*
  * grad_x[in_order[j]] = sum_k grad_y[nbr_t[k*n_in+j]] @ W[k]^T.

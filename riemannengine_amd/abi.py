@@ -31,7 +31,8 @@ EXPORTS = (
     "rhip_hash_workspace_bytes", "rhip_hash_build", "rhip_hash_lookup",
     "rhip_order_workspace_bytes", "rhip_spatial_order", "rhip_stride_coords",
     "rhip_expand_coords", "rhip_kmap_workspace_bytes", "rhip_kmap_count", "rhip_kmap_fill",
-    "rhip_conv_workspace_bytes", "rhip_conv_forward", "rhip_conv_forward_noalloc",
+    "rhip_conv_workspace_bytes", "rhip_conv_forward_workspace_bytes", "rhip_conv_forward",
+    "rhip_conv_forward_noalloc", "rhip_conv_bias_grad",
     "rhip_conv_backward_input", "rhip_conv_backward_weight", "rhip_conv_backward_weight_rows",
     "rhip_stride_map_workspace_bytes", "rhip_stride_map_count", "rhip_group_map_count",
     "rhip_stride_map_fill",
@@ -82,6 +83,9 @@ def _declare(lib):
                                                      _P(_sz)]),
         "rhip_conv_forward": (ctypes.c_int, [_vp, _i64, _i32, _vp, _i32, _i32, _vp, _vp,
                                              _vp, _i64, _vp, _i32, _vp, _sz, _vp]),
+        "rhip_conv_forward_workspace_bytes": (ctypes.c_int, [_i32, _i32, _i32, _i32, _i64, _i64,
+                                                             _P(_sz)]),
+        "rhip_conv_bias_grad": (ctypes.c_int, [_vp, _i64, _i32, _i32, _vp, _vp, _sz, _vp]),
         "rhip_conv_forward_noalloc": (ctypes.c_int, [_vp, _i64, _i32, _vp, _i32, _i32, _vp,
                                                      _vp, _vp, _i64, _vp, _i32, _vp]),
         "rhip_conv_backward_input": (ctypes.c_int, [_vp, _i64, _i32, _vp, _i32, _i32,
@@ -359,6 +363,27 @@ def _conv_ws(K, cin, cout, dtype, dev, kmap: "KernelMap") -> torch.Tensor:
                               kmap.n_out, kmap.n_pairs), dtype=torch.uint8, device=dev)
 
 
+def _conv_fwd_ws(K, cin, cout, dtype, dev, kmap: "KernelMap") -> torch.Tensor:
+    """Workspace of the forward, input-gradient and bias-gradient calls."""
+    return torch.empty(_sizeq(lib().rhip_conv_forward_workspace_bytes, K, cin, cout, dtype,
+                              kmap.n_in, kmap.n_out), dtype=torch.uint8, device=dev)
+
+
+def conv_bias_grad(grad_y: torch.Tensor) -> torch.Tensor:
+    """Column sums of grad_y in fp32 (the bias gradient) via rhip_conv_bias_grad."""
+    _require_cuda(grad_y, "grad_y")
+    grad_y = grad_y.contiguous()
+    n, C = grad_y.shape
+    gb = torch.empty(C, dtype=torch.float32, device=grad_y.device)
+    ws = torch.empty(_sizeq(lib().rhip_conv_forward_workspace_bytes, 1, 1, C,
+                            _dtype_code(grad_y.dtype), 0, n), dtype=torch.uint8,
+                     device=grad_y.device)
+    _check(lib().rhip_conv_bias_grad(_ptr(grad_y), n, C, _dtype_code(grad_y.dtype), _ptr(gb),
+                                     _ptr(ws), ws.numel(), _stream(grad_y.device)),
+           "rhip_conv_bias_grad")
+    return gb
+
+
 def conv_forward(x: torch.Tensor, weight: torch.Tensor, kmap: KernelMap,
                  bias: Optional[torch.Tensor] = None) -> torch.Tensor:
     """Y[out] = sum_k X[in_k] @ W[k] (+ bias) through rhip_conv_forward."""
@@ -371,7 +396,7 @@ def conv_forward(x: torch.Tensor, weight: torch.Tensor, kmap: KernelMap,
         raise RuntimeError("shape mismatch between features, weight and kernel map")
     b = None if bias is None else bias.reshape(-1).to(torch.float32).contiguous()
     y = torch.empty((kmap.n_out, cout), dtype=x.dtype, device=x.device)
-    ws = _conv_ws(K, cin, cout, dt, x.device, kmap)
+    ws = _conv_fwd_ws(K, cin, cout, dt, x.device, kmap)
     _check(lib().rhip_conv_forward(_ptr(x), kmap.n_in, cin, _ptr(weight), K, cout, _ptr(b),
                                    _ptr(kmap.nbr), _ptr(kmap.out_order), kmap.n_out, _ptr(y),
                                    dt, _ptr(ws), ws.numel(), _stream(x.device)),
@@ -406,7 +431,7 @@ def conv_backward_input(grad_y: torch.Tensor, weight: torch.Tensor, kmap: Kernel
     weight = weight.to(grad_y.dtype).contiguous()
     K, cin, cout = weight.shape
     gx = torch.empty((kmap.n_in, cin), dtype=grad_y.dtype, device=grad_y.device)
-    ws = _conv_ws(K, cin, cout, dt, grad_y.device, kmap)
+    ws = _conv_fwd_ws(K, cin, cout, dt, grad_y.device, kmap)
     _check(lib().rhip_conv_backward_input(_ptr(grad_y), kmap.n_out, cout, _ptr(weight), K, cin,
                                           _ptr(kmap.nbr_t), _ptr(kmap.in_order), kmap.n_in,
                                           _ptr(gx), dt, _ptr(ws), ws.numel(),

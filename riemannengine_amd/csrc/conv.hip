@@ -1639,6 +1639,51 @@ __global__ __launch_bounds__(kThreads) void cast_from_f32_kernel(const float *sr
 
 // ------------------------------------------------------------------ host
 
+// Bias gradient: dbias[c] = sum over rows of grad_y[r][c] in fp32. Each of
+// kBiasChunks workgroups sums a contiguous run of rows (thread t: column
+// t % C, row lane t / C, rows in order, row lanes combined in LDS in lane
+// order) into partial[chunk][c]; the final kernel adds the chunks in order:
+// deterministic.
+constexpr int kBiasChunks = 256;
+template <typename T>
+__global__ __launch_bounds__(kThreads) void colsum_partial_kernel(const T *__restrict__ gy,
+                                                                  int64_t n, int C, int64_t rpc,
+                                                                  float *__restrict__ partial) {
+  __shared__ float red[kThreads];
+  const int64_t r0 = blockIdx.x * rpc, r1 = min(n, r0 + rpc);
+  const int lanes = C <= kThreads ? kThreads / C : 1;
+  for (int c0 = 0; c0 < C; c0 += kThreads) {
+    const int t = threadIdx.x;
+    const int c = c0 + (C <= kThreads ? t % C : t);
+    const int rl = C <= kThreads ? t / C : 0;
+    float acc = 0.f;
+    if (rl < lanes && c < C)
+      for (int64_t r = r0 + rl; r < r1; r += lanes)
+        acc += to_f32(gy[r * C + c]);
+    red[t] = acc;
+    __syncthreads();
+    if (rl == 0 && c < C) {
+      float v = red[t];
+      for (int l = 1; l < lanes; ++l)
+        v += red[l * C + t];
+      partial[static_cast<int64_t>(blockIdx.x) * C + c] = v;
+    }
+    __syncthreads();
+  }
+}
+
+__global__ __launch_bounds__(kThreads) void colsum_final_kernel(const float *__restrict__ partial,
+                                                                int chunks, int C,
+                                                                float *__restrict__ out) {
+  const int c = blockIdx.x * kThreads + threadIdx.x;
+  if (c >= C)
+    return;
+  float v = 0.f;
+  for (int b = 0; b < chunks; ++b)
+    v += partial[static_cast<int64_t>(b) * C + c];
+  out[c] = v;
+}
+
 static bool aligned16(const void *p) {
   return (reinterpret_cast<uintptr_t>(p) & 15u) == 0;
 }
@@ -2058,15 +2103,26 @@ static int dw_pos_ranges(int K, int cin, int cout, int vb, int waves, int64_t n_
   return static_cast<int>(std::min<int64_t>(r, kDwRowsBlocks));
 }
 
+// Ranges of conv_dw_pos_bf16_kernel and conv_dw_pos_kernel for a shape
+// (the workspace query and the launches share them).
+static int dw_pos_bf16_ranges(int K, int cin, int cout, int64_t n_out) {
+  const int waves = K <= kDwPosMaxKSmall ? 4 : 2;
+  return dw_pos_ranges(K, cin, cout, cout % 64 == 0 ? 4 : 2, waves, n_out, 16);
+}
+static int dw_pos_f32_ranges(int K, int cin, int cout, int64_t n_out) {
+  const int vb = cout % 64 == 0 ? 4 : 2;
+  const int waves = K <= kDwPosMaxKSmall ? 3 : (vb == 4 ? kDwPosWaves<4> : kDwPosWaves<2>);
+  return dw_pos_ranges(K, cin, cout, vb, waves, n_out, 4);
+}
+
 // grad_w [K, cin, cout] (bf16, overwritten) from the neighbour table.
 static void run_dw_pos_bf16(const __bf16 *x, int64_t n_in, int cin, const __bf16 *gy,
                             int64_t n_out, int cout, int K, const int32_t *nbr,
                             const int32_t *out_order, float *partial, __bf16 *dw,
                             hipStream_t s) {
   const bool small = K <= kDwPosMaxKSmall;
-  const int waves = small ? 4 : 2;
   const int vb = cout % 64 == 0 ? 4 : 2;
-  const int ranges = dw_pos_ranges(K, cin, cout, vb, waves, n_out, 16);
+  const int ranges = dw_pos_bf16_ranges(K, cin, cout, n_out);
   const int groups = static_cast<int>(ceil_div(K, kWaves * dw_pos_kpw(K)));
   const int ct = cin / 16, ot = cout / (16 * vb);
   if (n_in > 0 && n_out > 0) {
@@ -2100,8 +2156,7 @@ static void run_dw_pos(const float *x, int64_t n_in, int cin, const float *gy, i
                        float *partial, float *dw, hipStream_t s) {
   const bool small = K <= kDwPosMaxKSmall;
   const int vb = cout % 64 == 0 ? 4 : 2;
-  const int waves = small ? 3 : (vb == 4 ? kDwPosWaves<4> : kDwPosWaves<2>);
-  const int ranges = dw_pos_ranges(K, cin, cout, vb, waves, n_out, 4);
+  const int ranges = dw_pos_f32_ranges(K, cin, cout, n_out);
   const int groups = static_cast<int>(ceil_div(K, kWaves * dw_pos_kpw(K)));
   const int ct = cin / 16, ot = cout / (16 * vb);
   if (n_in > 0 && n_out > 0) {
@@ -2133,9 +2188,26 @@ static void run_dw_pos(const float *x, int64_t n_in, int cin, const float *gy, i
   RHIP_LAUNCH_CHECK();
 }
 
-// Partial floats of the row kernel: one slot per row block and offset.
-static size_t dw_rows_floats(int K, int cin, int cout) {
-  return static_cast<size_t>(kDwRowsBlocks) * K * cin * cout;
+// Row blocks of conv_dw_rows_kernel for n_out output rows.
+static int dw_rows_blocks(int64_t n_out) {
+  return static_cast<int>(std::min<int64_t>(kDwRowsBlocks, ceil_div(n_out, kDwRowsSP)));
+}
+
+// Partial-slot floats the neighbour-table dW kernels use for this shape
+// (0 where rhip_conv_backward_weight_rows does not take it): one fp32 tile
+// per range or row block and offset.
+static size_t dw_table_floats(int32_t dtype, int cin, int cout, int K, int64_t n_in,
+                              int64_t n_out) {
+  if (!dw_rows_supported(dtype, cin, cout, K, n_in, n_out) || n_in == 0 || n_out == 0)
+    return 0;
+  int slots;
+  if (dtype == RHIP_F32)
+    slots = dw_pos_f32_ranges(K, cin, cout, n_out);
+  else if (dw_pos_supported(dtype, cin, cout, K, n_in, n_out))
+    slots = dw_pos_bf16_ranges(K, cin, cout, n_out);
+  else
+    slots = dw_rows_blocks(n_out);
+  return static_cast<size_t>(slots) * K * cin * cout;
 }
 
 template <int VA, int VB, int KW = kDwRowsKW>
@@ -2155,7 +2227,7 @@ static void run_dw_rows(const __bf16 *x, int64_t n_in, int cin, const __bf16 *gy
                         float *partial, __bf16 *dw, hipStream_t s) {
   int blocks = 0;
   if (n_in > 0 && n_out > 0) { // without rows every slot sum is empty: zeros
-    const int64_t rb = std::min<int64_t>(kDwRowsBlocks, ceil_div(n_out, kDwRowsSP));
+    const int64_t rb = dw_rows_blocks(n_out);
     const int64_t rpb = ceil_div(ceil_div(n_out, rb), kDwRowsSP) * kDwRowsSP;
     blocks = static_cast<int>(ceil_div(n_out, rpb));
     auto go = [&](auto va, auto vb) {
@@ -2180,19 +2252,23 @@ static void run_dw_rows(const __bf16 *x, int64_t n_in, int cin, const __bf16 *gy
   RHIP_LAUNCH_CHECK();
 }
 
-// One workspace serves the three calls of a layer: the transposed weights
-// (forward), the split partial sums of the output-stationary kernel
-// (forward and input gradient), and for dW either the per-workgroup partial
-// tiles or an fp32 accumulator.
+// One workspace serves the calls of a layer. Its front holds what the
+// forward, the input gradient and the bias gradient use: the transposed
+// weights, the split partial sums of the output-stationary kernel and the
+// bias gradient's chunk sums. Behind them, used by dW
+// only: the per-workgroup partial tiles (sized from the dW plans of this map)
+// and the fp32 accumulator of the any-shape kernel. A workspace of
+// rhip_conv_forward_workspace_bytes serves the forward and input gradient.
 struct ConvWs {
   void *wt = nullptr;
   float *os_partial = nullptr;
+  float *bias_partial = nullptr;
   float *partial = nullptr;
   float *acc = nullptr;
 };
 
-static ConvWs carve_conv(Carve &cv, int32_t K, int32_t cin, int32_t cout, int32_t dtype,
-                         int64_t n_in, int64_t n_out, const DwPlan &p) {
+static ConvWs carve_conv_front(Carve &cv, int32_t K, int32_t cin, int32_t cout, int32_t dtype,
+                               int64_t n_in, int64_t n_out) {
   ConvWs w;
   const size_t nw = static_cast<size_t>(K) * cin * cout;
   w.wt = cv.take<char>(nw * (dtype == RHIP_F32 ? 4 : 2));
@@ -2202,8 +2278,16 @@ static ConvWs carve_conv(Carve &cv, int32_t K, int32_t cin, int32_t cout, int32_
                : os_partial_floats<__bf16>(n, cred, ncols, K);
   };
   w.os_partial = cv.take<float>(std::max<size_t>({1, osp(n_out, cin, cout), osp(n_in, cout, cin)}));
-  w.partial = cv.take<float>(std::max<size_t>({1, p.partial_floats() * K, dw_rows_floats(K, cin, cout)}));
-  w.acc = cv.take<float>(nw);
+  w.bias_partial = cv.take<float>(static_cast<size_t>(kBiasChunks) * cout);
+  return w;
+}
+
+static ConvWs carve_conv(Carve &cv, int32_t K, int32_t cin, int32_t cout, int32_t dtype,
+                         int64_t n_in, int64_t n_out, const DwPlan &p) {
+  ConvWs w = carve_conv_front(cv, K, cin, cout, dtype, n_in, n_out);
+  w.partial = cv.take<float>(std::max<size_t>(
+      {1, p.partial_floats() * K, dw_table_floats(dtype, cin, cout, K, n_in, n_out)}));
+  w.acc = cv.take<float>(static_cast<size_t>(K) * cin * cout);
   return w;
 }
 
@@ -2278,6 +2362,20 @@ extern "C" int rhip_conv_workspace_bytes(int32_t K, int32_t cin, int32_t cout,
   });
 }
 
+extern "C" int rhip_conv_forward_workspace_bytes(int32_t K, int32_t cin, int32_t cout,
+                                                 int32_t dtype, int64_t n_in, int64_t n_out,
+                                                 size_t *bytes) {
+  return guarded([&] {
+    RHIP_CHECK_ARG(bytes != nullptr, "bytes is null");
+    RHIP_CHECK_ARG(K >= 1 && cin >= 1 && cout >= 1, "sizes must be positive");
+    RHIP_CHECK_ARG(n_in >= 0 && n_out >= 0, "counts must be >= 0");
+    check_dtype(dtype);
+    Carve cv(nullptr, 0);
+    carve_conv_front(cv, K, cin, cout, dtype, n_in, n_out);
+    *bytes = cv.used + 256;
+  });
+}
+
 extern "C" int rhip_conv_forward(const void *x, int64_t n_in, int32_t cin,
                                  const void *weight, int32_t K, int32_t cout,
                                  const float *bias, const int32_t *nbr,
@@ -2296,7 +2394,7 @@ extern "C" int rhip_conv_forward(const void *x, int64_t n_in, int32_t cin,
     // the workspace was sized for this layer's map (n_in, n_out); the dW
     // plan does not change the forward's pieces
     Carve cv(workspace, workspace_bytes);
-    const ConvWs w = carve_conv(cv, K, cin, cout, dtype, n_in, n_out, DwPlan{});
+    const ConvWs w = carve_conv_front(cv, K, cin, cout, dtype, n_in, n_out);
     conv_forward_into(x, n_in, cin, weight, K, cout, bias, nbr, out_order, n_out, y, dtype, w.wt,
                       w.os_partial, stream);
   });
@@ -2329,6 +2427,34 @@ extern "C" int rhip_conv_forward_noalloc(const void *x, int64_t n_in, int32_t ci
   });
 }
 
+extern "C" int rhip_conv_bias_grad(const void *grad_y, int64_t n_out, int32_t cout,
+                                   int32_t dtype, float *grad_bias, void *workspace,
+                                   size_t workspace_bytes, hipStream_t stream) {
+  return guarded([&] {
+    check_dtype(dtype);
+    RHIP_CHECK_ARG(cout >= 1 && n_out >= 0, "bad sizes");
+    RHIP_CHECK_ARG(grad_bias != nullptr, "grad_bias is null");
+    RHIP_CHECK_ARG(n_out == 0 || grad_y != nullptr, "grad_y is null");
+    RHIP_CHECK_ARG(workspace != nullptr, "workspace is null");
+    // the chunk sums go to the front of the layer workspace, whose forward
+    // part reserves room for them
+    Carve cv(workspace, workspace_bytes);
+    float *partial = cv.take<float>(static_cast<size_t>(kBiasChunks) * cout);
+    const int64_t rpc = ceil_div(std::max<int64_t>(n_out, 1), kBiasChunks);
+    const int chunks = static_cast<int>(ceil_div(std::max<int64_t>(n_out, 1), rpc));
+    if (dtype == RHIP_F32)
+      hipLaunchKernelGGL((colsum_partial_kernel<float>), dim3(chunks), dim3(kThreads), 0, stream,
+                         static_cast<const float *>(grad_y), n_out, cout, rpc, partial);
+    else
+      hipLaunchKernelGGL((colsum_partial_kernel<__bf16>), dim3(chunks), dim3(kThreads), 0, stream,
+                         static_cast<const __bf16 *>(grad_y), n_out, cout, rpc, partial);
+    RHIP_LAUNCH_CHECK();
+    hipLaunchKernelGGL(colsum_final_kernel, dim3(static_cast<unsigned>(ceil_div(cout, kThreads))),
+                       dim3(kThreads), 0, stream, partial, chunks, cout, grad_bias);
+    RHIP_LAUNCH_CHECK();
+  });
+}
+
 extern "C" int rhip_conv_backward_input(const void *grad_y, int64_t n_out,
                                         int32_t cout, const void *weight,
                                         int32_t K, int32_t cin,
@@ -2349,7 +2475,7 @@ extern "C" int rhip_conv_backward_input(const void *grad_y, int64_t n_out,
     float *os_partial = nullptr;
     if (workspace != nullptr) {
       Carve cv(workspace, workspace_bytes);
-      os_partial = carve_conv(cv, K, cin, cout, dtype, n_in, n_out, DwPlan{}).os_partial;
+      os_partial = carve_conv_front(cv, K, cin, cout, dtype, n_in, n_out).os_partial;
     }
     // dX rows gather dY rows; W[k] [cin][cout] is already [n = cin][c = cout].
     if (dtype == RHIP_F32)

@@ -46,6 +46,8 @@ template <typename Impl> ModuleClass<Impl> bind_module(py::module_ &m, const cha
   cls.def(
       "to", [](Impl &self, at::Device device) { self.to(device); }, py::arg("device"));
   cls.def(
+      "to", [](Impl &self, at::ScalarType dtype) { self.to(dtype); }, py::arg("dtype"));
+  cls.def(
       "to_dtype", [](Impl &self, at::ScalarType dtype) { self.to(dtype); }, py::arg("dtype"));
   cls.def("zero_grad", [](Impl &self) { self.zero_grad(); });
   cls.def("reset", [](Impl &self) { self.reset(); });
@@ -237,16 +239,28 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
       .def_property_readonly("dimension", &SparseTensor::dimension)
       .def_property_readonly("device", &SparseTensor::device)
       .def_property_readonly("dtype", &SparseTensor::dtype)
+      .def_property_readonly("requires_grad", &SparseTensor::requires_grad)
+      .def_property_readonly("shape",
+                             [](const SparseTensor &s) {
+                               return py::make_tuple(s.F().size(0), s.F().size(1));
+                             })
       .def("__len__", [](const SparseTensor &s) { return s.F().size(0); })
       .def("__add__", [](const SparseTensor &s, double v) { return s + v; })
+      .def("__radd__", [](const SparseTensor &s, double v) { return s + v; })
       .def("__mul__", [](const SparseTensor &s, double v) { return s * v; })
+      .def("__rmul__", [](const SparseTensor &s, double v) { return s * v; })
       .def("__iadd__", [](SparseTensor &s, const SparseTensor &o) -> SparseTensor & {
         return s += o;
       })
       .def("detach", &SparseTensor::detach)
-      .def("to_dtype", py::overload_cast<c10::ScalarType>(&SparseTensor::to, py::const_))
       .def("to", py::overload_cast<torch::Device>(&SparseTensor::to, py::const_),
            py::arg("device"))
+      .def("to", py::overload_cast<c10::ScalarType>(&SparseTensor::to, py::const_),
+           py::arg("dtype"))
+      .def("float", &SparseTensor::float_)
+      .def("double", &SparseTensor::double_)
+      // earlier spelling of to(dtype), kept as an alias
+      .def("to_dtype", py::overload_cast<c10::ScalarType>(&SparseTensor::to, py::const_))
       .def("__repr__", [](const SparseTensor &s) {
         return "SparseTensor(rows=" + std::to_string(s.F().size(0)) +
                ", channels=" + std::to_string(s.F().size(1)) + ", " +

@@ -21,12 +21,20 @@ int32_t rhip_dtype(const at::Tensor &t) {
               t.scalar_type());
 }
 
+// Workspace of a layer's calls; with_dw false: the forward, input-gradient
+// and bias-gradient calls only (the front of the full layout).
 at::Tensor conv_workspace(int32_t K, int64_t cin, int64_t cout, int32_t dt, int64_t n_in,
-                          int64_t n_out, int64_t n_pairs, const at::Device &dev) {
+                          int64_t n_out, int64_t n_pairs, bool with_dw, const at::Device &dev) {
   size_t bytes = 0;
-  check_rhip(rhip_conv_workspace_bytes(K, static_cast<int32_t>(cin), static_cast<int32_t>(cout),
-                                       dt, n_in, n_out, n_pairs, &bytes),
-             "rhip_conv_workspace_bytes");
+  if (with_dw)
+    check_rhip(rhip_conv_workspace_bytes(K, static_cast<int32_t>(cin), static_cast<int32_t>(cout),
+                                         dt, n_in, n_out, n_pairs, &bytes),
+               "rhip_conv_workspace_bytes");
+  else
+    check_rhip(rhip_conv_forward_workspace_bytes(K, static_cast<int32_t>(cin),
+                                                 static_cast<int32_t>(cout), dt, n_in, n_out,
+                                                 &bytes),
+               "rhip_conv_forward_workspace_bytes");
   return torch::empty({static_cast<int64_t>(bytes)},
                       torch::TensorOptions().dtype(torch::kUInt8).device(dev));
 }
@@ -34,11 +42,13 @@ at::Tensor conv_workspace(int32_t K, int64_t cin, int64_t cout, int32_t dt, int6
 using torch::autograd::AutogradContext;
 using torch::autograd::tensor_list;
 
-// Inputs after (features, kernel) are the kernel map's index tensors; they
-// are integer tensors, so autograd gives them no gradient.
+// Inputs after (features, kernel, bias) are the kernel map's index tensors;
+// they are integer tensors, so autograd gives them no gradient. bias is fp32
+// [cout], or empty for none (autograd needs a defined tensor for every
+// input); the forward adds it to the fp32 sums before rounding.
 struct HipConvolutionFunction : public torch::autograd::Function<HipConvolutionFunction> {
   static at::Tensor forward(AutogradContext *ctx, at::Tensor features, at::Tensor kernel,
-                            at::Tensor nbr, at::Tensor out_order, at::Tensor nbr_t,
+                            at::Tensor bias, at::Tensor nbr, at::Tensor out_order, at::Tensor nbr_t,
                             at::Tensor in_order, at::Tensor offsets, at::Tensor in_rows,
                             at::Tensor out_rows, int64_t n_out, int64_t n_pairs) {
     TORCH_CHECK(features.is_cuda() && kernel.is_cuda(),
@@ -54,9 +64,16 @@ struct HipConvolutionFunction : public torch::autograd::Function<HipConvolutionF
     TORCH_CHECK(x.size(1) == cin, "feature channels ", x.size(1), " != kernel in-channels ", cin);
     const int32_t dt = rhip_dtype(x);
     auto y = torch::empty({n_out, cout}, x.options());
-    auto ws = conv_workspace(K, cin, cout, dt, n_in, n_out, n_pairs, dev);
+    auto ws = conv_workspace(K, cin, cout, dt, n_in, n_out, n_pairs, false, dev);
+    const bool has_bias = bias.numel() > 0;
+    if (has_bias)
+      TORCH_CHECK(bias.is_cuda() && bias.scalar_type() == torch::kFloat &&
+                      bias.numel() == cout && bias.is_contiguous(),
+                  "bias must be a contiguous fp32 device tensor of ", cout, " values");
     check_rhip(rhip_conv_forward(x.data_ptr(), n_in, static_cast<int32_t>(cin), w.data_ptr(), K,
-                                 static_cast<int32_t>(cout), nullptr, nbr.data_ptr<int32_t>(),
+                                 static_cast<int32_t>(cout),
+                                 has_bias ? bias.data_ptr<float>() : nullptr,
+                                 nbr.data_ptr<int32_t>(),
                                  out_order.data_ptr<int32_t>(), n_out, y.data_ptr(), dt,
                                  ws.data_ptr(), ws.numel(),
                                  c10::hip::getCurrentHIPStream(dev.index()).stream()),
@@ -64,6 +81,7 @@ struct HipConvolutionFunction : public torch::autograd::Function<HipConvolutionF
     ctx->save_for_backward({x, w, nbr_t, in_order, offsets, in_rows, out_rows, nbr, out_order});
     ctx->saved_data["n_pairs"] = n_pairs;
     ctx->saved_data["n_out"] = n_out;
+    ctx->saved_data["has_bias"] = has_bias;
     return y;
   }
 
@@ -81,8 +99,15 @@ struct HipConvolutionFunction : public torch::autograd::Function<HipConvolutionF
     const int32_t K = static_cast<int32_t>(w.size(0));
     const int64_t cin = w.size(1), cout = w.size(2), n_in = x.size(0);
     const int32_t dt = rhip_dtype(x);
-    auto ws = conv_workspace(K, cin, cout, dt, n_in, n_out, n_pairs, dev);
-    at::Tensor gx, gw;
+    const bool need_dw = ctx->needs_input_grad(1);
+    auto ws = conv_workspace(K, cin, cout, dt, n_in, n_out, n_pairs, need_dw, dev);
+    at::Tensor gx, gw, gb;
+    if (ctx->saved_data["has_bias"].toBool() && ctx->needs_input_grad(2)) {
+      gb = torch::empty({cout}, x.options().dtype(torch::kFloat));
+      check_rhip(rhip_conv_bias_grad(gy.data_ptr(), n_out, static_cast<int32_t>(cout), dt,
+                                     gb.data_ptr<float>(), ws.data_ptr(), ws.numel(), st),
+                 "rhip_conv_bias_grad");
+    }
     if (ctx->needs_input_grad(0)) {
       gx = torch::empty_like(x);
       check_rhip(rhip_conv_backward_input(gy.data_ptr(), n_out, static_cast<int32_t>(cout),
@@ -92,7 +117,7 @@ struct HipConvolutionFunction : public torch::autograd::Function<HipConvolutionF
                                           ws.data_ptr(), ws.numel(), st),
                  "rhip_conv_backward_input");
     }
-    if (ctx->needs_input_grad(1)) {
+    if (need_dw) {
       gw = torch::empty_like(w);
       // dW from the neighbour table where the library has a kernel for the
       // shape (K <= 8 or K >= 20 with C_in % 16 and C_out % 32; narrow bf16),
@@ -113,19 +138,22 @@ struct HipConvolutionFunction : public torch::autograd::Function<HipConvolutionF
                                        gw.data_ptr(), dt, ws.data_ptr(), ws.numel(), st);
       check_rhip(rc, "rhip_conv_backward_weight(_rows)");
     }
-    return {gx, gw, {}, {}, {}, {}, {}, {}, {}, {}, {}};
+    return {gx, gw, gb, {}, {}, {}, {}, {}, {}, {}, {}, {}};
   }
 };
 
 } // namespace
 
 at::Tensor hip_sparse_convolution(const at::Tensor &features, const at::Tensor &kernel,
-                                  const HipKernelMap &map) {
+                                  const HipKernelMap &map, const at::Tensor &bias) {
   TORCH_CHECK(kernel.dim() == 3 && kernel.size(0) == map.K, "kernel volume ", kernel.size(0),
               " does not match the kernel map's ", map.K, " offsets");
   TORCH_CHECK(features.size(0) == map.n_in, "feature rows ", features.size(0),
               " != input map size ", map.n_in);
-  return HipConvolutionFunction::apply(features, kernel, map.nbr, map.out_order, map.nbr_t,
+  const at::Tensor b =
+      bias.defined() ? bias
+                     : torch::empty({0}, features.options().dtype(torch::kFloat));
+  return HipConvolutionFunction::apply(features, kernel, b, map.nbr, map.out_order, map.nbr_t,
                                        map.in_order, map.offsets, map.in_rows, map.out_rows,
                                        map.n_out, map.size());
 }
@@ -200,9 +228,11 @@ SparseTensor RiemannConvolutionBaseImpl::forward(const SparseTensor &input) {
       input.coordinate_map_key(), output_key, params.kernel_size, params.kernel_stride,
       params.kernel_dilation, params.region_type, params.region_offsets, is_transpose_, false);
   const auto &x = input.F();
-  auto result = hip_sparse_convolution(x, kernel_.to(x.scalar_type()), map);
-  if (bias_.defined())
-    result = result + bias_.to(result.scalar_type());
+  // the bias is added in the kernel, to the fp32 sums (conv.cpp:135-136 adds
+  // it to the output afterwards)
+  auto result = hip_sparse_convolution(
+      x, kernel_.to(x.scalar_type()), map,
+      bias_.defined() ? bias_.to(torch::kFloat).reshape({-1}) : at::Tensor());
   return SparseTensor(std::move(result), output_key, std::move(manager));
 }
 

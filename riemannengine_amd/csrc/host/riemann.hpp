@@ -310,6 +310,8 @@ public:
   SparseTensor operator+(at::Scalar scalar) const;
   SparseTensor operator*(at::Scalar scalar) const;
   SparseTensor to(c10::ScalarType dtype) const;
+  SparseTensor float_() const;
+  SparseTensor double_() const;
   // Re-hash onto `device` (RiemannEngine/engine/tensor/sparse_tensor.cpp:
   // 397-429): a new manager holding this map's rows, features aligned to its
   // representative rows. Device targets only (there is no CPU manager).
@@ -317,6 +319,8 @@ public:
   SparseTensor detach() const;
 
 private:
+  // The same map and manager with other features.
+  SparseTensor with_features(at::Tensor features) const;
   static at::Tensor quantize_features(const at::Tensor &features, const at::Tensor &first_rows,
                                       const at::Tensor &row_to_unique, int64_t unique_count,
                                       SparseTensorQuantizationMode::Type mode);
@@ -330,11 +334,12 @@ private:
 
 // ---------------------------------------------------------------- layers
 
-// Y = sum_k X[in_k] @ W[k] over the map, with its input and weight
-// gradients, through the HIP kernels (autograd-aware). features and kernel
-// must share the dtype (fp32 or bf16).
+// Y = sum_k X[in_k] @ W[k] (+ bias) over the map, with its input, weight and
+// bias gradients, through the HIP kernels (autograd-aware). features and
+// kernel must share the dtype (fp32 or bf16); bias is an fp32 [cout] tensor
+// or undefined.
 at::Tensor hip_sparse_convolution(const at::Tensor &features, const at::Tensor &kernel,
-                                  const HipKernelMap &map);
+                                  const HipKernelMap &map, const at::Tensor &bias = at::Tensor());
 
 class RiemannConvolutionBaseImpl : public torch::nn::Cloneable<RiemannConvolutionBaseImpl> {
 public:

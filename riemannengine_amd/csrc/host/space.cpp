@@ -424,7 +424,8 @@ CoordinateManager::stride_region(const CoordinateMapKey &in_key, const at::Tenso
 
 const CoordinateMapHIP &CoordinateManager::coordinate_map(const CoordinateMapKey &key) const {
   auto it = maps_.find(key.get_key());
-  TORCH_CHECK(it != maps_.end(), "coordinate map not found: ", key.to_string());
+  // the reference ASSERTs with ERROR_MAP_NOT_FOUND (engine/foundation/errors.hpp:13)
+  TORCH_CHECK(it != maps_.end(), "CoordinateMap not found: ", key.to_string());
   return it->second;
 }
 

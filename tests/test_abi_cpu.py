@@ -50,6 +50,11 @@ def test_workspace_queries():
     wide = abi._sizeq(L.rhip_conv_workspace_bytes, 27, 256, 256, abi.BF16, 1000, 1000, 0)
     assert wide >= 27 * 256 * 256 * (2 + 4) + 2 * 1000 * 256 * 4
     assert L.rhip_table_bytes(100) == 256 * 16  # next power of two >= 2n, 16 B slots
+    # forward / dX / dbias alone: transposed weights and the bias chunk sums,
+    # without the dW partial tiles and accumulator behind them
+    fwd = abi._sizeq(L.rhip_conv_forward_workspace_bytes, 27, 64, 64, abi.BF16, 10**5, 10**5)
+    full = abi._sizeq(L.rhip_conv_workspace_bytes, 27, 64, 64, abi.BF16, 10**5, 10**5, 10**6)
+    assert 27 * 64 * 64 * 2 + 256 * 64 * 4 <= fwd < full - 27 * 64 * 64 * 4
 
 
 @pytest.mark.parametrize("call,msg", [

@@ -409,6 +409,20 @@ def test_config2_full_size_vs_torch(dtype):
     assert_rel(gw_timed.float().cpu().numpy(), rgw.cpu().numpy(), tol, "dW (timed dispatch)")
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_bias_gradient_column_sums(dtype):
+    """rhip_conv_bias_grad: fp32 column sums in a fixed order, for row counts
+    below and above one row per chunk and channel counts below, at and above
+    one workgroup's 256 threads; bitwise repeatable."""
+    g = torch.Generator(device="cpu").manual_seed(9)
+    for n, C in ((1, 3), (100, 64), (5000, 5), (300000, 64), (2000, 300)):
+        gy = torch.randn((n, C), generator=g).to(DEV, dtype)
+        got = abi.conv_bias_grad(gy)
+        ref = gy.double().sum(0).float()
+        assert_rel(got.cpu().numpy(), ref.cpu().numpy(), 1e-5, f"dbias n={n} C={C}")
+        assert torch.equal(got, abi.conv_bias_grad(gy))
+
+
 def test_resident_weight_kernel_on_large_maps():
     """bf16 maps of at least 131072 output rows whose weights for all output
     columns fit in LDS take the resident-weight kernel: a 3^3 same-set map

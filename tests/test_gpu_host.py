@@ -159,13 +159,65 @@ def test_strided_then_transposed(dtype):
     assert_rel(_np(up.kernel.grad), rgw, tol, "up dW")
 
 
-def test_transposed_without_finer_map_fails():
+def test_transposed_stride_must_divide_tensor_stride():
     c, _, _ = oracle.insert_and_map(_cloud(4, dup=0))
     x = re_.SparseTensor(torch.randn(len(c), 4, device=DEV), torch.from_numpy(c).to(DEV))
     up = re_.nn.RiemannConvolutionTranspose(4, 4, kernel_size=2, stride=2)
     up.to(DEV)
     with pytest.raises(RuntimeError, match="stride must divide"):
         up(x)
+
+
+def test_transposed_without_finer_map_fails():
+    """A transposed convolution maps onto the finer map {tensor_stride / s,
+    same id}; when the manager holds no such map the reference ASSERTs with
+    ERROR_MAP_NOT_FOUND (space_impl.hpp:576-578)."""
+    c, _, _ = oracle.insert_and_map(_cloud(4, dup=0))
+    c[:, 1:] *= 2  # coordinates of a tensor-stride-2 map
+    mgr = re_.CoordinateManager(3)
+    key, _ = mgr.insert_and_map(torch.from_numpy(c).to(DEV), [2, 2, 2])
+    x = re_.SparseTensor(torch.randn(len(c), 4, device=DEV), key, mgr)
+    assert x.tensor_stride == [2, 2, 2]
+    up = re_.nn.RiemannConvolutionTranspose(4, 4, kernel_size=2, stride=2)
+    up.to(DEV)
+    with pytest.raises(RuntimeError, match="CoordinateMap not found"):
+        up(x)
+
+
+def test_sparse_tensor_reference_spellings():
+    """The reference's Python surface (python/src/sparse_bindings.cpp:
+    149-191): shape, requires_grad, to(dtype) beside to(device), float(),
+    double(), scalar arithmetic from either side; module.to(dtype)."""
+    c, _, _ = oracle.insert_and_map(_cloud(6, dup=0))
+    f = torch.randn(len(c), 8, device=DEV)
+    x = re_.SparseTensor(f, torch.from_numpy(c).to(DEV))
+    assert x.shape == (len(c), 8) and x.requires_grad is False
+    assert re_.SparseTensor(f.clone().requires_grad_(True), torch.from_numpy(c).to(DEV)).requires_grad
+    b = x.to(torch.bfloat16)
+    assert b.dtype == torch.bfloat16 and b.coordinate_map_key == x.coordinate_map_key
+    assert b.float().dtype == torch.float32 and x.double().dtype == torch.float64
+    assert torch.equal(x.to(torch.device("cuda:0")).F, x.F)
+    assert torch.equal((2.0 * x).F, 2.0 * x.F) and torch.equal((1.0 + x).F, x.F + 1.0)
+    conv = re_.nn.RiemannConvolution(8, 4, kernel_size=3)
+    conv.to(DEV)
+    conv.to(torch.bfloat16)
+    assert conv.kernel.dtype == torch.bfloat16
+    assert conv(b).F.dtype == torch.bfloat16
+
+
+def test_quantization_reductions_need_fp32_or_bf16():
+    """Sum / average / max quantization runs on the HIP pooling kernels,
+    which take fp32 or bf16 features; other dtypes are refused, and the
+    row-picking modes take any dtype."""
+    c = _cloud(7, n=500)
+    cd = torch.from_numpy(c).to(DEV)
+    f = torch.randn(len(c), 3, device=DEV, dtype=torch.float64)
+    Q = re_.QuantizationMode
+    with pytest.raises(RuntimeError, match="fp32 or bf16"):
+        re_.SparseTensor(f, cd, quantization_mode=Q.UNWEIGHTED_SUM)
+    uq, mp, _ = oracle.insert_and_map(c)
+    x = re_.SparseTensor(f, cd, quantization_mode=Q.RANDOM_SUBSAMPLE)
+    np.testing.assert_array_equal(x.F.cpu().numpy(), f.cpu().numpy()[mp])
 
 
 def test_convolution_4d():

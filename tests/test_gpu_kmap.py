@@ -244,3 +244,31 @@ def test_generative_expansion_matches_oracle_and_reference(ks, region):
     if ref.available():
         exp = ref.stride_region(coarse, 2, 2, ks, 1, region)
         assert sorted(map(tuple, got.tolist())) == sorted(map(tuple, exp.tolist()))
+
+
+@pytest.mark.parametrize("same", [True, False])
+def test_row_reference_kernel_map(same):
+    """A coordinate set whose column ranges need more than 63 bits builds a
+    row-reference table (whole-row compares); its kernel map comes from
+    kmap_query_kernel. Dense clusters scattered over the full int32 range,
+    so that neighbours exist: the map is bit-exact with the oracle after
+    canonical ordering, same-set (symmetric path) and onto another set."""
+    rng = np.random.default_rng(21)
+    centres = rng.integers(-2**31 + 64, 2**31 - 64, (40, 4), dtype=np.int64)
+    pts = []
+    for cen in centres:
+        pts.append(cen + np.concatenate([rng.integers(0, 2, (300, 1)),
+                                         rng.integers(-6, 7, (300, 3))], 1))
+    c = np.unique(np.concatenate(pts).astype(np.int32), axis=0)
+    c = c[rng.permutation(len(c))]
+    if same:
+        cout = c
+    else:  # half the rows, and shifted copies of a third of them
+        shifted = c[1::3] + np.array([0, 1, 0, 0], np.int32)
+        cout = np.unique(np.concatenate([c[::2], shifted]), axis=0)
+    off = oracle.region_offsets(3, 3)
+    tin, tout, km = gpu_tables_and_map(c, cout, off, same=same)
+    assert tin.struct.mode == abi.KEY_ROWREF
+    _, ref = _ref_map(c, cout, off)
+    np.testing.assert_array_equal(gpu_canonical(km), ref)
+    assert km.n_pairs > len(cout)  # neighbours were found

@@ -317,3 +317,92 @@ def test_basic_block_with_downsample_matches_torch_composition():
     assert_rel(_np(feats.grad), xr.grad.numpy(), 1e-4, "block grad x")
     for k, v in p.items():
         assert_rel(_np(v.grad), leaf[k].grad.numpy(), 1e-4, "block grad " + k)
+
+
+def _torch_conv_gpu(x, w, km):
+    """fp32 gather-GEMM-scatter over a GPU kernel map's per-offset pairs, on
+    the GPU (autograd)."""
+    y = torch.zeros((km.n_out, w.shape[2]), device=x.device, dtype=x.dtype)
+    for k in range(km.K):
+        ir, orr = km.pairs(k)
+        if ir.numel():
+            y = y.index_add(0, orr.long(), x.index_select(0, ir.long()) @ w[k])
+    return y
+
+
+class _RoundBF16(torch.autograd.Function):
+    """Rounds to bf16 in the forward and the gradient to bf16 in the backward:
+    where the bf16 path stores a tensor (or its gradient) in bf16."""
+
+    @staticmethod
+    def forward(ctx, v):
+        return v.to(torch.bfloat16).float()
+
+    @staticmethod
+    def backward(ctx, g):
+        return g.to(torch.bfloat16).float()
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_basic_block_config5_stage1_full_size(dtype):
+    """Config 5's first stage at full size: 8 indoor scenes (808,219 voxels),
+    one BasicBlock(32, 32), forward and backward, against the reference's
+    composition (conv3 -> BN -> ReLU -> conv3 -> BN -> += -> ReLU,
+    residual.cpp:44-52) in fp32 torch on the GPU over the same map's pairs,
+    with the block's own parameters and input.
+
+    fp32: rel 1e-4. bf16: rel 2e-2, against the same composition with its
+    tensors rounded to bf16 where the bf16 path stores them (each conv and
+    batch-norm output and the gradients between the layers): the parameter
+    gradients are sums over 800k rows that cancel to a few per mille of their
+    terms, so bf16 storage alone moves them several percent from fp32.
+
+    Over 26M activations some pre-activations lie within rounding of zero,
+    where the reference's ReLU would decide differently and its gradient
+    element differ by its whole value; the reference therefore takes the
+    HIP path's ReLU decisions: the block output's sign for the last ReLU, and
+    for the inner one the same kernels' conv -> BN -> ReLU recomputed through
+    the C ABI (deterministic kernels on the same operands, same values)."""
+    from riemannengine_amd import scenes
+    c = scenes.indoor_batch(8, 2)
+    torch.manual_seed(8)
+    blk = re_.nn.BasicBlock(32, 32)
+    blk.to(DEV)
+    blk.to(dtype)
+    g = torch.Generator().manual_seed(9)
+    feats = torch.randn(len(c), 32, generator=g).to(DEV, dtype).requires_grad_(True)
+    x = re_.SparseTensor(feats, torch.from_numpy(c).to(DEV))
+    n = len(x)
+    print(f"config-5 stage-1 block n={n} {dtype}", flush=True)
+    assert n == 808219
+    out = blk(x)
+    gy = torch.randn(out.F.shape, generator=g).to(DEV, dtype)
+    (out.F.float() * gy.float()).sum().backward()
+    t = abi.hash_build(x.C.contiguous())
+    km = abi.kernel_map(t, t, oracle.region_offsets(3, 3))
+    p = blk.named_parameters()
+    w1 = p["conv1.base.kernel"].detach()
+    g1, b1 = p["norm1.normalization.weight"].detach(), p["norm1.normalization.bias"].detach()
+    # the inner ReLU's decisions of the HIP path
+    y1 = abi.conv_forward(feats.detach(), w1, km)
+    m1, s1 = abi.bn_stats(y1)
+    mask1 = abi.bn_forward(y1, m1, s1, g1.float(), b1.float(), relu=True) > 0
+    mask2 = out.F.detach() > 0
+    R = _RoundBF16.apply if dtype == torch.bfloat16 else (lambda v: v)
+    leaf = {k: v.detach().float().requires_grad_(True) for k, v in p.items()}
+    xr = feats.detach().float().requires_grad_(True)
+    bn = lambda v, i: F.batch_norm(v, None, None, leaf[f"norm{i}.normalization.weight"],
+                                   leaf[f"norm{i}.normalization.bias"], True, 0.1, 1e-5)
+    z1 = bn(R(_torch_conv_gpu(xr, leaf["conv1.base.kernel"], km)), 1)
+    h = R(z1 * mask1)
+    ref = R((bn(R(_torch_conv_gpu(h, leaf["conv2.base.kernel"], km)), 2) + xr) * mask2)
+    (ref * gy.float()).sum().backward()
+    flips = int(((z1 > 0) != mask1).sum())
+    print(f"inner ReLU decisions that differ from the reference's own: {flips} of "
+          f"{mask1.numel()}", flush=True)
+    assert flips < mask1.numel() // 1000
+    tol = TOL[dtype]
+    assert_rel(_np(out.F), _np(ref), tol, "block y")
+    assert_rel(_np(feats.grad), _np(xr.grad), tol, "block grad x")
+    for k, v in p.items():
+        assert_rel(_np(v.grad), _np(leaf[k].grad), tol, "block grad " + k)
