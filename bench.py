@@ -12,12 +12,18 @@ timed region starts.
 Printed as ONE JSON line:
   value        whole-job Mvoxels/s = N_in / (t_fwd + t_dX + t_dW) / 1e6
   kernel_map_ms  hash build + locality order + kernel map, from device coords
+  kernel_map_roofline  the map build's algorithmic bytes (hash: rows read, slot
+               and row-index writes; map: both sides' rows, one 8-byte probe
+               per query, the pairs and offsets) / kernel_map_ms vs 8 TB/s
+  bf16         the same step in bf16 (fp32 accumulate): its own ms_per_step,
+               breakdown and HBM roofline with measured traffic
   roofline     the dominant kernel's algorithmic FLOP/s (fp32, MFMA-bound) or
                bytes/s (bf16, HBM-bound), from HIP events recorded on the
                stream the kernels run on, against MI355X's published peak
   cpu_baseline the reference's own CPU path (compiled from its sources into
                oracle/_ref) timed on one scene of the same workload, or the
                scalar C oracle where that library was not built
+  cpu_kernel_map_baseline  the reference's CPU map build alone (same sample)
 
 --gpus N > 1 is refused: this build runs on one GPU.
 """
@@ -103,17 +109,22 @@ def conv_traffic(n_in, n_out, P, K, cin, cout, s):
 
 
 def measured_traffic(dtype: str, pass_name: str, record: str = "traffic_config2.json"):
-    """HBM bytes per launch of a pass's kernel, from the committed rocprofv3
-    FETCH_SIZE / WRITE_SIZE passes (profiles/traffic_config2.json for the
-    convolution, traffic_pool.json for pooling; scaled by the counters'
-    reading for a device copy of known size); None if absent."""
+    """(HBM bytes per launch of a pass's kernels, source) from the committed
+    rocprofv3 FETCH_SIZE / WRITE_SIZE passes (profiles/traffic_config2.json for
+    the convolution, traffic_pool.json for pooling), scaled by the counters'
+    reading for a device copy of known size. The source names the record and
+    the commit of the kernels it was taken on; (None, None) if absent."""
     path = os.path.join(ROOT, "profiles", record)
     try:
         with open(path) as f:
-            rec = json.load(f)[dtype][pass_name]
+            doc = json.load(f)
+        rec = doc[dtype][pass_name]
     except (OSError, KeyError, ValueError):
-        return None
-    return round(float(rec["traffic_bytes"]))
+        return None, None
+    src = f"profiles/{record}"
+    if doc.get("kernels_commit"):
+        src += f" (kernels at commit {doc['kernels_commit']})"
+    return round(float(rec["traffic_bytes"])), src
 
 
 def cpu_model() -> str:
@@ -183,6 +194,31 @@ def cpu_baseline(coords, offsets, cin, cout, seed, dtype):
 
 
 # ------------------------------------------------------- other configs
+
+def cpu_map_baseline(coords):
+    """The reference's CPU kernel-map build (insert_and_map, then the 3^3 cube
+    kernel map) on scene 0 of the workload, timed apart from the convolution;
+    None where oracle/_ref was not built (the scalar C oracle's map time is in
+    the cpu_baseline record then)."""
+    from oracle import ref  # CPU baseline only
+    if not ref.available():
+        return None
+    c1 = coords[coords[:, 0] == 0]
+    reps = 3
+    P, hash_ms, map_ms = ref.map_time(c1, ks=3, reps=reps)
+    return {
+        "value": round(len(c1) / ((hash_ms + map_ms) * 1e-3) / 1e6, 4),
+        "unit": "Mvoxels/s",
+        "ms": round(hash_ms + map_ms, 2),
+        "hash_ms": round(hash_ms, 2),
+        "kernel_map_ms": round(map_ms, 2),
+        "cores": ref.num_threads(),
+        "kind": "reference",
+        "sample": (f"scene 0 of the workload: {len(c1)} voxels, P={P}; "
+                   f"CoordinateManager::insert_and_map then the 3^3 kernel map, "
+                   f"mean of {reps} runs from a fresh manager"),
+    }
+
 
 def _timed_passes(passes, steps, warmup):
     """Run the named passes in order `warmup` times, then `steps` times with
@@ -475,7 +511,9 @@ def run_pool(args):
                "global_backward": "gpool_bwd_kernel (avg)"}
     roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
             "frac": round(achieved / PEAK_HBM_GBS, 4),
-            "traffic": measured_traffic(args.dtype, dom, "traffic_pool.json"), "kernel": kernels[dom],
+            "traffic": measured_traffic(args.dtype, dom, "traffic_pool.json")[0],
+            "traffic_source": measured_traffic(args.dtype, dom, "traffic_pool.json")[1],
+            "kernel": kernels[dom],
             "kernel_ms": round(per[dom], 4), "algorithmic": {"bytes": B[dom]}}
     step_ms = sum(per.values())
     t_roof = sum(B.values()) / (PEAK_HBM_GBS * 1e9)
@@ -514,6 +552,7 @@ def main():
     if args.copy_mib > 0:
         copy_calibration(args.copy_mib)
         return
+    args.dtype_given = args.dtype is not None
     if args.dtype is None:
         args.dtype = "bf16" if args.config in (3, 5) else "f32"
     if args.op == "pool":
@@ -531,8 +570,6 @@ def main():
         sys.exit(1)
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
-    dt = torch.float32 if args.dtype == "f32" else torch.bfloat16
-    s = 4 if args.dtype == "f32" else 2
     cin = cout = 64
 
     # ---------------------------------------------------------- workload
@@ -557,7 +594,67 @@ def main():
     kmap_ms = statistics.median(map_ms[1:])
     n_in = n_out = km.n_in
     P = km.n_pairs
+    D = coords_np.shape[1] - 1
+    # algorithmic bytes of the map build: hash build (read the rows, one slot
+    # write, one row index) and map (read both sides' rows, one 8-byte probe
+    # per query, write the pairs and the offsets)
+    b_hash = len(coords_np) * (D + 1) * 4 + len(coords_np) * 8 + len(coords_np) * 4
+    b_map = (n_in + n_out) * (D + 1) * 4 + K * n_out * 8 + 8 * P + 4 * (K + 1)
+    map_gbs = (b_hash + b_map) / (kmap_ms * 1e-3) / 1e9
+    kmap_roof = {"bound": "hbm", "achieved": round(map_gbs, 1), "peak": PEAK_HBM_GBS,
+                 "unit": "GB/s", "frac": round(map_gbs / PEAK_HBM_GBS, 4),
+                 "algorithmic": {"hash_bytes": b_hash, "map_bytes": b_map},
+                 "ms": round(kmap_ms, 3),
+                 "note": "host clock around the build calls, which read sizes back to the host"}
 
+    dtypes = [args.dtype] if args.dtype_given else ["f32", "bf16"]
+    records = {dt_name: conv_step_record(args, dt_name, km, n_in, n_out, P, K, cin, cout)
+               for dt_name in dtypes}
+    head = records[dtypes[0]]
+    line = {
+        "metric": "sparse conv fwd+bwd Mvoxels/s @3^3 C64",
+        "value": head["value"],
+        "unit": "Mvoxels/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": head["ms_per_step"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": dtypes[0],
+        "data": "synthetic (seeded indoor scenes; random N(0,1) features, Kaiming-normal weights)",
+        "config": {"workload": "config 2: indoor scenes batch 4, 3^3 stride-1 conv C64->64, "
+                               "fwd+dX+dW, kernel map prebuilt",
+                   "n_voxels": n_in, "pairs": P, "offsets": K, "c_in": cin, "c_out": cout,
+                   "seed": args.seed, "accumulate": "f32"},
+        "kernel_map_ms": round(kmap_ms, 3),
+        "kernel_map_roofline": kmap_roof,
+        "breakdown_ms": head["breakdown_ms"],
+        "step_roofline": head["step_roofline"],
+        "roofline": head["roofline"],
+    }
+    for dt_name in dtypes[1:]:
+        line[dt_name] = records[dt_name]
+    if not args.no_cpu_baseline:
+        line["cpu_baseline"] = cpu_baseline(coords_np, offsets_np, cin, cout, args.seed,
+                                            dtypes[0])
+        line["cpu_kernel_map_baseline"] = cpu_map_baseline(coords_np)
+    else:
+        line["cpu_baseline"] = None
+    print(json.dumps(line), flush=True)
+
+
+def conv_step_record(args, dtype, km, n_in, n_out, P, K, cin, cout):
+    """Config 2 in one dtype: Mvoxels/s over the timed steps (forward, dX and
+    dW through the C ABI, the map prebuilt), the per-pass event times, the
+    whole-step roofline and the dominant pass's roofline with its measured
+    HBM traffic."""
+    import torch
+    from riemannengine_amd import abi
+    dev = torch.device("cuda:0")
+    dt = torch.float32 if dtype == "f32" else torch.bfloat16
+    s = 4 if dtype == "f32" else 2
     g = torch.Generator(device="cpu").manual_seed(args.seed)
     x = torch.randn((n_in, cin), generator=g).to(dev, dt)
     w = (torch.randn((K, cin, cout), generator=g) * (2.0 / (cin * K)) ** 0.5).to(dev, dt)
@@ -596,19 +693,19 @@ def main():
     dom = max(names, key=lambda n: per[n])
     F, B = work[dom]
     dur_s = per[dom] * 1e-3
-    if args.dtype == "f32":
+    if dtype == "f32":
         roof = {"bound": "mfma", "achieved": round(F / dur_s / 1e12, 3),
                 "peak": PEAK_TFLOPS["f32"], "unit": "TFLOP/s"}
     else:
         roof = {"bound": "hbm", "achieved": round(B / dur_s / 1e9, 1),
                 "peak": PEAK_HBM_GBS, "unit": "GB/s"}
     roof["frac"] = round(roof["achieved"] / roof["peak"], 4)
-    roof["traffic"] = measured_traffic(args.dtype, dom)
+    roof["traffic"], roof["traffic_source"] = measured_traffic(dtype, dom)
     roof["kernel"] = {"forward": "conv_os_kernel (forward)",
                       "backward_input": "conv_os_kernel (dX)",
                       "backward_weight": (
                           "conv_dw_pos_kernel + conv_dw_rows_reduce_kernel (dW pass)"
-                          if args.dtype == "f32" else
+                          if dtype == "f32" else
                           "conv_dw_pos_bf16_kernel + conv_dw_rows_reduce_kernel (dW pass)")}[dom]
     roof["kernel_ms"] = round(per[dom], 4)
     roof["algorithmic"] = {"flop": F, "bytes": B}
@@ -616,40 +713,19 @@ def main():
     # whole-step roofline: max(compute, memory) time at peak / measured
     Ft = sum(v[0] for v in work.values())
     Bt = sum(v[1] for v in work.values())
-    t_roof = max(Ft / (PEAK_TFLOPS[args.dtype] * 1e12), Bt / (PEAK_HBM_GBS * 1e9))
+    t_roof = max(Ft / (PEAK_TFLOPS[dtype] * 1e12), Bt / (PEAK_HBM_GBS * 1e9))
     step_ms_events = sum(per.values())
-
-    value = n_in / (ms_per_step * 1e-3) / 1e6
-    line = {
-        "metric": "sparse conv fwd+bwd Mvoxels/s @3^3 C64",
-        "value": round(value, 3),
+    return {
+        "value": round(n_in / (ms_per_step * 1e-3) / 1e6, 3),
         "unit": "Mvoxels/s",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
+        "dtype": dtype,
         "ms_per_step": round(ms_per_step, 4),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": args.dtype,
-        "data": "synthetic (seeded indoor scenes; random N(0,1) features, Kaiming-normal weights)",
-        "config": {"workload": "config 2: indoor scenes batch 4, 3^3 stride-1 conv C64->64, "
-                               "fwd+dX+dW, kernel map prebuilt",
-                   "n_voxels": n_in, "pairs": P, "offsets": K, "c_in": cin, "c_out": cout,
-                   "seed": args.seed, "accumulate": "f32"},
-        "kernel_map_ms": round(kmap_ms, 3),
         "breakdown_ms": {n: round(per[n], 4) for n in names},
         "step_roofline": {"t_roof_ms": round(t_roof * 1e3, 4),
                           "frac": round(t_roof * 1e3 / step_ms_events, 4),
                           "flop": Ft, "bytes": Bt},
         "roofline": roof,
     }
-    if not args.no_cpu_baseline:
-        line["cpu_baseline"] = cpu_baseline(coords_np, offsets_np, cin, cout, args.seed,
-                                            args.dtype)
-    else:
-        line["cpu_baseline"] = None
-    print(json.dumps(line), flush=True)
 
 
 if __name__ == "__main__":

@@ -46,6 +46,10 @@ def lib():
                                     ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
                                     ctypes.POINTER(ctypes.c_double),
                                     ctypes.POINTER(ctypes.c_double)]
+        L.ref_map_time.restype = _i64
+        L.ref_map_time.argtypes = [_vp, _i64, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                   ctypes.POINTER(ctypes.c_double),
+                                   ctypes.POINTER(ctypes.c_double)]
         L.ref_stride_region.restype = _i64
         L.ref_stride_region.argtypes = [_vp, _i64, ctypes.c_int, ctypes.c_int, ctypes.c_int,
                                         ctypes.c_int, ctypes.c_int, ctypes.c_int, _i64, _vp]
@@ -138,6 +142,17 @@ def conv_time(coords, cin, cout, ks=3, bf16=False, reps=3, seed=0):
     P = _check(lib().ref_conv_time(_p(c), n, ncol, cin, cout, ks, 1 if bf16 else 0, reps, seed,
                                    ctypes.byref(map_ms), ctypes.byref(step_ms)))
     return P, map_ms.value, step_ms.value
+
+
+def map_time(coords, ks=3, reps=3):
+    """(pairs, hash ms, kernel-map ms) of the reference's CPU map build over
+    the rows `coords`: insert_and_map, then the ks^D cube kernel map, each the
+    mean of `reps` runs from a fresh manager."""
+    c = np.ascontiguousarray(coords, np.int32)
+    n, ncol = c.shape
+    h, m = ctypes.c_double(0), ctypes.c_double(0)
+    P = _check(lib().ref_map_time(_p(c), n, ncol, ks, reps, ctypes.byref(h), ctypes.byref(m)))
+    return P, h.value, m.value
 
 
 def stride_region(coords, in_stride, stride, ks, dilation=1, region="cube"):

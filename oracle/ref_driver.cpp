@@ -198,6 +198,42 @@ int64_t ref_stride_region(const int32_t *coords, int64_t n, int ncol, int in_str
   });
 }
 
+// Times the reference's CPU kernel-map build alone, the work the GPU's
+// hash build + kernel map replace: CoordinateManager::insert_and_map over the
+// rows (the coordinate hash), then CpuManager::kernel_map for a ks^D stride-1
+// cube over that map (lattice_cpu.hpp's neighbour search). Each of `reps`
+// runs starts from a fresh manager; the means go to *hash_ms and *map_ms.
+// Returns the pair count.
+int64_t ref_map_time(const int32_t *coords, int64_t n, int ncol, int ks, int reps,
+                     double *hash_ms, double *map_ms) {
+  return guarded([&]() -> int64_t {
+    const int D = ncol - 1;
+    const auto rows = int_rows(coords, n, ncol);
+    const riemann::stride_type one(static_cast<size_t>(D), 1);
+    using clock = std::chrono::steady_clock;
+    double th = 0.0, tm = 0.0;
+    int64_t P = 0;
+    for (int r = 0; r < std::max(reps, 1); ++r) {
+      riemann::CoordinateManager m(D, riemann::CoordinateMapBackend::CPU);
+      auto t0 = clock::now();
+      auto key = m.insert_and_map(rows, one).first;
+      auto t1 = clock::now();
+      const auto &map = m.manager_ptr<CpuManager>()->kernel_map(
+          &key, &key, riemann::stride_type(static_cast<size_t>(D), ks), one, one,
+          riemann::RegionType::HYPER_CUBE, at::Tensor(), false, false);
+      auto t2 = clock::now();
+      th += std::chrono::duration<double, std::milli>(t1 - t0).count();
+      tm += std::chrono::duration<double, std::milli>(t2 - t1).count();
+      P = 0;
+      for (const auto &v : map.first)
+        P += static_cast<int64_t>(v.size());
+    }
+    *hash_ms = th / std::max(reps, 1);
+    *map_ms = tm / std::max(reps, 1);
+    return P;
+  });
+}
+
 // Times the reference on the CPU: one RiemannConvolution forward (which
 // builds and caches the kernel map) into *map_ms, then `reps` forward +
 // backward steps reusing the cached map, their mean into *step_ms. Random
