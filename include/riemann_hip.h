@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define RHIP_ABI_VERSION 11
+#define RHIP_ABI_VERSION 12
 #define RHIP_MAX_COLS 8 /* batch column + up to 7 spatial axes */
 
 typedef enum rhip_status {
@@ -65,6 +65,20 @@ typedef struct rhip_table {
   int32_t lo[RHIP_MAX_COLS];
   int32_t hi[RHIP_MAX_COLS];
   int32_t shift[RHIP_MAX_COLS];
+  /* Trailing zero bits common to every (c - lo[c]) of a column (coordinates
+   * at tensor stride 2^s have s); the locality key drops them. */
+  int32_t tz[RHIP_MAX_COLS];
+  /* Brick index, set by rhip_spatial_order when it is given brick storage
+   * (else bricks is NULL): the unique rows in locality order, and a dense
+   * grid over the bounding box of bricks of 2^(brick_levels * D) cells, each
+   * entry a 64-bit occupancy mask of the brick's cells and the locality-order
+   * position of its first row. A neighbour query reads one entry and a
+   * popcount instead of probing the hash table. */
+  const int32_t *order;
+  void *bricks;
+  int32_t morton_bits;  /* bits per spatial column of the locality key */
+  int32_t brick_levels; /* Morton levels inside a brick */
+  int32_t brick_dims[RHIP_MAX_COLS]; /* grid extent per column (0: batch) */
 } rhip_table;
 
 /* ---------------------------------------------------------------- misc */
@@ -107,14 +121,21 @@ int rhip_hash_lookup(const rhip_table *table, const int32_t *queries,
 /*
  * Locality order of a table's unique rows: order[j] is the row processed at
  * position j, pos is its inverse. Rows are sorted by batch, then by the
- * Morton (bit-interleaved) code of their spatial columns when that fits in
- * 63 bits, else by the packed key (x, then y, then z); identity in
- * RHIP_KEY_ROWREF mode. Used to order output rows so that neighbouring
- * positions have neighbouring rows; it does not renumber rows.
+ * Morton (bit-interleaved) code of their spatial columns, (c - lo) >> tz
+ * each, when that fits in 63 bits, else by the packed key (x, then y, then
+ * z); identity in RHIP_KEY_ROWREF mode. Used to order output rows so that
+ * neighbouring positions have neighbouring rows; it does not renumber rows.
+ *
+ * With brick storage (rhip_brick_bytes(table) bytes, non-zero) and a Morton
+ * order, also builds the table's brick index over `order` (which must then
+ * outlive the table's use in kernel maps) and records it in *table; bricks
+ * NULL or 0 bytes leave table->bricks NULL. rhip_brick_bytes is 0 when the
+ * bounding box of bricks exceeds 16 entries per row or 2^23 entries.
  */
 int rhip_order_workspace_bytes(int64_t n, size_t *bytes);
-int rhip_spatial_order(const rhip_table *table, int32_t *order, int32_t *pos,
-                       void *workspace, size_t workspace_bytes,
+int rhip_brick_bytes(const rhip_table *table, size_t *bytes);
+int rhip_spatial_order(rhip_table *table, int32_t *order, int32_t *pos, void *bricks,
+                       size_t brick_bytes, void *workspace, size_t workspace_bytes,
                        hipStream_t stream);
 
 /*

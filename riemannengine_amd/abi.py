@@ -29,7 +29,8 @@ POOL_MODES = {"sum": POOL_SUM, "avg": POOL_AVG, "max": POOL_MAX, "max_scatter": 
 EXPORTS = (
     "rhip_last_error", "rhip_abi_version", "rhip_table_bytes",
     "rhip_hash_workspace_bytes", "rhip_hash_build", "rhip_hash_lookup",
-    "rhip_order_workspace_bytes", "rhip_spatial_order", "rhip_stride_coords",
+    "rhip_order_workspace_bytes", "rhip_brick_bytes", "rhip_spatial_order",
+    "rhip_stride_coords",
     "rhip_expand_coords", "rhip_kmap_workspace_bytes", "rhip_kmap_count", "rhip_kmap_fill",
     "rhip_conv_workspace_bytes", "rhip_conv_forward_workspace_bytes", "rhip_conv_forward",
     "rhip_conv_forward_noalloc", "rhip_conv_bias_grad",
@@ -52,7 +53,10 @@ class RhipTable(ctypes.Structure):
         ("ncol", ctypes.c_int32), ("mode", ctypes.c_int32),
         ("key_bits", ctypes.c_int32),
         ("lo", ctypes.c_int32 * MAX_COLS), ("hi", ctypes.c_int32 * MAX_COLS),
-        ("shift", ctypes.c_int32 * MAX_COLS),
+        ("shift", ctypes.c_int32 * MAX_COLS), ("tz", ctypes.c_int32 * MAX_COLS),
+        ("order", ctypes.c_void_p), ("bricks", ctypes.c_void_p),
+        ("morton_bits", ctypes.c_int32), ("brick_levels", ctypes.c_int32),
+        ("brick_dims", ctypes.c_int32 * MAX_COLS),
     ]
 
 
@@ -70,7 +74,8 @@ def _declare(lib):
                                            _vp, _vp, _P(RhipTable), _vp]),
         "rhip_hash_lookup": (ctypes.c_int, [_P(RhipTable), _vp, _i64, _vp, _vp]),
         "rhip_order_workspace_bytes": (ctypes.c_int, [_i64, _P(_sz)]),
-        "rhip_spatial_order": (ctypes.c_int, [_P(RhipTable), _vp, _vp, _vp, _sz, _vp]),
+        "rhip_brick_bytes": (ctypes.c_int, [_P(RhipTable), _P(_sz)]),
+        "rhip_spatial_order": (ctypes.c_int, [_P(RhipTable), _vp, _vp, _vp, _sz, _vp, _sz, _vp]),
         "rhip_stride_coords": (ctypes.c_int, [_vp, _i64, _i32, _P(_i32), _vp, _vp]),
         "rhip_expand_coords": (ctypes.c_int, [_vp, _i64, _i32, _vp, _i32, _vp, _vp]),
         "rhip_kmap_workspace_bytes": (ctypes.c_int, [_i64, _i64, _i32, _P(_sz)]),
@@ -235,15 +240,22 @@ def hash_build(coords: torch.Tensor, with_inverse: bool = True,
     nu = int(st.n_unique)
     order = torch.empty(max(nu, 1), dtype=torch.int32, device=dev)
     pos = torch.empty(max(nu, 1), dtype=torch.int32, device=dev)
+    keep = []
     if with_order and nu > 0:
         ows = torch.empty(_sizeq(L.rhip_order_workspace_bytes, nu), dtype=torch.uint8, device=dev)
-        _check(L.rhip_spatial_order(ctypes.byref(st), _ptr(order), _ptr(pos), _ptr(ows),
-                                    ows.numel(), _stream(dev)), "rhip_spatial_order")
+        bb = ctypes.c_size_t(0)
+        _check(L.rhip_brick_bytes(ctypes.byref(st), ctypes.byref(bb)), "rhip_brick_bytes")
+        bricks = torch.empty(max(int(bb.value), 1), dtype=torch.uint8, device=dev)
+        keep.append(bricks)
+        _check(L.rhip_spatial_order(ctypes.byref(st), _ptr(order), _ptr(pos), _ptr(bricks),
+                                    int(bb.value), _ptr(ows), ows.numel(), _stream(dev)),
+               "rhip_spatial_order")
     elif nu > 0:
         torch.arange(nu, out=order[:nu])
         pos[:nu].copy_(order[:nu])
     return CoordTable(st, slots, ucoords[:nu], mapping[:nu],
-                      inverse[:n] if inverse is not None else None, order[:nu], pos[:nu])
+                      inverse[:n] if inverse is not None else None, order[:nu], pos[:nu],
+                      keep)
 
 
 def stride_coords(coords: torch.Tensor, out_tensor_stride) -> torch.Tensor:

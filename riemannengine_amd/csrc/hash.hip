@@ -25,25 +25,30 @@ __global__ void minmax_init_kernel(int32_t *mm, int ncol) {
   if (c < ncol) {
     mm[c] = INT_MAX;
     mm[ncol + c] = INT_MIN;
+    mm[2 * ncol + c] = 0;
   }
 }
 
-// Column-wise min/max of coords [n, ncol]; block-reduced in LDS then merged
-// with global atomics.
+// Column-wise min, max and OR of (value ^ row 0's value) of coords [n, ncol]
+// (the last gives the lowest bit in which a column varies); block-reduced in
+// LDS then merged with global atomics.
 __global__ __launch_bounds__(kBlock) void minmax_kernel(const int32_t *coords,
                                                         int64_t n, int ncol,
                                                         int32_t *mm) {
-  __shared__ int32_t smin[RHIP_MAX_COLS], smax[RHIP_MAX_COLS];
+  __shared__ int32_t smin[RHIP_MAX_COLS], smax[RHIP_MAX_COLS], sor[RHIP_MAX_COLS];
   if (threadIdx.x < RHIP_MAX_COLS) {
     smin[threadIdx.x] = INT_MAX;
     smax[threadIdx.x] = INT_MIN;
+    sor[threadIdx.x] = 0;
   }
   __syncthreads();
-  int32_t lmin[RHIP_MAX_COLS], lmax[RHIP_MAX_COLS];
+  int32_t lmin[RHIP_MAX_COLS], lmax[RHIP_MAX_COLS], lor[RHIP_MAX_COLS], c0[RHIP_MAX_COLS];
 #pragma unroll
   for (int c = 0; c < RHIP_MAX_COLS; ++c) {
     lmin[c] = INT_MAX;
     lmax[c] = INT_MIN;
+    lor[c] = 0;
+    c0[c] = c < ncol ? coords[c] : 0;
   }
 #pragma unroll 4
   for (int64_t r = blockIdx.x * (int64_t)kBlock + threadIdx.x; r < n;
@@ -55,20 +60,23 @@ __global__ __launch_bounds__(kBlock) void minmax_kernel(const int32_t *coords,
         int32_t v = row[c];
         lmin[c] = min(lmin[c], v);
         lmax[c] = max(lmax[c], v);
+        lor[c] |= v ^ c0[c];
       }
     }
   }
 #pragma unroll
   for (int c = 0; c < RHIP_MAX_COLS; ++c) {
     if (c < ncol) {
-      int32_t a = lmin[c], b = lmax[c];
+      int32_t a = lmin[c], b = lmax[c], o = lor[c];
       for (int off = 32; off > 0; off >>= 1) {
         a = min(a, __shfl_xor(a, off));
         b = max(b, __shfl_xor(b, off));
+        o |= __shfl_xor(o, off);
       }
       if (lane_id() == 0) {
         atomicMin(&smin[c], a);
         atomicMax(&smax[c], b);
+        atomicOr(&sor[c], o);
       }
     }
   }
@@ -76,6 +84,7 @@ __global__ __launch_bounds__(kBlock) void minmax_kernel(const int32_t *coords,
   if (threadIdx.x < ncol) {
     atomicMin(&mm[threadIdx.x], smin[threadIdx.x]);
     atomicMax(&mm[ncol + threadIdx.x], smax[threadIdx.x]);
+    atomicOr(&mm[2 * ncol + threadIdx.x], sor[threadIdx.x]);
   }
 }
 
@@ -224,9 +233,9 @@ __global__ __launch_bounds__(kBlock) void lookup_kernel(TableView t,
 }
 
 // Sort keys of the locality order. morton_bits > 0: batch offset in the top
-// bits, then the spatial offsets (from the column minima) bit-interleaved,
-// morton_bits bits each (bit i of column c at i * D + (D - c)); else the
-// packed key.
+// bits, then the spatial offsets from the column minima, each shifted right
+// by the column's common trailing zeros, bit-interleaved, morton_bits bits
+// each (bit i of column c at i * D + (D - c)); else the packed key.
 __global__ __launch_bounds__(kBlock) void pack_keys_kernel(TableView t, int64_t n,
                                                            int morton_bits,
                                                            uint64_t *keys,
@@ -241,11 +250,12 @@ __global__ __launch_bounds__(kBlock) void pack_keys_kernel(TableView t, int64_t 
   uint64_t key = 0;
   if (morton_bits > 0) {
     const int D = t.ncol - 1;
-    for (int b = 0; b < morton_bits; ++b)
-      for (int j = 1; j <= D; ++j) {
-        const uint32_t v = static_cast<uint32_t>(c[j]) - static_cast<uint32_t>(t.lo[j]);
+    for (int j = 1; j <= D; ++j) {
+      const uint32_t v =
+          (static_cast<uint32_t>(c[j]) - static_cast<uint32_t>(t.lo[j])) >> t.tz[j];
+      for (int b = 0; b < morton_bits; ++b)
         key |= static_cast<uint64_t>((v >> b) & 1u) << (b * D + (D - j));
-      }
+    }
     key |= static_cast<uint64_t>(static_cast<uint32_t>(c[0]) - static_cast<uint32_t>(t.lo[0]))
            << (morton_bits * D);
   } else {
@@ -253,6 +263,55 @@ __global__ __launch_bounds__(kBlock) void pack_keys_kernel(TableView t, int64_t 
   }
   keys[i] = key;
   rows[i] = static_cast<int32_t>(i);
+}
+
+__global__ __launch_bounds__(kBlock) void brick_clear_kernel(Brick *grid, int64_t n) {
+  const int64_t i = blockIdx.x * (int64_t)kBlock + threadIdx.x;
+  if (i < n) {
+    Brick b;
+    b.mask = 0;
+    b.base = -1;
+    b.pad = 0;
+    grid[i] = b;
+  }
+}
+
+// The first row of each brick in the locality order (skeys: the sorted
+// Morton keys, whose low cbits bits are the cell within the brick) writes the
+// brick's grid entry: the OR of its rows' cell bits and its own position.
+// A brick has at most 64 cells, so the scan of its rows is short.
+__global__ __launch_bounds__(kBlock) void brick_fill_kernel(TableView t,
+                                                            const uint64_t *__restrict__ skeys,
+                                                            const int32_t *__restrict__ order,
+                                                            int64_t n, int cbits,
+                                                            Brick *__restrict__ grid) {
+  const int64_t j = blockIdx.x * (int64_t)kBlock + threadIdx.x;
+  if (j >= n)
+    return;
+  const uint64_t code = skeys[j] >> cbits;
+  if (j > 0 && (skeys[j - 1] >> cbits) == code)
+    return;
+  const uint64_t cmask = (1ull << cbits) - 1;
+  uint64_t mask = 0;
+  for (int64_t i = j; i < n && i < j + 64; ++i) {
+    const uint64_t k = skeys[i];
+    if ((k >> cbits) != code)
+      break;
+    mask |= 1ull << (k & cmask);
+  }
+  const int64_t r = order[j];
+  int64_t g = static_cast<uint32_t>(t.rows[r * t.ncol]) - static_cast<uint32_t>(t.lo[0]);
+  for (int c = 1; c < t.ncol; ++c) {
+    const uint32_t v =
+        (static_cast<uint32_t>(t.rows[r * t.ncol + c]) - static_cast<uint32_t>(t.lo[c])) >>
+        t.tz[c];
+    g = g * t.dims[c] + (v >> t.levels);
+  }
+  Brick b;
+  b.mask = mask;
+  b.base = static_cast<int32_t>(j);
+  b.pad = 0;
+  grid[g] = b;
 }
 
 __global__ __launch_bounds__(kBlock) void iota_kernel(int64_t n, int32_t *order,
@@ -324,7 +383,7 @@ struct HashWs {
 static HashWs carve_hash(Carve &cv, int64_t n, int ncol) {
   HashWs w;
   const int64_t nb = std::max<int64_t>(1, ceil_div(n, kBlock));
-  w.minmax = cv.take<int32_t>(2 * RHIP_MAX_COLS);
+  w.minmax = cv.take<int32_t>(3 * RHIP_MAX_COLS);
   w.slot_of_row = cv.take<uint32_t>(std::max<int64_t>(n, 1));
   w.uid_by_row = cv.take<int32_t>(std::max<int64_t>(n, 1));
   w.block_counts = cv.take<int32_t>(nb);
@@ -402,8 +461,8 @@ extern "C" int rhip_hash_build(const int32_t *coords, int64_t n, int32_t ncol,
     hipLaunchKernelGGL(minmax_kernel, dim3(std::min<int64_t>(nb, 256)),
                        dim3(kBlock), 0, stream, coords, n, ncol, w.minmax);
     RHIP_LAUNCH_CHECK();
-    int32_t mm[2 * RHIP_MAX_COLS];
-    RHIP_HIP(hipMemcpyAsync(mm, w.minmax, sizeof(int32_t) * 2 * ncol,
+    int32_t mm[3 * RHIP_MAX_COLS];
+    RHIP_HIP(hipMemcpyAsync(mm, w.minmax, sizeof(int32_t) * 3 * ncol,
                             hipMemcpyDeviceToHost, stream));
     RHIP_HIP(hipStreamSynchronize(stream));
     int total_bits = 0;
@@ -422,6 +481,12 @@ extern "C" int rhip_hash_build(const int32_t *coords, int64_t n, int32_t ncol,
     }
     table->mode = total_bits <= 63 ? RHIP_KEY_PACKED64 : RHIP_KEY_ROWREF;
     table->key_bits = total_bits <= 63 ? total_bits : 0;
+    // the lowest bit in which each column varies (coordinates at tensor
+    // stride 2^s vary from bit s up)
+    for (int c = 0; c < ncol; ++c) {
+      const uint32_t orx = static_cast<uint32_t>(mm[2 * ncol + c]);
+      table->tz[c] = orx != 0 ? __builtin_ctz(orx) : 0;
+    }
 
     // The row-reference build probes the caller's coordinates; lookups after
     // the build probe unique_coords (resolve_kernel re-points the slots).
@@ -478,17 +543,88 @@ extern "C" int rhip_order_workspace_bytes(int64_t n, size_t *bytes) {
   });
 }
 
-extern "C" int rhip_spatial_order(const rhip_table *table, int32_t *order,
-                                  int32_t *pos, void *workspace,
+namespace rhip {
+namespace {
+
+// Locality-key layout of a table: bits per spatial column of the Morton
+// code (0: the packed key orders the rows instead) and its total width.
+struct OrderLayout {
+  int morton_bits = 0, total_bits = 0;
+};
+
+OrderLayout order_layout(const rhip_table &t) {
+  OrderLayout o;
+  if (t.mode != RHIP_KEY_PACKED64 || t.key_bits == 0)
+    return o;
+  const int D = t.ncol - 1;
+  int wide = 0;
+  for (int c = 1; c <= D; ++c)
+    wide = std::max(wide, bit_width_u32(static_cast<uint32_t>(
+                              (static_cast<int64_t>(t.hi[c]) - t.lo[c]) >> t.tz[c])));
+  const int batch_bits =
+      bit_width_u32(static_cast<uint32_t>(static_cast<int64_t>(t.hi[0]) - t.lo[0]));
+  if (D >= 1 && wide > 0 && batch_bits + D * wide <= 63) {
+    o.morton_bits = wide;
+    o.total_bits = batch_bits + D * wide;
+  } else {
+    o.total_bits = t.key_bits;
+  }
+  return o;
+}
+
+// Brick grid of a table: Morton levels per brick (cells = 2^(levels * D) <=
+// 64) and the grid extent per column; entries 0 when there is none.
+struct BrickLayout {
+  int levels = 0;
+  int32_t dims[RHIP_MAX_COLS] = {};
+  int64_t entries = 0;
+};
+
+BrickLayout brick_layout(const rhip_table &t) {
+  BrickLayout b;
+  const int D = t.ncol - 1;
+  if (order_layout(t).morton_bits == 0 || D < 1 || D > 6 || t.n_unique < 1)
+    return b;
+  b.levels = 6 / D;
+  int64_t entries = static_cast<int64_t>(t.hi[0]) - t.lo[0] + 1;
+  b.dims[0] = static_cast<int32_t>(entries);
+  const int64_t limit = std::min<int64_t>(int64_t(1) << 23,
+                                          std::max<int64_t>(4096, 16 * t.n_unique));
+  for (int c = 1; c <= D && entries <= limit; ++c) {
+    const int64_t ext = (((static_cast<int64_t>(t.hi[c]) - t.lo[c]) >> t.tz[c]) >> b.levels) + 1;
+    b.dims[c] = static_cast<int32_t>(std::min<int64_t>(ext, INT32_MAX));
+    entries *= ext;
+  }
+  b.entries = entries <= limit ? entries : 0;
+  return b;
+}
+
+} // namespace
+} // namespace rhip
+
+extern "C" int rhip_brick_bytes(const rhip_table *table, size_t *bytes) {
+  return guarded([&] {
+    RHIP_CHECK_ARG(table != nullptr && bytes != nullptr, "table and bytes are required");
+    *bytes = static_cast<size_t>(brick_layout(*table).entries) * sizeof(Brick);
+  });
+}
+
+extern "C" int rhip_spatial_order(rhip_table *table, int32_t *order, int32_t *pos,
+                                  void *bricks, size_t brick_bytes, void *workspace,
                                   size_t workspace_bytes, hipStream_t stream) {
   return guarded([&] {
     RHIP_CHECK_ARG(table != nullptr, "table is null");
+    table->order = nullptr;
+    table->bricks = nullptr;
+    table->morton_bits = 0;
+    table->brick_levels = 0;
     const int64_t n = table->n_unique;
     if (n == 0)
       return;
     RHIP_CHECK_ARG(order != nullptr, "order is null");
     const int64_t nb = ceil_div(n, kBlock);
-    if (table->mode != RHIP_KEY_PACKED64 || table->key_bits == 0) {
+    const OrderLayout ol = order_layout(*table);
+    if (ol.total_bits == 0) {
       hipLaunchKernelGGL(iota_kernel, dim3(nb), dim3(kBlock), 0, stream, n,
                          order, pos);
       RHIP_LAUNCH_CHECK();
@@ -501,27 +637,33 @@ extern "C" int rhip_spatial_order(const rhip_table *table, int32_t *order,
     int32_t *rows_in = cv.take<int32_t>(n);
     const size_t temp = sort_pairs_u64_bytes(n);
     void *tmp = cv.take<char>(temp);
-    // Morton order within a batch when it fits: batch bits + D * the widest
-    // spatial column
-    const int D = table->ncol - 1;
-    int wide = 0;
-    for (int c = 1; c <= D; ++c)
-      wide = std::max(wide, bit_width_u32(static_cast<uint32_t>(
-                                static_cast<int64_t>(table->hi[c]) - table->lo[c])));
-    const int batch_bits =
-        bit_width_u32(static_cast<uint32_t>(static_cast<int64_t>(table->hi[0]) - table->lo[0]));
-    const int morton_total = batch_bits + D * wide;
-    const bool morton = D >= 1 && wide > 0 && morton_total <= 63;
     hipLaunchKernelGGL(pack_keys_kernel, dim3(nb), dim3(kBlock), 0, stream,
-                       make_view(*table), n, morton ? wide : 0, keys_in, rows_in);
+                       make_view(*table), n, ol.morton_bits, keys_in, rows_in);
     RHIP_LAUNCH_CHECK();
-    sort_pairs_u64(tmp, temp, keys_in, keys_out, rows_in, order, n,
-                   morton ? morton_total : table->key_bits, stream);
+    sort_pairs_u64(tmp, temp, keys_in, keys_out, rows_in, order, n, ol.total_bits, stream);
     if (pos) {
       hipLaunchKernelGGL(invert_perm_kernel, dim3(nb), dim3(kBlock), 0, stream,
                          n, order, pos);
       RHIP_LAUNCH_CHECK();
     }
+    const BrickLayout bl = brick_layout(*table);
+    table->morton_bits = ol.morton_bits;
+    if (bricks == nullptr || bl.entries == 0 ||
+        brick_bytes < static_cast<size_t>(bl.entries) * sizeof(Brick))
+      return;
+    Brick *grid = static_cast<Brick *>(bricks);
+    hipLaunchKernelGGL(brick_clear_kernel, dim3(ceil_div(bl.entries, kBlock)), dim3(kBlock), 0,
+                       stream, grid, bl.entries);
+    RHIP_LAUNCH_CHECK();
+    table->order = order;
+    table->brick_levels = bl.levels;
+    for (int c = 0; c < RHIP_MAX_COLS; ++c)
+      table->brick_dims[c] = bl.dims[c];
+    const int D = table->ncol - 1;
+    hipLaunchKernelGGL(brick_fill_kernel, dim3(nb), dim3(kBlock), 0, stream, make_view(*table),
+                       keys_out, order, n, bl.levels * D, grid);
+    RHIP_LAUNCH_CHECK();
+    table->bricks = bricks;
   });
 }
 

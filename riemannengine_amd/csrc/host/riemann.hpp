@@ -181,7 +181,8 @@ struct CoordinateMapHIP {
   at::Tensor storage;   // [n_in_rows, D+1] int32 buffer the unique rows live in
   at::Tensor coords;    // [n, D+1] int32 view of the unique rows
   at::Tensor slots;     // hash slots (bytes)
-  at::Tensor order;     // [n] int32 locality order (sorted by packed key)
+  at::Tensor order;     // [n] int32 locality order (Morton, else packed key)
+  at::Tensor bricks;    // brick index over `order` (bytes; table.bricks NULL if none)
   rhip_table table;
   stride_type tensor_stride;
   int64_t size() const { return table.n_unique; }

@@ -326,8 +326,11 @@ CoordinateMapHIP CoordinateManager::build_map(const at::Tensor &coords,
     size_t ob = 0;
     check_rhip(rhip_order_workspace_bytes(nu, &ob), "rhip_order_workspace_bytes");
     auto ows = device_bytes(ob, dev);
-    check_rhip(rhip_spatial_order(&m.table, m.order.data_ptr<int32_t>(), nullptr, ows.data_ptr(),
-                                  ows.numel(), st),
+    size_t bb = 0;
+    check_rhip(rhip_brick_bytes(&m.table, &bb), "rhip_brick_bytes");
+    m.bricks = device_bytes(std::max<size_t>(bb, 1), dev);
+    check_rhip(rhip_spatial_order(&m.table, m.order.data_ptr<int32_t>(), nullptr,
+                                  m.bricks.data_ptr(), bb, ows.data_ptr(), ows.numel(), st),
                "rhip_spatial_order");
   }
   m.order = m.order.slice(0, 0, nu);

@@ -16,30 +16,35 @@
 // 16-row MFMA groups rarely multiply a missing neighbour.
 //
 // Phase 1 (rhip_kmap_count):
-//   query    one lane per (output, offset) probes the input table in the
-//            output map's locality order -> nbr_sp[k][j]. For a map of a set
-//            onto itself whose stencil is closed under negation (every offset
-//            k has a partner k' with offset k' = -offset k) only one offset
-//            of each pair is probed: o pairs with i under k iff i pairs with
-//            o under k', so the partner row is a scatter of the probed one and
-//            the zero offset is the identity;
-//   masks    one lane per output row folds its K hits into a sort key (the
-//            mask for K <= 16, else a 16-bit hash of it);
+//   probes   an output row's neighbour under offset k is found through the
+//            input table's brick index when it has one (a dense grid of
+//            brick entries over the locality order: one 16-byte load, a
+//            popcount and a look-up in the order), else by probing the hash
+//            table; probes are resolved 8 offsets at a time, their loads
+//            issued together;
+//   masks    one lane per output row (in the output map's locality order)
+//            folds the existence of its K neighbours into a sort key (the
+//            mask for K <= 16, else the neighbour count above a 15-bit hash
+//            of the mask);
 //   sort     stable radix sort of the rows by key;
-//   permute  nbr[k][p] = nbr_sp[k][j(p)], out_order[p] = row of p, and a
-//            wave-ballot count of hits per (offset, workgroup);
-//   scan     per-offset exclusive scans of the counts (one workgroup per
-//            offset), then the CSR offsets of the pairs.
+//   query    one lane per processing position p resolves its row's K
+//            neighbours and writes nbr[k][p] (coalesced over p), out_order[p]
+//            and per wave and offset the count of hits (ballots);
+//   scan     per-offset exclusive scans of the wave counts, then the CSR
+//            offsets of the pairs.
 // Phase 2 (rhip_kmap_fill):
 //   emit     ballot + mbcnt compaction of nbr into per-offset pair lists
 //            (ordered by offset, then processing position);
-//   symmetric maps: the input order is the output order and the transposed
-//            table is the forward table with partner offsets (a copy);
+//   symmetric maps (a set onto itself with a stencil closed under negation):
+//            the input order is the output order and the transposed table is
+//            the forward table with partner offsets (a copy): i pairs with o
+//            under k iff o pairs with i under the partner of k;
 //   otherwise: the input rows' transposed masks (atomicOr during the emit),
 //            a sort of the input rows by them -> in_order / in_pos, and
 //            nbr_t[k][in_pos[i]] = output row paired with i under k.
 #include <algorithm>
 #include <cstring>
+#include <type_traits>
 #include <vector>
 
 #include "rhip_internal.hpp"
@@ -49,139 +54,7 @@ namespace rhip {
 constexpr int kMapBlock = 256;
 constexpr int kMaskedK = 128; // neighbour masks (and mask order) for K <= 128
 constexpr int kKeyBits = 16;  // sort-key width of a neighbour mask
-
-__global__ __launch_bounds__(kMapBlock) void kmap_query_kernel(
-    TableView t, const int32_t *__restrict__ out_coords,
-    const int32_t *__restrict__ spatial, int64_t n_out,
-    const int32_t *__restrict__ offsets, const int32_t *__restrict__ klist,
-    int32_t *__restrict__ nbr_sp) {
-  const int k = klist ? klist[blockIdx.y] : blockIdx.y;
-  const int64_t j = blockIdx.x * (int64_t)kMapBlock + threadIdx.x;
-  if (j >= n_out)
-    return;
-  const int D = t.ncol - 1;
-  const int64_t o = spatial ? spatial[j] : j;
-  int32_t c[RHIP_MAX_COLS];
-#pragma unroll
-  for (int i = 0; i < RHIP_MAX_COLS; ++i)
-    c[i] = i < t.ncol ? out_coords[o * t.ncol + i] : 0;
-#pragma unroll
-  for (int i = 1; i < RHIP_MAX_COLS; ++i)
-    if (i < t.ncol) // wrap-around add, as int32 coordinate arithmetic does
-      c[i] = static_cast<int32_t>(static_cast<uint32_t>(c[i]) +
-                                  static_cast<uint32_t>(offsets[k * D + (i - 1)]));
-  nbr_sp[k * n_out + j] = table_find(t, c);
-}
-
-// Packed-key tables: one thread per output row j (spatial order) answers all
-// n_probe offsets k = klist[p] (klist NULL: k = p). The row's coordinates are
-// read once; a neighbour's key is packed column by column from them (a
-// column leaving the table's [lo, hi] range is a miss, as in pack_row), and
-// the first slots of kChunk probes are loaded before any is resolved.
-__global__ __launch_bounds__(kMapBlock) void kmap_query_rows_kernel(
-    TableView t, const int32_t *__restrict__ out_coords, const int32_t *__restrict__ spatial,
-    int64_t n_out, const int32_t *__restrict__ offsets, const int32_t *__restrict__ klist,
-    int n_probe, int32_t *__restrict__ nbr_sp) {
-  constexpr int kChunk = 8;
-  const int64_t j = blockIdx.x * (int64_t)kMapBlock + threadIdx.x;
-  if (j >= n_out)
-    return;
-  const int D = t.ncol - 1;
-  const int64_t o = spatial ? spatial[j] : j;
-  int32_t c[RHIP_MAX_COLS];
-#pragma unroll
-  for (int i = 0; i < RHIP_MAX_COLS; ++i)
-    c[i] = i < t.ncol ? out_coords[o * t.ncol + i] : 0;
-  const uint32_t d0 = static_cast<uint32_t>(c[0]) - static_cast<uint32_t>(t.lo[0]);
-  const bool row_ok = d0 <= t.span[0];
-  const uint64_t base = static_cast<uint64_t>(d0) << t.shift[0];
-  for (int p0 = 0; p0 < n_probe; p0 += kChunk) {
-    uint64_t key[kChunk], h[kChunk];
-    bool ok[kChunk];
-    Slot sl[kChunk];
-#pragma unroll
-    for (int u = 0; u < kChunk; ++u) {
-      const int p = p0 + u;
-      ok[u] = row_ok && p < n_probe;
-      key[u] = base;
-      if (p < n_probe) {
-        const int k = klist ? klist[p] : p;
-#pragma unroll
-        for (int i = 1; i < RHIP_MAX_COLS; ++i) {
-          if (i <= D) { // wrap-around add, as int32 coordinate arithmetic does
-            const uint32_t v = static_cast<uint32_t>(c[i]) +
-                               static_cast<uint32_t>(offsets[k * D + (i - 1)]);
-            const uint32_t d = v - static_cast<uint32_t>(t.lo[i]);
-            ok[u] = ok[u] && d <= t.span[i];
-            key[u] |= static_cast<uint64_t>(d) << t.shift[i];
-          }
-        }
-      }
-      h[u] = mix64(key[u]) & t.mask;
-    }
-#pragma unroll
-    for (int u = 0; u < kChunk; ++u)
-      if (ok[u])
-        sl[u] = t.slots[h[u]];
-#pragma unroll
-    for (int u = 0; u < kChunk; ++u) {
-      const int p = p0 + u;
-      if (p >= n_probe)
-        continue;
-      int32_t r = -1;
-      if (ok[u]) {
-        while (sl[u].word != key[u] && sl[u].word != kEmptyWord) {
-          h[u] = (h[u] + 1) & t.mask;
-          sl[u] = t.slots[h[u]];
-        }
-        if (sl[u].word == key[u])
-          r = static_cast<int32_t>(sl[u].uid);
-      }
-      const int k = klist ? klist[p] : p;
-      nbr_sp[k * n_out + j] = r;
-    }
-  }
-}
-
-// Symmetric maps: the partner row of every probed offset k = klist[y];
-// nbr_sp[partner[k]][pos[i]] = row of j for every hit i = nbr_sp[k][j].
-__global__ __launch_bounds__(kMapBlock) void kmap_mirror_kernel(
-    int32_t *__restrict__ nbr_sp, const int32_t *__restrict__ spatial,
-    const int32_t *__restrict__ pos, int64_t n, const int32_t *__restrict__ klist,
-    const int32_t *__restrict__ partner) {
-  const int k = klist[blockIdx.y];
-  const int64_t j = blockIdx.x * (int64_t)kMapBlock + threadIdx.x;
-  if (j >= n)
-    return;
-  const int32_t i = nbr_sp[k * n + j];
-  if (i >= 0)
-    nbr_sp[static_cast<int64_t>(partner[k]) * n + (pos ? pos[i] : i)] =
-        spatial ? spatial[j] : static_cast<int32_t>(j);
-}
-
-// table[partner[klist[y]]][j] = v: clears the rows the mirror scatters into.
-__global__ __launch_bounds__(kMapBlock) void fill_partner_rows_kernel(
-    int32_t *__restrict__ table, int64_t n, const int32_t *__restrict__ klist,
-    const int32_t *__restrict__ partner, int32_t v) {
-  const int64_t j = blockIdx.x * (int64_t)kMapBlock + threadIdx.x;
-  if (j < n)
-    table[static_cast<int64_t>(partner[klist[blockIdx.y]]) * n + j] = v;
-}
-
-// The zero offset of a map onto itself: every row is its own neighbour.
-__global__ __launch_bounds__(kMapBlock) void kmap_identity_kernel(
-    int32_t *__restrict__ row, const int32_t *__restrict__ spatial, int64_t n) {
-  const int64_t j = blockIdx.x * (int64_t)kMapBlock + threadIdx.x;
-  if (j < n)
-    row[j] = spatial ? spatial[j] : static_cast<int32_t>(j);
-}
-
-__global__ __launch_bounds__(kMapBlock) void invert_order_kernel(
-    const int32_t *__restrict__ order, int64_t n, int32_t *__restrict__ pos) {
-  const int64_t j = blockIdx.x * (int64_t)kMapBlock + threadIdx.x;
-  if (j < n)
-    pos[order[j]] = static_cast<int32_t>(j);
-}
+static int64_t map_waves(int64_t n) { return std::max<int64_t>(1, ceil_div(n, kWave)); }
 
 // Sort key of a neighbour mask: the mask itself for K <= 16; else 22 bits,
 // the neighbour count (largest first, 127 and more alike) above a 15-bit
@@ -200,60 +73,196 @@ __device__ __forceinline__ uint32_t mask_key(uint64_t m0, uint64_t m1, int K) {
 // Bits of mask_key for K offsets.
 static int mask_key_bits(int K) { return K <= kKeyBits ? K : 22; }
 
-__global__ __launch_bounds__(kMapBlock) void mask_key_kernel(
-    const int32_t *__restrict__ nbr_sp, int64_t n, int K,
-    uint32_t *__restrict__ keys, int32_t *__restrict__ vals) {
-  const int64_t j = blockIdx.x * (int64_t)kMapBlock + threadIdx.x;
-  if (j >= n)
+// Resolves probes k0 .. k0+7 of an output row with coordinates c (batch
+// offset d0 = c[0] - lo[0], row_ok = the batch is in range): r[u] = the
+// input row at c + offsets[k0 + u] (batch kept, wrap-around int32 arithmetic
+// as the coordinate type has), or -1. With kRows false only r[u] >= 0
+// matters, and brick tables skip the locality-order lookup.
+//   brick index: the neighbour's brick entry, then the rank of its cell among
+//     the brick's occupied cells gives its locality-order position;
+//   packed keys: each neighbour's key is packed column by column (a column
+//     leaving [lo, hi] is a miss, as in pack_row), the home slots of all 8
+//     probes are loaded before any chain is followed;
+//   row-reference tables: table_find.
+template <int D, bool kRows>
+__device__ __forceinline__ void probe8(const TableView &t, const int32_t *c, uint32_t d0,
+                                       bool row_ok, const int32_t *__restrict__ offsets, int k0,
+                                       int K, int32_t (&r)[8]) {
+  if constexpr (D <= 6) {
+    if (t.bricks != nullptr) {
+      constexpr int L = 6 / D;
+      uint64_t g[8];
+      uint32_t cell[8];
+      bool ok[8];
+      Brick br[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int k = k0 + u;
+        ok[u] = row_ok && k < K;
+        g[u] = d0;
+        cell[u] = 0;
+        const int kk = k < K ? k : 0;
+#pragma unroll
+        for (int i = 1; i <= D; ++i) {
+          const uint32_t v = static_cast<uint32_t>(c[i]) +
+                             static_cast<uint32_t>(offsets[kk * D + (i - 1)]) -
+                             static_cast<uint32_t>(t.lo[i]);
+          ok[u] = ok[u] && v <= t.span[i] && (v & ((1u << t.tz[i]) - 1u)) == 0;
+          const uint32_t w = v >> t.tz[i];
+          g[u] = g[u] * static_cast<uint32_t>(t.dims[i]) + (w >> L);
+#pragma unroll
+          for (int l = 0; l < L; ++l)
+            cell[u] |= ((w >> l) & 1u) << (l * D + (D - i));
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        if (ok[u])
+          br[u] = t.bricks[g[u]];
+      int32_t jj[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        jj[u] = -1;
+        if (ok[u] && ((br[u].mask >> cell[u]) & 1ull))
+          jj[u] = br[u].base + __popcll(br[u].mask & ((1ull << cell[u]) - 1ull));
+      }
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        r[u] = kRows ? (jj[u] >= 0 ? t.order[jj[u]] : -1) : jj[u];
+      return;
+    }
+  }
+  if (t.mode == RHIP_KEY_PACKED64) {
+    const uint64_t base = static_cast<uint64_t>(d0) << t.shift[0];
+    uint64_t key[8], h[8];
+    bool ok[8];
+    Slot sl[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int k = k0 + u;
+      ok[u] = row_ok && k < K;
+      key[u] = base;
+      const int kk = k < K ? k : 0;
+#pragma unroll
+      for (int i = 1; i <= D; ++i) {
+        const uint32_t v = static_cast<uint32_t>(c[i]) +
+                           static_cast<uint32_t>(offsets[kk * D + (i - 1)]);
+        const uint32_t d = v - static_cast<uint32_t>(t.lo[i]);
+        ok[u] = ok[u] && d <= t.span[i];
+        key[u] |= static_cast<uint64_t>(d) << t.shift[i];
+      }
+      h[u] = mix64(key[u]) & t.mask;
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      if (ok[u])
+        sl[u] = t.slots[h[u]];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      r[u] = -1;
+      if (ok[u]) {
+        while (sl[u].word != key[u] && sl[u].word != kEmptyWord) {
+          h[u] = (h[u] + 1) & t.mask;
+          sl[u] = t.slots[h[u]];
+        }
+        if (sl[u].word == key[u])
+          r[u] = static_cast<int32_t>(sl[u].uid);
+      }
+    }
     return;
+  }
+#pragma unroll
+  for (int u = 0; u < 8; ++u) {
+    const int k = k0 + u;
+    r[u] = -1;
+    if (k < K) {
+      int32_t q[RHIP_MAX_COLS] = {};
+      q[0] = c[0];
+#pragma unroll
+      for (int i = 1; i <= D; ++i)
+        q[i] = static_cast<int32_t>(static_cast<uint32_t>(c[i]) +
+                                    static_cast<uint32_t>(offsets[k * D + (i - 1)]));
+      r[u] = table_find(t, q);
+    }
+  }
+}
+
+// Mask pass: one lane per output row j in spatial order (row spatial[j]):
+// keys[j] = the sort key of the row's neighbour mask, vals[j] = j.
+template <int D>
+__global__ __launch_bounds__(kMapBlock) void kmap_mask_kernel(
+    TableView t, const int32_t *__restrict__ out_coords, const int32_t *__restrict__ spatial,
+    int64_t n_out, const int32_t *__restrict__ offsets, int K, uint32_t *__restrict__ keys,
+    int32_t *__restrict__ vals) {
+  const int64_t j = blockIdx.x * (int64_t)kMapBlock + threadIdx.x;
+  if (j >= n_out)
+    return;
+  const int64_t o = spatial ? spatial[j] : j;
+  int32_t c[D + 1];
+#pragma unroll
+  for (int i = 0; i <= D; ++i)
+    c[i] = out_coords[o * (D + 1) + i];
+  const uint32_t d0 = static_cast<uint32_t>(c[0]) - static_cast<uint32_t>(t.lo[0]);
+  const bool row_ok = d0 <= t.span[0];
   uint64_t m0 = 0, m1 = 0;
-  for (int k = 0; k < K; ++k) {
-    const uint64_t h = nbr_sp[k * n + j] >= 0 ? 1ull : 0ull;
-    if (k < 64)
-      m0 |= h << k;
-    else
-      m1 |= h << (k - 64);
+  for (int k0 = 0; k0 < K; k0 += 8) {
+    int32_t r[8];
+    probe8<D, false>(t, c, d0, row_ok, offsets, k0, K, r);
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int k = k0 + u;
+      if (r[u] >= 0) {
+        if (k < 64)
+          m0 |= 1ull << k;
+        else
+          m1 |= 1ull << (k - 64);
+      }
+    }
   }
   keys[j] = mask_key(m0, m1, K);
   vals[j] = static_cast<int32_t>(j);
 }
 
-__device__ __forceinline__ int32_t block_hit_base(bool hit, int32_t *wave_counts,
-                                                  uint64_t &ballot) {
-  ballot = __ballot(hit);
-  const int w = threadIdx.x / kWave;
-  if (lane_id() == 0)
-    wave_counts[w] = __popcll(ballot);
-  __syncthreads();
-  int32_t before = 0;
-  for (int i = 0; i < w; ++i)
-    before += wave_counts[i];
-  return before;
-}
-
-__global__ __launch_bounds__(kMapBlock) void kmap_permute_kernel(
-    const int32_t *__restrict__ nbr_sp, const int32_t *__restrict__ jpos,
-    const int32_t *__restrict__ spatial, int64_t n_out, int32_t *__restrict__ nbr,
-    int32_t *__restrict__ out_order, int32_t *__restrict__ block_counts) {
-  __shared__ int32_t wave_counts[kMapBlock / kWave];
-  const int k = blockIdx.y;
+// Query pass: one lane per processing position p (row j = jpos[p] of the
+// spatial order, or p): nbr[k][p] = the input row paired with it under k
+// (coalesced over p), out_order[p] = its row, and per offset k the number of
+// hits of each wave w, wave_counts[k][w].
+template <int D>
+__global__ __launch_bounds__(kMapBlock) void kmap_query_kernel(
+    TableView t, const int32_t *__restrict__ out_coords, const int32_t *__restrict__ spatial,
+    const int32_t *__restrict__ jpos, int64_t n_out, const int32_t *__restrict__ offsets, int K,
+    int64_t nw, int32_t *__restrict__ nbr, int32_t *__restrict__ out_order,
+    int32_t *__restrict__ wave_counts) {
   const int64_t p = blockIdx.x * (int64_t)kMapBlock + threadIdx.x;
-  bool hit = false;
-  if (p < n_out) {
+  const int64_t w = p / kWave;
+  if (w >= nw) // whole waves past the last row
+    return;
+  const bool in = p < n_out;
+  int32_t c[D + 1] = {};
+  if (in) {
     const int64_t j = jpos ? jpos[p] : p;
-    const int32_t v = nbr_sp[k * n_out + j];
-    nbr[k * n_out + p] = v;
-    hit = v >= 0;
-    if (k == 0)
-      out_order[p] = spatial ? spatial[j] : static_cast<int32_t>(j);
+    const int64_t o = spatial ? spatial[j] : j;
+    out_order[p] = static_cast<int32_t>(o);
+#pragma unroll
+    for (int i = 0; i <= D; ++i)
+      c[i] = out_coords[o * (D + 1) + i];
   }
-  uint64_t b;
-  block_hit_base(hit, wave_counts, b);
-  if (threadIdx.x == kMapBlock - 1) {
-    int32_t s = 0;
-    for (int w = 0; w < kMapBlock / kWave; ++w)
-      s += wave_counts[w];
-    block_counts[static_cast<int64_t>(k) * gridDim.x + blockIdx.x] = s;
+  const uint32_t d0 = static_cast<uint32_t>(c[0]) - static_cast<uint32_t>(t.lo[0]);
+  const bool row_ok = in && d0 <= t.span[0];
+  for (int k0 = 0; k0 < K; k0 += 8) {
+    int32_t r[8];
+    probe8<D, true>(t, c, d0, row_ok, offsets, k0, K, r);
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int k = k0 + u;
+      if (k < K) {
+        if (in)
+          nbr[k * n_out + p] = r[u];
+        const uint64_t hits = __ballot(r[u] >= 0);
+        if (lane_id() == 0)
+          wave_counts[k * nw + w] = __popcll(hits);
+      }
+    }
   }
 }
 
@@ -301,21 +310,22 @@ __global__ __launch_bounds__(kMapBlock) void zero_u64_kernel(unsigned long long 
     p[i] = 0ull;
 }
 
+// Lane per processing position p and offset k = blockIdx.y: a hit is written
+// at its offset's start + its wave's run (wave_base) + its rank in the wave.
 __global__ __launch_bounds__(kMapBlock) void kmap_emit_kernel(
     const int32_t *__restrict__ nbr, const int32_t *__restrict__ out_order,
-    int64_t n_out, const int64_t *__restrict__ kofs,
-    const int64_t *__restrict__ block_base, int32_t *__restrict__ in_rows,
+    int64_t n_out, int64_t nw, const int64_t *__restrict__ kofs,
+    const int64_t *__restrict__ wave_base, int32_t *__restrict__ in_rows,
     int32_t *__restrict__ out_rows, unsigned long long *__restrict__ mask_t) {
-  __shared__ int32_t wave_counts[kMapBlock / kWave];
   const int k = blockIdx.y;
   const int64_t p = blockIdx.x * (int64_t)kMapBlock + threadIdx.x;
+  const int64_t w = p / kWave;
+  if (w >= nw)
+    return;
   const int32_t v = p < n_out ? nbr[k * n_out + p] : -1;
-  const bool hit = v >= 0;
-  uint64_t b;
-  const int32_t before = block_hit_base(hit, wave_counts, b);
-  if (hit) {
-    const int64_t q = kofs[k] + block_base[static_cast<int64_t>(k) * gridDim.x + blockIdx.x] +
-                      before + lanes_below(b);
+  const uint64_t b = __ballot(v >= 0);
+  if (v >= 0) {
+    const int64_t q = kofs[k] + wave_base[k * nw + w] + lanes_below(b);
     in_rows[q] = v;
     out_rows[q] = out_order[p];
     if (mask_t)
@@ -406,17 +416,12 @@ static void upload_i32(int32_t *dst, const int32_t *src, size_t n, hipStream_t s
 }
 
 struct KmapWs {
-  int32_t *block_counts;
-  int64_t *block_base;
+  int32_t *wave_counts; // [K][waves] hits per wave and offset (phase 1)
+  int64_t *wave_base;   // their per-offset exclusive scans (phase 1 -> 2)
   int64_t *ktotal;
-  int32_t *offsets;  // [K][D] stencil (D = the table's ncol - 1)
-  int32_t *plan;     // partner[K] | probe list[K] | mirror list[K]
-  int32_t *partner;
-  int32_t *probe;
-  int32_t *mirror;
+  int32_t *offsets;     // [K][D] stencil (D = the table's ncol - 1)
+  int32_t *partner;     // [K] partner offsets of a symmetric map (phase 1 -> 2)
   // phase 1
-  int32_t *nbr_sp;
-  int32_t *pos;
   uint32_t *keys_a, *keys_b;
   int32_t *vals_a, *vals_b;
   void *sort_tmp;
@@ -430,20 +435,15 @@ struct KmapWs {
 };
 
 static KmapWs carve_kmap(Carve &cv, int64_t n_in, int64_t n_out, int32_t K, int32_t D) {
-  const int64_t nb = std::max<int64_t>(1, ceil_div(n_out, kMapBlock));
+  const int64_t nw = map_waves(n_out);
   const int64_t mo = std::max<int64_t>(n_out, 1), mi = std::max<int64_t>(n_in, 1);
   KmapWs w{};
-  w.block_counts = cv.take<int32_t>(nb * K);
-  w.block_base = cv.take<int64_t>(nb * K);
+  w.wave_counts = cv.take<int32_t>(nw * K);
+  w.wave_base = cv.take<int64_t>(nw * K);
   w.ktotal = cv.take<int64_t>(K);
   w.offsets = cv.take<int32_t>(static_cast<size_t>(K) * std::max(D, 1));
-  w.plan = cv.take<int32_t>(3 * static_cast<size_t>(K));
-  w.partner = w.plan;
-  w.probe = w.plan ? w.plan + K : nullptr;
-  w.mirror = w.plan ? w.plan + 2 * K : nullptr;
+  w.partner = cv.take<int32_t>(K);
   const size_t base = cv.used;
-  w.nbr_sp = cv.take<int32_t>(mo * K);
-  w.pos = cv.take<int32_t>(mo);
   w.keys_a = cv.take<uint32_t>(mo);
   w.keys_b = cv.take<uint32_t>(mo);
   w.vals_a = cv.take<int32_t>(mo);
@@ -464,35 +464,33 @@ static KmapWs carve_kmap(Carve &cv, int64_t n_in, int64_t n_out, int32_t K, int3
   return w;
 }
 
-// Host plan of a symmetric map: a map of a set onto itself (same rows, same
-// order) whose offsets are distinct and closed under negation: partner[K],
-// the offsets to probe and the probed offsets whose partner row is mirrored
-// from them (the KmapWs::plan layout).
-struct SymPlan {
-  bool ok = false;
-  int zero = -1; // the zero offset (identity row), if any
-  int n_probe = 0, n_mirror = 0;
-  std::vector<int32_t> lists; // partner | probe | mirror, K entries each
-};
+// Calls f(std::integral_constant<int, D>) for the table's spatial dimension.
+template <typename F> void with_dim(int D, F &&f) {
+  switch (D) {
+  case 1: f(std::integral_constant<int, 1>{}); break;
+  case 2: f(std::integral_constant<int, 2>{}); break;
+  case 3: f(std::integral_constant<int, 3>{}); break;
+  case 4: f(std::integral_constant<int, 4>{}); break;
+  case 5: f(std::integral_constant<int, 5>{}); break;
+  case 6: f(std::integral_constant<int, 6>{}); break;
+  case 7: f(std::integral_constant<int, 7>{}); break;
+  default: throw Error(RHIP_ERR_INVALID, "coordinate rows need 1 to 7 spatial columns");
+  }
+}
 
-static SymPlan symmetric_plan(const rhip_table *in_table, const int32_t *out_coords,
-                              int64_t n_out, int32_t K, const int32_t *offsets_host) {
-  SymPlan p;
+// Partner offsets of a symmetric map: a map of a set onto itself (same rows,
+// same order) whose offsets are distinct and closed under negation. Empty
+// when the map is not symmetric.
+static std::vector<int32_t> symmetric_partners(const rhip_table *in_table,
+                                               const int32_t *out_coords, int64_t n_out,
+                                               int32_t K, const int32_t *offsets_host) {
   const int D = in_table->ncol - 1;
-  p.lists.assign(3 * static_cast<size_t>(K), 0);
-  int32_t *partner = p.lists.data();
-  int32_t *probe = partner + K, *mirror = probe + K;
+  std::vector<int32_t> partner(static_cast<size_t>(K), -1);
   if (out_coords != in_table->rows || n_out != in_table->n_unique || n_out < 2 ||
       K > kMaskedK)
-    return p;
+    return {};
   auto row = [&](int k) { return offsets_host + static_cast<size_t>(k) * D; };
   for (int a = 0; a < K; ++a) {
-    partner[a] = -1;
-    bool zero = true;
-    for (int d = 0; d < D; ++d)
-      zero = zero && row(a)[d] == 0;
-    if (zero)
-      p.zero = a;
     for (int b = 0; b < K; ++b) {
       bool same = b != a, neg = true;
       for (int d = 0; d < D; ++d) {
@@ -501,25 +499,14 @@ static SymPlan symmetric_plan(const rhip_table *in_table, const int32_t *out_coo
                          0u - static_cast<uint32_t>(row(a)[d]); // wrap-around negation
       }
       if (same)
-        return p; // repeated offsets: the general path
+        return {}; // repeated offsets: the general path
       if (neg)
         partner[a] = b;
     }
     if (partner[a] < 0)
-      return p;
+      return {};
   }
-  for (int k = 0; k < K; ++k) {
-    if (k == p.zero)
-      continue;
-    if (partner[k] > k) {
-      probe[p.n_probe++] = k;
-      mirror[p.n_mirror++] = k;
-    } else if (partner[k] == k) { // offset == -offset without being zero
-      probe[p.n_probe++] = k;
-    }
-  }
-  p.ok = true;
-  return p;
+  return partner;
 }
 
 } // namespace rhip
@@ -553,13 +540,15 @@ extern "C" int rhip_kmap_count(const rhip_table *in_table, const int32_t *out_co
     Carve cv(workspace, workspace_bytes);
     KmapWs w = carve_kmap(cv, in_table->n_unique, n_out, K, RHIP_MAX_COLS - 1);
     const int64_t nb = std::max<int64_t>(1, ceil_div(n_out, kMapBlock));
-    const SymPlan plan = symmetric_plan(in_table, out_coords, n_out, K, offsets_host);
-    const bool sym = plan.ok;
+    const int64_t nw = map_waves(n_out);
+    const std::vector<int32_t> partner =
+        symmetric_partners(in_table, out_coords, n_out, K, offsets_host);
+    const bool sym = !partner.empty();
     if (flags)
       *flags = sym ? RHIP_KMAP_SYMMETRIC : 0;
     if (n_out == 0) {
-      hipLaunchKernelGGL(fill_i32_kernel, dim3(ceil_div(nb * K, kMapBlock)),
-                         dim3(kMapBlock), 0, stream, w.block_counts, nb * K, 0);
+      hipLaunchKernelGGL(fill_i32_kernel, dim3(ceil_div(nw * K, kMapBlock)),
+                         dim3(kMapBlock), 0, stream, w.wave_counts, nw * K, 0);
       RHIP_LAUNCH_CHECK();
     } else {
       RHIP_CHECK_ARG(out_coords && nbr && out_order, "out_coords, nbr and out_order are required");
@@ -567,65 +556,29 @@ extern "C" int rhip_kmap_count(const rhip_table *in_table, const int32_t *out_co
       // memory would wait for the device)
       upload_i32(w.offsets, offsets_host, static_cast<size_t>(K) * D, stream);
       if (sym)
-        upload_i32(w.plan, plan.lists.data(), plan.lists.size(), stream);
+        upload_i32(w.partner, partner.data(), partner.size(), stream);
+      const bool masks = K <= kMaskedK && n_out > 1 && in_table->n_unique > 0;
       const TableView tv = make_view(*in_table);
-      // all probes of a row in one thread for packed keys; one thread per
-      // (row, offset) for row-reference tables
-      auto query = [&](int n_probe, const int32_t *klist) {
-        if (in_table->mode == RHIP_KEY_PACKED64)
-          hipLaunchKernelGGL(kmap_query_rows_kernel, dim3(nb), dim3(kMapBlock), 0, stream, tv,
-                             out_coords, out_spatial_order, n_out, w.offsets, klist, n_probe,
-                             w.nbr_sp);
-        else
-          hipLaunchKernelGGL(kmap_query_kernel, dim3(nb, n_probe), dim3(kMapBlock), 0, stream,
-                             tv, out_coords, out_spatial_order, n_out, w.offsets, klist,
-                             w.nbr_sp);
-        RHIP_LAUNCH_CHECK();
-      };
-      if (sym) {
-        if (plan.n_mirror > 0) {
-          hipLaunchKernelGGL(fill_partner_rows_kernel, dim3(nb, plan.n_mirror),
-                             dim3(kMapBlock), 0, stream, w.nbr_sp, n_out, w.mirror, w.partner,
-                             -1);
-          RHIP_LAUNCH_CHECK();
-        }
-        if (plan.n_probe > 0)
-          query(plan.n_probe, w.probe);
-        if (plan.n_mirror > 0) {
-          if (out_spatial_order) {
-            hipLaunchKernelGGL(invert_order_kernel, dim3(nb), dim3(kMapBlock), 0, stream,
-                               out_spatial_order, n_out, w.pos);
-            RHIP_LAUNCH_CHECK();
-          }
-          hipLaunchKernelGGL(kmap_mirror_kernel, dim3(nb, plan.n_mirror), dim3(kMapBlock), 0,
-                             stream, w.nbr_sp, out_spatial_order,
-                             out_spatial_order ? w.pos : nullptr, n_out, w.mirror, w.partner);
-          RHIP_LAUNCH_CHECK();
-        }
-        if (plan.zero >= 0) {
-          hipLaunchKernelGGL(kmap_identity_kernel, dim3(nb), dim3(kMapBlock), 0, stream,
-                             w.nbr_sp + plan.zero * n_out, out_spatial_order, n_out);
-          RHIP_LAUNCH_CHECK();
-        }
-      } else {
-        query(K, nullptr);
-      }
       const int32_t *jpos = nullptr;
-      if (K <= kMaskedK && n_out > 1 && in_table->n_unique > 0) {
-        hipLaunchKernelGGL(mask_key_kernel, dim3(nb), dim3(kMapBlock), 0, stream,
-                           w.nbr_sp, n_out, K, w.keys_a, w.vals_a);
+      with_dim(D, [&](auto dc) {
+        constexpr int DD = decltype(dc)::value;
+        if (masks) {
+          hipLaunchKernelGGL(kmap_mask_kernel<DD>, dim3(nb), dim3(kMapBlock), 0, stream, tv,
+                             out_coords, out_spatial_order, n_out, w.offsets, K, w.keys_a,
+                             w.vals_a);
+          RHIP_LAUNCH_CHECK();
+          sort_pairs_u32(w.sort_tmp, w.sort_bytes, w.keys_a, w.keys_b, w.vals_a, w.vals_b,
+                         n_out, mask_key_bits(K), stream);
+          jpos = w.vals_b;
+        }
+        hipLaunchKernelGGL(kmap_query_kernel<DD>, dim3(nb), dim3(kMapBlock), 0, stream, tv,
+                           out_coords, out_spatial_order, jpos, n_out, w.offsets, K, nw, nbr,
+                           out_order, w.wave_counts);
         RHIP_LAUNCH_CHECK();
-        sort_pairs_u32(w.sort_tmp, w.sort_bytes, w.keys_a, w.keys_b, w.vals_a, w.vals_b,
-                       n_out, mask_key_bits(K), stream);
-        jpos = w.vals_b;
-      }
-      hipLaunchKernelGGL(kmap_permute_kernel, dim3(nb, K), dim3(kMapBlock), 0, stream,
-                         w.nbr_sp, jpos, out_spatial_order, n_out, nbr, out_order,
-                         w.block_counts);
-      RHIP_LAUNCH_CHECK();
+      });
     }
-    hipLaunchKernelGGL(scan_kernel<int32_t>, dim3(K), dim3(1024), 0, stream, w.block_counts,
-                       nb, w.block_base, w.ktotal);
+    hipLaunchKernelGGL(scan_kernel<int32_t>, dim3(K), dim3(1024), 0, stream, w.wave_counts,
+                       nw, w.wave_base, w.ktotal);
     RHIP_LAUNCH_CHECK();
     hipLaunchKernelGGL(kmap_offsets_kernel, dim3(1), dim3(1024), 0, stream, w.ktotal, K,
                        kmap_offsets, nullptr);
@@ -653,6 +606,7 @@ extern "C" int rhip_kmap_fill(const int32_t *nbr, const int32_t *out_order, int6
     Carve cv(workspace, workspace_bytes);
     KmapWs w = carve_kmap(cv, n_in, n_out, K, RHIP_MAX_COLS - 1);
     const int64_t nb = std::max<int64_t>(1, ceil_div(n_out, kMapBlock));
+    const int64_t nw = map_waves(n_out);
     const bool want_t = nbr_t != nullptr && n_in > 0;
     RHIP_CHECK_ARG(!want_t || in_order != nullptr, "in_order is required with nbr_t");
     const bool masks = want_t && !sym && K <= kMaskedK && n_in > 1;
@@ -664,7 +618,7 @@ extern "C" int rhip_kmap_fill(const int32_t *nbr, const int32_t *out_order, int6
     if (n_out > 0) {
       RHIP_CHECK_ARG(nbr && out_order, "nbr and out_order are required");
       hipLaunchKernelGGL(kmap_emit_kernel, dim3(nb, K), dim3(kMapBlock), 0, stream, nbr,
-                         out_order, n_out, kmap_offsets, w.block_base, in_rows, out_rows,
+                         out_order, n_out, nw, kmap_offsets, w.wave_base, in_rows, out_rows,
                          masks ? w.mask_t : nullptr);
       RHIP_LAUNCH_CHECK();
     }

@@ -115,7 +115,23 @@ struct TableView {
   int32_t lo[RHIP_MAX_COLS];
   uint32_t span[RHIP_MAX_COLS]; // hi - lo
   int32_t shift[RHIP_MAX_COLS];
+  int32_t tz[RHIP_MAX_COLS];    // common trailing zeros of (c - lo)
+  // brick index (bricks NULL when absent)
+  const int32_t *order;
+  const struct Brick *bricks;
+  int32_t morton_bits, levels;
+  int32_t dims[RHIP_MAX_COLS];
 };
+
+// One entry of a table's brick grid: occupancy of the brick's cells (bit =
+// the cell's Morton index within the brick) and the locality-order position
+// of the brick's first row; the brick's rows follow it in cell order.
+struct alignas(16) Brick {
+  uint64_t mask;
+  int32_t base;
+  int32_t pad;
+};
+static_assert(sizeof(Brick) == 16, "brick entry must stay 16 bytes");
 
 inline TableView make_view(const rhip_table &t) {
   TableView v{};
@@ -129,6 +145,14 @@ inline TableView make_view(const rhip_table &t) {
     v.span[c] = static_cast<uint32_t>(static_cast<int64_t>(t.hi[c]) - t.lo[c]);
     v.shift[c] = t.shift[c];
   }
+  for (int c = 0; c < RHIP_MAX_COLS; ++c) {
+    v.tz[c] = t.tz[c];
+    v.dims[c] = t.brick_dims[c];
+  }
+  v.order = t.order;
+  v.bricks = static_cast<const Brick *>(t.bricks);
+  v.morton_bits = t.morton_bits;
+  v.levels = t.brick_levels;
   return v;
 }
 

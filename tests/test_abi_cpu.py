@@ -32,9 +32,10 @@ def test_library_exports_every_declared_symbol():
 
 
 def test_abi_version_and_struct_layout():
-    assert abi.lib().rhip_abi_version() == 11
-    # void*, int64, void*, int64, 3 x int32, 3 x int32[8] -> 140 bytes, padded to 144
-    assert ctypes.sizeof(abi.RhipTable) == 144
+    assert abi.lib().rhip_abi_version() == 12
+    # void*, int64, void*, int64, 3 x int32, 4 x int32[8] (172 bytes, padded to 176),
+    # 2 x void*, 2 x int32, int32[8] -> 232 bytes
+    assert ctypes.sizeof(abi.RhipTable) == 232
 
 
 def test_workspace_queries():

@@ -65,25 +65,39 @@ def test_lookup_present_absent_and_out_of_range():
     np.testing.assert_array_equal(got, exp)
 
 
-def test_spatial_order_is_morton_permutation():
+def _morton_order(rows):
+    """Batch first, then the Morton code of the spatial offsets from the
+    column minima, each shifted right by the trailing zero bits all offsets
+    of its column share (bit b of column j at b * D + (D - j)), stable."""
+    rows = rows.astype(np.int64)
+    D = rows.shape[1] - 1
+    rel = rows - rows.min(axis=0)
+    tz = []
+    for j in range(D + 1):
+        o = int(np.bitwise_or.reduce(rel[:, j]))
+        tz.append((o & -o).bit_length() - 1 if o else 0)
+    sh = np.stack([rel[:, j] >> tz[j] for j in range(D + 1)], 1)
+    wide = int(max(int(sh[:, j].max()).bit_length() for j in range(1, D + 1)))
+    key = rel[:, 0] << (wide * D)
+    for b in range(wide):
+        for j in range(1, D + 1):
+            key |= ((sh[:, j] >> b) & 1) << (b * D + (D - j))
+    return np.argsort(key, kind="stable")
+
+
+@pytest.mark.parametrize("stride", [1, 2, 4])
+def test_spatial_order_is_morton_permutation(stride):
     rng = np.random.default_rng(2)
     c = random_coords(rng, 40000, 3, 50, batch=3)
+    c[:, 1:] *= stride
     t = abi.hash_build(to_dev(c))
     order = t.order.cpu().numpy()
     pos = t.pos.cpu().numpy()
     np.testing.assert_array_equal(np.sort(order), np.arange(t.n))
     np.testing.assert_array_equal(pos[order], np.arange(t.n))
-    # batch first, then the Morton code of the spatial offsets from the
-    # column minima (bit b of column j at b * D + (D - j)), stable
-    rows = t.ucoords.cpu().numpy().astype(np.int64)
-    D = rows.shape[1] - 1
-    rel = rows - rows.min(axis=0)
-    wide = int(max(int(rel[:, j].max()).bit_length() for j in range(1, D + 1)))
-    key = rel[:, 0] << (wide * D)
-    for b in range(wide):
-        for j in range(1, D + 1):
-            key |= ((rel[:, j] >> b) & 1) << (b * D + (D - j))
-    np.testing.assert_array_equal(order, np.argsort(key, kind="stable"))
+    np.testing.assert_array_equal(order, _morton_order(t.ucoords.cpu().numpy()))
+    # a compact set gets a brick index over this order
+    assert t.struct.bricks is not None and t.struct.morton_bits > 0
 
 
 @pytest.mark.parametrize("cfg", ["sphere", "indoor", "lidar", "shell4d"])
