@@ -11,7 +11,8 @@ timed region starts.
 
 Printed as ONE JSON line:
   value        whole-job Mvoxels/s = N_in / (t_fwd + t_dX + t_dW) / 1e6
-  kernel_map_ms  hash build + locality order + kernel map, from device coords
+  kernel_map_ms  hash build + locality order + kernel map, from device coords,
+               through the C++ CoordinateManager (insert_and_map + kernel_map)
   kernel_map_roofline  the map build's algorithmic bytes (hash: rows read, slot
                and row-index writes; map: both sides' rows, one 8-byte probe
                per query, the pairs and offsets) / kernel_map_ms vs 8 TB/s
@@ -577,21 +578,29 @@ def main():
     offsets_np = stencil.region_offsets(3, 3)
     K = offsets_np.shape[0]
     coords = torch.from_numpy(coords_np).to(dev)
-    offsets = torch.from_numpy(offsets_np).to(dev)
     torch.cuda.synchronize()
 
     # kernel map: hash build + locality order + map (count, fill), from
     # coordinates already on the device; these calls read sizes back to the
-    # host, so they are timed on the host clock around a synchronize.
-    map_ms = []
-    for _ in range(args.map_reps + 1):
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
+    # host, so they are timed on the host clock around a synchronize. The
+    # headline time goes through the C++ CoordinateManager (insert_and_map,
+    # then kernel_map: the drop-in API, as the reference's CPU time below);
+    # the C ABI driven from Python (abi.hash_build + abi.kernel_map, whose
+    # result the steps use) is timed beside it.
+    import riemannengine_amd as rea
+
+    def manager_build():
+        mgr = rea.CoordinateManager(3)
+        key, _ = mgr.insert_and_map(coords, [1, 1, 1])
+        return mgr.kernel_map(key, key, [3, 3, 3], [1, 1, 1], [1, 1, 1])
+
+    def abi_build():
         table = abi.hash_build(coords)
-        km = abi.kernel_map(table, table, offsets)
-        torch.cuda.synchronize()
-        map_ms.append((time.perf_counter() - t0) * 1e3)
-    kmap_ms = statistics.median(map_ms[1:])
+        return abi.kernel_map(table, table, offsets_np)
+
+    mgr_map, kmap_ms = _map_time(manager_build, args.map_reps)
+    km, abi_map_ms = _map_time(abi_build, args.map_reps)
+    assert int(mgr_map["offsets_host"][-1]) == km.n_pairs
     n_in = n_out = km.n_in
     P = km.n_pairs
     D = coords_np.shape[1] - 1
@@ -605,6 +614,8 @@ def main():
                  "unit": "GB/s", "frac": round(map_gbs / PEAK_HBM_GBS, 4),
                  "algorithmic": {"hash_bytes": b_hash, "map_bytes": b_map},
                  "ms": round(kmap_ms, 3),
+                 "path": "C++ CoordinateManager.insert_and_map + kernel_map",
+                 "c_abi_from_python_ms": round(abi_map_ms, 3),
                  "note": "host clock around the build calls, which read sizes back to the host"}
 
     dtypes = [args.dtype] if args.dtype_given else ["f32", "bf16"]

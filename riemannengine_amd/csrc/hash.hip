@@ -20,21 +20,45 @@ namespace rhip {
 
 constexpr int kBlock = 256;
 
-__global__ void minmax_init_kernel(int32_t *mm, int ncol) {
-  int c = threadIdx.x;
-  if (c < ncol) {
-    mm[c] = INT_MAX;
-    mm[ncol + c] = INT_MIN;
-    mm[2 * ncol + c] = 0;
-  }
-}
+// Packing layout of a set, computed on the device so that the build needs
+// no host round trip before the inserts: per column the minimum, maximum and
+// common trailing zero bits, the packed key's shifts and width, and the key
+// mode; dups is set when some row repeats an earlier one; n_unique is written
+// by the numbering scan. row_bits > 0 when a packed key and a row index fit
+// one 64-bit word together: the insert then claims a slot with the word
+// (key << row_bits | row) in one compare-and-swap, a repeat lowers it with
+// atomicMin (same key bits, so the smaller row wins), and the numbering puts
+// the plain key back. Read back to the host once, at the end of the build.
+struct HashLayout {
+  int64_t n_unique;
+  int32_t lo[RHIP_MAX_COLS], hi[RHIP_MAX_COLS], shift[RHIP_MAX_COLS], tz[RHIP_MAX_COLS];
+  int32_t mode, key_bits, dups, row_bits;
+};
 
-// Column-wise min, max and OR of (value ^ row 0's value) of coords [n, ncol]
-// (the last gives the lowest bit in which a column varies); block-reduced in
-// LDS then merged with global atomics.
-__global__ __launch_bounds__(kBlock) void minmax_kernel(const int32_t *coords,
-                                                        int64_t n, int ncol,
-                                                        int32_t *mm) {
+constexpr int kMinmaxBlocks = 256;
+
+// Blocks [0, mm_blocks): per-block column minimum, maximum and OR of
+// (value ^ row 0's value) (its lowest set bit is the lowest bit in which the
+// column varies), over the coordinates read as one flat array so that loads
+// are coalesced (a lane keeps one column: the stride is a multiple of ncol);
+// partials[block][0..ncol) = min, [8..) = max, [16..) = or. Blocks past
+// mm_blocks clear the hash slots.
+__global__ __launch_bounds__(kBlock) void hash_prep_kernel(const int32_t *__restrict__ coords,
+                                                           int64_t n, int ncol, int mm_blocks,
+                                                           int32_t *__restrict__ partials,
+                                                           Slot *__restrict__ slots,
+                                                           int64_t cap) {
+  if (static_cast<int>(blockIdx.x) >= mm_blocks) {
+    const int64_t i = (blockIdx.x - mm_blocks) * (int64_t)kBlock + threadIdx.x;
+    if (i < cap) {
+      Slot s;
+      s.word = kEmptyWord;
+      s.first_row = 0xffffffffu;
+      s.uid = 0xffffffffu;
+      slots[i] = s;
+    }
+    return;
+  }
   __shared__ int32_t smin[RHIP_MAX_COLS], smax[RHIP_MAX_COLS], sor[RHIP_MAX_COLS];
   if (threadIdx.x < RHIP_MAX_COLS) {
     smin[threadIdx.x] = INT_MAX;
@@ -42,73 +66,126 @@ __global__ __launch_bounds__(kBlock) void minmax_kernel(const int32_t *coords,
     sor[threadIdx.x] = 0;
   }
   __syncthreads();
-  int32_t lmin[RHIP_MAX_COLS], lmax[RHIP_MAX_COLS], lor[RHIP_MAX_COLS], c0[RHIP_MAX_COLS];
-#pragma unroll
-  for (int c = 0; c < RHIP_MAX_COLS; ++c) {
-    lmin[c] = INT_MAX;
-    lmax[c] = INT_MIN;
-    lor[c] = 0;
-    c0[c] = c < ncol ? coords[c] : 0;
-  }
-#pragma unroll 4
-  for (int64_t r = blockIdx.x * (int64_t)kBlock + threadIdx.x; r < n;
-       r += (int64_t)gridDim.x * kBlock) {
-    const int32_t *row = coords + r * ncol;
-#pragma unroll
-    for (int c = 0; c < RHIP_MAX_COLS; ++c) {
-      if (c < ncol) {
-        int32_t v = row[c];
-        lmin[c] = min(lmin[c], v);
-        lmax[c] = max(lmax[c], v);
-        lor[c] |= v ^ c0[c];
-      }
+  const int64_t threads = static_cast<int64_t>(mm_blocks) * kBlock;
+  const int64_t stride = threads - threads % ncol;
+  const int64_t i0 = blockIdx.x * (int64_t)kBlock + threadIdx.x;
+  if (i0 < stride) {
+    const int c = static_cast<int>(i0 % ncol);
+    const int32_t c0 = coords[c];
+    int32_t lmin = INT_MAX, lmax = INT_MIN, lor = 0;
+    for (int64_t f = i0; f < n * ncol; f += stride) {
+      const int32_t v = coords[f];
+      lmin = min(lmin, v);
+      lmax = max(lmax, v);
+      lor |= v ^ c0;
     }
-  }
-#pragma unroll
-  for (int c = 0; c < RHIP_MAX_COLS; ++c) {
-    if (c < ncol) {
-      int32_t a = lmin[c], b = lmax[c], o = lor[c];
-      for (int off = 32; off > 0; off >>= 1) {
-        a = min(a, __shfl_xor(a, off));
-        b = max(b, __shfl_xor(b, off));
-        o |= __shfl_xor(o, off);
-      }
-      if (lane_id() == 0) {
-        atomicMin(&smin[c], a);
-        atomicMax(&smax[c], b);
-        atomicOr(&sor[c], o);
-      }
-    }
+    atomicMin(&smin[c], lmin);
+    atomicMax(&smax[c], lmax);
+    atomicOr(&sor[c], lor);
   }
   __syncthreads();
   if (threadIdx.x < ncol) {
-    atomicMin(&mm[threadIdx.x], smin[threadIdx.x]);
-    atomicMax(&mm[ncol + threadIdx.x], smax[threadIdx.x]);
-    atomicOr(&mm[2 * ncol + threadIdx.x], sor[threadIdx.x]);
+    int32_t *p = partials + blockIdx.x * 3 * RHIP_MAX_COLS;
+    p[threadIdx.x] = smin[threadIdx.x];
+    p[RHIP_MAX_COLS + threadIdx.x] = smax[threadIdx.x];
+    p[2 * RHIP_MAX_COLS + threadIdx.x] = sor[threadIdx.x];
   }
 }
 
-__global__ __launch_bounds__(kBlock) void slots_init_kernel(Slot *slots,
-                                                            int64_t cap) {
-  int64_t i = blockIdx.x * (int64_t)kBlock + threadIdx.x;
-  if (i < cap) {
-    Slot s;
-    s.word = kEmptyWord;
-    s.first_row = 0xffffffffu;
-    s.uid = 0xffffffffu;
-    slots[i] = s;
+__device__ __forceinline__ int bit_width_dev(uint32_t v) { return v == 0 ? 0 : 32 - __clz(v); }
+
+// One workgroup: merges the prep partials into the layout (lane k reads
+// block k's partials; wave shuffles, then LDS, combine them). Columns are
+// packed with the batch column in the top bits, so the packed order is
+// batch-major lexicographic; more than 63 bits selects the row-reference mode.
+__global__ __launch_bounds__(kBlock) void hash_layout_kernel(const int32_t *__restrict__ partials,
+                                                             int mm_blocks, int ncol, int64_t n,
+                                                             HashLayout *__restrict__ L) {
+  constexpr int kWaves = kBlock / kWave;
+  __shared__ int32_t red[kWaves][3 * RHIP_MAX_COLS];
+  const int k = threadIdx.x, w = k / kWave, lane = lane_id();
+  for (int c = 0; c < ncol; ++c) {
+    int32_t a = INT_MAX, b = INT_MIN, o = 0;
+    for (int j = k; j < mm_blocks; j += kBlock) {
+      const int32_t *p = partials + j * 3 * RHIP_MAX_COLS;
+      a = min(a, p[c]);
+      b = max(b, p[RHIP_MAX_COLS + c]);
+      o |= p[2 * RHIP_MAX_COLS + c];
+    }
+    for (int off = 32; off > 0; off >>= 1) {
+      a = min(a, __shfl_xor(a, off));
+      b = max(b, __shfl_xor(b, off));
+      o |= __shfl_xor(o, off);
+    }
+    if (lane == 0) {
+      red[w][c] = a;
+      red[w][RHIP_MAX_COLS + c] = b;
+      red[w][2 * RHIP_MAX_COLS + c] = o;
+    }
+  }
+  __syncthreads();
+  if (k != 0)
+    return;
+  int32_t mn[RHIP_MAX_COLS], mx[RHIP_MAX_COLS], ox[RHIP_MAX_COLS];
+  int bits[RHIP_MAX_COLS] = {};
+  int total = 0;
+  for (int i = 0; i < ncol; ++i) {
+    mn[i] = red[0][i];
+    mx[i] = red[0][RHIP_MAX_COLS + i];
+    ox[i] = red[0][2 * RHIP_MAX_COLS + i];
+    for (int v = 1; v < kWaves; ++v) {
+      mn[i] = min(mn[i], red[v][i]);
+      mx[i] = max(mx[i], red[v][RHIP_MAX_COLS + i]);
+      ox[i] |= red[v][2 * RHIP_MAX_COLS + i];
+    }
+    bits[i] = bit_width_dev(static_cast<uint32_t>(static_cast<int64_t>(mx[i]) - mn[i]));
+    total += bits[i];
+  }
+  int sh = 0;
+  for (int i = ncol - 1; i >= 0; --i) {
+    L->shift[i] = total <= 63 ? sh : 0;
+    sh += bits[i];
+  }
+  for (int i = 0; i < RHIP_MAX_COLS; ++i) {
+    L->lo[i] = i < ncol ? mn[i] : 0;
+    L->hi[i] = i < ncol ? mx[i] : 0;
+    L->tz[i] = i < ncol && ox[i] != 0 ? __ffs(ox[i]) - 1 : 0;
+    if (i >= ncol)
+      L->shift[i] = 0;
+  }
+  L->mode = total <= 63 ? RHIP_KEY_PACKED64 : RHIP_KEY_ROWREF;
+  L->key_bits = total <= 63 ? total : 0;
+  L->dups = 0;
+  L->n_unique = 0;
+  const int rb = max(1, bit_width_dev(static_cast<uint32_t>(n - 1)));
+  L->row_bits = total + rb <= 63 ? rb : 0;
+}
+
+// The device layout's ranges and mode in a table view.
+__device__ __forceinline__ void apply_layout(TableView &t, const HashLayout *L) {
+  t.mode = L->mode;
+#pragma unroll
+  for (int c = 0; c < RHIP_MAX_COLS; ++c) {
+    t.lo[c] = L->lo[c];
+    t.span[c] = static_cast<uint32_t>(static_cast<int64_t>(L->hi[c]) - L->lo[c]);
+    t.shift[c] = L->shift[c];
   }
 }
 
-// One lane per input row: claim or find the row's slot, then lower the
-// slot's first_row to this row if it is earlier.
+// One lane per input row: claim or find the row's slot; the slot keeps the
+// earliest row that inserted the key (in the key word when row_bits > 0,
+// else in first_row through atomicMin). A row that finds its key already
+// there flags the set as having repeats.
 __global__ __launch_bounds__(kBlock) void insert_kernel(const int32_t *coords,
                                                         int64_t n,
                                                         TableView t,
+                                                        HashLayout *L,
                                                         uint32_t *slot_of_row) {
   int64_t r = blockIdx.x * (int64_t)kBlock + threadIdx.x;
   if (r >= n)
     return;
+  apply_layout(t, L);
+  const int rb = L->row_bits;
   int32_t c[RHIP_MAX_COLS];
 #pragma unroll
   for (int i = 0; i < RHIP_MAX_COLS; ++i)
@@ -124,18 +201,24 @@ __global__ __launch_bounds__(kBlock) void insert_kernel(const int32_t *coords,
     key = (static_cast<uint64_t>(hr) << 32) | static_cast<uint32_t>(r);
     h = mix64(hr) & t.mask;
   }
+  const uint64_t mine = rb > 0 ? (key << rb) | static_cast<uint64_t>(r) : key;
   while (true) {
     uint64_t *wp = &t.slots[h].word;
     uint64_t w = __hip_atomic_load(wp, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (w == kEmptyWord) {
       uint64_t prev = atomicCAS(reinterpret_cast<unsigned long long *>(wp),
-                                kEmptyWord, key);
-      if (prev == kEmptyWord)
+                                kEmptyWord, mine);
+      if (prev == kEmptyWord) {
+        if (rb == 0)
+          atomicMin(&t.slots[h].first_row, static_cast<uint32_t>(r));
         break; // claimed
+      }
       w = prev;
     }
     bool same;
-    if (t.mode == RHIP_KEY_PACKED64) {
+    if (rb > 0) {
+      same = (w >> rb) == key;
+    } else if (t.mode == RHIP_KEY_PACKED64) {
       same = (w == key);
     } else {
       same = static_cast<uint32_t>(w >> 32) == hr &&
@@ -143,21 +226,42 @@ __global__ __launch_bounds__(kBlock) void insert_kernel(const int32_t *coords,
                                      t.ncol,
                         c, t.ncol);
     }
-    if (same)
+    if (same) {
+      L->dups = 1;
+      if (rb > 0) {
+        if (mine < w)
+          atomicMin(reinterpret_cast<unsigned long long *>(wp), mine);
+      } else {
+        atomicMin(&t.slots[h].first_row, static_cast<uint32_t>(r));
+      }
       break;
+    }
     h = (h + 1) & t.mask;
   }
-  atomicMin(&t.slots[h].first_row, static_cast<uint32_t>(r));
   slot_of_row[r] = static_cast<uint32_t>(h);
 }
 
-// Per-block count of rows that are the first occurrence of their key.
+// Per-block count of rows that are the first occurrence of their key (every
+// row is when the set has no repeats). With repeats and row_bits > 0, the
+// first row also copies itself into its slot's first_row, where the later
+// kernels read it while the key word is rewritten.
 __global__ __launch_bounds__(kBlock) void count_first_kernel(
-    int64_t n, const Slot *slots, const uint32_t *slot_of_row,
+    int64_t n, const HashLayout *L, Slot *slots, const uint32_t *slot_of_row,
     int32_t *block_counts) {
   __shared__ int32_t wave_counts[kBlock / kWave];
   int64_t r = blockIdx.x * (int64_t)kBlock + threadIdx.x;
-  bool first = r < n && slots[slot_of_row[r]].first_row == static_cast<uint32_t>(r);
+  bool first = r < n;
+  if (first && L->dups) {
+    Slot &s = slots[slot_of_row[r]];
+    const int rb = L->row_bits;
+    if (rb > 0) {
+      first = (s.word & ((1ull << rb) - 1)) == static_cast<uint64_t>(r);
+      if (first)
+        s.first_row = static_cast<uint32_t>(r);
+    } else {
+      first = s.first_row == static_cast<uint32_t>(r);
+    }
+  }
   uint64_t b = __ballot(first);
   if (lane_id() == 0)
     wave_counts[threadIdx.x / kWave] = __popcll(b);
@@ -170,15 +274,19 @@ __global__ __launch_bounds__(kBlock) void count_first_kernel(
   }
 }
 
-// First rows get uid = block base + rank within the block; they also write
-// mapping[uid] and the unique coordinates.
+// First rows get uid = block base + rank within the block; they write
+// mapping[uid], the unique coordinates, their own inverse entry and their
+// slot's uid, and put the plain key back in the slot word (in row-reference
+// mode the key is re-pointed at the unique row). With repeats, uid_by_row
+// keeps the uid for the other rows' inverse.
 __global__ __launch_bounds__(kBlock) void assign_uid_kernel(
-    const int32_t *coords, int64_t n, int ncol, const Slot *slots,
+    const int32_t *coords, int64_t n, int ncol, const HashLayout *L, Slot *slots,
     const uint32_t *slot_of_row, const int64_t *block_base, int32_t *uid_by_row,
-    int64_t *mapping, int32_t *unique_coords) {
+    int64_t *mapping, int32_t *unique_coords, int64_t *inverse) {
   __shared__ int32_t wave_counts[kBlock / kWave];
   int64_t r = blockIdx.x * (int64_t)kBlock + threadIdx.x;
-  bool first = r < n && slots[slot_of_row[r]].first_row == static_cast<uint32_t>(r);
+  const bool first =
+      r < n && (L->dups == 0 || slots[slot_of_row[r]].first_row == static_cast<uint32_t>(r));
   uint64_t b = __ballot(first);
   const int w = threadIdx.x / kWave;
   if (lane_id() == 0)
@@ -188,34 +296,50 @@ __global__ __launch_bounds__(kBlock) void assign_uid_kernel(
   for (int i = 0; i < w; ++i)
     before += wave_counts[i];
   if (first) {
-    int64_t uid = block_base[blockIdx.x] + before + lanes_below(b);
-    uid_by_row[r] = static_cast<int32_t>(uid);
+    const int64_t uid = block_base[blockIdx.x] + before + lanes_below(b);
+    if (L->dups)
+      uid_by_row[r] = static_cast<int32_t>(uid);
     mapping[uid] = r;
-    for (int c = 0; c < ncol; ++c)
-      unique_coords[uid * ncol + c] = coords[r * ncol + c];
+    if (inverse)
+      inverse[r] = uid;
+    // the slot's final contents, from the row itself: one store, no read
+    int32_t c[RHIP_MAX_COLS];
+#pragma unroll
+    for (int i = 0; i < RHIP_MAX_COLS; ++i)
+      c[i] = i < ncol ? coords[r * ncol + i] : 0;
+#pragma unroll
+    for (int i = 0; i < RHIP_MAX_COLS; ++i)
+      if (i < ncol)
+        unique_coords[uid * ncol + i] = c[i];
+    Slot out;
+    out.first_row = static_cast<uint32_t>(r);
+    out.uid = static_cast<uint32_t>(uid);
+    if (L->mode == RHIP_KEY_PACKED64) {
+      uint64_t key = 0;
+#pragma unroll
+      for (int i = 0; i < RHIP_MAX_COLS; ++i)
+        if (i < ncol)
+          key |= static_cast<uint64_t>(static_cast<uint32_t>(c[i]) -
+                                       static_cast<uint32_t>(L->lo[i]))
+                 << L->shift[i];
+      out.word = key;
+    } else {
+      out.word = (static_cast<uint64_t>(hash_row(c, ncol)) << 32) | static_cast<uint32_t>(uid);
+    }
+    slots[slot_of_row[r]] = out;
   }
 }
 
-// inverse[r] = uid of r's first occurrence; first rows publish their uid in
-// the slot (and, in row-reference mode, re-point the key at the unique row).
+// Sets with repeats: inverse[r] = uid of the first occurrence of r's key.
 __global__ __launch_bounds__(kBlock) void resolve_kernel(
-    const int32_t *coords, int64_t n, TableView t, const uint32_t *slot_of_row,
+    int64_t n, const HashLayout *L, const Slot *slots, const uint32_t *slot_of_row,
     const int32_t *uid_by_row, int64_t *inverse) {
   int64_t r = blockIdx.x * (int64_t)kBlock + threadIdx.x;
-  if (r >= n)
+  if (r >= n || L->dups == 0)
     return;
-  uint32_t h = slot_of_row[r];
-  uint32_t fr = t.slots[h].first_row;
-  int32_t uid = uid_by_row[fr];
-  if (inverse)
-    inverse[r] = uid;
-  if (fr == static_cast<uint32_t>(r)) {
-    t.slots[h].uid = static_cast<uint32_t>(uid);
-    if (t.mode == RHIP_KEY_ROWREF) {
-      uint32_t hr = static_cast<uint32_t>(t.slots[h].word >> 32);
-      t.slots[h].word = (static_cast<uint64_t>(hr) << 32) | static_cast<uint32_t>(uid);
-    }
-  }
+  const uint32_t fr = slots[slot_of_row[r]].first_row;
+  if (fr != static_cast<uint32_t>(r))
+    inverse[r] = uid_by_row[fr];
 }
 
 __global__ __launch_bounds__(kBlock) void lookup_kernel(TableView t,
@@ -372,23 +496,23 @@ static int64_t table_capacity(int64_t n) {
 }
 
 struct HashWs {
-  int32_t *minmax;
+  HashLayout *layout;
+  int32_t *partials;
   uint32_t *slot_of_row;
   int32_t *uid_by_row;
   int32_t *block_counts;
   int64_t *block_base;
-  int64_t *total;
 };
 
 static HashWs carve_hash(Carve &cv, int64_t n, int ncol) {
   HashWs w;
   const int64_t nb = std::max<int64_t>(1, ceil_div(n, kBlock));
-  w.minmax = cv.take<int32_t>(3 * RHIP_MAX_COLS);
+  w.layout = cv.take<HashLayout>(1);
+  w.partials = cv.take<int32_t>(static_cast<size_t>(kMinmaxBlocks) * 3 * RHIP_MAX_COLS);
   w.slot_of_row = cv.take<uint32_t>(std::max<int64_t>(n, 1));
   w.uid_by_row = cv.take<int32_t>(std::max<int64_t>(n, 1));
   w.block_counts = cv.take<int32_t>(nb);
   w.block_base = cv.take<int64_t>(nb);
-  w.total = cv.take<int64_t>(1);
   (void)ncol;
   return w;
 }
@@ -440,79 +564,61 @@ extern "C" int rhip_hash_build(const int32_t *coords, int64_t n, int32_t ncol,
     table->rows = unique_coords;
     table->ncol = ncol;
     Slot *sl = static_cast<Slot *>(slots);
-    hipLaunchKernelGGL(slots_init_kernel, dim3(ceil_div(cap, kBlock)),
-                       dim3(kBlock), 0, stream, sl, cap);
-    RHIP_LAUNCH_CHECK();
     if (n == 0) {
+      hipLaunchKernelGGL(hash_prep_kernel, dim3(ceil_div(cap, kBlock)), dim3(kBlock), 0, stream,
+                         coords, n, ncol, 0, w.partials, sl, cap);
+      RHIP_LAUNCH_CHECK();
       table->mode = RHIP_KEY_PACKED64;
       table->n_unique = 0;
       for (int c = 0; c < ncol; ++c)
         table->hi[c] = -1; // empty range: every probe misses on span check
       return;
     }
-
-    // Column bounds -> packing layout (batch column in the top bits so the
-    // packed order is batch-major lexicographic).
-    hipLaunchKernelGGL(minmax_init_kernel, dim3(1), dim3(RHIP_MAX_COLS), 0,
-                       stream, w.minmax, ncol);
-    const int64_t nb = ceil_div(n, kBlock);
-    // few workgroups: each merges its result with 2 * ncol atomics on the
-    // same 2 * ncol addresses, which serialise
-    hipLaunchKernelGGL(minmax_kernel, dim3(std::min<int64_t>(nb, 256)),
-                       dim3(kBlock), 0, stream, coords, n, ncol, w.minmax);
+    // column ranges and slot clearing in one launch, then the layout on the
+    // device: the inserts start without a host round trip
+    const int mm = static_cast<int>(std::min<int64_t>(
+        kMinmaxBlocks, std::max<int64_t>(1, ceil_div(n * ncol, int64_t(kBlock) * 8))));
+    hipLaunchKernelGGL(hash_prep_kernel, dim3(mm + ceil_div(cap, kBlock)), dim3(kBlock), 0,
+                       stream, coords, n, ncol, mm, w.partials, sl, cap);
     RHIP_LAUNCH_CHECK();
-    int32_t mm[3 * RHIP_MAX_COLS];
-    RHIP_HIP(hipMemcpyAsync(mm, w.minmax, sizeof(int32_t) * 3 * ncol,
-                            hipMemcpyDeviceToHost, stream));
-    RHIP_HIP(hipStreamSynchronize(stream));
-    int total_bits = 0;
-    int bits[RHIP_MAX_COLS];
-    for (int c = 0; c < ncol; ++c) {
-      table->lo[c] = mm[c];
-      table->hi[c] = mm[ncol + c];
-      bits[c] = bit_width_u32(static_cast<uint32_t>(
-          static_cast<int64_t>(mm[ncol + c]) - mm[c]));
-      total_bits += bits[c];
-    }
-    int sh = 0;
-    for (int c = ncol - 1; c >= 0; --c) {
-      table->shift[c] = total_bits <= 63 ? sh : 0;
-      sh += bits[c];
-    }
-    table->mode = total_bits <= 63 ? RHIP_KEY_PACKED64 : RHIP_KEY_ROWREF;
-    table->key_bits = total_bits <= 63 ? total_bits : 0;
-    // the lowest bit in which each column varies (coordinates at tensor
-    // stride 2^s vary from bit s up)
-    for (int c = 0; c < ncol; ++c) {
-      const uint32_t orx = static_cast<uint32_t>(mm[2 * ncol + c]);
-      table->tz[c] = orx != 0 ? __builtin_ctz(orx) : 0;
-    }
-
+    hipLaunchKernelGGL(hash_layout_kernel, dim3(1), dim3(kBlock), 0, stream, w.partials, mm, ncol,
+                       n, w.layout);
+    RHIP_LAUNCH_CHECK();
     // The row-reference build probes the caller's coordinates; lookups after
-    // the build probe unique_coords (resolve_kernel re-points the slots).
+    // the build probe unique_coords (assign_uid_kernel re-points the slots).
     TableView tv = make_view(*table);
     tv.rows = coords;
-    hipLaunchKernelGGL(insert_kernel, dim3(nb), dim3(kBlock), 0, stream, coords,
-                       n, tv, w.slot_of_row);
+    const int64_t nb = ceil_div(n, kBlock);
+    hipLaunchKernelGGL(insert_kernel, dim3(nb), dim3(kBlock), 0, stream, coords, n, tv, w.layout,
+                       w.slot_of_row);
     RHIP_LAUNCH_CHECK();
-    hipLaunchKernelGGL(count_first_kernel, dim3(nb), dim3(kBlock), 0, stream, n,
-                       sl, w.slot_of_row, w.block_counts);
+    hipLaunchKernelGGL(count_first_kernel, dim3(nb), dim3(kBlock), 0, stream, n, w.layout, sl,
+                       w.slot_of_row, w.block_counts);
     RHIP_LAUNCH_CHECK();
-    hipLaunchKernelGGL(scan_kernel<int32_t>, dim3(1), dim3(1024), 0, stream,
-                       w.block_counts, nb, w.block_base, w.total);
+    hipLaunchKernelGGL(scan_kernel<int32_t>, dim3(1), dim3(1024), 0, stream, w.block_counts, nb,
+                       w.block_base, &w.layout->n_unique);
     RHIP_LAUNCH_CHECK();
-    hipLaunchKernelGGL(assign_uid_kernel, dim3(nb), dim3(kBlock), 0, stream,
-                       coords, n, ncol, sl, w.slot_of_row, w.block_base,
-                       w.uid_by_row, mapping, unique_coords);
+    hipLaunchKernelGGL(assign_uid_kernel, dim3(nb), dim3(kBlock), 0, stream, coords, n, ncol,
+                       w.layout, sl, w.slot_of_row, w.block_base, w.uid_by_row, mapping,
+                       unique_coords, inverse);
     RHIP_LAUNCH_CHECK();
-    hipLaunchKernelGGL(resolve_kernel, dim3(nb), dim3(kBlock), 0, stream,
-                       coords, n, tv, w.slot_of_row, w.uid_by_row, inverse);
-    RHIP_LAUNCH_CHECK();
-    int64_t nu = 0;
-    RHIP_HIP(hipMemcpyAsync(&nu, w.total, sizeof(int64_t),
-                            hipMemcpyDeviceToHost, stream));
+    if (inverse) {
+      hipLaunchKernelGGL(resolve_kernel, dim3(nb), dim3(kBlock), 0, stream, n, w.layout, sl,
+                         w.slot_of_row, w.uid_by_row, inverse);
+      RHIP_LAUNCH_CHECK();
+    }
+    HashLayout hl;
+    RHIP_HIP(hipMemcpyAsync(&hl, w.layout, sizeof(hl), hipMemcpyDeviceToHost, stream));
     RHIP_HIP(hipStreamSynchronize(stream));
-    table->n_unique = nu;
+    table->n_unique = hl.n_unique;
+    table->mode = hl.mode;
+    table->key_bits = hl.key_bits;
+    for (int c = 0; c < RHIP_MAX_COLS; ++c) {
+      table->lo[c] = hl.lo[c];
+      table->hi[c] = hl.hi[c];
+      table->shift[c] = hl.shift[c];
+      table->tz[c] = hl.tz[c];
+    }
   });
 }
 

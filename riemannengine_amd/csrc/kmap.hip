@@ -56,22 +56,24 @@ constexpr int kMaskedK = 128; // neighbour masks (and mask order) for K <= 128
 constexpr int kKeyBits = 16;  // sort-key width of a neighbour mask
 static int64_t map_waves(int64_t n) { return std::max<int64_t>(1, ceil_div(n, kWave)); }
 
-// Sort key of a neighbour mask: the mask itself for K <= 16; else 22 bits,
-// the neighbour count (largest first, 127 and more alike) above a 15-bit
-// hash of the mask (equal masks get equal keys; unequal ones rarely
-// collide, which only costs MFMA fill, never correctness). Largest first
-// puts the tiles with the most stages at the front of the convolution grid,
-// so the grid does not end on a few long workgroups; 22 bits sort in three
-// 8-bit passes.
+// Sort key of a neighbour mask: the mask itself for K <= 16; else the
+// neighbour count (largest first) above a hash of the mask: 5 + 11 bits for
+// K <= 31 (two 8-bit sort passes), 7 + 15 bits up to K = 128 (three). Equal
+// masks get equal keys; unequal ones with the same count rarely collide,
+// which only costs MFMA fill, never correctness. Largest first puts the
+// tiles with the most stages at the front of the convolution grid, so the
+// grid does not end on a few long workgroups.
 __device__ __forceinline__ uint32_t mask_key(uint64_t m0, uint64_t m1, int K) {
   if (K <= kKeyBits)
     return static_cast<uint32_t>(m0);
-  const uint32_t count = min(127u, static_cast<uint32_t>(__popcll(m0) + __popcll(m1)));
-  return ((127u - count) << 15) |
-         static_cast<uint32_t>(mix64(m0 ^ mix64(m1 ^ 0x9e3779b97f4a7c15ull)) >> 49);
+  const uint32_t count = static_cast<uint32_t>(__popcll(m0) + __popcll(m1));
+  const uint64_t h = mix64(m0 ^ mix64(m1 ^ 0x9e3779b97f4a7c15ull));
+  if (K <= 31)
+    return ((31u - count) << 11) | static_cast<uint32_t>(h >> 53);
+  return ((127u - min(127u, count)) << 15) | static_cast<uint32_t>(h >> 49);
 }
 // Bits of mask_key for K offsets.
-static int mask_key_bits(int K) { return K <= kKeyBits ? K : 22; }
+static int mask_key_bits(int K) { return K <= kKeyBits ? K : (K <= 31 ? 16 : 22); }
 
 // Resolves probes k0 .. k0+7 of an output row with coordinates c (batch
 // offset d0 = c[0] - lo[0], row_ok = the batch is in range): r[u] = the

@@ -46,8 +46,9 @@ def _mix64(k):
 
 def _mask_keys(table):
     """Sort key of each column's neighbour mask: the mask for K <= 16, else
-    (127 - min(neighbour count, 127)) above a 15-bit hash of its two 64-bit
-    words."""
+    the neighbour count, largest first, above a hash of the mask's two 64-bit
+    words: (31 - count) above 11 hash bits for K <= 31, (127 - min(count, 127))
+    above 15 hash bits otherwise."""
     K = table.shape[0]
     hit = (table >= 0).astype(np.uint64)
     m = np.zeros((2, table.shape[1]), np.uint64)
@@ -55,10 +56,13 @@ def _mask_keys(table):
         m[k // 64] |= hit[k] << np.uint64(k % 64)
     if K <= 16:
         return m[0]
-    count = np.minimum(np.bitwise_count(m[0]) + np.bitwise_count(m[1]), 127).astype(np.uint64)
+    count = (np.bitwise_count(m[0]) + np.bitwise_count(m[1])).astype(np.uint64)
     with np.errstate(over="ignore"):
-        h = _mix64(m[0] ^ _mix64(m[1] ^ np.uint64(0x9e3779b97f4a7c15))) >> np.uint64(49)
-    return ((np.uint64(127) - count) << np.uint64(15)) | h
+        h = _mix64(m[0] ^ _mix64(m[1] ^ np.uint64(0x9e3779b97f4a7c15)))
+    if K <= 31:
+        return ((np.uint64(31) - count) << np.uint64(11)) | (h >> np.uint64(53))
+    count = np.minimum(count, np.uint64(127))
+    return ((np.uint64(127) - count) << np.uint64(15)) | (h >> np.uint64(49))
 
 
 def _check_tables(km, tin, tout):
