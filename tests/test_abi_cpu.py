@@ -41,7 +41,9 @@ def test_abi_version_and_struct_layout():
 def test_workspace_queries():
     L = abi.lib()
     assert abi._sizeq(L.rhip_hash_workspace_bytes, 1000, 4) > 1000 * 8
-    assert abi._sizeq(L.rhip_kmap_workspace_bytes, 1000, 1000, 27) > 27 * 1000 * 4
+    # per-wave hit counts and their scans for each offset, the mask sort's keys
+    # and values (two pairs)
+    assert abi._sizeq(L.rhip_kmap_workspace_bytes, 1000, 1000, 27) > 27 * 16 * 12 + 4 * 1000 * 4
     # transposed weights + fp32 accumulator, plus the dW partial tiles
     base = 27 * 64 * 64 * (2 + 4)
     assert abi._sizeq(L.rhip_conv_workspace_bytes, 27, 64, 64, abi.BF16, 1000, 1000, 0) >= base
