@@ -3,24 +3,21 @@
 // (grouping rows by output). Least-significant-digit first with 8- or 9-bit
 // digits: the fewest passes the key bits allow, then the narrowest digit for
 // that many passes (26 bits: 3 passes of 9; 22 bits: 3 of 8; 16 bits: 2 of
-// 8). Two kernels per pass over tiles of 4096 keys:
+// 8). Three kernels per pass over tiles of 4096 keys:
 //
 //   radix_hist_kernel     one workgroup per tile: the tile's digit counts
-//                         (LDS atomics), stored digit-major, counts[d][tile],
-//                         so that one digit's counts over all tiles are
-//                         contiguous;
+//                         (LDS atomics), stored digit-major, counts[d][tile];
+//   radix_row_scan_kernel one wave per digit: exclusive scan of the digit's
+//                         counts over the tiles (the digit's keys in earlier
+//                         tiles) and the digit's total;
 //   radix_scatter_kernel  one workgroup per tile: ranks its keys by digit
 //                         (wave ballots in key order, so equal digits keep
-//                         their order), reads its digits' rows of the count
-//                         table (16-byte loads) for the keys of each digit in
-//                         all tiles and in the tiles before it, scans the
-//                         digit totals for where each digit's run starts, and
-//                         writes its keys staged in LDS by digit, so that each
-//                         digit's run goes out contiguously.
+//                         their order), scans the digit totals in LDS for
+//                         where each digit starts, stages its keys in LDS by
+//                         digit and writes each digit's run contiguously.
 //
-// No tile waits on another: every count the scatter needs is final when it
-// starts. Every buffer the sort needs is carved from the caller's scratch;
-// nothing is allocated or memset.
+// Every buffer the sort needs is carved from the caller's scratch; nothing is
+// allocated or memset.
 #include "rhip_internal.hpp"
 
 #include <algorithm>
@@ -100,11 +97,46 @@ __global__ __launch_bounds__(kSortThreads) void radix_hist_kernel(
     counts[d * tiles + blockIdx.x] = hist[d];
 }
 
+// Per digit (one wave each, blockIdx.x = digit): exclusive scan of the
+// digit's counts over the tiles, base[d][tile], and the digit's total.
+__global__ __launch_bounds__(kWave) void radix_row_scan_kernel(const uint32_t *__restrict__ counts,
+                                                              int64_t tiles,
+                                                              uint32_t *__restrict__ base,
+                                                              uint32_t *__restrict__ total) {
+  const int lane = lane_id();
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * tiles;
+  uint32_t carry = 0;
+  for (int64_t t0 = 0; t0 < tiles; t0 += 4 * kWave) {
+    // lane owns tiles t0 + 4 lane .. + 3 (tiles is a multiple of 4)
+    const int64_t e = t0 + 4 * lane;
+    const uint4 v = e < tiles ? *reinterpret_cast<const uint4 *>(counts + row + e)
+                              : uint4{0u, 0u, 0u, 0u};
+    const uint32_t sum = v.x + v.y + v.z + v.w;
+    uint32_t incl = sum;
+#pragma unroll
+    for (int off = 1; off < kWave; off <<= 1) {
+      const uint32_t o = __shfl_up(incl, off, kWave);
+      if (lane >= off)
+        incl += o;
+    }
+    uint4 o;
+    o.x = carry + incl - sum;
+    o.y = o.x + v.x;
+    o.z = o.y + v.y;
+    o.w = o.z + v.z;
+    if (e < tiles)
+      *reinterpret_cast<uint4 *>(base + row + e) = o;
+    carry += __shfl(incl, kWave - 1, kWave);
+  }
+  if (lane == 0)
+    total[blockIdx.x] = carry;
+}
+
 template <typename K, int R>
 __global__ __launch_bounds__(kSortThreads) void radix_scatter_kernel(
     const K *__restrict__ kin, const int32_t *__restrict__ vin, K *__restrict__ kout,
     int32_t *__restrict__ vout, int64_t n, int shift, uint32_t dmask,
-    const uint32_t *__restrict__ counts, int64_t tiles) {
+    const uint32_t *__restrict__ base, const uint32_t *__restrict__ total, int64_t tiles) {
   constexpr int kDigits = 1 << R;
   constexpr int kPer = kDigits / kSortThreads; // digits per thread (1 or 2)
   __shared__ uint32_t wh[kSortWaves][kDigits]; // per-wave digit runs, then wave offsets
@@ -150,9 +182,10 @@ __global__ __launch_bounds__(kSortThreads) void radix_scatter_kernel(
   }
   __syncthreads();
 
-  // this thread's digits: the tile's count (wave runs become wave offsets),
-  // and from the count table the keys in all tiles and in earlier tiles
-  uint32_t cnt[kPer], before[kPer], total[kPer];
+  // this thread's digits: the tile's count (wave runs become wave offsets)
+  // and the output position of the tile's run from the scanned count table
+  uint32_t cnt_mine = 0;
+  uint32_t cnt[kPer];
 #pragma unroll
   for (int q = 0; q < kPer; ++q) {
     const int d = t * kPer + q;
@@ -164,34 +197,28 @@ __global__ __launch_bounds__(kSortThreads) void radix_scatter_kernel(
       run += c;
     }
     cnt[q] = run;
-    before[q] = 0;
-    total[q] = 0;
-    if (d <= static_cast<int>(dmask)) {
-      const uint4 *row = reinterpret_cast<const uint4 *>(counts + d * tiles);
-      for (int64_t j = 0; j < tiles / 4; ++j) {
-        const uint4 c = row[j];
-        const int64_t tt = 4 * j;
-        total[q] += c.x + c.y + c.z + c.w;
-        before[q] += (tt < tile ? c.x : 0u) + (tt + 1 < tile ? c.y : 0u) +
-                     (tt + 2 < tile ? c.z : 0u) + (tt + 3 < tile ? c.w : 0u);
-      }
-    }
+    cnt_mine += run;
   }
-  // where each digit's run starts in the output, and in the tile
-  uint32_t tot_mine = 0, cnt_mine = 0;
-#pragma unroll
-  for (int q = 0; q < kPer; ++q) {
-    tot_mine += total[q];
-    cnt_mine += cnt[q];
-  }
-  uint32_t dbase = block_exclusive_scan(tot_mine, wave_sum[0]);
-  uint32_t lbase = block_exclusive_scan(cnt_mine, wave_sum[1]);
+  // where each digit's run starts in the output (keys of smaller digits, then
+  // this digit's keys in earlier tiles) and in the tile
+  uint32_t tot[kPer], tot_mine = 0;
 #pragma unroll
   for (int q = 0; q < kPer; ++q) {
     const int d = t * kPer + q;
-    gbase[d] = dbase + before[q];
-    loc[d] = lbase;
-    dbase += total[q];
+    tot[q] = d <= static_cast<int>(dmask) ? total[d] : 0u;
+    tot_mine += tot[q];
+  }
+  uint32_t dstart = block_exclusive_scan(tot_mine, wave_sum[0]);
+#pragma unroll
+  for (int q = 0; q < kPer; ++q) {
+    const int d = t * kPer + q;
+    gbase[d] = dstart + (d <= static_cast<int>(dmask) ? base[d * tiles + tile] : 0u);
+    dstart += tot[q];
+  }
+  uint32_t lbase = block_exclusive_scan(cnt_mine, wave_sum[1]);
+#pragma unroll
+  for (int q = 0; q < kPer; ++q) {
+    loc[t * kPer + q] = lbase;
     lbase += cnt[q];
   }
   __syncthreads();
@@ -218,6 +245,8 @@ __global__ __launch_bounds__(kSortThreads) void radix_scatter_kernel(
 
 struct SortWs {
   uint32_t *counts;
+  uint32_t *base;
+  uint32_t *total;
   void *keys;
   int32_t *vals;
 };
@@ -226,6 +255,8 @@ template <typename K> SortWs carve_sort(Carve &cv, int64_t n) {
   const int64_t m = n < 1 ? 1 : n;
   SortWs w{};
   w.counts = cv.take<uint32_t>(static_cast<size_t>(kMaxDigits) * sort_tiles(m));
+  w.base = cv.take<uint32_t>(static_cast<size_t>(kMaxDigits) * sort_tiles(m));
+  w.total = cv.take<uint32_t>(kMaxDigits);
   w.keys = cv.take<K>(m);
   w.vals = cv.take<int32_t>(m);
   return w;
@@ -264,10 +295,13 @@ void sort_run(void *tmp, size_t tmp_bytes, const K *kin, K *kout, const int32_t 
     hipLaunchKernelGGL((radix_hist_kernel<K>), dim3(tiles), dim3(kSortThreads), 0, s, src_k, n,
                        shift, dmask, w.counts, tiles);
     RHIP_LAUNCH_CHECK();
+    hipLaunchKernelGGL(radix_row_scan_kernel, dim3(dmask + 1), dim3(kWave), 0, s, w.counts, tiles,
+                       w.base, w.total);
+    RHIP_LAUNCH_CHECK();
     auto pass = [&](auto r) {
       constexpr int R = decltype(r)::value;
       hipLaunchKernelGGL((radix_scatter_kernel<K, R>), dim3(grid), dim3(kSortThreads), 0, s,
-                         src_k, src_v, dst_k, dst_v, n, shift, dmask, w.counts, tiles);
+                         src_k, src_v, dst_k, dst_v, n, shift, dmask, w.base, w.total, tiles);
       RHIP_LAUNCH_CHECK();
     };
     if (bits == 8)
