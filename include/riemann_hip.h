@@ -194,7 +194,10 @@ int rhip_kmap_workspace_bytes(int64_t n_in, int64_t n_out, int32_t K,
  *   kmap_offsets   device int64 [K+1], CSR of the pairs per offset, copied
  *                  to kmap_offsets_host;
  *   *flags         RHIP_KMAP_SYMMETRIC or 0 (flags may be NULL).
- * Synchronises `stream` once (to read the pair counts).
+ * Synchronises `stream` once (to read the pair counts) when kmap_offsets_host
+ * is given; with kmap_offsets_host NULL it is asynchronous, and the caller
+ * sizes the pair lists of rhip_kmap_fill by the bound K * n_out (or reads
+ * kmap_offsets itself first).
  * Replaces CoordinateMapGPU::kernel_map / direct_kernel_map / count_kernel
  * (engine/grid/lattice_gpu.cu:1140-1362, 1366-1549); the live reference
  * semantics are CoordinateMapCPU::kernel_map (engine/grid/lattice_cpu.hpp:606-673).

@@ -346,23 +346,24 @@ def kernel_map(in_table: CoordTable, out_table: CoordTable, offsets) -> KernelMa
     ws = torch.empty(_sizeq(L.rhip_kmap_workspace_bytes, n_in, n_out, K), dtype=torch.uint8,
                      device=dev)
     kofs = torch.empty(K + 1, dtype=torch.int64, device=dev)
-    kofs_host = np.zeros(K + 1, dtype=np.int64)
     flags = ctypes.c_int32(0)
     off_host = offsets.numpy()
     _check(L.rhip_kmap_count(ctypes.byref(in_table.struct), _ptr(out_table.ucoords),
                              _ptr(out_table.order), n_out, K,
                              off_host.ctypes.data_as(ctypes.POINTER(ctypes.c_int32)), _ptr(ws),
-                             ws.numel(), _ptr(nbr), _ptr(out_order), _ptr(kofs),
-                             kofs_host.ctypes.data_as(ctypes.POINTER(ctypes.c_int64)),
+                             ws.numel(), _ptr(nbr), _ptr(out_order), _ptr(kofs), None,
                              ctypes.byref(flags), st), "rhip_kmap_count")
-    P = int(kofs_host[-1])
-    in_rows = torch.empty(max(P, 1), dtype=torch.int32, device=dev)
-    out_rows = torch.empty(max(P, 1), dtype=torch.int32, device=dev)
+    # count and fill back to back: pair lists sized by the bound K * n_out,
+    # the pair counts read once after the fill
+    in_rows = torch.empty(max(K * n_out, 1), dtype=torch.int32, device=dev)
+    out_rows = torch.empty(max(K * n_out, 1), dtype=torch.int32, device=dev)
     nbr_t = torch.empty((K, max(n_in, 1)), dtype=torch.int32, device=dev)
     in_order = torch.empty(max(n_in, 1), dtype=torch.int32, device=dev)
     _check(L.rhip_kmap_fill(_ptr(nbr), _ptr(out_order), n_out, K, _ptr(in_table.order), n_in,
                             flags.value, _ptr(ws), ws.numel(), _ptr(kofs), _ptr(in_rows),
                             _ptr(out_rows), _ptr(nbr_t), _ptr(in_order), st), "rhip_kmap_fill")
+    kofs_host = kofs.cpu().numpy()
+    P = int(kofs_host[-1])
     return KernelMap(K, n_in, n_out, kofs, kofs_host, in_rows[:P], out_rows[:P],
                      nbr[:, :n_out], nbr_t[:, :n_in], in_order[:n_in], out_order[:n_out],
                      symmetric=bool(flags.value & KMAP_SYMMETRIC))

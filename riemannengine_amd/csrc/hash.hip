@@ -203,17 +203,14 @@ __global__ __launch_bounds__(kBlock) void insert_kernel(const int32_t *coords,
   }
   const uint64_t mine = rb > 0 ? (key << rb) | static_cast<uint64_t>(r) : key;
   while (true) {
+    // one round trip per probe: the CAS either claims the empty slot or
+    // returns the word already there
     uint64_t *wp = &t.slots[h].word;
-    uint64_t w = __hip_atomic_load(wp, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const uint64_t w = atomicCAS(reinterpret_cast<unsigned long long *>(wp), kEmptyWord, mine);
     if (w == kEmptyWord) {
-      uint64_t prev = atomicCAS(reinterpret_cast<unsigned long long *>(wp),
-                                kEmptyWord, mine);
-      if (prev == kEmptyWord) {
-        if (rb == 0)
-          atomicMin(&t.slots[h].first_row, static_cast<uint32_t>(r));
-        break; // claimed
-      }
-      w = prev;
+      if (rb == 0)
+        atomicMin(&t.slots[h].first_row, static_cast<uint32_t>(r));
+      break; // claimed
     }
     bool same;
     if (rb > 0) {

@@ -464,17 +464,18 @@ HipKernelMap CoordinateManager::generate(const CoordinateMapHIP &in_map,
   auto nbr = torch::empty({K, std::max<int64_t>(n_out, 1)}, iopt);
   auto out_order = torch::empty({std::max<int64_t>(n_out, 1)}, iopt);
   m.offsets = torch::empty({K + 1}, iopt.dtype(torch::kInt64));
-  m.offsets_host.assign(K + 1, 0);
   int32_t flags = 0;
+  // count and fill go back to back: the pair lists are sized by the bound
+  // K * n_out, and the pair counts are read once, after the fill
   check_rhip(rhip_kmap_count(&in_map.table, out_map.coords.data_ptr<int32_t>(),
                              out_map.order.data_ptr<int32_t>(), n_out, K,
                              offsets.data_ptr<int32_t>(), ws.data_ptr(), ws.numel(),
                              nbr.data_ptr<int32_t>(), out_order.data_ptr<int32_t>(),
-                             m.offsets.data_ptr<int64_t>(), m.offsets_host.data(), &flags, st),
+                             m.offsets.data_ptr<int64_t>(), nullptr, &flags, st),
              "rhip_kmap_count");
-  const int64_t P = m.offsets_host[K];
-  auto in_rows = torch::empty({std::max<int64_t>(P, 1)}, iopt);
-  auto out_rows = torch::empty({std::max<int64_t>(P, 1)}, iopt);
+  const int64_t p_bound = static_cast<int64_t>(K) * n_out;
+  auto in_rows = torch::empty({std::max<int64_t>(p_bound, 1)}, iopt);
+  auto out_rows = torch::empty({std::max<int64_t>(p_bound, 1)}, iopt);
   auto nbr_t = torch::empty({K, std::max<int64_t>(n_in, 1)}, iopt);
   auto in_order = torch::empty({std::max<int64_t>(n_in, 1)}, iopt);
   check_rhip(rhip_kmap_fill(nbr.data_ptr<int32_t>(), out_order.data_ptr<int32_t>(), n_out, K,
@@ -483,6 +484,10 @@ HipKernelMap CoordinateManager::generate(const CoordinateMapHIP &in_map,
                             in_rows.data_ptr<int32_t>(), out_rows.data_ptr<int32_t>(),
                             nbr_t.data_ptr<int32_t>(), in_order.data_ptr<int32_t>(), st),
              "rhip_kmap_fill");
+  const auto host_offsets = m.offsets.to(torch::kCPU); // the one synchronisation
+  const int64_t *ho = host_offsets.data_ptr<int64_t>();
+  m.offsets_host.assign(ho, ho + K + 1);
+  const int64_t P = m.offsets_host[K];
   m.in_rows = in_rows.slice(0, 0, P);
   m.out_rows = out_rows.slice(0, 0, P);
   m.nbr = nbr.slice(1, 0, n_out);

@@ -536,8 +536,8 @@ extern "C" int rhip_kmap_count(const rhip_table *in_table, const int32_t *out_co
     RHIP_CHECK_ARG(in_table != nullptr, "in_table is null");
     RHIP_CHECK_ARG(K >= 1 && K <= 65535, "K must be in [1, 65535]");
     RHIP_CHECK_ARG(n_out >= 0 && n_out < INT32_MAX, "bad n_out");
-    RHIP_CHECK_ARG(kmap_offsets && kmap_offsets_host && workspace && offsets_host,
-                   "offsets_host, kmap_offsets, kmap_offsets_host and workspace are required");
+    RHIP_CHECK_ARG(kmap_offsets && workspace && offsets_host,
+                   "offsets_host, kmap_offsets and workspace are required");
     const int D = in_table->ncol - 1;
     Carve cv(workspace, workspace_bytes);
     KmapWs w = carve_kmap(cv, in_table->n_unique, n_out, K, RHIP_MAX_COLS - 1);
@@ -585,9 +585,11 @@ extern "C" int rhip_kmap_count(const rhip_table *in_table, const int32_t *out_co
     hipLaunchKernelGGL(kmap_offsets_kernel, dim3(1), dim3(1024), 0, stream, w.ktotal, K,
                        kmap_offsets, nullptr);
     RHIP_LAUNCH_CHECK();
-    RHIP_HIP(hipMemcpyAsync(kmap_offsets_host, kmap_offsets, sizeof(int64_t) * (K + 1),
-                            hipMemcpyDeviceToHost, stream));
-    RHIP_HIP(hipStreamSynchronize(stream));
+    if (kmap_offsets_host) { // else asynchronous: the caller reads kmap_offsets later
+      RHIP_HIP(hipMemcpyAsync(kmap_offsets_host, kmap_offsets, sizeof(int64_t) * (K + 1),
+                              hipMemcpyDeviceToHost, stream));
+      RHIP_HIP(hipStreamSynchronize(stream));
+    }
   });
 }
 

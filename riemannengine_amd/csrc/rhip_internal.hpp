@@ -267,34 +267,52 @@ __device__ __forceinline__ uint32_t lanes_below(uint64_t mask) {
 
 // Segmented exclusive scan, one 1024-lane workgroup per segment (blockIdx.x):
 // base[s*m + i] = sum(counts[s*m .. s*m+i)), total[s] = sum of segment s.
-// Each lane owns a contiguous run of the segment.
+// The segment goes in chunks of 4096 entries, four consecutive ones per lane
+// (loads issued together), one workgroup scan per chunk and a carry.
 template <typename TIn>
 __global__ __launch_bounds__(1024) void scan_kernel(const TIn *counts, int64_t m,
                                                     int64_t *base, int64_t *total) {
-  __shared__ int64_t partial[1024];
-  const int t = threadIdx.x;
+  constexpr int kWaves = 1024 / kWave;
+  __shared__ int64_t wave_sum[kWaves];
+  const int t = threadIdx.x, lane = t & (kWave - 1), w = t / kWave;
   const int64_t seg = static_cast<int64_t>(blockIdx.x) * m;
-  const int64_t per = (m + 1023) / 1024;
-  const int64_t b = t * per, e = min(m, b + per);
-  int64_t s = 0;
-  for (int64_t i = b; i < e; ++i)
-    s += counts[seg + i];
-  partial[t] = s;
-  __syncthreads();
-  // Hillis-Steele inclusive scan over the 1024 partial sums.
-  for (int off = 1; off < 1024; off <<= 1) {
-    int64_t v = t >= off ? partial[t - off] : 0;
+  int64_t carry = 0;
+  for (int64_t c0 = 0; c0 < m; c0 += 4 * 1024) {
+    const int64_t e0 = c0 + 4 * t;
+    int64_t v[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      v[i] = e0 + i < m ? static_cast<int64_t>(counts[seg + e0 + i]) : 0;
+    const int64_t sum = v[0] + v[1] + v[2] + v[3];
+    int64_t incl = sum;
+#pragma unroll
+    for (int off = 1; off < kWave; off <<= 1) {
+      const int64_t o = __shfl_up(incl, off, kWave);
+      if (lane >= off)
+        incl += o;
+    }
+    if (lane == kWave - 1)
+      wave_sum[w] = incl;
     __syncthreads();
-    partial[t] += v;
-    __syncthreads();
+    int64_t before = carry, chunk = 0;
+#pragma unroll
+    for (int i = 0; i < kWaves; ++i) {
+      const int64_t ws = wave_sum[i];
+      before += i < w ? ws : 0;
+      chunk += ws;
+    }
+    int64_t run = before + incl - sum;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if (e0 + i < m)
+        base[seg + e0 + i] = run;
+      run += v[i];
+    }
+    carry += chunk;
+    __syncthreads(); // wave_sum is rewritten by the next chunk
   }
-  int64_t run = partial[t] - s;
-  for (int64_t i = b; i < e; ++i) {
-    base[seg + i] = run;
-    run += counts[seg + i];
-  }
-  if (t == 1023)
-    total[blockIdx.x] = partial[1023];
+  if (t == 0)
+    total[blockIdx.x] = carry;
 }
 
 } // namespace rhip
