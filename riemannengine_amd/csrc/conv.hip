@@ -148,16 +148,20 @@ __device__ __forceinline__ v4u quad_to_mfma(const v4u &v, int src) {
 // ------------------------------------------------ output-stationary GEMM
 //
 // y[order[j]][col] = sum_k sum_c x[nbr[k][j]][c] * wt[k][col][c] (+ bias[col])
-// wt is [K][ncols][cred] (reduction axis contiguous). A workgroup owns
+// wt is [K][ncols][credw] (reduction axis contiguous; credw >= cred, the
+// rows past cred zero: a bf16 reduction of 16 channels is padded to the
+// 32 of one MFMA, PADC, and lanes whose channels lie past cred read
+// nothing and contribute zeros). A workgroup owns
 // 4 * RG * 16 output rows and NT columns; RG: 16-row groups per wave; CSUB:
 // 16-byte lane loads per staged channel chunk (chunk = CSUB * kCh channels).
 // A stage is one (active offset, channel chunk); G stages go at once: their
 // neighbour indices, then their weight chunks (to G LDS slots) and gathered
 // rows (to registers) are all in flight together, so a group costs about
 // two memory latencies and two barriers however many stages it holds.
-template <typename T, int NT, int RG, int CSUB, int G, int WAVES = 1, bool COAL = true>
+template <typename T, int NT, int RG, int CSUB, int G, int WAVES = 1, bool COAL = true,
+          bool PADC = false>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(WAVES))) void conv_os_kernel(
-    const T *__restrict__ x, int cred, const T *__restrict__ wt, int ncols,
+    const T *__restrict__ x, int cred, const T *__restrict__ wt, int credw, int ncols,
     const float *__restrict__ bias, const int32_t *__restrict__ nbr,
     int64_t n_rows, int K, const int32_t *__restrict__ order,
     T *__restrict__ y, float *__restrict__ partial) {
@@ -257,7 +261,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(WAVES)
     scount = c;
   }
   __syncthreads();
-  const int nch = cred / CCH;
+  const int nch = credw / CCH;
   // stages: (active offset, channel chunk); split z of gridDim.z takes an
   // equal share of them and writes fp32 partial sums
   const int S = scount * nch;
@@ -317,7 +321,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(WAVES)
       for (int i = 0; i < NPT; ++i) {
         const int li = min(static_cast<int>(threadIdx.x) + i * kThreads, NV - 1);
         wreg[j][i] = *reinterpret_cast<const uint4 *>(
-            wt + (static_cast<int64_t>(kj[j]) * ncols + col0 + li / (CCH / VE)) * cred +
+            wt + (static_cast<int64_t>(kj[j]) * ncols + col0 + li / (CCH / VE)) * credw +
             ccj[j] + (li % (CCH / VE)) * VE);
       }
     Frag a[G][RG][CSUB];
@@ -327,9 +331,11 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(WAVES)
       for (int r = 0; r < RG; ++r)
 #pragma unroll
         for (int sub = 0; sub < CSUB; ++sub) {
+          const int ch = ccj[j] + sub * CH + (COAL ? (lane & 3) : g) * EPL;
+          const bool cok = !PADC || ch < cred; // a padded lane reads channel 0, zeroed
           const Frag v = M::load(x + static_cast<int64_t>(idx[j][r] < 0 ? 0 : idx[j][r]) * cred +
-                                 ccj[j] + sub * CH + (COAL ? (lane & 3) : g) * EPL);
-          a[j][r][sub] = M::mask(v, idx[j][r] >= 0);
+                                 (cok ? ch : 0));
+          a[j][r][sub] = M::mask(v, idx[j][r] >= 0 && cok);
         }
 #pragma unroll
     for (int j = 0; j < G; ++j)
@@ -408,7 +414,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(WAVES)
 // Any-shape fallback of conv_os_kernel: one lane per output element.
 template <typename T>
 __global__ __launch_bounds__(kThreads) void conv_os_generic_kernel(
-    const T *__restrict__ x, int cred, const T *__restrict__ wt, int ncols,
+    const T *__restrict__ x, int cred, const T *__restrict__ wt, int credw, int ncols,
     const float *__restrict__ bias, const int32_t *__restrict__ nbr,
     int64_t n_rows, int K, const int32_t *__restrict__ order,
     T *__restrict__ y) {
@@ -423,7 +429,7 @@ __global__ __launch_bounds__(kThreads) void conv_os_generic_kernel(
     if (s < 0)
       continue;
     const T *xr = x + static_cast<int64_t>(s) * cred;
-    const T *wr = wt + (static_cast<int64_t>(k) * ncols + col) * cred;
+    const T *wr = wt + (static_cast<int64_t>(k) * ncols + col) * credw;
     for (int c = 0; c < cred; ++c)
       acc += to_f32(xr[c]) * to_f32(wr[c]);
   }
@@ -683,18 +689,39 @@ __global__ __launch_bounds__(kThreads) void conv_os_reduce_kernel(
   dst[3] = from_f32<T>(a.w);
 }
 
-// wt[k][n][c] = w[k][c][n] (weights [K, cin, cout] -> [K, cout, cin]).
+// wt[k][n][c] = w[k][c][n] (weights [K, cin, cout] -> [K, cout, credw]),
+// zero for cin <= c < credw.
 template <typename T>
 __global__ __launch_bounds__(kThreads) void transpose_w_kernel(const T *__restrict__ w, int K,
-                                                               int cin, int cout,
+                                                               int cin, int cout, int credw,
                                                                T *__restrict__ wt) {
   const int64_t i = blockIdx.x * static_cast<int64_t>(kThreads) + threadIdx.x;
-  const int64_t per = static_cast<int64_t>(cin) * cout;
+  const int64_t per = static_cast<int64_t>(cout) * credw;
   if (i >= K * per)
     return;
   const int64_t k = i / per, rem = i % per;
-  const int c = static_cast<int>(rem / cout), n = static_cast<int>(rem % cout);
-  wt[(k * cout + n) * cin + c] = w[i];
+  const int n = static_cast<int>(rem / credw), c = static_cast<int>(rem % credw);
+  wt[i] = c < cin ? w[(k * cin + c) * cout + n] : from_f32<T>(0.f);
+}
+
+// dst[r][c] = src[r][c] for c < cols, zero up to credw (rows of cols -> credw).
+template <typename T>
+__global__ __launch_bounds__(kThreads) void pad_rows_kernel(const T *__restrict__ src,
+                                                            int64_t rows, int cols, int credw,
+                                                            T *__restrict__ dst) {
+  const int64_t i = blockIdx.x * static_cast<int64_t>(kThreads) + threadIdx.x;
+  if (i >= rows * credw)
+    return;
+  const int64_t r = i / credw;
+  const int c = static_cast<int>(i % credw);
+  dst[i] = c < cols ? src[r * cols + c] : from_f32<T>(0.f);
+}
+
+// Reduction width the MFMA forward / input-gradient kernels read the weights
+// at: a bf16 reduction of an odd multiple of 16 channels is padded to the
+// next multiple of 32 (one 16x16x32 MFMA); everything else as it is.
+static int red_width(int32_t dtype, int c) {
+  return dtype == RHIP_BF16 && c % 32 == 16 ? c + 16 : c;
 }
 
 // ------------------------------------------------------------------- dW
@@ -1689,17 +1716,28 @@ static bool aligned16(const void *p) {
 }
 
 template <typename T> constexpr int kChOf = Mfma<T>::kCh;
+template <typename T> constexpr bool kIsF32 = std::is_same<T, float>::value;
 
 template <typename T, int NT, int RG, int CSUB, int WAVES, int G>
-static void launch_os(const T *x, int cred, const T *wt, int ncols,
+static void launch_os(const T *x, int cred, const T *wt, int credw, int ncols,
                       const float *bias, const int32_t *nbr, int64_t n_rows,
                       int K, const int32_t *order, T *y, int splits, float *partial,
                       hipStream_t s) {
   constexpr int ROWS = kWaves * RG * 16;
   dim3 grid(static_cast<unsigned>(xcd_grid(ceil_div(n_rows, ROWS))), ncols / NT, splits);
-  hipLaunchKernelGGL((conv_os_kernel<T, NT, RG, CSUB, G, WAVES>), grid, dim3(kThreads), 0, s, x,
-                     cred, wt, ncols, bias, nbr, n_rows, K, order, y,
-                     splits > 1 ? partial : nullptr);
+  float *part = splits > 1 ? partial : nullptr;
+  bool padded = false;
+  if constexpr (!kIsF32<T> && CSUB == 1) {
+    if (credw != cred) { // bf16 reduction padded to the MFMA width
+      hipLaunchKernelGGL((conv_os_kernel<T, NT, RG, CSUB, G, WAVES, true, true>), grid,
+                         dim3(kThreads), 0, s, x, cred, wt, credw, ncols, bias, nbr, n_rows, K,
+                         order, y, part);
+      padded = true;
+    }
+  }
+  if (!padded)
+    hipLaunchKernelGGL((conv_os_kernel<T, NT, RG, CSUB, G, WAVES>), grid, dim3(kThreads), 0, s,
+                       x, cred, wt, credw, ncols, bias, nbr, n_rows, K, order, y, part);
   if (splits > 1) {
     RHIP_LAUNCH_CHECK();
     hipLaunchKernelGGL((conv_os_reduce_kernel<T>),
@@ -1717,8 +1755,6 @@ static void launch_os(const T *x, int cred, const T *wt, int ncols,
 // per barrier at 64 columns; 128-column tiles (4 waves per SIMD, 2 stages
 // per barrier) for 128 and 256 channels; 4 stages per barrier for 32-channel
 // chunks (6 waves per SIMD at 64 columns, where 8 do not fit the registers).
-template <typename T> constexpr bool kIsF32 = std::is_same<T, float>::value;
-
 template <typename T> static int os_nt(int ncols) {
   if (!kIsF32<T> && ncols % 128 == 0)
     return 128;
@@ -1726,7 +1762,7 @@ template <typename T> static int os_nt(int ncols) {
 }
 
 template <typename T, int NT, int CSUB>
-static void launch_shape(const T *x, int cred, const T *wt, int ncols, const float *bias,
+static void launch_shape(const T *x, int cred, const T *wt, int credw, int ncols, const float *bias,
                          const int32_t *nbr, int64_t n_rows, int K, const int32_t *order, T *y,
                          int splits, float *partial, hipStream_t s) {
   // bf16 at 64 columns and 64 reduction channels: two row groups per wave
@@ -1736,36 +1772,38 @@ static void launch_shape(const T *x, int cred, const T *wt, int ncols, const flo
   constexpr int W = kIsF32<T> ? (NT == 64 ? 6 : 8)
                               : (NT >= 128 || RG == 2 ? 4 : (CSUB == 1 && NT >= 64 ? 6 : 8));
   constexpr int G = kIsF32<T> ? 1 : (NT >= 128 || RG == 2 ? 2 : (CSUB == 1 ? 4 : 1));
-  launch_os<T, NT, RG, CSUB, W, G>(x, cred, wt, ncols, bias, nbr, n_rows, K, order, y, splits,
-                                   partial, s);
+  launch_os<T, NT, RG, CSUB, W, G>(x, cred, wt, credw, ncols, bias, nbr, n_rows, K, order, y,
+                                   splits, partial, s);
 }
 
 template <typename T, int NT>
-static void pick_csub(const T *x, int cred, const T *wt, int ncols,
+static void pick_csub(const T *x, int cred, const T *wt, int credw, int ncols,
                       const float *bias, const int32_t *nbr, int64_t n_rows,
                       int K, const int32_t *order, T *y, int splits, float *partial,
                       hipStream_t s) {
   constexpr int CH = kChOf<T>;
   if constexpr (kIsF32<T>) {
     if (cred % (4 * CH) == 0) {
-      launch_shape<T, NT, 4>(x, cred, wt, ncols, bias, nbr, n_rows, K, order, y, splits, partial,
-                             s);
+      launch_shape<T, NT, 4>(x, cred, wt, credw, ncols, bias, nbr, n_rows, K, order, y, splits,
+                             partial, s);
       return;
     }
   }
-  if (cred % (2 * CH) == 0)
-    launch_shape<T, NT, 2>(x, cred, wt, ncols, bias, nbr, n_rows, K, order, y, splits, partial,
-                           s);
+  if (cred == credw && cred % (2 * CH) == 0)
+    launch_shape<T, NT, 2>(x, cred, wt, credw, ncols, bias, nbr, n_rows, K, order, y, splits,
+                           partial, s);
   else
-    launch_shape<T, NT, 1>(x, cred, wt, ncols, bias, nbr, n_rows, K, order, y, splits, partial,
-                           s);
+    launch_shape<T, NT, 1>(x, cred, wt, credw, ncols, bias, nbr, n_rows, K, order, y, splits,
+                           partial, s);
 }
 
-// Whether run_os takes the MFMA kernel for these operands.
+// Whether run_os takes the MFMA kernel for these operands (a padded bf16
+// reduction needs 16-byte aligned rows of 16 channels at least).
 template <typename T>
-static bool os_fast(const T *x, int cred, const T *wt, int ncols, int K) {
-  return cred % kChOf<T> == 0 && ncols % 16 == 0 && K <= 32 * kMaskWords && aligned16(x) &&
-         aligned16(wt);
+static bool os_fast(const T *x, int cred, const T *wt, int credw, int ncols, int K) {
+  const bool red = cred == credw ? cred % kChOf<T> == 0
+                                 : (!kIsF32<T> && credw == cred + 16 && credw % kChOf<T> == 0);
+  return red && ncols % 16 == 0 && K <= 32 * kMaskWords && aligned16(x) && aligned16(wt);
 }
 
 // Splits of the offset axis for the MFMA kernel: a map with few rows and
@@ -1894,31 +1932,37 @@ static bool run_fr(const __bf16 *x, int64_t n_x, int cred, const __bf16 *wt, int
 // y[order[j]] = sum_k x[nbr[k][j]] @ W'[k] with W'[k][c][n] = wt[k][n][c];
 // x has n_x rows. partial: os_partial_floats(...) floats, or null to run
 // without a split.
+// credw: row stride of wt (cred, or the padded reduction of red_width).
 template <typename T>
-static void run_os(const T *x, int64_t n_x, int cred, const T *wt, int ncols,
+static void run_os(const T *x, int64_t n_x, int cred, const T *wt, int credw, int ncols,
                    const float *bias, const int32_t *nbr, int64_t n_rows, int K,
                    const int32_t *order, T *y, float *partial, hipStream_t s,
                    bool resident = true) {
   if (n_rows == 0)
     return;
   if constexpr (!kIsF32<T>) {
-    if (resident && run_fr(x, n_x, cred, wt, ncols, bias, nbr, n_rows, K, order, y, s))
+    if (resident && cred == credw &&
+        run_fr(x, n_x, cred, wt, ncols, bias, nbr, n_rows, K, order, y, s))
       return;
   }
-  const int splits = partial ? os_splits<T>(n_rows, cred, ncols, K) : 1;
-  if (!os_fast(x, cred, wt, ncols, K)) {
+  const int splits = partial ? os_splits<T>(n_rows, credw, ncols, K) : 1;
+  if (!os_fast(x, cred, wt, credw, ncols, K)) {
     hipLaunchKernelGGL((conv_os_generic_kernel<T>), dim3(ceil_div(n_rows * ncols, kThreads)),
-                       dim3(kThreads), 0, s, x, cred, wt, ncols, bias, nbr, n_rows, K,
+                       dim3(kThreads), 0, s, x, cred, wt, credw, ncols, bias, nbr, n_rows, K,
                        order, y);
   } else if (os_nt<T>(ncols) == 128) {
     if constexpr (!kIsF32<T>)
-      pick_csub<T, 128>(x, cred, wt, ncols, bias, nbr, n_rows, K, order, y, splits, partial, s);
+      pick_csub<T, 128>(x, cred, wt, credw, ncols, bias, nbr, n_rows, K, order, y, splits,
+                        partial, s);
   } else if (ncols % 64 == 0) {
-    pick_csub<T, 64>(x, cred, wt, ncols, bias, nbr, n_rows, K, order, y, splits, partial, s);
+    pick_csub<T, 64>(x, cred, wt, credw, ncols, bias, nbr, n_rows, K, order, y, splits, partial,
+                     s);
   } else if (ncols % 32 == 0) {
-    pick_csub<T, 32>(x, cred, wt, ncols, bias, nbr, n_rows, K, order, y, splits, partial, s);
+    pick_csub<T, 32>(x, cred, wt, credw, ncols, bias, nbr, n_rows, K, order, y, splits, partial,
+                     s);
   } else {
-    pick_csub<T, 16>(x, cred, wt, ncols, bias, nbr, n_rows, K, order, y, splits, partial, s);
+    pick_csub<T, 16>(x, cred, wt, credw, ncols, bias, nbr, n_rows, K, order, y, splits, partial,
+                     s);
   }
   RHIP_LAUNCH_CHECK();
 }
@@ -2270,7 +2314,10 @@ struct ConvWs {
 static ConvWs carve_conv_front(Carve &cv, int32_t K, int32_t cin, int32_t cout, int32_t dtype,
                                int64_t n_in, int64_t n_out) {
   ConvWs w;
-  const size_t nw = static_cast<size_t>(K) * cin * cout;
+  // transposed forward weights, or the padded copy of dX's
+  const size_t nw = static_cast<size_t>(K) *
+                    std::max(static_cast<size_t>(cout) * red_width(dtype, cin),
+                             static_cast<size_t>(cin) * red_width(dtype, cout));
   w.wt = cv.take<char>(nw * (dtype == RHIP_F32 ? 4 : 2));
   const bool f32 = dtype == RHIP_F32;
   auto osp = [&](int64_t n, int cred, int ncols) {
@@ -2297,24 +2344,25 @@ static void conv_forward_into(const void *x, int64_t n_in, int32_t cin, const vo
                               int32_t K, int32_t cout, const float *bias, const int32_t *nbr,
                               const int32_t *out_order, int64_t n_out, void *y, int32_t dtype,
                               void *wt, float *os_partial, hipStream_t stream) {
-  const int64_t nw = static_cast<int64_t>(K) * cin * cout;
-  // the MFMA path reads W[k] column-wise: stage the [K, cout, cin] copy
+  // the MFMA path reads W[k] column-wise: stage the [K, cout, credw] copy
+  const int credw = red_width(dtype, cin);
+  const int64_t nw = static_cast<int64_t>(K) * cout * credw;
   if (dtype == RHIP_F32) {
     float *w = static_cast<float *>(wt);
     hipLaunchKernelGGL((transpose_w_kernel<float>), dim3(ceil_div(nw, kThreads)),
                        dim3(kThreads), 0, stream, static_cast<const float *>(weight), K, cin,
-                       cout, w);
+                       cout, credw, w);
     RHIP_LAUNCH_CHECK();
-    run_os<float>(static_cast<const float *>(x), n_in, cin, w, cout, bias, nbr, n_out, K,
+    run_os<float>(static_cast<const float *>(x), n_in, cin, w, credw, cout, bias, nbr, n_out, K,
                   out_order, static_cast<float *>(y), os_partial, stream);
   } else {
     __bf16 *w = static_cast<__bf16 *>(wt);
     hipLaunchKernelGGL((transpose_w_kernel<__bf16>), dim3(ceil_div(nw, kThreads)),
                        dim3(kThreads), 0, stream, static_cast<const __bf16 *>(weight), K, cin,
-                       cout, w);
+                       cout, credw, w);
     RHIP_LAUNCH_CHECK();
-    run_os<__bf16>(static_cast<const __bf16 *>(x), n_in, cin, w, cout, bias, nbr, n_out, K,
-                   out_order, static_cast<__bf16 *>(y), os_partial, stream);
+    run_os<__bf16>(static_cast<const __bf16 *>(x), n_in, cin, w, credw, cout, bias, nbr, n_out,
+                   K, out_order, static_cast<__bf16 *>(y), os_partial, stream);
   }
 }
 
@@ -2409,8 +2457,8 @@ extern "C" int rhip_conv_forward_noalloc(const void *x, int64_t n_in, int32_t ci
     check_dtype(dtype);
     RHIP_CHECK_ARG(K >= 1 && cin >= 1 && cout >= 1, "sizes must be positive");
     RHIP_CHECK_ARG(n_in >= 0 && n_out >= 0, "row counts must be >= 0");
-    const size_t wt_bytes =
-        static_cast<size_t>(K) * cin * cout * (dtype == RHIP_F32 ? 4 : 2);
+    const size_t wt_bytes = static_cast<size_t>(K) * cout * red_width(dtype, cin) *
+                            (dtype == RHIP_F32 ? 4 : 2);
     if (wt_bytes > kConvScratchBytes)
       throw Error(RHIP_ERR_UNSUPPORTED,
                   "rhip_conv_forward_noalloc: the weights need " + std::to_string(wt_bytes) +
@@ -2471,20 +2519,34 @@ extern "C" int rhip_conv_backward_input(const void *grad_y, int64_t n_out,
       return;
     RHIP_CHECK_ARG(grad_x && weight && nbr_t, "grad_x, weight and nbr_t are required");
     RHIP_CHECK_ARG(n_out == 0 || grad_y != nullptr, "grad_y is null");
-    // without a workspace the offset axis is not split
+    // without a workspace the offset axis is not split, and a reduction the
+    // MFMA kernels would pad goes to the one-lane-per-output kernel
     float *os_partial = nullptr;
+    const void *wk = weight;
+    int credw = cout;
     if (workspace != nullptr) {
       Carve cv(workspace, workspace_bytes);
-      os_partial = carve_conv_front(cv, K, cin, cout, dtype, n_in, n_out).os_partial;
+      const ConvWs w = carve_conv_front(cv, K, cin, cout, dtype, n_in, n_out);
+      os_partial = w.os_partial;
+      if (red_width(dtype, cout) != cout) { // [K][cin][cout] rows padded to credw
+        credw = red_width(dtype, cout);
+        const int64_t ne = static_cast<int64_t>(K) * cin * credw;
+        hipLaunchKernelGGL((pad_rows_kernel<__bf16>), dim3(ceil_div(ne, kThreads)),
+                           dim3(kThreads), 0, stream, static_cast<const __bf16 *>(weight),
+                           static_cast<int64_t>(K) * cin, cout, credw,
+                           static_cast<__bf16 *>(w.wt));
+        RHIP_LAUNCH_CHECK();
+        wk = w.wt;
+      }
     }
     // dX rows gather dY rows; W[k] [cin][cout] is already [n = cin][c = cout].
     if (dtype == RHIP_F32)
       run_os<float>(static_cast<const float *>(grad_y), n_out, cout,
-                    static_cast<const float *>(weight), cin, nullptr, nbr_t, n_in, K,
+                    static_cast<const float *>(wk), credw, cin, nullptr, nbr_t, n_in, K,
                     in_order, static_cast<float *>(grad_x), os_partial, stream);
     else
       run_os<__bf16>(static_cast<const __bf16 *>(grad_y), n_out, cout,
-                     static_cast<const __bf16 *>(weight), cin, nullptr, nbr_t, n_in, K,
+                     static_cast<const __bf16 *>(wk), credw, cin, nullptr, nbr_t, n_in, K,
                      in_order, static_cast<__bf16 *>(grad_x), os_partial, stream);
   });
 }

@@ -53,7 +53,9 @@ def _run_and_check(km, cin, cout, dtype, seed, bias=False, tag=""):
     (16, 32, torch.float32), (64, 64, torch.float32), (32, 48, torch.float32),
     (128, 64, torch.float32), (64, 256, torch.float32), (3, 5, torch.float32),
     (64, 64, torch.bfloat16), (32, 64, torch.bfloat16), (128, 128, torch.bfloat16),
-    (256, 32, torch.bfloat16), (16, 16, torch.bfloat16), (8, 24, torch.bfloat16)])
+    (256, 32, torch.bfloat16), (16, 16, torch.bfloat16), (8, 24, torch.bfloat16),
+    # bf16 reductions of 16 / 48 channels: padded to the 32-channel MFMA
+    (16, 32, torch.bfloat16), (48, 16, torch.bfloat16), (16, 48, torch.bfloat16)])
 def test_conv_3x3x3_matches_oracle(cin, cout, dtype):
     rng = np.random.default_rng(cin + cout)
     c, _, _ = oracle.insert_and_map(random_coords(rng, 6000, 3, 12))
@@ -370,6 +372,26 @@ def test_config1_sphere_shell_full():
     assert_rel(y.cpu().numpy(), ry, 1e-4, "Y")
     assert_rel(gx.cpu().numpy(), rgx, 1e-4, "dX")
     assert_rel(gw.cpu().numpy(), rgw, 1e-4, "dW")
+
+
+def test_config1_sphere_shell_bf16_vs_torch():
+    """Config 1 in bf16 (C16->32: the forward's 16-channel reduction runs on
+    the MFMA kernel padded to 32 channels) against the PyTorch fp32
+    gather-matmul-scatter on the same bf16 operands, norm-wise 2e-2."""
+    c = scenes.sphere_shell()
+    _, _, km = gpu_tables_and_map(c, c, oracle.region_offsets(3, 3), same=True)
+    x = to_dev(scenes.features(len(c), 16, seed=1, dist="uniform"), torch.bfloat16)
+    w = to_dev(scenes.kaiming_weight(27, 16, 32, seed=2), torch.bfloat16)
+    gy = to_dev(scenes.features(len(c), 32, seed=3), torch.bfloat16)
+    print(f"config 1 bf16 n={km.n_out} P={km.n_pairs}", flush=True)
+    y = abi.conv_forward(x, w, km)
+    gx = abi.conv_backward_input(gy, w, km)
+    gw = abi.conv_weight_grad(x, gy, km, 27)
+    ry, rgx, rgw = _torch_gather_gemm_scatter(km, x, w, gy)
+    tol = TOL[torch.bfloat16]
+    assert_rel(y.float().cpu().numpy(), ry.cpu().numpy(), tol, "Y")
+    assert_rel(gx.float().cpu().numpy(), rgx.cpu().numpy(), tol, "dX")
+    assert_rel(gw.float().cpu().numpy(), rgw.cpu().numpy(), tol, "dW")
 
 
 def _torch_gather_gemm_scatter(km, x, w, gy):
