@@ -276,3 +276,36 @@ def test_row_reference_kernel_map(same):
     _, ref = _ref_map(c, cout, off)
     np.testing.assert_array_equal(gpu_canonical(km), ref)
     assert km.n_pairs > len(cout)  # neighbours were found
+
+
+def test_kmap_count_with_host_readback_matches_async():
+    """rhip_kmap_count with a host array for the pair counts (the call reads
+    them back and synchronises) gives the same CSR, neighbour table and order
+    as the asynchronous form that abi.kernel_map uses (no host array, CSR
+    read after the fill)."""
+    import ctypes
+    rng = np.random.default_rng(21)
+    c, _, _ = oracle.insert_and_map(random_coords(rng, 5000, 3, 11))
+    off = oracle.region_offsets(3, 3)
+    t, _, km = gpu_tables_and_map(c, c, off, same=True)
+    L = abi.lib()
+    K, n = off.shape[0], t.n
+    nbr = torch.empty((K, n), dtype=torch.int32, device=DEV)
+    order = torch.empty(n, dtype=torch.int32, device=DEV)
+    ws = torch.empty(abi._sizeq(L.rhip_kmap_workspace_bytes, n, n, K), dtype=torch.uint8,
+                     device=DEV)
+    kofs = torch.empty(K + 1, dtype=torch.int64, device=DEV)
+    kofs_host = np.full(K + 1, -7, dtype=np.int64)
+    flags = ctypes.c_int32(0)
+    off32 = np.ascontiguousarray(off, dtype=np.int32)
+    rc = L.rhip_kmap_count(ctypes.byref(t.struct), abi._ptr(t.ucoords), abi._ptr(t.order), n, K,
+                           off32.ctypes.data_as(ctypes.POINTER(ctypes.c_int32)), abi._ptr(ws),
+                           ws.numel(), abi._ptr(nbr), abi._ptr(order), abi._ptr(kofs),
+                           kofs_host.ctypes.data_as(ctypes.POINTER(ctypes.c_int64)),
+                           ctypes.byref(flags), abi._stream(torch.device(DEV)))
+    assert rc == 0, abi.lib().rhip_last_error()
+    # the host array is filled before the call returns
+    np.testing.assert_array_equal(kofs_host, km.offsets_host)
+    np.testing.assert_array_equal(kofs.cpu().numpy(), km.offsets_host)
+    assert torch.equal(nbr, km.nbr) and torch.equal(order, km.out_order)
+    assert bool(flags.value & abi.KMAP_SYMMETRIC) == km.symmetric
