@@ -109,17 +109,19 @@ def conv_traffic(n_in, n_out, P, K, cin, cout, s):
     }
 
 
-def measured_traffic(dtype: str, pass_name: str, record: str = "traffic_config2.json"):
+def measured_traffic(dtype: str, pass_name, record: str = "traffic_config2.json"):
     """(HBM bytes per launch of a pass's kernels, source) from the committed
     rocprofv3 FETCH_SIZE / WRITE_SIZE passes (profiles/traffic_config2.json for
     the convolution, traffic_pool.json for pooling), scaled by the counters'
-    reading for a device copy of known size. The source names the record and
-    the commit of the kernels it was taken on; (None, None) if absent."""
+    reading for a device copy of known size; pass_name None reads a record of
+    its own, such as the kernel-map build's ("kernel_map"). The source names
+    the record and the commit of the kernels it was taken on; (None, None) if
+    absent."""
     path = os.path.join(ROOT, "profiles", record)
     try:
         with open(path) as f:
             doc = json.load(f)
-        rec = doc[dtype][pass_name]
+        rec = doc[dtype] if pass_name is None else doc[dtype][pass_name]
     except (OSError, KeyError, ValueError):
         return None, None
     src = f"profiles/{record}"
@@ -610,12 +612,14 @@ def main():
     b_hash = len(coords_np) * (D + 1) * 4 + len(coords_np) * 8 + len(coords_np) * 4
     b_map = (n_in + n_out) * (D + 1) * 4 + K * n_out * 8 + 8 * P + 4 * (K + 1)
     map_gbs = (b_hash + b_map) / (kmap_ms * 1e-3) / 1e9
+    map_traffic = measured_traffic("kernel_map", None)
     kmap_roof = {"bound": "hbm", "achieved": round(map_gbs, 1), "peak": PEAK_HBM_GBS,
                  "unit": "GB/s", "frac": round(map_gbs / PEAK_HBM_GBS, 4),
                  "algorithmic": {"hash_bytes": b_hash, "map_bytes": b_map},
                  "ms": round(kmap_ms, 3),
                  "path": "C++ CoordinateManager.insert_and_map + kernel_map",
                  "c_abi_from_python_ms": round(abi_map_ms, 3),
+                 "traffic": map_traffic[0], "traffic_source": map_traffic[1],
                  "note": "host clock around the build calls, which read sizes back to the host"}
 
     dtypes = [args.dtype] if args.dtype_given else ["f32", "bf16"]
