@@ -31,6 +31,8 @@ Printed as ONE JSON line:
 from __future__ import annotations
 
 import argparse
+import contextlib
+import gc
 import json
 import os
 import platform
@@ -223,6 +225,19 @@ def cpu_map_baseline(coords):
     }
 
 
+@contextlib.contextmanager
+def _no_gc():
+    """Timed regions run with Python's cyclic collector off (collected just
+    before): a full collection stalls the launching thread for tens of ms,
+    which the GPU sees as idle time inside whichever pass it lands in."""
+    gc.collect()
+    gc.disable()
+    try:
+        yield
+    finally:
+        gc.enable()
+
+
 def _timed_passes(passes, steps, warmup):
     """Run the named passes in order `warmup` times, then `steps` times with
     HIP events between passes (torch's current stream, where the C ABI and
@@ -234,14 +249,15 @@ def _timed_passes(passes, steps, warmup):
     torch.cuda.synchronize()
     ev = [[torch.cuda.Event(enable_timing=True) for _ in range(len(passes) + 1)]
           for _ in range(steps)]
-    t0 = time.perf_counter()
-    for i in range(steps):
-        ev[i][0].record()
-        for j, (_, fn) in enumerate(passes):
-            fn()
-            ev[i][j + 1].record()
-    torch.cuda.synchronize()
-    wall = (time.perf_counter() - t0) * 1e3 / steps
+    with _no_gc():
+        t0 = time.perf_counter()
+        for i in range(steps):
+            ev[i][0].record()
+            for j, (_, fn) in enumerate(passes):
+                fn()
+                ev[i][j + 1].record()
+        torch.cuda.synchronize()
+        wall = (time.perf_counter() - t0) * 1e3 / steps
     per = {name: statistics.mean(e[j].elapsed_time(e[j + 1]) for e in ev)
            for j, (name, _) in enumerate(passes)}
     return per, wall
@@ -251,12 +267,13 @@ def _map_time(build, reps):
     """Host-clock median of `build()` (hash + map calls read sizes back)."""
     import torch
     out, ms = None, []
-    for _ in range(reps + 1):
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        out = build()
-        torch.cuda.synchronize()
-        ms.append((time.perf_counter() - t0) * 1e3)
+    with _no_gc():
+        for _ in range(reps + 1):
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            out = build()
+            torch.cuda.synchronize()
+            ms.append((time.perf_counter() - t0) * 1e3)
     return out, statistics.median(ms[1:])
 
 
@@ -694,11 +711,12 @@ def conv_step_record(args, dtype, km, n_in, n_out, P, K, cin, cout):
 
     events = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(args.steps)]
     torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for i in range(args.steps):
-        step(events[i])
-    torch.cuda.synchronize()
-    total_s = time.perf_counter() - t0
+    with _no_gc():
+        t0 = time.perf_counter()
+        for i in range(args.steps):
+            step(events[i])
+        torch.cuda.synchronize()
+        total_s = time.perf_counter() - t0
     ms_per_step = total_s * 1e3 / args.steps
 
     names = ["forward", "backward_input", "backward_weight"]

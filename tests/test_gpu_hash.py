@@ -100,6 +100,96 @@ def test_spatial_order_is_morton_permutation(stride):
     assert t.struct.bricks is not None and t.struct.morton_bits > 0
 
 
+def _brick_walk(rows):
+    """(grid entries, Morton indices of the grid walk, entry limit) of a set
+    of unique rows: bricks of 2^(6 // D) cells per column over the shifted
+    offsets, each column's brick extent rounded up to a power of two in the
+    walk, batches on top."""
+    rows = rows.astype(np.int64)
+    D = rows.shape[1] - 1
+    rel = rows - rows.min(axis=0)
+    L, entries, walk = 6 // D, int(rel[:, 0].max()) + 1, int(rel[:, 0].max()) + 1
+    for j in range(1, D + 1):
+        o = int(np.bitwise_or.reduce(rel[:, j]))
+        tz = (o & -o).bit_length() - 1 if o else 0
+        dim = (int(rel[:, j].max()) >> tz >> L) + 1
+        entries *= dim
+        walk *= 1 << (dim - 1).bit_length()
+    return entries, walk, min(1 << 23, max(4096, 16 * len(rows)))
+
+
+def _spatial_order(t, with_bricks):
+    """rhip_spatial_order once more on a built table (a copy of its struct),
+    with or without brick storage: (struct, order, pos)."""
+    import ctypes
+    L = abi.lib()
+    st = abi.RhipTable.from_buffer_copy(t.struct)
+    n = t.n
+    order = torch.empty(n, dtype=torch.int32, device=DEV)
+    pos = torch.empty(n, dtype=torch.int32, device=DEV)
+    ows = torch.empty(abi._sizeq(L.rhip_order_workspace_bytes, n), dtype=torch.uint8, device=DEV)
+    bb = ctypes.c_size_t(0)
+    if with_bricks:
+        assert L.rhip_brick_bytes(ctypes.byref(st), ctypes.byref(bb)) == 0
+    bricks = torch.empty(max(int(bb.value), 1), dtype=torch.uint8, device=DEV)
+    rc = L.rhip_spatial_order(ctypes.byref(st), abi._ptr(order), abi._ptr(pos),
+                              abi._ptr(bricks) if with_bricks else None, int(bb.value),
+                              abi._ptr(ows), ows.numel(), abi._stream(torch.device(DEV)))
+    assert rc == 0, L.rhip_last_error()
+    torch.cuda.synchronize()
+    return st, order.cpu().numpy(), pos.cpu().numpy()
+
+
+# (D, rows, span, stride, which): which = the path the brick storage takes,
+# "walk" (counting sort through the grid in brick Morton order) or "sort"
+# (radix sort of the keys, then the grid filled from the sorted keys)
+_ORDER_SETS = [(1, 3000, 2000, 1, "walk"), (2, 20000, 200, 1, "walk"), (3, 40000, 50, 2, "walk"),
+               (3, 30000, 37, 1, "walk"), (4, 30000, 12, 1, "walk"), (5, 20000, 5, 2, "walk"),
+               (6, 4000, 3, 1, "walk"), (6, 80000, 9, 1, "sort")]
+
+
+@pytest.mark.parametrize("D,n,span,stride,which", _ORDER_SETS)
+def test_spatial_order_paths_agree_with_morton(D, n, span, stride, which):
+    """The locality order with a brick grid (walked, or filled after a sort
+    when the power-of-two padding makes the walk too long) and without one
+    (sort only) is the Morton order of the rows; the brick path is the one
+    the set's shape selects."""
+    rng = np.random.default_rng(D * 1000 + span)
+    c = random_coords(rng, n, D, span, batch=2)
+    c[:, 1:] *= stride
+    print(f"spatial order D={D} n={n} span={span} stride={stride} path={which}", flush=True)
+    t = abi.hash_build(to_dev(c))
+    rows = t.ucoords.cpu().numpy()
+    entries, walk, limit = _brick_walk(rows)
+    assert entries <= limit
+    walks = walk <= max(8 * entries, 1 << 22)
+    assert walks == (which == "walk")
+    exp = _morton_order(rows)
+    for with_bricks in (True, False):
+        st, order, pos = _spatial_order(t, with_bricks)
+        np.testing.assert_array_equal(order, exp)
+        np.testing.assert_array_equal(pos[order], np.arange(t.n))
+        assert (st.bricks is not None) == with_bricks
+
+
+@pytest.mark.parametrize("n,span", [(4000, 3), (80000, 9)])
+def test_six_dim_cross_map_through_bricks(n, span):
+    """A 6-D kernel map (cross stencil) whose neighbour probes go through the
+    brick grid, walked (small set) or filled after the sort (large set)."""
+    rng = np.random.default_rng(n)
+    c, _, _ = oracle.insert_and_map(random_coords(rng, n, 6, span))
+    off = oracle.region_offsets(6, 3, region="cross")
+    print(f"6-D cross map n={len(c)} K={len(off)}", flush=True)
+    t = abi.hash_build(to_dev(c))
+    assert t.struct.bricks is not None
+    km = abi.kernel_map(t, t, to_dev(off))
+    kofs, in_rows, out_rows = oracle.kernel_map(c, c, off)
+    np.testing.assert_array_equal(km.offsets_host, kofs)
+    np.testing.assert_array_equal(
+        oracle.canonical_pairs(km.offsets_host, km.in_rows.cpu().numpy(), km.out_rows.cpu().numpy()),
+        oracle.canonical_pairs(kofs, in_rows, out_rows))
+
+
 @pytest.mark.parametrize("cfg", ["sphere", "indoor", "lidar", "shell4d"])
 def test_config_coordinate_sets(cfg):
     c = {"sphere": scenes.sphere_shell, "indoor": lambda: scenes.indoor_batch(4, 2),
