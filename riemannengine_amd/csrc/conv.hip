@@ -1463,8 +1463,11 @@ conv_dw_pos_kernel(const float *__restrict__ x, int64_t n_in, int cin,
 //    LDS traffic and MFMAs (wave-uniform).
 // Indices, out-of-range buffer loads, segments dealt to ranges and the
 // partial slots are as in conv_dw_pos_kernel; rows are loaded one step
-// (32 positions) ahead.
-template <int NB, int KPW, int WAVES>
+// (32 positions) ahead. With SHY the workgroup shares one dY tile per step:
+// wave w loads and stores positions 8w .. 8w+7 into one of two LDS buffers
+// and a barrier publishes it (a wave at step t writes the buffer of step
+// t-2, which every wave finished before the barrier of step t-1).
+template <int NB, int KPW, int WAVES, bool SHY = false>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(WAVES))) void
 conv_dw_pos_bf16_kernel(const __bf16 *__restrict__ x, int64_t n_in, int cin,
                         const __bf16 *__restrict__ gy, int cout, const int32_t *__restrict__ nbr,
@@ -1472,7 +1475,9 @@ conv_dw_pos_bf16_kernel(const __bf16 *__restrict__ x, int64_t n_in, int cin,
                         int ci_tiles, int co_tiles, float *__restrict__ partial) {
   constexpr int GK = kWaves * KPW;
   constexpr int LDY = 16 * NB + 8, LDX = 16 + 8; // LDS row strides (elements), 16-byte multiples
-  __shared__ __align__(16) __bf16 sY[kWaves][32 * LDY];
+  // SHY: one dY tile per step for the whole workgroup (wave w loads and
+  // writes positions 8w .. 8w+7), two buffers, one barrier per step
+  __shared__ __align__(16) __bf16 sY[SHY ? 2 : kWaves][32 * LDY];
   __shared__ __align__(16) __bf16 sX[kWaves][32 * LDX];
   const int groups = (K + GK - 1) / GK;
   const int units = ci_tiles * co_tiles * groups;
@@ -1510,9 +1515,10 @@ conv_dw_pos_bf16_kernel(const __bf16 *__restrict__ x, int64_t n_in, int cin,
     int32_t id[KPW];
     int32_t orow;
   };
+  constexpr int kYv = SHY ? 1 : NB;
   struct Dat {
     v4u xv[KPW];
-    v4u yv[NB];
+    v4u yv[kYv];
   };
   auto load_seg = [&](int sg, Seg &S) {
     const int64_t p = 64 * (rg + static_cast<int64_t>(sg) * ranges) + lane;
@@ -1549,10 +1555,22 @@ conv_dw_pos_bf16_kernel(const __bf16 *__restrict__ x, int64_t n_in, int cin,
       const uint32_t o = static_cast<uint32_t>(__builtin_amdgcn_ds_bpermute(src, S.id[j])) + 16 * half;
       D.xv[j] = __builtin_amdgcn_raw_buffer_load_b128(rx, o, 0, 0);
     }
-    const uint32_t o = static_cast<uint32_t>(__builtin_amdgcn_ds_bpermute(src, S.orow)) + 16 * NB * half;
+    if constexpr (SHY) {
+      // lane L: position 8w + L/(2NB) of the step, 16-byte chunk L%(2NB) of
+      // its row; lanes past 16*NB load nothing
+      const int q = 8 * wv + lane / (2 * NB);
+      const uint32_t o =
+          static_cast<uint32_t>(__builtin_amdgcn_ds_bpermute((32 * s + (q & 31)) * 4, S.orow)) +
+          16 * (lane % (2 * NB));
+      D.yv[0] = __builtin_amdgcn_raw_buffer_load_b128(
+          ry, pick(o, opaque(lane < 16 * NB ? -1 : 0)), 0, 0);
+    } else {
+      const uint32_t o =
+          static_cast<uint32_t>(__builtin_amdgcn_ds_bpermute(src, S.orow)) + 16 * NB * half;
 #pragma unroll
-    for (int q = 0; q < NB; ++q)
-      D.yv[q] = __builtin_amdgcn_raw_buffer_load_b128(ry, o + 16 * q, 0, 0);
+      for (int q = 0; q < NB; ++q)
+        D.yv[q] = __builtin_amdgcn_raw_buffer_load_b128(ry, o + 16 * q, 0, 0);
+    }
   };
 
   v4f acc[KPW][NB];
@@ -1561,28 +1579,40 @@ conv_dw_pos_bf16_kernel(const __bf16 *__restrict__ x, int64_t n_in, int cin,
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb)
       acc[j][nb] = v4f{0.f, 0.f, 0.f, 0.f};
-  __bf16 *const wy = sY[wv];
+  __bf16 *const wy = sY[SHY ? 0 : wv];
   __bf16 *const wx = sX[wv];
+  // SHY: publish step data D's dY chunk into buffer buf for every wave
+  auto share_dy = [&](const Dat &D, int buf) {
+    if (lane < 16 * NB)
+      *reinterpret_cast<v4u *>(sY[buf] + (8 * wv + lane / (2 * NB)) * LDY +
+                               8 * (lane % (2 * NB))) = D.yv[0];
+    __syncthreads();
+  };
   const int prow = 8 * g + i16 / 4, pcol = 4 * (i16 % 4);
   auto operand = [&](const __bf16 *base, int ld, int col) {
     const v4s lo = ds_read_tr16(base + prow * ld + col + pcol);
     const v4s hi = ds_read_tr16(base + (prow + 4) * ld + col + pcol);
     return __builtin_bit_cast(v8bf, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
   };
-  auto compute = [&](const Dat &D, const uint64_t (&live)[KPW], int s) {
+  auto compute = [&](const Dat &D, const uint64_t (&live)[KPW], int s, int buf) {
     bool any = false;
 #pragma unroll
     for (int j = 0; j < KPW; ++j)
       any |= ((live[j] >> (32 * s)) & 0xffffffffull) != 0;
     if (!any)
       return; // wave-uniform
+    const __bf16 *ty = wy;
+    if constexpr (SHY) {
+      ty = sY[buf];
+    } else {
 #pragma unroll
-    for (int q = 0; q < NB; ++q)
-      *reinterpret_cast<v4u *>(wy + (lane >> 1) * LDY + 8 * NB * half + 8 * q) = D.yv[q];
+      for (int q = 0; q < NB; ++q)
+        *reinterpret_cast<v4u *>(wy + (lane >> 1) * LDY + 8 * NB * half + 8 * q) = D.yv[q];
+    }
     v8bf b[NB];
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb)
-      b[nb] = operand(wy, LDY, 16 * nb);
+      b[nb] = operand(ty, LDY, 16 * nb);
 #pragma unroll
     for (int j = 0; j < KPW; ++j)
       if ((live[j] >> (32 * s)) & 0xffffffffull) { // wave-uniform
@@ -1598,13 +1628,19 @@ conv_dw_pos_bf16_kernel(const __bf16 *__restrict__ x, int64_t n_in, int cin,
   Seg SA, SB;
   uint64_t LA[KPW], LB[KPW];
   Dat DA, DB;
+  // SHY: step 0 of a segment uses buffer 0, step 1 buffer 1; each step's dY
+  // is published before the next step's loads are issued
   auto run_seg = [&](Seg &S, const uint64_t (&LS)[KPW], Seg &N, uint64_t (&LN)[KPW],
                      int next_load) {
+    if constexpr (SHY)
+      share_dy(DA, 0);
     load_dat(S, 1, DB);
-    compute(DA, LS, 0);
+    compute(DA, LS, 0, 0);
+    if constexpr (SHY)
+      share_dy(DB, 1);
     prep(N, LN);
     load_dat(N, 0, DA);
-    compute(DB, LS, 1);
+    compute(DB, LS, 1, 1);
     load_seg(next_load, S);
   };
   load_seg(0, SA);
@@ -2113,6 +2149,13 @@ template <int VB> constexpr int kDwPosWaves = VB == 4 ? 2 : 3;
 // against 142, C256 (9k rows, 8 ranges) 93 against 146; its 808k-row stage
 // against the narrow-channel conv_dw_rows_kernel: C32->32 139 us against
 // 189, C16->32 94 against 161 (3 waves per SIMD spills: 200 and 153).
+// 64-channel tiles with 7 offsets per wave share each step's dY tile through
+// LDS (a quarter loaded by each wave, one barrier per step): config 2
+// 145-147 us against 162-168 alternating on one box, config 5 6.22 ms a step
+// against 6.37; with 32-channel tiles (half of each wave's fill lanes idle)
+// or 2 offsets per wave the barrier costs more than it saves (config 1
+// 42 us against 37, config 3's 2^3 down map 32 against 27), so those load
+// their own dY.
 static bool dw_pos_supported(int32_t dtype, int cin, int cout, int K, int64_t n_in,
                              int64_t n_out) {
   const int64_t s = dtype == RHIP_F32 ? 4 : 2;
@@ -2173,7 +2216,9 @@ static void run_dw_pos_bf16(const __bf16 *x, int64_t n_in, int cin, const __bf16
     const dim3 grid(static_cast<unsigned>(ranges * ct * ot * groups));
     auto go = [&](auto nb, auto kpw, auto w) {
       hipLaunchKernelGGL((conv_dw_pos_bf16_kernel<decltype(nb)::value, decltype(kpw)::value,
-                                                  decltype(w)::value>),
+                                                  decltype(w)::value,
+                                                  decltype(nb)::value == 4 &&
+                                                      decltype(kpw)::value == kDwPosKPW>),
                          grid, dim3(kThreads), 0, s, x, n_in, cin, gy, cout, nbr, out_order, n_out,
                          K, ranges, ct, ot, partial);
     };
