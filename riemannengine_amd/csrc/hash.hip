@@ -177,66 +177,85 @@ __device__ __forceinline__ void apply_layout(TableView &t, const HashLayout *L) 
 // earliest row that inserted the key (in the key word when row_bits > 0,
 // else in first_row through atomicMin). A row that finds its key already
 // there flags the set as having repeats.
+// The wave cooperates on repeats: with packed keys, a lane whose key equals
+// the previous lane's follows that run's first lane, which probes once for
+// the whole run, and takes its slot by a shuffle. Points quantised in scan
+// order repeat their voxel in runs (config 3's raw LiDAR sweeps: 107k of
+// 250k rows repeat the previous row), and those runs would otherwise hammer
+// one slot with compare-and-swaps that the L2 serialises. The run's first
+// lane has its smallest row, so the first occurrence still wins.
 __global__ __launch_bounds__(kBlock) void insert_kernel(const int32_t *coords,
                                                         int64_t n,
                                                         TableView t,
                                                         HashLayout *L,
                                                         uint32_t *slot_of_row) {
-  int64_t r = blockIdx.x * (int64_t)kBlock + threadIdx.x;
-  if (r >= n)
-    return;
+  const int64_t r = blockIdx.x * (int64_t)kBlock + threadIdx.x;
+  const bool valid = r < n; // every lane stays for the wave's shuffles
   apply_layout(t, L);
   const int rb = L->row_bits;
   int32_t c[RHIP_MAX_COLS];
 #pragma unroll
   for (int i = 0; i < RHIP_MAX_COLS; ++i)
-    c[i] = i < t.ncol ? coords[r * t.ncol + i] : 0;
+    c[i] = valid && i < t.ncol ? coords[r * t.ncol + i] : 0;
 
-  uint64_t key, h;
+  uint64_t key = 0, h = 0;
   uint32_t hr = 0;
-  if (t.mode == RHIP_KEY_PACKED64) {
-    pack_row(t, c, key); // always in range: the bounds come from this set
+  const bool packed = t.mode == RHIP_KEY_PACKED64; // uniform
+  if (packed) {
+    pack_row(t, c, key); // in range for valid rows: the bounds come from this set
     h = mix64(key) & t.mask;
   } else {
     hr = hash_row(c, t.ncol);
     key = (static_cast<uint64_t>(hr) << 32) | static_cast<uint32_t>(r);
     h = mix64(hr) & t.mask;
   }
-  const uint64_t mine = rb > 0 ? (key << rb) | static_cast<uint64_t>(r) : key;
-  while (true) {
-    // one round trip per probe: the CAS either claims the empty slot or
-    // returns the word already there
-    uint64_t *wp = &t.slots[h].word;
-    const uint64_t w = atomicCAS(reinterpret_cast<unsigned long long *>(wp), kEmptyWord, mine);
-    if (w == kEmptyWord) {
-      if (rb == 0)
-        atomicMin(&t.slots[h].first_row, static_cast<uint32_t>(r));
-      break; // claimed
-    }
-    bool same;
-    if (rb > 0) {
-      same = (w >> rb) == key;
-    } else if (t.mode == RHIP_KEY_PACKED64) {
-      same = (w == key);
-    } else {
-      same = static_cast<uint32_t>(w >> 32) == hr &&
-             rows_equal(coords + static_cast<int64_t>(static_cast<uint32_t>(w)) *
-                                     t.ncol,
-                        c, t.ncol);
-    }
-    if (same) {
-      L->dups = 1;
-      if (rb > 0) {
-        if (mine < w)
-          atomicMin(reinterpret_cast<unsigned long long *>(wp), mine);
-      } else {
-        atomicMin(&t.slots[h].first_row, static_cast<uint32_t>(r));
+  const int lane = lane_id();
+  const uint64_t kprev = __shfl_up(key, 1, kWave);
+  // lane - 1 holds row r - 1, valid whenever r is
+  const bool follow = packed && valid && lane > 0 && kprev == key;
+  const uint64_t heads = __ballot(!follow);
+  if (valid && !follow) {
+    const uint64_t mine = rb > 0 ? (key << rb) | static_cast<uint64_t>(r) : key;
+    while (true) {
+      // one round trip per probe: the CAS either claims the empty slot or
+      // returns the word already there
+      uint64_t *wp = &t.slots[h].word;
+      const uint64_t w = atomicCAS(reinterpret_cast<unsigned long long *>(wp), kEmptyWord, mine);
+      if (w == kEmptyWord) {
+        if (rb == 0)
+          atomicMin(&t.slots[h].first_row, static_cast<uint32_t>(r));
+        break; // claimed
       }
-      break;
+      bool same;
+      if (rb > 0) {
+        same = (w >> rb) == key;
+      } else if (packed) {
+        same = (w == key);
+      } else {
+        same = static_cast<uint32_t>(w >> 32) == hr &&
+               rows_equal(coords + static_cast<int64_t>(static_cast<uint32_t>(w)) * t.ncol, c,
+                          t.ncol);
+      }
+      if (same) {
+        L->dups = 1;
+        if (rb > 0) {
+          if (mine < w)
+            atomicMin(reinterpret_cast<unsigned long long *>(wp), mine);
+        } else {
+          atomicMin(&t.slots[h].first_row, static_cast<uint32_t>(r));
+        }
+        break;
+      }
+      h = (h + 1) & t.mask;
     }
-    h = (h + 1) & t.mask;
   }
-  slot_of_row[r] = static_cast<uint32_t>(h);
+  // the slot of this lane's run: its first lane's
+  const uint32_t slot =
+      static_cast<uint32_t>(__shfl(static_cast<uint32_t>(h), run_head(heads), kWave));
+  if (__ballot(follow) != 0 && lane == 0)
+    L->dups = 1;
+  if (valid)
+    slot_of_row[r] = slot;
 }
 
 // Per-block count of rows that are the first occurrence of their key (every
@@ -344,14 +363,21 @@ __global__ __launch_bounds__(kBlock) void lookup_kernel(TableView t,
                                                         const int32_t *queries,
                                                         int64_t n,
                                                         int32_t *result) {
-  int64_t i = blockIdx.x * (int64_t)kBlock + threadIdx.x;
-  if (i >= n)
-    return;
+  const int64_t i = blockIdx.x * (int64_t)kBlock + threadIdx.x;
+  const bool valid = i < n; // every lane stays for the wave's shuffles
   int32_t c[RHIP_MAX_COLS];
 #pragma unroll
   for (int j = 0; j < RHIP_MAX_COLS; ++j)
-    c[j] = j < t.ncol ? queries[i * t.ncol + j] : 0;
-  result[i] = table_find(t, c);
+    c[j] = valid && j < t.ncol ? queries[i * t.ncol + j] : 0;
+  // a query that repeats the previous lane's takes that run's answer
+  const bool follow = repeats_prev_row(c, valid);
+  const uint64_t heads = __ballot(!follow);
+  int32_t res = -1;
+  if (valid && !follow)
+    res = table_find(t, c);
+  res = __shfl(res, run_head(heads), kWave);
+  if (valid)
+    result[i] = res;
 }
 
 // Sort keys of the locality order. morton_bits > 0: batch offset in the top
@@ -532,8 +558,7 @@ __global__ __launch_bounds__(kBlock) void brick_mark_kernel(TableView t, int64_t
   // takes bits only from lanes at or after the start of its own run
   const int64_t gprev = __shfl_up(g, 1, kWave);
   const uint64_t heads = __ballot(lane == 0 || gprev != g);
-  const uint64_t upto = lane == kWave - 1 ? ~0ull : (2ull << lane) - 1ull;
-  const int start = 63 - __clzll(heads & upto);
+  const int start = run_head(heads);
   for (int off = 1; off < kWave; off <<= 1) {
     const uint64_t bp = __shfl_up(bits, off, kWave);
     if (lane - off >= start)

@@ -324,14 +324,22 @@ __global__ __launch_bounds__(kPoolThreads) void stride_lookup_kernel(
     uint32_t *__restrict__ keys, int32_t *__restrict__ vals,
     unsigned long long *__restrict__ miss) {
   const int64_t i = blockIdx.x * static_cast<int64_t>(kPoolThreads) + threadIdx.x;
-  if (i >= n)
-    return;
+  const bool valid = i < n; // every lane stays for the wave's shuffles
   int32_t c[RHIP_MAX_COLS];
-  c[0] = in[i * t.ncol];
+  c[0] = valid ? in[i * t.ncol] : 0;
 #pragma unroll
   for (int j = 1; j < RHIP_MAX_COLS; ++j)
-    c[j] = j < t.ncol ? floor_align(in[i * t.ncol + j], st.s[j - 1]) : 0;
-  const int32_t o = table_find(t, c);
+    c[j] = valid && j < t.ncol ? floor_align(in[i * t.ncol + j], st.s[j - 1]) : 0;
+  // input rows in one stride cell query the same output row: a row whose
+  // cell repeats the previous lane's takes that run's answer
+  const bool follow = repeats_prev_row(c, valid);
+  const uint64_t heads = __ballot(!follow);
+  int32_t o = -1;
+  if (valid && !follow)
+    o = table_find(t, c);
+  o = __shfl(o, run_head(heads), kWave);
+  if (!valid)
+    return;
   if (o < 0) {
     atomicAdd(&miss[0], 1ull);
     atomicMin(&miss[1], static_cast<unsigned long long>(i));

@@ -265,6 +265,24 @@ __device__ __forceinline__ uint32_t lanes_below(uint64_t mask) {
                                        static_cast<uint32_t>(mask), 0u));
 }
 
+// Runs of lanes: `heads` has a bit for every lane that starts a run (lane 0
+// always does); the first lane of this lane's run.
+__device__ __forceinline__ int run_head(uint64_t heads) {
+  const int lane = lane_id();
+  const uint64_t upto = lane == kWave - 1 ? ~0ull : (2ull << lane) - 1ull;
+  return 63 - __clzll(heads & upto);
+}
+
+// Whether this lane's coordinate row equals the previous lane's (lane 0 and
+// lanes with valid false never do); every lane of the wave must call it.
+__device__ __forceinline__ bool repeats_prev_row(const int32_t (&c)[RHIP_MAX_COLS], bool valid) {
+  bool same = valid && lane_id() > 0;
+#pragma unroll
+  for (int j = 0; j < RHIP_MAX_COLS; ++j)
+    same = (__shfl_up(c[j], 1, kWave) == c[j]) && same;
+  return same;
+}
+
 // Segmented exclusive scan, one 1024-lane workgroup per segment (blockIdx.x):
 // base[s*m + i] = sum(counts[s*m .. s*m+i)), total[s] = sum of segment s.
 // The segment goes in chunks of 4096 entries, four consecutive ones per lane

@@ -109,9 +109,13 @@ def _ray_boxes(o, d, lo, hi):
 
 def lidar_sweep(rng: np.random.Generator, beams: int = 64, azimuths: int = 2048,
                 n_boxes: int = 40, voxel: float = 0.1, height: float = 1.8,
-                max_range: float = 80.0, noise: float = 0.02) -> np.ndarray:
+                max_range: float = 80.0, noise: float = 0.02,
+                unique: bool = True) -> np.ndarray:
     """Spinning LiDAR: beams at elevations -25..+3 deg x azimuths against a
-    ground plane (z=0) and random boxes, range noise N(0, noise), voxelised."""
+    ground plane (z=0) and random boxes, range noise N(0, noise), voxelised.
+    unique=False keeps every quantised point in scan order (beam by beam,
+    azimuth by azimuth), repeats included: the input a coordinate map
+    deduplicates."""
     el = np.deg2rad(np.linspace(-25.0, 3.0, beams))
     az = np.linspace(0.0, 2 * np.pi, azimuths, endpoint=False)
     E, A = np.meshgrid(el, az, indexing="ij")
@@ -132,7 +136,7 @@ def lidar_sweep(rng: np.random.Generator, beams: int = 64, azimuths: int = 2048,
     t = t[keep] + rng.normal(0.0, noise, keep.sum())
     pts = o + d[keep] * t[:, None]
     v = np.floor(pts / voxel).astype(np.int64)
-    return _unique_rows(v)
+    return _unique_rows(v) if unique else v
 
 
 def lidar_batch(batch: int = 2, seed: int = 3, **kw) -> np.ndarray:

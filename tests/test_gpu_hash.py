@@ -29,6 +29,46 @@ def test_build_matches_oracle(n, D, span):
     _check_build(random_coords(rng, n, D, span))
 
 
+def test_scan_order_points_match_oracle():
+    """Raw quantised LiDAR points in scan order, the input a coordinate map
+    deduplicates: most repeats follow the same point, in runs that one lane
+    inserts for the whole run."""
+    c = scenes.lidar_batch(2, 3, unique=False)
+    assert np.all(c[1:] == c[:-1], axis=1).sum() > len(c) // 3
+    t = _check_build(c)
+    assert t.n == len(scenes.lidar_batch(2, 3))
+
+
+@pytest.mark.parametrize("span", [20, 30000])
+def test_runs_of_repeats_match_oracle(span):
+    """Runs of one row of random lengths (some longer than a wave), and rows
+    that come back later after other rows; span 30000 leaves no room for
+    the row in the key word (the first row is kept beside the key)."""
+    rng = np.random.default_rng(span)
+    base = random_coords(rng, 6000, 3, span)
+    reps = rng.integers(1, 12, len(base))
+    reps[rng.integers(0, len(base), 20)] = rng.integers(60, 200, 20)
+    c = np.repeat(base, reps, axis=0)
+    c = np.concatenate([c, base[rng.integers(0, len(base), 3000)], c[:5000]])
+    print(f"runs: {len(c)} rows", flush=True)
+    _check_build(c)
+
+
+def test_lookup_repeated_queries():
+    """Queries in runs (present, absent and out-of-range rows) take their
+    run's answer."""
+    rng = np.random.default_rng(5)
+    c = random_coords(rng, 20000, 3, 30)
+    t = abi.hash_build(to_dev(c))
+    rows = np.concatenate([c[:3000], random_coords(rng, 1000, 3, 40),
+                           np.array([[0, 2**31 - 1, 0, 0], [1, -2**31, 7, 7]], np.int32)])
+    q = np.repeat(rows, rng.integers(1, 90, len(rows)), axis=0)
+    got = t.lookup(to_dev(q)).cpu().numpy()
+    uq, _, _ = oracle.insert_and_map(c)
+    where = {tuple(r): i for i, r in enumerate(uq.tolist())}
+    np.testing.assert_array_equal(got, [where.get(tuple(r), -1) for r in q.tolist()])
+
+
 def test_build_empty():
     t = abi.hash_build(torch.zeros((0, 4), dtype=torch.int32, device=DEV))
     assert t.n == 0

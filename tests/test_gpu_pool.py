@@ -69,6 +69,40 @@ def test_stride_map_matches_oracle(stride):
     assert km.n_pairs == len(c) and np.all(np.diff(orr) >= 0)
 
 
+def test_stride_map_sorted_input_matches_oracle():
+    """Input rows in coordinate order: neighbouring rows share a stride cell,
+    so the lookups come in runs that one lane resolves for the whole run."""
+    rng = np.random.default_rng(11)
+    c, _, _ = oracle.insert_and_map(random_coords(rng, 30000, 3, 12))
+    c = c[np.lexsort(c[:, ::-1].T)]
+    tin = abi.hash_build(to_dev(c))
+    tout = abi.hash_build(abi.stride_coords(tin.ucoords, [2, 2, 2]))
+    km = abi.stride_map(tin, tout, [2, 2, 2])
+    exp, miss = oracle.stride_map(c, tout.ucoords.cpu().numpy(), [2, 2, 2])
+    assert miss == 0
+    _check_table(km, exp)
+    np.testing.assert_array_equal(exp[km.in_rows.cpu().numpy()], km.out_rows.cpu().numpy())
+
+
+def test_stride_map_unmatched_run_counts_every_row():
+    """The rows of a stride cell missing from the output map all count in
+    the error, the run's followers included."""
+    rng = np.random.default_rng(12)
+    c, _, _ = oracle.insert_and_map(random_coords(rng, 20000, 3, 10))
+    c = c[np.lexsort(c[:, ::-1].T)]
+    sc = c.copy()
+    sc[:, 1:] = np.floor_divide(c[:, 1:], 2) * 2  # each row's floor-aligned row
+    cells, counts = np.unique(sc, axis=0, return_counts=True)
+    drop = cells[np.argmax(counts)]
+    keep = cells[np.any(cells != drop, axis=1)]
+    missing = np.flatnonzero(np.all(sc == drop, axis=1))
+    assert np.any(np.diff(missing) == 1)  # some missing row follows another
+    tin = abi.hash_build(to_dev(c))
+    tout = abi.hash_build(to_dev(keep))
+    with pytest.raises(RuntimeError, match=f"input row {missing[0]} .*\\({len(missing)} such rows\\)"):
+        abi.stride_map(tin, tout, [2, 2, 2])
+
+
 def test_stride_map_unmatched_input_raises():
     """An input whose floor-aligned row is not in the output map: the host
     gets an error (the reference ASSERTs); every kernel still ends normally."""
