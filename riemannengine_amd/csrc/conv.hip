@@ -1785,9 +1785,10 @@ static void launch_os(const T *x, int cred, const T *wt, int credw, int ncols,
 // Launch shape, measured on MI355X. One 16-row group per wave (64 rows per
 // workgroup: more workgroups in flight hide the gather latency better than
 // more rows per wave) and the widest channel chunk the reduction width
-// allows. fp32 (config 2, C64): a register budget for 8 waves per SIMD (62
-// registers: 356-360 us against 368-370 with the 6-wave budget's 64, in the
-// largest-first tile order), one stage per barrier. bf16 (config-5 stages): 8 waves per SIMD and one stage
+// allows. fp32 (config 2, C64): a register budget for 6 waves per SIMD at
+// 64 columns with quad-order gathers (dX 393-396 us against 404-406 at the
+// 8-wave budget, which fits in 60 registers; the 8-wave budget led before the
+// quad-order gathers), one stage per barrier. bf16 (config-5 stages): 8 waves per SIMD and one stage
 // per barrier at 64 columns; 128-column tiles (4 waves per SIMD, 2 stages
 // per barrier) for 128 and 256 channels; 4 stages per barrier for 32-channel
 // chunks (6 waves per SIMD at 64 columns, where 8 do not fit the registers).
