@@ -37,8 +37,9 @@
 //            (ordered by offset, then processing position);
 //   symmetric maps (a set onto itself with a stencil closed under negation):
 //            the input order is the output order and the transposed table is
-//            the forward table with partner offsets (a copy): i pairs with o
-//            under k iff o pairs with i under the partner of k;
+//            the forward table with partner offsets, stored by the emit from
+//            the entries it reads: i pairs with o under k iff o pairs with i
+//            under the partner of k;
 //   otherwise: the input rows' transposed masks (atomicOr during the emit),
 //            a sort of the input rows by them -> in_order / in_pos, and
 //            nbr_t[k][in_pos[i]] = output row paired with i under k.
@@ -314,17 +315,30 @@ __global__ __launch_bounds__(kMapBlock) void zero_u64_kernel(unsigned long long 
 
 // Lane per processing position p and offset k = blockIdx.y: a hit is written
 // at its offset's start + its wave's run (wave_base) + its rank in the wave.
+// Symmetric maps (partner given): the transposed table is the forward table
+// with partner rows, nbr_t[partner[k]][p] = nbr[k][p] (partner is its own
+// inverse), and the input order is the output order; the emit stores both
+// from the values it already holds instead of a second pass over nbr.
 __global__ __launch_bounds__(kMapBlock) void kmap_emit_kernel(
     const int32_t *__restrict__ nbr, const int32_t *__restrict__ out_order,
     int64_t n_out, int64_t nw, const int64_t *__restrict__ kofs,
     const int64_t *__restrict__ wave_base, int32_t *__restrict__ in_rows,
-    int32_t *__restrict__ out_rows, unsigned long long *__restrict__ mask_t) {
+    int32_t *__restrict__ out_rows, unsigned long long *__restrict__ mask_t,
+    const int32_t *__restrict__ partner, int K, int32_t *__restrict__ nbr_t,
+    int32_t *__restrict__ in_order) {
   const int k = blockIdx.y;
   const int64_t p = blockIdx.x * (int64_t)kMapBlock + threadIdx.x;
   const int64_t w = p / kWave;
   if (w >= nw)
     return;
   const int32_t v = p < n_out ? nbr[k * n_out + p] : -1;
+  if (partner != nullptr && p < n_out) {
+    const int32_t pk = partner[k];
+    if (pk >= 0 && pk < K) // a workspace not prepared by phase 1 writes nothing
+      nbr_t[static_cast<int64_t>(pk) * n_out + p] = v;
+    if (k == 0)
+      in_order[p] = out_order[p];
+  }
   const uint64_t b = __ballot(v >= 0);
   if (v >= 0) {
     const int64_t q = kofs[k] + wave_base[k * nw + w] + lanes_below(b);
@@ -333,27 +347,6 @@ __global__ __launch_bounds__(kMapBlock) void kmap_emit_kernel(
     if (mask_t)
       atomicOr(&mask_t[2 * static_cast<int64_t>(v) + (k >> 6)], 1ull << (k & 63));
   }
-}
-
-// Symmetric maps: nbr_t[k] = nbr[partner[k]] (rows of one map, same order).
-// A partner outside [0, K) (a workspace not prepared by phase 1) leaves the
-// row untouched instead of reading out of bounds.
-__global__ __launch_bounds__(kMapBlock) void kmap_partner_copy_kernel(
-    const int32_t *__restrict__ nbr, int64_t n, int K, const int32_t *__restrict__ partner,
-    int32_t *__restrict__ nbr_t) {
-  const int k = blockIdx.y;
-  const int64_t j = blockIdx.x * (int64_t)kMapBlock + threadIdx.x;
-  const int32_t pk = partner[k];
-  if (j < n && pk >= 0 && pk < K)
-    nbr_t[k * n + j] = nbr[static_cast<int64_t>(pk) * n + j];
-}
-
-__global__ __launch_bounds__(kMapBlock) void copy_i32_kernel(const int32_t *__restrict__ src,
-                                                             int64_t n,
-                                                             int32_t *__restrict__ dst) {
-  const int64_t j = blockIdx.x * (int64_t)kMapBlock + threadIdx.x;
-  if (j < n)
-    dst[j] = src[j];
 }
 
 __global__ __launch_bounds__(kMapBlock) void in_key_kernel(
@@ -619,25 +612,18 @@ extern "C" int rhip_kmap_fill(const int32_t *nbr, const int32_t *out_order, int6
                          dim3(kMapBlock), 0, stream, w.mask_t, 2 * n_in);
       RHIP_LAUNCH_CHECK();
     }
+    const bool fuse_t = want_t && sym; // the emit writes nbr_t and in_order
     if (n_out > 0) {
       RHIP_CHECK_ARG(nbr && out_order, "nbr and out_order are required");
       hipLaunchKernelGGL(kmap_emit_kernel, dim3(nb, K), dim3(kMapBlock), 0, stream, nbr,
                          out_order, n_out, nw, kmap_offsets, w.wave_base, in_rows, out_rows,
-                         masks ? w.mask_t : nullptr);
+                         masks ? w.mask_t : nullptr, fuse_t ? w.partner : nullptr, K,
+                         fuse_t ? nbr_t : nullptr, fuse_t ? in_order : nullptr);
       RHIP_LAUNCH_CHECK();
     }
-    if (!want_t)
+    if (!want_t || sym)
       return;
     const int64_t nbi = ceil_div(n_in, kMapBlock);
-    if (sym) {
-      hipLaunchKernelGGL(copy_i32_kernel, dim3(nbi), dim3(kMapBlock), 0, stream, out_order,
-                         n_in, in_order);
-      RHIP_LAUNCH_CHECK();
-      hipLaunchKernelGGL(kmap_partner_copy_kernel, dim3(nbi, K), dim3(kMapBlock), 0, stream,
-                         nbr, n_in, K, w.partner, nbr_t);
-      RHIP_LAUNCH_CHECK();
-      return;
-    }
     const int32_t *qpos = nullptr;
     if (masks) {
       hipLaunchKernelGGL(in_key_kernel, dim3(nbi), dim3(kMapBlock), 0, stream, w.mask_t,
