@@ -362,7 +362,11 @@ def kernel_map(in_table: CoordTable, out_table: CoordTable, offsets) -> KernelMa
     _check(L.rhip_kmap_fill(_ptr(nbr), _ptr(out_order), n_out, K, _ptr(in_table.order), n_in,
                             flags.value, _ptr(ws), ws.numel(), _ptr(kofs), _ptr(in_rows),
                             _ptr(out_rows), _ptr(nbr_t), _ptr(in_order), st), "rhip_kmap_fill")
-    kofs_host = kofs.cpu().numpy()
+    # the one read-back: the pair counts through pinned memory
+    kofs_pinned = torch.empty(K + 1, dtype=torch.int64, pin_memory=True)
+    kofs_pinned.copy_(kofs, non_blocking=True)
+    torch.cuda.current_stream(dev).synchronize()
+    kofs_host = kofs_pinned.numpy()
     P = int(kofs_host[-1])
     return KernelMap(K, n_in, n_out, kofs, kofs_host, in_rows[:P], out_rows[:P],
                      nbr[:, :n_out], nbr_t[:, :n_in], in_order[:n_in], out_order[:n_out],

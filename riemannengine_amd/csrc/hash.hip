@@ -828,8 +828,12 @@ extern "C" int rhip_hash_build(const int32_t *coords, int64_t n, int32_t ncol,
       RHIP_LAUNCH_CHECK();
     }
     HashLayout hl;
-    RHIP_HIP(hipMemcpyAsync(&hl, w.layout, sizeof(hl), hipMemcpyDeviceToHost, stream));
-    RHIP_HIP(hipStreamSynchronize(stream));
+    {
+      PinnedReadback rb = pinned_readback(sizeof(hl));
+      RHIP_HIP(hipMemcpyAsync(rb.ptr, w.layout, sizeof(hl), hipMemcpyDeviceToHost, stream));
+      RHIP_HIP(hipStreamSynchronize(stream));
+      std::memcpy(&hl, rb.ptr, sizeof(hl));
+    }
     table->n_unique = hl.n_unique;
     table->mode = hl.mode;
     table->key_bits = hl.key_bits;

@@ -18,6 +18,10 @@ void check_rhip(int status, const char *what) {
 
 namespace {
 
+void check_hip(hipError_t e, const char *what) {
+  TORCH_CHECK(e == hipSuccess, what, " failed: ", hipGetErrorString(e));
+}
+
 hipStream_t current_stream(const at::Device &device) {
   return c10::hip::getCurrentHIPStream(device.index()).stream();
 }
@@ -151,8 +155,9 @@ at::Tensor region_offsets(RegionType::Type region, const stride_type &kernel_siz
   TORCH_CHECK(dilation.size() == kernel_size.size() && tensor_stride.size() == kernel_size.size(),
               "kernel size, dilation and tensor stride must have the same length");
   const int K = region_volume(region, kernel_size, custom);
-  auto out = torch::zeros({K, D}, torch::kInt64);
-  auto o = out.accessor<int64_t, 2>();
+  // computed in plain int64 arithmetic (a few torch CPU ops here cost more
+  // than the map's first kernels)
+  std::vector<int64_t> o(static_cast<size_t>(K) * D, 0);
   std::vector<int64_t> step(D);
   for (int i = 0; i < D; ++i)
     step[i] = static_cast<int64_t>(dilation[i]) * tensor_stride[i];
@@ -164,7 +169,7 @@ at::Tensor region_offsets(RegionType::Type region, const stride_type &kernel_siz
         const int64_t ks = kernel_size[i];
         const int64_t idx = rem % ks;
         rem /= ks;
-        o[k][i] = (ks % 2 == 0 ? idx : idx - ks / 2) * step[i];
+        o[static_cast<size_t>(k) * D + i] = (ks % 2 == 0 ? idx : idx - ks / 2) * step[i];
       }
     }
   } else if (region == RegionType::HYPER_CROSS) {
@@ -173,18 +178,24 @@ at::Tensor region_offsets(RegionType::Type region, const stride_type &kernel_siz
     for (int axis = 0; axis < D; ++axis) {
       const int64_t r = (static_cast<int64_t>(kernel_size[axis]) - 1) / 2;
       for (int64_t ind = 0; ind < static_cast<int64_t>(kernel_size[axis]) - 1; ++ind, ++k)
-        o[k][axis] = (ind < r ? ind + 1 : ind - 2 * r) * step[axis];
+        o[static_cast<size_t>(k) * D + axis] = (ind < r ? ind + 1 : ind - 2 * r) * step[axis];
     }
   } else {
     auto c = normalize_region_offsets(custom, D);
     auto ca = c.accessor<int32_t, 2>();
     for (int k = 0; k < K; ++k)
       for (int i = 0; i < D; ++i)
-        o[k][i] = static_cast<int64_t>(ca[k][i]) * step[i];
+        o[static_cast<size_t>(k) * D + i] = static_cast<int64_t>(ca[k][i]) * step[i];
   }
-  TORCH_CHECK(K == 0 || (out.abs().max().item<int64_t>() <= std::numeric_limits<int32_t>::max()),
-              "Scaled offsets must fit the coordinate type");
-  return out.to(torch::kInt32);
+  auto out = torch::empty({K, D}, torch::kInt32);
+  int32_t *po = out.data_ptr<int32_t>();
+  for (size_t i = 0; i < o.size(); ++i) {
+    TORCH_CHECK(o[i] >= -static_cast<int64_t>(std::numeric_limits<int32_t>::max()) &&
+                    o[i] <= std::numeric_limits<int32_t>::max(),
+                "Scaled offsets must fit the coordinate type");
+    po[i] = static_cast<int32_t>(o[i]);
+  }
+  return out;
 }
 
 // ------------------------------------------------------ KernelGenerator
@@ -484,7 +495,11 @@ HipKernelMap CoordinateManager::generate(const CoordinateMapHIP &in_map,
                             in_rows.data_ptr<int32_t>(), out_rows.data_ptr<int32_t>(),
                             nbr_t.data_ptr<int32_t>(), in_order.data_ptr<int32_t>(), st),
              "rhip_kmap_fill");
-  const auto host_offsets = m.offsets.to(torch::kCPU); // the one synchronisation
+  // the one synchronisation: the pair counts through pinned memory (a copy
+  // to pageable memory goes through a staging copy)
+  auto host_offsets = torch::empty({K + 1}, torch::TensorOptions().dtype(torch::kInt64).pinned_memory(true));
+  host_offsets.copy_(m.offsets, /*non_blocking=*/true);
+  check_hip(hipStreamSynchronize(st), "hipStreamSynchronize");
   const int64_t *ho = host_offsets.data_ptr<int64_t>();
   m.offsets_host.assign(ho, ho + K + 1);
   const int64_t P = m.offsets_host[K];

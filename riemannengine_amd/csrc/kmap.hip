@@ -549,9 +549,14 @@ extern "C" int rhip_kmap_count(const rhip_table *in_table, const int32_t *out_co
       RHIP_CHECK_ARG(out_coords && nbr && out_order, "out_coords, nbr and out_order are required");
       // small host arrays go in kernel arguments (a copy from pageable
       // memory would wait for the device)
-      upload_i32(w.offsets, offsets_host, static_cast<size_t>(K) * D, stream);
-      if (sym)
-        upload_i32(w.partner, partner.data(), partner.size(), stream);
+      // the stencil and the partners are consecutive in the workspace: one
+      // upload for both
+      std::vector<int32_t> up(offsets_host, offsets_host + static_cast<size_t>(K) * D);
+      if (sym) {
+        up.resize(static_cast<size_t>(w.partner - w.offsets));
+        up.insert(up.end(), partner.begin(), partner.end());
+      }
+      upload_i32(w.offsets, up.data(), up.size(), stream);
       const bool masks = K <= kMaskedK && n_out > 1 && in_table->n_unique > 0;
       const TableView tv = make_view(*in_table);
       const int32_t *jpos = nullptr;

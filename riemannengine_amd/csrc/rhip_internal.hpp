@@ -5,6 +5,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <algorithm>
+#include <mutex>
 #include <stdexcept>
 #include <string>
 
@@ -33,6 +35,14 @@ struct Error : std::runtime_error {
 };
 
 void set_last_error(const std::string &msg);
+
+// A pinned host buffer of at least `bytes` for small device-to-host
+// read-backs, held (and the buffer reserved) while the holder lives.
+struct PinnedReadback {
+  std::unique_lock<std::mutex> lock;
+  void *ptr;
+};
+PinnedReadback pinned_readback(size_t bytes);
 
 #define RHIP_CHECK_ARG(cond, msg)                                              \
   do {                                                                         \
