@@ -569,6 +569,65 @@ __global__ __launch_bounds__(kBlock) void brick_mark_kernel(TableView t, int64_t
     atomicOr(reinterpret_cast<unsigned long long *>(&grid[g].mask), bits);
 }
 
+// Grid entries of the kSpanPer indices m0 .. m0 + kSpanPer - 1 (m0 a
+// multiple of kSpanPer; -1 for indices past the space or the grid). The
+// decode is linear in the index bits, so the aligned base is decoded once and
+// each index adds the (wave-uniform) decode of its low bits; brick_at per
+// index spent most of the walk kernels' time in the bit loop.
+template <int D>
+__device__ __forceinline__ void brick_span(const BrickSpace &s, const int32_t *dims, int64_t m0,
+                                           int64_t (&g)[kSpanPer]) {
+  static_assert((kSpanPer & (kSpanPer - 1)) == 0, "kSpanPer must be a power of two");
+  constexpr int LB = __builtin_ctz(kSpanPer);
+  if (s.mbits < LB) {
+#pragma unroll
+    for (int i = 0; i < kSpanPer; ++i)
+      g[i] = m0 + i < s.total ? brick_at<D>(s, dims, m0 + i) : -1;
+    return;
+  }
+  // base coordinates of m0 (its low LB bits are zero)
+  uint32_t bh[D + 1] = {};
+  {
+    uint64_t bits = static_cast<uint64_t>(m0) & ((1ull << s.mbits) - 1);
+    for (int l = 0; l < s.top; ++l) {
+#pragma unroll
+      for (int j = D; j >= 1; --j) {
+        if (l < s.pbits[j]) {
+          bh[j] |= static_cast<uint32_t>(bits & 1u) << l;
+          bits >>= 1;
+        }
+      }
+    }
+  }
+  const int64_t batch = m0 >> s.mbits;
+#pragma unroll
+  for (int i = 0; i < kSpanPer; ++i) {
+    // decode of the low bits i (the same for every lane)
+    uint32_t bl[D + 1] = {};
+    uint32_t bits = static_cast<uint32_t>(i);
+    int used = 0;
+    for (int l = 0; l < s.top && used < LB; ++l) {
+#pragma unroll
+      for (int j = D; j >= 1; --j) {
+        if (l < s.pbits[j] && used < LB) {
+          bl[j] |= (bits & 1u) << l;
+          bits >>= 1;
+          ++used;
+        }
+      }
+    }
+    int64_t gi = batch;
+    bool ok = m0 + i < s.total;
+#pragma unroll
+    for (int j = 1; j <= D; ++j) {
+      const uint32_t b = bh[j] | bl[j];
+      ok = ok && b < static_cast<uint32_t>(dims[j]);
+      gi = gi * dims[j] + b;
+    }
+    g[i] = ok ? gi : -1;
+  }
+}
+
 // Occupied cells of each kSpan-index chunk of the brick Morton space.
 template <int D>
 __global__ __launch_bounds__(kBlock) void brick_count_kernel(BrickSpace s, TableView t,
@@ -576,15 +635,16 @@ __global__ __launch_bounds__(kBlock) void brick_count_kernel(BrickSpace s, Table
                                                              int32_t *__restrict__ chunk_rows) {
   __shared__ int32_t wave_sum[kBlock / kWave];
   const int64_t m0 = blockIdx.x * kSpan + static_cast<int64_t>(threadIdx.x) * kSpanPer;
+  int64_t g[kSpanPer];
+  brick_span<D>(s, t.dims, m0, g);
+  uint64_t mk[kSpanPer];
+#pragma unroll
+  for (int i = 0; i < kSpanPer; ++i) // the loads issue back to back
+    mk[i] = g[i] >= 0 ? grid[g[i]].mask : 0;
   int32_t cnt = 0;
-  for (int i = 0; i < kSpanPer; ++i) {
-    const int64_t m = m0 + i;
-    if (m >= s.total)
-      break;
-    const int64_t g = brick_at<D>(s, t.dims, m);
-    if (g >= 0)
-      cnt += __popcll(grid[g].mask);
-  }
+#pragma unroll
+  for (int i = 0; i < kSpanPer; ++i)
+    cnt += __popcll(mk[i]);
   for (int off = kWave / 2; off > 0; off >>= 1)
     cnt += __shfl_xor(cnt, off);
   if (lane_id() == 0)
@@ -609,11 +669,10 @@ __global__ __launch_bounds__(kBlock) void brick_base_kernel(BrickSpace s, TableV
   const int64_t m0 = blockIdx.x * kSpan + static_cast<int64_t>(threadIdx.x) * kSpanPer;
   int64_t g[kSpanPer];
   uint64_t mk[kSpanPer];
+  brick_span<D>(s, t.dims, m0, g);
   int32_t cnt = 0;
 #pragma unroll
   for (int i = 0; i < kSpanPer; ++i) {
-    const int64_t m = m0 + i;
-    g[i] = m < s.total ? brick_at<D>(s, t.dims, m) : -1;
     mk[i] = g[i] >= 0 ? grid[g[i]].mask : 0;
     cnt += __popcll(mk[i]);
   }
