@@ -3,7 +3,7 @@
 // (grouping rows by output). Least-significant-digit first with 8- or 9-bit
 // digits: the fewest passes the key bits allow, then the narrowest digit for
 // that many passes (26 bits: 3 passes of 9; 22 bits: 3 of 8; 16 bits: 2 of
-// 8). Three kernels per pass over tiles of 4096 keys:
+// 8). Three kernels per pass over tiles of 2048 keys:
 //
 //   radix_hist_kernel     one workgroup per tile: the tile's digit counts
 //                         (LDS atomics), stored digit-major, counts[d][tile];
@@ -30,7 +30,9 @@ constexpr int kMaxRadixBits = 9;
 constexpr int kMaxDigits = 1 << kMaxRadixBits;
 constexpr int kSortThreads = 256;
 constexpr int kSortWaves = kSortThreads / kWave;
-constexpr int kSortItems = 16;
+// 2048-key tiles: config 2's 409,553 keys make 200 workgroups per pass (100
+// with 4096-key tiles left most CUs idle: mask sort 46 -> ~32 us)
+constexpr int kSortItems = 8;
 constexpr int kSortTile = kSortThreads * kSortItems;
 constexpr int kWaveKeys = kSortTile / kSortWaves;
 
