@@ -325,6 +325,14 @@ CoordinateMapHIP CoordinateManager::build_map(const at::Tensor &coords,
   at::Tensor inv_t;
   if (inverse)
     inv_t = torch::empty({std::max<int64_t>(n, 1)}, iopt.dtype(torch::kInt64));
+  // the locality order's buffers, sized by the row count (an upper bound of
+  // the unique rows), are allocated before the build, whose end waits for
+  // the device: after it only the brick grid is allocated before the order's
+  // launches
+  m.order = torch::empty({std::max<int64_t>(n, 1)}, iopt.dtype(torch::kInt32));
+  size_t ob = 0;
+  check_rhip(rhip_order_workspace_bytes(n, &ob), "rhip_order_workspace_bytes");
+  auto ows = device_bytes(ob, dev);
   check_rhip(rhip_hash_build(coords.data_ptr<int32_t>(), n, ncol, m.slots.data_ptr(),
                              m.slots.numel(), ws.data_ptr(), ws.numel(),
                              m.storage.data_ptr<int32_t>(), map_t.data_ptr<int64_t>(),
@@ -332,11 +340,7 @@ CoordinateMapHIP CoordinateManager::build_map(const at::Tensor &coords,
              "rhip_hash_build");
   const int64_t nu = m.table.n_unique;
   m.coords = m.storage.slice(0, 0, nu);
-  m.order = torch::empty({std::max<int64_t>(nu, 1)}, iopt.dtype(torch::kInt32));
   if (nu > 0) {
-    size_t ob = 0;
-    check_rhip(rhip_order_workspace_bytes(nu, &ob), "rhip_order_workspace_bytes");
-    auto ows = device_bytes(ob, dev);
     size_t bb = 0;
     check_rhip(rhip_brick_bytes(&m.table, &bb), "rhip_brick_bytes");
     m.bricks = device_bytes(std::max<size_t>(bb, 1), dev);
