@@ -429,7 +429,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(WAVES)
 //    zeros, so nothing is masked after the loads.
 // Measured on MI355X, config 2 bf16 forward (quad-order gathers both): 76 us
 // against 108 for conv_os_kernel with runtime widths.
-template <typename T, int NT, int RG, int CSUB, int G, int WAVES, int CW>
+template <typename T, int NT, int RG, int CSUB, int G, int WAVES, int CW, int KQ = 8>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(WAVES))) void
 conv_os_lds_kernel(const T *__restrict__ x, int64_t n_x, const T *__restrict__ wt, int ncols,
                    const float *__restrict__ bias, const int32_t *__restrict__ nbr,
@@ -447,11 +447,13 @@ conv_os_lds_kernel(const T *__restrict__ x, int64_t n_x, const T *__restrict__ w
   constexpr int NB = NT / 16;
   constexpr int NV = NT * (CCH / VE);    // 16-byte pieces per staged chunk
   constexpr int NPT = (NV + kThreads - 1) / kThreads;
-  constexpr int KQ = 8;                  // index slots of four offsets (K <= 32)
+  // KQ: index slots of four offsets (K <= 4 KQ); MW: 32-bit mask words
+  static_assert(KQ % 8 == 0, "index slots come in groups of eight");
+  constexpr int MW = KQ / 8;
 
   __shared__ __align__(16) T sB[G][NT * LDW];
   __shared__ int32_t sK[kWaves][RG][KQ][kWave];
-  __shared__ uint32_t smask[kWaves * RG];
+  __shared__ uint32_t smask[kWaves * RG][MW];
 
   const int lane = threadIdx.x & (kWave - 1);
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
@@ -464,39 +466,60 @@ conv_os_lds_kernel(const T *__restrict__ x, int64_t n_x, const T *__restrict__ w
 
   // Neighbour indices of the wave's row groups to LDS (absent or past the
   // end: -1) and the offsets with any neighbour in each group.
-  uint32_t wmask = 0;
+  uint32_t wmask[MW] = {};
 #pragma unroll
   for (int r = 0; r < RG; ++r) {
     const int64_t pos = tile0 + (wv * RG + r) * 16 + i16;
     const bool in = pos < n_rows;
     const int64_t pc = in ? pos : n_rows - 1;
-    int32_t v[KQ];
 #pragma unroll
-    for (int q = 0; q < KQ; ++q) {
-      const int k = 4 * q + g;
-      // a mask, not a select of the load: the loads issue back to back
-      v[q] = nbr[(k < K ? k : K - 1) * n_rows + pc] | ((in && k < K) ? 0 : -1);
+    for (int mw = 0; mw < MW; ++mw) { // eight slots (32 offsets) at a time
+      int32_t v[8];
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        const int k = 32 * mw + 4 * q + g;
+        // a mask, not a select of the load: the loads issue back to back
+        v[q] = nbr[(k < K ? k : K - 1) * n_rows + pc] | ((in && k < K) ? 0 : -1);
+      }
+      uint32_t w = 0;
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        sK[wv][r][8 * mw + q][lane] = v[q];
+        const uint64_t bal = __ballot(v[q] >= 0);
+#pragma unroll
+        for (int gg = 0; gg < 4; ++gg)
+          w |= (((bal >> (16 * gg)) & 0xffffull) != 0 ? 1u : 0u) << (4 * q + gg);
+      }
+      w = __builtin_amdgcn_readfirstlane(w);
+      wmask[mw] |= w;
+      if (lane == 0)
+        smask[wv * RG + r][mw] = w;
     }
-    uint32_t w = 0;
-#pragma unroll
-    for (int q = 0; q < KQ; ++q) {
-      sK[wv][r][q][lane] = v[q];
-      const uint64_t bal = __ballot(v[q] >= 0);
-#pragma unroll
-      for (int gg = 0; gg < 4; ++gg)
-        w |= (((bal >> (16 * gg)) & 0xffffull) != 0 ? 1u : 0u) << (4 * q + gg);
-    }
-    w = __builtin_amdgcn_readfirstlane(w);
-    wmask |= w;
-    if (lane == 0)
-      smask[wv * RG + r] = w;
   }
   __syncthreads();
-  uint32_t m = 0; // the workgroup's offsets, walked in ascending order
+  uint32_t m[MW] = {}; // the workgroup's offsets, walked in ascending order
 #pragma unroll
-  for (int i = 0; i < kWaves * RG; ++i)
-    m |= smask[i];
-  m = __builtin_amdgcn_readfirstlane(m);
+  for (int mw = 0; mw < MW; ++mw) {
+#pragma unroll
+    for (int i = 0; i < kWaves * RG; ++i)
+      m[mw] |= smask[i][mw];
+    m[mw] = __builtin_amdgcn_readfirstlane(m[mw]);
+  }
+  auto any_left = [&]() {
+    uint32_t o = 0;
+#pragma unroll
+    for (int mw = 0; mw < MW; ++mw)
+      o |= m[mw];
+    return o != 0;
+  };
+  auto lowest = [&]() { // the smallest offset left (some word is non-zero)
+    int k = 0;
+#pragma unroll
+    for (int mw = MW - 1; mw >= 0; --mw)
+      if (m[mw])
+        k = 32 * mw + __builtin_ctz(m[mw]);
+    return k;
+  };
 
   v4f acc[RG][NB];
 #pragma unroll
@@ -512,19 +535,19 @@ conv_os_lds_kernel(const T *__restrict__ x, int64_t n_x, const T *__restrict__ w
   const __amdgpu_buffer_rsrc_t rx = buf_rsrc(x, n_x * CW * static_cast<int64_t>(sizeof(T)));
   const uint32_t lane_byte = static_cast<uint32_t>((lane & 3) * EPL * sizeof(T));
   int cc = 0; // channel chunk of the next stage
-  while (m) {
+  while (any_left()) {
     // G stages: (offset, chunk) in order; past the last one a stage repeats
     // the previous one with every load out of range and no multiply
     int kj[G], ccj[G];
     bool live[G];
 #pragma unroll
     for (int j = 0; j < G; ++j) {
-      live[j] = m != 0;
-      kj[j] = live[j] ? __builtin_ctz(m) : kj[j > 0 ? j - 1 : 0];
+      live[j] = any_left();
+      kj[j] = live[j] ? lowest() : kj[j > 0 ? j - 1 : 0];
       ccj[j] = cc;
       if (live[j] && ++cc == NCH) {
         cc = 0;
-        m &= m - 1;
+        m[kj[j] >> 5] &= m[kj[j] >> 5] - 1; // kj is that word's lowest bit
       }
     }
     uint32_t off[G][RG];
@@ -570,7 +593,7 @@ conv_os_lds_kernel(const T *__restrict__ x, int64_t n_x, const T *__restrict__ w
     __syncthreads(); // the group's weights are staged
 #pragma unroll
     for (int j = 0; j < G; ++j) {
-      if (live[j] && ((wmask >> kj[j]) & 1u)) { // uniform
+      if (live[j] && ((wmask[kj[j] >> 5] >> (kj[j] & 31)) & 1u)) { // uniform
 #pragma unroll
         for (int sub = 0; sub < CSUB; ++sub) {
           Frag at[RG];
@@ -2091,7 +2114,7 @@ static size_t os_partial_floats(int64_t n_rows, int cred, int ncols, int K) {
 
 // conv_os_lds_kernel launches: the reduction width as one, two or four
 // chunks; false where it is none of these.
-template <typename T, int NT, int RG, int CSUB, int G, int WAVES>
+template <typename T, int NT, int RG, int CSUB, int G, int WAVES, int KQ>
 static bool launch_os_lds(const T *x, int64_t n_x, int cred, const T *wt, int ncols,
                           const float *bias, const int32_t *nbr, int64_t n_rows, int K,
                           const int32_t *order, T *y, hipStream_t s) {
@@ -2099,13 +2122,13 @@ static bool launch_os_lds(const T *x, int64_t n_x, int cred, const T *wt, int nc
   constexpr int ROWS = kWaves * RG * 16;
   const dim3 grid(static_cast<unsigned>(xcd_grid(ceil_div(n_rows, ROWS))), ncols / NT);
   if (cred == CCH)
-    hipLaunchKernelGGL((conv_os_lds_kernel<T, NT, RG, CSUB, G, WAVES, CCH>), grid, dim3(kThreads),
+    hipLaunchKernelGGL((conv_os_lds_kernel<T, NT, RG, CSUB, G, WAVES, CCH, KQ>), grid, dim3(kThreads),
                        0, s, x, n_x, wt, ncols, bias, nbr, n_rows, K, order, y);
   else if (cred == 2 * CCH)
-    hipLaunchKernelGGL((conv_os_lds_kernel<T, NT, RG, CSUB, G, WAVES, 2 * CCH>), grid,
+    hipLaunchKernelGGL((conv_os_lds_kernel<T, NT, RG, CSUB, G, WAVES, 2 * CCH, KQ>), grid,
                        dim3(kThreads), 0, s, x, n_x, wt, ncols, bias, nbr, n_rows, K, order, y);
   else if (cred == 4 * CCH)
-    hipLaunchKernelGGL((conv_os_lds_kernel<T, NT, RG, CSUB, G, WAVES, 4 * CCH>), grid,
+    hipLaunchKernelGGL((conv_os_lds_kernel<T, NT, RG, CSUB, G, WAVES, 4 * CCH, KQ>), grid,
                        dim3(kThreads), 0, s, x, n_x, wt, ncols, bias, nbr, n_rows, K, order, y);
   else
     return false;
@@ -2117,36 +2140,52 @@ static bool launch_os_lds(const T *x, int64_t n_x, int cred, const T *wt, int nc
 // barrier (6 waves per SIMD; config 2 forward 76 us against 78 with two
 // stages per barrier and 80 with three row groups); the other shapes keep
 // conv_os_kernel's.
-template <typename T, int NT, int CSUB>
+template <typename T, int NT, int CSUB, int KQ>
 static bool os_lds_shape(const T *x, int64_t n_x, int cred, const T *wt, int ncols,
                          const float *bias, const int32_t *nbr, int64_t n_rows, int K,
                          const int32_t *order, T *y, hipStream_t s) {
   if constexpr (kIsF32<T>) {
-    return launch_os_lds<T, NT, 1, CSUB, 1, NT == 64 ? 6 : 8>(x, n_x, cred, wt, ncols, bias, nbr,
-                                                              n_rows, K, order, y, s);
+    return launch_os_lds<T, NT, 1, CSUB, 1, NT == 64 ? 6 : 8, KQ>(x, n_x, cred, wt, ncols, bias,
+                                                                  nbr, n_rows, K, order, y, s);
   } else if constexpr (NT == 64 && CSUB == 2) {
-    return launch_os_lds<T, NT, 2, CSUB, 1, 6>(x, n_x, cred, wt, ncols, bias, nbr, n_rows, K,
-                                               order, y, s);
+    return launch_os_lds<T, NT, 2, CSUB, 1, 6, KQ>(x, n_x, cred, wt, ncols, bias, nbr, n_rows, K,
+                                                   order, y, s);
   } else {
     constexpr int W = NT >= 128 ? 4 : (CSUB == 1 && NT >= 64 ? 6 : 8);
     constexpr int G = NT >= 128 ? 2 : (CSUB == 1 ? 4 : 1);
-    return launch_os_lds<T, NT, 1, CSUB, G, W>(x, n_x, cred, wt, ncols, bias, nbr, n_rows, K,
-                                               order, y, s);
+    return launch_os_lds<T, NT, 1, CSUB, G, W, KQ>(x, n_x, cred, wt, ncols, bias, nbr, n_rows, K,
+                                                   order, y, s);
   }
 }
 
-template <typename T, int NT>
+template <typename T, int NT, int KQ>
 static bool os_lds_csub(const T *x, int64_t n_x, int cred, const T *wt, int ncols,
                         const float *bias, const int32_t *nbr, int64_t n_rows, int K,
                         const int32_t *order, T *y, hipStream_t s) {
   constexpr int CH = kChOf<T>;
   if constexpr (kIsF32<T>) {
     if (cred % (4 * CH) == 0)
-      return os_lds_shape<T, NT, 4>(x, n_x, cred, wt, ncols, bias, nbr, n_rows, K, order, y, s);
+      return os_lds_shape<T, NT, 4, KQ>(x, n_x, cred, wt, ncols, bias, nbr, n_rows, K, order, y, s);
   }
   if (cred % (2 * CH) == 0)
-    return os_lds_shape<T, NT, 2>(x, n_x, cred, wt, ncols, bias, nbr, n_rows, K, order, y, s);
-  return os_lds_shape<T, NT, 1>(x, n_x, cred, wt, ncols, bias, nbr, n_rows, K, order, y, s);
+    return os_lds_shape<T, NT, 2, KQ>(x, n_x, cred, wt, ncols, bias, nbr, n_rows, K, order, y, s);
+  return os_lds_shape<T, NT, 1, KQ>(x, n_x, cred, wt, ncols, bias, nbr, n_rows, K, order, y, s);
+}
+
+template <typename T, int KQ>
+static bool run_os_lds_nt(const T *x, int64_t n_x, int cred, const T *wt, int ncols,
+                          const float *bias, const int32_t *nbr, int64_t n_rows, int K,
+                          const int32_t *order, T *y, hipStream_t s) {
+  const int nt = os_nt<T>(ncols);
+  if constexpr (!kIsF32<T>) {
+    if (nt == 128)
+      return os_lds_csub<T, 128, KQ>(x, n_x, cred, wt, ncols, bias, nbr, n_rows, K, order, y, s);
+  }
+  if (nt == 64)
+    return os_lds_csub<T, 64, KQ>(x, n_x, cred, wt, ncols, bias, nbr, n_rows, K, order, y, s);
+  if (nt == 32)
+    return os_lds_csub<T, 32, KQ>(x, n_x, cred, wt, ncols, bias, nbr, n_rows, K, order, y, s);
+  return os_lds_csub<T, 16, KQ>(x, n_x, cred, wt, ncols, bias, nbr, n_rows, K, order, y, s);
 }
 
 // The fast forward/dX kernel where it applies: at most 32 offsets, no split,
@@ -2156,19 +2195,12 @@ template <typename T>
 static bool run_os_lds(const T *x, int64_t n_x, int cred, const T *wt, int credw, int ncols,
                        const float *bias, const int32_t *nbr, int64_t n_rows, int K,
                        const int32_t *order, T *y, hipStream_t s) {
-  if (K > 32 || cred != credw || n_x < 1 || !os_fast(x, cred, wt, credw, ncols, K) ||
+  if (K > 96 || cred != credw || n_x < 1 || !os_fast(x, cred, wt, credw, ncols, K) ||
       n_x * cred * static_cast<int64_t>(sizeof(T)) > kBufMaxBytes)
     return false;
-  const int nt = os_nt<T>(ncols);
-  if constexpr (!kIsF32<T>) {
-    if (nt == 128)
-      return os_lds_csub<T, 128>(x, n_x, cred, wt, ncols, bias, nbr, n_rows, K, order, y, s);
-  }
-  if (nt == 64)
-    return os_lds_csub<T, 64>(x, n_x, cred, wt, ncols, bias, nbr, n_rows, K, order, y, s);
-  if (nt == 32)
-    return os_lds_csub<T, 32>(x, n_x, cred, wt, ncols, bias, nbr, n_rows, K, order, y, s);
-  return os_lds_csub<T, 16>(x, n_x, cred, wt, ncols, bias, nbr, n_rows, K, order, y, s);
+  if (K > 32)
+    return run_os_lds_nt<T, 24>(x, n_x, cred, wt, ncols, bias, nbr, n_rows, K, order, y, s);
+  return run_os_lds_nt<T, 8>(x, n_x, cred, wt, ncols, bias, nbr, n_rows, K, order, y, s);
 }
 
 // Shape of the resident-weight kernel (conv_fr_kernel) for a bf16 map: the

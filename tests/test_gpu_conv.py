@@ -64,33 +64,35 @@ def test_conv_3x3x3_matches_oracle(cin, cout, dtype):
     _run_and_check(km, cin, cout, dtype, seed=cin * 7 + cout, tag="3^3")
 
 
+@pytest.mark.parametrize("extra", [6, 70])
 @pytest.mark.parametrize("cin,cout,dtype", [
     (64, 64, torch.float32), (32, 32, torch.float32), (64, 64, torch.bfloat16),
     (128, 128, torch.bfloat16), (32, 64, torch.bfloat16)])
-def test_fast_forward_kernel_equals_general_kernel(cin, cout, dtype):
+def test_fast_forward_kernel_equals_general_kernel(cin, cout, dtype, extra):
     """Stencils of at most 32 offsets run on the LDS-indexed forward/dX
-    kernel, larger ones on the general kernel; both add a row's active
-    offsets in ascending order. The 3^3 map and the same map with six more
-    offsets that pair nothing (K = 33) must give bit-identical forward and
-    dX (the extra weights are never read). The cloud is large enough that
-    neither splits its offset axis over workgroups (a split changes the
-    order of the sums)."""
+    kernel with one mask word, those of 33 to 96 on it with three, larger
+    ones on the general kernel; all add a row's active offsets in ascending
+    order. The 3^3 map and the same map with 6 (K = 33) or 70 (K = 97) more
+    offsets that pair nothing must give bit-identical forward and dX (the
+    extra weights are never read). The cloud is large enough that no kernel
+    splits its offset axis over workgroups (a split changes the order of the
+    sums)."""
     rng = np.random.default_rng(cin * 3 + cout)
     c, _, _ = oracle.insert_and_map(random_coords(rng, 60000, 3, 30))
     off = oracle.region_offsets(3, 3)
-    far = np.array([[200 + i, 200, 200] for i in range(6)], np.int32)  # beyond the span
+    far = np.array([[200 + i, 200, 200] for i in range(extra)], np.int32)  # beyond the span
     tin = abi.hash_build(to_dev(c))
     km27 = abi.kernel_map(tin, tin, to_dev(off))
-    km33 = abi.kernel_map(tin, tin, to_dev(np.concatenate([off, far])))
-    assert km33.K == 33 and km33.n_pairs == km27.n_pairs
+    kmx = abi.kernel_map(tin, tin, to_dev(np.concatenate([off, far])))
+    assert kmx.K == 27 + extra and kmx.n_pairs == km27.n_pairs
     x = to_dev(rng.standard_normal((km27.n_in, cin)).astype(np.float32), dtype)
     gy = to_dev(rng.standard_normal((km27.n_out, cout)).astype(np.float32), dtype)
-    w = rng.standard_normal((33, cin, cout)).astype(np.float32) / np.sqrt(cin * 27)
-    w27, w33 = to_dev(w[:27], dtype), to_dev(w, dtype)
-    print(f"fast vs general kernel cin={cin} cout={cout} {dtype}", flush=True)
-    assert torch.equal(abi.conv_forward(x, w27, km27), abi.conv_forward(x, w33, km33))
+    w = rng.standard_normal((27 + extra, cin, cout)).astype(np.float32) / np.sqrt(cin * 27)
+    w27, wx = to_dev(w[:27], dtype), to_dev(w, dtype)
+    print(f"fast vs K={27 + extra} kernel cin={cin} cout={cout} {dtype}", flush=True)
+    assert torch.equal(abi.conv_forward(x, w27, km27), abi.conv_forward(x, wx, kmx))
     assert torch.equal(abi.conv_backward_input(gy, w27, km27),
-                       abi.conv_backward_input(gy, w33, km33))
+                       abi.conv_backward_input(gy, wx, kmx))
 
 
 def test_conv_bias_fp32():
