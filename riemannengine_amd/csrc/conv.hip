@@ -2213,7 +2213,9 @@ static bool run_os_lds(const T *x, int64_t n_x, int cred, const T *wt, int credw
 // conv_os_kernel save; measured on MI355X (quad-order gathers both):
 // config-5 stage 1 (808k rows, C32->32, 27 offsets) 105 us against 133, its
 // 2^3 downsample (C32->64) 28 against 33; config 2 (C64, two slices) 117
-// against 104; config 3's maps (40k-85k rows) 19-20 against 16-19.
+// against 104; config 3's maps (40k-85k rows) 19-20 against 16-19. Where the
+// LDS-indexed kernel applies it is faster still, so run_os tries that first
+// and this kernel serves the maps it does not take.
 constexpr int kCus = 256;
 constexpr int kFrLdsBytes = 160 * 1024;
 constexpr int kFrMaxSlices = 1;
@@ -2317,16 +2319,18 @@ static void run_os(const T *x, int64_t n_x, int cred, const T *wt, int credw, in
                    bool resident = true) {
   if (n_rows == 0)
     return;
-  if constexpr (!kIsF32<T>) {
-    if (resident && cred == credw &&
-        run_fr(x, n_x, cred, wt, ncols, bias, nbr, n_rows, K, order, y, s))
-      return;
-  }
+  // the LDS-indexed kernel first: it now beats the resident-weight kernel on
+  // the maps that took that one (config 5 step 6.01 -> 5.86 ms)
   const int splits = partial ? os_splits<T>(n_rows, credw, ncols, K) : 1;
   if (splits == 1 &&
       run_os_lds(x, n_x, cred, wt, credw, ncols, bias, nbr, n_rows, K, order, y, s)) {
     RHIP_LAUNCH_CHECK();
     return;
+  }
+  if constexpr (!kIsF32<T>) {
+    if (resident && cred == credw &&
+        run_fr(x, n_x, cred, wt, ncols, bias, nbr, n_rows, K, order, y, s))
+      return;
   }
   if (!os_fast(x, cred, wt, credw, ncols, K)) {
     hipLaunchKernelGGL((conv_os_generic_kernel<T>), dim3(ceil_div(n_rows * ncols, kThreads)),
