@@ -431,12 +431,15 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(WAVES)
 //  * a missing neighbour is an out-of-range buffer offset, which loads
 //    zeros, so nothing is masked after the loads.
 // Measured on MI355X, config 2 bf16 forward (quad-order gathers both): 76 us
-// against 108 for conv_os_kernel with runtime widths.
-template <typename T, int NT, int RG, int CSUB, int G, int WAVES, int CW, int KQ = 8>
+// against 108 for conv_os_kernel with runtime widths. SPLIT: gridDim.z
+// workgroups share a tile's (offset, chunk) stages and write fp32 partial
+// sums (config 5 step 5.87 -> 5.73 ms against conv_os_kernel's split).
+template <typename T, int NT, int RG, int CSUB, int G, int WAVES, int CW, int KQ, bool SPLIT>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(WAVES))) void
 conv_os_lds_kernel(const T *__restrict__ x, int64_t n_x, const T *__restrict__ wt, int ncols,
                    const float *__restrict__ bias, const int32_t *__restrict__ nbr,
-                   int64_t n_rows, int K, const int32_t *__restrict__ order, T *__restrict__ y) {
+                   int64_t n_rows, int K, const int32_t *__restrict__ order, T *__restrict__ y,
+                   float *__restrict__ partial) {
   using M = Mfma<T>;
   using Frag = typename M::Frag;
   constexpr int CH = M::kCh;
@@ -508,13 +511,6 @@ conv_os_lds_kernel(const T *__restrict__ x, int64_t n_x, const T *__restrict__ w
       m[mw] |= smask[i][mw];
     m[mw] = __builtin_amdgcn_readfirstlane(m[mw]);
   }
-  auto any_left = [&]() {
-    uint32_t o = 0;
-#pragma unroll
-    for (int mw = 0; mw < MW; ++mw)
-      o |= m[mw];
-    return o != 0;
-  };
   auto lowest = [&]() { // the smallest offset left (some word is non-zero)
     int k = 0;
 #pragma unroll
@@ -538,19 +534,48 @@ conv_os_lds_kernel(const T *__restrict__ x, int64_t n_x, const T *__restrict__ w
   const __amdgpu_buffer_rsrc_t rx = buf_rsrc(x, n_x * CW * static_cast<int64_t>(sizeof(T)));
   const uint32_t lane_byte = static_cast<uint32_t>((lane & 3) * EPL * sizeof(T));
   int cc = 0; // channel chunk of the next stage
-  while (any_left()) {
+  auto advance = [&](int k) {
+    if (++cc == NCH) {
+      cc = 0;
+      m[k >> 5] &= m[k >> 5] - 1; // k is that word's lowest bit
+    }
+  };
+  // split z of gridDim.z takes an equal share of the (offset, chunk) stages
+  // and writes fp32 partial sums (reduced by conv_os_reduce_kernel)
+  int left = 0;
+  if constexpr (SPLIT) {
+#pragma unroll
+    for (int mw = 0; mw < MW; ++mw)
+      left += __builtin_popcount(m[mw]) * NCH;
+    const int s_begin = static_cast<int>(static_cast<int64_t>(left) * blockIdx.z / gridDim.z);
+    const int s_end = static_cast<int>(static_cast<int64_t>(left) * (blockIdx.z + 1) / gridDim.z);
+    for (int i = 0; i < s_begin; ++i)
+      advance(lowest());
+    left = s_end - s_begin;
+  }
+  auto more = [&]() {
+    if constexpr (SPLIT)
+      return left > 0;
+    uint32_t o = 0;
+#pragma unroll
+    for (int mw = 0; mw < MW; ++mw)
+      o |= m[mw];
+    return o != 0;
+  };
+  while (more()) {
     // G stages: (offset, chunk) in order; past the last one a stage repeats
     // the previous one with every load out of range and no multiply
     int kj[G], ccj[G];
     bool live[G];
 #pragma unroll
     for (int j = 0; j < G; ++j) {
-      live[j] = any_left();
+      live[j] = more();
       kj[j] = live[j] ? lowest() : kj[j > 0 ? j - 1 : 0];
       ccj[j] = cc;
-      if (live[j] && ++cc == NCH) {
-        cc = 0;
-        m[kj[j] >> 5] &= m[kj[j] >> 5] - 1; // kj is that word's lowest bit
+      if (live[j]) {
+        advance(kj[j]);
+        if constexpr (SPLIT)
+          --left;
       }
     }
     uint32_t off[G][RG];
@@ -617,6 +642,21 @@ conv_os_lds_kernel(const T *__restrict__ x, int64_t n_x, const T *__restrict__ w
     __syncthreads(); // every wave is done reading the group's weights
   }
 
+  if constexpr (SPLIT) { // [split][position][column]
+#pragma unroll
+    for (int r = 0; r < RG; ++r)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int64_t pos = tile0 + (wv * RG + r) * 16 + 4 * g + e;
+        if (pos < n_rows) {
+          float *dst = partial + (blockIdx.z * n_rows + pos) * ncols + col0 + i16;
+#pragma unroll
+          for (int nb = 0; nb < NB; ++nb)
+            dst[nb * 16] = acc[r][nb][e];
+        }
+      }
+    return;
+  }
 #pragma unroll
   for (int r = 0; r < RG; ++r) {
 #pragma unroll
@@ -2115,26 +2155,55 @@ static size_t os_partial_floats(int64_t n_rows, int cred, int ncols, int K) {
   return sp > 1 ? static_cast<size_t>(sp) * n_rows * ncols : 0;
 }
 
+// One conv_os_lds_kernel launch; the split form is built for bf16 only (fp32
+// splits stay on conv_os_kernel).
+template <typename T, int NT, int RG, int CSUB, int G, int WAVES, int CW, int KQ>
+static void launch_os_lds_cw(dim3 grid, bool split, const T *x, int64_t n_x, const T *wt,
+                             int ncols, const float *bias, const int32_t *nbr, int64_t n_rows,
+                             int K, const int32_t *order, T *y, float *partial, hipStream_t s) {
+  if constexpr (!kIsF32<T>) {
+    if (split) {
+      hipLaunchKernelGGL((conv_os_lds_kernel<T, NT, RG, CSUB, G, WAVES, CW, KQ, true>), grid,
+                         dim3(kThreads), 0, s, x, n_x, wt, ncols, bias, nbr, n_rows, K, order, y,
+                         partial);
+      return;
+    }
+  }
+  hipLaunchKernelGGL((conv_os_lds_kernel<T, NT, RG, CSUB, G, WAVES, CW, KQ, false>), grid,
+                     dim3(kThreads), 0, s, x, n_x, wt, ncols, bias, nbr, n_rows, K, order, y,
+                     nullptr);
+}
+
 // conv_os_lds_kernel launches: the reduction width as one, two or four
-// chunks; false where it is none of these.
+// chunks; false where it is none of these (or an fp32 split).
 template <typename T, int NT, int RG, int CSUB, int G, int WAVES, int KQ>
 static bool launch_os_lds(const T *x, int64_t n_x, int cred, const T *wt, int ncols,
                           const float *bias, const int32_t *nbr, int64_t n_rows, int K,
-                          const int32_t *order, T *y, hipStream_t s) {
+                          const int32_t *order, T *y, int splits, float *partial,
+                          hipStream_t s) {
   constexpr int CCH = CSUB * kChOf<T>;
   constexpr int ROWS = kWaves * RG * 16;
-  const dim3 grid(static_cast<unsigned>(xcd_grid(ceil_div(n_rows, ROWS))), ncols / NT);
+  const bool sp = splits > 1;
+  if (kIsF32<T> && sp)
+    return false;
+  const dim3 grid(static_cast<unsigned>(xcd_grid(ceil_div(n_rows, ROWS))), ncols / NT, splits);
   if (cred == CCH)
-    hipLaunchKernelGGL((conv_os_lds_kernel<T, NT, RG, CSUB, G, WAVES, CCH, KQ>), grid, dim3(kThreads),
-                       0, s, x, n_x, wt, ncols, bias, nbr, n_rows, K, order, y);
+    launch_os_lds_cw<T, NT, RG, CSUB, G, WAVES, CCH, KQ>(grid, sp, x, n_x, wt, ncols, bias, nbr,
+                                                         n_rows, K, order, y, partial, s);
   else if (cred == 2 * CCH)
-    hipLaunchKernelGGL((conv_os_lds_kernel<T, NT, RG, CSUB, G, WAVES, 2 * CCH, KQ>), grid,
-                       dim3(kThreads), 0, s, x, n_x, wt, ncols, bias, nbr, n_rows, K, order, y);
+    launch_os_lds_cw<T, NT, RG, CSUB, G, WAVES, 2 * CCH, KQ>(grid, sp, x, n_x, wt, ncols, bias,
+                                                             nbr, n_rows, K, order, y, partial, s);
   else if (cred == 4 * CCH)
-    hipLaunchKernelGGL((conv_os_lds_kernel<T, NT, RG, CSUB, G, WAVES, 4 * CCH, KQ>), grid,
-                       dim3(kThreads), 0, s, x, n_x, wt, ncols, bias, nbr, n_rows, K, order, y);
+    launch_os_lds_cw<T, NT, RG, CSUB, G, WAVES, 4 * CCH, KQ>(grid, sp, x, n_x, wt, ncols, bias,
+                                                             nbr, n_rows, K, order, y, partial, s);
   else
     return false;
+  if (splits > 1) {
+    RHIP_LAUNCH_CHECK();
+    hipLaunchKernelGGL((conv_os_reduce_kernel<T>),
+                       dim3(static_cast<unsigned>(ceil_div(n_rows * (ncols / 4), kThreads))),
+                       dim3(kThreads), 0, s, partial, splits, n_rows, ncols, bias, order, y);
+  }
   return true;
 }
 
@@ -2146,49 +2215,59 @@ static bool launch_os_lds(const T *x, int64_t n_x, int cred, const T *wt, int nc
 template <typename T, int NT, int CSUB, int KQ>
 static bool os_lds_shape(const T *x, int64_t n_x, int cred, const T *wt, int ncols,
                          const float *bias, const int32_t *nbr, int64_t n_rows, int K,
-                         const int32_t *order, T *y, hipStream_t s) {
+                         const int32_t *order, T *y, int splits, float *partial, hipStream_t s) {
   if constexpr (kIsF32<T>) {
     return launch_os_lds<T, NT, 1, CSUB, 1, NT == 64 ? 6 : 8, KQ>(x, n_x, cred, wt, ncols, bias,
-                                                                  nbr, n_rows, K, order, y, s);
+                                                                  nbr, n_rows, K, order, y, splits,
+                                                                  partial, s);
   } else if constexpr (NT == 64 && CSUB == 2) {
     return launch_os_lds<T, NT, 2, CSUB, 1, 6, KQ>(x, n_x, cred, wt, ncols, bias, nbr, n_rows, K,
-                                                   order, y, s);
+                                                   order, y, splits, partial, s);
   } else {
     constexpr int W = NT >= 128 ? 4 : (CSUB == 1 && NT >= 64 ? 6 : 8);
     constexpr int G = NT >= 128 ? 2 : (CSUB == 1 ? 4 : 1);
     return launch_os_lds<T, NT, 1, CSUB, G, W, KQ>(x, n_x, cred, wt, ncols, bias, nbr, n_rows, K,
-                                                   order, y, s);
+                                                   order, y, splits, partial, s);
   }
 }
 
 template <typename T, int NT, int KQ>
 static bool os_lds_csub(const T *x, int64_t n_x, int cred, const T *wt, int ncols,
                         const float *bias, const int32_t *nbr, int64_t n_rows, int K,
-                        const int32_t *order, T *y, hipStream_t s) {
+                        const int32_t *order, T *y, int splits, float *partial,
+                        hipStream_t s) {
   constexpr int CH = kChOf<T>;
   if constexpr (kIsF32<T>) {
     if (cred % (4 * CH) == 0)
-      return os_lds_shape<T, NT, 4, KQ>(x, n_x, cred, wt, ncols, bias, nbr, n_rows, K, order, y, s);
+      return os_lds_shape<T, NT, 4, KQ>(x, n_x, cred, wt, ncols, bias, nbr, n_rows, K, order, y,
+                                        splits, partial, s);
   }
   if (cred % (2 * CH) == 0)
-    return os_lds_shape<T, NT, 2, KQ>(x, n_x, cred, wt, ncols, bias, nbr, n_rows, K, order, y, s);
-  return os_lds_shape<T, NT, 1, KQ>(x, n_x, cred, wt, ncols, bias, nbr, n_rows, K, order, y, s);
+    return os_lds_shape<T, NT, 2, KQ>(x, n_x, cred, wt, ncols, bias, nbr, n_rows, K, order, y,
+                                        splits, partial, s);
+  return os_lds_shape<T, NT, 1, KQ>(x, n_x, cred, wt, ncols, bias, nbr, n_rows, K, order, y,
+                                        splits, partial, s);
 }
 
 template <typename T, int KQ>
 static bool run_os_lds_nt(const T *x, int64_t n_x, int cred, const T *wt, int ncols,
                           const float *bias, const int32_t *nbr, int64_t n_rows, int K,
-                          const int32_t *order, T *y, hipStream_t s) {
+                          const int32_t *order, T *y, int splits, float *partial,
+                          hipStream_t s) {
   const int nt = os_nt<T>(ncols);
   if constexpr (!kIsF32<T>) {
     if (nt == 128)
-      return os_lds_csub<T, 128, KQ>(x, n_x, cred, wt, ncols, bias, nbr, n_rows, K, order, y, s);
+      return os_lds_csub<T, 128, KQ>(x, n_x, cred, wt, ncols, bias, nbr, n_rows, K, order, y,
+                                      splits, partial, s);
   }
   if (nt == 64)
-    return os_lds_csub<T, 64, KQ>(x, n_x, cred, wt, ncols, bias, nbr, n_rows, K, order, y, s);
+    return os_lds_csub<T, 64, KQ>(x, n_x, cred, wt, ncols, bias, nbr, n_rows, K, order, y,
+                                      splits, partial, s);
   if (nt == 32)
-    return os_lds_csub<T, 32, KQ>(x, n_x, cred, wt, ncols, bias, nbr, n_rows, K, order, y, s);
-  return os_lds_csub<T, 16, KQ>(x, n_x, cred, wt, ncols, bias, nbr, n_rows, K, order, y, s);
+    return os_lds_csub<T, 32, KQ>(x, n_x, cred, wt, ncols, bias, nbr, n_rows, K, order, y,
+                                      splits, partial, s);
+  return os_lds_csub<T, 16, KQ>(x, n_x, cred, wt, ncols, bias, nbr, n_rows, K, order, y,
+                                      splits, partial, s);
 }
 
 // The fast forward/dX kernel where it applies: at most 96 offsets, no split,
@@ -2197,13 +2276,15 @@ static bool run_os_lds_nt(const T *x, int64_t n_x, int cred, const T *wt, int nc
 template <typename T>
 static bool run_os_lds(const T *x, int64_t n_x, int cred, const T *wt, int credw, int ncols,
                        const float *bias, const int32_t *nbr, int64_t n_rows, int K,
-                       const int32_t *order, T *y, hipStream_t s) {
+                       const int32_t *order, T *y, int splits, float *partial, hipStream_t s) {
   if (K > 96 || cred != credw || n_x < 1 || !os_fast(x, cred, wt, credw, ncols, K) ||
       n_x * cred * static_cast<int64_t>(sizeof(T)) > kBufMaxBytes)
     return false;
   if (K > 32)
-    return run_os_lds_nt<T, 24>(x, n_x, cred, wt, ncols, bias, nbr, n_rows, K, order, y, s);
-  return run_os_lds_nt<T, 8>(x, n_x, cred, wt, ncols, bias, nbr, n_rows, K, order, y, s);
+    return run_os_lds_nt<T, 24>(x, n_x, cred, wt, ncols, bias, nbr, n_rows, K, order, y, splits,
+                                 partial, s);
+  return run_os_lds_nt<T, 8>(x, n_x, cred, wt, ncols, bias, nbr, n_rows, K, order, y, splits,
+                               partial, s);
 }
 
 // Shape of the resident-weight kernel (conv_fr_kernel) for a bf16 map: the
@@ -2319,11 +2400,12 @@ static void run_os(const T *x, int64_t n_x, int cred, const T *wt, int credw, in
                    bool resident = true) {
   if (n_rows == 0)
     return;
-  // the LDS-indexed kernel first: it now beats the resident-weight kernel on
-  // the maps that took that one (config 5 step 6.01 -> 5.86 ms)
+  // the LDS-indexed kernel first: it beats the resident-weight kernel on the
+  // maps that took that one (config 5 step 6.01 -> 5.86 ms), and with an
+  // offset-axis split it takes the small coarse maps as well
   const int splits = partial ? os_splits<T>(n_rows, credw, ncols, K) : 1;
-  if (splits == 1 &&
-      run_os_lds(x, n_x, cred, wt, credw, ncols, bias, nbr, n_rows, K, order, y, s)) {
+  if (run_os_lds(x, n_x, cred, wt, credw, ncols, bias, nbr, n_rows, K, order, y, splits, partial,
+                 s)) {
     RHIP_LAUNCH_CHECK();
     return;
   }
