@@ -9,12 +9,16 @@
 // MI355X design:
 //  * Forward and dX are one output-stationary implicit GEMM over the dense
 //    neighbour table of the kernel map, whose rows come grouped by neighbour
-//    mask (so a 16-row group rarely multiplies a missing neighbour):
-//    conv_os_kernel stages each active offset's weight slice in LDS and
-//    gathers the rows straight into MFMA operands; conv_fr_kernel keeps every
-//    offset's weights for its columns resident in LDS for the whole launch
-//    (large maps whose weights fit). Each output row is written once: no
-//    atomics, no zero fill.
+//    mask (so a 16-row group rarely multiplies a missing neighbour). Each
+//    stage stages one active offset's weight slice in LDS and gathers the
+//    rows straight into MFMA operands. conv_os_lds_kernel (stencils of up to
+//    96 offsets) keeps its row groups' neighbour indices in LDS and walks the
+//    workgroup's offsets as a bit mask; conv_os_kernel is the general form
+//    (larger stencils, fp32 offset splits, padded 16-channel bf16 layers);
+//    conv_fr_kernel keeps every offset's weights for its columns resident in
+//    LDS (bf16 maps the first does not take whose weights fit). Without an
+//    offset split each output row is written once: no atomics, no zero
+//    fill; with one, fp32 partial sums are added in split order.
 //  * Gathered rows are loaded in quad order (four consecutive lanes read 64
 //    contiguous bytes of one row, one L1 access) and moved to the MFMA layout
 //    with ds_bpermute.
