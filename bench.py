@@ -10,7 +10,8 @@ cached by the coordinate manager). Inputs are resident in HBM before the
 timed region starts.
 
 Printed as ONE JSON line:
-  value        whole-job Mvoxels/s = N_in / (t_fwd + t_dX + t_dW) / 1e6
+  value        whole-job Mvoxels/s = N_in / (host-clock time per timed step,
+               forward + dX + dW) / 1e6
   kernel_map_ms  hash build + locality order + kernel map, from device coords,
                through the C++ CoordinateManager (insert_and_map + kernel_map)
   kernel_map_roofline  the map build's algorithmic bytes (hash: rows read, slot
