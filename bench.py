@@ -74,6 +74,8 @@ def parse_args():
     ap.add_argument("--no-cpu-baseline", action="store_true",
                     help="skip the CPU oracle timing (profiling runs)")
     ap.add_argument("--map-reps", type=int, default=5)
+    ap.add_argument("--no-other-configs", action="store_true",
+                    help="the headline run without the compact records of configs 1, 3, 4, 5")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="calibration mode: time a plain device copy of this many MiB "
                          "(the reference kernel for scaling FETCH_SIZE/WRITE_SIZE) and exit")
@@ -290,16 +292,117 @@ def _map_time(build, reps):
     return out, statistics.median(ms[1:])
 
 
+def _roof(F, B, ms, dtype):
+    """(bound, achieved, peak, unit, frac, t_roof_ms) of one pass: bound by
+    whichever of the MFMA peak (the dtype's) and the HBM peak would take
+    longer on its algorithmic work."""
+    t_f = F / (PEAK_TFLOPS[dtype] * 1e12)
+    t_b = B / (PEAK_HBM_GBS * 1e9)
+    dur = ms * 1e-3
+    if t_f >= t_b:
+        rec = {"bound": "mfma", "achieved": round(F / dur / 1e12, 3), "peak": PEAK_TFLOPS[dtype],
+               "unit": "TFLOP/s"}
+    else:
+        rec = {"bound": "hbm", "achieved": round(B / dur / 1e9, 1), "peak": PEAK_HBM_GBS,
+               "unit": "GB/s"}
+    rec["frac"] = round(max(t_f, t_b) / dur, 4)
+    rec["ms"] = round(ms, 4)
+    return rec
+
+
+def _event_time(fn, reps=10, warm=3):
+    """Mean duration (ms) of fn() from HIP events on torch's current stream
+    (where the C ABI launches)."""
+    import torch
+    for _ in range(warm):
+        fn()
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(reps + 1)]
+    ev[0].record()
+    for i in range(reps):
+        fn()
+        ev[i + 1].record()
+    torch.cuda.synchronize()
+    return statistics.mean(ev[i].elapsed_time(ev[i + 1]) for i in range(reps))
+
+
+def config5_per_kernel(stage_in, stage_out, chans, dt, s, reps=10):
+    """Config 5's kernels one by one, at each stage's real shapes, through
+    the C ABI on maps built from the encoder's own coordinates: per stage,
+    the 3^3 conv (C->C; 4 per step: two BasicBlocks of two convs) forward,
+    dX and dW, the 2^3 stride-2 conv (C->C') forward, dX and dW (1 per
+    step), and batch norm forward (statistics + apply with ReLU) and
+    backward (4 each per step). Each entry: HIP-event mean over `reps`
+    launches and its roofline fraction (bytes of the section-3 table for
+    batch norm: statistics N C s, apply 2 N C s, backward sums 3 N C s and
+    apply 5 N C s with the residual)."""
+    import torch
+    from riemannengine_amd import abi, stencil
+    out = []
+    g = torch.Generator(device="cpu").manual_seed(5)
+    dev = stage_in[0].device
+    rnd = lambda *shape: torch.randn(shape, generator=g).to(dev, dt)
+    dname = "f32" if dt == torch.float32 else "bf16"
+    for i, (ci, co_) in enumerate(zip(stage_in, stage_out)):
+        C, Cn = chans[i], chans[min(i + 1, 3)]
+        ts = 2 ** i
+        ti = abi.hash_build(ci.contiguous())
+        tn = abi.hash_build(co_.contiguous())
+        k3 = abi.kernel_map(ti, ti, stencil.region_offsets(3, 3, 1, ts))
+        kd = abi.kernel_map(ti, tn, stencil.region_offsets(3, 2, 1, ts))
+        n, nn_ = k3.n_in, kd.n_out
+        for op, km, cin, cout, count in (("conv 3^3", k3, C, C, 4), ("conv 2^3 s2", kd, C, Cn, 1)):
+            x, gy = rnd(km.n_in, cin), rnd(km.n_out, cout)
+            w = rnd(km.K, cin, cout) * 0.05
+            work = conv_traffic(km.n_in, km.n_out, km.n_pairs, km.K, cin, cout, s)
+            for pname, fn in (("forward", lambda: abi.conv_forward(x, w, km)),
+                              ("backward_input", lambda: abi.conv_backward_input(gy, w, km)),
+                              ("backward_weight", lambda: abi.conv_weight_grad(x, gy, km, km.K))):
+                ms = _event_time(fn, reps)
+                F, B = work[pname]
+                rec = {"stage": i + 1, "op": f"{op} C{cin}->{cout}", "pass": pname,
+                       "rows_in": km.n_in, "rows_out": km.n_out, "pairs": km.n_pairs,
+                       "per_step": count}
+                rec.update(_roof(F, B, ms, dname))
+                out.append(rec)
+            del x, gy, w
+        x, r, gy = rnd(n, C), rnd(n, C), rnd(n, C)
+        gamma = torch.ones(C, device=dev)
+        beta = torch.zeros(C, device=dev)
+        st = {}
+
+        def bn_fwd():
+            st["m"], st["v"] = abi.bn_stats(x)
+            st["y"] = abi.bn_forward(x, st["m"], st["v"], gamma, beta, residual=r, relu=True)
+
+        bn_fwd()
+        for pname, fn, B in (
+                ("batch norm forward", bn_fwd, n * C * s * 4),
+                ("batch norm backward",
+                 lambda: abi.bn_backward(gy, st["y"], x, st["m"], st["v"], gamma, relu=True,
+                                         want_residual=True), n * C * s * 8)):
+            ms = _event_time(fn, reps)
+            rec = {"stage": i + 1, "op": f"batch norm C{C}", "pass": pname, "rows_in": n,
+                   "per_step": 4}
+            rec.update(_roof(0.0, float(B), ms, dname))
+            out.append(rec)
+        del x, r, gy, k3, kd, ti, tn
+    return out
+
+
 def run_other_config(args):
     """Configs 1, 3, 4 and 5 of the benchmark set, one JSON record each:
       1  sphere shell (N = 51,554), 3^3 C16->32, fwd+dX+dW (C ABI)
-      3  LiDAR batch 2: 2^3 stride-2 conv C64->128, then the 2^3 transposed
-         conv C128->64 back onto the input coordinates, fwd+bwd (C ABI)
+      3  LiDAR batch 2 (151,273 voxels): 2^3 stride-2 conv C64->128, then the
+         2^3 transposed conv C128->64 back onto the input coordinates,
+         fwd+bwd (C ABI)
       4  4-D moving shell (N = 232,528), 3^4 (81 offsets) C32->32 (C ABI)
       5  residual encoder on 8 indoor scenes: 4 stages of 2 BasicBlocks and a
          2^3 stride-2 conv, channels 32->64->128->256, fwd+bwd through the
          C++ host layer (autograd, batch norm, maps cached by the manager)
-    value = N_in / ms_per_step (Mvoxels/s) with the maps prebuilt."""
+    value = N_in / ms_per_step (Mvoxels/s) with the maps prebuilt; the step
+    roofline fraction divides the step's roofline time by the timed
+    ms_per_step; `passes` gives each pass's own roofline fraction from
+    event times (config 5: `per_kernel`, each kernel at each stage)."""
     import torch
     from riemannengine_amd import abi, scenes, stencil
 
@@ -315,7 +418,7 @@ def run_other_config(args):
     kaiming = lambda K, ci, co: rnd(K, ci, co) * (2.0 / (ci * K)) ** 0.5
     cfg = args.config
     extra = {}
-    flop = byts = 0.0
+    work = {}  # pass name -> (F, B)
 
     if cfg in (1, 4):
         if cfg == 1:
@@ -335,8 +438,7 @@ def run_other_config(args):
         passes = [("forward", lambda: abi.conv_forward(x, w, km)),
                   ("backward_input", lambda: abi.conv_backward_input(gy, w, km)),
                   ("backward_weight", lambda: abi.conv_weight_grad(x, gy, km, K))]
-        for F, B in conv_traffic(n_in, n_in, km.n_pairs, K, cin, cout, s).values():
-            flop, byts = flop + F, byts + B
+        work = conv_traffic(n_in, n_in, km.n_pairs, K, cin, cout, s)
         extra = {"n_voxels": n_in, "pairs": km.n_pairs, "offsets": K, "c_in": cin, "c_out": cout}
     elif cfg == 3:
         c_np = scenes.lidar_batch(2, 3)
@@ -360,9 +462,9 @@ def run_other_config(args):
                   ("up_backward_weight", lambda: abi.conv_weight_grad(y, gz, up, 8)),
                   ("down_backward_input", lambda: abi.conv_backward_input(gy, wd, down)),
                   ("down_backward_weight", lambda: abi.conv_weight_grad(x, gy, down, 8))]
-        for (ni, no, ci, co) in ((n_f, n_c, 64, 128), (n_c, n_f, 128, 64)):
-            for F, B in conv_traffic(ni, no, P, 8, ci, co, s).values():
-                flop, byts = flop + F, byts + B
+        for pre, (ni, no, ci, co) in (("down_", (n_f, n_c, 64, 128)), ("up_", (n_c, n_f, 128, 64))):
+            for name, fb in conv_traffic(ni, no, P, 8, ci, co, s).items():
+                work[pre + name] = fb
         n_in = n_f
         desc = ("config 3: LiDAR batch 2, 2^3 stride-2 conv C64->128 then 2^3 transposed conv "
                 "C128->64 onto the input coordinates, fwd+bwd")
@@ -384,11 +486,16 @@ def run_other_config(args):
         x0 = re_.SparseTensor(feats, coords)
         n_in = len(x0)
         state = {}
+        stage_in, stage_out = [], []
 
-        def forward():
+        def forward(record=False):
             h = x0
-            for m in mods:
+            for j, m in enumerate(mods):
+                if record and j % 3 == 0:
+                    stage_in.append(h.C)
                 h = m(h)
+                if record and j % 3 == 2:
+                    stage_out.append(h.C)
             state["out"] = h
 
         def backward():
@@ -398,7 +505,7 @@ def run_other_config(args):
 
         torch.cuda.synchronize()
         t0 = time.perf_counter()
-        forward()  # builds every stage's maps; the manager caches them
+        forward(record=True)  # builds every stage's maps; the manager caches them
         torch.cuda.synchronize()
         first_ms = (time.perf_counter() - t0) * 1e3
         backward()
@@ -410,7 +517,6 @@ def run_other_config(args):
                  "channels": chans, "first_forward_ms_incl_maps": round(first_ms, 2)}
 
     per, wall = _timed_passes(passes, args.steps, args.warmup)
-    step_ms = sum(per.values())
     line = {
         "metric": f"sparse conv fwd+bwd Mvoxels/s (config {cfg})",
         "value": round(n_in / (wall * 1e-3) / 1e6, 3),
@@ -421,13 +527,41 @@ def run_other_config(args):
         "config": dict({"workload": desc, "seed": args.seed, "accumulate": "f32"}, **extra),
         "kernel_map_ms": None if map_ms is None else round(map_ms, 3),
         "breakdown_ms": {k: round(v, 4) for k, v in per.items()},
+        "breakdown_source": "events around each pass in untimed steps after the timed ones",
     }
-    if flop:
+    if work:
+        flop = sum(v[0] for v in work.values())
+        byts = sum(v[1] for v in work.values())
         t_roof = max(flop / (PEAK_TFLOPS[args.dtype] * 1e12), byts / (PEAK_HBM_GBS * 1e9))
         line["step_roofline"] = {"t_roof_ms": round(t_roof * 1e3, 4),
-                                 "frac": round(t_roof * 1e3 / step_ms, 4),
+                                 "frac": round(t_roof * 1e3 / wall, 4),
+                                 "frac_source": "t_roof / timed ms_per_step",
                                  "flop": flop, "bytes": byts}
+        line["passes"] = {name: _roof(*work[name], per[name], args.dtype) for name in per}
+        dom = max(per, key=per.get)
+        line["roofline"] = dict(line["passes"][dom], **{"pass": dom})
+    else:  # config 5: each kernel at each stage
+        pk = config5_per_kernel(stage_in, stage_out, chans, dt, s)
+        t_roof = sum(r["frac"] * r["ms"] * r["per_step"] for r in pk)
+        t_sum = sum(r["ms"] * r["per_step"] for r in pk)
+        line["per_kernel"] = pk
+        line["step_roofline"] = {
+            "t_roof_ms": round(t_roof, 4), "frac": round(t_roof / wall, 4),
+            "frac_source": "sum over the per-kernel entries of (roofline time x launches per "
+                           "step) / timed ms_per_step",
+            "kernels_ms": round(t_sum, 4)}
+        dom = max(pk, key=lambda r: r["ms"] * r["per_step"])
+        line["roofline"] = dict(dom)
     return line
+
+
+def compact(line):
+    """The fields of a config's line that the headline line carries."""
+    keep = ("value", "unit", "dtype", "ms_per_step", "kernel_map_ms", "breakdown_ms",
+            "step_roofline", "roofline", "passes", "per_kernel")
+    out = {k: line[k] for k in keep if k in line}
+    out["config"] = line["config"]
+    return out
 
 
 def pool_traffic(kind, n_in, n_out, K, C, s, ncol=4, K_t=None):
@@ -548,7 +682,6 @@ def run_pool(args):
             "traffic_source": measured_traffic(args.dtype, dom, "traffic_pool.json")[1],
             "kernel": kernels[dom],
             "kernel_ms": round(per[dom], 4), "algorithmic": {"bytes": B[dom]}}
-    step_ms = sum(per.values())
     t_roof = sum(B.values()) / (PEAK_HBM_GBS * 1e9)
     line = {
         "metric": "sparse pooling fwd+bwd Mvoxels/s (max 2^3/2 + avg 3^3/2 + global avg, C64)",
@@ -565,7 +698,8 @@ def run_pool(args):
         "kernel_map_ms": round(map_ms, 3),
         "breakdown_ms": {k: round(v, 4) for k, v in per.items()},
         "step_roofline": {"t_roof_ms": round(t_roof * 1e3, 4),
-                          "frac": round(t_roof * 1e3 / step_ms, 4), "bytes": sum(B.values())},
+                          "frac": round(t_roof * 1e3 / wall, 4),
+                          "frac_source": "t_roof / timed ms_per_step", "bytes": sum(B.values())},
         "roofline": roof,
         "cpu_baseline": None if args.no_cpu_baseline else pool_cpu_baseline(coords_np, C,
                                                                             args.seed),
@@ -681,6 +815,18 @@ def main():
     }
     for dt_name in dtypes[1:]:
         line[dt_name] = records[dt_name]
+    if not args.dtype_given and not args.no_other_configs:
+        # the other configurations, each in its own dtype, as compact records
+        import copy
+        import torch
+        line["configs"] = {}
+        for cfg in (1, 3, 4, 5):
+            sub = copy.copy(args)
+            sub.config = cfg
+            sub.dtype = "bf16" if cfg in (3, 5) else "f32"
+            line["configs"][str(cfg)] = compact(run_other_config(sub))
+            gc.collect()
+            torch.cuda.empty_cache()
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(coords_np, offsets_np, cin, cout, args.seed,
                                             dtypes[0])
@@ -775,7 +921,6 @@ def conv_step_record(args, dtype, km, n_in, n_out, P, K, cin, cout):
     Ft = sum(v[0] for v in work.values())
     Bt = sum(v[1] for v in work.values())
     t_roof = max(Ft / (PEAK_TFLOPS[dtype] * 1e12), Bt / (PEAK_HBM_GBS * 1e9))
-    step_ms_events = sum(per.values())
     return {
         "value": round(n_in / (ms_per_step * 1e-3) / 1e6, 3),
         "unit": "Mvoxels/s",
@@ -784,7 +929,8 @@ def conv_step_record(args, dtype, km, n_in, n_out, P, K, cin, cout):
         "breakdown_ms": {n: round(per[n], 4) for n in names},
         "breakdown_source": "events around each pass in %d untimed steps after the timed ones" % nb,
         "step_roofline": {"t_roof_ms": round(t_roof * 1e3, 4),
-                          "frac": round(t_roof * 1e3 / step_ms_events, 4),
+                          "frac": round(t_roof * 1e3 / ms_per_step, 4),
+                          "frac_source": "t_roof / timed ms_per_step",
                           "flop": Ft, "bytes": Bt},
         "roofline": roof,
     }

@@ -426,14 +426,38 @@ def conv_forward_noalloc(x: torch.Tensor, weight: torch.Tensor, kmap: KernelMap,
                          out: Optional[torch.Tensor] = None) -> torch.Tensor:
     """The forward through rhip_conv_forward_noalloc (the library's own
     device scratch instead of a workspace). `out` may be given so that the
-    call itself allocates nothing."""
+    call itself allocates nothing.
+
+    Nothing is converted here (a conversion would allocate): x and weight
+    must be contiguous and of one dtype, bias (if any) a contiguous fp32
+    vector of cout values and out a contiguous [n_out, cout] tensor of x's
+    dtype, all on x's device; anything else raises ValueError before the
+    library is called."""
     _require_cuda(x, "x")
     dt = _dtype_code(x.dtype)
+    if weight.dim() != 3:
+        raise ValueError("weight must be [K, cin, cout]")
     K, cin, cout = weight.shape
-    if K != kmap.K or x.shape[1] != cin or x.shape[0] != kmap.n_in:
+    if K != kmap.K or x.dim() != 2 or x.shape[1] != cin or x.shape[0] != kmap.n_in:
         raise RuntimeError("shape mismatch between features, weight and kernel map")
+    if weight.dtype != x.dtype:
+        raise ValueError(f"weight dtype {weight.dtype} differs from x dtype {x.dtype}")
+    for name, t in (("x", x), ("weight", weight)):
+        if not t.is_contiguous():
+            raise ValueError(f"{name} must be contiguous")
+        if t.device != x.device:
+            raise ValueError(f"{name} must be on {x.device}")
+    if bias is not None:
+        if (bias.dtype != torch.float32 or not bias.is_contiguous() or bias.numel() != cout
+                or bias.device != x.device):
+            raise ValueError(f"bias must be a contiguous fp32 tensor of {cout} values on "
+                             f"{x.device}")
     if out is None:
         out = torch.empty((kmap.n_out, cout), dtype=x.dtype, device=x.device)
+    elif (out.dtype != x.dtype or tuple(out.shape) != (kmap.n_out, cout)
+          or not out.is_contiguous() or out.device != x.device):
+        raise ValueError(f"out must be a contiguous [{kmap.n_out}, {cout}] {x.dtype} tensor "
+                         f"on {x.device}")
     _check(lib().rhip_conv_forward_noalloc(_ptr(x), kmap.n_in, cin, _ptr(weight), K, cout,
                                            _ptr(bias), _ptr(kmap.nbr), _ptr(kmap.out_order),
                                            kmap.n_out, _ptr(out), dt, _stream(x.device)),

@@ -245,6 +245,10 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
                                return py::make_tuple(s.F().size(0), s.F().size(1));
                              })
       .def("__len__", [](const SparseTensor &s) { return s.F().size(0); })
+      .def("__add__", [](const SparseTensor &a, const SparseTensor &b) { return a + b; })
+      .def("__sub__", [](const SparseTensor &a, const SparseTensor &b) { return a - b; })
+      .def("__mul__", [](const SparseTensor &a, const SparseTensor &b) { return a * b; })
+      .def("__truediv__", [](const SparseTensor &a, const SparseTensor &b) { return a / b; })
       .def("__add__", [](const SparseTensor &s, double v) { return s + v; })
       .def("__radd__", [](const SparseTensor &s, double v) { return s + v; })
       .def("__mul__", [](const SparseTensor &s, double v) { return s * v; })

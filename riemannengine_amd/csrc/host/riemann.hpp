@@ -308,6 +308,14 @@ public:
   bool requires_grad() const { return features_.requires_grad(); }
 
   SparseTensor &operator+=(const SparseTensor &other);
+  // Elementwise over the union of both operands' coordinates
+  // (sparse_tensor.cpp:32-57, 331-379): the rows of both go through one
+  // dedup hash build on a fresh manager at the finer tensor stride, each
+  // operand's features land on their union rows and the other rows hold 0.
+  SparseTensor operator+(const SparseTensor &other) const;
+  SparseTensor operator-(const SparseTensor &other) const;
+  SparseTensor operator*(const SparseTensor &other) const;
+  SparseTensor operator/(const SparseTensor &other) const;
   SparseTensor operator+(at::Scalar scalar) const;
   SparseTensor operator*(at::Scalar scalar) const;
   SparseTensor to(c10::ScalarType dtype) const;
@@ -322,6 +330,8 @@ public:
 private:
   // The same map and manager with other features.
   SparseTensor with_features(at::Tensor features) const;
+  // The union operation behind operator+, -, * and / (op: '+', '-', '*', '/').
+  SparseTensor union_op(const SparseTensor &other, char op) const;
   static at::Tensor quantize_features(const at::Tensor &features, const at::Tensor &first_rows,
                                       const at::Tensor &row_to_unique, int64_t unique_count,
                                       SparseTensorQuantizationMode::Type mode);

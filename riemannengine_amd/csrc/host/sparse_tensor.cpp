@@ -90,6 +90,50 @@ SparseTensor &SparseTensor::operator+=(const SparseTensor &other) {
   return *this;
 }
 
+SparseTensor SparseTensor::union_op(const SparseTensor &other, char op) const {
+  const char *what = op == '+' ? "add" : op == '-' ? "subtract" : op == '*' ? "multiply"
+                                                                            : "divide";
+  // the argument contract of sparse_tensor.cpp:331-343
+  TORCH_CHECK(dimension_ == other.dimension_, "Cannot ", what,
+              " tensors with different dimensions");
+  TORCH_CHECK(features_.size(1) == other.features_.size(1), "Cannot ", what,
+              " tensors with different feature channel counts");
+  TORCH_CHECK(features_.device() == other.features_.device(), "Cannot ", what,
+              " tensors on different devices");
+  stride_type stride = tensor_stride();
+  const stride_type other_stride = other.tensor_stride();
+  for (size_t i = 0; i < stride.size() && i < other_stride.size(); ++i)
+    stride[i] = std::min(stride[i], other_stride[i]);
+  at::DeviceGuard guard(features_.device());
+  auto manager = std::make_shared<CoordinateManager>(dimension_, CoordinateMapBackend::CUDA);
+  const int64_t n_self = features_.size(0);
+  auto inserted = manager->insert_and_map(
+      torch::cat({C(), other.C().to(C().device())}, 0).contiguous(), stride);
+  const int64_t n = manager->size(inserted.first);
+  const at::Tensor &row = inserted.second.second; // union row of every input row
+  // each operand's rows are unique, so no two of them share a union row
+  auto place = [&](const at::Tensor &f, const at::Tensor &rows) {
+    return torch::zeros({n, f.size(1)}, f.options()).index_copy(0, rows, f);
+  };
+  const at::Tensor a = place(features_, row.slice(0, 0, n_self));
+  const at::Tensor b = place(other.features_, row.slice(0, n_self));
+  at::Tensor out = op == '+' ? a + b : op == '-' ? a - b : op == '*' ? a * b : a / b;
+  return SparseTensor(std::move(out), std::move(inserted.first), std::move(manager));
+}
+
+SparseTensor SparseTensor::operator+(const SparseTensor &other) const {
+  return union_op(other, '+');
+}
+SparseTensor SparseTensor::operator-(const SparseTensor &other) const {
+  return union_op(other, '-');
+}
+SparseTensor SparseTensor::operator*(const SparseTensor &other) const {
+  return union_op(other, '*');
+}
+SparseTensor SparseTensor::operator/(const SparseTensor &other) const {
+  return union_op(other, '/');
+}
+
 SparseTensor SparseTensor::operator+(at::Scalar scalar) const {
   return with_features(at::add(features_, scalar));
 }

@@ -399,10 +399,13 @@ def test_config1_sphere_shell_full():
     y = abi.conv_forward(to_dev(x), to_dev(w), km)
     gx = abi.conv_backward_input(to_dev(gy), to_dev(w), km)
     gw = abi.conv_backward_weight(to_dev(x), to_dev(gy), km, 27)
+    # the dW dispatch the layer and the bench time (neighbour-table kernels)
+    gw_timed = abi.conv_weight_grad(to_dev(x), to_dev(gy), km, 27)
     ry, rgx, rgw = _oracle_conv(km, x, w, gy)
     assert_rel(y.cpu().numpy(), ry, 1e-4, "Y")
     assert_rel(gx.cpu().numpy(), rgx, 1e-4, "dX")
-    assert_rel(gw.cpu().numpy(), rgw, 1e-4, "dW")
+    assert_rel(gw.cpu().numpy(), rgw, 1e-4, "dW (pair list)")
+    assert_rel(gw_timed.cpu().numpy(), rgw, 1e-4, "dW (timed dispatch)")
 
 
 def test_config1_sphere_shell_bf16_vs_torch():
@@ -526,40 +529,49 @@ def test_repeat_calls_are_bitwise_deterministic(dtype):
                        abi.conv_backward_weight(x, gy, km, 27))
 
 
-def test_config3_lidar_down_up_full_size():
-    """Config 3 at full size in bf16: 2^3 stride-2 conv C64->128 over the
-    LiDAR batch, then the 2^3 transposed conv C128->64 back onto the input
-    coordinates (the swapped map), forward and backward, against the plain
-    PyTorch fp32 gather-matmul-scatter on the same bf16 operands."""
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_config3_lidar_down_up_full_size(dtype):
+    """Config 3 at its stated size (the batch of two sweeps, 151,273 voxels,
+    ~150k quoted): 2^3 stride-2 conv C64->128 over the LiDAR batch, then the
+    2^3 transposed conv C128->64 back onto the input coordinates (the
+    swapped map), forward and backward, against the plain PyTorch fp32
+    gather-matmul-scatter on the same operands. bf16 is the configuration's
+    dtype; fp32 takes the other dW kernels. Both dW entry points are checked:
+    the pair-list kernel and the dispatch the bench and the layer time."""
     c = scenes.lidar_batch(2, 3)
+    assert len(c) >= 140000
     tin = abi.hash_build(to_dev(c))
     tout = abi.hash_build(abi.stride_coords(to_dev(c), [2, 2, 2]))
     down = abi.kernel_map(tin, tout, oracle.region_offsets(3, 2))
     up = down.swapped()
     assert down.n_pairs == down.n_in  # every fine voxel has exactly one parent
     g = torch.Generator(device="cpu").manual_seed(3)
-    dt = torch.bfloat16
+    dt = dtype
     x = torch.randn((down.n_in, 64), generator=g).to(DEV, dt)
     wd = (torch.randn((8, 64, 128), generator=g) * (2.0 / 512) ** 0.5).to(DEV, dt)
     wu = (torch.randn((8, 128, 64), generator=g) * (2.0 / 1024) ** 0.5).to(DEV, dt)
     gz = torch.randn((down.n_in, 64), generator=g).to(DEV, dt)
-    print(f"config 3: fine {down.n_in} coarse {down.n_out}", flush=True)
+    print(f"config 3 {dt}: fine {down.n_in} coarse {down.n_out}", flush=True)
     y = abi.conv_forward(x, wd, down)
     z = abi.conv_forward(y, wu, up)
     gy = abi.conv_backward_input(gz, wu, up)
     gwu = abi.conv_backward_weight(y, gz, up, 8)
+    gwu_t = abi.conv_weight_grad(y, gz, up, 8)
     gx = abi.conv_backward_input(gy, wd, down)
     gwd = abi.conv_backward_weight(x, gy, down, 8)
+    gwd_t = abi.conv_weight_grad(x, gy, down, 8)
     tol = TOL[dt]
     ry, _, _ = _torch_gather_gemm_scatter(down, x, wd, torch.zeros_like(y))
     assert_rel(y.float().cpu().numpy(), ry.cpu().numpy(), tol, "down Y")
     rz, rgy, rgwu = _torch_gather_gemm_scatter(up, y, wu, gz)
     assert_rel(z.float().cpu().numpy(), rz.cpu().numpy(), tol, "up Y")
     assert_rel(gy.float().cpu().numpy(), rgy.cpu().numpy(), tol, "up dX")
-    assert_rel(gwu.float().cpu().numpy(), rgwu.cpu().numpy(), tol, "up dW")
+    assert_rel(gwu.float().cpu().numpy(), rgwu.cpu().numpy(), tol, "up dW (pair list)")
+    assert_rel(gwu_t.float().cpu().numpy(), rgwu.cpu().numpy(), tol, "up dW (timed dispatch)")
     _, rgx, rgwd = _torch_gather_gemm_scatter(down, x, wd, gy)
     assert_rel(gx.float().cpu().numpy(), rgx.cpu().numpy(), tol, "down dX")
-    assert_rel(gwd.float().cpu().numpy(), rgwd.cpu().numpy(), tol, "down dW")
+    assert_rel(gwd.float().cpu().numpy(), rgwd.cpu().numpy(), tol, "down dW (pair list)")
+    assert_rel(gwd_t.float().cpu().numpy(), rgwd.cpu().numpy(), tol, "down dW (timed dispatch)")
 
 
 def test_config4_4d_full_size():
@@ -576,7 +588,10 @@ def test_config4_4d_full_size():
     y = abi.conv_forward(x, w, km)
     gx = abi.conv_backward_input(gy, w, km)
     gw = abi.conv_backward_weight(x, gy, km, 81)
+    # the dW dispatch the layer and the bench time (neighbour-table kernels)
+    gw_timed = abi.conv_weight_grad(x, gy, km, 81)
     ry, rgx, rgw = _torch_gather_gemm_scatter(km, x, w, gy)
     assert_rel(y.cpu().numpy(), ry.cpu().numpy(), 1e-4, "Y")
     assert_rel(gx.cpu().numpy(), rgx.cpu().numpy(), 1e-4, "dX")
-    assert_rel(gw.cpu().numpy(), rgw.cpu().numpy(), 1e-4, "dW")
+    assert_rel(gw.cpu().numpy(), rgw.cpu().numpy(), 1e-4, "dW (pair list)")
+    assert_rel(gw_timed.cpu().numpy(), rgw.cpu().numpy(), 1e-4, "dW (timed dispatch)")

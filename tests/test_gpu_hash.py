@@ -32,11 +32,15 @@ def test_build_matches_oracle(n, D, span):
 def test_scan_order_points_match_oracle():
     """Raw quantised LiDAR points in scan order, the input a coordinate map
     deduplicates: most repeats follow the same point, in runs that one lane
-    inserts for the whole run."""
-    c = scenes.lidar_batch(2, 3, unique=False)
+    inserts for the whole run (the car-height recipe, whose near ground
+    puts many beams into each voxel), and the configuration's own sweeps."""
+    c = scenes.lidar_batch(2, 3, unique=False, recipe="literal")
     assert np.all(c[1:] == c[:-1], axis=1).sum() > len(c) // 3
     t = _check_build(c)
-    assert t.n == len(scenes.lidar_batch(2, 3))
+    assert t.n == len(scenes.lidar_batch(2, 3, recipe="literal"))
+    c = scenes.lidar_batch(2, 3, unique=False)
+    t = _check_build(c)
+    assert t.n == len(scenes.lidar_batch(2, 3)) == 151273
 
 
 @pytest.mark.parametrize("span", [20, 30000])

@@ -406,3 +406,73 @@ def test_basic_block_config5_stage1_full_size(dtype):
     assert_rel(_np(feats.grad), _np(xr.grad), tol, "block grad x")
     for k, v in p.items():
         assert_rel(_np(v.grad), _np(leaf[k].grad), tol, "block grad " + k)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_config5_stage3_full_size(dtype):
+    """Config 5's third stage at full size: the 2^3 stride-2 conv C64->128
+    that takes stage 2 (tensor stride 2, 8 indoor scenes) down to stage 3
+    (tensor stride 4), then one BasicBlock(128, 128) on the stage-3 maps
+    (3^3 offsets scaled by the tensor stride), forward and backward through
+    the host layer, against the reference's composition (conv.cpp:47-64,
+    residual.cpp:44-52) in fp32 torch on the GPU over the same maps' pairs,
+    with the layers' own parameters and input. Tolerances, bf16 rounding and
+    ReLU decisions are handled as in the stage-1 test above."""
+    from riemannengine_amd import scenes
+    c = scenes.indoor_batch(8, 2)
+    mgr = re_.CoordinateManager(3)
+    k1, _ = mgr.insert_and_map(torch.from_numpy(c).to(DEV), [1, 1, 1])
+    k2 = mgr.stride(k1, [2, 2, 2])
+    c2 = mgr.get_coordinates(k2)
+    torch.manual_seed(10)
+    down = re_.nn.RiemannConvolution(64, 128, kernel_size=2, stride=2, dimension=3)
+    blk = re_.nn.BasicBlock(128, 128)
+    for m in (down, blk):
+        m.to(DEV)
+        m.to_dtype(dtype)
+    g = torch.Generator().manual_seed(11)
+    feats = torch.randn(len(c2), 64, generator=g).to(DEV, dtype).requires_grad_(True)
+    x2 = re_.SparseTensor(feats, k2, mgr)
+    h = down(x2)
+    out = blk(h)
+    n3 = len(out)
+    print(f"config-5 stage-3: stage-2 rows {len(c2)}, stage-3 rows {n3} {dtype}", flush=True)
+    assert list(h.tensor_stride) == [4, 4, 4] and n3 > 30000
+    gy = torch.randn(out.F.shape, generator=g).to(DEV, dtype)
+    (out.F.float() * gy.float()).sum().backward()
+
+    c3 = h.C.contiguous()
+    t2 = abi.hash_build(c2.contiguous())
+    t3 = abi.hash_build(c3)
+    kmd = abi.kernel_map(t2, t3, oracle.region_offsets(3, 2, 1, 2))
+    km3 = abi.kernel_map(t3, t3, oracle.region_offsets(3, 3, 1, 4))
+    assert kmd.n_pairs == len(c2)  # every stage-2 voxel has exactly one parent
+    pd = dict(down.named_parameters())
+    pb = blk.named_parameters()
+    w1 = pb["conv1.base.kernel"].detach()
+    g1, b1 = pb["norm1.normalization.weight"].detach(), pb["norm1.normalization.bias"].detach()
+    y1 = abi.conv_forward(h.F.detach(), w1, km3)
+    m1, s1 = abi.bn_stats(y1)
+    mask1 = abi.bn_forward(y1, m1, s1, g1.float(), b1.float(), relu=True) > 0
+    mask2 = out.F.detach() > 0
+    R = _RoundBF16.apply if dtype == torch.bfloat16 else (lambda v: v)
+    leaf_d = {k: v.detach().float().requires_grad_(True) for k, v in pd.items()}
+    leaf = {k: v.detach().float().requires_grad_(True) for k, v in pb.items()}
+    xr = feats.detach().float().requires_grad_(True)
+    bn = lambda v, i: F.batch_norm(v, None, None, leaf[f"norm{i}.normalization.weight"],
+                                   leaf[f"norm{i}.normalization.bias"], True, 0.1, 1e-5)
+    hr = R(_torch_conv_gpu(xr, leaf_d["base.kernel"], kmd))
+    assert_rel(_np(h.F), _np(hr), TOL[dtype], "downsample y")
+    z1 = bn(R(_torch_conv_gpu(hr, leaf["conv1.base.kernel"], km3)), 1)
+    hh = R(z1 * mask1)
+    ref = R((bn(R(_torch_conv_gpu(hh, leaf["conv2.base.kernel"], km3)), 2) + hr) * mask2)
+    (ref * gy.float()).sum().backward()
+    flips = int(((z1 > 0) != mask1).sum())
+    assert flips < mask1.numel() // 1000
+    tol = TOL[dtype]
+    assert_rel(_np(out.F), _np(ref), tol, "block y")
+    assert_rel(_np(feats.grad), _np(xr.grad), tol, "stage-2 grad x")
+    for k, v in pb.items():
+        assert_rel(_np(v.grad), _np(leaf[k].grad), tol, "block grad " + k)
+    for k, v in pd.items():
+        assert_rel(_np(v.grad), _np(leaf_d[k].grad), tol, "downsample grad " + k)

@@ -115,3 +115,16 @@ def test_invalid_layer_arguments():
         re_.nn.RiemannConvolution(0, 4)
     with pytest.raises(RuntimeError, match="positive"):
         re_.nn.RiemannConvolution(4, 4, kernel_size=0)
+
+
+def test_reference_module_path():
+    """`import riemannengine` and `import riemannengine.nn`, the reference's
+    module path (python/riemannengine/__init__.py:14-37), expose the host
+    layer's classes themselves."""
+    import riemannengine
+    import riemannengine.nn as rnn
+    assert riemannengine.SparseTensor is re_.SparseTensor
+    assert riemannengine.CoordinateManager is re_.CoordinateManager
+    assert rnn is re_.nn and rnn.RiemannConvolution is re_.nn.RiemannConvolution
+    for name in riemannengine.__all__:
+        assert getattr(riemannengine, name) is not None

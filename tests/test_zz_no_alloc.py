@@ -23,6 +23,39 @@ def test_noalloc_rejects_weights_beyond_the_scratch():
     assert "scratch" in L.rhip_last_error().decode()
 
 
+def test_noalloc_wrapper_raises_instead_of_converting(monkeypatch):
+    """conv_forward_noalloc converts nothing (a conversion would allocate):
+    each operand that the library would misread raises ValueError before
+    the library is called. Host tensors stand in for device ones here (the
+    device check is switched off and the library is never reached)."""
+    from types import SimpleNamespace
+    monkeypatch.setattr(abi, "_require_cuda", lambda t, name: None)
+    monkeypatch.setattr(abi, "lib", lambda: pytest.fail("the library was called"))
+    km = SimpleNamespace(K=27, n_in=10, n_out=7)
+    f32, bf = torch.float32, torch.bfloat16
+    x = torch.zeros(10, 16)
+    w = torch.zeros(27, 16, 32)
+    ok_out = torch.empty(7, 32)
+    cases = {
+        "weight dtype": dict(weight=w.to(bf)),
+        "x not contiguous": dict(x=torch.zeros(16, 10).t()),
+        "weight not contiguous": dict(weight=torch.zeros(27, 32, 16).transpose(1, 2)),
+        "bias bf16": dict(bias=torch.zeros(32, dtype=bf)),
+        "bias size": dict(bias=torch.zeros(31)),
+        "bias not contiguous": dict(bias=torch.zeros(64)[::2]),
+        "out dtype": dict(out=torch.empty(7, 32, dtype=bf)),
+        "out shape": dict(out=torch.empty(7, 31)),
+        "out not contiguous": dict(out=torch.empty(32, 7).t()),
+    }
+    for what, kw in cases.items():
+        args = dict(x=x, weight=w, bias=torch.zeros(32, dtype=f32), out=ok_out)
+        args.update(kw)
+        with pytest.raises(ValueError):
+            abi.conv_forward_noalloc(args["x"], args["weight"], km, bias=args["bias"],
+                                     out=args["out"])
+            pytest.fail(what)
+
+
 @pytest.mark.gpu
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_noalloc_forward_matches_workspace_forward(dtype):
