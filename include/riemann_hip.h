@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define RHIP_ABI_VERSION 12
+#define RHIP_ABI_VERSION 13
 #define RHIP_MAX_COLS 8 /* batch column + up to 7 spatial axes */
 
 typedef enum rhip_status {
@@ -212,11 +212,15 @@ int rhip_kmap_count(const rhip_table *in_table, const int32_t *out_coords,
 /*
  * Phase 2: emit the pairs of offset k at [kmap_offsets[k], kmap_offsets[k+1])
  * of in_rows / out_rows, ordered by offset, then by output processing
- * position. If nbr_t is not NULL, also fix a processing order of the input
- * rows (in_order, grouping equal transposed masks; ties keep
- * in_spatial_order, NULL = row order) and fill the transposed table
- * nbr_t[k*n_in+q] = output row paired with in_order[q] under k, or -1.
- * flags and the workspace must be what phase 1 produced. Asynchronous.
+ * position (in_rows and out_rows both NULL: no pair lists; rhip_kmap_pairs
+ * emits them later from the table). If nbr_t is not NULL, also fix a
+ * processing order of the input rows (in_order, grouping equal transposed
+ * masks; ties keep in_spatial_order, NULL = row order) and fill the
+ * transposed table nbr_t[k*n_in+q] = output row paired with in_order[q]
+ * under k, or -1. A symmetric map without pair lists and without nbr_t
+ * launches nothing: its convolution runs from nbr alone (see
+ * rhip_conv_backward_input). flags and the workspace must be what phase 1
+ * produced. Asynchronous.
  * Replaces gpu_kernel_map::decompose (engine/grid/lattice_gpu.cuh:438-488);
  * the set of pairs equals the reference's cpu_kernel_map.
  */
@@ -226,6 +230,36 @@ int rhip_kmap_fill(const int32_t *nbr, const int32_t *out_order, int64_t n_out,
                    const int64_t *kmap_offsets, int32_t *in_rows,
                    int32_t *out_rows, int32_t *nbr_t, int32_t *in_order,
                    hipStream_t stream);
+
+/* Workspace of rhip_kmap_pairs for a table of n_out positions and K offsets. */
+int rhip_kmap_pairs_workspace_bytes(int64_t n_out, int32_t K, size_t *bytes);
+
+/*
+ * The pair lists of a finished map from its table: the same in_rows /
+ * out_rows (order included) that rhip_kmap_fill emits, sized by
+ * kmap_offsets[K] (the device CSR of rhip_kmap_count). For maps whose pair
+ * lists are needed only sometimes (the pair-list weight gradient,
+ * kernel_map_to_tensors): the build then writes no 8 P bytes it may never
+ * read. Asynchronous.
+ * Replaces the triplet output of gpu_kernel_map::decompose
+ * (engine/grid/lattice_gpu.cuh:438-488) on demand.
+ */
+int rhip_kmap_pairs(const int32_t *nbr, const int32_t *out_order, int64_t n_out,
+                    int32_t K, const int64_t *kmap_offsets, void *workspace,
+                    size_t workspace_bytes, int32_t *in_rows, int32_t *out_rows,
+                    hipStream_t stream);
+
+/*
+ * partner_host[a] = the offset b with offsets[b] = -offsets[a] (int32
+ * wrap-around negation, the coordinate type's) for a stencil [K, D] (host)
+ * closed under negation with distinct offsets; RHIP_ERR_UNSUPPORTED
+ * otherwise. Host only. The partners of a symmetric map (RHIP_KMAP_SYMMETRIC)
+ * are the weight permutation of its input gradient. Replaces the transposed
+ * map a cached forward map yields by swap_in_out_map (engine/grid/
+ * space_impl.hpp:649-697) for a map of a set onto itself.
+ */
+int rhip_stencil_partners(const int32_t *offsets_host, int32_t K, int32_t D,
+                          int32_t *partner_host);
 
 /* ----------------------------------------------------------- convolution */
 
@@ -286,16 +320,23 @@ int rhip_conv_bias_grad(const void *grad_y, int64_t n_out, int32_t cout,
                         size_t workspace_bytes, hipStream_t stream);
 
 /*
- * grad_x[in_order[j]] = sum_k grad_y[nbr_t[k*n_in+j]] @ W[k]^T.
+ * grad_x[in_order[j]] = sum_k grad_y[nbr_t[k*n_in+j]] @ W[p(k)]^T, where
+ * p(k) = weight_perm[k] (device int32 [K]) or k when weight_perm is NULL.
+ * A symmetric map (RHIP_KMAP_SYMMETRIC) needs no transposed table: pass its
+ * nbr as nbr_t, its out_order as in_order and its stencil partners
+ * (rhip_stencil_partners, uploaded) as weight_perm, since input row i pairs
+ * with output row o under k exactly when o pairs with i under the partner
+ * of k. With weight_perm, shapes the LDS-indexed kernel does not take copy
+ * the reordered weights into the workspace first, so it is then required.
  * Replaces the autograd replay of IndexAddBackward/MmBackward/
  * IndexSelectBackward for dX (engine/nn/conv.cpp:62-63).
  */
 int rhip_conv_backward_input(const void *grad_y, int64_t n_out, int32_t cout,
                              const void *weight, int32_t K, int32_t cin,
-                             const int32_t *nbr_t, const int32_t *in_order,
-                             int64_t n_in, void *grad_x, int32_t dtype,
-                             void *workspace, size_t workspace_bytes,
-                             hipStream_t stream);
+                             const int32_t *nbr_t, const int32_t *weight_perm,
+                             const int32_t *in_order, int64_t n_in, void *grad_x,
+                             int32_t dtype, void *workspace,
+                             size_t workspace_bytes, hipStream_t stream);
 
 /*
  * grad_w[k] = sum over pairs p of offset k of x[in_rows[p]]^T grad_y[out_rows[p]]
@@ -336,6 +377,13 @@ int rhip_conv_backward_weight_rows(const void *x, int64_t n_in, int32_t cin,
                                    const int32_t *out_order, void *grad_w,
                                    int32_t dtype, void *workspace,
                                    size_t workspace_bytes, hipStream_t stream);
+
+/* 1 if rhip_conv_backward_weight_rows takes this shape, else 0 (no status:
+ * a pure query of its dispatch rules, for callers that decide ahead of time
+ * whether the pair lists will be needed, e.g. RiemannConvolution's forward,
+ * engine/nn/conv.cpp:104-138). */
+int rhip_conv_backward_weight_rows_supported(int32_t dtype, int32_t cin, int32_t cout,
+                                             int32_t K, int64_t n_in, int64_t n_out);
 
 /* --------------------------------------------------------------- pooling */
 

@@ -32,6 +32,8 @@ EXPORTS = (
     "rhip_order_workspace_bytes", "rhip_brick_bytes", "rhip_spatial_order",
     "rhip_stride_coords",
     "rhip_expand_coords", "rhip_kmap_workspace_bytes", "rhip_kmap_count", "rhip_kmap_fill",
+    "rhip_kmap_pairs_workspace_bytes", "rhip_kmap_pairs", "rhip_stencil_partners",
+    "rhip_conv_backward_weight_rows_supported",
     "rhip_conv_workspace_bytes", "rhip_conv_forward_workspace_bytes", "rhip_conv_forward",
     "rhip_conv_forward_noalloc", "rhip_conv_bias_grad",
     "rhip_conv_backward_input", "rhip_conv_backward_weight", "rhip_conv_backward_weight_rows",
@@ -94,8 +96,13 @@ def _declare(lib):
         "rhip_conv_forward_noalloc": (ctypes.c_int, [_vp, _i64, _i32, _vp, _i32, _i32, _vp,
                                                      _vp, _vp, _i64, _vp, _i32, _vp]),
         "rhip_conv_backward_input": (ctypes.c_int, [_vp, _i64, _i32, _vp, _i32, _i32,
-                                                    _vp, _vp, _i64, _vp, _i32, _vp,
+                                                    _vp, _vp, _vp, _i64, _vp, _i32, _vp,
                                                     _sz, _vp]),
+        "rhip_conv_backward_weight_rows_supported": (ctypes.c_int, [_i32, _i32, _i32, _i32,
+                                                                    _i64, _i64]),
+        "rhip_kmap_pairs_workspace_bytes": (ctypes.c_int, [_i64, _i32, _P(_sz)]),
+        "rhip_kmap_pairs": (ctypes.c_int, [_vp, _vp, _i64, _i32, _vp, _vp, _sz, _vp, _vp, _vp]),
+        "rhip_stencil_partners": (ctypes.c_int, [_P(_i32), _i32, _i32, _P(_i32)]),
         "rhip_conv_backward_weight": (ctypes.c_int, [_vp, _i64, _i32, _vp, _i64, _i32,
                                                      _i32, _vp, _i64, _vp, _vp, _vp,
                                                      _i32, _vp, _sz, _vp]),
@@ -290,46 +297,107 @@ def expand_coords(coords: torch.Tensor, offsets) -> torch.Tensor:
 
 # ------------------------------------------------------------- kernel maps
 
-@dataclass
 class KernelMap:
     """Per-offset (in, out) pairs plus the dense neighbour tables.
 
     nbr[k, j]   : input row of output position j (output order) or -1
     nbr_t[k, i] : output row of input position i (input order) or -1
     offsets     : CSR over pairs, pairs of offset k at [offsets[k], offsets[k+1])
+
+    The pair lists (in_rows, out_rows) are emitted from nbr on first access
+    (rhip_kmap_pairs), at their exact size. A symmetric map (a set onto
+    itself, stencil closed under negation) has `partner` (device int32 [K],
+    the offset that negates each offset) and no transposed table: its input
+    gradient runs on nbr with partner as weight permutation; nbr_t and
+    in_order, if read, are built then from nbr's rows.
     """
-    K: int
-    n_in: int
-    n_out: int
-    offsets: torch.Tensor        # device int64 [K+1]
-    offsets_host: np.ndarray     # int64 [K+1]
-    in_rows: torch.Tensor        # int32 [P]
-    out_rows: torch.Tensor       # int32 [P]
-    nbr: torch.Tensor            # int32 [K, n_out]
-    nbr_t: torch.Tensor          # int32 [K, n_in]
-    in_order: torch.Tensor
-    out_order: torch.Tensor
-    symmetric: bool = False
+
+    def __init__(self, K, n_in, n_out, offsets, offsets_host, in_rows, out_rows, nbr, nbr_t,
+                 in_order, out_order, symmetric=False, partner=None):
+        self.K, self.n_in, self.n_out = K, n_in, n_out
+        self.offsets, self.offsets_host = offsets, offsets_host
+        self._in_rows, self._out_rows = in_rows, out_rows
+        self.nbr, self._nbr_t = nbr, nbr_t
+        self._in_order, self.out_order = in_order, out_order
+        self.symmetric, self.partner = symmetric, partner
 
     @property
     def n_pairs(self) -> int:
         return int(self.offsets_host[-1])
 
+    def _build_pairs(self):
+        L = lib()
+        dev = self.nbr.device
+        P = self.n_pairs
+        ir = torch.empty(max(P, 1), dtype=torch.int32, device=dev)
+        orr = torch.empty(max(P, 1), dtype=torch.int32, device=dev)
+        if P > 0:
+            ws = torch.empty(_sizeq(L.rhip_kmap_pairs_workspace_bytes, self.n_out, self.K),
+                             dtype=torch.uint8, device=dev)
+            _check(L.rhip_kmap_pairs(_ptr(self.nbr), _ptr(self.out_order), self.n_out, self.K,
+                                     _ptr(self.offsets), _ptr(ws), ws.numel(), _ptr(ir),
+                                     _ptr(orr), _stream(dev)), "rhip_kmap_pairs")
+        self._in_rows, self._out_rows = ir[:P], orr[:P]
+
+    @property
+    def in_rows(self) -> torch.Tensor:
+        if self._in_rows is None:
+            self._build_pairs()
+        return self._in_rows
+
+    @property
+    def out_rows(self) -> torch.Tensor:
+        if self._out_rows is None:
+            self._build_pairs()
+        return self._out_rows
+
+    def _build_transposed(self):
+        # i pairs with o under k iff o pairs with i under partner[k]
+        inv = torch.empty(self.K, dtype=torch.long, device=self.nbr.device)
+        inv[self.partner.long()] = torch.arange(self.K, device=self.nbr.device)
+        self._nbr_t = self.nbr.index_select(0, inv)
+        self._in_order = self.out_order
+
+    @property
+    def nbr_t(self) -> torch.Tensor:
+        if self._nbr_t is None:
+            self._build_transposed()
+        return self._nbr_t
+
+    @property
+    def in_order(self) -> torch.Tensor:
+        if self._in_order is None:
+            self._build_transposed()
+        return self._in_order
+
     def swapped(self) -> "KernelMap":
-        """Transposed map: in and out exchanged, zero copy."""
+        """Transposed map: in and out exchanged (zero copy once built)."""
         return KernelMap(self.K, self.n_out, self.n_in, self.offsets, self.offsets_host,
                          self.out_rows, self.in_rows, self.nbr_t, self.nbr,
-                         self.out_order, self.in_order, self.symmetric)
+                         self.out_order, self.in_order)
 
     def pairs(self, k: int):
         a, b = int(self.offsets_host[k]), int(self.offsets_host[k + 1])
         return self.in_rows[a:b], self.out_rows[a:b]
 
 
+def stencil_partners(offsets) -> Optional[np.ndarray]:
+    """The offset that negates each offset of a stencil [K, D] (host), or None
+    where the stencil is not closed under negation (rhip_stencil_partners)."""
+    off = np.ascontiguousarray(np.asarray(offsets, dtype=np.int32))
+    K, D = off.shape
+    out = np.empty(K, np.int32)
+    st = lib().rhip_stencil_partners(off.ctypes.data_as(ctypes.POINTER(ctypes.c_int32)), K, D,
+                                     out.ctypes.data_as(ctypes.POINTER(ctypes.c_int32)))
+    return out if st == 0 else None
+
+
 def kernel_map(in_table: CoordTable, out_table: CoordTable, offsets) -> KernelMap:
     """Pairs (in, out) with coord(in) = coord(out) + offsets[k] (batch kept),
     the dense neighbour tables and the processing orders of both sides.
-    offsets: [K, D] int32 (numpy or tensor; read on the host)."""
+    offsets: [K, D] int32 (numpy or tensor; read on the host). The pair
+    lists are built when first read; a symmetric map builds no transposed
+    table (see KernelMap)."""
     L = lib()
     dev = in_table.ucoords.device
     offsets = torch.as_tensor(np.asarray(offsets.cpu() if torch.is_tensor(offsets) else offsets),
@@ -353,24 +421,24 @@ def kernel_map(in_table: CoordTable, out_table: CoordTable, offsets) -> KernelMa
                              off_host.ctypes.data_as(ctypes.POINTER(ctypes.c_int32)), _ptr(ws),
                              ws.numel(), _ptr(nbr), _ptr(out_order), _ptr(kofs), None,
                              ctypes.byref(flags), st), "rhip_kmap_count")
-    # count and fill back to back: pair lists sized by the bound K * n_out,
-    # the pair counts read once after the fill
-    in_rows = torch.empty(max(K * n_out, 1), dtype=torch.int32, device=dev)
-    out_rows = torch.empty(max(K * n_out, 1), dtype=torch.int32, device=dev)
-    nbr_t = torch.empty((K, max(n_in, 1)), dtype=torch.int32, device=dev)
-    in_order = torch.empty(max(n_in, 1), dtype=torch.int32, device=dev)
-    _check(L.rhip_kmap_fill(_ptr(nbr), _ptr(out_order), n_out, K, _ptr(in_table.order), n_in,
-                            flags.value, _ptr(ws), ws.numel(), _ptr(kofs), _ptr(in_rows),
-                            _ptr(out_rows), _ptr(nbr_t), _ptr(in_order), st), "rhip_kmap_fill")
+    symmetric = bool(flags.value & KMAP_SYMMETRIC)
+    nbr_t = in_order = partner = None
+    if symmetric:
+        partner = torch.from_numpy(stencil_partners(off_host)).to(dev)
+    else:
+        nbr_t = torch.empty((K, max(n_in, 1)), dtype=torch.int32, device=dev)
+        in_order = torch.empty(max(n_in, 1), dtype=torch.int32, device=dev)
+        _check(L.rhip_kmap_fill(_ptr(nbr), _ptr(out_order), n_out, K, _ptr(in_table.order),
+                                n_in, flags.value, _ptr(ws), ws.numel(), _ptr(kofs), None, None,
+                                _ptr(nbr_t), _ptr(in_order), st), "rhip_kmap_fill")
+        nbr_t, in_order = nbr_t[:, :n_in], in_order[:n_in]
     # the one read-back: the pair counts through pinned memory
     kofs_pinned = torch.empty(K + 1, dtype=torch.int64, pin_memory=True)
     kofs_pinned.copy_(kofs, non_blocking=True)
     torch.cuda.current_stream(dev).synchronize()
     kofs_host = kofs_pinned.numpy()
-    P = int(kofs_host[-1])
-    return KernelMap(K, n_in, n_out, kofs, kofs_host, in_rows[:P], out_rows[:P],
-                     nbr[:, :n_out], nbr_t[:, :n_in], in_order[:n_in], out_order[:n_out],
-                     symmetric=bool(flags.value & KMAP_SYMMETRIC))
+    return KernelMap(K, n_in, n_out, kofs, kofs_host, None, None, nbr[:, :n_out], nbr_t,
+                     in_order, out_order[:n_out], symmetric=symmetric, partner=partner)
 
 
 # ------------------------------------------------------------ convolution
@@ -473,8 +541,12 @@ def conv_backward_input(grad_y: torch.Tensor, weight: torch.Tensor, kmap: Kernel
     K, cin, cout = weight.shape
     gx = torch.empty((kmap.n_in, cin), dtype=grad_y.dtype, device=grad_y.device)
     ws = _conv_fwd_ws(K, cin, cout, dt, grad_y.device, kmap)
+    if kmap.symmetric:  # nbr with the stencil partners as weight permutation
+        table, perm, order = kmap.nbr, kmap.partner, kmap.out_order
+    else:
+        table, perm, order = kmap.nbr_t, None, kmap.in_order
     _check(lib().rhip_conv_backward_input(_ptr(grad_y), kmap.n_out, cout, _ptr(weight), K, cin,
-                                          _ptr(kmap.nbr_t), _ptr(kmap.in_order), kmap.n_in,
+                                          _ptr(table), _ptr(perm), _ptr(order), kmap.n_in,
                                           _ptr(gx), dt, _ptr(ws), ws.numel(),
                                           _stream(grad_y.device)), "rhip_conv_backward_input")
     return gx
@@ -630,8 +702,8 @@ def pooling_map(kmap: KernelMap) -> KernelMap:
     """A kernel map for pooling: its transposed table compacted (the input
     side of a strided pooling map has few of the K offsets)."""
     return KernelMap(kmap.K, kmap.n_in, kmap.n_out, kmap.offsets, kmap.offsets_host,
-                     kmap.in_rows, kmap.out_rows, kmap.nbr, table_compact(kmap.nbr_t),
-                     kmap.in_order, kmap.out_order, kmap.symmetric)
+                     kmap._in_rows, kmap._out_rows, kmap.nbr, table_compact(kmap.nbr_t),
+                     kmap.in_order, kmap.out_order)
 
 
 def _pool_mode(mode) -> int:

@@ -440,7 +440,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(WAVES)
 // sums (config 5 step 5.87 -> 5.73 ms against conv_os_kernel's split).
 template <typename T, int NT, int RG, int CSUB, int G, int WAVES, int CW, int KQ, bool SPLIT>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(WAVES))) void
-conv_os_lds_kernel(const T *__restrict__ x, int64_t n_x, const T *__restrict__ wt, int ncols,
+conv_os_lds_kernel(const T *__restrict__ x, int64_t n_x, const T *__restrict__ wt,
+                   const int32_t *__restrict__ wperm, int ncols,
                    const float *__restrict__ bias, const int32_t *__restrict__ nbr,
                    int64_t n_rows, int K, const int32_t *__restrict__ order, T *__restrict__ y,
                    float *__restrict__ partial) {
@@ -595,14 +596,17 @@ conv_os_lds_kernel(const T *__restrict__ x, int64_t n_x, const T *__restrict__ w
       }
     uint4 wreg[G][NPT];
 #pragma unroll
-    for (int j = 0; j < G; ++j)
+    for (int j = 0; j < G; ++j) {
+      // table row kj multiplies weight slice wperm[kj] (uniform) when given
+      const int kw = wperm ? wperm[kj[j]] : kj[j];
 #pragma unroll
       for (int i = 0; i < NPT; ++i) {
         const int li = min(static_cast<int>(threadIdx.x) + i * kThreads, NV - 1);
         wreg[j][i] = *reinterpret_cast<const uint4 *>(
-            wt + (static_cast<int64_t>(kj[j]) * ncols + col0 + li / (CCH / VE)) * CW +
+            wt + (static_cast<int64_t>(kw) * ncols + col0 + li / (CCH / VE)) * CW +
             ccj[j] * CCH + (li % (CCH / VE)) * VE);
       }
+    }
     v4u a[G][RG][CSUB];
 #pragma unroll
     for (int j = 0; j < G; ++j)
@@ -978,15 +982,20 @@ __global__ __launch_bounds__(kThreads) void transpose_w_kernel(const T *__restri
   wt[i] = c < cin ? w[(k * cin + c) * cout + n] : from_f32<T>(0.f);
 }
 
-// dst[r][c] = src[r][c] for c < cols, zero up to credw (rows of cols -> credw).
+// dst[r][c] = src[r'][c] for c < cols, zero up to credw (rows of cols ->
+// credw), where r' = r, or with perm the row of slice perm[r / rpk] that r
+// is of slice r / rpk (slices of rpk rows reordered).
 template <typename T>
 __global__ __launch_bounds__(kThreads) void pad_rows_kernel(const T *__restrict__ src,
                                                             int64_t rows, int cols, int credw,
-                                                            T *__restrict__ dst) {
+                                                            const int32_t *__restrict__ perm,
+                                                            int64_t rpk, T *__restrict__ dst) {
   const int64_t i = blockIdx.x * static_cast<int64_t>(kThreads) + threadIdx.x;
   if (i >= rows * credw)
     return;
-  const int64_t r = i / credw;
+  int64_t r = i / credw;
+  if (perm)
+    r = static_cast<int64_t>(perm[r / rpk]) * rpk + r % rpk;
   const int c = static_cast<int>(i % credw);
   dst[i] = c < cols ? src[r * cols + c] : from_f32<T>(0.f);
 }
@@ -2163,27 +2172,28 @@ static size_t os_partial_floats(int64_t n_rows, int cred, int ncols, int K) {
 // splits stay on conv_os_kernel).
 template <typename T, int NT, int RG, int CSUB, int G, int WAVES, int CW, int KQ>
 static void launch_os_lds_cw(dim3 grid, bool split, const T *x, int64_t n_x, const T *wt,
-                             int ncols, const float *bias, const int32_t *nbr, int64_t n_rows,
-                             int K, const int32_t *order, T *y, float *partial, hipStream_t s) {
+                             const int32_t *wperm, int ncols, const float *bias,
+                             const int32_t *nbr, int64_t n_rows, int K, const int32_t *order,
+                             T *y, float *partial, hipStream_t s) {
   if constexpr (!kIsF32<T>) {
     if (split) {
       hipLaunchKernelGGL((conv_os_lds_kernel<T, NT, RG, CSUB, G, WAVES, CW, KQ, true>), grid,
-                         dim3(kThreads), 0, s, x, n_x, wt, ncols, bias, nbr, n_rows, K, order, y,
-                         partial);
+                         dim3(kThreads), 0, s, x, n_x, wt, wperm, ncols, bias, nbr, n_rows, K,
+                         order, y, partial);
       return;
     }
   }
   hipLaunchKernelGGL((conv_os_lds_kernel<T, NT, RG, CSUB, G, WAVES, CW, KQ, false>), grid,
-                     dim3(kThreads), 0, s, x, n_x, wt, ncols, bias, nbr, n_rows, K, order, y,
-                     nullptr);
+                     dim3(kThreads), 0, s, x, n_x, wt, wperm, ncols, bias, nbr, n_rows, K, order,
+                     y, nullptr);
 }
 
 // conv_os_lds_kernel launches: the reduction width as one, two or four
 // chunks; false where it is none of these (or an fp32 split).
 template <typename T, int NT, int RG, int CSUB, int G, int WAVES, int KQ>
-static bool launch_os_lds(const T *x, int64_t n_x, int cred, const T *wt, int ncols,
-                          const float *bias, const int32_t *nbr, int64_t n_rows, int K,
-                          const int32_t *order, T *y, int splits, float *partial,
+static bool launch_os_lds(const T *x, int64_t n_x, int cred, const T *wt, const int32_t *wperm,
+                          int ncols, const float *bias, const int32_t *nbr, int64_t n_rows,
+                          int K, const int32_t *order, T *y, int splits, float *partial,
                           hipStream_t s) {
   constexpr int CCH = CSUB * kChOf<T>;
   constexpr int ROWS = kWaves * RG * 16;
@@ -2192,14 +2202,16 @@ static bool launch_os_lds(const T *x, int64_t n_x, int cred, const T *wt, int nc
     return false;
   const dim3 grid(static_cast<unsigned>(xcd_grid(ceil_div(n_rows, ROWS))), ncols / NT, splits);
   if (cred == CCH)
-    launch_os_lds_cw<T, NT, RG, CSUB, G, WAVES, CCH, KQ>(grid, sp, x, n_x, wt, ncols, bias, nbr,
-                                                         n_rows, K, order, y, partial, s);
+    launch_os_lds_cw<T, NT, RG, CSUB, G, WAVES, CCH, KQ>(grid, sp, x, n_x, wt, wperm, ncols, bias,
+                                                         nbr, n_rows, K, order, y, partial, s);
   else if (cred == 2 * CCH)
-    launch_os_lds_cw<T, NT, RG, CSUB, G, WAVES, 2 * CCH, KQ>(grid, sp, x, n_x, wt, ncols, bias,
-                                                             nbr, n_rows, K, order, y, partial, s);
+    launch_os_lds_cw<T, NT, RG, CSUB, G, WAVES, 2 * CCH, KQ>(grid, sp, x, n_x, wt, wperm, ncols,
+                                                             bias, nbr, n_rows, K, order, y,
+                                                             partial, s);
   else if (cred == 4 * CCH)
-    launch_os_lds_cw<T, NT, RG, CSUB, G, WAVES, 4 * CCH, KQ>(grid, sp, x, n_x, wt, ncols, bias,
-                                                             nbr, n_rows, K, order, y, partial, s);
+    launch_os_lds_cw<T, NT, RG, CSUB, G, WAVES, 4 * CCH, KQ>(grid, sp, x, n_x, wt, wperm, ncols,
+                                                             bias, nbr, n_rows, K, order, y,
+                                                             partial, s);
   else
     return false;
   if (splits > 1) {
@@ -2217,78 +2229,78 @@ static bool launch_os_lds(const T *x, int64_t n_x, int cred, const T *wt, int nc
 // stages per barrier and 80 with three row groups); the other shapes keep
 // conv_os_kernel's.
 template <typename T, int NT, int CSUB, int KQ>
-static bool os_lds_shape(const T *x, int64_t n_x, int cred, const T *wt, int ncols,
-                         const float *bias, const int32_t *nbr, int64_t n_rows, int K,
+static bool os_lds_shape(const T *x, int64_t n_x, int cred, const T *wt, const int32_t *wperm,
+                         int ncols, const float *bias, const int32_t *nbr, int64_t n_rows, int K,
                          const int32_t *order, T *y, int splits, float *partial, hipStream_t s) {
   if constexpr (kIsF32<T>) {
-    return launch_os_lds<T, NT, 1, CSUB, 1, NT == 64 ? 6 : 8, KQ>(x, n_x, cred, wt, ncols, bias,
-                                                                  nbr, n_rows, K, order, y, splits,
-                                                                  partial, s);
+    return launch_os_lds<T, NT, 1, CSUB, 1, NT == 64 ? 6 : 8, KQ>(
+        x, n_x, cred, wt, wperm, ncols, bias, nbr, n_rows, K, order, y, splits, partial, s);
   } else if constexpr (NT == 64 && CSUB == 2) {
-    return launch_os_lds<T, NT, 2, CSUB, 1, 6, KQ>(x, n_x, cred, wt, ncols, bias, nbr, n_rows, K,
-                                                   order, y, splits, partial, s);
+    return launch_os_lds<T, NT, 2, CSUB, 1, 6, KQ>(x, n_x, cred, wt, wperm, ncols, bias, nbr,
+                                                   n_rows, K, order, y, splits, partial, s);
   } else {
     constexpr int W = NT >= 128 ? 4 : (CSUB == 1 && NT >= 64 ? 6 : 8);
     constexpr int G = NT >= 128 ? 2 : (CSUB == 1 ? 4 : 1);
-    return launch_os_lds<T, NT, 1, CSUB, G, W, KQ>(x, n_x, cred, wt, ncols, bias, nbr, n_rows, K,
-                                                   order, y, splits, partial, s);
+    return launch_os_lds<T, NT, 1, CSUB, G, W, KQ>(x, n_x, cred, wt, wperm, ncols, bias, nbr,
+                                                   n_rows, K, order, y, splits, partial, s);
   }
 }
 
 template <typename T, int NT, int KQ>
-static bool os_lds_csub(const T *x, int64_t n_x, int cred, const T *wt, int ncols,
-                        const float *bias, const int32_t *nbr, int64_t n_rows, int K,
+static bool os_lds_csub(const T *x, int64_t n_x, int cred, const T *wt, const int32_t *wperm,
+                        int ncols, const float *bias, const int32_t *nbr, int64_t n_rows, int K,
                         const int32_t *order, T *y, int splits, float *partial,
                         hipStream_t s) {
   constexpr int CH = kChOf<T>;
   if constexpr (kIsF32<T>) {
     if (cred % (4 * CH) == 0)
-      return os_lds_shape<T, NT, 4, KQ>(x, n_x, cred, wt, ncols, bias, nbr, n_rows, K, order, y,
-                                        splits, partial, s);
+      return os_lds_shape<T, NT, 4, KQ>(x, n_x, cred, wt, wperm, ncols, bias, nbr, n_rows, K,
+                                        order, y, splits, partial, s);
   }
   if (cred % (2 * CH) == 0)
-    return os_lds_shape<T, NT, 2, KQ>(x, n_x, cred, wt, ncols, bias, nbr, n_rows, K, order, y,
-                                        splits, partial, s);
-  return os_lds_shape<T, NT, 1, KQ>(x, n_x, cred, wt, ncols, bias, nbr, n_rows, K, order, y,
-                                        splits, partial, s);
+    return os_lds_shape<T, NT, 2, KQ>(x, n_x, cred, wt, wperm, ncols, bias, nbr, n_rows, K, order,
+                                      y, splits, partial, s);
+  return os_lds_shape<T, NT, 1, KQ>(x, n_x, cred, wt, wperm, ncols, bias, nbr, n_rows, K, order,
+                                    y, splits, partial, s);
 }
 
 template <typename T, int KQ>
-static bool run_os_lds_nt(const T *x, int64_t n_x, int cred, const T *wt, int ncols,
-                          const float *bias, const int32_t *nbr, int64_t n_rows, int K,
-                          const int32_t *order, T *y, int splits, float *partial,
+static bool run_os_lds_nt(const T *x, int64_t n_x, int cred, const T *wt, const int32_t *wperm,
+                          int ncols, const float *bias, const int32_t *nbr, int64_t n_rows,
+                          int K, const int32_t *order, T *y, int splits, float *partial,
                           hipStream_t s) {
   const int nt = os_nt<T>(ncols);
   if constexpr (!kIsF32<T>) {
     if (nt == 128)
-      return os_lds_csub<T, 128, KQ>(x, n_x, cred, wt, ncols, bias, nbr, n_rows, K, order, y,
-                                      splits, partial, s);
+      return os_lds_csub<T, 128, KQ>(x, n_x, cred, wt, wperm, ncols, bias, nbr, n_rows, K, order,
+                                     y, splits, partial, s);
   }
   if (nt == 64)
-    return os_lds_csub<T, 64, KQ>(x, n_x, cred, wt, ncols, bias, nbr, n_rows, K, order, y,
-                                      splits, partial, s);
+    return os_lds_csub<T, 64, KQ>(x, n_x, cred, wt, wperm, ncols, bias, nbr, n_rows, K, order, y,
+                                  splits, partial, s);
   if (nt == 32)
-    return os_lds_csub<T, 32, KQ>(x, n_x, cred, wt, ncols, bias, nbr, n_rows, K, order, y,
-                                      splits, partial, s);
-  return os_lds_csub<T, 16, KQ>(x, n_x, cred, wt, ncols, bias, nbr, n_rows, K, order, y,
-                                      splits, partial, s);
+    return os_lds_csub<T, 32, KQ>(x, n_x, cred, wt, wperm, ncols, bias, nbr, n_rows, K, order, y,
+                                  splits, partial, s);
+  return os_lds_csub<T, 16, KQ>(x, n_x, cred, wt, wperm, ncols, bias, nbr, n_rows, K, order, y,
+                                splits, partial, s);
 }
 
 // The fast forward/dX kernel where it applies: at most 96 offsets, no split,
 // unpadded reductions of one, two or four chunks and inputs that 32-bit
 // buffer offsets reach. Returns whether it launched.
 template <typename T>
-static bool run_os_lds(const T *x, int64_t n_x, int cred, const T *wt, int credw, int ncols,
-                       const float *bias, const int32_t *nbr, int64_t n_rows, int K,
-                       const int32_t *order, T *y, int splits, float *partial, hipStream_t s) {
+static bool run_os_lds(const T *x, int64_t n_x, int cred, const T *wt, const int32_t *wperm,
+                       int credw, int ncols, const float *bias, const int32_t *nbr,
+                       int64_t n_rows, int K, const int32_t *order, T *y, int splits,
+                       float *partial, hipStream_t s) {
   if (K > 96 || cred != credw || n_x < 1 || !os_fast(x, cred, wt, credw, ncols, K) ||
       n_x * cred * static_cast<int64_t>(sizeof(T)) > kBufMaxBytes)
     return false;
   if (K > 32)
-    return run_os_lds_nt<T, 24>(x, n_x, cred, wt, ncols, bias, nbr, n_rows, K, order, y, splits,
-                                 partial, s);
-  return run_os_lds_nt<T, 8>(x, n_x, cred, wt, ncols, bias, nbr, n_rows, K, order, y, splits,
-                               partial, s);
+    return run_os_lds_nt<T, 24>(x, n_x, cred, wt, wperm, ncols, bias, nbr, n_rows, K, order, y,
+                                splits, partial, s);
+  return run_os_lds_nt<T, 8>(x, n_x, cred, wt, wperm, ncols, bias, nbr, n_rows, K, order, y,
+                             splits, partial, s);
 }
 
 // Shape of the resident-weight kernel (conv_fr_kernel) for a bf16 map: the
@@ -2393,25 +2405,52 @@ static bool run_fr(const __bf16 *x, int64_t n_x, int cred, const __bf16 *wt, int
   return true;
 }
 
-// y[order[j]] = sum_k x[nbr[k][j]] @ W'[k] with W'[k][c][n] = wt[k][n][c];
-// x has n_x rows. partial: os_partial_floats(...) floats, or null to run
-// without a split.
-// credw: row stride of wt (cred, or the padded reduction of red_width).
+// Weight slices reordered for a table whose row k multiplies slice
+// perm[k]: dst[k][r][c] = src[perm[k]][r][c] ([K][rows][cols], same layout).
+template <typename T>
+__global__ __launch_bounds__(kThreads) void permute_w_kernel(const T *__restrict__ src,
+                                                             const int32_t *__restrict__ perm,
+                                                             int K, int64_t per,
+                                                             T *__restrict__ dst) {
+  const int64_t i = blockIdx.x * static_cast<int64_t>(kThreads) + threadIdx.x;
+  if (i >= K * per)
+    return;
+  const int64_t k = i / per;
+  dst[i] = src[static_cast<int64_t>(perm[k]) * per + i % per];
+}
+
+// y[order[j]] = sum_k x[nbr[k][j]] @ W'[wperm[k]] with W'[k][c][n] = wt[k][n][c]
+// (wperm NULL: the identity); x has n_x rows. partial: os_partial_floats(...)
+// floats, or null to run without a split. credw: row stride of wt (cred, or
+// the padded reduction of red_width). The LDS-indexed kernel reads slice
+// wperm[k] itself; for the other kernels the slices are first copied in
+// table order to wperm_buf (K * ncols * credw elements; required with wperm).
 template <typename T>
 static void run_os(const T *x, int64_t n_x, int cred, const T *wt, int credw, int ncols,
                    const float *bias, const int32_t *nbr, int64_t n_rows, int K,
                    const int32_t *order, T *y, float *partial, hipStream_t s,
-                   bool resident = true) {
+                   bool resident = true, const int32_t *wperm = nullptr,
+                   T *wperm_buf = nullptr) {
   if (n_rows == 0)
     return;
   // the LDS-indexed kernel first: it beats the resident-weight kernel on the
   // maps that took that one (config 5 step 6.01 -> 5.86 ms), and with an
   // offset-axis split it takes the small coarse maps as well
   const int splits = partial ? os_splits<T>(n_rows, credw, ncols, K) : 1;
-  if (run_os_lds(x, n_x, cred, wt, credw, ncols, bias, nbr, n_rows, K, order, y, splits, partial,
-                 s)) {
+  if (run_os_lds(x, n_x, cred, wt, wperm, credw, ncols, bias, nbr, n_rows, K, order, y, splits,
+                 partial, s)) {
     RHIP_LAUNCH_CHECK();
     return;
+  }
+  if (wperm != nullptr) {
+    if (wperm_buf == nullptr)
+      throw Error(RHIP_ERR_INVALID, "a weight permutation needs the workspace for this shape");
+    const int64_t per = static_cast<int64_t>(ncols) * credw;
+    hipLaunchKernelGGL((permute_w_kernel<T>), dim3(static_cast<unsigned>(ceil_div(K * per,
+                                                                                   kThreads))),
+                       dim3(kThreads), 0, s, wt, wperm, K, per, wperm_buf);
+    RHIP_LAUNCH_CHECK();
+    wt = wperm_buf;
   }
   if constexpr (!kIsF32<T>) {
     if (resident && cred == credw &&
@@ -2988,6 +3027,7 @@ extern "C" int rhip_conv_backward_input(const void *grad_y, int64_t n_out,
                                         int32_t cout, const void *weight,
                                         int32_t K, int32_t cin,
                                         const int32_t *nbr_t,
+                                        const int32_t *weight_perm,
                                         const int32_t *in_order, int64_t n_in,
                                         void *grad_x, int32_t dtype,
                                         void *workspace, size_t workspace_bytes,
@@ -3004,31 +3044,37 @@ extern "C" int rhip_conv_backward_input(const void *grad_y, int64_t n_out,
     // MFMA kernels would pad goes to the one-lane-per-output kernel
     float *os_partial = nullptr;
     const void *wk = weight;
+    const int32_t *wperm = weight_perm;
+    void *wperm_buf = nullptr;
     int credw = cout;
     if (workspace != nullptr) {
       Carve cv(workspace, workspace_bytes);
       const ConvWs w = carve_conv_front(cv, K, cin, cout, dtype, n_in, n_out);
       os_partial = w.os_partial;
+      wperm_buf = w.wt;
       if (red_width(dtype, cout) != cout) { // [K][cin][cout] rows padded to credw
         credw = red_width(dtype, cout);
         const int64_t ne = static_cast<int64_t>(K) * cin * credw;
         hipLaunchKernelGGL((pad_rows_kernel<__bf16>), dim3(ceil_div(ne, kThreads)),
                            dim3(kThreads), 0, stream, static_cast<const __bf16 *>(weight),
-                           static_cast<int64_t>(K) * cin, cout, credw,
-                           static_cast<__bf16 *>(w.wt));
+                           static_cast<int64_t>(K) * cin, cout, credw, wperm,
+                           static_cast<int64_t>(cin), static_cast<__bf16 *>(w.wt));
         RHIP_LAUNCH_CHECK();
         wk = w.wt;
+        wperm = nullptr; // applied by the padding copy
       }
     }
     // dX rows gather dY rows; W[k] [cin][cout] is already [n = cin][c = cout].
     if (dtype == RHIP_F32)
       run_os<float>(static_cast<const float *>(grad_y), n_out, cout,
                     static_cast<const float *>(wk), credw, cin, nullptr, nbr_t, n_in, K,
-                    in_order, static_cast<float *>(grad_x), os_partial, stream);
+                    in_order, static_cast<float *>(grad_x), os_partial, stream, true, wperm,
+                    static_cast<float *>(wperm_buf));
     else
       run_os<__bf16>(static_cast<const __bf16 *>(grad_y), n_out, cout,
                      static_cast<const __bf16 *>(wk), credw, cin, nullptr, nbr_t, n_in, K,
-                     in_order, static_cast<__bf16 *>(grad_x), os_partial, stream);
+                     in_order, static_cast<__bf16 *>(grad_x), os_partial, stream, true, wperm,
+                     static_cast<__bf16 *>(wperm_buf));
   });
 }
 
@@ -3093,4 +3139,13 @@ extern "C" int rhip_conv_backward_weight_rows(
                   static_cast<const __bf16 *>(grad_y), n_out, cout, K, nbr, out_order, w.partial,
                   static_cast<__bf16 *>(grad_w), stream);
   });
+}
+
+extern "C" int rhip_conv_backward_weight_rows_supported(int32_t dtype, int32_t cin, int32_t cout,
+                                                        int32_t K, int64_t n_in,
+                                                        int64_t n_out) {
+  if ((dtype != RHIP_F32 && dtype != RHIP_BF16) || K < 1 || cin < 1 || cout < 1 || n_in < 0 ||
+      n_out < 0)
+    return 0;
+  return dw_rows_supported(dtype, cin, cout, K, n_in, n_out) ? 1 : 0;
 }

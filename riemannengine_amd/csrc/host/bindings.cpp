@@ -66,21 +66,40 @@ template <typename Impl> ModuleClass<Impl> bind_unary(py::module_ &m, const char
   return cls;
 }
 
-py::dict kernel_map_dict(const HipKernelMap &m) {
-  py::dict d;
-  d["K"] = m.K;
-  d["n_in"] = m.n_in;
-  d["n_out"] = m.n_out;
-  d["offsets"] = m.offsets;
-  d["offsets_host"] = m.offsets_host;
-  d["in_rows"] = m.in_rows;
-  d["out_rows"] = m.out_rows;
-  d["nbr"] = m.nbr;
-  d["nbr_t"] = m.nbr_t;
-  d["in_order"] = m.in_order;
-  d["out_order"] = m.out_order;
-  d["stride_map"] = m.stride_map;
-  return d;
+// A kernel map's fields by name (the reference's Python callers read maps as
+// dicts); the pair lists and a symmetric map's transposed table are built on
+// first access.
+py::object kernel_map_field(const HipKernelMap &m, const std::string &name) {
+  if (name == "K")
+    return py::int_(m.K);
+  if (name == "n_in")
+    return py::int_(m.n_in);
+  if (name == "n_out")
+    return py::int_(m.n_out);
+  if (name == "offsets")
+    return py::cast(m.offsets);
+  if (name == "offsets_host")
+    return py::cast(m.offsets_host);
+  if (name == "nbr")
+    return py::cast(m.nbr);
+  if (name == "out_order")
+    return py::cast(m.out_order);
+  if (name == "stride_map")
+    return py::bool_(m.stride_map);
+  if (name == "symmetric")
+    return py::bool_(m.symmetric);
+  if (name == "partner")
+    return m.partner.defined() ? py::cast(m.partner) : py::none();
+  if (name == "in_rows" || name == "out_rows") {
+    m.ensure_pairs();
+    return py::cast(name == "in_rows" ? m.in_rows : m.out_rows);
+  }
+  if (name == "nbr_t" || name == "in_order") {
+    if (m.symmetric)
+      m.ensure_transposed();
+    return py::cast(name == "nbr_t" ? m.nbr_t : m.in_order);
+  }
+  throw py::key_error(name);
 }
 
 stride_type as_stride(const std::vector<int64_t> &v) {
@@ -157,6 +176,18 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
       .def("__hash__", &CoordinateMapKey::hash)
       .def("__repr__", &CoordinateMapKey::to_string);
 
+  // a cached map of a manager (alive as long as the manager): fields as
+  // attributes or by name, m["in_rows"]
+  py::class_<HipKernelMap>(m, "KernelMap")
+      .def("__getitem__", &kernel_map_field)
+      .def("__getattr__", &kernel_map_field)
+      .def("__len__", &HipKernelMap::size)
+      .def("__repr__", [](const HipKernelMap &k) {
+        return "KernelMap(K=" + std::to_string(k.K) + ", n_in=" + std::to_string(k.n_in) +
+               ", n_out=" + std::to_string(k.n_out) + ", pairs=" + std::to_string(k.size()) +
+               (k.symmetric ? ", symmetric" : "") + ")";
+      });
+
   py::class_<CoordinateManager, std::shared_ptr<CoordinateManager>>(m, "CoordinateManager")
       .def(py::init([](int dimension, CoordinateMapBackend::Type backend,
                        RiemannAlgorithm::Mode algorithm) {
@@ -202,11 +233,11 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
              const std::vector<int64_t> &kernel_stride, const std::vector<int64_t> &dilation,
              RegionType::Type region, c10::optional<at::Tensor> offsets, bool is_transpose,
              bool is_pool) {
-            return kernel_map_dict(self.kernel_map(
-                in_key, out_key, as_stride(kernel_size), as_stride(kernel_stride),
-                as_stride(dilation), region, offsets.value_or(at::Tensor()), is_transpose,
-                is_pool));
+            return &self.kernel_map(in_key, out_key, as_stride(kernel_size),
+                                    as_stride(kernel_stride), as_stride(dilation), region,
+                                    offsets.value_or(at::Tensor()), is_transpose, is_pool);
           },
+          py::return_value_policy::reference_internal,
           py::arg("in_key"), py::arg("out_key"), py::arg("kernel_size"),
           py::arg("kernel_stride"), py::arg("kernel_dilation"),
           py::arg("region_type") = RegionType::HYPER_CUBE, py::arg("offsets") = py::none(),

@@ -45,12 +45,17 @@ using torch::autograd::tensor_list;
 // Inputs after (features, kernel, bias) are the kernel map's index tensors;
 // they are integer tensors, so autograd gives them no gradient. bias is fp32
 // [cout], or empty for none (autograd needs a defined tensor for every
-// input); the forward adds it to the fp32 sums before rounding.
+// input); the forward adds it to the fp32 sums before rounding. The input
+// gradient runs on (dx_table, dx_order) with weight slice wperm[k] for table
+// row k (wperm empty: k): the transposed table, or for a symmetric map nbr
+// itself with the stencil partners. pairs_dw: the weight gradient takes the
+// pair lists (in_rows, out_rows), else the neighbour table.
 struct HipConvolutionFunction : public torch::autograd::Function<HipConvolutionFunction> {
   static at::Tensor forward(AutogradContext *ctx, at::Tensor features, at::Tensor kernel,
-                            at::Tensor bias, at::Tensor nbr, at::Tensor out_order, at::Tensor nbr_t,
-                            at::Tensor in_order, at::Tensor offsets, at::Tensor in_rows,
-                            at::Tensor out_rows, int64_t n_out, int64_t n_pairs) {
+                            at::Tensor bias, at::Tensor nbr, at::Tensor out_order,
+                            at::Tensor dx_table, at::Tensor dx_order, at::Tensor wperm,
+                            at::Tensor offsets, at::Tensor in_rows, at::Tensor out_rows,
+                            int64_t n_out, int64_t n_pairs, bool pairs_dw) {
     TORCH_CHECK(features.is_cuda() && kernel.is_cuda(),
                 "features and kernel must be device tensors");
     TORCH_CHECK(features.scalar_type() == kernel.scalar_type(),
@@ -78,8 +83,10 @@ struct HipConvolutionFunction : public torch::autograd::Function<HipConvolutionF
                                  ws.data_ptr(), ws.numel(),
                                  c10::hip::getCurrentHIPStream(dev.index()).stream()),
                "rhip_conv_forward");
-    ctx->save_for_backward({x, w, nbr_t, in_order, offsets, in_rows, out_rows, nbr, out_order});
+    ctx->save_for_backward({x, w, dx_table, dx_order, offsets, in_rows, out_rows, nbr, out_order,
+                            wperm});
     ctx->saved_data["n_pairs"] = n_pairs;
+    ctx->saved_data["pairs_dw"] = pairs_dw;
     ctx->saved_data["n_out"] = n_out;
     ctx->saved_data["has_bias"] = has_bias;
     return y;
@@ -87,9 +94,10 @@ struct HipConvolutionFunction : public torch::autograd::Function<HipConvolutionF
 
   static tensor_list backward(AutogradContext *ctx, tensor_list grads) {
     auto saved = ctx->get_saved_variables();
-    auto x = saved[0], w = saved[1], nbr_t = saved[2], in_order = saved[3];
+    auto x = saved[0], w = saved[1], dx_table = saved[2], dx_order = saved[3];
     auto offsets = saved[4], in_rows = saved[5], out_rows = saved[6];
-    auto nbr = saved[7], out_order = saved[8];
+    auto nbr = saved[7], out_order = saved[8], wperm = saved[9];
+    const bool pairs_dw = ctx->saved_data["pairs_dw"].toBool();
     const int64_t n_pairs = ctx->saved_data["n_pairs"].toInt();
     const int64_t n_out = ctx->saved_data["n_out"].toInt();
     const auto dev = x.device();
@@ -112,33 +120,32 @@ struct HipConvolutionFunction : public torch::autograd::Function<HipConvolutionF
       gx = torch::empty_like(x);
       check_rhip(rhip_conv_backward_input(gy.data_ptr(), n_out, static_cast<int32_t>(cout),
                                           w.data_ptr(), K, static_cast<int32_t>(cin),
-                                          nbr_t.data_ptr<int32_t>(),
-                                          in_order.data_ptr<int32_t>(), n_in, gx.data_ptr(), dt,
+                                          dx_table.data_ptr<int32_t>(),
+                                          wperm.numel() > 0 ? wperm.data_ptr<int32_t>() : nullptr,
+                                          dx_order.data_ptr<int32_t>(), n_in, gx.data_ptr(), dt,
                                           ws.data_ptr(), ws.numel(), st),
                  "rhip_conv_backward_input");
     }
     if (need_dw) {
       gw = torch::empty_like(w);
-      // dW from the neighbour table where the library has a kernel for the
-      // shape (K <= 8 or K >= 20 with C_in % 16 and C_out % 32; narrow bf16),
-      // else from the pair list. bf16 maps of at most 8 offsets with fewer
-      // than 2 pairs per output row (a transposed stride-2 map) take the pair
-      // list: config 3's transposed map, 38 us against 46.
-      const bool sparse_small = dt == RHIP_BF16 && K <= 8 && n_pairs < 2 * n_out;
-      int rc = sparse_small ? RHIP_ERR_UNSUPPORTED : rhip_conv_backward_weight_rows(
-          x.data_ptr(), n_in, static_cast<int32_t>(cin), gy.data_ptr(), n_out,
-          static_cast<int32_t>(cout), K, nbr.data_ptr<int32_t>(),
-          out_order.numel() > 0 ? out_order.data_ptr<int32_t>() : nullptr, gw.data_ptr(), dt,
-          ws.data_ptr(), ws.numel(), st);
-      if (rc == RHIP_ERR_UNSUPPORTED)
+      int rc;
+      if (!pairs_dw) {
+        rc = rhip_conv_backward_weight_rows(
+            x.data_ptr(), n_in, static_cast<int32_t>(cin), gy.data_ptr(), n_out,
+            static_cast<int32_t>(cout), K, nbr.data_ptr<int32_t>(),
+            out_order.numel() > 0 ? out_order.data_ptr<int32_t>() : nullptr, gw.data_ptr(), dt,
+            ws.data_ptr(), ws.numel(), st);
+      } else {
+        TORCH_CHECK(in_rows.numel() == n_pairs, "the kernel map's pair lists were not built");
         rc = rhip_conv_backward_weight(x.data_ptr(), n_in, static_cast<int32_t>(cin),
                                        gy.data_ptr(), n_out, static_cast<int32_t>(cout), K,
                                        offsets.data_ptr<int64_t>(), n_pairs,
                                        in_rows.data_ptr<int32_t>(), out_rows.data_ptr<int32_t>(),
                                        gw.data_ptr(), dt, ws.data_ptr(), ws.numel(), st);
+      }
       check_rhip(rc, "rhip_conv_backward_weight(_rows)");
     }
-    return {gx, gw, gb, {}, {}, {}, {}, {}, {}, {}, {}, {}};
+    return {gx, gw, gb, {}, {}, {}, {}, {}, {}, {}, {}, {}, {}, {}};
   }
 };
 
@@ -153,9 +160,31 @@ at::Tensor hip_sparse_convolution(const at::Tensor &features, const at::Tensor &
   const at::Tensor b =
       bias.defined() ? bias
                      : torch::empty({0}, features.options().dtype(torch::kFloat));
-  return HipConvolutionFunction::apply(features, kernel, b, map.nbr, map.out_order, map.nbr_t,
-                                       map.in_order, map.offsets, map.in_rows, map.out_rows,
-                                       map.n_out, map.size());
+  // dW from the neighbour table where the library has a kernel for the
+  // shape, else from the pair lists (built now, once per map, when a weight
+  // gradient may follow). bf16 maps of at most 8 offsets with fewer than 2
+  // pairs per output row (a transposed stride-2 map) take the pair lists:
+  // config 3's transposed map, 38 us against 46.
+  const int32_t dt = rhip_dtype(features);
+  const bool sparse_small = dt == RHIP_BF16 && map.K <= 8 && map.size() < 2 * map.n_out;
+  const bool pairs_dw =
+      sparse_small || rhip_conv_backward_weight_rows_supported(
+                          dt, static_cast<int32_t>(kernel.size(1)),
+                          static_cast<int32_t>(kernel.size(2)), map.K, map.n_in, map.n_out) == 0;
+  const auto iempty = torch::empty({0}, map.nbr.options());
+  at::Tensor in_rows = iempty, out_rows = iempty;
+  if (pairs_dw && kernel.requires_grad() && torch::autograd::GradMode::is_enabled()) {
+    map.ensure_pairs();
+    in_rows = map.in_rows;
+    out_rows = map.out_rows;
+  }
+  if (!map.symmetric)
+    return HipConvolutionFunction::apply(features, kernel, b, map.nbr, map.out_order, map.nbr_t,
+                                         map.in_order, iempty, map.offsets, in_rows, out_rows,
+                                         map.n_out, map.size(), pairs_dw);
+  return HipConvolutionFunction::apply(features, kernel, b, map.nbr, map.out_order, map.nbr,
+                                       map.out_order, map.partner, map.offsets, in_rows, out_rows,
+                                       map.n_out, map.size(), pairs_dw);
 }
 
 // ------------------------------------------------------------ layers

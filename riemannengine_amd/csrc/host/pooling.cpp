@@ -230,6 +230,8 @@ at::Tensor hip_sparse_pooling(const at::Tensor &features, const HipKernelMap &ma
   TORCH_CHECK(is_local(mode), "Local pooling requires a local pooling mode");
   TORCH_CHECK(features.dim() == 2 && features.size(0) == map.n_in, "feature rows ",
               features.size(0), " != input map size ", map.n_in);
+  if (map.symmetric)
+    map.ensure_transposed();
   return HipPoolingFunction::apply(features, map.nbr, map.out_order, map.nbr_t, map.in_order,
                                    map.n_out, pool_reduction(mode));
 }

@@ -188,23 +188,39 @@ struct CoordinateMapHIP {
   int64_t size() const { return table.n_unique; }
 };
 
-// A kernel map: per-offset pair lists (CSR) plus the dense neighbour tables
-// and processing orders the convolution kernels consume. A pooling stride map
-// (stride_map set) has the reference's single pair list (offsets = [0, P]),
-// an nbr K rows high (K = most inputs on one output) and a one-row nbr_t
-// (each input has one output); swapped() exchanges the two tables.
+// A kernel map: the dense neighbour table and processing order the
+// convolution kernels consume, the per-offset pair counts (CSR) and, built on
+// first use, the per-offset pair lists and the transposed table. A pooling
+// stride map (stride_map set) has the reference's single pair list (offsets
+// = [0, P]), an nbr K rows high (K = most inputs on one output) and a one-row
+// nbr_t (each input has one output); swapped() exchanges the two tables.
+// A symmetric map (a set onto itself, stencil closed under negation) keeps
+// no transposed table: its input gradient runs on nbr with the stencil
+// partners as weight permutation (rhip_conv_backward_input).
 struct HipKernelMap {
   int32_t K = 0;
   bool stride_map = false;
+  bool symmetric = false;
   int64_t n_in = 0, n_out = 0;
   std::vector<int64_t> offsets_host; // [K+1]
   at::Tensor offsets;                // device int64 [K+1]
-  at::Tensor in_rows, out_rows;      // int32 [P]
   at::Tensor nbr;                    // int32 [K, n_out], -1 = no neighbour
-  at::Tensor nbr_t;                  // int32 [K, n_in]
-  at::Tensor in_order, out_order;    // int32 processing orders
+  at::Tensor out_order;              // int32 output processing order
+  std::vector<int32_t> partner_host; // symmetric: the offset that negates each offset
+  at::Tensor partner;                // the same on the device (int32 [K])
+  // built on first use (a cached map is shared as const): ensure_pairs(),
+  // ensure_transposed()
+  mutable at::Tensor in_rows, out_rows; // int32 [P]
+  mutable at::Tensor nbr_t;             // int32 [K, n_in]
+  mutable at::Tensor in_order;          // int32 input processing order
   int64_t size() const { return offsets_host.empty() ? 0 : offsets_host.back(); }
-  // in and out exchanged (transposed convolution), zero copy
+  // the pair lists from the table (rhip_kmap_pairs), once
+  void ensure_pairs() const;
+  // the transposed table of a symmetric map (rows of nbr under the partner
+  // offsets) and its input order (the output order), once
+  void ensure_transposed() const;
+  // in and out exchanged (transposed convolution), zero copy once both
+  // sides are built
   HipKernelMap swapped() const;
   // the reference's cpu_kernel_map layout: (in rows per offset, out rows per
   // offset), as int64 device tensors

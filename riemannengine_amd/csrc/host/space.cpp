@@ -251,7 +251,56 @@ KernelGenerator::KernelParams KernelGenerator::get_kernel(const stride_type &ten
 
 // --------------------------------------------------------- kernel maps
 
+void HipKernelMap::ensure_pairs() const {
+  if (in_rows.defined())
+    return;
+  const auto dev = nbr.device();
+  at::DeviceGuard guard(dev);
+  const int64_t P = size();
+  auto iopt = torch::TensorOptions().device(dev).dtype(torch::kInt32);
+  // exact size: the pair counts are known
+  auto ir = torch::empty({std::max<int64_t>(P, 1)}, iopt);
+  auto orr = torch::empty({std::max<int64_t>(P, 1)}, iopt);
+  if (P > 0) {
+    size_t bytes = 0;
+    check_rhip(rhip_kmap_pairs_workspace_bytes(n_out, K, &bytes),
+               "rhip_kmap_pairs_workspace_bytes");
+    auto ws = device_bytes(bytes, dev);
+    check_rhip(rhip_kmap_pairs(nbr.data_ptr<int32_t>(), out_order.data_ptr<int32_t>(), n_out, K,
+                               offsets.data_ptr<int64_t>(), ws.data_ptr(), ws.numel(),
+                               ir.data_ptr<int32_t>(), orr.data_ptr<int32_t>(),
+                               current_stream(dev)),
+               "rhip_kmap_pairs");
+  }
+  in_rows = ir.slice(0, 0, P);
+  out_rows = orr.slice(0, 0, P);
+}
+
+void HipKernelMap::ensure_transposed() const {
+  if (nbr_t.defined())
+    return;
+  TORCH_CHECK(symmetric && static_cast<int32_t>(partner_host.size()) == K,
+              "this kernel map has no transposed table");
+  const auto dev = nbr.device();
+  at::DeviceGuard guard(dev);
+  const hipStream_t st = current_stream(dev);
+  // i pairs with o under k iff o pairs with i under partner[k]: row k of
+  // the table is row partner[k] of the transposed one
+  auto t = torch::empty({K, std::max<int64_t>(n_in, 1)}, nbr.options());
+  const size_t row = static_cast<size_t>(n_out) * sizeof(int32_t);
+  for (int32_t k = 0; k < K && n_out > 0; ++k)
+    check_hip(hipMemcpyAsync(t.data_ptr<int32_t>() + static_cast<int64_t>(partner_host[k]) * n_in,
+                             nbr.data_ptr<int32_t>() + static_cast<int64_t>(k) * n_out, row,
+                             hipMemcpyDeviceToDevice, st),
+              "hipMemcpyAsync");
+  nbr_t = t.slice(1, 0, n_in);
+  in_order = out_order;
+}
+
 HipKernelMap HipKernelMap::swapped() const {
+  ensure_pairs();
+  if (symmetric)
+    ensure_transposed();
   HipKernelMap m;
   m.K = K;
   m.stride_map = stride_map;
@@ -269,6 +318,7 @@ HipKernelMap HipKernelMap::swapped() const {
 }
 
 std::pair<std::vector<at::Tensor>, std::vector<at::Tensor>> HipKernelMap::per_offset() const {
+  ensure_pairs();
   std::vector<at::Tensor> ins, outs;
   for (int k = 0; k < (stride_map ? 1 : K); ++k) {
     const int64_t a = offsets_host[k], b = offsets_host[k + 1];
@@ -480,25 +530,33 @@ HipKernelMap CoordinateManager::generate(const CoordinateMapHIP &in_map,
   auto out_order = torch::empty({std::max<int64_t>(n_out, 1)}, iopt);
   m.offsets = torch::empty({K + 1}, iopt.dtype(torch::kInt64));
   int32_t flags = 0;
-  // count and fill go back to back: the pair lists are sized by the bound
-  // K * n_out, and the pair counts are read once, after the fill
   check_rhip(rhip_kmap_count(&in_map.table, out_map.coords.data_ptr<int32_t>(),
                              out_map.order.data_ptr<int32_t>(), n_out, K,
                              offsets.data_ptr<int32_t>(), ws.data_ptr(), ws.numel(),
                              nbr.data_ptr<int32_t>(), out_order.data_ptr<int32_t>(),
                              m.offsets.data_ptr<int64_t>(), nullptr, &flags, st),
              "rhip_kmap_count");
-  const int64_t p_bound = static_cast<int64_t>(K) * n_out;
-  auto in_rows = torch::empty({std::max<int64_t>(p_bound, 1)}, iopt);
-  auto out_rows = torch::empty({std::max<int64_t>(p_bound, 1)}, iopt);
-  auto nbr_t = torch::empty({K, std::max<int64_t>(n_in, 1)}, iopt);
-  auto in_order = torch::empty({std::max<int64_t>(n_in, 1)}, iopt);
-  check_rhip(rhip_kmap_fill(nbr.data_ptr<int32_t>(), out_order.data_ptr<int32_t>(), n_out, K,
-                            in_map.order.data_ptr<int32_t>(), n_in, flags, ws.data_ptr(),
-                            ws.numel(), m.offsets.data_ptr<int64_t>(),
-                            in_rows.data_ptr<int32_t>(), out_rows.data_ptr<int32_t>(),
-                            nbr_t.data_ptr<int32_t>(), in_order.data_ptr<int32_t>(), st),
-             "rhip_kmap_fill");
+  // A symmetric map keeps no transposed table (its input gradient runs on
+  // nbr with the stencil partners as weight permutation); any other map gets
+  // its transposed table and input order now. Pair lists wait for a caller
+  // that needs them (ensure_pairs), sized exactly then.
+  m.symmetric = (flags & RHIP_KMAP_SYMMETRIC) != 0;
+  at::Tensor nbr_t, in_order;
+  if (m.symmetric) {
+    m.partner_host.resize(K);
+    check_rhip(rhip_stencil_partners(offsets.data_ptr<int32_t>(), K,
+                                     static_cast<int32_t>(offsets.size(1)),
+                                     m.partner_host.data()),
+               "rhip_stencil_partners");
+  } else {
+    nbr_t = torch::empty({K, std::max<int64_t>(n_in, 1)}, iopt);
+    in_order = torch::empty({std::max<int64_t>(n_in, 1)}, iopt);
+    check_rhip(rhip_kmap_fill(nbr.data_ptr<int32_t>(), out_order.data_ptr<int32_t>(), n_out, K,
+                              in_map.order.data_ptr<int32_t>(), n_in, flags, ws.data_ptr(),
+                              ws.numel(), m.offsets.data_ptr<int64_t>(), nullptr, nullptr,
+                              nbr_t.data_ptr<int32_t>(), in_order.data_ptr<int32_t>(), st),
+               "rhip_kmap_fill");
+  }
   // the one synchronisation: the pair counts through pinned memory (a copy
   // to pageable memory goes through a staging copy)
   auto host_offsets = torch::empty({K + 1}, torch::TensorOptions().dtype(torch::kInt64).pinned_memory(true));
@@ -506,13 +564,14 @@ HipKernelMap CoordinateManager::generate(const CoordinateMapHIP &in_map,
   check_hip(hipStreamSynchronize(st), "hipStreamSynchronize");
   const int64_t *ho = host_offsets.data_ptr<int64_t>();
   m.offsets_host.assign(ho, ho + K + 1);
-  const int64_t P = m.offsets_host[K];
-  m.in_rows = in_rows.slice(0, 0, P);
-  m.out_rows = out_rows.slice(0, 0, P);
+  if (m.symmetric) // after the synchronisation: no pageable copy in flight
+    m.partner = torch::from_blob(m.partner_host.data(), {K}, torch::kInt32).to(dev);
   m.nbr = nbr.slice(1, 0, n_out);
-  m.nbr_t = nbr_t.slice(1, 0, n_in);
-  m.in_order = in_order.slice(0, 0, n_in);
   m.out_order = out_order.slice(0, 0, n_out);
+  if (!m.symmetric) {
+    m.nbr_t = nbr_t.slice(1, 0, n_in);
+    m.in_order = in_order.slice(0, 0, n_in);
+  }
   return m;
 }
 
@@ -604,6 +663,8 @@ const HipKernelMap &CoordinateManager::kernel_map(
   // input side of a strided map uses few of the K offsets.
   auto store_pool = [&](HipKernelMap m) -> const HipKernelMap & {
     if (is_pool && !m.stride_map && m.n_in > 0 && m.K > 1) {
+      if (m.symmetric) // pooling reduces through the transposed table itself
+        m.ensure_transposed();
       const auto dev = m.nbr_t.device();
       at::DeviceGuard guard(dev);
       auto src = m.nbr_t.contiguous();

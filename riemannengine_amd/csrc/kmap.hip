@@ -349,12 +349,31 @@ __global__ __launch_bounds__(kMapBlock) void kmap_emit_kernel(
   }
   const uint64_t b = __ballot(v >= 0);
   if (v >= 0) {
-    const int64_t q = kofs[k] + wave_base[k * nw + w] + lanes_below(b);
-    in_rows[q] = v;
-    out_rows[q] = out_order[p];
+    if (in_rows != nullptr) { // pair lists requested
+      const int64_t q = kofs[k] + wave_base[k * nw + w] + lanes_below(b);
+      in_rows[q] = v;
+      out_rows[q] = out_order[p];
+    }
     if (mask_t)
       atomicOr(&mask_t[2 * static_cast<int64_t>(v) + (k >> 6)], 1ull << (k & 63));
   }
+}
+
+// Hits of each wave and offset in a finished table (lane per processing
+// position p, offset k = blockIdx.y): wave_counts[k][w], as the query pass
+// counts them, for pair lists emitted after the build.
+__global__ __launch_bounds__(kMapBlock) void kmap_wave_count_kernel(
+    const int32_t *__restrict__ nbr, int64_t n_out, int64_t nw,
+    int32_t *__restrict__ wave_counts) {
+  const int k = blockIdx.y;
+  const int64_t p = blockIdx.x * (int64_t)kMapBlock + threadIdx.x;
+  const int64_t w = p / kWave;
+  if (w >= nw)
+    return;
+  const int32_t v = p < n_out ? nbr[k * n_out + p] : -1;
+  const uint64_t b = __ballot(v >= 0);
+  if (lane_id() == 0)
+    wave_counts[k * nw + w] = __popcll(b);
 }
 
 __global__ __launch_bounds__(kMapBlock) void in_key_kernel(
@@ -638,7 +657,10 @@ extern "C" int rhip_kmap_fill(const int32_t *nbr, const int32_t *out_order, int6
       RHIP_LAUNCH_CHECK();
     }
     const bool fuse_t = want_t && sym; // the emit writes nbr_t and in_order
-    if (n_out > 0) {
+    RHIP_CHECK_ARG((in_rows == nullptr) == (out_rows == nullptr),
+                   "in_rows and out_rows go together");
+    // nothing to emit: no pair lists, no transposed masks, no symmetric copy
+    if (n_out > 0 && (in_rows != nullptr || masks || fuse_t)) {
       RHIP_CHECK_ARG(nbr && out_order, "nbr and out_order are required");
       hipLaunchKernelGGL(kmap_emit_kernel, dim3(nb, K), dim3(kMapBlock), 0, stream, nbr,
                          out_order, n_out, nw, kmap_offsets, w.wave_base, in_rows, out_rows,
@@ -668,6 +690,78 @@ extern "C" int rhip_kmap_fill(const int32_t *nbr, const int32_t *out_order, int6
       hipLaunchKernelGGL(kmap_transpose_kernel, dim3(nb, K), dim3(kMapBlock), 0, stream,
                          nbr, out_order, n_out, w.in_pos, n_in, nbr_t);
       RHIP_LAUNCH_CHECK();
+    }
+  });
+}
+
+extern "C" int rhip_kmap_pairs_workspace_bytes(int64_t n_out, int32_t K, size_t *bytes) {
+  return guarded([&] {
+    RHIP_CHECK_ARG(bytes != nullptr, "bytes is null");
+    RHIP_CHECK_ARG(n_out >= 0 && K >= 1, "need n_out >= 0 and K >= 1");
+    const int64_t nw = map_waves(n_out);
+    Carve cv(nullptr, 0); // the layout rhip_kmap_pairs carves
+    cv.take<int32_t>(nw * K);
+    cv.take<int64_t>(nw * K);
+    cv.take<int64_t>(K);
+    *bytes = cv.used + 256;
+  });
+}
+
+extern "C" int rhip_kmap_pairs(const int32_t *nbr, const int32_t *out_order, int64_t n_out,
+                               int32_t K, const int64_t *kmap_offsets, void *workspace,
+                               size_t workspace_bytes, int32_t *in_rows, int32_t *out_rows,
+                               hipStream_t stream) {
+  return guarded([&] {
+    RHIP_CHECK_ARG(K >= 1 && K <= 65535, "K must be in [1, 65535]");
+    RHIP_CHECK_ARG(n_out >= 0 && n_out < INT32_MAX, "bad n_out");
+    RHIP_CHECK_ARG(workspace != nullptr && kmap_offsets != nullptr,
+                   "workspace and kmap_offsets are required");
+    if (n_out == 0)
+      return;
+    RHIP_CHECK_ARG(nbr && out_order && in_rows && out_rows,
+                   "nbr, out_order, in_rows and out_rows are required");
+    const int64_t nw = map_waves(n_out);
+    const int64_t nb = std::max<int64_t>(1, ceil_div(n_out, kMapBlock));
+    Carve cv(workspace, workspace_bytes);
+    int32_t *counts = cv.take<int32_t>(nw * K);
+    int64_t *base = cv.take<int64_t>(nw * K);
+    int64_t *total = cv.take<int64_t>(K);
+    hipLaunchKernelGGL(kmap_wave_count_kernel, dim3(nb, K), dim3(kMapBlock), 0, stream, nbr,
+                       n_out, nw, counts);
+    RHIP_LAUNCH_CHECK();
+    hipLaunchKernelGGL(scan_kernel<int32_t>, dim3(K), dim3(1024), 0, stream, counts, nw, base,
+                       total);
+    RHIP_LAUNCH_CHECK();
+    hipLaunchKernelGGL(kmap_emit_kernel, dim3(nb, K), dim3(kMapBlock), 0, stream, nbr, out_order,
+                       n_out, nw, kmap_offsets, base, in_rows, out_rows, nullptr, nullptr, K,
+                       nullptr, nullptr);
+    RHIP_LAUNCH_CHECK();
+  });
+}
+
+extern "C" int rhip_stencil_partners(const int32_t *offsets_host, int32_t K, int32_t D,
+                                     int32_t *partner_host) {
+  return guarded([&] {
+    RHIP_CHECK_ARG(offsets_host && partner_host, "offsets_host and partner_host are required");
+    RHIP_CHECK_ARG(K >= 1 && D >= 1 && D < RHIP_MAX_COLS, "bad K or D");
+    for (int a = 0; a < K; ++a) {
+      int32_t found = -1;
+      for (int b = 0; b < K; ++b) {
+        bool same = b != a, neg = true;
+        for (int d = 0; d < D; ++d) {
+          const int32_t oa = offsets_host[static_cast<size_t>(a) * D + d];
+          const int32_t ob = offsets_host[static_cast<size_t>(b) * D + d];
+          same = same && oa == ob;
+          neg = neg && static_cast<uint32_t>(ob) == 0u - static_cast<uint32_t>(oa);
+        }
+        if (same)
+          throw Error(RHIP_ERR_UNSUPPORTED, "the stencil repeats an offset");
+        if (neg)
+          found = b;
+      }
+      if (found < 0)
+        throw Error(RHIP_ERR_UNSUPPORTED, "the stencil is not closed under negation");
+      partner_host[a] = found;
     }
   });
 }

@@ -32,7 +32,7 @@ def test_library_exports_every_declared_symbol():
 
 
 def test_abi_version_and_struct_layout():
-    assert abi.lib().rhip_abi_version() == 12
+    assert abi.lib().rhip_abi_version() == 13
     # void*, int64, void*, int64, 3 x int32, 4 x int32[8] (172 bytes, padded to 176),
     # 2 x void*, 2 x int32, int32[8] -> 232 bytes
     assert ctypes.sizeof(abi.RhipTable) == 232
@@ -82,3 +82,24 @@ def test_cpu_tensors_are_rejected():
     import torch
     with pytest.raises(RuntimeError, match="device tensor"):
         abi.hash_build(torch.zeros((4, 4), dtype=torch.int32))
+
+
+def test_stencil_partners_and_rows_query_without_a_gpu():
+    """rhip_stencil_partners (host only): the 3^3 cube's offsets negate in
+    reverse enumeration order (k -> 26 - k), the cross stencil pairs +r with
+    -r, the even 2^3 cube has no partners; rhip_conv_backward_weight_rows_
+    supported answers without a GPU."""
+    import numpy as np
+    import oracle
+    p = abi.stencil_partners(oracle.region_offsets(3, 3))
+    assert p is not None and list(p) == list(range(26, -1, -1))
+    off = oracle.region_offsets(3, 5, region="cross")
+    p = abi.stencil_partners(off)
+    assert p is not None and np.array_equal(off[p], -off)
+    assert abi.stencil_partners(oracle.region_offsets(3, 2)) is None
+    assert abi.stencil_partners(np.array([[1, 0], [-1, 0], [1, 0]], np.int32)) is None
+    L = abi.lib()
+    assert L.rhip_conv_backward_weight_rows_supported(abi.F32, 64, 64, 27, 1000, 1000) == 1
+    assert L.rhip_conv_backward_weight_rows_supported(abi.F32, 64, 64, 13, 1000, 1000) == 0
+    assert L.rhip_conv_backward_weight_rows_supported(abi.BF16, 16, 32, 13, 1000, 1000) == 1
+    assert L.rhip_conv_backward_weight_rows_supported(7, 64, 64, 27, 1000, 1000) == 0

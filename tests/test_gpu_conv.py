@@ -91,8 +91,25 @@ def test_fast_forward_kernel_equals_general_kernel(cin, cout, dtype, extra):
     w27, wx = to_dev(w[:27], dtype), to_dev(w, dtype)
     print(f"fast vs K={27 + extra} kernel cin={cin} cout={cout} {dtype}", flush=True)
     assert torch.equal(abi.conv_forward(x, w27, km27), abi.conv_forward(x, wx, kmx))
-    assert torch.equal(abi.conv_backward_input(gy, w27, km27),
+    # the 3^3 map is symmetric: its usual input gradient runs on nbr with
+    # partner weights (offsets summed in another order); over its transposed
+    # table it adds them in ascending order like the K = 33 / 97 map
+    assert not kmx.symmetric and km27.symmetric
+    assert torch.equal(_dx_over_transposed_table(gy, w27, km27),
                        abi.conv_backward_input(gy, wx, kmx))
+
+
+def _dx_over_transposed_table(gy, w, km):
+    """The input gradient over the map's transposed table (built from nbr's
+    rows for a symmetric map) without a weight permutation."""
+    K, cin, cout = w.shape
+    gx = torch.empty((km.n_in, cin), dtype=gy.dtype, device=gy.device)
+    ws = abi._conv_fwd_ws(K, cin, cout, abi._dtype_code(gy.dtype), gy.device, km)
+    abi._check(abi.lib().rhip_conv_backward_input(
+        abi._ptr(gy), km.n_out, cout, abi._ptr(w), K, cin, abi._ptr(km.nbr_t), None,
+        abi._ptr(km.in_order), km.n_in, abi._ptr(gx), abi._dtype_code(gy.dtype), abi._ptr(ws),
+        ws.numel(), abi._stream(gy.device)), "rhip_conv_backward_input")
+    return gx
 
 
 def test_conv_bias_fp32():
@@ -118,7 +135,7 @@ def test_offset_split_matches_unsplit_and_oracle(dtype):
     split = abi.conv_backward_input(gy, w, km)
     plain = torch.empty_like(split)
     abi._check(abi.lib().rhip_conv_backward_input(
-        abi._ptr(gy), km.n_out, 256, abi._ptr(w), 27, 256, abi._ptr(km.nbr_t),
+        abi._ptr(gy), km.n_out, 256, abi._ptr(w), 27, 256, abi._ptr(km.nbr_t), None,
         abi._ptr(km.in_order), km.n_in, abi._ptr(plain), abi._dtype_code(dtype), None, 0,
         abi._stream(gy.device)), "rhip_conv_backward_input")
     assert_rel(split.float().cpu().numpy(), plain.float().cpu().numpy(),
@@ -595,3 +612,53 @@ def test_config4_4d_full_size():
     assert_rel(gx.cpu().numpy(), rgx.cpu().numpy(), 1e-4, "dX")
     assert_rel(gw.cpu().numpy(), rgw.cpu().numpy(), 1e-4, "dW (pair list)")
     assert_rel(gw_timed.cpu().numpy(), rgw.cpu().numpy(), 1e-4, "dW (timed dispatch)")
+
+
+@pytest.mark.parametrize("cin,cout,dtype", [
+    (64, 64, torch.float32), (64, 64, torch.bfloat16), (32, 128, torch.bfloat16),
+    (3, 5, torch.float32), (16, 48, torch.bfloat16)])
+def test_symmetric_input_gradient_runs_on_nbr_with_partner_weights(cin, cout, dtype):
+    """A symmetric map's input gradient runs on its forward table nbr with
+    the stencil partners as weight permutation (the LDS-indexed kernel reads
+    slice partner[k] itself; the generic kernel (3->5) and the padded bf16
+    reduction (48 output channels) copy the reordered weights first). It
+    equals the input gradient over the materialised transposed table
+    without a permutation (the sums run in another offset order: within the
+    dtype's rounding) and the oracle's."""
+    rng = np.random.default_rng(cin * 5 + cout)
+    c, _, _ = oracle.insert_and_map(random_coords(rng, 12000, 3, 15))
+    _, _, km = gpu_tables_and_map(c, c, oracle.region_offsets(3, 3), same=True)
+    assert km.symmetric
+    w = to_dev((rng.standard_normal((27, cin, cout)) / np.sqrt(27 * cout)).astype(np.float32),
+               dtype)
+    gy = to_dev(rng.standard_normal((km.n_out, cout)).astype(np.float32), dtype)
+    print(f"symmetric dX cin={cin} cout={cout} {dtype}", flush=True)
+    got = abi.conv_backward_input(gy, w, km)  # nbr + partner permutation
+    ref = torch.empty_like(got)
+    ws = abi._conv_fwd_ws(27, cin, cout, abi._dtype_code(dtype), DEV, km)
+    abi._check(abi.lib().rhip_conv_backward_input(
+        abi._ptr(gy), km.n_out, cout, abi._ptr(w), 27, cin, abi._ptr(km.nbr_t), None,
+        abi._ptr(km.in_order), km.n_in, abi._ptr(ref), abi._dtype_code(dtype), abi._ptr(ws),
+        ws.numel(), abi._stream(DEV)), "rhip_conv_backward_input")
+    torch.cuda.synchronize()
+    tol = 1e-5 if dtype == torch.float32 else 1e-2
+    assert_rel(got.float().cpu().numpy(), ref.float().cpu().numpy(), tol, "perm vs nbr_t")
+    _, rgx, _ = _oracle_conv(km, np.zeros((km.n_in, cin), np.float32),
+                             w.float().cpu().numpy(), gy.float().cpu().numpy())
+    assert_rel(got.float().cpu().numpy(), rgx, TOL[dtype], "dX vs oracle")
+
+
+def test_weight_permutation_outside_the_lds_kernel_needs_the_workspace():
+    """Without a workspace a weight permutation is refused (RHIP_ERR_INVALID)
+    for a shape the LDS-indexed kernel does not take, before any launch."""
+    rng = np.random.default_rng(2)
+    c, _, _ = oracle.insert_and_map(random_coords(rng, 2000, 3, 10))
+    _, _, km = gpu_tables_and_map(c, c, oracle.region_offsets(3, 3), same=True)
+    gy = to_dev(rng.standard_normal((km.n_out, 5)).astype(np.float32))
+    w = to_dev(rng.standard_normal((27, 3, 5)).astype(np.float32))
+    gx = torch.empty((km.n_in, 3), device=DEV)
+    st = abi.lib().rhip_conv_backward_input(abi._ptr(gy), km.n_out, 5, abi._ptr(w), 27, 3,
+                                            abi._ptr(km.nbr), abi._ptr(km.partner),
+                                            abi._ptr(km.out_order), km.n_in, abi._ptr(gx),
+                                            abi.F32, None, 0, abi._stream(DEV))
+    assert st == 1 and "workspace" in abi.lib().rhip_last_error().decode()

@@ -309,3 +309,64 @@ def test_kmap_count_with_host_readback_matches_async():
     np.testing.assert_array_equal(kofs.cpu().numpy(), km.offsets_host)
     assert torch.equal(nbr, km.nbr) and torch.equal(order, km.out_order)
     assert bool(flags.value & abi.KMAP_SYMMETRIC) == km.symmetric
+
+
+@pytest.mark.parametrize("same", [True, False])
+def test_lazy_pair_lists_equal_the_fill_emission(same):
+    """rhip_kmap_pairs (the pair lists built from a finished table, as the
+    maps now do on first use) writes exactly what rhip_kmap_fill emits when
+    given pair buffers: same pairs, same order. same=True is a symmetric map
+    (its fill then writes the transposed table too), False the general path."""
+    rng = np.random.default_rng(31)
+    c, _, _ = oracle.insert_and_map(random_coords(rng, 30000, 3, 16))
+    off = oracle.region_offsets(3, 3)
+    tin = abi.hash_build(to_dev(c))
+    tout = tin if same else abi.hash_build(to_dev(c))
+    km = abi.kernel_map(tin, tout, off)
+    assert km.symmetric == same
+    L = abi.lib()
+    K, n_in, n_out, P = km.K, km.n_in, km.n_out, km.n_pairs
+    ws = torch.empty(abi._sizeq(L.rhip_kmap_workspace_bytes, n_in, n_out, K), dtype=torch.uint8,
+                     device=DEV)
+    nbr = torch.empty((K, n_out), dtype=torch.int32, device=DEV)
+    order = torch.empty(n_out, dtype=torch.int32, device=DEV)
+    kofs = torch.empty(K + 1, dtype=torch.int64, device=DEV)
+    flags = abi.ctypes.c_int32(0)
+    o = np.ascontiguousarray(off, np.int32)
+    abi._check(L.rhip_kmap_count(abi.ctypes.byref(tin.struct), abi._ptr(tout.ucoords),
+                                 abi._ptr(tout.order), n_out, K,
+                                 o.ctypes.data_as(abi.ctypes.POINTER(abi.ctypes.c_int32)),
+                                 abi._ptr(ws), ws.numel(), abi._ptr(nbr), abi._ptr(order),
+                                 abi._ptr(kofs), None, abi.ctypes.byref(flags), abi._stream(DEV)),
+               "rhip_kmap_count")
+    ir = torch.empty(K * n_out, dtype=torch.int32, device=DEV)
+    orr = torch.empty(K * n_out, dtype=torch.int32, device=DEV)
+    nbr_t = torch.empty((K, n_in), dtype=torch.int32, device=DEV)
+    in_order = torch.empty(n_in, dtype=torch.int32, device=DEV)
+    abi._check(L.rhip_kmap_fill(abi._ptr(nbr), abi._ptr(order), n_out, K, abi._ptr(tin.order),
+                                n_in, flags.value, abi._ptr(ws), ws.numel(), abi._ptr(kofs),
+                                abi._ptr(ir), abi._ptr(orr), abi._ptr(nbr_t),
+                                abi._ptr(in_order), abi._stream(DEV)), "rhip_kmap_fill")
+    torch.cuda.synchronize()
+    assert torch.equal(nbr, km.nbr) and torch.equal(order, km.out_order)
+    assert torch.equal(ir[:P], km.in_rows) and torch.equal(orr[:P], km.out_rows)
+    # the transposed table of a symmetric map built from nbr's rows equals
+    # the one the fill writes
+    assert torch.equal(nbr_t, km.nbr_t) and torch.equal(in_order, km.in_order)
+
+
+def test_symmetric_map_partners_are_the_negated_offsets():
+    """A symmetric map's partner offsets negate its stencil, and its pair
+    lists are the swapped pair lists under the partner offset."""
+    rng = np.random.default_rng(8)
+    c, _, _ = oracle.insert_and_map(random_coords(rng, 8000, 3, 12))
+    off = oracle.region_offsets(3, 3, 2)
+    _, _, km = gpu_tables_and_map(c, c, off, same=True)
+    assert km.symmetric
+    p = km.partner.cpu().numpy()
+    np.testing.assert_array_equal(off[p], -off)
+    for k in range(km.K):
+        a, b = km.pairs(k)
+        ta, tb = km.pairs(int(p[k]))
+        got = sorted(zip(a.cpu().tolist(), b.cpu().tolist()))
+        assert got == sorted(zip(tb.cpu().tolist(), ta.cpu().tolist()))
