@@ -78,7 +78,8 @@ def parse_args():
                     help="the headline run without the compact records of configs 1, 3, 4, 5")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="calibration mode: time a plain device copy of this many MiB "
-                         "(the reference kernel for scaling FETCH_SIZE/WRITE_SIZE) and exit")
+                         "(the kernel of known traffic the HBM byte counters are checked "
+                         "against) and exit")
     return ap.parse_args()
 
 
@@ -120,12 +121,13 @@ def conv_traffic(n_in, n_out, P, K, cin, cout, s):
 
 def measured_traffic(dtype: str, pass_name, record: str = "traffic_config2.json"):
     """(HBM bytes per launch of a pass's kernels, source) from the committed
-    rocprofv3 FETCH_SIZE / WRITE_SIZE passes (profiles/traffic_config2.json for
-    the convolution, traffic_pool.json for pooling), scaled by the counters'
-    reading for a device copy of known size; pass_name None reads a record of
-    its own, such as the kernel-map build's ("kernel_map"). The source names
-    the record and the commit of the kernels it was taken on; (None, None) if
-    absent."""
+    rocprofv3 passes: profiles/traffic_config2.json for the convolution (read
+    bytes from the TCC_EA0_RDREQ_{32B,64B,128B} request counts, write bytes
+    from WRITE_SIZE, both exact on a device copy of known size),
+    traffic_pool.json for pooling (FETCH_SIZE / WRITE_SIZE scaled by their
+    reading for such a copy); pass_name None reads a record of its own, such
+    as the kernel-map build's ("kernel_map"). The source names the record and
+    the commit of the kernels it was taken on; (None, None) if absent."""
     path = os.path.join(ROOT, "profiles", record)
     try:
         with open(path) as f:
@@ -137,6 +139,27 @@ def measured_traffic(dtype: str, pass_name, record: str = "traffic_config2.json"
     if doc.get("kernels_commit"):
         src += f" (kernels at commit {doc['kernels_commit']})"
     return round(float(rec["traffic_bytes"])), src
+
+
+def measured_mfma(dtype: str, pass_name: str, flop: float):
+    """Counter-backed MFMA record of a config-2 pass from the committed
+    rocprofv3 passes (profiles/traffic_config2.json): the share of the
+    kernel's time the matrix pipes were busy, the MFMA FLOP issued per
+    algorithmic FLOP (work on masked rows of the 16-row groups and empty
+    positions shows as > 1) and the clock the box ran at; None if absent."""
+    path = os.path.join(ROOT, "profiles", "traffic_config2.json")
+    try:
+        with open(path) as f:
+            doc = json.load(f)
+        rec = doc[dtype][pass_name]
+        return {"util": round(rec["mfma_util"], 4),
+                "flop_ratio": round(rec["mfma_flop"] / flop, 4),
+                "clock_ghz": round(rec["clock_ghz"], 3),
+                "source": "profiles/traffic_config2.json (SQ_VALU_MFMA_BUSY_CYCLES, "
+                          "SQ_INSTS_VALU_MFMA_MOPS_*, GRBM_GUI_ACTIVE; kernels at commit %s)"
+                          % doc.get("kernels_commit")}
+    except (OSError, KeyError, ValueError, ZeroDivisionError):
+        return None
 
 
 def cpu_model() -> str:
@@ -906,12 +929,13 @@ def conv_step_record(args, dtype, km, n_in, n_out, P, K, cin, cout):
                 "peak": PEAK_HBM_GBS, "unit": "GB/s"}
     roof["frac"] = round(roof["achieved"] / roof["peak"], 4)
     roof["traffic"], roof["traffic_source"] = measured_traffic(dtype, dom)
+    roof["mfma"] = measured_mfma(dtype, dom, F)
     roof["kernel"] = {"forward": "conv_os_lds_kernel (forward)",
                       "backward_input": "conv_os_lds_kernel (dX)",
                       "backward_weight": (
                           "conv_dw_pos_kernel + conv_dw_rows_reduce_kernel (dW pass)"
                           if dtype == "f32" else
-                          "conv_dw_pos_bf16_kernel + conv_dw_rows_reduce_kernel (dW pass)")}[dom]
+                          "conv_dw_shx_bf16_kernel + conv_dw_rows_reduce_kernel (dW pass)")}[dom]
     roof["kernel_ms"] = round(kernel_ms, 4)
     roof["kernel_ms_source"] = ("events around dW in the timed steps" if dom == "backward_weight"
                                 else "events in %d untimed steps after the timed ones" % nb)

@@ -299,8 +299,14 @@ int rhip_conv_forward(const void *x, int64_t n_in, int32_t cin,
  * routine. The transposed weights go to an 8 MiB device array of the
  * library (one per GPU, held until the process ends), so K*cin*cout times
  * the dtype size must not exceed 8 MiB (RHIP_ERR_UNSUPPORTED otherwise),
- * and the offset axis is never split. Calls that overlap on one GPU share
- * that array and race. Same arguments and results as rhip_conv_forward.
+ * and the offset axis is never split. Calls share that array: calls on one
+ * stream run in order, and a call on another stream first waits (on the
+ * device) for the previous call's kernels through an event the library
+ * creates once per GPU, so eager calls from several streams take turns.
+ * Under graph capture a call is refused (RHIP_ERR_INVALID) while another
+ * stream's call may still be running; replays of a captured graph are not
+ * ordered against other streams' calls by the library. Same arguments and
+ * results as rhip_conv_forward.
  */
 int rhip_conv_forward_noalloc(const void *x, int64_t n_in, int32_t cin,
                               const void *weight, int32_t K, int32_t cout,

@@ -1605,9 +1605,13 @@ conv_dw_pos_kernel(const float *__restrict__ x, int64_t n_in, int cin,
 
   // a segment's indices, lane l holding position 64*sg + l: the neighbour
   // row under each offset (-1 = none) and the dY row (-1 past the range)
+  // raw loads: the masks for absent entries (-1) are applied in prep, a
+  // segment later, so that nothing waits for these loads when they are issued
+  // (an in-order wait would also wait for the rows prefetched before them)
   struct Seg {
     int32_t id[KPW];
     int32_t orow;
+    int32_t in; // -1 for a position of the map, 0 past its end
   };
   struct Dat {
     float a[KPW];
@@ -1620,15 +1624,14 @@ conv_dw_pos_kernel(const float *__restrict__ x, int64_t n_in, int cin,
     for (int j = 0; j < KPW; ++j) {
       const int32_t keep = in & kval[j];
       S.id[j] = static_cast<int32_t>(__builtin_amdgcn_raw_buffer_load_b32(
-                    rn, pick(static_cast<uint32_t>((kk[j] * n_out + p) * 4), keep), 0, 0)) |
-                ~keep;
+          rn, pick(static_cast<uint32_t>((kk[j] * n_out + p) * 4), keep), 0, 0));
     }
     if (out_order)
       S.orow = static_cast<int32_t>(__builtin_amdgcn_raw_buffer_load_b32(
-                   ro, pick(static_cast<uint32_t>(p * 4), in), 0, 0)) |
-               ~in;
+          ro, pick(static_cast<uint32_t>(p * 4), in), 0, 0));
     else
-      S.orow = static_cast<int32_t>(p) | ~in;
+      S.orow = static_cast<int32_t>(p);
+    S.in = in;
   };
   // Once a segment's indices have arrived: the live masks (bit l: position
   // l has a neighbour under offset j), then the indices become byte offsets
@@ -1636,11 +1639,11 @@ conv_dw_pos_kernel(const float *__restrict__ x, int64_t n_in, int cin,
   auto prep = [&](Seg &S, uint64_t (&live)[KPW]) {
 #pragma unroll
     for (int j = 0; j < KPW; ++j) {
-      const int32_t r = S.id[j];
+      const int32_t r = S.id[j] | ~(S.in & kval[j]);
       live[j] = __ballot(r >= 0);
       S.id[j] = static_cast<int32_t>(pick(static_cast<uint32_t>((r * cin + ci0) * 4), opaque(~(r >> 31))));
     }
-    const int32_t r = S.orow;
+    const int32_t r = S.orow | ~S.in;
     S.orow = static_cast<int32_t>(pick(static_cast<uint32_t>((r * cout + co0) * 4), opaque(~(r >> 31))));
   };
   // rows of step s of a segment: lane (i16, g) takes position 4s + g's
@@ -1794,9 +1797,13 @@ conv_dw_pos_bf16_kernel(const __bf16 *__restrict__ x, int64_t n_in, int cin,
     return (off & static_cast<uint32_t>(keep)) | (kBufOob & ~static_cast<uint32_t>(keep));
   };
 
+  // raw loads: the masks for absent entries (-1) are applied in prep, a
+  // segment later, so that nothing waits for these loads when they are issued
+  // (an in-order wait would also wait for the rows prefetched before them)
   struct Seg {
     int32_t id[KPW];
     int32_t orow;
+    int32_t in; // -1 for a position of the map, 0 past its end
   };
   constexpr int kYv = SHY ? 1 : NB;
   struct Dat {
@@ -1810,24 +1817,23 @@ conv_dw_pos_bf16_kernel(const __bf16 *__restrict__ x, int64_t n_in, int cin,
     for (int j = 0; j < KPW; ++j) {
       const int32_t keep = in & kval[j];
       S.id[j] = static_cast<int32_t>(__builtin_amdgcn_raw_buffer_load_b32(
-                    rn, pick(static_cast<uint32_t>((kk[j] * n_out + p) * 4), keep), 0, 0)) |
-                ~keep;
+          rn, pick(static_cast<uint32_t>((kk[j] * n_out + p) * 4), keep), 0, 0));
     }
     if (out_order)
       S.orow = static_cast<int32_t>(__builtin_amdgcn_raw_buffer_load_b32(
-                   ro, pick(static_cast<uint32_t>(p * 4), in), 0, 0)) |
-               ~in;
+          ro, pick(static_cast<uint32_t>(p * 4), in), 0, 0));
     else
-      S.orow = static_cast<int32_t>(p) | ~in;
+      S.orow = static_cast<int32_t>(p);
+    S.in = in;
   };
   auto prep = [&](Seg &S, uint64_t (&live)[KPW]) {
 #pragma unroll
     for (int j = 0; j < KPW; ++j) {
-      const int32_t r = S.id[j];
+      const int32_t r = S.id[j] | ~(S.in & kval[j]);
       live[j] = __ballot(r >= 0);
       S.id[j] = static_cast<int32_t>(pick(static_cast<uint32_t>((r * cin + ci0) * 2), opaque(~(r >> 31))));
     }
-    const int32_t r = S.orow;
+    const int32_t r = S.orow | ~S.in;
     S.orow = static_cast<int32_t>(pick(static_cast<uint32_t>((r * cout + co0) * 2), opaque(~(r >> 31))));
   };
   // step s (0 or 1) of a segment: lane l takes position 32s + l/2's offsets
@@ -1924,6 +1930,214 @@ conv_dw_pos_bf16_kernel(const __bf16 *__restrict__ x, int64_t n_in, int cin,
     prep(N, LN);
     load_dat(N, 0, DA);
     compute(DB, LS, 1, 1);
+    load_seg(next_load, S);
+  };
+  load_seg(0, SA);
+  load_seg(1, SB);
+  prep(SA, LA);
+  load_dat(SA, 0, DA);
+  for (int sg = 0; sg < segs; sg += 2) {
+    run_seg(SA, LA, SB, LB, sg + 2);
+    run_seg(SB, LB, SA, LA, sg + 3);
+  }
+
+  // lane holds D[4g+e][i16] of block nb: dW[k][ci0 + 4g + e][co0 + 16nb + i16]
+#pragma unroll
+  for (int j = 0; j < KPW; ++j) {
+    if (kk[j] >= K)
+      continue;
+    float *dst = partial + ((static_cast<int64_t>(rg) * K + kk[j]) * cin + ci0 + 4 * g) * cout +
+                 co0 + i16;
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb)
+        dst[static_cast<int64_t>(e) * cout + 16 * nb] = acc[j][nb][e];
+  }
+}
+
+// bf16 dW from the neighbour table with the X rows shared by the workgroup:
+// position-stationary like conv_dw_pos_bf16_kernel, but a workgroup owns a
+// 64-channel input chunk c0 (wave w takes channels c0 + 16w .. c0 + 16w + 15),
+// 16*NB output channels co0 and KPW consecutive offsets that all four waves
+// multiply. At each step (32 positions) wave w loads the whole 128-byte rows
+// (the chunk) of positions 8w .. 8w+7 under every offset of the group (lane
+// l: position 8w + l/8, 16-byte piece l%8), so a load instruction touches 8
+// cache lines where the per-wave 16-channel slices of conv_dw_pos_bf16_kernel
+// touch 32, and the dY rows of the same positions; both go to one of two LDS
+// buffers that one barrier per step publishes (a wave at step t writes the
+// buffer of step t-2, which every wave finished before the barrier of step
+// t-1). Each wave then reads its 16-channel column of the rows transposed
+// (ds_read_b64_tr_b16) as the MFMA's A operand. The offsets' live masks are
+// the same in every wave (the same positions), so a step without a
+// neighbour under an offset skips that offset's LDS stores and MFMAs in the
+// whole workgroup. Indices, out-of-range buffer loads, segments dealt to
+// ranges and the partial slots [range][k][cin][cout] are as in
+// conv_dw_pos_bf16_kernel.
+template <int NB, int KPW, int WAVES>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(WAVES))) void
+conv_dw_shx_bf16_kernel(const __bf16 *__restrict__ x, int64_t n_in, int cin,
+                        const __bf16 *__restrict__ gy, int cout, const int32_t *__restrict__ nbr,
+                        const int32_t *__restrict__ out_order, int64_t n_out, int K, int ranges,
+                        int c_chunks, int co_tiles, float *__restrict__ partial) {
+  static_assert(NB * 16 <= 64, "a dY row piece per lane: at most 64 output channels");
+  constexpr int LDX = 64 + 8, LDY = 16 * NB + 8; // LDS row strides (elements)
+  __shared__ __align__(16) __bf16 sX[2][KPW][32 * LDX];
+  __shared__ __align__(16) __bf16 sY[2][32 * LDY];
+  const int groups = (K + KPW - 1) / KPW;
+  const int units = c_chunks * co_tiles * groups;
+  const int r8 = ranges / kXcds;
+  const int xcd = static_cast<int>(blockIdx.x % kXcds), m = static_cast<int>(blockIdx.x / kXcds);
+  const int rg = xcd * r8 + m / units;
+  int u = m % units;
+  const int grp = u % groups;
+  u /= groups;
+  const int c0 = (u % c_chunks) * 64, co0 = (u / c_chunks) * (16 * NB);
+
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const int i16 = lane & 15;
+  const int g = lane >> 4;
+  const int ci0 = c0 + 16 * wv; // this wave's input channels
+  const int64_t total = (n_out + 63) / 64;
+  const int segs = static_cast<int>((total + 2LL * ranges - 1) / (2LL * ranges)) * 2;
+  int kk[KPW], kval[KPW];
+#pragma unroll
+  for (int j = 0; j < KPW; ++j) {
+    kk[j] = grp * KPW + j;
+    kval[j] = opaque(kk[j] < K ? -1 : 0);
+  }
+
+  const __amdgpu_buffer_rsrc_t rx = buf_rsrc(x, n_in * cin * 2);
+  const __amdgpu_buffer_rsrc_t ry = buf_rsrc(gy, n_out * cout * 2);
+  const __amdgpu_buffer_rsrc_t rn = buf_rsrc(nbr, static_cast<int64_t>(K) * n_out * 4);
+  const __amdgpu_buffer_rsrc_t ro = buf_rsrc(out_order, out_order ? n_out * 4 : 0);
+  auto pick = [](uint32_t off, int32_t keep) {
+    return (off & static_cast<uint32_t>(keep)) | (kBufOob & ~static_cast<uint32_t>(keep));
+  };
+
+  // raw loads: the masks for absent entries (-1) are applied in prep, a
+  // segment later, so that nothing waits for these loads when they are issued
+  // (an in-order wait would also wait for the rows prefetched before them)
+  struct Seg {
+    int32_t id[KPW];
+    int32_t orow;
+    int32_t in; // -1 for a position of the map, 0 past its end
+  };
+  struct Dat {
+    v4u xv[KPW];
+    v4u yv;
+  };
+  // a segment's indices, lane l holding position 64*sg + l
+  auto load_seg = [&](int sg, Seg &S) {
+    const int64_t p = 64 * (rg + static_cast<int64_t>(sg) * ranges) + lane;
+    const int32_t in = opaque(static_cast<int32_t>((p - n_out) >> 63));
+#pragma unroll
+    for (int j = 0; j < KPW; ++j) {
+      const int32_t keep = in & kval[j];
+      S.id[j] = static_cast<int32_t>(__builtin_amdgcn_raw_buffer_load_b32(
+          rn, pick(static_cast<uint32_t>((kk[j] * n_out + p) * 4), keep), 0, 0));
+    }
+    if (out_order)
+      S.orow = static_cast<int32_t>(__builtin_amdgcn_raw_buffer_load_b32(
+          ro, pick(static_cast<uint32_t>(p * 4), in), 0, 0));
+    else
+      S.orow = static_cast<int32_t>(p);
+    S.in = in;
+  };
+  // live masks, then byte offsets of the rows' chunk (out of range if absent)
+  auto prep = [&](Seg &S, uint64_t (&live)[KPW]) {
+#pragma unroll
+    for (int j = 0; j < KPW; ++j) {
+      const int32_t r = S.id[j] | ~(S.in & kval[j]);
+      live[j] = __ballot(r >= 0);
+      S.id[j] = static_cast<int32_t>(pick(static_cast<uint32_t>((r * cin + c0) * 2), opaque(~(r >> 31))));
+    }
+    const int32_t r = S.orow | ~S.in;
+    S.orow = static_cast<int32_t>(pick(static_cast<uint32_t>((r * cout + co0) * 2), opaque(~(r >> 31))));
+  };
+  // step s (0 or 1) of a segment: lane l loads position 32s + 8*wv + l/8,
+  // 16-byte piece l%8 of its X rows (64 channels) and of its dY row (16*NB
+  // channels: lanes past 16*NB load nothing)
+  const int prow8 = 8 * wv + (lane >> 3);
+  auto load_dat = [&](const Seg &S, int s, Dat &D) {
+    const int src = (32 * s + prow8) * 4;
+#pragma unroll
+    for (int j = 0; j < KPW; ++j) {
+      const uint32_t o = static_cast<uint32_t>(__builtin_amdgcn_ds_bpermute(src, S.id[j])) + 16 * (lane & 7);
+      D.xv[j] = __builtin_amdgcn_raw_buffer_load_b128(rx, o, 0, 0);
+    }
+    const int q = 8 * wv + lane / (2 * NB);
+    const uint32_t o =
+        static_cast<uint32_t>(__builtin_amdgcn_ds_bpermute((32 * s + (q & 31)) * 4, S.orow)) +
+        16 * (lane % (2 * NB));
+    D.yv = __builtin_amdgcn_raw_buffer_load_b128(ry, pick(o, opaque(lane < 16 * NB ? -1 : 0)), 0,
+                                                 0);
+  };
+  auto step_live = [](const uint64_t (&live)[KPW], int j, int s) {
+    return ((live[j] >> (32 * s)) & 0xffffffffull) != 0;
+  };
+  // publish step data D into buffer buf (offsets without a neighbour in the
+  // step are not stored: nobody reads them)
+  auto share = [&](const Dat &D, const uint64_t (&live)[KPW], int s, int buf) {
+#pragma unroll
+    for (int j = 0; j < KPW; ++j)
+      if (step_live(live, j, s)) // uniform
+        *reinterpret_cast<v4u *>(sX[buf][j] + prow8 * LDX + 8 * (lane & 7)) = D.xv[j];
+    if (lane < 16 * NB)
+      *reinterpret_cast<v4u *>(sY[buf] + (8 * wv + lane / (2 * NB)) * LDY +
+                               8 * (lane % (2 * NB))) = D.yv;
+    __syncthreads();
+  };
+
+  v4f acc[KPW][NB];
+#pragma unroll
+  for (int j = 0; j < KPW; ++j)
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+      acc[j][nb] = v4f{0.f, 0.f, 0.f, 0.f};
+  const int prow = 8 * g + i16 / 4, pcol = 4 * (i16 % 4);
+  auto operand = [&](const __bf16 *base, int ld, int col) {
+    const v4s lo = ds_read_tr16(base + prow * ld + col + pcol);
+    const v4s hi = ds_read_tr16(base + (prow + 4) * ld + col + pcol);
+    return __builtin_bit_cast(v8bf, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+  };
+  auto compute = [&](const uint64_t (&live)[KPW], int s, int buf) {
+    bool any = false;
+#pragma unroll
+    for (int j = 0; j < KPW; ++j)
+      any |= step_live(live, j, s);
+    if (!any)
+      return; // uniform
+    v8bf b[NB];
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+      b[nb] = operand(sY[buf], LDY, 16 * nb);
+#pragma unroll
+    for (int j = 0; j < KPW; ++j)
+      if (step_live(live, j, s)) { // uniform
+        const v8bf a = operand(sX[buf][j], LDX, 16 * wv);
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb)
+          acc[j][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b[nb], acc[j][nb], 0, 0, 0);
+      }
+  };
+
+  // segments in two slots; step 0 of a segment uses buffer 0, step 1
+  // buffer 1; each step's rows are published before the next step's loads
+  // are issued
+  Seg SA, SB;
+  uint64_t LA[KPW], LB[KPW];
+  Dat DA, DB;
+  auto run_seg = [&](Seg &S, const uint64_t (&LS)[KPW], Seg &N, uint64_t (&LN)[KPW],
+                     int next_load) {
+    share(DA, LS, 0, 0);
+    load_dat(S, 1, DB);
+    compute(LS, 0, 0);
+    share(DB, LS, 1, 1);
+    prep(N, LN);
+    load_dat(N, 0, DA);
+    compute(LS, 1, 1);
     load_seg(next_load, S);
   };
   load_seg(0, SA);
@@ -2655,19 +2869,36 @@ static bool dw_rows_supported(int32_t dtype, int cin, int cout, int K, int64_t n
 // segments of 64 positions each (4 for fp32; 16 for bf16, whose small maps
 // lose more to partial slots than they gain from a full round: config 3's
 // down map 32 us at 32 ranges, 38 at 128).
-static int dw_pos_ranges(int K, int cin, int cout, int vb, int waves, int64_t n_out,
-                         int min_segs) {
-  const int groups = static_cast<int>(ceil_div(K, kWaves * dw_pos_kpw(K)));
-  const int units = (cin / 16) * (cout / (16 * vb)) * groups;
+static int dw_ranges_for(int units, int waves, int64_t n_out, int min_segs) {
   int64_t r = std::max<int64_t>(kXcds, (256 * waves / units) / kXcds * kXcds);
   const int64_t segs = ceil_div(std::max<int64_t>(n_out, 1), 64);
   r = std::min<int64_t>(r, std::max<int64_t>(kXcds, segs / min_segs / kXcds * kXcds));
   return static_cast<int>(std::min<int64_t>(r, kDwRowsBlocks));
 }
+static int dw_pos_ranges(int K, int cin, int cout, int vb, int waves, int64_t n_out,
+                         int min_segs) {
+  const int groups = static_cast<int>(ceil_div(K, kWaves * dw_pos_kpw(K)));
+  return dw_ranges_for((cin / 16) * (cout / (16 * vb)) * groups, waves, n_out, min_segs);
+}
 
-// Ranges of conv_dw_pos_bf16_kernel and conv_dw_pos_kernel for a shape
-// (the workspace query and the launches share them).
+// The shared-X bf16 kernel (conv_dw_shx_bf16_kernel): 64-channel input
+// chunks, 64 output channels and 7 offsets per workgroup, 2 waves per SIMD.
+// Measured on MI355X, config 2 dW (kernel + reduce): 133-138 us against
+// conv_dw_pos_bf16_kernel's 136-142, alternating in one process. Stencils of
+// at most 8 offsets and channel counts that are not multiples of 64 keep
+// conv_dw_pos_bf16_kernel.
+constexpr int kDwShxKPW = 7;
+static bool dw_shx_bf16(int K, int cin, int cout) {
+  return K > kDwPosMaxKSmall && cin % 64 == 0 && cout % 64 == 0;
+}
+
+// Ranges of conv_dw_pos_bf16_kernel (or conv_dw_shx_bf16_kernel) and
+// conv_dw_pos_kernel for a shape (the workspace query and the launches share
+// them).
 static int dw_pos_bf16_ranges(int K, int cin, int cout, int64_t n_out) {
+  if (dw_shx_bf16(K, cin, cout))
+    return dw_ranges_for((cin / 64) * (cout / 64) * static_cast<int>(ceil_div(K, kDwShxKPW)), 2,
+                         n_out, 16);
   const int waves = K <= kDwPosMaxKSmall ? 4 : 2;
   return dw_pos_ranges(K, cin, cout, cout % 64 == 0 ? 4 : 2, waves, n_out, 16);
 }
@@ -2687,7 +2918,14 @@ static void run_dw_pos_bf16(const __bf16 *x, int64_t n_in, int cin, const __bf16
   const int ranges = dw_pos_bf16_ranges(K, cin, cout, n_out);
   const int groups = static_cast<int>(ceil_div(K, kWaves * dw_pos_kpw(K)));
   const int ct = cin / 16, ot = cout / (16 * vb);
-  if (n_in > 0 && n_out > 0) {
+  if (n_in > 0 && n_out > 0 && dw_shx_bf16(K, cin, cout)) {
+    const int cc = cin / 64, sgroups = static_cast<int>(ceil_div(K, kDwShxKPW));
+    hipLaunchKernelGGL((conv_dw_shx_bf16_kernel<4, kDwShxKPW, 2>),
+                       dim3(static_cast<unsigned>(ranges * cc * ot * sgroups)), dim3(kThreads), 0,
+                       s, x, n_in, cin, gy, cout, nbr, out_order, n_out, K, ranges, cc, ot,
+                       partial);
+    RHIP_LAUNCH_CHECK();
+  } else if (n_in > 0 && n_out > 0) {
     const dim3 grid(static_cast<unsigned>(ranges * ct * ot * groups));
     auto go = [&](auto nb, auto kpw, auto w) {
       hipLaunchKernelGGL((conv_dw_pos_bf16_kernel<decltype(nb)::value, decltype(kpw)::value,
@@ -2893,22 +3131,58 @@ static void conv_forward_into(const void *x, int64_t n_in, int32_t cin, const vo
 constexpr size_t kConvScratchBytes = size_t(8) << 20;
 static __device__ __align__(256) char scratch[kConvScratchBytes];
 
-// This device's address of `scratch` (the host-side name is only a stand-in
-// for it), looked up once per device with that device current.
-static void *device_scratch() {
-  constexpr int kMaxDevices = 64;
-  static std::mutex mu;
-  static void *addr[kMaxDevices] = {};
+// Per device: the address of `scratch` (the host-side name is only a
+// stand-in for it), looked up once with that device current, and the
+// stream and completion event of the last call that used it. A call on
+// another stream waits for that event on the device (hipStreamWaitEvent),
+// so eager calls from several streams take their turns; a call under graph
+// capture cannot wait on an event recorded outside the capture, so it is
+// refused while another stream's call may still be using the array. Replays
+// of a captured graph are not tracked (the caller orders them). The event
+// is created once per device at set-up.
+struct ScratchSlot {
+  void *addr = nullptr;
+  hipEvent_t done = nullptr;
+  hipStream_t last = nullptr;
+  bool used = false;
+};
+constexpr int kMaxDevices = 64;
+static std::mutex scratch_mu;
+static ScratchSlot scratch_slots[kMaxDevices];
+
+// Runs f(scratch address) in this device's turn on `stream` (see above).
+template <typename F> static void with_device_scratch(hipStream_t stream, F &&f) {
   int dev = 0;
   RHIP_HIP(hipGetDevice(&dev));
   RHIP_CHECK_ARG(dev >= 0 && dev < kMaxDevices, "device index out of range");
-  std::lock_guard<std::mutex> lock(mu);
-  if (addr[dev] == nullptr) {
+  std::lock_guard<std::mutex> lock(scratch_mu);
+  ScratchSlot &sl = scratch_slots[dev];
+  if (sl.addr == nullptr) {
     void *p = nullptr;
     RHIP_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
-    addr[dev] = p;
+    RHIP_HIP(hipEventCreateWithFlags(&sl.done, hipEventDisableTiming));
+    sl.addr = p;
   }
-  return addr[dev];
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  RHIP_HIP(hipStreamIsCapturing(stream, &cap));
+  const bool capturing = cap != hipStreamCaptureStatusNone;
+  if (sl.used && sl.last != stream) {
+    if (capturing) {
+      const hipError_t q = hipEventQuery(sl.done);
+      if (q == hipErrorNotReady)
+        throw Error(RHIP_ERR_INVALID,
+                    "rhip_conv_forward_noalloc: a call on another stream may still be using "
+                    "the device scratch; synchronise it before capturing");
+      RHIP_HIP(q);
+    } else {
+      RHIP_HIP(hipStreamWaitEvent(stream, sl.done, 0));
+    }
+  }
+  f(sl.addr);
+  if (!capturing)
+    RHIP_HIP(hipEventRecord(sl.done, stream));
+  sl.last = stream;
+  sl.used = !capturing || sl.used;
 }
 
 } // namespace rhip
@@ -2990,8 +3264,10 @@ extern "C" int rhip_conv_forward_noalloc(const void *x, int64_t n_in, int32_t ci
     RHIP_CHECK_ARG(y && weight && nbr, "y, weight and nbr are required");
     RHIP_CHECK_ARG(n_in == 0 || x != nullptr, "x is null");
     // no split of the offset axis: it would need partial sums beyond the scratch
-    conv_forward_into(x, n_in, cin, weight, K, cout, bias, nbr, out_order, n_out, y, dtype,
-                      device_scratch(), nullptr, stream);
+    with_device_scratch(stream, [&](void *scratch_ptr) {
+      conv_forward_into(x, n_in, cin, weight, K, cout, bias, nbr, out_order, n_out, y, dtype,
+                        scratch_ptr, nullptr, stream);
+    });
   });
 }
 

@@ -36,10 +36,9 @@ struct Error : std::runtime_error {
 
 void set_last_error(const std::string &msg);
 
-// A pinned host buffer of at least `bytes` for small device-to-host
-// read-backs, held (and the buffer reserved) while the holder lives.
+// The calling thread's pinned host buffer of at least `bytes` for small
+// device-to-host read-backs (valid until the thread's next request).
 struct PinnedReadback {
-  std::unique_lock<std::mutex> lock;
   void *ptr;
 };
 PinnedReadback pinned_readback(size_t bytes);

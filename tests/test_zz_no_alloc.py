@@ -74,3 +74,28 @@ def test_noalloc_forward_matches_workspace_forward(dtype):
         assert got.data_ptr() == out.data_ptr()
         assert_rel(got.float().cpu().numpy(), ref.float().cpu().numpy(), TOL[dtype],
                    f"noalloc vs workspace forward, n={km.n_in}")
+
+
+@pytest.mark.gpu
+def test_noalloc_calls_from_two_streams_take_turns():
+    """Two calls on two streams back to back, with other weights each: the
+    second waits for the first's kernels before it rewrites the shared
+    scratch, so both outputs equal the workspace forward's."""
+    rng = np.random.default_rng(7)
+    c, _, _ = oracle.insert_and_map(random_coords(rng, 40000, 3, 30))
+    _, _, km = gpu_tables_and_map(c, c, oracle.region_offsets(3, 3), same=True)
+    x = to_dev(rng.standard_normal((km.n_in, 64)).astype(np.float32))
+    w1 = to_dev((rng.standard_normal((27, 64, 64)) / 40).astype(np.float32))
+    w2 = to_dev((rng.standard_normal((27, 64, 64)) / 40).astype(np.float32))
+    ref1, ref2 = abi.conv_forward(x, w1, km), abi.conv_forward(x, w2, km)
+    out1, out2 = torch.empty_like(ref1), torch.empty_like(ref2)
+    torch.cuda.synchronize()
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    for _ in range(3):
+        with torch.cuda.stream(s1):
+            abi.conv_forward_noalloc(x, w1, km, out=out1)
+        with torch.cuda.stream(s2):
+            abi.conv_forward_noalloc(x, w2, km, out=out2)
+        torch.cuda.synchronize()
+        assert_rel(out1.cpu().numpy(), ref1.cpu().numpy(), TOL[torch.float32], "stream 1")
+        assert_rel(out2.cpu().numpy(), ref2.cpu().numpy(), TOL[torch.float32], "stream 2")
