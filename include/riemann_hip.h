@@ -98,7 +98,10 @@ int rhip_hash_workspace_bytes(int64_t n, int32_t ncol, size_t *bytes);
  *   unique_coords = coords[mapping],  coords == unique_coords[inverse].
  * unique_coords needs room for n rows and mapping for n entries; only the
  * first table->n_unique are written. inverse (n entries) may be NULL.
- * Synchronises `stream` once to read n_unique.
+ * Synchronises `stream` once to read n_unique. When some row repeats an
+ * earlier one, the repeats' inverse entries are written by a launch queued
+ * after that synchronisation: as with the asynchronous entry points, the
+ * workspace and inverse stay in use until `stream` has passed the call.
  *
  * Replaces CoordinateMapGPU::insert_and_map (engine/grid/lattice_gpu.cu:157-243,
  * insert_and_map_kernel :26-51, remap_inverse_map :54-71), with the semantics

@@ -884,17 +884,19 @@ extern "C" int rhip_hash_build(const int32_t *coords, int64_t n, int32_t ncol,
                        w.layout, sl, w.slot_of_row, w.block_base, w.uid_by_row, mapping,
                        unique_coords, inverse);
     RHIP_LAUNCH_CHECK();
-    if (inverse) {
-      hipLaunchKernelGGL(resolve_kernel, dim3(nb), dim3(kBlock), 0, stream, n, w.layout, sl,
-                         w.slot_of_row, w.uid_by_row, inverse);
-      RHIP_LAUNCH_CHECK();
-    }
     HashLayout hl;
     {
       PinnedReadback rb = pinned_readback(sizeof(hl));
       RHIP_HIP(hipMemcpyAsync(rb.ptr, w.layout, sizeof(hl), hipMemcpyDeviceToHost, stream));
       RHIP_HIP(hipStreamSynchronize(stream));
       std::memcpy(&hl, rb.ptr, sizeof(hl));
+    }
+    // the repeats' inverse entries, launched after the read-back and only for
+    // a set that has repeats (assign_uid_kernel wrote every first row's)
+    if (inverse && hl.dups) {
+      hipLaunchKernelGGL(resolve_kernel, dim3(nb), dim3(kBlock), 0, stream, n, w.layout, sl,
+                         w.slot_of_row, w.uid_by_row, inverse);
+      RHIP_LAUNCH_CHECK();
     }
     table->n_unique = hl.n_unique;
     table->mode = hl.mode;

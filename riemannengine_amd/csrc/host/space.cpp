@@ -548,6 +548,11 @@ HipKernelMap CoordinateManager::generate(const CoordinateMapHIP &in_map,
                                      static_cast<int32_t>(offsets.size(1)),
                                      m.partner_host.data()),
                "rhip_stencil_partners");
+    // to the device from pinned memory, ordered before the synchronisation
+    // below (a copy from pageable memory would block the host once more)
+    auto pinned = torch::empty({K}, torch::TensorOptions().dtype(torch::kInt32).pinned_memory(true));
+    std::memcpy(pinned.data_ptr<int32_t>(), m.partner_host.data(), sizeof(int32_t) * K);
+    m.partner = pinned.to(dev, /*non_blocking=*/true);
   } else {
     nbr_t = torch::empty({K, std::max<int64_t>(n_in, 1)}, iopt);
     in_order = torch::empty({std::max<int64_t>(n_in, 1)}, iopt);
@@ -564,8 +569,6 @@ HipKernelMap CoordinateManager::generate(const CoordinateMapHIP &in_map,
   check_hip(hipStreamSynchronize(st), "hipStreamSynchronize");
   const int64_t *ho = host_offsets.data_ptr<int64_t>();
   m.offsets_host.assign(ho, ho + K + 1);
-  if (m.symmetric) // after the synchronisation: no pageable copy in flight
-    m.partner = torch::from_blob(m.partner_host.data(), {K}, torch::kInt32).to(dev);
   m.nbr = nbr.slice(1, 0, n_out);
   m.out_order = out_order.slice(0, 0, n_out);
   if (!m.symmetric) {

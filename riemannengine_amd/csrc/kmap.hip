@@ -21,7 +21,9 @@
 //            brick entries over the locality order: one 16-byte load, a
 //            popcount and a look-up in the order), else by probing the hash
 //            table; probes are resolved 8 offsets at a time, their loads
-//            issued together;
+//            issued together; a symmetric 3^3 map in 3-D reads the (at most
+//            8) bricks of a row's neighbourhood once and derives all 27
+//            probes from them (probe27_bricks);
 //   masks    one lane per output row (in the output map's locality order)
 //            folds the existence of its K neighbours into a sort key (the
 //            mask for K <= 16, else the neighbour count above a 15-bit hash
@@ -53,6 +55,13 @@
 namespace rhip {
 
 constexpr int kMapBlock = 256;
+
+// Up to kSmallUpload int32 from the host, passed by value in a kernel's
+// arguments (the stencil and its partners of a 3^3 map: 108 values).
+constexpr int kSmallUpload = 128;
+struct SmallUpload {
+  int32_t v[kSmallUpload];
+};
 constexpr int kMaskedK = 128; // neighbour masks (and mask order) for K <= 128
 constexpr int kKeyBits = 16;  // sort-key width of a neighbour mask
 static int64_t map_waves(int64_t n) { return std::max<int64_t>(1, ceil_div(n, kWave)); }
@@ -190,11 +199,99 @@ __device__ __forceinline__ void probe8(const TableView &t, const int32_t *c, uin
   }
 }
 
+// The 3^3 neighbourhood of a row of a symmetric map through the brick grid:
+// D = 3, bricks of 4 x 4 x 4 cells (brick levels 2), and the stencil in cell
+// units (offsets divided by the column's 2^tz) the canonical 3^3 region,
+// offset k = (k % 3 - 1, k / 3 % 3 - 1, k / 9 - 1) along columns 1..3. The
+// row is one of the table's own rows, so its cell w = (c - lo) >> tz is
+// exact. Its 27 neighbours lie in at most 8 bricks: along each column the
+// row's brick and, where the cell sits on the brick's low (high) face, the
+// brick below (above). The row loads those bricks once, corner cc holding
+// the brick shifted along column i when bit i - 1 of cc is set (probe8 loads
+// one brick per offset: 27 loads, most of them the row's own brick again),
+// and reads every neighbour's occupancy bit and rank from the brick its
+// offset reaches. kRows: r[k] = the neighbour's row (through the locality
+// order) or -1, else r[k] >= 0 marks a neighbour.
+template <bool kRows>
+__device__ __forceinline__ void probe27_bricks(const TableView &t, const int32_t *c, uint32_t d0,
+                                               bool row_ok, int32_t (&r)[27]) {
+  uint32_t q[4], b[4];
+  bool lo_face[4], hi_face[4];
+#pragma unroll
+  for (int i = 1; i <= 3; ++i) {
+    const uint32_t w = (static_cast<uint32_t>(c[i]) - static_cast<uint32_t>(t.lo[i])) >> t.tz[i];
+    q[i] = w & 3u;
+    b[i] = w >> 2;
+    lo_face[i] = q[i] == 0u;
+    hi_face[i] = q[i] == 3u;
+  }
+  uint64_t mk[8];
+  int32_t base[8];
+#pragma unroll
+  for (int cc = 0; cc < 8; ++cc) {
+    bool need = row_ok;
+    int64_t g = d0;
+#pragma unroll
+    for (int i = 1; i <= 3; ++i) {
+      const bool sh = (cc >> (i - 1)) & 1;
+      // a shifted column is needed only on a face; the brick below a cell
+      // in brick 0 wraps to 2^32 - 1 and fails the extent check
+      if (sh)
+        need = need && (lo_face[i] || hi_face[i]);
+      const uint32_t bc = b[i] + (sh ? (lo_face[i] ? 0xffffffffu : 1u) : 0u);
+      need = need && bc < static_cast<uint32_t>(t.dims[i]);
+      g = g * t.dims[i] + bc;
+    }
+    mk[cc] = 0;
+    base[cc] = 0;
+    if (need) {
+      const Brick br = t.bricks[g];
+      mk[cc] = br.mask;
+      base[cc] = br.base;
+    }
+  }
+  // cell bit of in-brick coordinate v along column i: bit l of v at l*3 + 3 - i
+  auto spread = [](uint32_t v, int i) {
+    return ((v & 1u) << (3 - i)) | (((v >> 1) & 1u) << (6 - i));
+  };
+#pragma unroll
+  for (int k = 0; k < 27; ++k) {
+    const int dl[4] = {0, k % 3 - 1, (k / 3) % 3 - 1, k / 9 - 1};
+    bool x[4];
+    uint32_t cell = 0;
+#pragma unroll
+    for (int i = 1; i <= 3; ++i) {
+      x[i] = dl[i] < 0 ? lo_face[i] : (dl[i] > 0 ? hi_face[i] : false);
+      cell |= spread((q[i] + static_cast<uint32_t>(dl[i])) & 3u, i);
+    }
+    // mk[x1 + 2 x2 + 4 x3] as a select tree over the columns the offset moves
+    uint64_t m4[4];
+    int32_t b4[4];
+#pragma unroll
+    for (int a = 0; a < 4; ++a) {
+      m4[a] = x[3] ? mk[a + 4] : mk[a];
+      b4[a] = x[3] ? base[a + 4] : base[a];
+    }
+    const uint64_t m2_0 = x[2] ? m4[2] : m4[0], m2_1 = x[2] ? m4[3] : m4[1];
+    const int32_t b2_0 = x[2] ? b4[2] : b4[0], b2_1 = x[2] ? b4[3] : b4[1];
+    const uint64_t m = x[1] ? m2_1 : m2_0;
+    const int32_t bs = x[1] ? b2_1 : b2_0;
+    const bool hit = (m >> cell) & 1ull;
+    if constexpr (kRows) {
+      const int32_t jj = bs + __popcll(m & ((1ull << cell) - 1ull));
+      r[k] = hit ? t.order[jj] : -1;
+    } else {
+      r[k] = hit ? 0 : -1;
+    }
+  }
+}
+
 // Mask pass: one lane per output row j in spatial order (row spatial[j]):
 // keys[j] = the sort key of the row's neighbour mask, vals[j] = j.
 // KC > 0: K == KC at compile time (the probe rounds unroll and the stencil
-// loads hoist out of them).
-template <int D, int KC = 0>
+// loads hoist out of them). NBHD: the symmetric 3^3 map through
+// probe27_bricks (KC == 27, D == 3).
+template <int D, int KC = 0, bool NBHD = false>
 __global__ __launch_bounds__(kMapBlock) void kmap_mask_kernel(
     TableView t, const int32_t *__restrict__ out_coords, const int32_t *__restrict__ spatial,
     int64_t n_out, const int32_t *__restrict__ offsets, int K, uint32_t *__restrict__ keys,
@@ -212,6 +309,18 @@ __global__ __launch_bounds__(kMapBlock) void kmap_mask_kernel(
   const uint32_t d0 = static_cast<uint32_t>(c[0]) - static_cast<uint32_t>(t.lo[0]);
   const bool row_ok = d0 <= t.span[0];
   uint64_t m0 = 0, m1 = 0;
+  if constexpr (NBHD) {
+    static_assert(D == 3 && KC == 27, "the neighbourhood probe is the 3^3 stencil in 3-D");
+    int32_t r[27];
+    probe27_bricks<false>(t, c, d0, row_ok, r);
+#pragma unroll
+    for (int k = 0; k < 27; ++k)
+      if (r[k] >= 0)
+        m0 |= 1ull << k;
+    keys[j] = mask_key(m0, m1, K);
+    vals[j] = static_cast<int32_t>(j);
+    return;
+  }
 #pragma unroll
   for (int k0 = 0; k0 < (KC > 0 ? KC : K); k0 += 8) {
     int32_t r[8];
@@ -235,14 +344,18 @@ __global__ __launch_bounds__(kMapBlock) void kmap_mask_kernel(
 // spatial order, or p): nbr[k][p] = the input row paired with it under k
 // (coalesced over p), out_order[p] = its row, and per offset k the number of
 // hits of each wave w, wave_counts[k][w].
-template <int D, int KC = 0>
+template <int D, int KC = 0, bool NBHD = false>
 __global__ __launch_bounds__(kMapBlock) void kmap_query_kernel(
     TableView t, const int32_t *__restrict__ out_coords, const int32_t *__restrict__ spatial,
     const int32_t *__restrict__ jpos, int64_t n_out, const int32_t *__restrict__ offsets, int K,
     int64_t nw, int32_t *__restrict__ nbr, int32_t *__restrict__ out_order,
-    int32_t *__restrict__ wave_counts) {
+    int32_t *__restrict__ wave_counts, SmallUpload up, int32_t *__restrict__ up_dst, int up_n) {
   if constexpr (KC > 0)
     K = KC;
+  // a few host values for later launches, carried in the arguments
+  if (blockIdx.x == 0)
+    for (int i = threadIdx.x; i < up_n; i += kMapBlock)
+      up_dst[i] = up.v[i];
   const int64_t p = blockIdx.x * (int64_t)kMapBlock + threadIdx.x;
   const int64_t w = p / kWave;
   if (w >= nw) // whole waves past the last row
@@ -259,6 +372,20 @@ __global__ __launch_bounds__(kMapBlock) void kmap_query_kernel(
   }
   const uint32_t d0 = static_cast<uint32_t>(c[0]) - static_cast<uint32_t>(t.lo[0]);
   const bool row_ok = in && d0 <= t.span[0];
+  if constexpr (NBHD) {
+    static_assert(D == 3 && KC == 27, "the neighbourhood probe is the 3^3 stencil in 3-D");
+    int32_t r[27];
+    probe27_bricks<true>(t, c, d0, row_ok, r);
+#pragma unroll
+    for (int k = 0; k < 27; ++k) {
+      if (in)
+        nbr[k * n_out + p] = r[k];
+      const uint64_t hits = __ballot(r[k] >= 0);
+      if (lane_id() == 0)
+        wave_counts[k * nw + w] = __popcll(hits);
+    }
+    return;
+  }
 #pragma unroll
   for (int k0 = 0; k0 < (KC > 0 ? KC : K); k0 += 8) {
     int32_t r[8];
@@ -531,6 +658,25 @@ static std::vector<int32_t> symmetric_partners(const rhip_table *in_table,
   return partner;
 }
 
+// Whether a symmetric 3-D map takes probe27_bricks: a brick grid of
+// 4 x 4 x 4 cells and the stencil, in cell units of the table (offset
+// column i divided by 2^tz[i]), the canonical 3^3 region in its order.
+static bool nbhd27(const rhip_table *t, int32_t K, const int32_t *offsets_host) {
+  if (K != 27 || t->ncol != 4 || t->bricks == nullptr || t->order == nullptr ||
+      t->brick_levels != 2)
+    return false;
+  for (int k = 0; k < 27; ++k) {
+    const int dl[3] = {k % 3 - 1, (k / 3) % 3 - 1, k / 9 - 1};
+    for (int i = 0; i < 3; ++i) {
+      const int tz = t->tz[i + 1];
+      if (tz < 0 || tz > 30 ||
+          static_cast<int64_t>(offsets_host[k * 3 + i]) != int64_t(dl[i]) * (int64_t(1) << tz))
+        return false;
+    }
+  }
+  return true;
+}
+
 } // namespace rhip
 
 using namespace rhip;
@@ -583,14 +729,41 @@ extern "C" int rhip_kmap_count(const rhip_table *in_table, const int32_t *out_co
         up.resize(static_cast<size_t>(w.partner - w.offsets));
         up.insert(up.end(), partner.begin(), partner.end());
       }
-      upload_i32(w.offsets, up.data(), up.size(), stream);
       const bool masks = K <= kMaskedK && n_out > 1 && in_table->n_unique > 0;
       const TableView tv = make_view(*in_table);
       const int32_t *jpos = nullptr;
+      // the symmetric 3^3 map reads each row's neighbourhood bricks once; its
+      // probes need no stencil on the device, so the upload rides in the
+      // query's arguments
+      const bool nbhd = sym && nbhd27(in_table, K, offsets_host) && up.size() <= kSmallUpload;
+      SmallUpload small{};
+      if (nbhd)
+        std::memcpy(small.v, up.data(), sizeof(int32_t) * up.size());
+      else
+        upload_i32(w.offsets, up.data(), up.size(), stream);
       with_dim(D, [&](auto dc) {
         constexpr int DD = decltype(dc)::value;
         // the 3^3 stencil unrolled (config 2: mask 30 -> 25 us, query 36 -> 33 us)
         const bool k27 = K == 27 && DD == 3;
+        if constexpr (DD == 3) {
+          if (nbhd) {
+            if (masks) {
+              hipLaunchKernelGGL((kmap_mask_kernel<3, 27, true>), dim3(nb), dim3(kMapBlock), 0,
+                                 stream, tv, out_coords, out_spatial_order, n_out, w.offsets, K,
+                                 w.keys_a, w.vals_a);
+              RHIP_LAUNCH_CHECK();
+              sort_pairs_u32(w.sort_tmp, w.sort_bytes, w.keys_a, w.keys_b, w.vals_a, w.vals_b,
+                             n_out, mask_key_bits(K), stream);
+              jpos = w.vals_b;
+            }
+            hipLaunchKernelGGL((kmap_query_kernel<3, 27, true>), dim3(nb), dim3(kMapBlock), 0,
+                               stream, tv, out_coords, out_spatial_order, jpos, n_out, w.offsets,
+                               K, nw, nbr, out_order, w.wave_counts, small, w.offsets,
+                               static_cast<int>(up.size()));
+            RHIP_LAUNCH_CHECK();
+            return;
+          }
+        }
         if (masks) {
           if (k27)
             hipLaunchKernelGGL((kmap_mask_kernel<DD, 27>), dim3(nb), dim3(kMapBlock), 0, stream,
@@ -608,11 +781,11 @@ extern "C" int rhip_kmap_count(const rhip_table *in_table, const int32_t *out_co
         if (k27)
           hipLaunchKernelGGL((kmap_query_kernel<DD, 27>), dim3(nb), dim3(kMapBlock), 0, stream,
                              tv, out_coords, out_spatial_order, jpos, n_out, w.offsets, K, nw,
-                             nbr, out_order, w.wave_counts);
+                             nbr, out_order, w.wave_counts, small, w.offsets, 0);
         else
           hipLaunchKernelGGL((kmap_query_kernel<DD>), dim3(nb), dim3(kMapBlock), 0, stream, tv,
                              out_coords, out_spatial_order, jpos, n_out, w.offsets, K, nw, nbr,
-                             out_order, w.wave_counts);
+                             out_order, w.wave_counts, small, w.offsets, 0);
         RHIP_LAUNCH_CHECK();
       });
     }
