@@ -73,7 +73,7 @@ def parse_args():
     ap.add_argument("--seed", type=int, default=2)
     ap.add_argument("--no-cpu-baseline", action="store_true",
                     help="skip the CPU oracle timing (profiling runs)")
-    ap.add_argument("--map-reps", type=int, default=5)
+    ap.add_argument("--map-reps", type=int, default=20)
     ap.add_argument("--no-other-configs", action="store_true",
                     help="the headline run without the compact records of configs 1, 3, 4, 5")
     ap.add_argument("--copy-mib", type=int, default=0,
@@ -301,18 +301,21 @@ def _timed_passes(passes, steps, warmup):
     return per, wall
 
 
-def _map_time(build, reps):
-    """Host-clock median of `build()` (hash + map calls read sizes back)."""
+def _map_time(build, reps, warmup=5):
+    """Host-clock median of `build()` over `reps` builds after `warmup`
+    untimed ones (hash + map calls read sizes back), the way the steps get
+    their warm-up."""
     import torch
     out, ms = None, []
     with _no_gc():
-        for _ in range(reps + 1):
+        for i in range(warmup + reps):
             torch.cuda.synchronize()
             t0 = time.perf_counter()
             out = build()
             torch.cuda.synchronize()
-            ms.append((time.perf_counter() - t0) * 1e3)
-    return out, statistics.median(ms[1:])
+            if i >= warmup:
+                ms.append((time.perf_counter() - t0) * 1e3)
+    return out, statistics.median(ms)
 
 
 def _roof(F, B, ms, dtype):
