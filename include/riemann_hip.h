@@ -181,6 +181,10 @@ int rhip_kmap_workspace_bytes(int64_t n_in, int64_t n_out, int32_t K,
  * transposed table is the forward table with each offset's negation. Pass
  * it to rhip_kmap_fill. */
 #define RHIP_KMAP_SYMMETRIC 1
+/* Reported by rhip_kmap_count when its probes read each output row's
+ * neighbourhood bricks once (a symmetric 3^3 map in 3-D whose in_table has a
+ * brick grid); the map is the same either way. rhip_kmap_fill ignores it. */
+#define RHIP_KMAP_BRICK_NBHD 2
 
 /*
  * Phase 1 of kernel-map generation. For every output row and every offset
@@ -196,7 +200,8 @@ int rhip_kmap_workspace_bytes(int64_t n_in, int64_t n_out, int32_t K,
  *   nbr[k*n_out+p] input row paired with out_order[p] under k, or -1;
  *   kmap_offsets   device int64 [K+1], CSR of the pairs per offset, copied
  *                  to kmap_offsets_host;
- *   *flags         RHIP_KMAP_SYMMETRIC or 0 (flags may be NULL).
+ *   *flags         RHIP_KMAP_SYMMETRIC and RHIP_KMAP_BRICK_NBHD bits, or 0
+ *                  (flags may be NULL).
  * Synchronises `stream` once (to read the pair counts) when kmap_offsets_host
  * is given; with kmap_offsets_host NULL it is asynchronous, and the caller
  * sizes the pair lists of rhip_kmap_fill by the bound K * n_out (or reads

@@ -22,6 +22,7 @@ MAX_COLS = 8
 F32, BF16 = 0, 1
 KEY_PACKED64, KEY_ROWREF = 0, 1
 KMAP_SYMMETRIC = 1
+KMAP_BRICK_NBHD = 2  # rhip_kmap_count's probes read each row's neighbourhood bricks once
 POOL_SUM, POOL_AVG, POOL_MAX, POOL_MAX_SCATTER = 0, 1, 2, 3
 POOL_MODES = {"sum": POOL_SUM, "avg": POOL_AVG, "max": POOL_MAX, "max_scatter": POOL_MAX_SCATTER}
 
@@ -313,8 +314,9 @@ class KernelMap:
     """
 
     def __init__(self, K, n_in, n_out, offsets, offsets_host, in_rows, out_rows, nbr, nbr_t,
-                 in_order, out_order, symmetric=False, partner=None):
+                 in_order, out_order, symmetric=False, partner=None, flags=0):
         self.K, self.n_in, self.n_out = K, n_in, n_out
+        self.flags = flags  # RHIP_KMAP_* bits reported by rhip_kmap_count
         self.offsets, self.offsets_host = offsets, offsets_host
         self._in_rows, self._out_rows = in_rows, out_rows
         self.nbr, self._nbr_t = nbr, nbr_t
@@ -438,7 +440,8 @@ def kernel_map(in_table: CoordTable, out_table: CoordTable, offsets) -> KernelMa
     torch.cuda.current_stream(dev).synchronize()
     kofs_host = kofs_pinned.numpy()
     return KernelMap(K, n_in, n_out, kofs, kofs_host, None, None, nbr[:, :n_out], nbr_t,
-                     in_order, out_order[:n_out], symmetric=symmetric, partner=partner)
+                     in_order, out_order[:n_out], symmetric=symmetric, partner=partner,
+                     flags=flags.value)
 
 
 # ------------------------------------------------------------ convolution

@@ -349,13 +349,18 @@ __global__ __launch_bounds__(kMapBlock) void kmap_query_kernel(
     TableView t, const int32_t *__restrict__ out_coords, const int32_t *__restrict__ spatial,
     const int32_t *__restrict__ jpos, int64_t n_out, const int32_t *__restrict__ offsets, int K,
     int64_t nw, int32_t *__restrict__ nbr, int32_t *__restrict__ out_order,
-    int32_t *__restrict__ wave_counts, SmallUpload up, int32_t *__restrict__ up_dst, int up_n) {
+    int32_t *__restrict__ wave_counts, SmallUpload up, int32_t *__restrict__ up_dst0, int up_n0,
+    int32_t *__restrict__ up_dst1, int up_n1) {
   if constexpr (KC > 0)
     K = KC;
-  // a few host values for later launches, carried in the arguments
-  if (blockIdx.x == 0)
-    for (int i = threadIdx.x; i < up_n; i += kMapBlock)
-      up_dst[i] = up.v[i];
+  // a few host values for later launches, carried in the arguments: the
+  // first up_n0 go to up_dst0, the next up_n1 to up_dst1
+  if (blockIdx.x == 0) {
+    for (int i = threadIdx.x; i < up_n0; i += kMapBlock)
+      up_dst0[i] = up.v[i];
+    for (int i = threadIdx.x; i < up_n1; i += kMapBlock)
+      up_dst1[i] = up.v[up_n0 + i];
+  }
   const int64_t p = blockIdx.x * (int64_t)kMapBlock + threadIdx.x;
   const int64_t w = p / kWave;
   if (w >= nw) // whole waves past the last row
@@ -733,14 +738,21 @@ extern "C" int rhip_kmap_count(const rhip_table *in_table, const int32_t *out_co
       const TableView tv = make_view(*in_table);
       const int32_t *jpos = nullptr;
       // the symmetric 3^3 map reads each row's neighbourhood bricks once; its
-      // probes need no stencil on the device, so the upload rides in the
-      // query's arguments
-      const bool nbhd = sym && nbhd27(in_table, K, offsets_host) && up.size() <= kSmallUpload;
+      // probes need no stencil on the device, so the stencil and the partners
+      // ride in the query's arguments (two spans: the partners sit after the
+      // stencil's padded slot in the workspace)
+      const int n_sten = K * D, n_part = sym ? K : 0;
+      const bool nbhd = sym && nbhd27(in_table, K, offsets_host) &&
+                        n_sten + n_part <= kSmallUpload;
       SmallUpload small{};
-      if (nbhd)
-        std::memcpy(small.v, up.data(), sizeof(int32_t) * up.size());
-      else
+      if (nbhd && flags)
+        *flags |= RHIP_KMAP_BRICK_NBHD;
+      if (nbhd) {
+        std::memcpy(small.v, offsets_host, sizeof(int32_t) * n_sten);
+        std::memcpy(small.v + n_sten, partner.data(), sizeof(int32_t) * n_part);
+      } else {
         upload_i32(w.offsets, up.data(), up.size(), stream);
+      }
       with_dim(D, [&](auto dc) {
         constexpr int DD = decltype(dc)::value;
         // the 3^3 stencil unrolled (config 2: mask 30 -> 25 us, query 36 -> 33 us)
@@ -759,7 +771,7 @@ extern "C" int rhip_kmap_count(const rhip_table *in_table, const int32_t *out_co
             hipLaunchKernelGGL((kmap_query_kernel<3, 27, true>), dim3(nb), dim3(kMapBlock), 0,
                                stream, tv, out_coords, out_spatial_order, jpos, n_out, w.offsets,
                                K, nw, nbr, out_order, w.wave_counts, small, w.offsets,
-                               static_cast<int>(up.size()));
+                               n_sten, w.partner, n_part);
             RHIP_LAUNCH_CHECK();
             return;
           }
@@ -781,11 +793,11 @@ extern "C" int rhip_kmap_count(const rhip_table *in_table, const int32_t *out_co
         if (k27)
           hipLaunchKernelGGL((kmap_query_kernel<DD, 27>), dim3(nb), dim3(kMapBlock), 0, stream,
                              tv, out_coords, out_spatial_order, jpos, n_out, w.offsets, K, nw,
-                             nbr, out_order, w.wave_counts, small, w.offsets, 0);
+                             nbr, out_order, w.wave_counts, small, w.offsets, 0, w.partner, 0);
         else
           hipLaunchKernelGGL((kmap_query_kernel<DD>), dim3(nb), dim3(kMapBlock), 0, stream, tv,
                              out_coords, out_spatial_order, jpos, n_out, w.offsets, K, nw, nbr,
-                             out_order, w.wave_counts, small, w.offsets, 0);
+                             out_order, w.wave_counts, small, w.offsets, 0, w.partner, 0);
         RHIP_LAUNCH_CHECK();
       });
     }

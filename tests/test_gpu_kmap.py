@@ -115,10 +115,14 @@ def test_same_set_map_matches_oracle(D, ks, dil, ts, region):
     _check_tables(km, tin, tout)
     # odd cubes and crosses are closed under negation: half the offsets are probed
     assert km.symmetric == (ks % 2 == 1)
+    # the 3^3 cube in cell units (tensor stride 1 or 2, no dilation) reads each
+    # row's neighbourhood bricks once; the general path below must agree
+    nbhd = D == 3 and ks == 3 and dil == 1 and region == "cube"
+    assert bool(km.flags & abi.KMAP_BRICK_NBHD) == nbhd
     # the same coordinates in a second table take the general path; it must
     # agree with the mirrored one row for row
     _, tout2, km2 = gpu_tables_and_map(c, c, off, same=False)
-    assert not km2.symmetric
+    assert not km2.symmetric and not km2.flags & abi.KMAP_BRICK_NBHD
     np.testing.assert_array_equal(km2.offsets_host, kofs)
     np.testing.assert_array_equal(km2.out_order.cpu().numpy(), km.out_order.cpu().numpy())
     np.testing.assert_array_equal(km2.nbr.cpu().numpy(), km.nbr.cpu().numpy())
@@ -216,6 +220,8 @@ def test_config_maps_match_oracle(cfg):
     np.testing.assert_array_equal(cnt, cnt[::-1])
     if cfg == "sphere":
         assert len(c) == 51554 and km.n_pairs == 544970
+    # the 3-D configurations' maps take the neighbourhood-brick probes
+    assert bool(km.flags & abi.KMAP_BRICK_NBHD) == (D == 3)
 
 
 def test_lidar_down_up_maps():
