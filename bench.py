@@ -121,13 +121,13 @@ def conv_traffic(n_in, n_out, P, K, cin, cout, s):
 
 def measured_traffic(dtype: str, pass_name, record: str = "traffic_config2.json"):
     """(HBM bytes per launch of a pass's kernels, source) from the committed
-    rocprofv3 passes: profiles/traffic_config2.json for the convolution (read
-    bytes from the TCC_EA0_RDREQ_{32B,64B,128B} request counts, write bytes
-    from WRITE_SIZE, both exact on a device copy of known size),
-    traffic_pool.json for pooling (FETCH_SIZE / WRITE_SIZE scaled by their
-    reading for such a copy); pass_name None reads a record of its own, such
-    as the kernel-map build's ("kernel_map"). The source names the record and
-    the commit of the kernels it was taken on; (None, None) if absent."""
+    rocprofv3 passes, profiles/traffic_config2.json for the convolution and
+    traffic_pool.json for pooling: read bytes from the
+    TCC_EA0_RDREQ_{32B,64B,128B} request counts, write bytes from WRITE_SIZE,
+    both exact on a device copy of known size; pass_name None reads a record
+    of its own, such as the kernel-map build's ("kernel_map"). The source
+    names the record and the commit of the kernels it was taken on; (None,
+    None) if absent."""
     path = os.path.join(ROOT, "profiles", record)
     try:
         with open(path) as f:
