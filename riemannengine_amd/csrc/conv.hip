@@ -438,7 +438,13 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(WAVES)
 // against 108 for conv_os_kernel with runtime widths. SPLIT: gridDim.z
 // workgroups share a tile's (offset, chunk) stages and write fp32 partial
 // sums (config 5 step 5.87 -> 5.73 ms against conv_os_kernel's split).
-template <typename T, int NT, int RG, int CSUB, int G, int WAVES, int CW, int KQ, bool SPLIT>
+// REGK: the indices stay in registers instead, one vector of slots per row
+// group; a stage takes its slot with one uniform indexed register move and
+// moves the row's index to the lane with a ds_bpermute. LDS then holds only
+// the staged weights, which is what limits occupancy where a stencil has
+// many slots (config 4's 81 offsets: 48 KB of indices per workgroup).
+template <typename T, int NT, int RG, int CSUB, int G, int WAVES, int CW, int KQ, bool SPLIT,
+          bool REGK = false>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(WAVES))) void
 conv_os_lds_kernel(const T *__restrict__ x, int64_t n_x, const T *__restrict__ wt,
                    const int32_t *__restrict__ wperm, int ncols,
@@ -466,7 +472,11 @@ conv_os_lds_kernel(const T *__restrict__ x, int64_t n_x, const T *__restrict__ w
   constexpr int MW = KQ / 8;
 
   __shared__ __align__(16) T sB[G][NT * LDW];
-  __shared__ int32_t sK[kWaves][RG][KQ][kWave];
+  __shared__ int32_t sK[REGK ? 1 : kWaves][REGK ? 1 : RG][REGK ? 1 : KQ][kWave];
+  static_assert(!REGK || KQ <= 32, "register-held slots fit one vector");
+  constexpr int KV = KQ <= 8 ? 8 : (KQ <= 16 ? 16 : 32);
+  typedef int32_t vki __attribute__((ext_vector_type(KV)));
+  vki kreg[RG]; // REGK: lane (i16, g) of slot q holds offset 4q + g of row i16
   __shared__ uint32_t smask[kWaves * RG][MW];
 
   const int lane = threadIdx.x & (kWave - 1);
@@ -478,8 +488,8 @@ conv_os_lds_kernel(const T *__restrict__ x, int64_t n_x, const T *__restrict__ w
     return; // padding workgroup (uniform)
   const int col0 = blockIdx.y * NT;
 
-  // Neighbour indices of the wave's row groups to LDS (absent or past the
-  // end: -1) and the offsets with any neighbour in each group.
+  // Neighbour indices of the wave's row groups to LDS or registers (absent
+  // or past the end: -1) and the offsets with any neighbour in each group.
   uint32_t wmask[MW] = {};
 #pragma unroll
   for (int r = 0; r < RG; ++r) {
@@ -498,7 +508,10 @@ conv_os_lds_kernel(const T *__restrict__ x, int64_t n_x, const T *__restrict__ w
       uint32_t w = 0;
 #pragma unroll
       for (int q = 0; q < 8; ++q) {
-        sK[wv][r][8 * mw + q][lane] = v[q];
+        if constexpr (REGK)
+          kreg[r][8 * mw + q] = v[q];
+        else
+          sK[wv][r][8 * mw + q][lane] = v[q];
         const uint64_t bal = __ballot(v[q] >= 0);
 #pragma unroll
         for (int gg = 0; gg < 4; ++gg)
@@ -591,7 +604,11 @@ conv_os_lds_kernel(const T *__restrict__ x, int64_t n_x, const T *__restrict__ w
     for (int j = 0; j < G; ++j)
 #pragma unroll
       for (int r = 0; r < RG; ++r) {
-        const int32_t id = sK[wv][r][kj[j] >> 2][(kj[j] & 3) * 16 + rsel];
+        int32_t id;
+        if constexpr (REGK) // kj is uniform: one indexed move, then the row's lane
+          id = __builtin_amdgcn_ds_bpermute(((kj[j] & 3) * 16 + rsel) * 4, kreg[r][kj[j] >> 2]);
+        else
+          id = sK[wv][r][kj[j] >> 2][(kj[j] & 3) * 16 + rsel];
         const int32_t keep = live[j] ? ~(id >> 31) : 0;
         off[j][r] = pick_off(static_cast<uint32_t>(id) * static_cast<uint32_t>(CW * sizeof(T)) +
                                  static_cast<uint32_t>(ccj[j] * CCH * sizeof(T)) + lane_byte,
@@ -2387,27 +2404,27 @@ static size_t os_partial_floats(int64_t n_rows, int cred, int ncols, int K) {
 
 // One conv_os_lds_kernel launch; the split form is built for bf16 only (fp32
 // splits stay on conv_os_kernel).
-template <typename T, int NT, int RG, int CSUB, int G, int WAVES, int CW, int KQ>
+template <typename T, int NT, int RG, int CSUB, int G, int WAVES, int CW, int KQ, bool REGK>
 static void launch_os_lds_cw(dim3 grid, bool split, const T *x, int64_t n_x, const T *wt,
                              const int32_t *wperm, int ncols, const float *bias,
                              const int32_t *nbr, int64_t n_rows, int K, const int32_t *order,
                              T *y, float *partial, hipStream_t s) {
   if constexpr (!kIsF32<T>) {
     if (split) {
-      hipLaunchKernelGGL((conv_os_lds_kernel<T, NT, RG, CSUB, G, WAVES, CW, KQ, true>), grid,
+      hipLaunchKernelGGL((conv_os_lds_kernel<T, NT, RG, CSUB, G, WAVES, CW, KQ, true, REGK>), grid,
                          dim3(kThreads), 0, s, x, n_x, wt, wperm, ncols, bias, nbr, n_rows, K,
                          order, y, partial);
       return;
     }
   }
-  hipLaunchKernelGGL((conv_os_lds_kernel<T, NT, RG, CSUB, G, WAVES, CW, KQ, false>), grid,
+  hipLaunchKernelGGL((conv_os_lds_kernel<T, NT, RG, CSUB, G, WAVES, CW, KQ, false, REGK>), grid,
                      dim3(kThreads), 0, s, x, n_x, wt, wperm, ncols, bias, nbr, n_rows, K, order,
                      y, nullptr);
 }
 
 // conv_os_lds_kernel launches: the reduction width as one, two or four
 // chunks; false where it is none of these (or an fp32 split).
-template <typename T, int NT, int RG, int CSUB, int G, int WAVES, int KQ>
+template <typename T, int NT, int RG, int CSUB, int G, int WAVES, int KQ, bool REGK = false>
 static bool launch_os_lds(const T *x, int64_t n_x, int cred, const T *wt, const int32_t *wperm,
                           int ncols, const float *bias, const int32_t *nbr, int64_t n_rows,
                           int K, const int32_t *order, T *y, int splits, float *partial,
@@ -2419,14 +2436,14 @@ static bool launch_os_lds(const T *x, int64_t n_x, int cred, const T *wt, const 
     return false;
   const dim3 grid(static_cast<unsigned>(xcd_grid(ceil_div(n_rows, ROWS))), ncols / NT, splits);
   if (cred == CCH)
-    launch_os_lds_cw<T, NT, RG, CSUB, G, WAVES, CCH, KQ>(grid, sp, x, n_x, wt, wperm, ncols, bias,
+    launch_os_lds_cw<T, NT, RG, CSUB, G, WAVES, CCH, KQ, REGK>(grid, sp, x, n_x, wt, wperm, ncols, bias,
                                                          nbr, n_rows, K, order, y, partial, s);
   else if (cred == 2 * CCH)
-    launch_os_lds_cw<T, NT, RG, CSUB, G, WAVES, 2 * CCH, KQ>(grid, sp, x, n_x, wt, wperm, ncols,
+    launch_os_lds_cw<T, NT, RG, CSUB, G, WAVES, 2 * CCH, KQ, REGK>(grid, sp, x, n_x, wt, wperm, ncols,
                                                              bias, nbr, n_rows, K, order, y,
                                                              partial, s);
   else if (cred == 4 * CCH)
-    launch_os_lds_cw<T, NT, RG, CSUB, G, WAVES, 4 * CCH, KQ>(grid, sp, x, n_x, wt, wperm, ncols,
+    launch_os_lds_cw<T, NT, RG, CSUB, G, WAVES, 4 * CCH, KQ, REGK>(grid, sp, x, n_x, wt, wperm, ncols,
                                                              bias, nbr, n_rows, K, order, y,
                                                              partial, s);
   else
@@ -2443,13 +2460,20 @@ static bool launch_os_lds(const T *x, int64_t n_x, int cred, const T *wt, const 
 // Launch shape of conv_os_lds_kernel, measured on MI355X: bf16 at 64 columns
 // and 64-channel chunks takes two row groups per wave and one stage per
 // barrier (6 waves per SIMD; config 2 forward 76 us against 78 with two
-// stages per barrier and 80 with three row groups); the other shapes keep
-// conv_os_kernel's.
+// stages per barrier and 80 with three row groups); fp32 at 32 columns with
+// 24 index slots (stencils of 33 to 96 offsets) holds the indices in
+// registers and takes two stages per barrier at 5 waves per SIMD (config 4
+// forward 305 -> 256 us; the LDS indices with two stages: 309 us; register
+// indices in config 2's shapes: fp32 314 against 312 us, bf16 80 against
+// 75); the other shapes keep conv_os_kernel's.
 template <typename T, int NT, int CSUB, int KQ>
 static bool os_lds_shape(const T *x, int64_t n_x, int cred, const T *wt, const int32_t *wperm,
                          int ncols, const float *bias, const int32_t *nbr, int64_t n_rows, int K,
                          const int32_t *order, T *y, int splits, float *partial, hipStream_t s) {
-  if constexpr (kIsF32<T>) {
+  if constexpr (kIsF32<T> && NT == 32 && KQ == 24) {
+    return launch_os_lds<T, NT, 1, CSUB, 2, 5, KQ, true>(
+        x, n_x, cred, wt, wperm, ncols, bias, nbr, n_rows, K, order, y, splits, partial, s);
+  } else if constexpr (kIsF32<T>) {
     return launch_os_lds<T, NT, 1, CSUB, 1, NT == 64 ? 6 : 8, KQ>(
         x, n_x, cred, wt, wperm, ncols, bias, nbr, n_rows, K, order, y, splits, partial, s);
   } else if constexpr (NT == 64 && CSUB == 2) {
