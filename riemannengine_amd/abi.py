@@ -418,27 +418,33 @@ def kernel_map(in_table: CoordTable, out_table: CoordTable, offsets) -> KernelMa
     kofs = torch.empty(K + 1, dtype=torch.int64, device=dev)
     flags = ctypes.c_int32(0)
     off_host = offsets.numpy()
+    # a map of a table onto itself whose stencil is closed under negation is
+    # symmetric (the count confirms it): its partners go to the device ahead
+    # of the count, which then waits for that copy with its own kernels
+    nbr_t = in_order = partner = None
+    if out_table is in_table:
+        ph = stencil_partners(off_host)
+        if ph is not None:
+            partner = torch.from_numpy(ph).pin_memory().to(dev, non_blocking=True)
+    # the one read-back: the count synchronises and fills kofs_host
+    kofs_host = np.empty(K + 1, np.int64)
     _check(L.rhip_kmap_count(ctypes.byref(in_table.struct), _ptr(out_table.ucoords),
                              _ptr(out_table.order), n_out, K,
                              off_host.ctypes.data_as(ctypes.POINTER(ctypes.c_int32)), _ptr(ws),
-                             ws.numel(), _ptr(nbr), _ptr(out_order), _ptr(kofs), None,
+                             ws.numel(), _ptr(nbr), _ptr(out_order), _ptr(kofs),
+                             kofs_host.ctypes.data_as(ctypes.POINTER(ctypes.c_int64)),
                              ctypes.byref(flags), st), "rhip_kmap_count")
     symmetric = bool(flags.value & KMAP_SYMMETRIC)
-    nbr_t = in_order = partner = None
-    if symmetric:
+    if symmetric and partner is None:
         partner = torch.from_numpy(stencil_partners(off_host)).to(dev)
-    else:
+    if not symmetric:
+        partner = None
         nbr_t = torch.empty((K, max(n_in, 1)), dtype=torch.int32, device=dev)
         in_order = torch.empty(max(n_in, 1), dtype=torch.int32, device=dev)
         _check(L.rhip_kmap_fill(_ptr(nbr), _ptr(out_order), n_out, K, _ptr(in_table.order),
                                 n_in, flags.value, _ptr(ws), ws.numel(), _ptr(kofs), None, None,
                                 _ptr(nbr_t), _ptr(in_order), st), "rhip_kmap_fill")
         nbr_t, in_order = nbr_t[:, :n_in], in_order[:n_in]
-    # the one read-back: the pair counts through pinned memory
-    kofs_pinned = torch.empty(K + 1, dtype=torch.int64, pin_memory=True)
-    kofs_pinned.copy_(kofs, non_blocking=True)
-    torch.cuda.current_stream(dev).synchronize()
-    kofs_host = kofs_pinned.numpy()
     return KernelMap(K, n_in, n_out, kofs, kofs_host, None, None, nbr[:, :n_out], nbr_t,
                      in_order, out_order[:n_out], symmetric=symmetric, partner=partner,
                      flags=flags.value)

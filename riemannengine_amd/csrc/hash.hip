@@ -43,12 +43,17 @@ constexpr int kMinmaxBlocks = 256;
 // column varies), over the coordinates read as one flat array so that loads
 // are coalesced (a lane keeps one column: the stride is a multiple of ncol);
 // partials[block][0..ncol) = min, [8..) = max, [16..) = or. Blocks past
-// mm_blocks clear the hash slots.
+// mm_blocks clear the hash slots. Block 0 clears the layout's repeat flag
+// and unique count, which the insert and numbering kernels then write.
 __global__ __launch_bounds__(kBlock) void hash_prep_kernel(const int32_t *__restrict__ coords,
                                                            int64_t n, int ncol, int mm_blocks,
                                                            int32_t *__restrict__ partials,
                                                            Slot *__restrict__ slots,
-                                                           int64_t cap) {
+                                                           int64_t cap, HashLayout *L) {
+  if (blockIdx.x == 0 && threadIdx.x == 0 && L) {
+    L->dups = 0;
+    L->n_unique = 0;
+  }
   if (static_cast<int>(blockIdx.x) >= mm_blocks) {
     const int64_t i = (blockIdx.x - mm_blocks) * (int64_t)kBlock + threadIdx.x;
     if (i < cap) {
@@ -107,13 +112,14 @@ __global__ __launch_bounds__(kBlock) void hash_prep_kernel(const int32_t *__rest
 
 __device__ __forceinline__ int bit_width_dev(uint32_t v) { return v == 0 ? 0 : 32 - __clz(v); }
 
-// One workgroup: merges the prep partials into the layout (lane k reads
-// block k's partials; wave shuffles, then LDS, combine them). Columns are
-// packed with the batch column in the top bits, so the packed order is
-// batch-major lexicographic; more than 63 bits selects the row-reference mode.
-__global__ __launch_bounds__(kBlock) void hash_layout_kernel(const int32_t *__restrict__ partials,
-                                                             int mm_blocks, int ncol, int64_t n,
-                                                             HashLayout *__restrict__ L) {
+// The whole workgroup merges the prep partials into the layout (lane k
+// reads block k's partials; wave shuffles, then LDS, combine them) and
+// thread 0 writes it to *L (every field but dups and n_unique); the caller
+// synchronises the workgroup before reading it. Columns are packed with the
+// batch column in the top bits, so the packed order is batch-major
+// lexicographic; more than 63 bits selects the row-reference mode.
+__device__ void block_layout(const int32_t *__restrict__ partials, int mm_blocks, int ncol,
+                             int64_t n, HashLayout *L) {
   constexpr int kWaves = kBlock / kWave;
   __shared__ int32_t red[kWaves][3 * RHIP_MAX_COLS];
   const int k = threadIdx.x, w = k / kWave, lane = lane_id();
@@ -138,7 +144,7 @@ __global__ __launch_bounds__(kBlock) void hash_layout_kernel(const int32_t *__re
   }
   __syncthreads();
   if (k != 0)
-    return;
+    return; // no barrier follows inside this function
   int32_t mn[RHIP_MAX_COLS], mx[RHIP_MAX_COLS], ox[RHIP_MAX_COLS];
   int bits[RHIP_MAX_COLS] = {};
   int total = 0;
@@ -168,8 +174,6 @@ __global__ __launch_bounds__(kBlock) void hash_layout_kernel(const int32_t *__re
   }
   L->mode = total <= 63 ? RHIP_KEY_PACKED64 : RHIP_KEY_ROWREF;
   L->key_bits = total <= 63 ? total : 0;
-  L->dups = 0;
-  L->n_unique = 0;
   const int rb = max(1, bit_width_dev(static_cast<uint32_t>(n - 1)));
   L->row_bits = total + rb <= 63 ? rb : 0;
 }
@@ -189,6 +193,9 @@ __device__ __forceinline__ void apply_layout(TableView &t, const HashLayout *L) 
 // earliest row that inserted the key (in the key word when row_bits > 0,
 // else in first_row through atomicMin). A row that finds its key already
 // there flags the set as having repeats.
+// Every workgroup computes the layout from the prep partials itself (a few
+// loads per lane from the L2), which saves a one-workgroup launch between
+// prep and insert; workgroup 0 publishes it for the later kernels.
 // The wave cooperates on repeats: with packed keys, a lane whose key equals
 // the previous lane's follows that run's first lane, which probes once for
 // the whole run, and takes its slot by a shuffle. Points quantised in scan
@@ -199,12 +206,28 @@ __device__ __forceinline__ void apply_layout(TableView &t, const HashLayout *L) 
 __global__ __launch_bounds__(kBlock) void insert_kernel(const int32_t *coords,
                                                         int64_t n,
                                                         TableView t,
+                                                        const int32_t *__restrict__ partials,
+                                                        int mm_blocks,
                                                         HashLayout *L,
                                                         uint32_t *slot_of_row) {
   const int64_t r = blockIdx.x * (int64_t)kBlock + threadIdx.x;
   const bool valid = r < n; // every lane stays for the wave's shuffles
-  apply_layout(t, L);
-  const int rb = L->row_bits;
+  __shared__ HashLayout sl;
+  block_layout(partials, mm_blocks, t.ncol, n, &sl);
+  __syncthreads();
+  if (blockIdx.x == 0 && threadIdx.x == 0) {
+    for (int i = 0; i < RHIP_MAX_COLS; ++i) {
+      L->lo[i] = sl.lo[i];
+      L->hi[i] = sl.hi[i];
+      L->shift[i] = sl.shift[i];
+      L->tz[i] = sl.tz[i];
+    }
+    L->mode = sl.mode;
+    L->key_bits = sl.key_bits;
+    L->row_bits = sl.row_bits;
+  }
+  apply_layout(t, &sl);
+  const int rb = sl.row_bits;
   int32_t c[RHIP_MAX_COLS];
 #pragma unroll
   for (int i = 0; i < RHIP_MAX_COLS; ++i)
@@ -308,24 +331,72 @@ __global__ __launch_bounds__(kBlock) void count_first_kernel(
 // slot's uid, and put the plain key back in the slot word (in row-reference
 // mode the key is re-pointed at the unique row). With repeats, uid_by_row
 // keeps the uid for the other rows' inverse.
+// Without block_base (grids of at most kSelfScanBlocks workgroups) each
+// workgroup sums the counts of the workgroups before it itself (none to sum
+// for a set without repeats: every earlier block holds kBlock first rows),
+// and the last workgroup writes n_unique: no scan launch in between. The
+// last workgroup then copies the finished layout to host_L (pinned host
+// memory mapped for the device, or null), which the host reads after its
+// synchronisation without a copy launch.
+constexpr int64_t kSelfScanBlocks = 4096;
 __global__ __launch_bounds__(kBlock) void assign_uid_kernel(
-    const int32_t *coords, int64_t n, int ncol, const HashLayout *L, Slot *slots,
-    const uint32_t *slot_of_row, const int64_t *block_base, int32_t *uid_by_row,
-    int64_t *mapping, int32_t *unique_coords, int64_t *inverse) {
-  __shared__ int32_t wave_counts[kBlock / kWave];
+    const int32_t *coords, int64_t n, int ncol, HashLayout *L, Slot *slots,
+    const uint32_t *slot_of_row, const int32_t *block_counts, const int64_t *block_base,
+    int32_t *uid_by_row, int64_t *mapping, int32_t *unique_coords, int64_t *inverse,
+    HashLayout *host_L) {
+  constexpr int kWaves = kBlock / kWave;
+  __shared__ int32_t wave_counts[kWaves];
+  __shared__ int64_t wave_prefix[kWaves];
   int64_t r = blockIdx.x * (int64_t)kBlock + threadIdx.x;
+  const int dups = L->dups;
   const bool first =
-      r < n && (L->dups == 0 || slots[slot_of_row[r]].first_row == static_cast<uint32_t>(r));
+      r < n && (dups == 0 || slots[slot_of_row[r]].first_row == static_cast<uint32_t>(r));
   uint64_t b = __ballot(first);
   const int w = threadIdx.x / kWave;
-  if (lane_id() == 0)
+  int64_t prefix = 0;
+  if (!block_base && dups) { // uniform: the earlier workgroups' first rows
+    for (int64_t i = threadIdx.x; i < blockIdx.x; i += kBlock)
+      prefix += block_counts[i];
+    for (int off = 32; off > 0; off >>= 1)
+      prefix += __shfl_xor(prefix, off);
+  }
+  if (lane_id() == 0) {
     wave_counts[w] = __popcll(b);
+    wave_prefix[w] = prefix;
+  }
   __syncthreads();
-  int32_t before = 0;
-  for (int i = 0; i < w; ++i)
-    before += wave_counts[i];
+  int32_t before = 0, mine = 0;
+  int64_t base = 0;
+  for (int i = 0; i < kWaves; ++i) {
+    before += i < w ? wave_counts[i] : 0;
+    mine += wave_counts[i];
+    base += wave_prefix[i];
+  }
+  if (block_base)
+    base = block_base[blockIdx.x];
+  else if (!dups)
+    base = static_cast<int64_t>(blockIdx.x) * kBlock;
+  if (blockIdx.x == gridDim.x - 1 && threadIdx.x == 0) {
+    if (!block_base)
+      L->n_unique = base + mine;
+    if (host_L) {
+      HashLayout h;
+      h.n_unique = block_base ? L->n_unique : base + mine;
+      for (int i = 0; i < RHIP_MAX_COLS; ++i) {
+        h.lo[i] = L->lo[i];
+        h.hi[i] = L->hi[i];
+        h.shift[i] = L->shift[i];
+        h.tz[i] = L->tz[i];
+      }
+      h.mode = L->mode;
+      h.key_bits = L->key_bits;
+      h.dups = dups;
+      h.row_bits = L->row_bits;
+      *host_L = h;
+    }
+  }
   if (first) {
-    const int64_t uid = block_base[blockIdx.x] + before + lanes_below(b);
+    const int64_t uid = base + before + lanes_below(b);
     if (L->dups)
       uid_by_row[r] = static_cast<int32_t>(uid);
     mapping[uid] = r;
@@ -675,12 +746,17 @@ __global__ __launch_bounds__(kBlock) void brick_count_kernel(BrickSpace s, Table
 
 // Each occupied brick's base: the locality-order position of its first row,
 // the rows of every brick before it in Morton order (chunk base from the
-// scan of brick_count_kernel's totals, then an in-workgroup scan).
+// scan of brick_count_kernel's totals, then an in-workgroup scan). Without
+// chunk_base (walks of at most kSelfScanBlocks chunks) each workgroup sums
+// the earlier chunks' totals itself, which saves the scan launch.
 template <int D>
 __global__ __launch_bounds__(kBlock) void brick_base_kernel(BrickSpace s, TableView t,
+                                                            const int32_t *__restrict__ chunk_rows,
                                                             const int64_t *__restrict__ chunk_base,
                                                             Brick *__restrict__ grid) {
-  __shared__ int32_t wave_sum[kBlock / kWave];
+  constexpr int kWaves = kBlock / kWave;
+  __shared__ int32_t wave_sum[kWaves];
+  __shared__ int64_t wave_prefix[kWaves];
   const int64_t m0 = blockIdx.x * kSpan + static_cast<int64_t>(threadIdx.x) * kSpanPer;
   int64_t g[kSpanPer];
   uint64_t mk[kSpanPer];
@@ -692,6 +768,13 @@ __global__ __launch_bounds__(kBlock) void brick_base_kernel(BrickSpace s, TableV
     cnt += __popcll(mk[i]);
   }
   const int lane = lane_id(), w = threadIdx.x / kWave;
+  int64_t prefix = 0;
+  if (!chunk_base) {
+    for (int64_t i = threadIdx.x; i < blockIdx.x; i += kBlock)
+      prefix += chunk_rows[i];
+    for (int off = 32; off > 0; off >>= 1)
+      prefix += __shfl_xor(prefix, off);
+  }
   int32_t incl = cnt;
   for (int off = 1; off < kWave; off <<= 1) {
     const int32_t o = __shfl_up(incl, off, kWave);
@@ -700,8 +783,16 @@ __global__ __launch_bounds__(kBlock) void brick_base_kernel(BrickSpace s, TableV
   }
   if (lane == kWave - 1)
     wave_sum[w] = incl;
+  if (lane == 0)
+    wave_prefix[w] = prefix;
   __syncthreads();
-  int64_t run = chunk_base[blockIdx.x] + incl - cnt;
+  int64_t run = incl - cnt;
+  if (chunk_base) {
+    run += chunk_base[blockIdx.x];
+  } else {
+    for (int i = 0; i < kWaves; ++i)
+      run += wave_prefix[i];
+  }
   for (int i = 0; i < w; ++i)
     run += wave_sum[i];
 #pragma unroll
@@ -860,7 +951,7 @@ extern "C" int rhip_hash_build(const int32_t *coords, int64_t n, int32_t ncol,
     Slot *sl = static_cast<Slot *>(slots);
     if (n == 0) {
       hipLaunchKernelGGL(hash_prep_kernel, dim3(ceil_div(cap, kBlock)), dim3(kBlock), 0, stream,
-                         coords, n, ncol, 0, w.partials, sl, cap);
+                         coords, n, ncol, 0, w.partials, sl, cap, nullptr);
       RHIP_LAUNCH_CHECK();
       table->mode = RHIP_KEY_PACKED64;
       table->n_unique = 0;
@@ -868,38 +959,45 @@ extern "C" int rhip_hash_build(const int32_t *coords, int64_t n, int32_t ncol,
         table->hi[c] = -1; // empty range: every probe misses on span check
       return;
     }
-    // column ranges and slot clearing in one launch, then the layout on the
-    // device: the inserts start without a host round trip
+    // column ranges and slot clearing in one launch; each insert workgroup
+    // merges the ranges into the layout: no host round trip before the
+    // inserts
     const int mm = static_cast<int>(std::min<int64_t>(
         kMinmaxBlocks, std::max<int64_t>(1, ceil_div(n * ncol, int64_t(kBlock) * 8))));
     hipLaunchKernelGGL(hash_prep_kernel, dim3(mm + ceil_div(cap, kBlock)), dim3(kBlock), 0,
-                       stream, coords, n, ncol, mm, w.partials, sl, cap);
-    RHIP_LAUNCH_CHECK();
-    hipLaunchKernelGGL(hash_layout_kernel, dim3(1), dim3(kBlock), 0, stream, w.partials, mm, ncol,
-                       n, w.layout);
+                       stream, coords, n, ncol, mm, w.partials, sl, cap, w.layout);
     RHIP_LAUNCH_CHECK();
     // The row-reference build probes the caller's coordinates; lookups after
     // the build probe unique_coords (assign_uid_kernel re-points the slots).
     TableView tv = make_view(*table);
     tv.rows = coords;
     const int64_t nb = ceil_div(n, kBlock);
-    hipLaunchKernelGGL(insert_kernel, dim3(nb), dim3(kBlock), 0, stream, coords, n, tv, w.layout,
-                       w.slot_of_row);
+    hipLaunchKernelGGL(insert_kernel, dim3(nb), dim3(kBlock), 0, stream, coords, n, tv,
+                       w.partials, mm, w.layout, w.slot_of_row);
     RHIP_LAUNCH_CHECK();
     hipLaunchKernelGGL(count_first_kernel, dim3(nb), dim3(kBlock), 0, stream, n, w.layout, sl,
                        w.slot_of_row, w.block_counts);
     RHIP_LAUNCH_CHECK();
-    hipLaunchKernelGGL(scan_kernel<int32_t>, dim3(1), dim3(1024), 0, stream, w.block_counts, nb,
-                       w.block_base, &w.layout->n_unique);
-    RHIP_LAUNCH_CHECK();
-    hipLaunchKernelGGL(assign_uid_kernel, dim3(nb), dim3(kBlock), 0, stream, coords, n, ncol,
-                       w.layout, sl, w.slot_of_row, w.block_base, w.uid_by_row, mapping,
-                       unique_coords, inverse);
-    RHIP_LAUNCH_CHECK();
+    // up to kSelfScanBlocks workgroups the numbering sums the earlier
+    // workgroups' counts itself
+    const bool self_scan = nb <= kSelfScanBlocks;
+    if (!self_scan) {
+      hipLaunchKernelGGL(scan_kernel<int32_t>, dim3(1), dim3(1024), 0, stream, w.block_counts, nb,
+                         w.block_base, &w.layout->n_unique);
+      RHIP_LAUNCH_CHECK();
+    }
     HashLayout hl;
     {
+      // the numbering's last workgroup writes the layout into the pinned
+      // buffer when the device can address it, else one copy reads it back
       PinnedReadback rb = pinned_readback(sizeof(hl));
-      RHIP_HIP(hipMemcpyAsync(rb.ptr, w.layout, sizeof(hl), hipMemcpyDeviceToHost, stream));
+      hipLaunchKernelGGL(assign_uid_kernel, dim3(nb), dim3(kBlock), 0, stream, coords, n, ncol,
+                         w.layout, sl, w.slot_of_row, w.block_counts,
+                         self_scan ? nullptr : w.block_base, w.uid_by_row, mapping,
+                         unique_coords, inverse, static_cast<HashLayout *>(rb.dev));
+      RHIP_LAUNCH_CHECK();
+      if (!rb.dev)
+        RHIP_HIP(hipMemcpyAsync(rb.ptr, w.layout, sizeof(hl), hipMemcpyDeviceToHost, stream));
       RHIP_HIP(hipStreamSynchronize(stream));
       std::memcpy(&hl, rb.ptr, sizeof(hl));
     }
@@ -1035,8 +1133,9 @@ BrickSpace brick_space(const BrickLayout &bl, int D) {
 
 // Locality order through the brick grid, a counting sort: the rows mark
 // their cells in the cleared grid, a walk of the grid in brick Morton order
-// counts the occupied cells per chunk, a scan of the chunk totals and a
-// second walk give every occupied brick its base, and each row lands at its
+// counts the occupied cells per chunk, a scan of the chunk totals (inside
+// the second walk for up to kSelfScanBlocks chunks) and a second walk give
+// every occupied brick its base, and each row lands at its
 // brick's base plus the occupied cells below its own. The order equals the
 // sorted locality keys'. (Counting rows per chunk with atomics in the mark
 // pass instead serialises on the few chunk counters: 1.2 ms against 12 us
@@ -1060,11 +1159,14 @@ void order_by_bricks(const rhip_table &table, const BrickLayout &bl, const Brick
   hipLaunchKernelGGL(brick_count_kernel<D>, dim3(chunks), dim3(kBlock), 0, stream, bs, t, grid,
                      chunk_rows);
   RHIP_LAUNCH_CHECK();
-  hipLaunchKernelGGL(scan_kernel<int32_t>, dim3(1), dim3(1024), 0, stream, chunk_rows, chunks,
-                     chunk_base, total);
-  RHIP_LAUNCH_CHECK();
+  const bool self_scan = chunks <= kSelfScanBlocks;
+  if (!self_scan) {
+    hipLaunchKernelGGL(scan_kernel<int32_t>, dim3(1), dim3(1024), 0, stream, chunk_rows, chunks,
+                       chunk_base, total);
+    RHIP_LAUNCH_CHECK();
+  }
   hipLaunchKernelGGL(brick_base_kernel<D>, dim3(chunks), dim3(kBlock), 0, stream, bs, t,
-                     chunk_base, grid);
+                     chunk_rows, self_scan ? nullptr : chunk_base, grid);
   RHIP_LAUNCH_CHECK();
   hipLaunchKernelGGL(brick_place_kernel<D>, dim3(nb), dim3(kBlock), 0, stream, t, n, grid, order,
                      pos);

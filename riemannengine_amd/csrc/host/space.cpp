@@ -530,11 +530,31 @@ HipKernelMap CoordinateManager::generate(const CoordinateMapHIP &in_map,
   auto out_order = torch::empty({std::max<int64_t>(n_out, 1)}, iopt);
   m.offsets = torch::empty({K + 1}, iopt.dtype(torch::kInt64));
   int32_t flags = 0;
+  // A map of a set onto itself whose stencil is closed under negation is
+  // symmetric (the count confirms it): its partners go to the device from
+  // pinned memory ahead of the count, whose synchronisation covers the copy.
+  auto upload_partners = [&]() {
+    auto pinned = torch::empty({K}, torch::TensorOptions().dtype(torch::kInt32).pinned_memory(true));
+    std::memcpy(pinned.data_ptr<int32_t>(), m.partner_host.data(), sizeof(int32_t) * K);
+    m.partner = pinned.to(dev, /*non_blocking=*/true);
+  };
+  if (&in_map == &out_map) {
+    m.partner_host.resize(K);
+    if (rhip_stencil_partners(offsets.data_ptr<int32_t>(), K,
+                              static_cast<int32_t>(offsets.size(1)),
+                              m.partner_host.data()) == RHIP_OK)
+      upload_partners();
+    else
+      m.partner_host.clear();
+  }
+  // the one synchronisation: the count reads the pair counts back into
+  // m.offsets_host
+  m.offsets_host.resize(K + 1);
   check_rhip(rhip_kmap_count(&in_map.table, out_map.coords.data_ptr<int32_t>(),
                              out_map.order.data_ptr<int32_t>(), n_out, K,
                              offsets.data_ptr<int32_t>(), ws.data_ptr(), ws.numel(),
                              nbr.data_ptr<int32_t>(), out_order.data_ptr<int32_t>(),
-                             m.offsets.data_ptr<int64_t>(), nullptr, &flags, st),
+                             m.offsets.data_ptr<int64_t>(), m.offsets_host.data(), &flags, st),
              "rhip_kmap_count");
   // A symmetric map keeps no transposed table (its input gradient runs on
   // nbr with the stencil partners as weight permutation); any other map gets
@@ -543,17 +563,17 @@ HipKernelMap CoordinateManager::generate(const CoordinateMapHIP &in_map,
   m.symmetric = (flags & RHIP_KMAP_SYMMETRIC) != 0;
   at::Tensor nbr_t, in_order;
   if (m.symmetric) {
-    m.partner_host.resize(K);
-    check_rhip(rhip_stencil_partners(offsets.data_ptr<int32_t>(), K,
-                                     static_cast<int32_t>(offsets.size(1)),
-                                     m.partner_host.data()),
-               "rhip_stencil_partners");
-    // to the device from pinned memory, ordered before the synchronisation
-    // below (a copy from pageable memory would block the host once more)
-    auto pinned = torch::empty({K}, torch::TensorOptions().dtype(torch::kInt32).pinned_memory(true));
-    std::memcpy(pinned.data_ptr<int32_t>(), m.partner_host.data(), sizeof(int32_t) * K);
-    m.partner = pinned.to(dev, /*non_blocking=*/true);
+    if (!m.partner.defined()) {
+      m.partner_host.resize(K);
+      check_rhip(rhip_stencil_partners(offsets.data_ptr<int32_t>(), K,
+                                       static_cast<int32_t>(offsets.size(1)),
+                                       m.partner_host.data()),
+                 "rhip_stencil_partners");
+      upload_partners();
+    }
   } else {
+    m.partner = at::Tensor();
+    m.partner_host.clear();
     nbr_t = torch::empty({K, std::max<int64_t>(n_in, 1)}, iopt);
     in_order = torch::empty({std::max<int64_t>(n_in, 1)}, iopt);
     check_rhip(rhip_kmap_fill(nbr.data_ptr<int32_t>(), out_order.data_ptr<int32_t>(), n_out, K,
@@ -562,13 +582,6 @@ HipKernelMap CoordinateManager::generate(const CoordinateMapHIP &in_map,
                               nbr_t.data_ptr<int32_t>(), in_order.data_ptr<int32_t>(), st),
                "rhip_kmap_fill");
   }
-  // the one synchronisation: the pair counts through pinned memory (a copy
-  // to pageable memory goes through a staging copy)
-  auto host_offsets = torch::empty({K + 1}, torch::TensorOptions().dtype(torch::kInt64).pinned_memory(true));
-  host_offsets.copy_(m.offsets, /*non_blocking=*/true);
-  check_hip(hipStreamSynchronize(st), "hipStreamSynchronize");
-  const int64_t *ho = host_offsets.data_ptr<int64_t>();
-  m.offsets_host.assign(ho, ho + K + 1);
   m.nbr = nbr.slice(1, 0, n_out);
   m.out_order = out_order.slice(0, 0, n_out);
   if (!m.symmetric) {

@@ -343,14 +343,15 @@ __global__ __launch_bounds__(kMapBlock) void kmap_mask_kernel(
 // Query pass: one lane per processing position p (row j = jpos[p] of the
 // spatial order, or p): nbr[k][p] = the input row paired with it under k
 // (coalesced over p), out_order[p] = its row, and per offset k the number of
-// hits of each wave w, wave_counts[k][w].
+// hits of each wave w, wave_counts[k][w]. Workgroup 0 also clears the
+// ticket of kmap_totals_kernel, which runs next.
 template <int D, int KC = 0, bool NBHD = false>
 __global__ __launch_bounds__(kMapBlock) void kmap_query_kernel(
     TableView t, const int32_t *__restrict__ out_coords, const int32_t *__restrict__ spatial,
     const int32_t *__restrict__ jpos, int64_t n_out, const int32_t *__restrict__ offsets, int K,
     int64_t nw, int32_t *__restrict__ nbr, int32_t *__restrict__ out_order,
     int32_t *__restrict__ wave_counts, SmallUpload up, int32_t *__restrict__ up_dst0, int up_n0,
-    int32_t *__restrict__ up_dst1, int up_n1) {
+    int32_t *__restrict__ up_dst1, int up_n1, uint32_t *__restrict__ ticket) {
   if constexpr (KC > 0)
     K = KC;
   // a few host values for later launches, carried in the arguments: the
@@ -360,6 +361,8 @@ __global__ __launch_bounds__(kMapBlock) void kmap_query_kernel(
       up_dst0[i] = up.v[i];
     for (int i = threadIdx.x; i < up_n1; i += kMapBlock)
       up_dst1[i] = up.v[up_n0 + i];
+    if (threadIdx.x == 0)
+      *ticket = 0;
   }
   const int64_t p = blockIdx.x * (int64_t)kMapBlock + threadIdx.x;
   const int64_t w = p / kWave;
@@ -410,16 +413,19 @@ __global__ __launch_bounds__(kMapBlock) void kmap_query_kernel(
 }
 
 // kmap_offsets[k] = sum of the per-offset totals before k (one workgroup).
-__global__ __launch_bounds__(1024) void kmap_offsets_kernel(const int64_t *ktotal, int K,
-                                                            int64_t *kmap_offsets,
-                                                            int64_t *scratch) {
+// The CSR offsets of K pair totals, by one 1024-thread workgroup: total(i)
+// reads total i; the offsets go to kmap_offsets and, when given, to host
+// memory mapped for the device.
+template <typename Total>
+__device__ void offsets_from_totals(Total total, int K, int64_t *kmap_offsets,
+                                    int64_t *host_offsets) {
   __shared__ int64_t partial[1024];
   const int t = threadIdx.x;
   const int per = (K + 1023) / 1024;
   const int b = t * per, e = min(K, b + per);
   int64_t s = 0;
   for (int i = b; i < e; ++i)
-    s += ktotal[i];
+    s += total(i);
   partial[t] = s;
   __syncthreads();
   for (int off = 1; off < 1024; off <<= 1) {
@@ -431,11 +437,51 @@ __global__ __launch_bounds__(1024) void kmap_offsets_kernel(const int64_t *ktota
   int64_t run = partial[t] - s;
   for (int i = b; i < e; ++i) {
     kmap_offsets[i] = run;
-    run += ktotal[i];
+    if (host_offsets)
+      host_offsets[i] = run;
+    run += total(i);
   }
-  if (t == 1023)
+  if (t == 1023) {
     kmap_offsets[K] = partial[1023];
-  (void)scratch;
+    if (host_offsets)
+      host_offsets[K] = partial[1023];
+  }
+}
+
+__global__ __launch_bounds__(1024) void kmap_offsets_kernel(const int64_t *ktotal, int K,
+                                                            int64_t *kmap_offsets,
+                                                            int64_t *host_offsets) {
+  offsets_from_totals([&](int i) { return ktotal[i]; }, K, kmap_offsets, host_offsets);
+}
+
+// Workgroup k: the exclusive scan of offset k's wave counts (wave_base, for
+// phase 2's emit) and its pair total. The workgroup that finishes last (by
+// a ticket the query kernel cleared) turns the K totals into the CSR
+// offsets: one launch where a scan and an offsets launch were. The totals
+// are stored and read as agent-scope atomics, after a release (the ticket's
+// increment) and an acquire, so the last workgroup sees every other
+// workgroup's total whichever XCD wrote it.
+__global__ __launch_bounds__(1024) void kmap_totals_kernel(const int32_t *wave_counts, int64_t nw,
+                                                           int K, int64_t *wave_base,
+                                                           int64_t *ktotal, uint32_t *ticket,
+                                                           int64_t *kmap_offsets,
+                                                           int64_t *host_offsets) {
+  __shared__ int last;
+  const int64_t total = segment_scan(wave_counts, nw, wave_base);
+  if (threadIdx.x == 0) {
+    __hip_atomic_store(&ktotal[blockIdx.x], total, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __threadfence();
+    last = atomicAdd(ticket, 1u) == static_cast<uint32_t>(K - 1);
+    __threadfence();
+  }
+  __syncthreads();
+  if (!last)
+    return; // uniform
+  offsets_from_totals(
+      [&](int i) {
+        return __hip_atomic_load(&ktotal[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      },
+      K, kmap_offsets, host_offsets);
 }
 
 __global__ __launch_bounds__(kMapBlock) void fill_i32_kernel(int32_t *p,
@@ -573,6 +619,7 @@ struct KmapWs {
   int32_t *wave_counts; // [K][waves] hits per wave and offset (phase 1)
   int64_t *wave_base;   // their per-offset exclusive scans (phase 1 -> 2)
   int64_t *ktotal;
+  uint32_t *ticket;     // kmap_totals_kernel's finished workgroups
   int32_t *offsets;     // [K][D] stencil (D = the table's ncol - 1)
   int32_t *partner;     // [K] partner offsets of a symmetric map (phase 1 -> 2)
   // phase 1
@@ -595,6 +642,7 @@ static KmapWs carve_kmap(Carve &cv, int64_t n_in, int64_t n_out, int32_t K, int3
   w.wave_counts = cv.take<int32_t>(nw * K);
   w.wave_base = cv.take<int64_t>(nw * K);
   w.ktotal = cv.take<int64_t>(K);
+  w.ticket = cv.take<uint32_t>(1);
   w.offsets = cv.take<int32_t>(static_cast<size_t>(K) * std::max(D, 1));
   w.partner = cv.take<int32_t>(K);
   const size_t base = cv.used;
@@ -771,7 +819,7 @@ extern "C" int rhip_kmap_count(const rhip_table *in_table, const int32_t *out_co
             hipLaunchKernelGGL((kmap_query_kernel<3, 27, true>), dim3(nb), dim3(kMapBlock), 0,
                                stream, tv, out_coords, out_spatial_order, jpos, n_out, w.offsets,
                                K, nw, nbr, out_order, w.wave_counts, small, w.offsets,
-                               n_sten, w.partner, n_part);
+                               n_sten, w.partner, n_part, w.ticket);
             RHIP_LAUNCH_CHECK();
             return;
           }
@@ -793,24 +841,41 @@ extern "C" int rhip_kmap_count(const rhip_table *in_table, const int32_t *out_co
         if (k27)
           hipLaunchKernelGGL((kmap_query_kernel<DD, 27>), dim3(nb), dim3(kMapBlock), 0, stream,
                              tv, out_coords, out_spatial_order, jpos, n_out, w.offsets, K, nw,
-                             nbr, out_order, w.wave_counts, small, w.offsets, 0, w.partner, 0);
+                             nbr, out_order, w.wave_counts, small, w.offsets, 0, w.partner, 0,
+                             w.ticket);
         else
           hipLaunchKernelGGL((kmap_query_kernel<DD>), dim3(nb), dim3(kMapBlock), 0, stream, tv,
                              out_coords, out_spatial_order, jpos, n_out, w.offsets, K, nw, nbr,
-                             out_order, w.wave_counts, small, w.offsets, 0, w.partner, 0);
+                             out_order, w.wave_counts, small, w.offsets, 0, w.partner, 0,
+                             w.ticket);
         RHIP_LAUNCH_CHECK();
       });
     }
-    hipLaunchKernelGGL(scan_kernel<int32_t>, dim3(K), dim3(1024), 0, stream, w.wave_counts,
-                       nw, w.wave_base, w.ktotal);
-    RHIP_LAUNCH_CHECK();
-    hipLaunchKernelGGL(kmap_offsets_kernel, dim3(1), dim3(1024), 0, stream, w.ktotal, K,
-                       kmap_offsets, nullptr);
-    RHIP_LAUNCH_CHECK();
+    // with kmap_offsets_host, the offsets also go to the thread's pinned
+    // read-back buffer: written by the kernel where the device can address
+    // it, else copied
+    const size_t hb = sizeof(int64_t) * (K + 1);
+    PinnedReadback rb{nullptr, nullptr};
+    if (kmap_offsets_host)
+      rb = pinned_readback(hb);
+    int64_t *host_dev = static_cast<int64_t *>(rb.dev);
+    if (n_out > 0) { // the query kernel cleared the ticket
+      hipLaunchKernelGGL(kmap_totals_kernel, dim3(K), dim3(1024), 0, stream, w.wave_counts, nw, K,
+                         w.wave_base, w.ktotal, w.ticket, kmap_offsets, host_dev);
+      RHIP_LAUNCH_CHECK();
+    } else {
+      hipLaunchKernelGGL(scan_kernel<int32_t>, dim3(K), dim3(1024), 0, stream, w.wave_counts,
+                         nw, w.wave_base, w.ktotal);
+      RHIP_LAUNCH_CHECK();
+      hipLaunchKernelGGL(kmap_offsets_kernel, dim3(1), dim3(1024), 0, stream, w.ktotal, K,
+                         kmap_offsets, host_dev);
+      RHIP_LAUNCH_CHECK();
+    }
     if (kmap_offsets_host) { // else asynchronous: the caller reads kmap_offsets later
-      RHIP_HIP(hipMemcpyAsync(kmap_offsets_host, kmap_offsets, sizeof(int64_t) * (K + 1),
-                              hipMemcpyDeviceToHost, stream));
+      if (!host_dev)
+        RHIP_HIP(hipMemcpyAsync(rb.ptr, kmap_offsets, hb, hipMemcpyDeviceToHost, stream));
       RHIP_HIP(hipStreamSynchronize(stream));
+      std::memcpy(kmap_offsets_host, rb.ptr, hb);
     }
   });
 }

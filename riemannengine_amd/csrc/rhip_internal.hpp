@@ -37,9 +37,12 @@ struct Error : std::runtime_error {
 void set_last_error(const std::string &msg);
 
 // The calling thread's pinned host buffer of at least `bytes` for small
-// device-to-host read-backs (valid until the thread's next request).
+// device-to-host read-backs (valid until the thread's next request): ptr for
+// the host, dev the address a kernel writes it through (null when the
+// runtime gives none; then read back with a copy).
 struct PinnedReadback {
   void *ptr;
+  void *dev;
 };
 PinnedReadback pinned_readback(size_t bytes);
 
@@ -296,9 +299,10 @@ __device__ __forceinline__ bool repeats_prev_row(const int32_t (&c)[RHIP_MAX_COL
 // base[s*m + i] = sum(counts[s*m .. s*m+i)), total[s] = sum of segment s.
 // The segment goes in chunks of 4096 entries, four consecutive ones per lane
 // (loads issued together), one workgroup scan per chunk and a carry.
+// segment_scan is the workgroup's part; it returns the segment's total in
+// every thread.
 template <typename TIn>
-__global__ __launch_bounds__(1024) void scan_kernel(const TIn *counts, int64_t m,
-                                                    int64_t *base, int64_t *total) {
+__device__ int64_t segment_scan(const TIn *counts, int64_t m, int64_t *base) {
   constexpr int kWaves = 1024 / kWave;
   __shared__ int64_t wave_sum[kWaves];
   const int t = threadIdx.x, lane = t & (kWave - 1), w = t / kWave;
@@ -338,7 +342,14 @@ __global__ __launch_bounds__(1024) void scan_kernel(const TIn *counts, int64_t m
     carry += chunk;
     __syncthreads(); // wave_sum is rewritten by the next chunk
   }
-  if (t == 0)
+  return carry;
+}
+
+template <typename TIn>
+__global__ __launch_bounds__(1024) void scan_kernel(const TIn *counts, int64_t m,
+                                                    int64_t *base, int64_t *total) {
+  const int64_t carry = segment_scan(counts, m, base);
+  if (threadIdx.x == 0)
     total[blockIdx.x] = carry;
 }
 
