@@ -42,7 +42,9 @@ constexpr int kMinmaxBlocks = 256;
 // (value ^ row 0's value) (its lowest set bit is the lowest bit in which the
 // column varies), over the coordinates read as one flat array so that loads
 // are coalesced (a lane keeps one column: the stride is a multiple of ncol);
-// partials[block][0..ncol) = min, [8..) = max, [16..) = or. Blocks past
+// field f of block b at partials[f * kMinmaxBlocks + b], fields [0..ncol) =
+// min, [8..) = max, [16..) = or (field-major: the layout's lanes read one
+// field of consecutive blocks together). Blocks past
 // mm_blocks clear the hash slots. Block 0 clears the layout's repeat flag
 // and unique count, which the insert and numbering kernels then write.
 __global__ __launch_bounds__(kBlock) void hash_prep_kernel(const int32_t *__restrict__ coords,
@@ -103,33 +105,36 @@ __global__ __launch_bounds__(kBlock) void hash_prep_kernel(const int32_t *__rest
   }
   __syncthreads();
   if (threadIdx.x < ncol) {
-    int32_t *p = partials + blockIdx.x * 3 * RHIP_MAX_COLS;
-    p[threadIdx.x] = smin[threadIdx.x];
-    p[RHIP_MAX_COLS + threadIdx.x] = smax[threadIdx.x];
-    p[2 * RHIP_MAX_COLS + threadIdx.x] = sor[threadIdx.x];
+    int32_t *p = partials + blockIdx.x;
+    p[threadIdx.x * kMinmaxBlocks] = smin[threadIdx.x];
+    p[(RHIP_MAX_COLS + threadIdx.x) * kMinmaxBlocks] = smax[threadIdx.x];
+    p[(2 * RHIP_MAX_COLS + threadIdx.x) * kMinmaxBlocks] = sor[threadIdx.x];
   }
 }
 
 __device__ __forceinline__ int bit_width_dev(uint32_t v) { return v == 0 ? 0 : 32 - __clz(v); }
 
-// The whole workgroup merges the prep partials into the layout (lane k
-// reads block k's partials; wave shuffles, then LDS, combine them) and
-// thread 0 writes it to *L (every field but dups and n_unique); the caller
-// synchronises the workgroup before reading it. Columns are packed with the
-// batch column in the top bits, so the packed order is batch-major
-// lexicographic; more than 63 bits selects the row-reference mode.
-__device__ void block_layout(const int32_t *__restrict__ partials, int mm_blocks, int ncol,
-                             int64_t n, HashLayout *L) {
+// One workgroup merges the prep partials into the layout (lane k reads
+// block k's partials, field-major; wave shuffles, then LDS, combine them)
+// and thread 0 writes it to *L (every field but dups and n_unique, which
+// prep cleared). Columns are packed with the batch column in the top bits,
+// so the packed order is batch-major lexicographic; more than 63 bits
+// selects the row-reference mode. (The same merge at the start of every
+// insert workgroup, to save this launch, ran the insert 29 -> 37 us on
+// config 2: the serial tail and two barriers in each of 1,600 workgroups.)
+__global__ __launch_bounds__(kBlock) void hash_layout_kernel(const int32_t *__restrict__ partials,
+                                                             int mm_blocks, int ncol, int64_t n,
+                                                             HashLayout *__restrict__ L) {
   constexpr int kWaves = kBlock / kWave;
   __shared__ int32_t red[kWaves][3 * RHIP_MAX_COLS];
   const int k = threadIdx.x, w = k / kWave, lane = lane_id();
   for (int c = 0; c < ncol; ++c) {
     int32_t a = INT_MAX, b = INT_MIN, o = 0;
     for (int j = k; j < mm_blocks; j += kBlock) {
-      const int32_t *p = partials + j * 3 * RHIP_MAX_COLS;
-      a = min(a, p[c]);
-      b = max(b, p[RHIP_MAX_COLS + c]);
-      o |= p[2 * RHIP_MAX_COLS + c];
+      const int32_t *p = partials + j;
+      a = min(a, p[c * kMinmaxBlocks]);
+      b = max(b, p[(RHIP_MAX_COLS + c) * kMinmaxBlocks]);
+      o |= p[(2 * RHIP_MAX_COLS + c) * kMinmaxBlocks];
     }
     for (int off = 32; off > 0; off >>= 1) {
       a = min(a, __shfl_xor(a, off));
@@ -144,7 +149,7 @@ __device__ void block_layout(const int32_t *__restrict__ partials, int mm_blocks
   }
   __syncthreads();
   if (k != 0)
-    return; // no barrier follows inside this function
+    return;
   int32_t mn[RHIP_MAX_COLS], mx[RHIP_MAX_COLS], ox[RHIP_MAX_COLS];
   int bits[RHIP_MAX_COLS] = {};
   int total = 0;
@@ -193,9 +198,6 @@ __device__ __forceinline__ void apply_layout(TableView &t, const HashLayout *L) 
 // earliest row that inserted the key (in the key word when row_bits > 0,
 // else in first_row through atomicMin). A row that finds its key already
 // there flags the set as having repeats.
-// Every workgroup computes the layout from the prep partials itself (a few
-// loads per lane from the L2), which saves a one-workgroup launch between
-// prep and insert; workgroup 0 publishes it for the later kernels.
 // The wave cooperates on repeats: with packed keys, a lane whose key equals
 // the previous lane's follows that run's first lane, which probes once for
 // the whole run, and takes its slot by a shuffle. Points quantised in scan
@@ -206,28 +208,12 @@ __device__ __forceinline__ void apply_layout(TableView &t, const HashLayout *L) 
 __global__ __launch_bounds__(kBlock) void insert_kernel(const int32_t *coords,
                                                         int64_t n,
                                                         TableView t,
-                                                        const int32_t *__restrict__ partials,
-                                                        int mm_blocks,
                                                         HashLayout *L,
                                                         uint32_t *slot_of_row) {
   const int64_t r = blockIdx.x * (int64_t)kBlock + threadIdx.x;
   const bool valid = r < n; // every lane stays for the wave's shuffles
-  __shared__ HashLayout sl;
-  block_layout(partials, mm_blocks, t.ncol, n, &sl);
-  __syncthreads();
-  if (blockIdx.x == 0 && threadIdx.x == 0) {
-    for (int i = 0; i < RHIP_MAX_COLS; ++i) {
-      L->lo[i] = sl.lo[i];
-      L->hi[i] = sl.hi[i];
-      L->shift[i] = sl.shift[i];
-      L->tz[i] = sl.tz[i];
-    }
-    L->mode = sl.mode;
-    L->key_bits = sl.key_bits;
-    L->row_bits = sl.row_bits;
-  }
-  apply_layout(t, &sl);
-  const int rb = sl.row_bits;
+  apply_layout(t, L);
+  const int rb = L->row_bits;
   int32_t c[RHIP_MAX_COLS];
 #pragma unroll
   for (int i = 0; i < RHIP_MAX_COLS; ++i)
@@ -253,7 +239,9 @@ __global__ __launch_bounds__(kBlock) void insert_kernel(const int32_t *coords,
     const uint64_t mine = rb > 0 ? (key << rb) | static_cast<uint64_t>(r) : key;
     while (true) {
       // one round trip per probe: the CAS either claims the empty slot or
-      // returns the word already there
+      // returns the word already there (a load before it, to spare the
+      // atomic on occupied slots, adds a round trip: config 2's insert 31.6
+      // -> 39.5 us)
       uint64_t *wp = &t.slots[h].word;
       const uint64_t w = atomicCAS(reinterpret_cast<unsigned long long *>(wp), kEmptyWord, mine);
       if (w == kEmptyWord) {
@@ -959,21 +947,23 @@ extern "C" int rhip_hash_build(const int32_t *coords, int64_t n, int32_t ncol,
         table->hi[c] = -1; // empty range: every probe misses on span check
       return;
     }
-    // column ranges and slot clearing in one launch; each insert workgroup
-    // merges the ranges into the layout: no host round trip before the
-    // inserts
+    // column ranges and slot clearing in one launch, then the layout on the
+    // device: the inserts start without a host round trip
     const int mm = static_cast<int>(std::min<int64_t>(
         kMinmaxBlocks, std::max<int64_t>(1, ceil_div(n * ncol, int64_t(kBlock) * 8))));
     hipLaunchKernelGGL(hash_prep_kernel, dim3(mm + ceil_div(cap, kBlock)), dim3(kBlock), 0,
                        stream, coords, n, ncol, mm, w.partials, sl, cap, w.layout);
+    RHIP_LAUNCH_CHECK();
+    hipLaunchKernelGGL(hash_layout_kernel, dim3(1), dim3(kBlock), 0, stream, w.partials, mm, ncol,
+                       n, w.layout);
     RHIP_LAUNCH_CHECK();
     // The row-reference build probes the caller's coordinates; lookups after
     // the build probe unique_coords (assign_uid_kernel re-points the slots).
     TableView tv = make_view(*table);
     tv.rows = coords;
     const int64_t nb = ceil_div(n, kBlock);
-    hipLaunchKernelGGL(insert_kernel, dim3(nb), dim3(kBlock), 0, stream, coords, n, tv,
-                       w.partials, mm, w.layout, w.slot_of_row);
+    hipLaunchKernelGGL(insert_kernel, dim3(nb), dim3(kBlock), 0, stream, coords, n, tv, w.layout,
+                       w.slot_of_row);
     RHIP_LAUNCH_CHECK();
     hipLaunchKernelGGL(count_first_kernel, dim3(nb), dim3(kBlock), 0, stream, n, w.layout, sl,
                        w.slot_of_row, w.block_counts);
