@@ -287,7 +287,8 @@ __device__ __forceinline__ void probe27_bricks(const TableView &t, const int32_t
 }
 
 // Mask pass: one lane per output row j in spatial order (row spatial[j]):
-// keys[j] = the sort key of the row's neighbour mask, vals[j] = j.
+// keys[j] = the sort key of the row's neighbour mask, vals[j] = its output
+// row spatial[j].
 // KC > 0: K == KC at compile time (the probe rounds unroll and the stencil
 // loads hoist out of them). NBHD: the symmetric 3^3 map through
 // probe27_bricks (KC == 27, D == 3).
@@ -318,7 +319,7 @@ __global__ __launch_bounds__(kMapBlock) void kmap_mask_kernel(
       if (r[k] >= 0)
         m0 |= 1ull << k;
     keys[j] = mask_key(m0, m1, K);
-    vals[j] = static_cast<int32_t>(j);
+    vals[j] = static_cast<int32_t>(o);
     return;
   }
 #pragma unroll
@@ -337,11 +338,12 @@ __global__ __launch_bounds__(kMapBlock) void kmap_mask_kernel(
     }
   }
   keys[j] = mask_key(m0, m1, K);
-  vals[j] = static_cast<int32_t>(j);
+  vals[j] = static_cast<int32_t>(o);
 }
 
-// Query pass: one lane per processing position p (row j = jpos[p] of the
-// spatial order, or p): nbr[k][p] = the input row paired with it under k
+// Query pass: one lane per processing position p (output row jpos[p] from
+// the mask sort, else spatial[p], else p): nbr[k][p] = the input row paired
+// with it under k
 // (coalesced over p; streaming stores for it ran the kernel 22.8 -> 28.9 us
 // on config 2), out_order[p] = its row, and per offset k the number of
 // hits of each wave w, wave_counts[k][w]. Workgroup 0 also clears the
@@ -372,8 +374,8 @@ __global__ __launch_bounds__(kMapBlock) void kmap_query_kernel(
   const bool in = p < n_out;
   int32_t c[D + 1] = {};
   if (in) {
-    const int64_t j = jpos ? jpos[p] : p;
-    const int64_t o = spatial ? spatial[j] : j;
+    // the mask sort carries the output row itself: one dependent load less
+    const int64_t o = jpos ? jpos[p] : (spatial ? spatial[p] : p);
     out_order[p] = static_cast<int32_t>(o);
 #pragma unroll
     for (int i = 0; i <= D; ++i)
