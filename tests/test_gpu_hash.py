@@ -162,16 +162,19 @@ def _brick_walk(rows):
     return entries, walk, min(1 << 23, max(4096, 16 * len(rows)))
 
 
-def _spatial_order(t, with_bricks):
+def _spatial_order(t, with_bricks, ws_bytes=None):
     """rhip_spatial_order once more on a built table (a copy of its struct),
-    with or without brick storage: (struct, order, pos)."""
+    with or without brick storage, in a workspace of ws_bytes (default: the
+    size rhip_order_workspace_bytes gives): (struct, order, pos)."""
     import ctypes
     L = abi.lib()
     st = abi.RhipTable.from_buffer_copy(t.struct)
     n = t.n
     order = torch.empty(n, dtype=torch.int32, device=DEV)
     pos = torch.empty(n, dtype=torch.int32, device=DEV)
-    ows = torch.empty(abi._sizeq(L.rhip_order_workspace_bytes, n), dtype=torch.uint8, device=DEV)
+    if ws_bytes is None:
+        ws_bytes = abi._sizeq(L.rhip_order_workspace_bytes, n)
+    ows = torch.empty(ws_bytes, dtype=torch.uint8, device=DEV)
     bb = ctypes.c_size_t(0)
     if with_bricks:
         assert L.rhip_brick_bytes(ctypes.byref(st), ctypes.byref(bb)) == 0
@@ -197,7 +200,11 @@ def test_spatial_order_paths_agree_with_morton(D, n, span, stride, which):
     """The locality order with a brick grid (walked, or filled after a sort
     when the power-of-two padding makes the walk too long) and without one
     (sort only) is the Morton order of the rows; the brick path is the one
-    the set's shape selects."""
+    the set's shape selects. A walk marks the cells with a byte each where
+    the workspace holds them (always, at the size rhip_order_workspace_bytes
+    gives, for these sets) and with atomic ORs into the grid otherwise: a
+    workspace of only the walk's chunk totals and bases takes the atomic
+    marks, and both give the same order."""
     rng = np.random.default_rng(D * 1000 + span)
     c = random_coords(rng, n, D, span, batch=2)
     c[:, 1:] *= stride
@@ -209,8 +216,13 @@ def test_spatial_order_paths_agree_with_morton(D, n, span, stride, which):
     walks = walk <= max(8 * entries, 1 << 22)
     assert walks == (which == "walk")
     exp = _morton_order(rows)
-    for with_bricks in (True, False):
-        st, order, pos = _spatial_order(t, with_bricks)
+    runs = [(True, None), (False, None)]
+    if walks:  # chunks of 1024 walk indices: int32 totals, int64 bases, one int64, 256-aligned
+        chunks = -(-walk // 1024)
+        a256 = lambda b: -(-b // 256) * 256
+        runs.append((True, a256(4 * chunks) + a256(8 * chunks) + 8))
+    for with_bricks, ws in runs:
+        st, order, pos = _spatial_order(t, with_bricks, ws)
         np.testing.assert_array_equal(order, exp)
         np.testing.assert_array_equal(pos[order], np.arange(t.n))
         assert (st.bricks is not None) == with_bricks
