@@ -394,6 +394,22 @@ def stencil_partners(offsets) -> Optional[np.ndarray]:
     return out if st == 0 else None
 
 
+_PARTNERS = {}
+
+
+def _device_partners(ph: np.ndarray, dev) -> torch.Tensor:
+    """A stencil's partner permutation on a device, uploaded once per device
+    and permutation and shared (read-only) by the symmetric maps with it. The
+    first upload goes from pinned memory on the current stream, ahead of the
+    map count's synchronisation."""
+    key = (torch.device(dev).index, ph.tobytes())
+    t = _PARTNERS.get(key)
+    if t is None:
+        t = torch.from_numpy(ph).pin_memory().to(dev, non_blocking=True)
+        _PARTNERS[key] = t
+    return t
+
+
 def kernel_map(in_table: CoordTable, out_table: CoordTable, offsets) -> KernelMap:
     """Pairs (in, out) with coord(in) = coord(out) + offsets[k] (batch kept),
     the dense neighbour tables and the processing orders of both sides.
@@ -425,7 +441,7 @@ def kernel_map(in_table: CoordTable, out_table: CoordTable, offsets) -> KernelMa
     if out_table is in_table:
         ph = stencil_partners(off_host)
         if ph is not None:
-            partner = torch.from_numpy(ph).pin_memory().to(dev, non_blocking=True)
+            partner = _device_partners(ph, dev)
     # the one read-back: the count synchronises and fills kofs_host
     kofs_host = np.empty(K + 1, np.int64)
     _check(L.rhip_kmap_count(ctypes.byref(in_table.struct), _ptr(out_table.ucoords),
@@ -436,7 +452,7 @@ def kernel_map(in_table: CoordTable, out_table: CoordTable, offsets) -> KernelMa
                              ctypes.byref(flags), st), "rhip_kmap_count")
     symmetric = bool(flags.value & KMAP_SYMMETRIC)
     if symmetric and partner is None:
-        partner = torch.from_numpy(stencil_partners(off_host)).to(dev)
+        partner = _device_partners(stencil_partners(off_host), dev)
     if not symmetric:
         partner = None
         nbr_t = torch.empty((K, max(n_in, 1)), dtype=torch.int32, device=dev)

@@ -5,6 +5,8 @@
 
 #include <algorithm>
 #include <limits>
+#include <map>
+#include <mutex>
 #include <random>
 #include <sstream>
 
@@ -26,10 +28,61 @@ hipStream_t current_stream(const at::Device &device) {
   return c10::hip::getCurrentHIPStream(device.index()).stream();
 }
 
+// A stencil's partner permutation on a device (int32 [K]), uploaded once
+// per device and permutation and shared, read-only, by every symmetric map
+// with it: its input gradient's weight permutation. The first upload goes
+// from pinned memory on the current stream, ahead of the map count's
+// synchronisation, so it has landed before any later map or stream uses it.
+// The cache is never destroyed (its tensors must not outlive the runtime at
+// process exit).
+at::Tensor device_partners(const std::vector<int32_t> &partner, const at::Device &dev) {
+  static std::mutex mu;
+  static auto *cache = new std::map<std::pair<int, std::vector<int32_t>>, at::Tensor>();
+  std::lock_guard<std::mutex> lock(mu);
+  auto key = std::make_pair(static_cast<int>(dev.index()), partner);
+  auto it = cache->find(key);
+  if (it != cache->end())
+    return it->second;
+  const int64_t K = static_cast<int64_t>(partner.size());
+  auto pinned = torch::empty({K}, torch::TensorOptions().dtype(torch::kInt32).pinned_memory(true));
+  std::memcpy(pinned.data_ptr<int32_t>(), partner.data(), sizeof(int32_t) * K);
+  at::Tensor t = pinned.to(dev, /*non_blocking=*/true);
+  cache->emplace(std::move(key), t);
+  return t;
+}
+
 at::Tensor device_bytes(size_t bytes, const at::Device &device) {
   return torch::empty({static_cast<int64_t>(std::max<size_t>(bytes, 1))},
                       torch::TensorOptions().dtype(torch::kUInt8).device(device));
 }
+
+// Several buffers in one device allocation: add() reserves 256-aligned byte
+// ranges, alloc() makes the block, and take() returns each range as a
+// tensor view (int32 or uint8) that keeps the block alive. A map build's
+// long-lived buffers share one block, its scratch another: each allocator
+// call costs the host a few microseconds on the build's critical path.
+struct Block {
+  std::vector<std::pair<size_t, size_t>> parts; // (offset, bytes)
+  size_t used = 0;
+  at::Tensor base;
+  int add(size_t bytes) {
+    const size_t off = (used + 255) / 256 * 256;
+    parts.emplace_back(off, std::max<size_t>(bytes, 1));
+    used = off + std::max<size_t>(bytes, 1);
+    return static_cast<int>(parts.size()) - 1;
+  }
+  void alloc(const at::Device &dev) { base = device_bytes(used, dev); }
+  at::Tensor bytes(int i) const {
+    return base.narrow(0, static_cast<int64_t>(parts[i].first),
+                       static_cast<int64_t>(parts[i].second));
+  }
+  at::Tensor i32(int i, at::IntArrayRef shape) const {
+    return bytes(i).view(torch::kInt32).view(shape);
+  }
+  at::Tensor i64(int i, at::IntArrayRef shape) const {
+    return bytes(i).view(torch::kInt64).view(shape);
+  }
+};
 
 std::string stride_string(const stride_type &s) {
   std::ostringstream o;
@@ -366,23 +419,30 @@ CoordinateMapHIP CoordinateManager::build_map(const at::Tensor &coords,
   CoordinateMapHIP m;
   m.tensor_stride = tensor_stride;
   auto iopt = torch::TensorOptions().device(dev);
-  m.slots = device_bytes(rhip_table_bytes(n), dev);
-  size_t ws_bytes = 0;
+  // the map's slots, unique rows and locality order in one block, and one
+  // scratch block that the hash build and then the order use (stream-ordered:
+  // the order's kernels run after the build's); the order's buffers, sized
+  // by the row count (an upper bound of the unique rows), are allocated
+  // before the build, whose end waits for the device: after it only the
+  // brick grid is allocated before the order's launches
+  const int64_t rows = std::max<int64_t>(n, 1);
+  size_t ws_bytes = 0, ob = 0;
   check_rhip(rhip_hash_workspace_bytes(n, ncol, &ws_bytes), "rhip_hash_workspace_bytes");
-  auto ws = device_bytes(ws_bytes, dev);
-  m.storage = torch::empty({std::max<int64_t>(n, 1), ncol}, iopt.dtype(torch::kInt32));
-  auto map_t = torch::empty({std::max<int64_t>(n, 1)}, iopt.dtype(torch::kInt64));
+  check_rhip(rhip_order_workspace_bytes(n, &ob), "rhip_order_workspace_bytes");
+  Block own;
+  const int i_slots = own.add(rhip_table_bytes(n));
+  const int i_rows = own.add(sizeof(int32_t) * rows * ncol);
+  const int i_order = own.add(sizeof(int32_t) * rows);
+  own.alloc(dev);
+  m.slots = own.bytes(i_slots);
+  m.storage = own.i32(i_rows, {rows, ncol});
+  m.order = own.i32(i_order, {rows});
+  auto ws = device_bytes(std::max(ws_bytes, ob), dev);
+  auto &ows = ws;
+  auto map_t = torch::empty({rows}, iopt.dtype(torch::kInt64));
   at::Tensor inv_t;
   if (inverse)
-    inv_t = torch::empty({std::max<int64_t>(n, 1)}, iopt.dtype(torch::kInt64));
-  // the locality order's buffers, sized by the row count (an upper bound of
-  // the unique rows), are allocated before the build, whose end waits for
-  // the device: after it only the brick grid is allocated before the order's
-  // launches
-  m.order = torch::empty({std::max<int64_t>(n, 1)}, iopt.dtype(torch::kInt32));
-  size_t ob = 0;
-  check_rhip(rhip_order_workspace_bytes(n, &ob), "rhip_order_workspace_bytes");
-  auto ows = device_bytes(ob, dev);
+    inv_t = torch::empty({rows}, iopt.dtype(torch::kInt64));
   check_rhip(rhip_hash_build(coords.data_ptr<int32_t>(), n, ncol, m.slots.data_ptr(),
                              m.slots.numel(), ws.data_ptr(), ws.numel(),
                              m.storage.data_ptr<int32_t>(), map_t.data_ptr<int64_t>(),
@@ -395,7 +455,8 @@ CoordinateMapHIP CoordinateManager::build_map(const at::Tensor &coords,
     check_rhip(rhip_brick_bytes(&m.table, &bb), "rhip_brick_bytes");
     m.bricks = device_bytes(std::max<size_t>(bb, 1), dev);
     check_rhip(rhip_spatial_order(&m.table, m.order.data_ptr<int32_t>(), nullptr,
-                                  m.bricks.data_ptr(), bb, ows.data_ptr(), ows.numel(), st),
+                                  m.bricks.data_ptr(), bb, ows.data_ptr(),
+                                  static_cast<size_t>(ows.numel()), st),
                "rhip_spatial_order");
   }
   m.order = m.order.slice(0, 0, nu);
@@ -526,18 +587,22 @@ HipKernelMap CoordinateManager::generate(const CoordinateMapHIP &in_map,
   size_t ws_bytes = 0;
   check_rhip(rhip_kmap_workspace_bytes(n_in, n_out, K, &ws_bytes), "rhip_kmap_workspace_bytes");
   auto ws = device_bytes(ws_bytes, dev);
-  auto nbr = torch::empty({K, std::max<int64_t>(n_out, 1)}, iopt);
-  auto out_order = torch::empty({std::max<int64_t>(n_out, 1)}, iopt);
-  m.offsets = torch::empty({K + 1}, iopt.dtype(torch::kInt64));
+  // the map's table, processing order and CSR offsets in one block
+  const int64_t rows_out = std::max<int64_t>(n_out, 1);
+  Block own;
+  const int i_nbr = own.add(sizeof(int32_t) * K * rows_out);
+  const int i_order = own.add(sizeof(int32_t) * rows_out);
+  const int i_ofs = own.add(sizeof(int64_t) * (K + 1));
+  own.alloc(dev);
+  auto nbr = own.i32(i_nbr, {K, rows_out});
+  auto out_order = own.i32(i_order, {rows_out});
+  m.offsets = own.i64(i_ofs, {K + 1});
   int32_t flags = 0;
   // A map of a set onto itself whose stencil is closed under negation is
-  // symmetric (the count confirms it): its partners go to the device from
-  // pinned memory ahead of the count, whose synchronisation covers the copy.
-  auto upload_partners = [&]() {
-    auto pinned = torch::empty({K}, torch::TensorOptions().dtype(torch::kInt32).pinned_memory(true));
-    std::memcpy(pinned.data_ptr<int32_t>(), m.partner_host.data(), sizeof(int32_t) * K);
-    m.partner = pinned.to(dev, /*non_blocking=*/true);
-  };
+  // symmetric (the count confirms it): its partners (shared per device and
+  // stencil) are on the device ahead of the count, whose synchronisation
+  // covers a first upload.
+  auto upload_partners = [&]() { m.partner = device_partners(m.partner_host, dev); };
   if (&in_map == &out_map) {
     m.partner_host.resize(K);
     if (rhip_stencil_partners(offsets.data_ptr<int32_t>(), K,
