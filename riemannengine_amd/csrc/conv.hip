@@ -48,6 +48,7 @@ typedef uint32_t v4u __attribute__((ext_vector_type(4)));
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / kWave;
 constexpr int kMaskWords = 4; // the MFMA paths handle K <= 128 offsets
+constexpr int kWideRG = 2;    // row groups per wave of conv_os_lds_kernel's bf16 128-column tiles
 
 template <typename T> struct Mfma;
 
@@ -2384,11 +2385,14 @@ static bool os_fast(const T *x, int cred, const T *wt, int credw, int ncols, int
 // for 9k rows at 256 channels), so the (offset, channel chunk) stages are
 // shared among up to 8 workgroups per tile, aiming at ~640 workgroups
 // (measured on the config-5 stages), each keeping at least 4 stages on
-// average. 1 = no split.
+// average. 1 = no split. The tiles counted are the fast kernel's (bf16
+// 128-column tiles hold kWideRG row groups per wave).
 template <typename T> static int os_splits(int64_t n_rows, int cred, int ncols, int K) {
   if (n_rows <= 0 || ncols % 16 != 0)
     return 1;
-  const int64_t blocks = ceil_div(n_rows, kWaves * 16) * (ncols / os_nt<T>(ncols));
+  const int nt = os_nt<T>(ncols);
+  const int rows = kWaves * 16 * (!kIsF32<T> && nt >= 128 ? kWideRG : 1);
+  const int64_t blocks = ceil_div(n_rows, rows) * (ncols / nt);
   const int64_t stages = static_cast<int64_t>(K) * std::max(1, cred / 64);
   const int64_t want = (640 + blocks / 2) / blocks; // nearest
   return static_cast<int>(
@@ -2460,7 +2464,12 @@ static bool launch_os_lds(const T *x, int64_t n_x, int cred, const T *wt, const 
 // Launch shape of conv_os_lds_kernel, measured on MI355X: bf16 at 64 columns
 // and 64-channel chunks takes two row groups per wave and one stage per
 // barrier (6 waves per SIMD; config 2 forward 76 us against 78 with two
-// stages per barrier and 80 with three row groups); fp32 at 32 columns with
+// stages per barrier and 80 with three row groups); bf16 128-column tiles
+// (layers of 128 or 256 channels) take two row groups and one stage per
+// barrier too, which halves the weight slices each row re-stages (config 5
+// stage 4, 9,342 rows at C256: forward 118.8 -> 102.8 us, dX 106.5 -> 91.9
+// us with the splits os_splits then picks; stage 3, 43,444 rows at C128:
+// 81.0 -> 78.9 and 75.1 -> 74.5 us); fp32 at 32 columns with
 // 24 index slots (stencils of 33 to 96 offsets) holds the indices in
 // registers and takes two stages per barrier at 5 waves per SIMD (config 4
 // forward 305 -> 256 us; the LDS indices with two stages: 309 us; register
@@ -2481,9 +2490,10 @@ static bool os_lds_shape(const T *x, int64_t n_x, int cred, const T *wt, const i
                                                    n_rows, K, order, y, splits, partial, s);
   } else {
     constexpr int W = NT >= 128 ? 4 : (CSUB == 1 && NT >= 64 ? 6 : 8);
-    constexpr int G = NT >= 128 ? 2 : (CSUB == 1 ? 4 : 1);
-    return launch_os_lds<T, NT, 1, CSUB, G, W, KQ>(x, n_x, cred, wt, wperm, ncols, bias, nbr,
-                                                   n_rows, K, order, y, splits, partial, s);
+    constexpr int G = NT >= 128 ? 1 : (CSUB == 1 ? 4 : 1);
+    constexpr int RG = NT >= 128 ? kWideRG : 1;
+    return launch_os_lds<T, NT, RG, CSUB, G, W, KQ>(x, n_x, cred, wt, wperm, ncols, bias, nbr,
+                                                    n_rows, K, order, y, splits, partial, s);
   }
 }
 
