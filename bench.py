@@ -21,8 +21,9 @@ Printed as ONE JSON line:
                breakdown and HBM roofline with measured traffic
   roofline     the dominant kernel's algorithmic FLOP/s (fp32, MFMA-bound) or
                bytes/s (bf16, HBM-bound), from HIP events recorded on the
-               stream the kernels run on around the dW pass of every timed
-               step, against MI355X's published peak
+               stream the kernels run on around the dW pass of every tenth
+               timed step (an event record idles the device ~6 us), against
+               MI355X's published peak
   breakdown_ms per-pass event times from untimed steps after the timed ones
                (events between every pass would cost the timed steps a few
                microseconds each)
@@ -895,19 +896,22 @@ def conv_step_record(args, dtype, km, n_in, n_out, P, K, cin, cout):
         step()
     torch.cuda.synchronize()
 
-    # the timed steps record events around the dW pass only (the dominant
-    # pass of this workload in both dtypes): each event record costs the step
-    # a few microseconds of command-processor time
-    events = [[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(args.steps)]
+    # every tenth timed step (at least one) records events around the dW
+    # pass, the dominant pass of this workload in both dtypes: an event record
+    # leaves the device idle for ~6 us (kernel trace: a gap at each one), so
+    # events in every step would add ~12 us to each
+    every = 10
+    sampled = set(range(0, args.steps, every))
+    events = {i: [torch.cuda.Event(enable_timing=True) for _ in range(2)] for i in sampled}
     torch.cuda.synchronize()
     with _no_gc():
         t0 = time.perf_counter()
         for i in range(args.steps):
-            step(events[i])
+            step(events.get(i))
         torch.cuda.synchronize()
         total_s = time.perf_counter() - t0
     ms_per_step = total_s * 1e3 / args.steps
-    dw_timed = statistics.mean(e[0].elapsed_time(e[1]) for e in events)
+    dw_timed = statistics.mean(e[0].elapsed_time(e[1]) for e in events.values())
 
     # per-pass breakdown from untimed steps after the timed region
     names = ["forward", "backward_input", "backward_weight"]
@@ -940,7 +944,8 @@ def conv_step_record(args, dtype, km, n_in, n_out, P, K, cin, cout):
                           if dtype == "f32" else
                           "conv_dw_shx_bf16_kernel + conv_dw_rows_reduce_kernel (dW pass)")}[dom]
     roof["kernel_ms"] = round(kernel_ms, 4)
-    roof["kernel_ms_source"] = ("events around dW in the timed steps" if dom == "backward_weight"
+    roof["kernel_ms_source"] = ("events around dW in every %dth timed step" % every
+                                if dom == "backward_weight"
                                 else "events in %d untimed steps after the timed ones" % nb)
     roof["algorithmic"] = {"flop": F, "bytes": B}
 
