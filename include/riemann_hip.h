@@ -182,8 +182,9 @@ int rhip_kmap_workspace_bytes(int64_t n_in, int64_t n_out, int32_t K,
  * it to rhip_kmap_fill. */
 #define RHIP_KMAP_SYMMETRIC 1
 /* Reported by rhip_kmap_count when its probes read each output row's
- * neighbourhood bricks once (a symmetric 3^3 map in 3-D whose in_table has a
- * brick grid); the map is the same either way. rhip_kmap_fill ignores it. */
+ * neighbourhood bricks once (a symmetric 3^3 map in 3-D or 3^4 map in 4-D
+ * whose in_table has a brick grid); the map is the same either way.
+ * rhip_kmap_fill ignores it. */
 #define RHIP_KMAP_BRICK_NBHD 2
 
 /*

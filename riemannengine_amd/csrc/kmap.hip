@@ -286,12 +286,100 @@ __device__ __forceinline__ void probe27_bricks(const TableView &t, const int32_t
   }
 }
 
+// The 3^4 neighbourhood of a row of a symmetric 4-D map through the brick
+// grid: D = 4, bricks of 2 x 2 x 2 x 2 cells (brick level 1), and the stencil
+// in cell units the canonical 3^4 region in its order, offset k =
+// (k % 3 - 1, k / 3 % 3 - 1, k / 9 % 3 - 1, k / 27 - 1) along columns 1..4.
+// A cell sits on a face of its brick along every column (cell coordinate 0:
+// the low face, 1: the high one), so its 81 neighbours lie in 16 bricks: the
+// row's own and, along each column, the one below (cell 0) or above (cell
+// 1). The row loads those 16 once, corner cc holding the brick shifted along
+// column i when bit i - 1 of cc is set (probe8 loads one brick per offset:
+// 81 loads), and each offset reads its neighbour's occupancy bit and rank
+// from the brick it reaches, selected by a 16-way tree. f(k, v) receives
+// each offset's result: the neighbour's row (through the locality order) or
+// -1 with kRows, else v >= 0 marks a neighbour.
+template <bool kRows, typename F>
+__device__ __forceinline__ void probe81_bricks(const TableView &t, const int32_t *c, uint32_t d0,
+                                               bool row_ok, F &&f) {
+  uint32_t q[5], b[5];
+#pragma unroll
+  for (int i = 1; i <= 4; ++i) {
+    const uint32_t w = (static_cast<uint32_t>(c[i]) - static_cast<uint32_t>(t.lo[i])) >> t.tz[i];
+    q[i] = w & 1u;
+    b[i] = w >> 1;
+  }
+  uint32_t mk[16]; // 16 cells: the low half of the brick's mask
+  int32_t base[16];
+#pragma unroll
+  for (int cc = 0; cc < 16; ++cc) {
+    bool need = row_ok;
+    int64_t g = d0;
+#pragma unroll
+    for (int i = 1; i <= 4; ++i) {
+      const bool sh = (cc >> (i - 1)) & 1;
+      // the brick below a cell in brick 0 wraps to 2^32 - 1 and fails the
+      // extent check
+      const uint32_t bc = b[i] + (sh ? (q[i] == 0u ? 0xffffffffu : 1u) : 0u);
+      need = need && bc < static_cast<uint32_t>(t.dims[i]);
+      g = g * t.dims[i] + bc;
+    }
+    mk[cc] = 0;
+    base[cc] = 0;
+    if (need) {
+      const Brick br = t.bricks[g];
+      mk[cc] = static_cast<uint32_t>(br.mask);
+      base[cc] = br.base;
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < 81; ++k) {
+    const int dl[5] = {0, k % 3 - 1, (k / 3) % 3 - 1, (k / 9) % 3 - 1, k / 27 - 1};
+    bool x[5];
+    uint32_t cell = 0;
+#pragma unroll
+    for (int i = 1; i <= 4; ++i) {
+      // the offset leaves the brick along column i: down from cell 0, up
+      // from cell 1
+      x[i] = dl[i] < 0 ? q[i] == 0u : (dl[i] > 0 ? q[i] == 1u : false);
+      cell |= ((q[i] + static_cast<uint32_t>(dl[i])) & 1u) << (4 - i);
+    }
+    // mk[x1 + 2 x2 + 4 x3 + 8 x4] as a select tree over the columns
+    uint32_t m8[8];
+    int32_t b8[8];
+#pragma unroll
+    for (int a = 0; a < 8; ++a) {
+      m8[a] = x[4] ? mk[a + 8] : mk[a];
+      b8[a] = x[4] ? base[a + 8] : base[a];
+    }
+    uint32_t m4[4];
+    int32_t b4[4];
+#pragma unroll
+    for (int a = 0; a < 4; ++a) {
+      m4[a] = x[3] ? m8[a + 4] : m8[a];
+      b4[a] = x[3] ? b8[a + 4] : b8[a];
+    }
+    const uint32_t m2_0 = x[2] ? m4[2] : m4[0], m2_1 = x[2] ? m4[3] : m4[1];
+    const int32_t b2_0 = x[2] ? b4[2] : b4[0], b2_1 = x[2] ? b4[3] : b4[1];
+    const uint32_t m = x[1] ? m2_1 : m2_0;
+    const int32_t bs = x[1] ? b2_1 : b2_0;
+    const bool hit = (m >> cell) & 1u;
+    if constexpr (kRows) {
+      const int32_t jj = bs + __popc(m & ((1u << cell) - 1u));
+      f(k, hit ? t.order[jj] : -1);
+    } else {
+      f(k, hit ? 0 : -1);
+    }
+  }
+}
+
 // Mask pass: one lane per output row j in spatial order (row spatial[j]):
 // keys[j] = the sort key of the row's neighbour mask, vals[j] = its output
 // row spatial[j].
 // KC > 0: K == KC at compile time (the probe rounds unroll and the stencil
 // loads hoist out of them). NBHD: the symmetric 3^3 map through
-// probe27_bricks (KC == 27, D == 3).
+// probe27_bricks (KC == 27, D == 3) or 3^4 map through probe81_bricks
+// (KC == 81, D == 4).
 template <int D, int KC = 0, bool NBHD = false>
 __global__ __launch_bounds__(kMapBlock) void kmap_mask_kernel(
     TableView t, const int32_t *__restrict__ out_coords, const int32_t *__restrict__ spatial,
@@ -311,13 +399,25 @@ __global__ __launch_bounds__(kMapBlock) void kmap_mask_kernel(
   const bool row_ok = d0 <= t.span[0];
   uint64_t m0 = 0, m1 = 0;
   if constexpr (NBHD) {
-    static_assert(D == 3 && KC == 27, "the neighbourhood probe is the 3^3 stencil in 3-D");
-    int32_t r[27];
-    probe27_bricks<false>(t, c, d0, row_ok, r);
+    static_assert((D == 3 && KC == 27) || (D == 4 && KC == 81),
+                  "the neighbourhood probes are the 3^3 stencil in 3-D and 3^4 in 4-D");
+    if constexpr (D == 3) {
+      int32_t r[27];
+      probe27_bricks<false>(t, c, d0, row_ok, r);
 #pragma unroll
-    for (int k = 0; k < 27; ++k)
-      if (r[k] >= 0)
-        m0 |= 1ull << k;
+      for (int k = 0; k < 27; ++k)
+        if (r[k] >= 0)
+          m0 |= 1ull << k;
+    } else {
+      probe81_bricks<false>(t, c, d0, row_ok, [&](int k, int32_t v) {
+        if (v >= 0) {
+          if (k < 64)
+            m0 |= 1ull << k;
+          else
+            m1 |= 1ull << (k - 64);
+        }
+      });
+    }
     keys[j] = mask_key(m0, m1, K);
     vals[j] = static_cast<int32_t>(o);
     return;
@@ -384,16 +484,23 @@ __global__ __launch_bounds__(kMapBlock) void kmap_query_kernel(
   const uint32_t d0 = static_cast<uint32_t>(c[0]) - static_cast<uint32_t>(t.lo[0]);
   const bool row_ok = in && d0 <= t.span[0];
   if constexpr (NBHD) {
-    static_assert(D == 3 && KC == 27, "the neighbourhood probe is the 3^3 stencil in 3-D");
-    int32_t r[27];
-    probe27_bricks<true>(t, c, d0, row_ok, r);
-#pragma unroll
-    for (int k = 0; k < 27; ++k) {
+    static_assert((D == 3 && KC == 27) || (D == 4 && KC == 81),
+                  "the neighbourhood probes are the 3^3 stencil in 3-D and 3^4 in 4-D");
+    auto put = [&](int k, int32_t v) {
       if (in)
-        nbr[k * n_out + p] = r[k];
-      const uint64_t hits = __ballot(r[k] >= 0);
+        nbr[k * n_out + p] = v;
+      const uint64_t hits = __ballot(v >= 0);
       if (lane_id() == 0)
         wave_counts[k * nw + w] = __popcll(hits);
+    };
+    if constexpr (D == 3) {
+      int32_t r[27];
+      probe27_bricks<true>(t, c, d0, row_ok, r);
+#pragma unroll
+      for (int k = 0; k < 27; ++k)
+        put(k, r[k]);
+    } else {
+      probe81_bricks<true>(t, c, d0, row_ok, put);
     }
     return;
   }
@@ -732,6 +839,25 @@ static bool nbhd27(const rhip_table *t, int32_t K, const int32_t *offsets_host) 
   return true;
 }
 
+// Whether a symmetric 4-D map takes probe81_bricks: a brick grid of
+// 2 x 2 x 2 x 2 cells and the stencil, in cell units of the table, the
+// canonical 3^4 region in its order.
+static bool nbhd81(const rhip_table *t, int32_t K, const int32_t *offsets_host) {
+  if (K != 81 || t->ncol != 5 || t->bricks == nullptr || t->order == nullptr ||
+      t->brick_levels != 1)
+    return false;
+  for (int k = 0; k < 81; ++k) {
+    const int dl[4] = {k % 3 - 1, (k / 3) % 3 - 1, (k / 9) % 3 - 1, k / 27 - 1};
+    for (int i = 0; i < 4; ++i) {
+      const int tz = t->tz[i + 1];
+      if (tz < 0 || tz > 30 ||
+          static_cast<int64_t>(offsets_host[k * 4 + i]) != int64_t(dl[i]) * (int64_t(1) << tz))
+        return false;
+    }
+  }
+  return true;
+}
+
 } // namespace rhip
 
 using namespace rhip;
@@ -794,8 +920,11 @@ extern "C" int rhip_kmap_count(const rhip_table *in_table, const int32_t *out_co
       const int n_sten = K * D, n_part = sym ? K : 0;
       const bool nbhd = sym && nbhd27(in_table, K, offsets_host) &&
                         n_sten + n_part <= kSmallUpload;
+      // the symmetric 3^4 map reads its 16 neighbourhood bricks once per row
+      // (its stencil and partners are too many for the arguments: uploaded)
+      const bool nbhd4 = sym && nbhd81(in_table, K, offsets_host);
       SmallUpload small{};
-      if (nbhd && flags)
+      if ((nbhd || nbhd4) && flags)
         *flags |= RHIP_KMAP_BRICK_NBHD;
       if (nbhd) {
         std::memcpy(small.v, offsets_host, sizeof(int32_t) * n_sten);
@@ -822,6 +951,25 @@ extern "C" int rhip_kmap_count(const rhip_table *in_table, const int32_t *out_co
                                stream, tv, out_coords, out_spatial_order, jpos, n_out, w.offsets,
                                K, nw, nbr, out_order, w.wave_counts, small, w.offsets,
                                n_sten, w.partner, n_part, w.ticket);
+            RHIP_LAUNCH_CHECK();
+            return;
+          }
+        }
+        if constexpr (DD == 4) {
+          if (nbhd4) {
+            if (masks) {
+              hipLaunchKernelGGL((kmap_mask_kernel<4, 81, true>), dim3(nb), dim3(kMapBlock), 0,
+                                 stream, tv, out_coords, out_spatial_order, n_out, w.offsets, K,
+                                 w.keys_a, w.vals_a);
+              RHIP_LAUNCH_CHECK();
+              sort_pairs_u32(w.sort_tmp, w.sort_bytes, w.keys_a, w.keys_b, w.vals_a, w.vals_b,
+                             n_out, mask_key_bits(K), stream);
+              jpos = w.vals_b;
+            }
+            hipLaunchKernelGGL((kmap_query_kernel<4, 81, true>), dim3(nb), dim3(kMapBlock), 0,
+                               stream, tv, out_coords, out_spatial_order, jpos, n_out, w.offsets,
+                               K, nw, nbr, out_order, w.wave_counts, small, w.offsets, 0,
+                               w.partner, 0, w.ticket);
             RHIP_LAUNCH_CHECK();
             return;
           }

@@ -115,9 +115,10 @@ def test_same_set_map_matches_oracle(D, ks, dil, ts, region):
     _check_tables(km, tin, tout)
     # odd cubes and crosses are closed under negation: half the offsets are probed
     assert km.symmetric == (ks % 2 == 1)
-    # the 3^3 cube in cell units (tensor stride 1 or 2, no dilation) reads each
-    # row's neighbourhood bricks once; the general path below must agree
-    nbhd = D == 3 and ks == 3 and dil == 1 and region == "cube"
+    # the 3^3 cube in 3-D and the 3^4 cube in 4-D, in cell units (tensor
+    # stride 1 or 2, no dilation), read each row's neighbourhood bricks once;
+    # the general path below must agree
+    nbhd = D in (3, 4) and ks == 3 and dil == 1 and region == "cube"
     assert bool(km.flags & abi.KMAP_BRICK_NBHD) == nbhd
     # the same coordinates in a second table take the general path; it must
     # agree with the mirrored one row for row
@@ -220,8 +221,9 @@ def test_config_maps_match_oracle(cfg):
     np.testing.assert_array_equal(cnt, cnt[::-1])
     if cfg == "sphere":
         assert len(c) == 51554 and km.n_pairs == 544970
-    # the 3-D configurations' maps take the neighbourhood-brick probes
-    assert bool(km.flags & abi.KMAP_BRICK_NBHD) == (D == 3)
+    # every configuration's map (3^3 in 3-D, 3^4 in 4-D) takes the
+    # neighbourhood-brick probes
+    assert km.flags & abi.KMAP_BRICK_NBHD
 
 
 def test_lidar_down_up_maps():
