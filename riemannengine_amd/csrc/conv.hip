@@ -1253,15 +1253,17 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(WAVES)
     slot[i] = red[i];
 }
 
-// dw[k][ci0 + i / TN][co0 + i % TN] = sum over the chunks c of offset k of
-// partial[k][tile][c][i]: a deterministic second stage. A workgroup owns 256
+// dw[k][ci0 + i / TN][co0 + i % TN] (colmajor: dw[k][ci0 + i % TM][co0 + i /
+// TM]) = sum over the chunks c of offset k of partial[k][tile][c][i]: a
+// deterministic second stage. The chunks are those holding pairs of offset k
+// (ppb pairs each), or all of them when ppb is 0. A workgroup owns 256
 // consecutive elements (64 lanes x 4 floats); its 4 waves sum the chunks
 // c = wave (mod 4) with 16-byte loads, then the 4 phase sums are added in a
 // fixed order.
 template <typename OutT>
 __global__ __launch_bounds__(kThreads) void conv_dw_reduce_kernel(
     const float *__restrict__ partial, const int64_t *__restrict__ kofs, int64_t ppb,
-    int chunks, int tiles, int tiles_n, int TM, int TN, int cin, int cout,
+    int chunks, int tiles, int tiles_n, int TM, int TN, int cin, int cout, int colmajor,
     OutT *__restrict__ dw) {
   __shared__ v4f phase_sum[kWaves][kWave];
   const int k = blockIdx.y, t = blockIdx.z;
@@ -1269,7 +1271,7 @@ __global__ __launch_bounds__(kThreads) void conv_dw_reduce_kernel(
   const int n4 = TM * TN / 4; // a multiple of 64
   const int i4 = blockIdx.x * kWave + lane;
   const int64_t pk = kofs[k + 1] - kofs[k];
-  const int nck = static_cast<int>(min<int64_t>(chunks, (pk + ppb - 1) / ppb));
+  const int nck = ppb > 0 ? static_cast<int>(min<int64_t>(chunks, (pk + ppb - 1) / ppb)) : chunks;
   const v4f *src = reinterpret_cast<const v4f *>(partial) +
                    (static_cast<int64_t>(k) * tiles + t) * chunks * n4 + i4;
   v4f sum = v4f{0.f, 0.f, 0.f, 0.f};
@@ -1287,8 +1289,198 @@ __global__ __launch_bounds__(kThreads) void conv_dw_reduce_kernel(
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
     const int i = 4 * i4 + e;
-    const int ci = (t / tiles_n) * TM + i / TN, co = (t % tiles_n) * TN + i % TN;
+    const int ci = (t / tiles_n) * TM + (colmajor ? i % TM : i / TN);
+    const int co = (t % tiles_n) * TN + (colmajor ? i / TM : i % TN);
     dw[(static_cast<int64_t>(k) * cin + ci) * cout + co] = from_f32<OutT>(v[e]);
+  }
+}
+
+// Pair-list dW for bf16 layers whose channel counts are multiples of 64, in
+// tiles of TM x TN channels (64 or 128 each). Workgroup (r, k, tile) takes
+// the r-th of `ranges` equal parts of offset k's pairs (split on the device
+// from the CSR offsets, so the grid has no idle workgroups) and stores its
+// TM x TN tile, column-major, in partial slot [k][tile][r]; the second stage
+// (conv_dw_reduce_kernel) adds the slots of each offset in order. Inside a
+// workgroup the waves share no rows: the part's pair indices go to LDS in
+// batches of up to kDwPairsMaxPpb (two barriers per batch), and wave w takes
+// the w-th quarter of a batch in steps of 32 pairs on its own. It loads a
+// step's X and dY rows (lane l: row l / P of a load instruction's 64 / P
+// rows, 16-byte piece l % P of the tile's P pieces per row), D steps ahead in
+// registers, stores them to its own LDS rows and reads them back transposed
+// (ds_read_b64_tr_b16, as in conv_dw_kernel) as the operands of its whole
+// TM x TN tile. DS instructions of one wave execute in order, so a step's
+// stores follow the previous step's reads without a wait. The four waves'
+// tiles are added in LDS in wave order.
+constexpr int kDwPairsMaxPpb = 2048; // pairs per index batch (the LDS index rows)
+template <int TM, int TN>
+constexpr int dw_pairs_lds_bytes() {
+  constexpr int stage = kWaves * 32 * ((TM + 8) + (TN + 8)) * 2 + 2 * kDwPairsMaxPpb * 4;
+  constexpr int red = kWaves * (TM + 4) * TN * 4 / (TM * TN > 4096 ? 2 : 1);
+  return stage > red ? stage : red;
+}
+template <int TM, int TN, int D, int WAVES>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(WAVES))) void
+conv_dw_pairs_bf16_kernel(const __bf16 *__restrict__ x, int64_t n_in, int cin,
+                          const __bf16 *__restrict__ gy, int64_t n_out, int cout,
+                          const int64_t *__restrict__ kofs, const int32_t *__restrict__ in_rows,
+                          const int32_t *__restrict__ out_rows, int ranges,
+                          float *__restrict__ partial) {
+  static_assert((TM == 64 || TM == 128) && (TN == 64 || TN == 128), "64- or 128-channel tiles");
+  constexpr int PX = TM / 8, PY = TN / 8;   // 16-byte pieces per row
+  constexpr int NX = TM / 16, NY = TN / 16; // load instructions per 32-pair step
+  constexpr int LDX = TM + 8, LDY = TN + 8; // LDS row strides (elements)
+  constexpr int MB = TM / 16, NB = TN / 16;
+  constexpr int RR = TM * TN > 4096 ? 2 : 1; // rounds of the final sum
+  constexpr int NBR = NB / RR;               // column blocks per round
+  constexpr int LDR = TM + 4;                // column stride of the sum (floats)
+  __shared__ __align__(16) char smem[dw_pairs_lds_bytes<TM, TN>()];
+
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const int i16 = lane & 15;
+  const int g = lane >> 4;
+  const int k = blockIdx.y;
+  const int tiles_n = cout / TN;
+  const int ci0 = (blockIdx.z / tiles_n) * TM;
+  const int co0 = (blockIdx.z % tiles_n) * TN;
+  const int64_t kb = kofs[k], pk = kofs[k + 1] - kb;
+  const int64_t b0 = kb + pk * blockIdx.x / ranges;
+  const int64_t len = kb + pk * (blockIdx.x + 1) / ranges - b0; // may be 0: the slot is zeros
+
+  __bf16 *sX = reinterpret_cast<__bf16 *>(smem) + wv * 32 * (LDX + LDY);
+  __bf16 *sY = sX + 32 * LDX;
+  int32_t *sIn = reinterpret_cast<int32_t *>(smem + kWaves * 32 * (LDX + LDY) * 2);
+  int32_t *sOut = sIn + kDwPairsMaxPpb;
+  int wb = 0, wlen = 0; // this wave's pairs of the current batch (LDS rows)
+  const __amdgpu_buffer_rsrc_t rx = buf_rsrc(x, n_in * cin * 2);
+  const __amdgpu_buffer_rsrc_t ry = buf_rsrc(gy, n_out * cout * 2);
+  const uint32_t xcol = static_cast<uint32_t>((ci0 + (lane % PX) * 8) * 2);
+  const uint32_t ycol = static_cast<uint32_t>((co0 + (lane % PY) * 8) * 2);
+
+  // step s's rows (all out of range, so no memory access, past the wave's pairs)
+  auto load_step = [&](int s, v4u (&r)[NX + NY]) {
+#pragma unroll
+    for (int j = 0; j < NX; ++j) {
+      const int li = 32 * s + j * (64 / PX) + lane / PX;
+      const bool ok = li < wlen;
+      const int32_t id = sIn[ok ? wb + li : 0];
+      r[j] = __builtin_amdgcn_raw_buffer_load_b128(
+          rx, pick_off(static_cast<uint32_t>(id) * static_cast<uint32_t>(cin * 2) + xcol,
+                       ok ? -1 : 0),
+          0, 0);
+    }
+#pragma unroll
+    for (int j = 0; j < NY; ++j) {
+      const int li = 32 * s + j * (64 / PY) + lane / PY;
+      const bool ok = li < wlen;
+      const int32_t id = sOut[ok ? wb + li : 0];
+      r[NX + j] = __builtin_amdgcn_raw_buffer_load_b128(
+          ry, pick_off(static_cast<uint32_t>(id) * static_cast<uint32_t>(cout * 2) + ycol,
+                       ok ? -1 : 0),
+          0, 0);
+    }
+  };
+  auto store_step = [&](const v4u (&r)[NX + NY]) {
+#pragma unroll
+    for (int j = 0; j < NX; ++j)
+      *reinterpret_cast<v4u *>(sX + (j * (64 / PX) + lane / PX) * LDX + (lane % PX) * 8) = r[j];
+#pragma unroll
+    for (int j = 0; j < NY; ++j)
+      *reinterpret_cast<v4u *>(sY + (j * (64 / PY) + lane / PY) * LDY + (lane % PY) * 8) =
+          r[NX + j];
+  };
+  const int prow = 8 * g + i16 / 4, pcol = 4 * (i16 % 4);
+  auto operand = [&](const __bf16 *base, int ld, int col) {
+    const v4s lo = ds_read_tr16(base + prow * ld + col + pcol);
+    const v4s hi = ds_read_tr16(base + (prow + 4) * ld + col + pcol);
+    return __builtin_bit_cast(v8bf, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+  };
+
+  v4f acc[MB][NB];
+#pragma unroll
+  for (int m = 0; m < MB; ++m)
+#pragma unroll
+    for (int n = 0; n < NB; ++n)
+      acc[m][n] = v4f{0.f, 0.f, 0.f, 0.f};
+  v4u R[D][NX + NY];
+  for (int64_t bs = 0; bs < len; bs += kDwPairsMaxPpb) {
+    const int blen = static_cast<int>(min<int64_t>(kDwPairsMaxPpb, len - bs));
+    if (bs > 0)
+      __syncthreads(); // every wave is done with the previous batch's indices
+    { // every load issued before the first store: one round trip
+      constexpr int kPer = kDwPairsMaxPpb / kThreads;
+      int32_t vi[kPer], vo[kPer];
+#pragma unroll
+      for (int j = 0; j < kPer; ++j) {
+        const int i = threadIdx.x + j * kThreads;
+        const int64_t p = b0 + bs + (i < blen ? i : 0);
+        vi[j] = in_rows[p];
+        vo[j] = out_rows[p];
+      }
+#pragma unroll
+      for (int j = 0; j < kPer; ++j) {
+        const int i = threadIdx.x + j * kThreads;
+        if (i < blen) {
+          sIn[i] = vi[j];
+          sOut[i] = vo[j];
+        }
+      }
+    }
+    __syncthreads();
+    const int q = (blen + 4 * 32 - 1) / (4 * 32) * 32; // pairs per wave, a multiple of 32
+    wb = wv * q;
+    wlen = max(0, min(blen - wb, q));
+    const int nst = (wlen + 31) / 32;
+#pragma unroll
+    for (int d = 0; d < D; ++d)
+      load_step(d, R[d]);
+    for (int s0 = 0; s0 < nst; s0 += D) {
+#pragma unroll
+      for (int d = 0; d < D; ++d) {
+        if (s0 + d < nst) { // uniform
+          store_step(R[d]);
+          load_step(s0 + d + D, R[d]);
+          v8bf b[NB];
+#pragma unroll
+          for (int n = 0; n < NB; ++n)
+            b[n] = operand(sY, LDY, 16 * n);
+#pragma unroll
+          for (int m = 0; m < MB; ++m) {
+            const v8bf a = operand(sX, LDX, 16 * m);
+#pragma unroll
+            for (int n = 0; n < NB; ++n)
+              acc[m][n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b[n], acc[m][n], 0, 0, 0);
+          }
+        }
+      }
+    }
+  }
+
+  // the four tiles, added in wave order, into the slot [TN][TM] (column-
+  // major); RR rounds of NBR column blocks. Lane (i16, g) holds rows
+  // 4g..4g+3 of column i16 of block (m, n): one 16-byte LDS store each
+  // (columns LDR floats apart: the 16 lanes of a row group hit distinct banks)
+  float *red = reinterpret_cast<float *>(smem);
+  float *slot = partial + ((static_cast<int64_t>(k) * gridDim.z + blockIdx.z) * ranges +
+                           blockIdx.x) * (TM * TN);
+#pragma unroll
+  for (int rr = 0; rr < RR; ++rr) {
+    __syncthreads(); // the staging rows (or the previous round) are free
+#pragma unroll
+    for (int m = 0; m < MB; ++m)
+#pragma unroll
+      for (int n = 0; n < NBR; ++n)
+        *reinterpret_cast<v4f *>(red + (wv * 16 * NBR + 16 * n + i16) * LDR + 16 * m + 4 * g) =
+            acc[m][rr * NBR + n];
+    __syncthreads();
+    for (int i = threadIdx.x; i < TM * 16 * NBR / 4; i += kThreads) {
+      const int c = i / (TM / 4), r4 = 4 * (i % (TM / 4)); // column of the round, first row
+      v4f v = *reinterpret_cast<const v4f *>(red + c * LDR + r4);
+#pragma unroll
+      for (int w = 1; w < kWaves; ++w)
+        v += *reinterpret_cast<const v4f *>(red + (w * 16 * NBR + c) * LDR + r4);
+      *reinterpret_cast<v4f *>(slot + (rr * 16 * NBR + c) * TM + r4) = v;
+    }
   }
 }
 
@@ -2735,8 +2927,13 @@ struct DwPlan {
   int va = 1, vb = 1, tiles = 1;
   int64_t ppb = 1, chunks = 1;
   bool fast = false;
+  // bf16 tiles of tm x tn channels on conv_dw_pairs_bf16_kernel (else
+  // conv_dw_kernel's 16va x 16vb tiles)
+  bool pw = false;
+  int tm = 0, tn = 0;
   size_t partial_floats() const {
-    return fast ? static_cast<size_t>(chunks) * tiles * (16 * va) * (16 * vb) : 0;
+    const size_t tile = pw ? static_cast<size_t>(tm) * tn : static_cast<size_t>(16 * va) * (16 * vb);
+    return fast ? static_cast<size_t>(chunks) * tiles * tile : 0;
   }
 };
 
@@ -2744,9 +2941,33 @@ static int dw_width(int c) { return c % 64 == 0 ? 4 : (c % 32 == 0 ? 2 : 1); }
 
 // wgs: busy workgroups to aim for over the whole map (0 = the measured best
 // on MI355X: 2048 for fp32, where the MFMA work dominates, 512 for bf16).
-static DwPlan dw_plan(int32_t dtype, int cin, int cout, int64_t n_pairs, int64_t max_pk,
-                      int wgs = 0) {
+// conv_dw_pairs_bf16_kernel's shape: 64 x 64 tiles, rows kDwPairsD steps
+// ahead per wave, kDwPairsWaves waves per SIMD, so 256 * kDwPairsWaves
+// workgroups fill the chip once. Measured on MI355X, config 3's two dW passes
+// (kernel alone, 2^3 stride-2 down C64->128 and up C128->64): 13.9 us each,
+// against 16.4-17.5 for 64 x 128 / 128 x 64 tiles (each row staged once, but
+// 256 registers), 14.9 with 2048-pair ranges on a grid sized by the row
+// counts (most workgroups idle), 15.5 at 3 waves per SIMD, 15.9-18.7 with
+// rows 2 to 4 steps ahead, and 36.3 for conv_dw_kernel.
+constexpr int kDwPairsD = 1, kDwPairsWaves = 2;
+static DwPlan dw_plan(int32_t dtype, int cin, int cout, int K, int64_t n_pairs, int64_t n_in,
+                      int64_t n_out, int wgs = 0) {
   DwPlan p;
+  const int64_t max_pk = std::min(n_in, n_out); // an offset pairs each row at most once
+  if (dtype == RHIP_BF16 && n_pairs > 0 && cin % 64 == 0 && cout % 64 == 0 &&
+      n_in * cin * 2 <= kBufMaxBytes && n_out * cout * 2 <= kBufMaxBytes) {
+    p.fast = p.pw = true;
+    p.tm = p.tn = 64;
+    p.tiles = (cin / p.tm) * (cout / p.tn);
+    // ranges per (offset, tile): about `target` workgroups over the map, at
+    // least 128 pairs (one step per wave) per range on average
+    const int64_t target = wgs > 0 ? wgs : 256 * kDwPairsWaves;
+    const int64_t per_k = ceil_div(n_pairs, static_cast<int64_t>(K));
+    p.chunks = std::max<int64_t>(1, std::min(target / (static_cast<int64_t>(K) * p.tiles),
+                                             ceil_div(per_k, kWaves * 32)));
+    p.ppb = 0; // the kernel splits each offset's pairs itself
+    return p;
+  }
   if (wgs <= 0)
     wgs = dtype == RHIP_F32 ? 2048 : 512;
   const int VE = dtype == RHIP_F32 ? 4 : 8;
@@ -2795,11 +3016,29 @@ static void pick_dw_b(const T *x, int cin, const T *gy, int cout, const int64_t 
 // dw [K, cin, cout] in T (fully overwritten). `partial` holds
 // plan.partial_floats() * K floats; `acc` (generic path) K*cin*cout floats.
 template <typename T>
-static void run_dw(const T *x, int cin, const T *gy, int cout, const int64_t *kofs, int K,
-                   const int32_t *in_rows, const int32_t *out_rows, int64_t n_pairs,
-                   const DwPlan &p, float *partial, float *acc, T *dw, hipStream_t s) {
+static void run_dw(const T *x, int64_t n_in, int cin, const T *gy, int64_t n_out, int cout,
+                   const int64_t *kofs, int K, const int32_t *in_rows, const int32_t *out_rows,
+                   int64_t n_pairs, const DwPlan &p, float *partial, float *acc, T *dw,
+                   hipStream_t s) {
   const int64_t nw = static_cast<int64_t>(K) * cin * cout;
-  if (p.fast && aligned16(x) && aligned16(gy)) {
+  if constexpr (!std::is_same<T, float>::value) {
+    // the plan checked the shape and the buffer sizes; rows that are not
+    // 16-byte aligned take the any-shape path below
+    if (p.pw && aligned16(x) && aligned16(gy)) {
+      const dim3 grid(static_cast<unsigned>(p.chunks), K, p.tiles);
+      hipLaunchKernelGGL((conv_dw_pairs_bf16_kernel<64, 64, kDwPairsD, kDwPairsWaves>), grid,
+                         dim3(kThreads), 0, s, x, n_in, cin, gy, n_out, cout, kofs, in_rows,
+                         out_rows, static_cast<int>(p.chunks), partial);
+      RHIP_LAUNCH_CHECK();
+      const dim3 rgrid(static_cast<unsigned>(p.tm * p.tn / (4 * kWave)), K, p.tiles);
+      hipLaunchKernelGGL((conv_dw_reduce_kernel<T>), rgrid, dim3(kThreads), 0, s, partial, kofs,
+                         int64_t(0), static_cast<int>(p.chunks), p.tiles, cout / p.tn, p.tm, p.tn,
+                         cin, cout, 1, dw);
+      RHIP_LAUNCH_CHECK();
+      return;
+    }
+  }
+  if (p.fast && !p.pw && aligned16(x) && aligned16(gy)) {
     if (p.va == 4)
       pick_dw_b<T, 4>(x, cin, gy, cout, kofs, K, in_rows, out_rows, p, partial, s);
     else if (p.va == 2)
@@ -2810,7 +3049,7 @@ static void run_dw(const T *x, int cin, const T *gy, int cout, const int64_t *ko
     const int TM = 16 * p.va, TN = 16 * p.vb;
     dim3 grid(static_cast<unsigned>(TM * TN / (4 * kWave)), K, p.tiles);
     hipLaunchKernelGGL((conv_dw_reduce_kernel<T>), grid, dim3(kThreads), 0, s, partial, kofs,
-                       p.ppb, static_cast<int>(p.chunks), p.tiles, cout / TN, TM, TN, cin, cout,
+                       p.ppb, static_cast<int>(p.chunks), p.tiles, cout / TN, TM, TN, cin, cout, 0,
                        dw);
     RHIP_LAUNCH_CHECK();
     return;
@@ -3236,7 +3475,7 @@ extern "C" int rhip_conv_workspace_bytes(int32_t K, int32_t cin, int32_t cout,
     check_dtype(dtype);
     Carve cv(nullptr, 0);
     carve_conv(cv, K, cin, cout, dtype, n_in, n_out,
-               dw_plan(dtype, cin, cout, n_pairs, std::min(n_in, n_out)));
+               dw_plan(dtype, cin, cout, K, n_pairs, n_in, n_out));
     *bytes = cv.used + 256;
   });
 }
@@ -3405,17 +3644,19 @@ extern "C" int rhip_conv_backward_weight(
                    "x, grad_y, kmap_offsets, in_rows and out_rows are required");
     RHIP_CHECK_ARG(workspace != nullptr, "workspace is null");
     // an offset pairs each input and each output row at most once
-    const DwPlan plan = dw_plan(dtype, cin, cout, n_pairs, std::min(n_in, n_out));
+    const DwPlan plan = dw_plan(dtype, cin, cout, K, n_pairs, n_in, n_out);
     Carve cv(workspace, workspace_bytes);
     const ConvWs w = carve_conv(cv, K, cin, cout, dtype, n_in, n_out, plan);
     if (dtype == RHIP_F32)
-      run_dw<float>(static_cast<const float *>(x), cin, static_cast<const float *>(grad_y), cout,
-                    kmap_offsets, K, in_rows, out_rows, n_pairs, plan, w.partial, w.acc,
-                    static_cast<float *>(grad_w), stream);
+      run_dw<float>(static_cast<const float *>(x), n_in, cin,
+                    static_cast<const float *>(grad_y), n_out, cout, kmap_offsets, K, in_rows,
+                    out_rows, n_pairs, plan, w.partial, w.acc, static_cast<float *>(grad_w),
+                    stream);
     else
-      run_dw<__bf16>(static_cast<const __bf16 *>(x), cin, static_cast<const __bf16 *>(grad_y),
-                     cout, kmap_offsets, K, in_rows, out_rows, n_pairs, plan, w.partial, w.acc,
-                     static_cast<__bf16 *>(grad_w), stream);
+      run_dw<__bf16>(static_cast<const __bf16 *>(x), n_in, cin,
+                     static_cast<const __bf16 *>(grad_y), n_out, cout, kmap_offsets, K, in_rows,
+                     out_rows, n_pairs, plan, w.partial, w.acc, static_cast<__bf16 *>(grad_w),
+                     stream);
   });
 }
 
