@@ -600,9 +600,10 @@ def conv_weight_grad(x: torch.Tensor, grad_y: torch.Tensor, kmap: KernelMap,
                      K: int) -> torch.Tensor:
     """dW as the convolution layer computes it: from the neighbour table where
     the library has a kernel for the shape, else from the pair list. bf16
-    maps of at most 8 offsets with fewer than 2 pairs per output row (a
-    transposed stride-2 map: one neighbour per row) also take the pair list,
-    which is faster there."""
+    maps of at most 8 offsets also take the pair list, which is faster there,
+    when they hold fewer than 2 pairs per output row (a transposed stride-2
+    map: one neighbour per row) or pair each input row at most once (a
+    stride-2 map) with channel counts that are multiples of 64."""
     _require_cuda(x, "x")
     dt = _dtype_code(x.dtype)
     x, grad_y = x.contiguous(), grad_y.to(x.dtype).contiguous()
@@ -610,7 +611,10 @@ def conv_weight_grad(x: torch.Tensor, grad_y: torch.Tensor, kmap: KernelMap,
     gw = torch.empty((K, cin, cout), dtype=x.dtype, device=x.device)
     ws = _conv_ws(K, cin, cout, dt, x.device, kmap)
     st = RHIP_ERR_UNSUPPORTED
-    if not (x.dtype == torch.bfloat16 and K <= 8 and kmap.n_pairs < 2 * kmap.n_out):
+    pair_list = x.dtype == torch.bfloat16 and K <= 8 and (
+        kmap.n_pairs < 2 * kmap.n_out
+        or (kmap.n_pairs <= kmap.n_in and cin % 64 == 0 and cout % 64 == 0))
+    if not pair_list:
         st = lib().rhip_conv_backward_weight_rows(_ptr(x), kmap.n_in, cin, _ptr(grad_y),
                                                   kmap.n_out, cout, K, _ptr(kmap.nbr),
                                                   _ptr(kmap.out_order), _ptr(gw), dt, _ptr(ws),

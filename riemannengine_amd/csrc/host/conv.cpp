@@ -162,11 +162,18 @@ at::Tensor hip_sparse_convolution(const at::Tensor &features, const at::Tensor &
                      : torch::empty({0}, features.options().dtype(torch::kFloat));
   // dW from the neighbour table where the library has a kernel for the
   // shape, else from the pair lists (built now, once per map, when a weight
-  // gradient may follow). bf16 maps of at most 8 offsets with fewer than 2
-  // pairs per output row (a transposed stride-2 map) take the pair lists:
-  // config 3's transposed map, 38 us against 46.
+  // gradient may follow). bf16 maps of at most 8 offsets take the pair lists
+  // when they hold fewer than 2 pairs per output row (a transposed stride-2
+  // map), or pair each input row at most once (a stride-2 map) with channel
+  // counts that are multiples of 64 (the per-wave pair kernel). Measured per
+  // call: config 3's maps 19 us each against 27 and 46 for the table kernel;
+  // config 5's C64->128, 128->256 and 256->256 downs 30, 30 and 27 us
+  // against 46, 38 and 33.
   const int32_t dt = rhip_dtype(features);
-  const bool sparse_small = dt == RHIP_BF16 && map.K <= 8 && map.size() < 2 * map.n_out;
+  const int64_t kin = kernel.size(1), kout = kernel.size(2);
+  const bool sparse_small =
+      dt == RHIP_BF16 && map.K <= 8 &&
+      (map.size() < 2 * map.n_out || (map.size() <= map.n_in && kin % 64 == 0 && kout % 64 == 0));
   const bool pairs_dw =
       sparse_small || rhip_conv_backward_weight_rows_supported(
                           dt, static_cast<int32_t>(kernel.size(1)),

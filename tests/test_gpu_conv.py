@@ -163,6 +163,31 @@ def test_strided_and_transposed(dtype):
     _run_and_check(km.swapped(), 128, 64, dtype, seed=6, tag="up")
 
 
+def test_stride2_dw_dispatch_bf16():
+    """bf16 2^3 stride-2 maps pair each input row once: with channel counts
+    that are multiples of 64 the dispatch (abi.conv_weight_grad, as the host
+    layer) takes the per-wave pair-list kernel, else the neighbour table;
+    both against the oracle."""
+    rng = np.random.default_rng(31)
+    c, _, _ = oracle.insert_and_map(random_coords(rng, 20000, 3, 12))  # about half the cells
+    tin = abi.hash_build(to_dev(c))
+    tout = abi.hash_build(abi.stride_coords(to_dev(c), [2, 2, 2]))
+    km = abi.kernel_map(tin, tout, to_dev(oracle.region_offsets(3, 2)))
+    assert km.n_pairs == km.n_in and km.n_pairs >= 2 * km.n_out
+    g = torch.Generator().manual_seed(3)
+    for cin, cout, path in ((64, 128, "pairs"), (128, 64, "pairs"), (32, 64, "rows")):
+        x = torch.randn(km.n_in, cin, generator=g).to(torch.bfloat16).to(DEV)
+        gy = torch.randn(km.n_out, cout, generator=g).to(torch.bfloat16).to(DEV)
+        print(f"stride-2 dW dispatch {cin}->{cout}", flush=True)
+        got = abi.conv_weight_grad(x, gy, km, 8)
+        want = (abi.conv_backward_weight(x, gy, km, 8) if path == "pairs"
+                else abi.conv_backward_weight_rows(x, gy, km, 8))
+        assert torch.equal(got, want), path
+        _, _, rgw = _oracle_conv(km, x.float().cpu().numpy(),
+                                 np.zeros((8, cin, cout), np.float32), gy.float().cpu().numpy())
+        assert_rel(got.float().cpu().numpy(), rgw, TOL[torch.bfloat16], f"{cin}->{cout} dW")
+
+
 def _rows_check(km, cin, cout, seed, tag, dtype=torch.bfloat16):
     """dW from the neighbour table vs the oracle on the map's own pairs (the
     oracle sees the operands rounded to dtype) and vs the pair-list kernel."""
