@@ -2661,7 +2661,9 @@ static bool launch_os_lds(const T *x, int64_t n_x, int cred, const T *wt, const 
 // barrier too, which halves the weight slices each row re-stages (config 5
 // stage 4, 9,342 rows at C256: forward 118.8 -> 102.8 us, dX 106.5 -> 91.9
 // us with the splits os_splits then picks; stage 3, 43,444 rows at C128:
-// 81.0 -> 78.9 and 75.1 -> 74.5 us); fp32 at 32 columns with
+// 81.0 -> 78.9 and 75.1 -> 74.5 us), or one row group where the offset axis
+// is not split (config 3's 87,195 coarse rows at C64->128, forward and the
+// transposed layer's dX: 32.9 -> 31.1 and 29.3 -> 27.8 us per call); fp32 at 32 columns with
 // 24 index slots (stencils of 33 to 96 offsets) holds the indices in
 // registers and takes two stages per barrier at 5 waves per SIMD (config 4
 // forward 305 -> 256 us; the LDS indices with two stages: 309 us; register
@@ -2684,6 +2686,9 @@ static bool os_lds_shape(const T *x, int64_t n_x, int cred, const T *wt, const i
     constexpr int W = NT >= 128 ? 4 : (CSUB == 1 && NT >= 64 ? 6 : 8);
     constexpr int G = NT >= 128 ? 1 : (CSUB == 1 ? 4 : 1);
     constexpr int RG = NT >= 128 ? kWideRG : 1;
+    if (NT >= 128 && splits <= 1) // without a split: one row group, twice the workgroups
+      return launch_os_lds<T, NT, 1, CSUB, G, W, KQ>(x, n_x, cred, wt, wperm, ncols, bias, nbr,
+                                                     n_rows, K, order, y, splits, partial, s);
     return launch_os_lds<T, NT, RG, CSUB, G, W, KQ>(x, n_x, cred, wt, wperm, ncols, bias, nbr,
                                                     n_rows, K, order, y, splits, partial, s);
   }
