@@ -2677,7 +2677,12 @@ static bool os_lds_shape(const T *x, int64_t n_x, int cred, const T *wt, const i
     return launch_os_lds<T, NT, 1, CSUB, 2, 5, KQ, true>(
         x, n_x, cred, wt, wperm, ncols, bias, nbr, n_rows, K, order, y, splits, partial, s);
   } else if constexpr (kIsF32<T>) {
-    return launch_os_lds<T, NT, 1, CSUB, 1, NT == 64 ? 6 : 8, KQ>(
+    // tiles of at most 32 columns: four 16-channel chunks per barrier group
+    // (config 1, 51,554 rows: a workgroup's stages are a chain of memory
+    // round trips; forward C16->32 39.2 -> 35.2 us at G = 4, dX C32->16 39.6
+    // -> 36.0 us at G = 2, per call)
+    constexpr int G = NT <= 32 ? 4 / CSUB : 1;
+    return launch_os_lds<T, NT, 1, CSUB, G, NT == 64 ? 6 : 8, KQ>(
         x, n_x, cred, wt, wperm, ncols, bias, nbr, n_rows, K, order, y, splits, partial, s);
   } else if constexpr (NT == 64 && CSUB == 2) {
     return launch_os_lds<T, NT, 2, CSUB, 1, 6, KQ>(x, n_x, cred, wt, wperm, ncols, bias, nbr,
@@ -3147,9 +3152,10 @@ static bool dw_rows_supported(int32_t dtype, int cin, int cout, int K, int64_t n
 // XCD), one round of resident workgroups (256 CUs x the waves per SIMD:
 // each workgroup puts one wave on every SIMD of its CU), at most
 // kDwRowsBlocks (the partial slots of the workspace), at least min_segs
-// segments of 64 positions each (4 for fp32; 16 for bf16, whose small maps
-// lose more to partial slots than they gain from a full round: config 3's
-// down map 32 us at 32 ranges, 38 at 128).
+// segments of 64 positions each (2 for fp32: config 1's dW 44.7 -> 39.0 us
+// per call against 4; 16 for bf16, whose small maps lose more to partial
+// slots than they gain from a full round: config 3's down map 32 us at 32
+// ranges, 38 at 128).
 static int dw_ranges_for(int units, int waves, int64_t n_out, int min_segs) {
   int64_t r = std::max<int64_t>(kXcds, (256 * waves / units) / kXcds * kXcds);
   const int64_t segs = ceil_div(std::max<int64_t>(n_out, 1), 64);
@@ -3186,7 +3192,7 @@ static int dw_pos_bf16_ranges(int K, int cin, int cout, int64_t n_out) {
 static int dw_pos_f32_ranges(int K, int cin, int cout, int64_t n_out) {
   const int vb = cout % 64 == 0 ? 4 : 2;
   const int waves = K <= kDwPosMaxKSmall ? 3 : (vb == 4 ? kDwPosWaves<4> : kDwPosWaves<2>);
-  return dw_pos_ranges(K, cin, cout, vb, waves, n_out, 4);
+  return dw_pos_ranges(K, cin, cout, vb, waves, n_out, 2);
 }
 
 // grad_w [K, cin, cout] (bf16, overwritten) from the neighbour table.
