@@ -188,6 +188,27 @@ def test_stride2_dw_dispatch_bf16():
         assert_rel(got.float().cpu().numpy(), rgw, TOL[torch.bfloat16], f"{cin}->{cout} dW")
 
 
+@pytest.mark.parametrize("npts,cin,cout", [(1, 64, 64), (33, 64, 128), (65, 128, 64),
+                                           (700, 192, 64), (3000, 64, 192)])
+def test_pair_list_dw_bf16_tiles_small_maps(npts, cin, cout):
+    """The per-wave pair-list dW (bf16, 64-channel tiles) where offsets hold
+    no pairs, fewer than one 32-pair step or a few steps, and with 3 tiles
+    per axis, against the oracle on the map's own pairs; repeat calls are
+    bitwise equal."""
+    rng = np.random.default_rng(npts + cin)
+    c, _, _ = oracle.insert_and_map(random_coords(rng, npts, 3, 4 if npts < 100 else 9))
+    _, _, km = gpu_tables_and_map(c, c, oracle.region_offsets(3, 3), same=True)
+    g = torch.Generator().manual_seed(npts)
+    x = torch.randn(km.n_in, cin, generator=g).to(torch.bfloat16).to(DEV)
+    gy = torch.randn(km.n_out, cout, generator=g).to(torch.bfloat16).to(DEV)
+    print(f"pair-list dW bf16 {cin}->{cout} n={km.n_in} P={km.n_pairs}", flush=True)
+    gw = abi.conv_backward_weight(x, gy, km, km.K)
+    assert torch.equal(gw, abi.conv_backward_weight(x, gy, km, km.K))
+    _, _, rgw = _oracle_conv(km, x.float().cpu().numpy(),
+                             np.zeros((km.K, cin, cout), np.float32), gy.float().cpu().numpy())
+    assert_rel(gw.float().cpu().numpy(), rgw, TOL[torch.bfloat16], f"{npts} {cin}->{cout} dW")
+
+
 def _rows_check(km, cin, cout, seed, tag, dtype=torch.bfloat16):
     """dW from the neighbour table vs the oracle on the map's own pairs (the
     oracle sees the operands rounded to dtype) and vs the pair-list kernel."""
