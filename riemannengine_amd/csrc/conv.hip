@@ -45,6 +45,17 @@ typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
 typedef uint32_t v2u __attribute__((ext_vector_type(2)));
 typedef uint32_t v4u __attribute__((ext_vector_type(4)));
 
+// LDS transpose read: within a 16-lane group, lane i receives the (i % 4)-th
+// 16-bit element at the address of lane 4e + i/4 as element e.
+typedef short v4s __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) v4s lds_v4s;
+
+__device__ __forceinline__ v4s ds_read_tr16(const void *p) {
+  // generic LDS pointer -> LDS address space (the low 32 bits are the offset)
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      reinterpret_cast<lds_v4s *>(static_cast<uint32_t>(reinterpret_cast<uintptr_t>(p))));
+}
+
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / kWave;
 constexpr int kMaskWords = 4; // the MFMA paths handle K <= 128 offsets
@@ -444,8 +455,13 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(WAVES)
 // moves the row's index to the lane with a ds_bpermute. LDS then holds only
 // the staged weights, which is what limits occupancy where a stencil has
 // many slots (config 4's 81 offsets: 48 KB of indices per workgroup).
+// WTR (bf16): the weights are W itself, [K][CW][ncols] (the forward needs no
+// transposed copy): a stage's chunk goes to LDS as CCH rows of NT columns
+// and each B operand is two transposed reads (ds_read_b64_tr_b16) that give
+// lane (n, g) reduction rows 8g..8g+7 of column n, the order of the A
+// operand's channels.
 template <typename T, int NT, int RG, int CSUB, int G, int WAVES, int CW, int KQ, bool SPLIT,
-          bool REGK = false>
+          bool REGK = false, bool WTR = false>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(WAVES))) void
 conv_os_lds_kernel(const T *__restrict__ x, int64_t n_x, const T *__restrict__ wt,
                    const int32_t *__restrict__ wperm, int ncols,
@@ -472,7 +488,9 @@ conv_os_lds_kernel(const T *__restrict__ x, int64_t n_x, const T *__restrict__ w
   static_assert(KQ % 8 == 0, "index slots come in groups of eight");
   constexpr int MW = KQ / 8;
 
-  __shared__ __align__(16) T sB[G][NT * LDW];
+  static_assert(!WTR || !std::is_same<T, float>::value, "untransposed weights: bf16 only");
+  constexpr int LDT = NT + 8; // WTR: LDS row stride (elements) of a chunk's CCH rows
+  __shared__ __align__(16) T sB[G][WTR ? CCH * LDT : NT * LDW];
   __shared__ int32_t sK[REGK ? 1 : kWaves][REGK ? 1 : RG][REGK ? 1 : KQ][kWave];
   static_assert(!REGK || KQ <= 32, "register-held slots fit one vector");
   constexpr int KV = KQ <= 8 ? 8 : (KQ <= 16 ? 16 : 32);
@@ -623,9 +641,14 @@ conv_os_lds_kernel(const T *__restrict__ x, int64_t n_x, const T *__restrict__ w
 #pragma unroll
       for (int i = 0; i < NPT; ++i) {
         const int li = min(static_cast<int>(threadIdx.x) + i * kThreads, NV - 1);
-        wreg[j][i] = *reinterpret_cast<const uint4 *>(
-            wt + (static_cast<int64_t>(kw) * ncols + col0 + li / (CCH / VE)) * CW +
-            ccj[j] * CCH + (li % (CCH / VE)) * VE);
+        if constexpr (WTR) // row li / (NT / VE) of the chunk, 16-byte piece li % (NT / VE)
+          wreg[j][i] = *reinterpret_cast<const uint4 *>(
+              wt + (static_cast<int64_t>(kw) * CW + ccj[j] * CCH + li / (NT / VE)) * ncols +
+              col0 + (li % (NT / VE)) * VE);
+        else
+          wreg[j][i] = *reinterpret_cast<const uint4 *>(
+              wt + (static_cast<int64_t>(kw) * ncols + col0 + li / (CCH / VE)) * CW +
+              ccj[j] * CCH + (li % (CCH / VE)) * VE);
       }
     }
     v4u a[G][RG][CSUB];
@@ -643,9 +666,14 @@ conv_os_lds_kernel(const T *__restrict__ x, int64_t n_x, const T *__restrict__ w
 #pragma unroll
       for (int i = 0; i < NPT; ++i) {
         const int li = threadIdx.x + i * kThreads;
-        if (NV % kThreads == 0 || li < NV)
-          *reinterpret_cast<uint4 *>(&sB[j][(li / (CCH / VE)) * LDW + (li % (CCH / VE)) * VE]) =
-              wreg[j][i];
+        if (NV % kThreads == 0 || li < NV) {
+          if constexpr (WTR)
+            *reinterpret_cast<uint4 *>(&sB[j][(li / (NT / VE)) * LDT + (li % (NT / VE)) * VE]) =
+                wreg[j][i];
+          else
+            *reinterpret_cast<uint4 *>(&sB[j][(li / (CCH / VE)) * LDW + (li % (CCH / VE)) * VE]) =
+                wreg[j][i];
+        }
       }
     __syncthreads(); // the group's weights are staged
 #pragma unroll
@@ -659,8 +687,14 @@ conv_os_lds_kernel(const T *__restrict__ x, int64_t n_x, const T *__restrict__ w
             at[r] = __builtin_bit_cast(Frag, quad_to_mfma(a[j][r][sub], tsrc));
 #pragma unroll
           for (int nb = 0; nb < NB; ++nb) {
-            const Frag b = *reinterpret_cast<const Frag *>(
-                &sB[j][(nb * 16 + i16) * LDW + sub * CH + g * EPL]);
+            Frag b;
+            if constexpr (WTR) {
+              const T *base = &sB[j][(sub * CH + 8 * g + i16 / 4) * LDT + nb * 16 + 4 * (i16 % 4)];
+              const v4s lo = ds_read_tr16(base), hi = ds_read_tr16(base + 4 * LDT);
+              b = __builtin_bit_cast(Frag, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+            } else {
+              b = *reinterpret_cast<const Frag *>(&sB[j][(nb * 16 + i16) * LDW + sub * CH + g * EPL]);
+            }
 #pragma unroll
             for (int r = 0; r < RG; ++r)
               M::mma(at[r], b, acc[r][nb]);
@@ -1059,14 +1093,6 @@ template <typename T> struct DwShape;
 template <> struct DwShape<float> { static constexpr int kPairsPerWave = 16; };
 template <> struct DwShape<__bf16> { static constexpr int kPairsPerWave = 32; };
 
-typedef short v4s __attribute__((ext_vector_type(4)));
-typedef __attribute__((address_space(3))) v4s lds_v4s;
-
-__device__ __forceinline__ v4s ds_read_tr16(const void *p) {
-  // generic LDS pointer -> LDS address space (the low 32 bits are the offset)
-  return __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-      reinterpret_cast<lds_v4s *>(static_cast<uint32_t>(reinterpret_cast<uintptr_t>(p))));
-}
 
 template <typename T, int VA, int VB, bool DB, int WAVES = 1>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(WAVES))) void conv_dw_kernel(
@@ -2604,8 +2630,17 @@ template <typename T, int NT, int RG, int CSUB, int G, int WAVES, int CW, int KQ
 static void launch_os_lds_cw(dim3 grid, bool split, const T *x, int64_t n_x, const T *wt,
                              const int32_t *wperm, int ncols, const float *bias,
                              const int32_t *nbr, int64_t n_rows, int K, const int32_t *order,
-                             T *y, float *partial, hipStream_t s) {
+                             T *y, float *partial, hipStream_t s, bool wtr = false) {
   if constexpr (!kIsF32<T>) {
+    if constexpr (NT >= 128) {
+      if (wtr && !split) { // weights as [K][CW][ncols] (not transposed)
+        hipLaunchKernelGGL(
+            (conv_os_lds_kernel<T, NT, RG, CSUB, G, WAVES, CW, KQ, false, REGK, true>), grid,
+            dim3(kThreads), 0, s, x, n_x, wt, wperm, ncols, bias, nbr, n_rows, K, order, y,
+            nullptr);
+        return;
+      }
+    }
     if (split) {
       hipLaunchKernelGGL((conv_os_lds_kernel<T, NT, RG, CSUB, G, WAVES, CW, KQ, true, REGK>), grid,
                          dim3(kThreads), 0, s, x, n_x, wt, wperm, ncols, bias, nbr, n_rows, K,
@@ -2624,24 +2659,24 @@ template <typename T, int NT, int RG, int CSUB, int G, int WAVES, int KQ, bool R
 static bool launch_os_lds(const T *x, int64_t n_x, int cred, const T *wt, const int32_t *wperm,
                           int ncols, const float *bias, const int32_t *nbr, int64_t n_rows,
                           int K, const int32_t *order, T *y, int splits, float *partial,
-                          hipStream_t s) {
+                          hipStream_t s, bool wtr = false) {
   constexpr int CCH = CSUB * kChOf<T>;
   constexpr int ROWS = kWaves * RG * 16;
   const bool sp = splits > 1;
-  if (kIsF32<T> && sp)
-    return false;
+  if ((kIsF32<T> && sp) || (wtr && (kIsF32<T> || sp || NT < 128)))
+    return false; // untransposed weights: bf16 128-column tiles without a split only
   const dim3 grid(static_cast<unsigned>(xcd_grid(ceil_div(n_rows, ROWS))), ncols / NT, splits);
   if (cred == CCH)
     launch_os_lds_cw<T, NT, RG, CSUB, G, WAVES, CCH, KQ, REGK>(grid, sp, x, n_x, wt, wperm, ncols, bias,
-                                                         nbr, n_rows, K, order, y, partial, s);
+                                                         nbr, n_rows, K, order, y, partial, s, wtr);
   else if (cred == 2 * CCH)
     launch_os_lds_cw<T, NT, RG, CSUB, G, WAVES, 2 * CCH, KQ, REGK>(grid, sp, x, n_x, wt, wperm, ncols,
                                                              bias, nbr, n_rows, K, order, y,
-                                                             partial, s);
+                                                             partial, s, wtr);
   else if (cred == 4 * CCH)
     launch_os_lds_cw<T, NT, RG, CSUB, G, WAVES, 4 * CCH, KQ, REGK>(grid, sp, x, n_x, wt, wperm, ncols,
                                                              bias, nbr, n_rows, K, order, y,
-                                                             partial, s);
+                                                             partial, s, wtr);
   else
     return false;
   if (splits > 1) {
@@ -2672,7 +2707,10 @@ static bool launch_os_lds(const T *x, int64_t n_x, int cred, const T *wt, const 
 template <typename T, int NT, int CSUB, int KQ>
 static bool os_lds_shape(const T *x, int64_t n_x, int cred, const T *wt, const int32_t *wperm,
                          int ncols, const float *bias, const int32_t *nbr, int64_t n_rows, int K,
-                         const int32_t *order, T *y, int splits, float *partial, hipStream_t s) {
+                         const int32_t *order, T *y, int splits, float *partial, hipStream_t s,
+                         bool wtr = false) {
+  if (kIsF32<T> && wtr)
+    return false; // untransposed weights: bf16 only
   if constexpr (kIsF32<T> && NT == 32 && KQ == 24) {
     return launch_os_lds<T, NT, 1, CSUB, 2, 5, KQ, true>(
         x, n_x, cred, wt, wperm, ncols, bias, nbr, n_rows, K, order, y, splits, partial, s);
@@ -2684,18 +2722,30 @@ static bool os_lds_shape(const T *x, int64_t n_x, int cred, const T *wt, const i
     constexpr int G = NT <= 32 ? 4 / CSUB : 1;
     return launch_os_lds<T, NT, 1, CSUB, G, NT == 64 ? 6 : 8, KQ>(
         x, n_x, cred, wt, wperm, ncols, bias, nbr, n_rows, K, order, y, splits, partial, s);
-  } else if constexpr (NT == 64 && CSUB == 2) {
-    return launch_os_lds<T, NT, 2, CSUB, 1, 6, KQ>(x, n_x, cred, wt, wperm, ncols, bias, nbr,
-                                                   n_rows, K, order, y, splits, partial, s);
-  } else {
-    constexpr int W = NT >= 128 ? 4 : (CSUB == 1 && NT >= 64 ? 6 : 8);
-    constexpr int G = NT >= 128 ? 1 : (CSUB == 1 ? 4 : 1);
-    constexpr int RG = NT >= 128 ? kWideRG : 1;
-    if (NT >= 128 && splits <= 1) // without a split: one row group, twice the workgroups
-      return launch_os_lds<T, NT, 1, CSUB, G, W, KQ>(x, n_x, cred, wt, wperm, ncols, bias, nbr,
+  } else if constexpr (NT < 128) {
+    // untransposed weights only in 128-column tiles: the narrower shapes run
+    // at 6-8 waves per SIMD, where the transposed reads' registers spill
+    // (config 2 bf16 forward 92-99 -> 103 us)
+    if (wtr)
+      return false;
+    if constexpr (NT == 64 && CSUB == 2)
+      return launch_os_lds<T, NT, 2, CSUB, 1, 6, KQ>(x, n_x, cred, wt, wperm, ncols, bias, nbr,
                                                      n_rows, K, order, y, splits, partial, s);
-    return launch_os_lds<T, NT, RG, CSUB, G, W, KQ>(x, n_x, cred, wt, wperm, ncols, bias, nbr,
-                                                    n_rows, K, order, y, splits, partial, s);
+    constexpr int W = CSUB == 1 && NT >= 64 ? 6 : 8;
+    constexpr int G = CSUB == 1 ? 4 : 1;
+    return launch_os_lds<T, NT, 1, CSUB, G, W, KQ>(x, n_x, cred, wt, wperm, ncols, bias, nbr,
+                                                   n_rows, K, order, y, splits, partial, s);
+  } else { // bf16 128-column tiles: 4 waves per SIMD, one stage per barrier group
+    if (splits <= 1) // without a split: one row group, twice the workgroups
+      return launch_os_lds<T, NT, 1, CSUB, 1, 4, KQ>(x, n_x, cred, wt, wperm, ncols, bias, nbr,
+                                                     n_rows, K, order, y, splits, partial, s, wtr);
+    // untransposed weights only without a split (config 3's C64->128 forward
+    // 33.4 -> 29.0 us per call; config 5's split stages gained nothing)
+    if (wtr)
+      return false;
+    return launch_os_lds<T, NT, kWideRG, CSUB, 1, 4, KQ>(x, n_x, cred, wt, wperm, ncols, bias,
+                                                         nbr, n_rows, K, order, y, splits, partial,
+                                                         s);
   }
 }
 
@@ -2703,39 +2753,39 @@ template <typename T, int NT, int KQ>
 static bool os_lds_csub(const T *x, int64_t n_x, int cred, const T *wt, const int32_t *wperm,
                         int ncols, const float *bias, const int32_t *nbr, int64_t n_rows, int K,
                         const int32_t *order, T *y, int splits, float *partial,
-                        hipStream_t s) {
+                        hipStream_t s, bool wtr = false) {
   constexpr int CH = kChOf<T>;
   if constexpr (kIsF32<T>) {
     if (cred % (4 * CH) == 0)
       return os_lds_shape<T, NT, 4, KQ>(x, n_x, cred, wt, wperm, ncols, bias, nbr, n_rows, K,
-                                        order, y, splits, partial, s);
+                                        order, y, splits, partial, s, wtr);
   }
   if (cred % (2 * CH) == 0)
     return os_lds_shape<T, NT, 2, KQ>(x, n_x, cred, wt, wperm, ncols, bias, nbr, n_rows, K, order,
-                                      y, splits, partial, s);
+                                      y, splits, partial, s, wtr);
   return os_lds_shape<T, NT, 1, KQ>(x, n_x, cred, wt, wperm, ncols, bias, nbr, n_rows, K, order,
-                                    y, splits, partial, s);
+                                    y, splits, partial, s, wtr);
 }
 
 template <typename T, int KQ>
 static bool run_os_lds_nt(const T *x, int64_t n_x, int cred, const T *wt, const int32_t *wperm,
                           int ncols, const float *bias, const int32_t *nbr, int64_t n_rows,
                           int K, const int32_t *order, T *y, int splits, float *partial,
-                          hipStream_t s) {
+                          hipStream_t s, bool wtr = false) {
   const int nt = os_nt<T>(ncols);
   if constexpr (!kIsF32<T>) {
     if (nt == 128)
       return os_lds_csub<T, 128, KQ>(x, n_x, cred, wt, wperm, ncols, bias, nbr, n_rows, K, order,
-                                     y, splits, partial, s);
+                                     y, splits, partial, s, wtr);
   }
   if (nt == 64)
     return os_lds_csub<T, 64, KQ>(x, n_x, cred, wt, wperm, ncols, bias, nbr, n_rows, K, order, y,
-                                  splits, partial, s);
+                                  splits, partial, s, wtr);
   if (nt == 32)
     return os_lds_csub<T, 32, KQ>(x, n_x, cred, wt, wperm, ncols, bias, nbr, n_rows, K, order, y,
-                                  splits, partial, s);
+                                  splits, partial, s, wtr);
   return os_lds_csub<T, 16, KQ>(x, n_x, cred, wt, wperm, ncols, bias, nbr, n_rows, K, order, y,
-                                splits, partial, s);
+                                splits, partial, s, wtr);
 }
 
 // The fast forward/dX kernel where it applies: at most 96 offsets, no split,
@@ -2745,15 +2795,15 @@ template <typename T>
 static bool run_os_lds(const T *x, int64_t n_x, int cred, const T *wt, const int32_t *wperm,
                        int credw, int ncols, const float *bias, const int32_t *nbr,
                        int64_t n_rows, int K, const int32_t *order, T *y, int splits,
-                       float *partial, hipStream_t s) {
+                       float *partial, hipStream_t s, bool wtr = false) {
   if (K > 96 || cred != credw || n_x < 1 || !os_fast(x, cred, wt, credw, ncols, K) ||
       n_x * cred * static_cast<int64_t>(sizeof(T)) > kBufMaxBytes)
     return false;
   if (K > 32)
     return run_os_lds_nt<T, 24>(x, n_x, cred, wt, wperm, ncols, bias, nbr, n_rows, K, order, y,
-                                splits, partial, s);
+                                splits, partial, s, wtr);
   return run_os_lds_nt<T, 8>(x, n_x, cred, wt, wperm, ncols, bias, nbr, n_rows, K, order, y,
-                             splits, partial, s);
+                             splits, partial, s, wtr);
 }
 
 // Shape of the resident-weight kernel (conv_fr_kernel) for a bf16 map: the
@@ -3401,6 +3451,17 @@ static void conv_forward_into(const void *x, int64_t n_in, int32_t cin, const vo
     run_os<float>(static_cast<const float *>(x), n_in, cin, w, credw, cout, bias, nbr, n_out, K,
                   out_order, static_cast<float *>(y), os_partial, stream);
   } else {
+    // the LDS-indexed kernel reads W itself where it takes the shape
+    // (unpadded reductions, unsplit 128-column tiles): no transposed copy
+    if (n_out > 0 && credw == cin) {
+      const int splits = os_partial ? os_splits<__bf16>(n_out, cin, cout, K) : 1;
+      if (run_os_lds(static_cast<const __bf16 *>(x), n_in, cin,
+                     static_cast<const __bf16 *>(weight), nullptr, cin, cout, bias, nbr, n_out, K,
+                     out_order, static_cast<__bf16 *>(y), splits, os_partial, stream, true)) {
+        RHIP_LAUNCH_CHECK();
+        return;
+      }
+    }
     __bf16 *w = static_cast<__bf16 *>(wt);
     hipLaunchKernelGGL((transpose_w_kernel<__bf16>), dim3(ceil_div(nw, kThreads)),
                        dim3(kThreads), 0, stream, static_cast<const __bf16 *>(weight), K, cin,
