@@ -505,6 +505,26 @@ def _torch_gather_gemm_scatter(km, x, w, gy):
     return y.detach(), x.grad, w.grad
 
 
+@pytest.mark.parametrize("cin", [64, 128])
+def test_bf16_forward_untransposed_weights(cin):
+    """bf16 128-column tiles without an offset-axis split read W itself (two
+    transposed LDS reads per B operand) instead of a transposed copy: a 3^3
+    map with enough rows that the forward does not split (> 55k output rows
+    at C_out = 128), against the plain PyTorch fp32 gather-matmul-scatter."""
+    c = scenes.indoor_batch(1, 4)
+    _, _, km = gpu_tables_and_map(c, c, oracle.region_offsets(3, 3), same=True)
+    assert km.n_out > 60000
+    g = torch.Generator(device="cpu").manual_seed(cin)
+    x = torch.randn((km.n_in, cin), generator=g).to(DEV, torch.bfloat16)
+    w = (torch.randn((27, cin, 128), generator=g) * (2.0 / (cin * 27)) ** 0.5).to(DEV, torch.bfloat16)
+    gy = torch.zeros((km.n_out, 128), device=DEV)
+    print(f"untransposed-weight forward C{cin}->128 n={km.n_out}", flush=True)
+    y = abi.conv_forward(x, w, km)
+    ry, _, _ = _torch_gather_gemm_scatter(km, x, w, gy)
+    assert_rel(y.float().cpu().numpy(), ry.cpu().numpy(), TOL[torch.bfloat16], "Y")
+    assert torch.equal(y, abi.conv_forward(x, w, km))
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_config2_full_size_vs_torch(dtype):
     """Config 2 at full size (4 x ~100k voxels, C64, 3^3) against the plain
