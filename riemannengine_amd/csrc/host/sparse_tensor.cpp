@@ -185,13 +185,28 @@ at::Tensor SparseTensor::quantize_features(const at::Tensor &features,
       return features;
     return features.index_select(0, first_rows.to(features.device(), torch::kLong));
   }
-  TORCH_CHECK(features.is_cuda() && (features.scalar_type() == torch::kFloat ||
-                                     features.scalar_type() == torch::kBFloat16),
-              "quantization by sum, average or max runs on the HIP pooling kernels, which "
-              "take fp32 or bf16 device features; got ",
-              features.scalar_type(), " on ", features.device());
-  return hip_group_reduce(features, row_to_unique.to(features.device()), unique_count,
-                          reduction);
+  TORCH_CHECK(features.is_cuda(), "quantization runs on the device; got features on ",
+              features.device());
+  if (features.scalar_type() == torch::kFloat || features.scalar_type() == torch::kBFloat16)
+    return hip_group_reduce(features, row_to_unique.to(features.device()), unique_count,
+                            reduction);
+  // other dtypes (fp64, fp16): torch's own scatter reductions, the operations
+  // the reference applies to every dtype (sparse_tensor.cpp:461-477)
+  const auto idx = row_to_unique.to(features.device(), torch::kLong);
+  auto shape = features.sizes().vec();
+  shape[0] = unique_count;
+  auto out = torch::zeros(shape, features.options());
+  if (reduction == RHIP_POOL_MAX_SCATTER) {
+    auto index = idx.view({-1, 1}).expand_as(features);
+    return out.scatter_reduce(0, index, features, "amax", /*include_self=*/false);
+  }
+  out = out.index_add(0, idx, features);
+  if (reduction == RHIP_POOL_AVG) {
+    auto counts = torch::zeros({unique_count}, features.options())
+                      .index_add(0, idx, torch::ones({features.size(0)}, features.options()));
+    out = out / counts.view({-1, 1});
+  }
+  return out;
 }
 
 } // namespace riemann

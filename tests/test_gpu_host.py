@@ -205,19 +205,31 @@ def test_sparse_tensor_reference_spellings():
     assert conv(b).F.dtype == torch.bfloat16
 
 
-def test_quantization_reductions_need_fp32_or_bf16():
-    """Sum / average / max quantization runs on the HIP pooling kernels,
-    which take fp32 or bf16 features; other dtypes are refused, and the
-    row-picking modes take any dtype."""
+def test_quantization_reductions_other_dtypes():
+    """Sum / average / max quantization of fp32 and bf16 features runs on the
+    HIP pooling kernels; other dtypes (fp64 here) take torch's scatter
+    reductions, as the reference does for every dtype
+    (sparse_tensor.cpp:461-477). The row-picking modes take any dtype."""
     c = _cloud(7, n=500)
     cd = torch.from_numpy(c).to(DEV)
     f = torch.randn(len(c), 3, device=DEV, dtype=torch.float64)
+    fn = f.cpu().numpy()
     Q = re_.QuantizationMode
-    with pytest.raises(RuntimeError, match="fp32 or bf16"):
-        re_.SparseTensor(f, cd, quantization_mode=Q.UNWEIGHTED_SUM)
-    uq, mp, _ = oracle.insert_and_map(c)
+    uq, mp, inv = oracle.insert_and_map(c)
+    assert len(uq) < len(c)  # the cloud repeats rows
+    nu = len(uq)
+    want_sum = np.zeros((nu, 3))
+    np.add.at(want_sum, inv, fn)
+    counts = np.bincount(inv, minlength=nu)[:, None]
+    want_max = np.full((nu, 3), -np.inf)
+    np.maximum.at(want_max, inv, fn)
+    for mode, want in ((Q.UNWEIGHTED_SUM, want_sum), (Q.UNWEIGHTED_AVERAGE, want_sum / counts),
+                       (Q.MAX_POOL, want_max)):
+        x = re_.SparseTensor(f, cd, quantization_mode=mode)
+        assert x.F.dtype == torch.float64
+        np.testing.assert_allclose(x.F.cpu().numpy(), want, rtol=1e-12, atol=1e-12)
     x = re_.SparseTensor(f, cd, quantization_mode=Q.RANDOM_SUBSAMPLE)
-    np.testing.assert_array_equal(x.F.cpu().numpy(), f.cpu().numpy()[mp])
+    np.testing.assert_array_equal(x.F.cpu().numpy(), fn[mp])
 
 
 def test_convolution_4d():
