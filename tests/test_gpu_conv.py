@@ -505,7 +505,7 @@ def _torch_gather_gemm_scatter(km, x, w, gy):
     return y.detach(), x.grad, w.grad
 
 
-@pytest.mark.parametrize("cin", [64, 128])
+@pytest.mark.parametrize("cin", [64, 128, 256])
 def test_bf16_forward_untransposed_weights(cin):
     """bf16 128-column tiles without an offset-axis split read W itself (two
     transposed LDS reads per B operand) instead of a transposed copy: a 3^3
