@@ -1836,6 +1836,7 @@ conv_dw_pos_kernel(const float *__restrict__ x, int64_t n_in, int cin,
   const __amdgpu_buffer_rsrc_t ry = buf_rsrc(gy, n_out * cout * 4);
   const __amdgpu_buffer_rsrc_t rn = buf_rsrc(nbr, static_cast<int64_t>(K) * n_out * 4);
   const __amdgpu_buffer_rsrc_t ro = buf_rsrc(out_order, out_order ? n_out * 4 : 0);
+  const int32_t has_order = opaque(out_order ? -1 : 0);
   // offsets are chosen with opaque all-ones / zero masks rather than
   // selects, so that no load ends up behind a divergent branch
   auto pick = [](uint32_t off, int32_t keep) {
@@ -1850,6 +1851,7 @@ conv_dw_pos_kernel(const float *__restrict__ x, int64_t n_in, int cin,
   struct Seg {
     int32_t id[KPW];
     int32_t orow;
+    int32_t pos;
     int32_t in; // -1 for a position of the map, 0 past its end
   };
   struct Dat {
@@ -1865,11 +1867,12 @@ conv_dw_pos_kernel(const float *__restrict__ x, int64_t n_in, int cin,
       S.id[j] = static_cast<int32_t>(__builtin_amdgcn_raw_buffer_load_b32(
           rn, pick(static_cast<uint32_t>((kk[j] * n_out + p) * 4), keep), 0, 0));
     }
-    if (out_order)
-      S.orow = static_cast<int32_t>(__builtin_amdgcn_raw_buffer_load_b32(
-          ro, pick(static_cast<uint32_t>(p * 4), in), 0, 0));
-    else
-      S.orow = static_cast<int32_t>(p);
+    // loaded also without an order (from an empty buffer, as zero): a load
+    // behind a branch leaves the in-order waits for the rows prefetched
+    // before it uncounted, and the loop head then waits for every load
+    S.orow = static_cast<int32_t>(__builtin_amdgcn_raw_buffer_load_b32(
+        ro, pick(static_cast<uint32_t>(p * 4), in & has_order), 0, 0));
+    S.pos = static_cast<int32_t>(p);
     S.in = in;
   };
   // Once a segment's indices have arrived: the live masks (bit l: position
@@ -1882,7 +1885,7 @@ conv_dw_pos_kernel(const float *__restrict__ x, int64_t n_in, int cin,
       live[j] = __ballot(r >= 0);
       S.id[j] = static_cast<int32_t>(pick(static_cast<uint32_t>((r * cin + ci0) * 4), opaque(~(r >> 31))));
     }
-    const int32_t r = S.orow | ~S.in;
+    const int32_t r = (S.orow & has_order) | (S.pos & ~has_order) | ~S.in;
     S.orow = static_cast<int32_t>(pick(static_cast<uint32_t>((r * cout + co0) * 4), opaque(~(r >> 31))));
   };
   // rows of step s of a segment: lane (i16, g) takes position 4s + g's
@@ -1897,6 +1900,9 @@ conv_dw_pos_kernel(const float *__restrict__ x, int64_t n_in, int cin,
     }
     const uint32_t o = static_cast<uint32_t>(__builtin_amdgcn_ds_bpermute(src, S.orow)) + 4 * VB * i16;
     D.d = DV::load(ry, o);
+    // a compiler-only barrier: the loads stay here instead of sinking into
+    // the live branch of their step, where they would be waited for at once
+    asm volatile("" ::: "memory");
   };
 
   v4f acc[KPW][VB];
@@ -1972,6 +1978,215 @@ conv_dw_pos_kernel(const float *__restrict__ x, int64_t n_in, int cin,
   }
 }
 
+// Lane n of each 16-lane row of v, broadcast to the whole row (DPP
+// row_newbcast; n must fold to a constant).
+__device__ __forceinline__ int32_t row_bcast(int32_t v, int n) {
+  switch (n) {
+  case 0: return __builtin_amdgcn_mov_dpp(v, 0x150, 0xf, 0xf, false);
+  case 1: return __builtin_amdgcn_mov_dpp(v, 0x151, 0xf, 0xf, false);
+  case 2: return __builtin_amdgcn_mov_dpp(v, 0x152, 0xf, 0xf, false);
+  case 3: return __builtin_amdgcn_mov_dpp(v, 0x153, 0xf, 0xf, false);
+  case 4: return __builtin_amdgcn_mov_dpp(v, 0x154, 0xf, 0xf, false);
+  case 5: return __builtin_amdgcn_mov_dpp(v, 0x155, 0xf, 0xf, false);
+  case 6: return __builtin_amdgcn_mov_dpp(v, 0x156, 0xf, 0xf, false);
+  case 7: return __builtin_amdgcn_mov_dpp(v, 0x157, 0xf, 0xf, false);
+  case 8: return __builtin_amdgcn_mov_dpp(v, 0x158, 0xf, 0xf, false);
+  case 9: return __builtin_amdgcn_mov_dpp(v, 0x159, 0xf, 0xf, false);
+  case 10: return __builtin_amdgcn_mov_dpp(v, 0x15a, 0xf, 0xf, false);
+  case 11: return __builtin_amdgcn_mov_dpp(v, 0x15b, 0xf, 0xf, false);
+  case 12: return __builtin_amdgcn_mov_dpp(v, 0x15c, 0xf, 0xf, false);
+  case 13: return __builtin_amdgcn_mov_dpp(v, 0x15d, 0xf, 0xf, false);
+  case 14: return __builtin_amdgcn_mov_dpp(v, 0x15e, 0xf, 0xf, false);
+  default: return __builtin_amdgcn_mov_dpp(v, 0x15f, 0xf, 0xf, false);
+  }
+}
+
+// fp32 dW from the neighbour table for 64-channel input and output tiles
+// (C_in and C_out multiples of 64), the same position-stationary design as
+// conv_dw_pos_kernel with each lane's X load widened to 16 bytes:
+//  * lane (i16, g) reads X[nbr[k][p0 + 4s + g]][ci0 + 4*i16 .. +3] and
+//    dY[out_order[p0 + 4s + g]][co0 + 4*i16 .. +3]; element m of the X vector
+//    is the A operand of MFMA row block m (row i16 = channel ci0 + 4*i16 + m)
+//    and element e of the dY vector the B operand of column block e, so one
+//    X load and one index move feed 16 MFMAs (4 with 16-channel slices);
+//  * wave w of a WPB-wave workgroup of offset group q keeps the 64 x 64
+//    tiles of offsets q + G*(w + WPB*j) (j < KPW, G groups) in registers (64
+//    floats per lane and offset). Dealing the offsets with stride G mixes the
+//    dense and the sparse ones in every group: on config 2's scenes the
+//    heaviest group holds 1.05x the mean pair count, against 1.86x for
+//    groups of consecutive offsets (every plane of a 3^3 stencil has its
+//    own density);
+//  * a segment's indices are loaded transposed, lane (i16, g) holding
+//    position 4*i16 + g, so that step s's four positions are column s of the
+//    four 16-lane rows and one DPP row broadcast hands each lane its
+//    position's index (no LDS round trip before the row loads, which a
+//    ds_bpermute puts between every step's multiplies and its next loads);
+//  * segment dealing, row slots, skipped steps and the partial slots
+//    [range][k][cin][cout] are as in conv_dw_pos_kernel.
+// Lane (i16, g) ends with D[4g+r][i16] of block (m, e), which is
+// dW[k][ci0 + 16g + 4r + m][co0 + 4*i16 + e].
+template <int KPW, int NSLOT, int WAVES, int WPB>
+__global__ __launch_bounds__(WPB * kWave) __attribute__((amdgpu_waves_per_eu(WAVES))) void
+conv_dw_pos64_kernel(const float *__restrict__ x, int64_t n_in, int cin,
+                     const float *__restrict__ gy, int cout, const int32_t *__restrict__ nbr,
+                     const int32_t *__restrict__ out_order, int64_t n_out, int K, int ranges,
+                     int ci_tiles, int co_tiles, float *__restrict__ partial) {
+  constexpr int GK = WPB * KPW; // offsets per group
+  const int groups = (K + GK - 1) / GK;
+  const int units = ci_tiles * co_tiles * groups;
+  const int r8 = ranges / kXcds;
+  const int xcd = static_cast<int>(blockIdx.x % kXcds), m = static_cast<int>(blockIdx.x / kXcds);
+  const int rg = xcd * r8 + m / units;
+  int u = m % units;
+  const int grp = u % groups;
+  u /= groups;
+  const int ci0 = (u % ci_tiles) * 64, co0 = (u / ci_tiles) * 64;
+
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const int i16 = lane & 15;
+  const int g = lane >> 4;
+  if (grp + groups * wv >= K) // a wave without offsets (no barrier follows)
+    return;
+  const int64_t total = (n_out + 63) / 64;
+  const int segs = static_cast<int>((total + 2LL * ranges - 1) / (2LL * ranges)) * 2;
+  int kk[KPW], kval[KPW];
+#pragma unroll
+  for (int j = 0; j < KPW; ++j) {
+    kk[j] = grp + groups * (wv + WPB * j);
+    kval[j] = opaque(kk[j] < K ? -1 : 0);
+  }
+
+  const __amdgpu_buffer_rsrc_t rx = buf_rsrc(x, n_in * cin * 4);
+  const __amdgpu_buffer_rsrc_t ry = buf_rsrc(gy, n_out * cout * 4);
+  const __amdgpu_buffer_rsrc_t rn = buf_rsrc(nbr, static_cast<int64_t>(K) * n_out * 4);
+  const __amdgpu_buffer_rsrc_t ro = buf_rsrc(out_order, out_order ? n_out * 4 : 0);
+  const int32_t has_order = opaque(out_order ? -1 : 0);
+
+  struct Seg {
+    int32_t id[KPW];
+    int32_t orow;
+    int32_t pos;
+    int32_t in;
+  };
+  struct Dat {
+    v4u a[KPW];
+    v4u d;
+  };
+  auto load_seg = [&](int sg, Seg &S) {
+    const int64_t p = 64 * (rg + static_cast<int64_t>(sg) * ranges) + 4 * i16 + g;
+    const int32_t in = opaque(static_cast<int32_t>((p - n_out) >> 63)); // -1 for a position
+#pragma unroll
+    for (int j = 0; j < KPW; ++j) {
+      const int32_t keep = in & kval[j];
+      S.id[j] = static_cast<int32_t>(__builtin_amdgcn_raw_buffer_load_b32(
+          rn, pick_off(static_cast<uint32_t>((kk[j] * n_out + p) * 4), keep), 0, 0));
+    }
+    // loaded also without an order (from an empty buffer, as zero): a load
+    // behind a branch leaves the in-order waits for the rows prefetched
+    // before it uncounted, and the loop head then waits for every load
+    S.orow = static_cast<int32_t>(__builtin_amdgcn_raw_buffer_load_b32(
+        ro, pick_off(static_cast<uint32_t>(p * 4), in & has_order), 0, 0));
+    S.pos = static_cast<int32_t>(p);
+    S.in = in;
+  };
+  auto prep = [&](Seg &S, uint64_t (&live)[KPW]) {
+#pragma unroll
+    for (int j = 0; j < KPW; ++j) {
+      const int32_t r = S.id[j] | ~(S.in & kval[j]);
+      live[j] = __ballot(r >= 0);
+      S.id[j] = static_cast<int32_t>(
+          pick_off(static_cast<uint32_t>((r * cin + ci0) * 4), opaque(~(r >> 31))));
+    }
+    const int32_t r = (S.orow & has_order) | (S.pos & ~has_order) | ~S.in;
+    S.orow = static_cast<int32_t>(
+        pick_off(static_cast<uint32_t>((r * cout + co0) * 4), opaque(~(r >> 31))));
+  };
+  auto load_dat = [&](const Seg &S, int s, Dat &D) {
+#pragma unroll
+    for (int j = 0; j < KPW; ++j) {
+      const uint32_t o = static_cast<uint32_t>(row_bcast(S.id[j], s)) + 16 * i16;
+      D.a[j] = __builtin_amdgcn_raw_buffer_load_b128(rx, o, 0, 0);
+    }
+    const uint32_t o = static_cast<uint32_t>(row_bcast(S.orow, s)) + 16 * i16;
+    D.d = __builtin_amdgcn_raw_buffer_load_b128(ry, o, 0, 0);
+    // a compiler-only barrier: the loads stay here instead of sinking into
+    // the live branch of their step, where they would be waited for at once
+    asm volatile("" ::: "memory");
+  };
+
+  v4f acc[KPW][4][4];
+#pragma unroll
+  for (int j = 0; j < KPW; ++j)
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+      for (int eb = 0; eb < 4; ++eb)
+        acc[j][mb][eb] = v4f{0.f, 0.f, 0.f, 0.f};
+  auto compute = [&](const Dat &D, const uint64_t (&live)[KPW], int s) {
+#pragma unroll
+    for (int j = 0; j < KPW; ++j)
+      if ((live[j] >> s) & 0x0001000100010001ull) { // wave-uniform: column s of the rows
+#pragma unroll
+        for (int mb = 0; mb < 4; ++mb) {
+          const uint32_t av = D.a[j][mb];
+#pragma unroll
+          for (int eb = 0; eb < 4; ++eb) {
+            const uint32_t dv = D.d[eb];
+            acc[j][mb][eb] = __builtin_amdgcn_mfma_f32_16x16x4f32(
+                __builtin_bit_cast(float, av), __builtin_bit_cast(float, dv), acc[j][mb][eb], 0, 0,
+                0);
+          }
+        }
+      }
+  };
+
+  static_assert(16 % NSLOT == 0, "row slots must divide a segment");
+  Seg SA, SB;
+  uint64_t LA[KPW], LB[KPW];
+  Dat D[NSLOT];
+  auto run_seg = [&](Seg &S, const uint64_t (&LS)[KPW], Seg &N, uint64_t (&LN)[KPW],
+                     int next_load) {
+#pragma unroll
+    for (int s = 0; s < 16; ++s) {
+      const int ahead = s + NSLOT - 1;
+      if (ahead < 16) {
+        load_dat(S, ahead, D[ahead % NSLOT]);
+      } else {
+        if (ahead == 16)
+          prep(N, LN);
+        load_dat(N, ahead - 16, D[ahead % NSLOT]);
+      }
+      compute(D[s % NSLOT], LS, s);
+    }
+    load_seg(next_load, S);
+  };
+  load_seg(0, SA);
+  load_seg(1, SB);
+  prep(SA, LA);
+#pragma unroll
+  for (int s = 0; s + 1 < NSLOT; ++s)
+    load_dat(SA, s, D[s]);
+  for (int sg = 0; sg < segs; sg += 2) {
+    run_seg(SA, LA, SB, LB, sg + 2);
+    run_seg(SB, LB, SA, LA, sg + 3);
+  }
+
+#pragma unroll
+  for (int j = 0; j < KPW; ++j) {
+    if (kk[j] >= K)
+      continue;
+    float *dst = partial + ((static_cast<int64_t>(rg) * K + kk[j]) * cin + ci0 + 16 * g) * cout +
+                 co0 + 4 * i16;
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+      for (int mb = 0; mb < 4; ++mb)
+        *reinterpret_cast<v4f *>(dst + static_cast<int64_t>(4 * r + mb) * cout) =
+            v4f{acc[j][mb][0][r], acc[j][mb][1][r], acc[j][mb][2][r], acc[j][mb][3][r]};
+  }
+}
+
 // bf16 dW from the neighbour table, position-stationary like
 // conv_dw_pos_kernel: a workgroup owns a 16-channel input slice ci0, 16*NB
 // output channels co0 and up to 4*KPW offsets; wave w keeps the 16 x 16*NB
@@ -2032,6 +2247,7 @@ conv_dw_pos_bf16_kernel(const __bf16 *__restrict__ x, int64_t n_in, int cin,
   const __amdgpu_buffer_rsrc_t ry = buf_rsrc(gy, n_out * cout * 2);
   const __amdgpu_buffer_rsrc_t rn = buf_rsrc(nbr, static_cast<int64_t>(K) * n_out * 4);
   const __amdgpu_buffer_rsrc_t ro = buf_rsrc(out_order, out_order ? n_out * 4 : 0);
+  const int32_t has_order = opaque(out_order ? -1 : 0);
   auto pick = [](uint32_t off, int32_t keep) {
     return (off & static_cast<uint32_t>(keep)) | (kBufOob & ~static_cast<uint32_t>(keep));
   };
@@ -2042,6 +2258,7 @@ conv_dw_pos_bf16_kernel(const __bf16 *__restrict__ x, int64_t n_in, int cin,
   struct Seg {
     int32_t id[KPW];
     int32_t orow;
+    int32_t pos;
     int32_t in; // -1 for a position of the map, 0 past its end
   };
   constexpr int kYv = SHY ? 1 : NB;
@@ -2058,11 +2275,12 @@ conv_dw_pos_bf16_kernel(const __bf16 *__restrict__ x, int64_t n_in, int cin,
       S.id[j] = static_cast<int32_t>(__builtin_amdgcn_raw_buffer_load_b32(
           rn, pick(static_cast<uint32_t>((kk[j] * n_out + p) * 4), keep), 0, 0));
     }
-    if (out_order)
-      S.orow = static_cast<int32_t>(__builtin_amdgcn_raw_buffer_load_b32(
-          ro, pick(static_cast<uint32_t>(p * 4), in), 0, 0));
-    else
-      S.orow = static_cast<int32_t>(p);
+    // loaded also without an order (from an empty buffer, as zero): a load
+    // behind a branch leaves the in-order waits for the rows prefetched
+    // before it uncounted, and the loop head then waits for every load
+    S.orow = static_cast<int32_t>(__builtin_amdgcn_raw_buffer_load_b32(
+        ro, pick(static_cast<uint32_t>(p * 4), in & has_order), 0, 0));
+    S.pos = static_cast<int32_t>(p);
     S.in = in;
   };
   auto prep = [&](Seg &S, uint64_t (&live)[KPW]) {
@@ -2072,7 +2290,7 @@ conv_dw_pos_bf16_kernel(const __bf16 *__restrict__ x, int64_t n_in, int cin,
       live[j] = __ballot(r >= 0);
       S.id[j] = static_cast<int32_t>(pick(static_cast<uint32_t>((r * cin + ci0) * 2), opaque(~(r >> 31))));
     }
-    const int32_t r = S.orow | ~S.in;
+    const int32_t r = (S.orow & has_order) | (S.pos & ~has_order) | ~S.in;
     S.orow = static_cast<int32_t>(pick(static_cast<uint32_t>((r * cout + co0) * 2), opaque(~(r >> 31))));
   };
   // step s (0 or 1) of a segment: lane l takes position 32s + l/2's offsets
@@ -2251,6 +2469,7 @@ conv_dw_shx_bf16_kernel(const __bf16 *__restrict__ x, int64_t n_in, int cin,
   const __amdgpu_buffer_rsrc_t ry = buf_rsrc(gy, n_out * cout * 2);
   const __amdgpu_buffer_rsrc_t rn = buf_rsrc(nbr, static_cast<int64_t>(K) * n_out * 4);
   const __amdgpu_buffer_rsrc_t ro = buf_rsrc(out_order, out_order ? n_out * 4 : 0);
+  const int32_t has_order = opaque(out_order ? -1 : 0);
   auto pick = [](uint32_t off, int32_t keep) {
     return (off & static_cast<uint32_t>(keep)) | (kBufOob & ~static_cast<uint32_t>(keep));
   };
@@ -2261,6 +2480,7 @@ conv_dw_shx_bf16_kernel(const __bf16 *__restrict__ x, int64_t n_in, int cin,
   struct Seg {
     int32_t id[KPW];
     int32_t orow;
+    int32_t pos;
     int32_t in; // -1 for a position of the map, 0 past its end
   };
   struct Dat {
@@ -2277,11 +2497,12 @@ conv_dw_shx_bf16_kernel(const __bf16 *__restrict__ x, int64_t n_in, int cin,
       S.id[j] = static_cast<int32_t>(__builtin_amdgcn_raw_buffer_load_b32(
           rn, pick(static_cast<uint32_t>((kk[j] * n_out + p) * 4), keep), 0, 0));
     }
-    if (out_order)
-      S.orow = static_cast<int32_t>(__builtin_amdgcn_raw_buffer_load_b32(
-          ro, pick(static_cast<uint32_t>(p * 4), in), 0, 0));
-    else
-      S.orow = static_cast<int32_t>(p);
+    // loaded also without an order (from an empty buffer, as zero): a load
+    // behind a branch leaves the in-order waits for the rows prefetched
+    // before it uncounted, and the loop head then waits for every load
+    S.orow = static_cast<int32_t>(__builtin_amdgcn_raw_buffer_load_b32(
+        ro, pick(static_cast<uint32_t>(p * 4), in & has_order), 0, 0));
+    S.pos = static_cast<int32_t>(p);
     S.in = in;
   };
   // live masks, then byte offsets of the rows' chunk (out of range if absent)
@@ -2292,7 +2513,7 @@ conv_dw_shx_bf16_kernel(const __bf16 *__restrict__ x, int64_t n_in, int cin,
       live[j] = __ballot(r >= 0);
       S.id[j] = static_cast<int32_t>(pick(static_cast<uint32_t>((r * cin + c0) * 2), opaque(~(r >> 31))));
     }
-    const int32_t r = S.orow | ~S.in;
+    const int32_t r = (S.orow & has_order) | (S.pos & ~has_order) | ~S.in;
     S.orow = static_cast<int32_t>(pick(static_cast<uint32_t>((r * cout + co0) * 2), opaque(~(r >> 31))));
   };
   // step s (0 or 1) of a segment: lane l loads position 32s + 8*wv + l/8,
@@ -3239,7 +3460,31 @@ static int dw_pos_bf16_ranges(int K, int cin, int cout, int64_t n_out) {
   const int waves = K <= kDwPosMaxKSmall ? 4 : 2;
   return dw_pos_ranges(K, cin, cout, cout % 64 == 0 ? 4 : 2, waves, n_out, 16);
 }
+// fp32 dW on 64-channel input and output tiles (conv_dw_pos64_kernel):
+// 2 offsets per wave, 2-wave workgroups (groups of 4 offsets: 28 offset
+// slots for a 3^3 stencil), 2 waves per SIMD, the one-round grid. Measured
+// on MI355X, config 2 (C64, 410k rows, 144 ranges), kernel + reduce per
+// call: 381-385 us against 437-440 for conv_dw_pos_kernel's 16-channel
+// slices in the same run; with ds_bpermute index moves instead of the DPP
+// row broadcasts 390-399; with groups of consecutive offsets 473; 4-wave
+// workgroups 432; one offset per wave at 3 or 4 waves per SIMD 489-576
+// (each offset re-reads the dY rows). Without the multiplies the kernel
+// takes 216 us, without the row loads 357: the MFMA issue, not the
+// gathers, sets its time.
+constexpr int kDwPos64KPW = 2, kDwPos64WPB = 2, kDwPos64Waves = 2;
+static bool dw_pos64(int K, int cin, int cout) {
+  return K > kDwPosMaxKSmall && cin % 64 == 0 && cout % 64 == 0;
+}
+static int dw_pos64_ranges(int K, int cin, int cout, int64_t n_out) {
+  const int groups = static_cast<int>(ceil_div(K, kDwPos64WPB * kDwPos64KPW));
+  // workgroups of WPB waves: 4 / WPB of them put one wave on each SIMD
+  return dw_ranges_for((cin / 64) * (cout / 64) * groups, kDwPos64Waves * (kWaves / kDwPos64WPB),
+                       n_out, 2);
+}
+
 static int dw_pos_f32_ranges(int K, int cin, int cout, int64_t n_out) {
+  if (dw_pos64(K, cin, cout))
+    return dw_pos64_ranges(K, cin, cout, n_out);
   const int vb = cout % 64 == 0 ? 4 : 2;
   const int waves = K <= kDwPosMaxKSmall ? 3 : (vb == 4 ? kDwPosWaves<4> : kDwPosWaves<2>);
   return dw_pos_ranges(K, cin, cout, vb, waves, n_out, 2);
@@ -3298,7 +3543,14 @@ static void run_dw_pos(const float *x, int64_t n_in, int cin, const float *gy, i
   const int ranges = dw_pos_f32_ranges(K, cin, cout, n_out);
   const int groups = static_cast<int>(ceil_div(K, kWaves * dw_pos_kpw(K)));
   const int ct = cin / 16, ot = cout / (16 * vb);
-  if (n_in > 0 && n_out > 0) {
+  if (n_in > 0 && n_out > 0 && dw_pos64(K, cin, cout)) {
+    const int g64 = static_cast<int>(ceil_div(K, kDwPos64WPB * kDwPos64KPW));
+    const dim3 grid(static_cast<unsigned>(ranges * (cin / 64) * (cout / 64) * g64));
+    hipLaunchKernelGGL((conv_dw_pos64_kernel<kDwPos64KPW, kDwPosSlots, kDwPos64Waves, kDwPos64WPB>),
+                       grid, dim3(kDwPos64WPB * kWave), 0, s, x, n_in, cin, gy, cout, nbr,
+                       out_order, n_out, K, ranges, cin / 64, cout / 64, partial);
+    RHIP_LAUNCH_CHECK();
+  } else if (n_in > 0 && n_out > 0) {
     const dim3 grid(static_cast<unsigned>(ranges * ct * ot * groups));
     auto go = [&](auto v, auto kpw, auto w) {
       hipLaunchKernelGGL((conv_dw_pos_kernel<decltype(v)::value, decltype(kpw)::value, kDwPosSlots,

@@ -250,10 +250,13 @@ def test_weight_gradient_from_neighbour_table_strided_and_4d():
     _rows_check(km4, 32, 32, seed=3, tag="3^4")
 
 
-@pytest.mark.parametrize("cin,cout", [(16, 64), (64, 64), (48, 128), (16, 32), (32, 96)])
+@pytest.mark.parametrize("cin,cout", [(16, 64), (64, 64), (48, 128), (16, 32), (32, 96),
+                                      (128, 64), (64, 192)])
 def test_weight_gradient_from_neighbour_table_f32(cin, cout):
-    """fp32: the position-stationary kernel (16-channel input slices, 64 or
-    32 output channels per tile, all 27 offsets in one workgroup)."""
+    """fp32: the position-stationary kernels (16-channel input slices with 64
+    or 32 output channels per tile and all 27 offsets in one workgroup; 64 x
+    64 tiles with 4 offsets per workgroup where both channel counts are
+    multiples of 64)."""
     rng = np.random.default_rng(cin + 7 * cout)
     c, _, _ = oracle.insert_and_map(random_coords(rng, 9000, 3, 14))
     _, _, km = gpu_tables_and_map(c, c, oracle.region_offsets(3, 3), same=True)
@@ -298,20 +301,23 @@ def test_weight_gradient_from_neighbour_table_f32_strided_4d_and_tiny():
     _, _, km4 = gpu_tables_and_map(c4, c4, oracle.region_offsets(4, 3), same=True)
     _rows_check(km4, 16, 64, seed=3, tag="3^4", dtype=torch.float32)
     _rows_check(km4, 32, 32, seed=5, tag="3^4 C32", dtype=torch.float32)
+    _rows_check(km4, 64, 64, seed=7, tag="3^4 C64", dtype=torch.float32)
     for npts in (1, 5, 63, 65):
         ct, _, _ = oracle.insert_and_map(random_coords(rng, npts, 3, 3))
         _, _, kmt = gpu_tables_and_map(ct, ct, oracle.region_offsets(3, 3), same=True)
         _rows_check(kmt, 16, 64, seed=npts, tag=f"tiny{npts}", dtype=torch.float32)
+        _rows_check(kmt, 64, 64, seed=npts, tag=f"tiny{npts} C64", dtype=torch.float32)
 
 
-def test_weight_gradient_from_neighbour_table_f32_row_order_and_empty():
+@pytest.mark.parametrize("cin", [32, 64])
+def test_weight_gradient_from_neighbour_table_f32_row_order_and_empty(cin):
     """out_order NULL (the table indexed by output row) gives the same dW as
     the processing-order table; no output rows gives zeros."""
     import types
     rng = np.random.default_rng(37)
     c, _, _ = oracle.insert_and_map(random_coords(rng, 5000, 3, 12))
     _, _, km = gpu_tables_and_map(c, c, oracle.region_offsets(3, 3), same=True)
-    x, gy, rows = _rows_check(km, 32, 64, seed=4, tag="order", dtype=torch.float32)
+    x, gy, rows = _rows_check(km, cin, 64, seed=4, tag="order", dtype=torch.float32)
     nbr = km.nbr.view(km.K, km.n_out)
     by_row = torch.empty_like(nbr)
     by_row[:, km.out_order.long()] = nbr
@@ -323,7 +329,7 @@ def test_weight_gradient_from_neighbour_table_f32_row_order_and_empty():
     km0 = types.SimpleNamespace(n_in=km.n_in, n_out=0, n_pairs=0, K=km.K,
                                 nbr=km.nbr, out_order=km.out_order)
     z = abi.conv_backward_weight_rows(x, gy[:0], km0, km.K)
-    assert z.shape == (km.K, 32, 64) and not z.any()
+    assert z.shape == (km.K, cin, 64) and not z.any()
 
 
 def test_weight_gradient_from_neighbour_table_f32_full_size():
