@@ -940,7 +940,7 @@ def conv_step_record(args, dtype, km, n_in, n_out, P, K, cin, cout):
     roof["kernel"] = {"forward": "conv_os_lds_kernel (forward)",
                       "backward_input": "conv_os_lds_kernel (dX)",
                       "backward_weight": (
-                          "conv_dw_pos_kernel + conv_dw_rows_reduce_kernel (dW pass)"
+                          "conv_dw_pos64_kernel + conv_dw_rows_reduce_kernel (dW pass)"
                           if dtype == "f32" else
                           "conv_dw_shx_bf16_kernel + conv_dw_rows_reduce_kernel (dW pass)")}[dom]
     roof["kernel_ms"] = round(kernel_ms, 4)
